@@ -1,0 +1,122 @@
+/* lithos_mi355.h — the C ABI of the gfx950 (MI355X) decode-layer backend.
+ *
+ * Everything here is plain C: opaque handles are void*, device memory is void*, sizes are int32/size_t. No torch
+ * types cross this boundary. Every function returns 0 (MI_OK) or an MI_E* code; mi_last_error() returns the message
+ * of the calling thread's last failure. Work is enqueued asynchronously on the given HIP stream (NULL = the null
+ * stream); nothing blocks unless its name says so (…_synchronize, mi_memcpy_d2h on the null stream).
+ *
+ * Each entry point replaces a piece of the reference's native layer or one of its kernels; the citation names the
+ * reference interface (paths relative to lithos-ai/lithos-metal).
+ */
+#ifndef LITHOS_MI355_H
+#define LITHOS_MI355_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MI_OK 0
+#define MI_E_INVALID 1     /* bad argument, shape or format: nothing was enqueued */
+#define MI_E_HIP 2         /* a HIP runtime call failed */
+#define MI_E_UNSUPPORTED 3 /* not built for this device (needs gfx950) */
+
+/* weight storage formats (reference plugin names in monolith/formats/registry.py) */
+#define MI_FMT_NVFP4 1       /* "nvfp4": E2M1 codes, E4M3 scale per 16, FP32 tensor scale (formats/nvfp4.py) */
+#define MI_FMT_INT4_AFFINE 2 /* "int4_affine": u4 codes, BF16 (scale, bias) per 64 (formats/int4_affine.py) */
+#define MI_FMT_BF16 3        /* "bf16": plain BF16 rows (formats/bf16.py) — the router / gate projections */
+
+/* GEMV epilogues (ops/gemv.py:1-12, nn/linear.py:114-135) */
+#define MI_EPI_NONE 0
+#define MI_EPI_RESIDUAL 1         /* y = bf16(acc + residual) */
+#define MI_EPI_SILU_MUL 2         /* rows are gate|up interleaved by 8: y = bf16(silu(gate)·up), N/2 columns */
+#define MI_EPI_SILU_MUL_ROUNDED 3 /* as above with gate and up rounded to BF16 first (nn/moe.py:333-336) */
+
+/* ---- errors / device (runtime/src/metal_core.h:20-35 Device/DeviceInfo; native.mm:13-20) ---------------------- */
+const char* mi_version(void);
+int mi_last_error(char* buf, size_t n);
+typedef struct mi_device_info {
+  char name[64];
+  char arch[64];         /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+  int32_t compute_units;
+  int32_t clock_khz;
+  int64_t hbm_bytes;
+  int32_t lds_bytes_per_block;
+  int32_t warp_size;
+} mi_device_info;
+int mi_device_count(int32_t* count);
+int mi_device_info_get(int32_t device, mi_device_info* out);
+int mi_set_device(int32_t device);
+
+/* ---- buffers (metal_core.h:37-48 Buffer: alloc / init-from-bytes / read / write / fill) ------------------------- */
+int mi_malloc(void** ptr, size_t bytes);
+int mi_free(void* ptr);
+int mi_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
+int mi_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
+int mi_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
+int mi_memset(void* dst, int32_t byte, size_t bytes, void* stream);
+
+/* ---- streams, timing, graphs (metal_core.mm:128-210 Queue.run/profile; metal_core.h:106-116 Icb) ---------------- */
+int mi_stream_create(void** stream);
+int mi_stream_destroy(void* stream);
+int mi_stream_synchronize(void* stream);
+int mi_event_create(void** event);
+int mi_event_destroy(void* event);
+int mi_event_record(void* event, void* stream);
+int mi_event_synchronize(void* event);
+int mi_event_elapsed_ms(void* start, void* end, float* ms);
+int mi_graph_begin(void* stream);                        /* start capturing the stream's launches (Icb encode) */
+int mi_graph_end(void* stream, void** graph_exec);       /* finish capture, instantiate */
+int mi_graph_launch(void* graph_exec, void* stream);     /* replay (Icb executeCommandsInBuffer) */
+int mi_graph_destroy(void* graph_exec);
+
+/* ---- weight packs ----------------------------------------------------------------------------------------------
+ * The T16 pack: 16-row tiles × 128-column chunks (32 for BF16), one 1152-byte unit per (tile, chunk) holding the
+ * 64 lanes' 16-byte code words followed by the tile's block scales — the gfx950 counterpart of the reference's
+ * block-lane-major pack (formats/blm.py:56-266, PackLayout formats/base.py:10-34). Host code writes it
+ * (monolith_mi355/formats/pack.py); mi_pack_bytes gives its size. */
+size_t mi_pack_bytes(int32_t format, int32_t n, int32_t k);
+
+/* ---- GEMV / skinny GEMM (ops/gemv.py `gemv`; kernels/common/gemv_T.metal:232-587; kernels.py:222-226 GemvParams;
+ *      the M>=2 matrix path kernels/common/gemm_tile.metal:259) and its MoE pairs mode (ops/moe.py `moe_gemv`,
+ *      gemv_T.metal:331-358 PAIRS, moe_group.metal + moe_gemm.metal) ------------------------------------------- */
+typedef struct mi_gemv_desc {
+  int32_t format;            /* MI_FMT_* */
+  int32_t n, k;              /* rows and columns of one matrix (one expert in grouped mode) */
+  int32_t m;                 /* tokens (dense mode, 1..16); in grouped mode the token count of the step */
+  const void* w;             /* T16 pack; grouped mode: n_experts packs back to back */
+  const float* row_scale;    /* NVFP4 tensor scale per row [experts·n_pad] (the reference's row-scale table); NULL=1 */
+  const uint16_t* x;         /* BF16 activations, row stride ldx */
+  int32_t ldx;
+  uint16_t* y;               /* BF16 output, row stride ldy */
+  int32_t ldy;
+  int32_t epilogue;          /* MI_EPI_* */
+  const uint16_t* residual;  /* BF16 [m, ldr] for MI_EPI_RESIDUAL */
+  int32_t ldr;
+  const float* norm_w;       /* fused input RMSNorm: x = bf16(h·rsqrt(mean h²+eps)·norm_w), norm_w = (1+w) [k]; NULL = off */
+  float eps;
+  const int32_t* groups;     /* grouped (MoE) mode: [max_groups][18] = expert, count, 16 pair ids (mi_moe_group) */
+  int32_t max_groups;
+  int32_t top_k;             /* pair p = token·top_k + slot */
+  int32_t x_per_slot;        /* grouped: x row = p (1) or p / top_k (0); y row = p */
+  void* workspace;           /* split-K counters + partials (zero it once; reusable by any later GEMV shape, but
+                                calls overlapping in time need distinct workspaces); NULL = the library's own */
+  size_t workspace_bytes;
+  int32_t out_f32;           /* 1: y is FP32 (the lm_head / kernel-test output, ops/gemv.py:12), unrounded */
+} mi_gemv_desc;
+size_t mi_gemv_workspace_bytes(const mi_gemv_desc* d);   /* 0 when the plan needs none */
+int mi_gemv(const mi_gemv_desc* d, void* stream);
+/* the launch plan mi_gemv would use (host only, no device call): tiles per wave, waves per workgroup (K slices),
+ * chunks per wave, chunks per staged window, windows (-1: the VALU kernel for M <= 2), LDS bytes, workgroups */
+int mi_gemv_plan(const mi_gemv_desc* d, int32_t out[7]);
+
+/* exact dequantization of a T16 pack to FP32 [n, k] through the kernels' own decode (the bit-exact check of
+ * Format.dequantize, formats/base.py:52-81 / nvfp4.py:139-144 / int4_affine.py:85-91) */
+int mi_dequant(int32_t format, const void* w, const float* row_scale, int32_t n, int32_t k, float* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LITHOS_MI355_H */

@@ -1,0 +1,194 @@
+"""ctypes binding of ``libmi355.so`` — the C ABI declared in ``include/lithos_mi355.h``.
+
+This module replaces the reference's nanobind ``_native`` module (``runtime/src/native.mm:13-95``): it loads the
+shared library built from ``lithos-metal_amd/csrc`` and turns every non-zero return code into a ``RuntimeError``
+carrying ``mi_last_error()`` (the reference raises C++ ``std::runtime_error`` as Python exceptions,
+``runtime/src/metal_core.mm:49,67,106,117``). There is no fallback: a missing library raises at load time.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+from typing import Optional
+
+LIB_NAME = "libmi355.so"
+_PKG_ROOT = Path(__file__).resolve().parents[2]          # lithos-metal_amd/
+LIB_PATH = Path(os.environ.get("LITHOS_MI355_LIB", _PKG_ROOT / "lib" / LIB_NAME))
+
+MI_FMT = {"nvfp4": 1, "int4_affine": 2, "bf16": 3}
+MI_EPI = {None: 0, "none": 0, "residual": 1, "silu_mul": 2, "silu_mul_rounded": 3}
+
+
+class MiDeviceInfo(C.Structure):
+    _fields_ = [("name", C.c_char * 64), ("arch", C.c_char * 64), ("compute_units", C.c_int32),
+                ("clock_khz", C.c_int32), ("hbm_bytes", C.c_int64), ("lds_bytes_per_block", C.c_int32),
+                ("warp_size", C.c_int32)]
+
+
+class MiGemvDesc(C.Structure):
+    _fields_ = [("format", C.c_int32), ("n", C.c_int32), ("k", C.c_int32), ("m", C.c_int32),
+                ("w", C.c_void_p), ("row_scale", C.c_void_p), ("x", C.c_void_p), ("ldx", C.c_int32),
+                ("y", C.c_void_p), ("ldy", C.c_int32), ("epilogue", C.c_int32), ("residual", C.c_void_p),
+                ("ldr", C.c_int32), ("norm_w", C.c_void_p), ("eps", C.c_float), ("groups", C.c_void_p),
+                ("max_groups", C.c_int32), ("top_k", C.c_int32), ("x_per_slot", C.c_int32),
+                ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t), ("out_f32", C.c_int32)]
+
+
+# name -> (restype, argtypes); every int-returning entry point is error-checked
+_VP, _I32, _SZ, _F = C.c_void_p, C.c_int32, C.c_size_t, C.c_float
+SIGNATURES = {
+    "mi_version": (C.c_char_p, []),
+    "mi_last_error": (C.c_int, [C.c_char_p, _SZ]),
+    "mi_device_count": (C.c_int, [C.POINTER(_I32)]),
+    "mi_device_info_get": (C.c_int, [_I32, C.POINTER(MiDeviceInfo)]),
+    "mi_set_device": (C.c_int, [_I32]),
+    "mi_malloc": (C.c_int, [C.POINTER(_VP), _SZ]),
+    "mi_free": (C.c_int, [_VP]),
+    "mi_memcpy_h2d": (C.c_int, [_VP, _VP, _SZ, _VP]),
+    "mi_memcpy_d2h": (C.c_int, [_VP, _VP, _SZ, _VP]),
+    "mi_memcpy_d2d": (C.c_int, [_VP, _VP, _SZ, _VP]),
+    "mi_memset": (C.c_int, [_VP, _I32, _SZ, _VP]),
+    "mi_stream_create": (C.c_int, [C.POINTER(_VP)]),
+    "mi_stream_destroy": (C.c_int, [_VP]),
+    "mi_stream_synchronize": (C.c_int, [_VP]),
+    "mi_event_create": (C.c_int, [C.POINTER(_VP)]),
+    "mi_event_destroy": (C.c_int, [_VP]),
+    "mi_event_record": (C.c_int, [_VP, _VP]),
+    "mi_event_synchronize": (C.c_int, [_VP]),
+    "mi_event_elapsed_ms": (C.c_int, [_VP, _VP, C.POINTER(_F)]),
+    "mi_graph_begin": (C.c_int, [_VP]),
+    "mi_graph_end": (C.c_int, [_VP, C.POINTER(_VP)]),
+    "mi_graph_launch": (C.c_int, [_VP, _VP]),
+    "mi_graph_destroy": (C.c_int, [_VP]),
+    "mi_pack_bytes": (_SZ, [_I32, _I32, _I32]),
+    "mi_gemv_workspace_bytes": (_SZ, [C.POINTER(MiGemvDesc)]),
+    "mi_gemv": (C.c_int, [C.POINTER(MiGemvDesc), _VP]),
+    "mi_gemv_plan": (C.c_int, [C.POINTER(MiGemvDesc), C.POINTER(_I32)]),
+    "mi_dequant": (C.c_int, [_I32, _VP, _VP, _I32, _I32, _VP, _VP]),
+}
+
+
+class MiError(RuntimeError):
+    pass
+
+
+_lib: Optional[C.CDLL] = None
+
+
+def load(path: Optional[os.PathLike] = None) -> C.CDLL:
+    """Load (once) and type the library. Raises if it is missing — the product path has no CPU fallback."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise MiError(f"{p} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
+                      f"or `python lithos-metal_amd/build.py`")
+    lib = C.CDLL(str(p))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype, fn.argtypes = res, args
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    buf = C.create_string_buffer(512)
+    load().mi_last_error(buf, 512)
+    return buf.value.decode(errors="replace")
+
+
+def call(name: str, *args) -> int:
+    rc = getattr(load(), name)(*args)
+    if rc != 0:
+        raise MiError(f"{name} failed ({rc}): {last_error()}")
+    return rc
+
+
+def device_info(device: int = 0) -> MiDeviceInfo:
+    info = MiDeviceInfo()
+    call("mi_device_info_get", device, C.byref(info))
+    return info
+
+
+def ptr(t) -> int:
+    """Device address of a tensor-like (``.data_ptr()``), an int, or None → 0."""
+    if t is None:
+        return 0
+    if isinstance(t, int):
+        return t
+    return int(t.data_ptr())
+
+
+def stream_handle(stream=None) -> Optional[int]:
+    """A HIP stream handle: an int, a ``torch.cuda.Stream``, or None → torch's current stream when torch has one."""
+    if stream is None:
+        try:
+            import torch
+            if torch.cuda.is_available():
+                return int(torch.cuda.current_stream().cuda_stream)
+        except ImportError:
+            pass
+        return None
+    if isinstance(stream, int):
+        return stream
+    return int(stream.cuda_stream)
+
+
+class Event:
+    """A HIP event pair helper for timing work on one stream (``Queue.profile``'s per-dispatch timestamps,
+    ``runtime/src/metal_core.mm:157-210``)."""
+
+    def __init__(self):
+        h = C.c_void_p()
+        call("mi_event_create", C.byref(h))
+        self.h = h
+
+    def record(self, stream=None):
+        call("mi_event_record", self.h, stream_handle(stream))
+
+    def synchronize(self):
+        call("mi_event_synchronize", self.h)
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = C.c_float()
+        call("mi_event_elapsed_ms", self.h, end.h, C.byref(ms))
+        return float(ms.value)
+
+    def __del__(self):
+        try:
+            if _lib is not None and self.h:
+                _lib.mi_event_destroy(self.h)
+        except Exception:
+            pass
+
+
+class Graph:
+    """Stream capture → replayable graph: the reference's pre-encoded ICB (``runtime/src/metal_core.h:106-116``)."""
+
+    def __init__(self, stream):
+        self.stream = stream_handle(stream)
+        self.exec = None
+
+    def __enter__(self):
+        call("mi_graph_begin", self.stream)
+        return self
+
+    def __exit__(self, *exc):
+        h = C.c_void_p()
+        call("mi_graph_end", self.stream, C.byref(h))
+        self.exec = h
+        return False
+
+    def launch(self, stream=None):
+        call("mi_graph_launch", self.exec, stream_handle(stream) if stream is not None else self.stream)
+
+    def __del__(self):
+        try:
+            if _lib is not None and self.exec:
+                _lib.mi_graph_destroy(self.exec)
+        except Exception:
+            pass

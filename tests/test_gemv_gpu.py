@@ -1,0 +1,175 @@
+"""The HIP GEMV / skinny GEMM against the oracle (the reference's ``tests/kernels/test_gemv_T.py`` strategy):
+
+* dequantized weights decoded by the kernels' own decode path are bit-identical to the oracle's ``dequantize``
+  (all three formats, including every E4M3 block-scale code);
+* ``y = x·Wᵀ`` within the reference's leaf gate (``OracleCheck.ok``: ≤ 2 BF16 ULP at the output RMS, relative error
+  < 1e-4) against a float64 matmul of the exact dequantized matrix, for M = 1, 2, 8, 16, ragged N, the residual and
+  silu·mul epilogues (rounded chains gated by ``ok_rounded``) and the fused input RMSNorm;
+* the BASELINE shapes (INT4 4096×4096, NVFP4 17408×5120 and 5120×17408 at M = 1 and 8).
+"""
+
+import numpy as np
+import pytest
+
+from helpers import from_dev_bf16, spec_of, to_dev_bf16
+from oracle import formats as OF
+from oracle import nn as ON
+from oracle.fp import rbf
+from oracle.gates import check_against_oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _matrix(fmt, n, k, rng):
+    if fmt == "nvfp4":
+        return OF.nvfp4_random(n, k, rng)
+    if fmt == "int4_affine":
+        return OF.int4_random(n, k, rng)
+    from oracle.fp import f32_to_bf16
+    return {"format": "bf16", "weight": f32_to_bf16((rng.standard_normal((n, k)) * 0.02).astype(np.float32))}
+
+
+def _dequant(m):
+    if m["format"] == "bf16":
+        from oracle.fp import bf16_to_f32
+        return bf16_to_f32(m["weight"])
+    return OF.dequantize(m)
+
+
+def _upload(torch, m):
+    from monolith_mi355 import kernels
+    return kernels.upload(spec_of(m))
+
+
+@pytest.mark.parametrize("fmt", ["nvfp4", "int4_affine", "bf16"])
+@pytest.mark.parametrize("n,k", [(16, 128), (37, 512), (300, 1024)])
+def test_dequant_bit_exact(torch_gpu, fmt, n, k, rng):
+    from monolith_mi355 import kernels
+    if fmt == "bf16" and k % 32:
+        pytest.skip()
+    m = _matrix(fmt, n, k, rng)
+    w = _upload(torch_gpu, m)
+    got = kernels.dequant(w).cpu().numpy()
+    ref = _dequant(m)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_dequant_every_scale_code(torch_gpu, rng):
+    """All 126 finite non-negative E4M3 block-scale codes and all 16 E2M1 codes, bit for bit
+    (the reference's tests/kernels/test_nvfp4_scale_decode.py:11-27)."""
+    from monolith_mi355 import kernels
+    n, k = 128, 256
+    m = OF.nvfp4_random(n, k, rng)
+    codes = np.arange(n * k // 16) % 0x7F                      # 0x00..0x7E cycling
+    m["weight_scale"] = codes.astype(np.uint8).reshape(n, k // 16)
+    m["weight"] = (np.arange(n * k // 2) % 256).astype(np.uint8).reshape(n, k // 2)
+    got = kernels.dequant(_upload(torch_gpu, m)).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), OF.nvfp4_dequantize(m).view(np.uint32))
+
+
+def _run(torch, m, x, **kw):
+    """FP32 output, as the reference's gemv_T test reads it (tests/kernels/test_gemv_T.py:21-46)."""
+    from monolith_mi355 import kernels
+    w = _upload(torch, m)
+    y = kernels.gemv(w, to_dev_bf16(torch, x), out_f32=True, **kw)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+@pytest.mark.parametrize("fmt", ["nvfp4", "int4_affine", "bf16"])
+@pytest.mark.parametrize("mtok", [1, 2, 8, 16])
+@pytest.mark.parametrize("n,k", [(48, 256), (77, 1024), (1040, 2048)])
+def test_gemv_matches_oracle(torch_gpu, fmt, mtok, n, k, rng):
+    m = _matrix(fmt, n, k, rng)
+    x = rbf(rng.standard_normal((mtok, k)).astype(np.float32))
+    got = _run(torch_gpu, m, x)
+    ref = ON.matmul_acc(x, _dequant(m))
+    chk = check_against_oracle(got, ref)
+    assert chk.ok(), (fmt, mtok, n, k, chk)
+    from monolith_mi355 import kernels                      # the BF16 output is the same number rounded once
+    yb = from_dev_bf16(kernels.gemv(_upload(torch_gpu, m), to_dev_bf16(torch_gpu, x)))
+    assert np.array_equal(yb, rbf(got))
+
+
+@pytest.mark.parametrize("fmt", ["nvfp4", "int4_affine"])
+@pytest.mark.parametrize("mtok", [1, 8])
+def test_gemv_residual(torch_gpu, fmt, mtok, rng):
+    n, k = 160, 1024
+    m = _matrix(fmt, n, k, rng)
+    x = rbf(rng.standard_normal((mtok, k)))
+    res = rbf(rng.standard_normal((mtok, n)))
+    from monolith_mi355 import kernels
+    w = _upload(torch_gpu, m)
+    y = kernels.gemv(w, to_dev_bf16(torch_gpu, x), epilogue="residual", residual=to_dev_bf16(torch_gpu, res))
+    got = from_dev_bf16(y)
+    ref = ON.linear(x, _dequant(m), epilogue="residual", residual=res)
+    chk = check_against_oracle(got, ref)
+    assert chk.ok_rounded() and chk.max_ulp_elementwise <= 1, chk
+
+
+@pytest.mark.parametrize("fmt", ["nvfp4", "int4_affine"])
+@pytest.mark.parametrize("rounded", [False, True])
+@pytest.mark.parametrize("mtok", [1, 8])
+def test_gemv_silu_mul(torch_gpu, fmt, rounded, mtok, rng):
+    inter, k = 96, 512
+    gate, up = _matrix(fmt, inter, k, rng), _matrix(fmt, inter, k, rng)
+    if fmt == "nvfp4":
+        up["weight_scale_2"] = gate["weight_scale_2"] * 1.5              # distinct tensor scales per part
+    slab = OF.stack_rows([gate, up])
+    perm = ON.interleave_chunks(inter, inter, 8)
+    slab = OF.permute_rows(slab, perm)
+    from monolith_mi355 import kernels
+    from monolith_mi355.formats import DequantSpec
+    spec = spec_of(dict(slab, weight_scale_2=1.0))
+    w = kernels.upload(spec, row_scales=[slab["row_scale"]] if fmt == "nvfp4" else None)
+    x = rbf(rng.standard_normal((mtok, k)))
+    epi = "silu_mul_rounded" if rounded else "silu_mul"
+    got = from_dev_bf16(kernels.gemv(w, to_dev_bf16(torch_gpu, x), epilogue=epi))
+    wg, wu = OF.dequantize(gate), OF.dequantize(up)
+    ref = ON.linear(x, np.concatenate([wg, wu]), epilogue="silu_mul", round_silu=rounded)
+    chk = check_against_oracle(got, ref)
+    assert got.shape == (mtok, inter)
+    assert chk.ok_rounded(), chk
+
+
+@pytest.mark.parametrize("fmt", ["nvfp4", "int4_affine", "bf16"])
+@pytest.mark.parametrize("mtok", [1, 8])
+def test_gemv_fused_norm(torch_gpu, fmt, mtok, rng):
+    n, k = 200, 2048
+    m = _matrix(fmt, n, k, rng)
+    h = rbf(rng.standard_normal((mtok, k)) * 3)
+    wn = rbf(rng.standard_normal(k) * 0.2)
+    nw = (1.0 + wn).astype(np.float32)
+    from monolith_mi355 import kernels
+    w = _upload(torch_gpu, m)
+    got = kernels.gemv(w, to_dev_bf16(torch_gpu, h), norm_w=torch_gpu.from_numpy(nw).cuda(), eps=1e-6,
+                       out_f32=True).cpu().numpy()
+    xn = ON.rms_norm(h, wn, 1e-6)
+    ref = ON.matmul_acc(xn, _dequant(m))
+    chk = check_against_oracle(got, ref)
+    assert chk.ok_rounded(), chk
+
+
+@pytest.mark.parametrize("fmt,n,k,mtok", [("int4_affine", 4096, 4096, 1), ("nvfp4", 17408, 5120, 1),
+                                          ("nvfp4", 17408, 5120, 8), ("nvfp4", 5120, 17408, 1),
+                                          ("nvfp4", 5120, 17408, 8)])
+def test_gemv_baseline_shapes(torch_gpu, fmt, n, k, mtok):
+    rng = np.random.default_rng(n + k + mtok)
+    m = _matrix(fmt, n, k, rng)
+    x = rbf(rng.standard_normal((mtok, k)))
+    got = _run(torch_gpu, m, x)
+    w = _dequant(m)
+    ref = ON.matmul_acc(x, w)
+    chk = check_against_oracle(got, ref)
+    assert chk.ok(), chk
+
+
+def test_gemv_repeat_is_bit_identical(torch_gpu, rng):
+    """Split-K partials are combined in a fixed order: two runs give the same bits."""
+    from monolith_mi355 import kernels
+    m = _matrix("nvfp4", 5120, 17408, rng)
+    w = _upload(torch_gpu, m)
+    x = to_dev_bf16(torch_gpu, rbf(rng.standard_normal((8, 17408))))
+    a = kernels.gemv(w, x).clone()
+    b = kernels.gemv(w, x)
+    assert torch_gpu.equal(a, b)
