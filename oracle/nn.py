@@ -210,11 +210,11 @@ def kv_dequantize(codes, scales):
     return (np.asarray(codes, F32) * np.asarray(scales, np.float16).astype(F32)[..., None]).astype(F32)
 
 
-def gqa_mix(proj, k_codes, k_scales, v_codes, v_scales, pos, *, heads, kv_heads, head_dim, rotary_dim, theta, eps,
-            gate=True, qk_norm=False, q_norm=None, k_norm=None):
-    """``GQAAttention.mix`` (``nn/attention.py:215-243``) over the int8 cache: ``proj [T, N1]`` in checkpoint column
-    order ``q|gate`` per head, then ``k``, ``v``. The fresh k/v (after q/k norm and RoPE) are quantized into the cache
-    at ``pos..pos+T`` (arrays updated in place); the step attends over the dequantized cache. Returns ``[T, H·D]``."""
+def gqa_prepare(proj, pos, *, heads, kv_heads, head_dim, rotary_dim, theta, eps, gate=True, qk_norm=False,
+                q_norm=None, k_norm=None):
+    """The first half of ``GQAAttention.mix`` (``nn/attention.py:222-238``): split ``proj [T, N1]`` (checkpoint
+    column order: ``q|gate`` per head, then ``k``, ``v``), optional q/k RMSNorm(1 + w), partial RoPE with BF16 tables.
+    Returns ``(q [T,H,D], k [T,Hkv,D], v [T,Hkv,D], gate [T,H,D] or None)``."""
     proj = np.asarray(proj, F32)
     t = proj.shape[0]
     d = head_dim
@@ -231,19 +231,37 @@ def gqa_mix(proj, k_codes, k_scales, v_codes, v_scales, pos, *, heads, kv_heads,
         k = rms_norm(k, k_norm, eps)
     cos, sin = rope_tables(theta, rotary_dim, np.arange(pos, pos + t))
     cos, sin = rbf(cos), rbf(sin)
-    q = apply_partial_rope(q, cos, sin)
-    k = apply_partial_rope(k, cos, sin)
+    return apply_partial_rope(q, cos, sin), apply_partial_rope(k, cos, sin), v, g
+
+
+def _gate(o, g, heads, head_dim):
+    if g is not None:
+        o = rbf(o * rbf(sigmoid(g)))
+    return o.reshape(o.shape[0], heads * head_dim)
+
+
+def gqa_mix_bf16(proj, k_cache, v_cache, pos, **cfg):
+    """``GQAAttention.mix`` over BF16 caches ``[ctx_max, Hkv, D]`` (updated in place) — the reference's layer."""
+    q, k, v, g = gqa_prepare(proj, pos, **cfg)
+    o = attention_step(q, k, v, k_cache, v_cache, pos, cfg["head_dim"] ** -0.5)
+    return _gate(o, g, cfg["heads"], cfg["head_dim"])
+
+
+def gqa_mix(proj, k_codes, k_scales, v_codes, v_scales, pos, **cfg):
+    """The same layer over the build's int8 cache (codes ``[ctx_max, Hkv, D]`` int8, scales ``[ctx_max, Hkv]`` f16,
+    updated in place): the fresh k/v are quantized into the cache at ``pos..pos+T`` and the step attends over the
+    dequantized cache, new tokens included."""
+    q, k, v, g = gqa_prepare(proj, pos, **cfg)
+    t = q.shape[0]
     kc, ks = kv_quantize(k)
     vc, vs = kv_quantize(v)
     k_codes[pos: pos + t], k_scales[pos: pos + t] = kc, ks
     v_codes[pos: pos + t], v_scales[pos: pos + t] = vc, vs
     n = pos + t
-    kd_full = kv_dequantize(k_codes[:n], k_scales[:n])
-    vd_full = kv_dequantize(v_codes[:n], v_scales[:n])
-    o = attention_step(q, kd_full[pos:n], vd_full[pos:n], kd_full.copy(), vd_full.copy(), pos, d ** -0.5)
-    if g is not None:
-        o = rbf(o * rbf(sigmoid(g)))
-    return o.reshape(t, heads * d)
+    kd = kv_dequantize(k_codes[:n], k_scales[:n])
+    vd = kv_dequantize(v_codes[:n], v_scales[:n])
+    o = attention_step(q, kd[pos:n], vd[pos:n], kd.copy(), vd.copy(), pos, cfg["head_dim"] ** -0.5)
+    return _gate(o, g, cfg["heads"], cfg["head_dim"])
 
 
 # ---- MoE -------------------------------------------------------------------------------------------------------------

@@ -1,0 +1,74 @@
+"""The C ABI without a GPU: the built ``libmi355.so`` loads and exports every entry point ``include/*.h`` declares;
+host-only entry points (pack sizes, launch plans, argument validation) behave; the ctypes signature table covers
+the header."""
+
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared():
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(mi_[a-z0-9_]+)\s*\(", text))
+    return names
+
+
+def test_header_declares_entry_points():
+    names = declared()
+    assert {"mi_gemv", "mi_dequant", "mi_malloc", "mi_graph_launch"} <= names
+
+
+def test_library_exports_every_declared_symbol():
+    from monolith_mi355.runtime import hip
+    lib = hip.load()
+    missing = [n for n in sorted(declared()) if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_ctypes_table_covers_header():
+    from monolith_mi355.runtime import hip
+    assert declared() == set(hip.SIGNATURES), declared() ^ set(hip.SIGNATURES)
+
+
+def test_pack_bytes_matches_host_pack():
+    from monolith_mi355.formats import pack as P
+    from monolith_mi355.runtime import hip
+    lib = hip.load()
+    for fmt, fid in hip.MI_FMT.items():
+        for n, k in ((37, 512), (17408, 5120), (5120, 17408)):
+            assert lib.mi_pack_bytes(fid, n, k) == P.pack_bytes(fmt, n, k)
+    assert lib.mi_pack_bytes(1, 16, 100) == 0            # K not a multiple of the chunk
+
+
+def _desc(hip, **kw):
+    base = dict(format=1, n=17408, k=5120, m=1, w=256, x=256, ldx=5120, y=256, ldy=17408)
+    base.update(kw)
+    return hip.MiGemvDesc(**base)
+
+
+@pytest.mark.parametrize("n,k,m", [(34816, 5120, 1), (5120, 17408, 1), (34816, 5120, 8), (5120, 17408, 8),
+                                   (4096, 4096, 1), (1024, 2048, 16), (16, 128, 3)])
+def test_gemv_plans_fit_the_hardware(n, k, m):
+    from monolith_mi355.runtime import hip
+    out = (C.c_int32 * 7)()
+    hip.call("mi_gemv_plan", C.byref(_desc(hip, n=n, k=k, m=m, ldx=k, ldy=n)), out)
+    rt, wk, kw, win, nwin, lds, wgs = list(out)
+    assert rt in (1, 2, 4) and 1 <= wk <= 8 and kw >= 1 and lds <= 64 * 1024 and wgs >= 1
+    assert (nwin == -1) == (m <= 2)                      # the VALU kernel for M <= 2, MFMA above
+    assert wk * kw >= k // 128
+
+
+def test_gemv_rejects_bad_descriptors_before_launch():
+    from monolith_mi355.runtime import hip
+    lib = hip.load()
+    bad = [dict(format=9), dict(k=100), dict(m=0), dict(m=17), dict(ldx=64), dict(w=0), dict(x=8),
+           dict(epilogue=1, residual=0), dict(epilogue=2, n=40, ldy=20), dict(ldy=16)]
+    for kw in bad:
+        assert lib.mi_gemv(C.byref(_desc(hip, **kw)), None) == 1, kw      # MI_E_INVALID, nothing enqueued
+        assert hip.last_error().startswith("mi_gemv")
