@@ -116,6 +116,32 @@ int mi_gemv_plan(const mi_gemv_desc* d, int32_t out[7]);
  * Format.dequantize, formats/base.py:52-81 / nvfp4.py:139-144 / int4_affine.py:85-91) */
 int mi_dequant(int32_t format, const void* w, const float* row_scale, int32_t n, int32_t k, float* out, void* stream);
 
+/* ---- Gated DeltaNet decode step (ops/gdn.py `gdn_mixer` + `gdn_norm`; nn/gdn.py:64-93;
+ *      kernels/common/gdn_mixer.metal:272-589; GdnParams kernels.py:686-720) ------------------------------------
+ * proj holds the in-projection output of T tokens: z | q | k | v | a | b at the given column offsets (a|b may sit
+ * in a second buffer). conv_in/conv_out: the causal-conv state [2·hk·dk + hv·dv][W-1] BF16, channel order q|k|v
+ * (distinct buffers: ping-pong them by step parity); rec_in/rec_out: the recurrent state [hv][dk][dv] FP32 (may
+ * alias). y [T][hv·dv] BF16 = the gated RMSNorm output. Built for dk = dv = 128, W = 4, T <= 16. */
+typedef struct mi_gdn_desc {
+  int32_t t, k_heads, v_heads, dk, dv, conv_width;
+  const uint16_t* proj;
+  int32_t ld_proj, z_off, q_off, k_off, v_off;
+  const uint16_t* ab;        /* NULL: a|b are in proj */
+  int32_t ld_ab, a_off, b_off;
+  const uint16_t* conv_w;    /* [conv_dim][W] BF16 */
+  const float* neg_exp_a;    /* [hv] −exp(A_log) (the pack's transform, packs/transforms.py:595-598) */
+  const float* dt_bias;      /* [hv] */
+  const float* norm_w;       /* [dv] BF16-valued gated-norm weight */
+  const uint16_t* conv_in;
+  uint16_t* conv_out;
+  const float* rec_in;
+  float* rec_out;
+  uint16_t* y;
+  int32_t ld_y;
+  float eps;
+} mi_gdn_desc;
+int mi_gdn_step(const mi_gdn_desc* d, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,194 @@
+// Gated DeltaNet decode step for T tokens (ops/gdn.py `gdn_mixer` + `gdn_norm`; nn/gdn.py:64-93; the kernel form
+// kernels/common/gdn_mixer.metal:272-589): causal conv1d + SiLU over q|k|v, L2-normalised q (/√dk) and k,
+// β = bf16(σ(b)), g = −exp(A_log)·softplus(a + dt_bias), the delta-rule recurrence on the FP32 state
+// S ← S·e^g; Δ = (v − Sᵀk)·β; S += k⊗Δ; o = Sᵀq, then the gated RMSNorm y = bf16(bf16(w·bf16(o·r))·silu(z)).
+//
+// MI355X design: one workgroup per value head, eight wave64s, wave w owning state columns [16w, 16w+16). Lane
+// (c = l%16, rg = l/16) holds S[32·rg .. 32·rg+32][16w + c] in 32 VGPRs for all T tokens; the Σ over dk is 32 FMAs
+// in-lane plus a 4-lane shuffle reduction, so the sequential token loop never touches memory or a barrier. The
+// conv for the head's q/k (its key head) and v channels is computed once per workgroup into LDS. Conv state is
+// read from one buffer and written to another (several value heads read the same key head's channels: the
+// reference solves the same race with two slots by step parity, gdn_mixer.metal:25-37); the recurrent state may be
+// updated in place (each workgroup owns its head).
+#include "mi_common.h"
+
+namespace {
+
+constexpr int DK = 128, DV = 128, CW = 4, TMAX = 16;
+constexpr int WAVES = 8, COLS = DV / WAVES;   // 16 columns per wave
+
+struct GdnArgs {
+  int t, hk, hv;
+  const uint16_t* proj; int ldp, z_off, q_off, k_off, v_off;
+  const uint16_t* ab; int ldab, a_off, b_off;
+  const uint16_t* conv_w;
+  const float* neg_exp_a;
+  const float* dt_bias;
+  const float* norm_w;
+  const uint16_t* conv_in;
+  uint16_t* conv_out;
+  const float* rec_in;
+  float* rec_out;
+  uint16_t* y; int ldy;
+  float eps;
+};
+
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + __expf(-x)); }
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
+__device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : log1pf(__expf(x)); }
+__device__ __forceinline__ float bf(const uint16_t* p, long long i) { return bf16_bits_to_f32(p[i]); }
+
+__global__ __launch_bounds__(512) void gdn_step(GdnArgs a) {
+  __shared__ float qs[TMAX][DK];   // conv → silu → L2-norm (q also /√dk)
+  __shared__ float ks[TMAX][DK];
+  __shared__ float vs[TMAX][DV];
+  __shared__ float os[TMAX][DV];   // BF16-valued read-out
+  __shared__ float beta_s[TMAX], eg_s[TMAX], rstd_s[TMAX];
+  const int h = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int T = a.t;
+  const int rep = a.hv / a.hk;
+  const int kh = h / rep;
+  const int key_dim = a.hk * DK;
+
+  // ---- the state slice into registers first (its latency hides under the conv) ---------------------------------
+  const int c = lane & 15, rg = lane >> 4;
+  const int col = wave * COLS + c;
+  float s[32];
+  const float* sin = a.rec_in + (long long)h * DK * DV;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) s[i] = sin[(long long)(32 * rg + i) * DV + col];
+
+  // ---- causal conv1d + SiLU over the head's q, k (key head kh) and v channels --------------------------------
+  if (tid < 2 * DK + DV) {
+    int ch;           // channel index in the conv input order q | k | v
+    int src_off;      // column of that channel in proj
+    float* dst;
+    bool writer;      // which workgroup writes this channel's new conv state
+    if (tid < DK) { ch = kh * DK + tid; src_off = a.q_off + kh * DK + tid; dst = &qs[0][tid]; writer = (h % rep) == 0; }
+    else if (tid < 2 * DK) { const int i = tid - DK; ch = key_dim + kh * DK + i; src_off = a.k_off + kh * DK + i; dst = &ks[0][i]; writer = (h % rep) == 0; }
+    else { const int i = tid - 2 * DK; ch = 2 * key_dim + h * DV + i; src_off = a.v_off + h * DV + i; dst = &vs[0][i]; writer = true; }
+    float w[CW], xs[CW - 1 + TMAX];
+#pragma unroll
+    for (int j = 0; j < CW; ++j) w[j] = bf(a.conv_w, (long long)ch * CW + j);
+#pragma unroll
+    for (int j = 0; j < CW - 1; ++j) xs[j] = bf(a.conv_in, (long long)ch * (CW - 1) + j);
+#pragma unroll
+    for (int t = 0; t < TMAX; ++t) xs[CW - 1 + t] = t < T ? bf(a.proj, (long long)t * a.ldp + src_off) : 0.0f;
+#pragma unroll
+    for (int t = 0; t < TMAX; ++t) {
+      if (t >= T) break;
+      float y = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CW; ++j) y = __fadd_rn(y, __fmul_rn(w[j], xs[j + t]));   // the oracle's y += w·x
+      dst[t * DK] = round_bf16(silu_f(round_bf16(y)));
+    }
+    if (writer) {                 // the last CW-1 inputs of [state | x]
+#pragma unroll
+      for (int j = 0; j < CW - 1; ++j) {
+        float v = xs[j];
+#pragma unroll
+        for (int t = 1; t <= TMAX; ++t) v = (t == T) ? xs[t + j] : v;
+        a.conv_out[(long long)ch * (CW - 1) + j] = f32_to_bf16_bits(v);
+      }
+    }
+  }
+  // gates per token: β = bf16(σ(b)), e^g with g = −exp(A_log)·softplus(a + dt_bias)
+  if (tid < T) {
+    const float bv = bf(a.ab, (long long)tid * a.ldab + a.b_off + h);
+    const float av = bf(a.ab, (long long)tid * a.ldab + a.a_off + h);
+    beta_s[tid] = round_bf16(sigmoid_f(bv));
+    eg_s[tid] = expf(a.neg_exp_a[h] * softplus_f(av + a.dt_bias[h]));
+  }
+  __syncthreads();
+
+  // ---- L2 norms: wave w takes tokens w, w + 8 ------------------------------------------------------------------
+  for (int t = wave; t < T; t += WAVES) {
+    const float q0 = qs[t][lane], q1 = qs[t][lane + 64];
+    const float k0 = ks[t][lane], k1 = ks[t][lane + 64];
+    const float rq = 1.0f / sqrtf(wave_sum(q0 * q0 + q1 * q1) + 1e-6f);
+    const float rk = 1.0f / sqrtf(wave_sum(k0 * k0 + k1 * k1) + 1e-6f);
+    qs[t][lane] = (q0 * rq) / sqrtf((float)DK);
+    qs[t][lane + 64] = (q1 * rq) / sqrtf((float)DK);
+    ks[t][lane] = k0 * rk;
+    ks[t][lane + 64] = k1 * rk;
+  }
+  __syncthreads();
+
+  // ---- the recurrence, token by token, state in registers --------------------------------------------------------
+  for (int t = 0; t < T; ++t) {
+    const float e = eg_s[t];
+    const float4* k4 = reinterpret_cast<const float4*>(&ks[t][32 * rg]);
+    const float4* q4 = reinterpret_cast<const float4*>(&qs[t][32 * rg]);
+    float kk[32], qq[32];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float4 kv = k4[i], qv = q4[i];
+      kk[4 * i] = kv.x; kk[4 * i + 1] = kv.y; kk[4 * i + 2] = kv.z; kk[4 * i + 3] = kv.w;
+      qq[4 * i] = qv.x; qq[4 * i + 1] = qv.y; qq[4 * i + 2] = qv.z; qq[4 * i + 3] = qv.w;
+    }
+    float m0 = 0.f, m1 = 0.f, m2 = 0.f, m3 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; i += 4) {
+      s[i] = __fmul_rn(s[i], e); s[i + 1] = __fmul_rn(s[i + 1], e);
+      s[i + 2] = __fmul_rn(s[i + 2], e); s[i + 3] = __fmul_rn(s[i + 3], e);
+      m0 = fmaf(s[i], kk[i], m0); m1 = fmaf(s[i + 1], kk[i + 1], m1);
+      m2 = fmaf(s[i + 2], kk[i + 2], m2); m3 = fmaf(s[i + 3], kk[i + 3], m3);
+    }
+    const float kv_mem = quad16_sum((m0 + m1) + (m2 + m3));
+    const float delta = (vs[t][col] - kv_mem) * beta_s[t];
+    float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; i += 4) {
+      s[i] = __fadd_rn(s[i], __fmul_rn(kk[i], delta));
+      s[i + 1] = __fadd_rn(s[i + 1], __fmul_rn(kk[i + 1], delta));
+      s[i + 2] = __fadd_rn(s[i + 2], __fmul_rn(kk[i + 2], delta));
+      s[i + 3] = __fadd_rn(s[i + 3], __fmul_rn(kk[i + 3], delta));
+      o0 = fmaf(s[i], qq[i], o0); o1 = fmaf(s[i + 1], qq[i + 1], o1);
+      o2 = fmaf(s[i + 2], qq[i + 2], o2); o3 = fmaf(s[i + 3], qq[i + 3], o3);
+    }
+    const float o = quad16_sum((o0 + o1) + (o2 + o3));
+    if (rg == 0) os[t][col] = round_bf16(o);
+  }
+  float* sout = a.rec_out + (long long)h * DK * DV;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) sout[(long long)(32 * rg + i) * DV + col] = s[i];
+  __syncthreads();
+
+  // ---- gated RMSNorm over the head's dv outputs of each token ------------------------------------------------------
+  for (int t = wave; t < T; t += WAVES) {
+    const float v0 = os[t][lane], v1 = os[t][lane + 64];
+    const float ms = wave_sum(v0 * v0 + v1 * v1) / (float)DV;
+    if (lane == 0) rstd_s[t] = 1.0f / sqrtf(ms + a.eps);
+  }
+  __syncthreads();
+  for (int idx = tid; idx < T * DV; idx += blockDim.x) {
+    const int t = idx / DV, cc = idx - t * DV;
+    const float n = round_bf16(os[t][cc] * rstd_s[t]);
+    const float nw = round_bf16(round_bf16(a.norm_w[cc]) * n);
+    const float z = bf(a.proj, (long long)t * a.ldp + a.z_off + h * DV + cc);
+    a.y[(long long)t * a.ldy + h * DV + cc] = f32_to_bf16_bits(nw * silu_f(z));
+  }
+}
+
+}  // namespace
+
+extern "C" int mi_gdn_step(const mi_gdn_desc* d, void* stream) {
+  MI_REQUIRE(d, "mi_gdn_step: null descriptor");
+  MI_REQUIRE(d->t >= 1 && d->t <= TMAX, "mi_gdn_step: t=%d must be in 1..%d", d->t, TMAX);
+  MI_REQUIRE(d->dk == DK && d->dv == DV && d->conv_width == CW, "mi_gdn_step: built for dk=dv=%d, conv width %d", DK, CW);
+  MI_REQUIRE(d->k_heads > 0 && d->v_heads > 0 && d->v_heads % d->k_heads == 0, "mi_gdn_step: v_heads must be a multiple of k_heads");
+  MI_REQUIRE(d->proj && d->conv_w && d->neg_exp_a && d->dt_bias && d->norm_w && d->conv_in && d->conv_out && d->rec_in &&
+             d->rec_out && d->y, "mi_gdn_step: null pointer");
+  MI_REQUIRE(d->conv_in != d->conv_out, "mi_gdn_step: conv_in and conv_out must be distinct buffers (shared key heads)");
+  GdnArgs a{};
+  a.t = d->t; a.hk = d->k_heads; a.hv = d->v_heads;
+  a.proj = d->proj; a.ldp = d->ld_proj; a.z_off = d->z_off; a.q_off = d->q_off; a.k_off = d->k_off; a.v_off = d->v_off;
+  a.ab = d->ab ? d->ab : d->proj; a.ldab = d->ab ? d->ld_ab : d->ld_proj; a.a_off = d->a_off; a.b_off = d->b_off;
+  a.conv_w = d->conv_w; a.neg_exp_a = d->neg_exp_a; a.dt_bias = d->dt_bias; a.norm_w = d->norm_w;
+  a.conv_in = d->conv_in; a.conv_out = d->conv_out; a.rec_in = d->rec_in; a.rec_out = d->rec_out;
+  a.y = d->y; a.ldy = d->ld_y; a.eps = d->eps;
+  hipLaunchKernelGGL(gdn_step, dim3(d->v_heads), dim3(512), 0, static_cast<hipStream_t>(stream), a);
+  MI_TRY_HIP(hipGetLastError(), "gdn_step launch");
+  return MI_OK;
+}

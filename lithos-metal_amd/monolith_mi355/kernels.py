@@ -62,11 +62,11 @@ def upload(specs, device="cuda", row_scales=None) -> PackedWeight:
     return PackedWeight(fmt, n, k, len(specs), data, rs)
 
 
-def _bf16_2d(t, name):
+def _bf16_2d(t, name, aligned=True):
     torch = _torch()
     if t.dtype != torch.bfloat16 or t.dim() != 2 or t.stride(1) != 1:
         raise ValueError(f"{name}: expected a row-major 2-D bfloat16 tensor, got {t.dtype} {tuple(t.shape)}")
-    if t.data_ptr() % 16 or t.stride(0) % 8:
+    if aligned and (t.data_ptr() % 16 or t.stride(0) % 8):
         raise ValueError(f"{name}: needs 16-byte alignment and a row stride multiple of 8")
 
 
@@ -114,4 +114,42 @@ def dequant(w: PackedWeight, expert: int = 0, stream=None):
     base = hip.ptr(w.data) + expert * nb
     rs = 0 if w.row_scale is None else hip.ptr(w.row_scale) + 4 * expert * w.n_pad
     hip.call("mi_dequant", hip.MI_FMT[w.format], base, rs, w.n, w.k, hip.ptr(out), hip.stream_handle(stream))
+    return out
+
+
+def gdn_step(proj, conv_in, conv_out, rec_in, rec_out, *, conv_w, neg_exp_a, dt_bias, norm_w, k_heads, v_heads,
+             dk=128, dv=128, conv_width=4, eps=1e-6, ab=None, offsets=None, out=None, stream=None):
+    """``gdn_mixer`` + ``gdn_norm`` (``ops/gdn.py:1-24``) for ``proj [T, N1]`` bf16 in part order
+    ``z | q | k | v | a | b`` (``nn/gdn.py:48-52``) unless ``offsets`` (z, q, k, v, a, b) says otherwise.
+    Conv state ``[conv_dim, W-1]`` bf16 is read from ``conv_in`` and written to ``conv_out`` (distinct); the FP32
+    recurrent state ``[hv, dk, dv]`` is read from ``rec_in`` and written to ``rec_out`` (may be the same tensor).
+    Returns ``[T, hv·dv]`` bf16."""
+    torch = _torch()
+    _bf16_2d(proj, "gdn proj", aligned=False)
+    t = proj.shape[0]
+    kd, vd = k_heads * dk, v_heads * dv
+    conv_dim = 2 * kd + vd
+    if offsets is None:
+        offsets = (0, vd, vd + kd, vd + 2 * kd, vd + conv_dim, vd + conv_dim + v_heads)
+    z_off, q_off, k_off, v_off, a_off, b_off = offsets
+    for name, tns, shape, dt in (("conv_in", conv_in, (conv_dim, conv_width - 1), torch.bfloat16),
+                                 ("conv_out", conv_out, (conv_dim, conv_width - 1), torch.bfloat16),
+                                 ("rec_in", rec_in, (v_heads, dk, dv), torch.float32),
+                                 ("rec_out", rec_out, (v_heads, dk, dv), torch.float32),
+                                 ("conv_w", conv_w, (conv_dim, conv_width), torch.bfloat16),
+                                 ("neg_exp_a", neg_exp_a, (v_heads,), torch.float32),
+                                 ("dt_bias", dt_bias, (v_heads,), torch.float32), ("norm_w", norm_w, (dv,), torch.float32)):
+        if tuple(tns.shape) != shape or tns.dtype != dt or not tns.is_contiguous():
+            raise ValueError(f"gdn_step: {name} must be a contiguous {dt} {shape}, got {tns.dtype} {tuple(tns.shape)}")
+    if max(offsets[:4]) + dk > proj.shape[1] and ab is None:
+        raise ValueError("gdn_step: proj is narrower than the z|q|k|v|a|b offsets")
+    if out is None:
+        out = torch.empty((t, vd), dtype=torch.bfloat16, device=proj.device)
+    d = hip.MiGdnDesc(t=t, k_heads=k_heads, v_heads=v_heads, dk=dk, dv=dv, conv_width=conv_width, proj=hip.ptr(proj),
+                      ld_proj=proj.stride(0), z_off=z_off, q_off=q_off, k_off=k_off, v_off=v_off, ab=hip.ptr(ab),
+                      ld_ab=ab.stride(0) if ab is not None else 0, a_off=a_off, b_off=b_off, conv_w=hip.ptr(conv_w),
+                      neg_exp_a=hip.ptr(neg_exp_a), dt_bias=hip.ptr(dt_bias), norm_w=hip.ptr(norm_w),
+                      conv_in=hip.ptr(conv_in), conv_out=hip.ptr(conv_out), rec_in=hip.ptr(rec_in),
+                      rec_out=hip.ptr(rec_out), y=hip.ptr(out), ld_y=out.stride(0), eps=eps)
+    hip.call("mi_gdn_step", C.byref(d), hip.stream_handle(stream))
     return out

@@ -36,6 +36,16 @@ class MiGemvDesc(C.Structure):
                 ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t), ("out_f32", C.c_int32)]
 
 
+class MiGdnDesc(C.Structure):
+    _fields_ = [("t", C.c_int32), ("k_heads", C.c_int32), ("v_heads", C.c_int32), ("dk", C.c_int32), ("dv", C.c_int32),
+                ("conv_width", C.c_int32), ("proj", C.c_void_p), ("ld_proj", C.c_int32), ("z_off", C.c_int32),
+                ("q_off", C.c_int32), ("k_off", C.c_int32), ("v_off", C.c_int32), ("ab", C.c_void_p),
+                ("ld_ab", C.c_int32), ("a_off", C.c_int32), ("b_off", C.c_int32), ("conv_w", C.c_void_p),
+                ("neg_exp_a", C.c_void_p), ("dt_bias", C.c_void_p), ("norm_w", C.c_void_p), ("conv_in", C.c_void_p),
+                ("conv_out", C.c_void_p), ("rec_in", C.c_void_p), ("rec_out", C.c_void_p), ("y", C.c_void_p),
+                ("ld_y", C.c_int32), ("eps", C.c_float)]
+
+
 # name -> (restype, argtypes); every int-returning entry point is error-checked
 _VP, _I32, _SZ, _F = C.c_void_p, C.c_int32, C.c_size_t, C.c_float
 SIGNATURES = {
@@ -67,6 +77,7 @@ SIGNATURES = {
     "mi_gemv": (C.c_int, [C.POINTER(MiGemvDesc), _VP]),
     "mi_gemv_plan": (C.c_int, [C.POINTER(MiGemvDesc), C.POINTER(_I32)]),
     "mi_dequant": (C.c_int, [_I32, _VP, _VP, _I32, _I32, _VP, _VP]),
+    "mi_gdn_step": (C.c_int, [C.POINTER(MiGdnDesc), _VP]),
 }
 
 

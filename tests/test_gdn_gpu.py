@@ -1,0 +1,104 @@
+"""The HIP Gated DeltaNet decode step against the oracle's ``GatedDeltaNet.mix`` (pinned to the reference by
+golden vectors), with the reference's own bars (``tests/kernels/test_gdn_mixer.py:161-175``): conv state exact,
+recurrent state within 8 FP32 ULP of its largest value, output within ``ok_rounded`` — at the 27B geometry
+(hk 16, hv 48, dk = dv = 128) and smaller ones, T = 1 / 4 / 8, two consecutive steps (continuation, conv state
+ping-pong), a|b in a second buffer, the BASELINE gates (A_log = dt_bias = 0), bit-identical repeats."""
+
+import numpy as np
+import pytest
+
+from helpers import from_dev_bf16, to_dev_bf16
+from oracle import nn as ON
+from oracle.fp import rbf
+from oracle.gates import check_against_oracle
+
+pytestmark = pytest.mark.gpu
+EPS = 1e-6
+
+
+def _params(rng, hk, hv, zero_gates=False):
+    conv_dim = 2 * hk * 128 + hv * 128
+    return dict(conv_w=rbf(rng.standard_normal((conv_dim, 4)) * 0.3),
+                a_log=np.zeros(hv, np.float32) if zero_gates else rbf(rng.uniform(-2, 1, hv)),
+                dt_bias=np.zeros(hv, np.float32) if zero_gates else rbf(rng.standard_normal(hv)),
+                norm_w=rbf(1 + rng.standard_normal(128) * 0.2))
+
+
+def _dev_params(torch, p):
+    return dict(conv_w=to_dev_bf16(torch, p["conv_w"]),
+                neg_exp_a=torch.from_numpy((-np.exp(p["a_log"])).astype(np.float32)).cuda(),
+                dt_bias=torch.from_numpy(p["dt_bias"].astype(np.float32)).cuda(),
+                norm_w=torch.from_numpy(p["norm_w"].astype(np.float32)).cuda())
+
+
+def _check(got, ref, conv_got, conv_ref, rec_got, rec_ref):
+    assert np.array_equal(conv_got, conv_ref), np.argwhere(conv_got != conv_ref)[:4]
+    scale = float(np.abs(rec_ref).max())
+    err = float(np.abs(rec_got - rec_ref).max())
+    assert err <= 8 * 2.0 ** -23 * scale, (err, scale)
+    chk = check_against_oracle(got, ref)
+    assert chk.ok_rounded(), chk
+
+
+@pytest.mark.parametrize("hk,hv", [(16, 48), (4, 4), (2, 6)])
+@pytest.mark.parametrize("t", [1, 4, 8])
+def test_gdn_step_matches_oracle(torch_gpu, hk, hv, t):
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    rng = np.random.default_rng(hk * 100 + hv + t)
+    p = _params(rng, hk, hv)
+    dp = _dev_params(torch, p)
+    conv_dim = 2 * hk * 128 + hv * 128
+    n1 = hv * 128 + conv_dim + 2 * hv
+    conv = rbf(rng.standard_normal((conv_dim, 3)) * 0.5)
+    rec = (rng.standard_normal((hv, 128, 128)) * 0.1).astype(np.float32)
+    bufs = [to_dev_bf16(torch, conv), torch.empty(conv_dim, 3, dtype=torch.bfloat16, device="cuda")]
+    rec_d = torch.from_numpy(rec).cuda()
+    for step in range(2):                                     # a step on the filled state, then its continuation
+        proj = rbf(rng.standard_normal((t, n1)))
+        ref, conv, rec = ON.gdn_mix(proj, conv, rec, k_heads=hk, v_heads=hv, dk=128, dv=128, eps=EPS, **p)
+        y = kernels.gdn_step(to_dev_bf16(torch, proj), bufs[step & 1], bufs[(step + 1) & 1], rec_d, rec_d,
+                             k_heads=hk, v_heads=hv, eps=EPS, **dp)
+        torch.cuda.synchronize()
+        _check(from_dev_bf16(y), ref, from_dev_bf16(bufs[(step + 1) & 1]), conv, rec_d.cpu().numpy(), rec)
+
+
+def test_gdn_separate_ab_and_baseline_gates(torch_gpu):
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    rng = np.random.default_rng(11)
+    hk, hv, t = 16, 48, 8
+    p = _params(rng, hk, hv, zero_gates=True)                 # C4: g = −softplus(a), A_log = dt_bias = 0
+    dp = _dev_params(torch, p)
+    conv_dim = 2 * hk * 128 + hv * 128
+    conv = rbf(rng.standard_normal((conv_dim, 3)) * 0.5)
+    rec = (rng.standard_normal((hv, 128, 128)) * 0.1).astype(np.float32)
+    proj = rbf(rng.standard_normal((t, hv * 128 + conv_dim + 2 * hv)))
+    ref, conv_ref, rec_ref = ON.gdn_mix(proj, conv, rec, k_heads=hk, v_heads=hv, dk=128, dv=128, eps=EPS, **p)
+    main = proj[:, : hv * 128 + conv_dim]
+    ab = np.ascontiguousarray(proj[:, hv * 128 + conv_dim:])
+    vd, kd = hv * 128, hk * 128
+    cin, cout = to_dev_bf16(torch, conv), torch.empty(conv_dim, 3, dtype=torch.bfloat16, device="cuda")
+    rin = torch.from_numpy(rec).cuda()
+    rout = torch.empty_like(rin)
+    y = kernels.gdn_step(to_dev_bf16(torch, main), cin, cout, rin, rout, k_heads=hk, v_heads=hv, eps=EPS,
+                         ab=to_dev_bf16(torch, ab), offsets=(0, vd, vd + kd, vd + 2 * kd, 0, hv), **dp)
+    torch.cuda.synchronize()
+    _check(from_dev_bf16(y), ref, from_dev_bf16(cout), conv_ref, rout.cpu().numpy(), rec_ref)
+    assert torch.equal(rin, torch.from_numpy(rec).cuda())     # the input state is untouched when out ≠ in
+    y2 = kernels.gdn_step(to_dev_bf16(torch, main), cin, cout, rin, torch.empty_like(rin), k_heads=hk, v_heads=hv,
+                          eps=EPS, ab=to_dev_bf16(torch, ab), offsets=(0, vd, vd + kd, vd + 2 * kd, 0, hv), **dp)
+    assert torch.equal(y, y2)                                 # bit-identical repeat
+
+
+def test_gdn_rejects_aliased_conv_state(torch_gpu):
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    from monolith_mi355.runtime.hip import MiError
+    rng = np.random.default_rng(0)
+    p = _dev_params(torch, _params(rng, 2, 2))
+    conv = torch.zeros(2 * 256 + 256, 3, dtype=torch.bfloat16, device="cuda")
+    rec = torch.zeros(2, 128, 128, device="cuda")
+    proj = torch.zeros(1, 256 + 768 + 4, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(MiError):
+        kernels.gdn_step(proj, conv, conv, rec, rec, k_heads=2, v_heads=2, **p)
