@@ -142,6 +142,34 @@ typedef struct mi_gdn_desc {
 } mi_gdn_desc;
 int mi_gdn_step(const mi_gdn_desc* d, void* stream);
 
+/* ---- GQA decode attention over an int8 KV cache (ops/attention.py `gqa_decode` + `gqa_merge`;
+ *      nn/attention.py:215-243; kernels/common/gqa_decode.metal:32-302; GqaParams kernels.py:604-611) ----------
+ * proj [T][heads·(gate ? 2 : 1)·D + 2·kv·D] BF16 in checkpoint column order (q|gate per head, then k, v). The new
+ * tokens are normed (qk_norm), roped (cos/sin [ctx_max][rotary_dim] BF16, cat(freqs, freqs)), quantized and
+ * appended at pos..pos+T. Cache (this backend's layout): k_codes [kv][ctx_max][D] int8, v_codes [kv][D][ctx_max]
+ * int8, k_scales / v_scales [kv][ctx_max] f16 bits (scale = f16(absmax/127) per token and KV head).
+ * y [T][heads·D] BF16 (× bf16(σ(gate)) when gate). D = 128, T <= 16, heads/kv·T <= 64 rows per KV head. */
+typedef struct mi_gqa_desc {
+  int32_t t, heads, kv_heads, head_dim, rotary_dim, pos, ctx_max, gate, qk_norm;
+  const uint16_t* proj;
+  int32_t ld_proj;
+  const uint16_t* rope_cos;
+  const uint16_t* rope_sin;
+  const float* q_norm;       /* (1 + w) [D], or NULL */
+  const float* k_norm;
+  float eps, scaling;
+  int8_t* k_codes;
+  uint16_t* k_scales;
+  int8_t* v_codes;
+  uint16_t* v_scales;
+  uint16_t* y;
+  int32_t ld_y;
+  void* workspace;           /* split partials; NULL = the library's own */
+  size_t workspace_bytes;
+} mi_gqa_desc;
+size_t mi_gqa_workspace_bytes(const mi_gqa_desc* d);
+int mi_gqa_decode(const mi_gqa_desc* d, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

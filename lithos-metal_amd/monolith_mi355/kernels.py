@@ -153,3 +153,77 @@ def gdn_step(proj, conv_in, conv_out, rec_in, rec_out, *, conv_w, neg_exp_a, dt_
                       rec_out=hip.ptr(rec_out), y=hip.ptr(out), ld_y=out.stride(0), eps=eps)
     hip.call("mi_gdn_step", C.byref(d), hip.stream_handle(stream))
     return out
+
+
+# ---- GQA decode attention over the int8 KV cache ---------------------------------------------------------------------
+def rope_tables(theta: float, rotary_dim: int, ctx: int, device="cuda"):
+    """BF16 ``cos``/``sin`` ``[ctx, rotary_dim]`` for positions ``0..ctx-1``, ``cat(freqs, freqs)``, computed in FP32
+    the way the reference builds them per step (``nn/oracle.py:49-55``, ``nn/attention.py:230-233``)."""
+    torch = _torch()
+    inv = 1.0 / (torch.tensor(float(theta), dtype=torch.float32) **
+                 (torch.arange(0, rotary_dim, 2, dtype=torch.float32) / rotary_dim))
+    freqs = torch.arange(ctx, dtype=torch.float32)[:, None] * inv[None, :]
+    emb = torch.cat([freqs, freqs], dim=-1)
+    return emb.cos().to(torch.bfloat16).to(device), emb.sin().to(torch.bfloat16).to(device)
+
+
+class KVCache:
+    """One attention layer's int8 KV cache in this backend's layout (the reference keeps BF16 ``[ctx_max, Hkv, D]``,
+    ``nn/attention.py:207-209``): ``k_codes [kv, ctx_max, D]`` int8, ``v_codes [kv, D, ctx_max]`` int8 (transposed,
+    so a P·V B tile is 8 consecutive keys of one dim), ``k_scales`` / ``v_scales [kv, ctx_max]`` float16 —
+    ``scale = f16(absmax / 127)`` per token and KV head. 288 GB of HBM holds a 262 144-token context for all 16
+    attention layers of the 27B model at 4 KV heads × 128 dims many times over."""
+
+    def __init__(self, kv_heads: int, ctx_max: int, head_dim: int = 128, device="cuda"):
+        torch = _torch()
+        if ctx_max % 8:
+            raise ValueError("KVCache: ctx_max must be a multiple of 8")
+        self.kv_heads, self.ctx_max, self.head_dim = kv_heads, ctx_max, head_dim
+        self.k_codes = torch.zeros((kv_heads, ctx_max, head_dim), dtype=torch.int8, device=device)
+        self.v_codes = torch.zeros((kv_heads, head_dim, ctx_max), dtype=torch.int8, device=device)
+        self.k_scales = torch.zeros((kv_heads, ctx_max), dtype=torch.float16, device=device)
+        self.v_scales = torch.zeros((kv_heads, ctx_max), dtype=torch.float16, device=device)
+
+    @property
+    def nbytes(self) -> int:
+        return sum(int(t.numel() * t.element_size()) for t in (self.k_codes, self.v_codes, self.k_scales, self.v_scales))
+
+
+def gqa_decode(proj, cache: KVCache, pos: int, *, heads: int, rope_cos, rope_sin, gate: bool = True,
+               q_norm=None, k_norm=None, eps: float = 1e-6, scaling: Optional[float] = None, out=None, stream=None,
+               workspace=None):
+    """``gqa_decode`` + ``gqa_merge`` (``ops/attention.py``; ``GQAAttention.mix``, ``nn/attention.py:215-243``) for
+    ``proj [T, N1]`` bf16 (``q|gate`` per head, then ``k``, ``v``): q/k norm (``q_norm``/``k_norm`` = the (1 + w)
+    float32 weights, both or neither), partial RoPE from the BF16 tables ``[ctx_max, rotary_dim]``, the new k/v
+    quantized into ``cache`` at ``pos..pos+T``, attention over the cache, × σ(gate). Returns ``[T, heads·D]`` bf16."""
+    torch = _torch()
+    _bf16_2d(proj, "gqa proj", aligned=False)
+    t = proj.shape[0]
+    d, kv = cache.head_dim, cache.kv_heads
+    q_cols = heads * (2 if gate else 1) * d
+    if proj.shape[1] < q_cols + 2 * kv * d:
+        raise ValueError(f"gqa_decode: proj has {proj.shape[1]} columns, needs {q_cols + 2 * kv * d}")
+    if (q_norm is None) != (k_norm is None):
+        raise ValueError("gqa_decode: q_norm and k_norm go together")
+    for name, tb in (("rope_cos", rope_cos), ("rope_sin", rope_sin)):
+        if tb.dtype != torch.bfloat16 or tb.dim() != 2 or tb.shape[0] < cache.ctx_max or not tb.is_contiguous():
+            raise ValueError(f"gqa_decode: {name} must be a contiguous bf16 [ctx_max, rotary_dim] table")
+    for name, w in (("q_norm", q_norm), ("k_norm", k_norm)):
+        if w is not None and (w.dtype != torch.float32 or w.numel() != d):
+            raise ValueError(f"gqa_decode: {name} must be float32 [{d}]")
+    if out is None:
+        out = torch.empty((t, heads * d), dtype=torch.bfloat16, device=proj.device)
+    _bf16_2d(out, "gqa out", aligned=False)
+    if out.shape[0] < t or out.shape[1] < heads * d:
+        raise ValueError("gqa_decode: out too small")
+    desc = hip.MiGqaDesc(t=t, heads=heads, kv_heads=kv, head_dim=d, rotary_dim=rope_cos.shape[1], pos=pos,
+                         ctx_max=cache.ctx_max, gate=int(gate), qk_norm=int(q_norm is not None), proj=hip.ptr(proj),
+                         ld_proj=proj.stride(0), rope_cos=hip.ptr(rope_cos), rope_sin=hip.ptr(rope_sin),
+                         q_norm=hip.ptr(q_norm), k_norm=hip.ptr(k_norm), eps=eps,
+                         scaling=d ** -0.5 if scaling is None else scaling, k_codes=hip.ptr(cache.k_codes),
+                         k_scales=hip.ptr(cache.k_scales), v_codes=hip.ptr(cache.v_codes),
+                         v_scales=hip.ptr(cache.v_scales), y=hip.ptr(out), ld_y=out.stride(0),
+                         workspace=hip.ptr(workspace),
+                         workspace_bytes=0 if workspace is None else workspace.numel() * workspace.element_size())
+    hip.call("mi_gqa_decode", C.byref(desc), hip.stream_handle(stream))
+    return out

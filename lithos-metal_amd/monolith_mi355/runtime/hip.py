@@ -46,6 +46,16 @@ class MiGdnDesc(C.Structure):
                 ("ld_y", C.c_int32), ("eps", C.c_float)]
 
 
+class MiGqaDesc(C.Structure):
+    _fields_ = [("t", C.c_int32), ("heads", C.c_int32), ("kv_heads", C.c_int32), ("head_dim", C.c_int32),
+                ("rotary_dim", C.c_int32), ("pos", C.c_int32), ("ctx_max", C.c_int32), ("gate", C.c_int32),
+                ("qk_norm", C.c_int32), ("proj", C.c_void_p), ("ld_proj", C.c_int32), ("rope_cos", C.c_void_p),
+                ("rope_sin", C.c_void_p), ("q_norm", C.c_void_p), ("k_norm", C.c_void_p), ("eps", C.c_float),
+                ("scaling", C.c_float), ("k_codes", C.c_void_p), ("k_scales", C.c_void_p), ("v_codes", C.c_void_p),
+                ("v_scales", C.c_void_p), ("y", C.c_void_p), ("ld_y", C.c_int32), ("workspace", C.c_void_p),
+                ("workspace_bytes", C.c_size_t)]
+
+
 # name -> (restype, argtypes); every int-returning entry point is error-checked
 _VP, _I32, _SZ, _F = C.c_void_p, C.c_int32, C.c_size_t, C.c_float
 SIGNATURES = {
@@ -78,6 +88,8 @@ SIGNATURES = {
     "mi_gemv_plan": (C.c_int, [C.POINTER(MiGemvDesc), C.POINTER(_I32)]),
     "mi_dequant": (C.c_int, [_I32, _VP, _VP, _I32, _I32, _VP, _VP]),
     "mi_gdn_step": (C.c_int, [C.POINTER(MiGdnDesc), _VP]),
+    "mi_gqa_workspace_bytes": (_SZ, [C.POINTER(MiGqaDesc)]),
+    "mi_gqa_decode": (C.c_int, [C.POINTER(MiGqaDesc), _VP]),
 }
 
 

@@ -211,9 +211,11 @@ def kv_dequantize(codes, scales):
 
 
 def gqa_prepare(proj, pos, *, heads, kv_heads, head_dim, rotary_dim, theta, eps, gate=True, qk_norm=False,
-                q_norm=None, k_norm=None):
+                q_norm=None, k_norm=None, tables=None):
     """The first half of ``GQAAttention.mix`` (``nn/attention.py:222-238``): split ``proj [T, N1]`` (checkpoint
     column order: ``q|gate`` per head, then ``k``, ``v``), optional q/k RMSNorm(1 + w), partial RoPE with BF16 tables.
+    ``tables`` = BF16 ``(cos, sin) [ctx, rotary_dim]`` to use instead of numpy's (torch's FP32 ``cos``/``sin`` of
+    large arguments differ from numpy's in the last bit, which flips a few BF16 roundings).
     Returns ``(q [T,H,D], k [T,Hkv,D], v [T,Hkv,D], gate [T,H,D] or None)``."""
     proj = np.asarray(proj, F32)
     t = proj.shape[0]
@@ -229,8 +231,11 @@ def gqa_prepare(proj, pos, *, heads, kv_heads, head_dim, rotary_dim, theta, eps,
     if qk_norm:
         q = rms_norm(q, q_norm, eps)
         k = rms_norm(k, k_norm, eps)
-    cos, sin = rope_tables(theta, rotary_dim, np.arange(pos, pos + t))
-    cos, sin = rbf(cos), rbf(sin)
+    if tables is None:
+        cos, sin = rope_tables(theta, rotary_dim, np.arange(pos, pos + t))
+        cos, sin = rbf(cos), rbf(sin)
+    else:
+        cos, sin = (np.asarray(tb, F32)[pos: pos + t] for tb in tables)
     return apply_partial_rope(q, cos, sin), apply_partial_rope(k, cos, sin), v, g
 
 

@@ -1,0 +1,176 @@
+"""The HIP GQA decode attention over the int8 KV cache against the oracle's ``gqa_mix`` (the reference's
+``GQAAttention.mix``, ``nn/attention.py:215-243``, with the build's int8 codec; pinned by golden vectors from the
+reference's torch layer): the BASELINE geometry (24 heads, 4 KV heads, D = 128, RoPE θ = 1e6), contexts up to 32K,
+M = 1 and M = 8 (causal inside the verify block), gate on/off, q/k norm on/off, two consecutive steps.
+
+Bars: the new cache rows (codes and f16 scales) bit-exact without q/k norm (with it, a mean taken in another order
+may flip a BF16 rounding: ≥ 99.9 % exact and never more than one code step); the rest of the cache untouched;
+outputs with cosine > 0.99999 and max |error| within 2 BF16 ULP of the output's largest magnitude — the reference's
+own kernel bar (``tests/kernels/test_gqa_decode.py:293-294``) — and so within 1e-2 of it (the 1e-2 relative bar taken
+norm-wise, as the reference's layer test does, ``:347``): the online softmax rounds P to BF16 per chunk before
+normalisation and the oracle after, so an output formed by cancellation (two keys, opposite values) carries an
+absolute, not relative, error of that size. Both sides use the product's BF16 RoPE tables (torch's FP32
+``cos``/``sin``, as the reference builds them); the tables are checked against numpy's in
+``test_rope_tables_match_oracle``."""
+
+import numpy as np
+import pytest
+
+from helpers import from_dev_bf16, to_dev_bf16
+from oracle import nn as ON
+from oracle.fp import rbf
+from oracle.gates import bf16_ulp_of
+
+EPS = 1e-6
+H, KV, D = 24, 4, 128
+
+
+def _cfg(rot, gate, qk_norm, rng):
+    return dict(heads=H, kv_heads=KV, head_dim=D, rotary_dim=rot, theta=1e6, eps=EPS, gate=gate, qk_norm=qk_norm,
+                q_norm=rbf(rng.standard_normal(D) * 0.1), k_norm=rbf(rng.standard_normal(D) * 0.1))
+
+
+def _filled_cache(rng, ctx, pos):
+    """Oracle-layout int8 cache ``[ctx, kv, D]`` holding ``pos`` quantized N(0, 1) tokens."""
+    kc = np.zeros((ctx, KV, D), np.int8)
+    vc = np.zeros((ctx, KV, D), np.int8)
+    ks = np.zeros((ctx, KV), np.float16)
+    vs = np.zeros((ctx, KV), np.float16)
+    if pos:
+        kc[:pos], ks[:pos] = ON.kv_quantize(rbf(rng.standard_normal((pos, KV, D))))
+        vc[:pos], vs[:pos] = ON.kv_quantize(rbf(rng.standard_normal((pos, KV, D))))
+    return kc, ks, vc, vs
+
+
+def _upload(torch, cache, kc, ks, vc, vs):
+    cache.k_codes.copy_(torch.from_numpy(np.ascontiguousarray(kc.transpose(1, 0, 2))))
+    cache.v_codes.copy_(torch.from_numpy(np.ascontiguousarray(vc.transpose(1, 2, 0))))
+    cache.k_scales.copy_(torch.from_numpy(np.ascontiguousarray(ks.T)))
+    cache.v_scales.copy_(torch.from_numpy(np.ascontiguousarray(vs.T)))
+
+
+def _download(cache):
+    return (cache.k_codes.cpu().numpy().transpose(1, 0, 2), cache.k_scales.cpu().numpy().T,
+            cache.v_codes.cpu().numpy().transpose(2, 0, 1), cache.v_scales.cpu().numpy().T)
+
+
+def _check_out(y, ref):
+    assert np.isfinite(y).all()
+    g, r = y.astype(np.float64).ravel(), ref.astype(np.float64).ravel()
+    cos = float(g @ r / (np.linalg.norm(g) * np.linalg.norm(r) + 1e-30))
+    scale = float(np.abs(r).max())
+    assert cos > 0.99999 and np.abs(g - r).max() <= 2 * bf16_ulp_of(scale), (cos, np.abs(g - r).max(), scale)
+
+
+def _check_cache(got, want, pos, t, exact):
+    for name, g, w in zip(("k_codes", "k_scales", "v_codes", "v_scales"), got, want):
+        assert np.array_equal(g[:pos], w[:pos]), f"{name}: cached rows changed"
+        assert np.array_equal(g[pos + t:], w[pos + t:]), f"{name}: rows past the step changed"
+        gn, wn = g[pos: pos + t], w[pos: pos + t]
+        if exact or name.startswith("v"):
+            assert np.array_equal(gn, wn), (name, np.argwhere(gn != wn)[:4])
+        elif name == "k_codes":
+            assert np.abs(gn.astype(int) - wn.astype(int)).max() <= 1 and np.mean(gn == wn) >= 0.999
+        else:
+            assert np.all(np.abs(gn.astype(np.float32) - wn.astype(np.float32)) <= 2 ** -9 * np.abs(wn.astype(np.float32)))
+
+
+def _run(torch, rng, ctx, pos, t, rot=64, gate=True, qk_norm=False, steps=1):
+    from monolith_mi355 import kernels
+    cfg = _cfg(rot, gate, qk_norm, rng)
+    cos, sin = kernels.rope_tables(1e6, rot, ctx)
+    cfg["tables"] = (from_dev_bf16(cos), from_dev_bf16(sin))
+    kc, ks, vc, vs = _filled_cache(rng, ctx, pos)
+    cache = kernels.KVCache(KV, ctx)
+    _upload(torch, cache, kc, ks, vc, vs)
+    qn = torch.from_numpy((1 + cfg["q_norm"]).astype(np.float32)).cuda() if qk_norm else None
+    kn = torch.from_numpy((1 + cfg["k_norm"]).astype(np.float32)).cuda() if qk_norm else None
+    n1 = H * (2 if gate else 1) * D + 2 * KV * D
+    for _ in range(steps):
+        proj = rbf(rng.standard_normal((t, n1)))
+        ref = ON.gqa_mix(proj, kc, ks, vc, vs, pos, **cfg)
+        y = kernels.gqa_decode(to_dev_bf16(torch, proj), cache, pos, heads=H, rope_cos=cos, rope_sin=sin, gate=gate,
+                               q_norm=qn, k_norm=kn, eps=EPS)
+        torch.cuda.synchronize()
+        _check_cache(_download(cache), (kc, ks, vc, vs), pos, t, exact=not qk_norm)
+        _check_out(from_dev_bf16(y), ref)
+        pos += t
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("ctx,pos", [(4096, 4000), (16384, 16000), (32768, 32752)])
+@pytest.mark.parametrize("t", [1, 8])
+def test_gqa_decode_baseline_contexts(torch_gpu, ctx, pos, t):
+    print(f"gqa ctx={ctx} pos={pos} t={t}", flush=True)
+    _run(torch_gpu, np.random.default_rng(ctx + t), ctx, pos, t)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("pos", [0, 1, 63, 64, 65, 200])
+@pytest.mark.parametrize("t", [1, 3, 8])
+def test_gqa_decode_short_and_ragged(torch_gpu, pos, t):
+    print(f"gqa short pos={pos} t={t}", flush=True)
+    _run(torch_gpu, np.random.default_rng(pos * 10 + t), 1024, pos, t)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("gate,qk_norm,rot", [(False, False, 64), (True, True, 64), (False, True, 128),
+                                              (True, False, 32), (True, False, 0)])
+def test_gqa_decode_variants(torch_gpu, gate, qk_norm, rot):
+    print(f"gqa variant gate={gate} qk_norm={qk_norm} rot={rot}", flush=True)
+    _run(torch_gpu, np.random.default_rng(rot + 2 * gate + qk_norm), 2048, 1500, 8, rot=rot, gate=gate,
+         qk_norm=qk_norm)
+
+
+@pytest.mark.gpu
+def test_gqa_decode_consecutive_steps(torch_gpu):
+    print("gqa consecutive", flush=True)
+    _run(torch_gpu, np.random.default_rng(7), 1024, 50, 8, steps=3)
+
+
+@pytest.mark.gpu
+def test_gqa_decode_deterministic(torch_gpu):
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    rng = np.random.default_rng(9)
+    cos, sin = kernels.rope_tables(1e6, 64, 8192)
+    kc, ks, vc, vs = _filled_cache(rng, 8192, 8000)
+    proj = to_dev_bf16(torch, rbf(rng.standard_normal((8, H * 2 * D + 2 * KV * D))))
+    outs = []
+    for _ in range(2):
+        cache = kernels.KVCache(KV, 8192)
+        _upload(torch, cache, kc, ks, vc, vs)
+        outs.append(kernels.gqa_decode(proj, cache, 8000, heads=H, rope_cos=cos, rope_sin=sin).cpu())
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+
+
+def test_rope_tables_match_oracle():
+    """The product's BF16 tables against numpy's FP32 ``cos``/``sin``: at most one BF16 step apart, rarely."""
+    torch = pytest.importorskip("torch")
+    from monolith_mi355 import kernels
+    for rot in (32, 64, 128):
+        c, s = kernels.rope_tables(1e6, rot, 32768, device="cpu")
+        oc, os_ = ON.rope_tables(1e6, rot, np.arange(32768))
+        for got, want in ((c, oc), (s, os_)):
+            got = got.float().numpy()
+            want = rbf(want)
+            assert np.abs(got - want).max() <= 2 ** -7
+            assert np.mean(got != want) < 0.01
+    c, s = kernels.rope_tables(1e6, 64, 8, device="cpu")
+    assert torch.all(c[0] == 1) and torch.all(s[0] == 0)
+
+
+def test_gqa_rejects_bad_descriptors():
+    import ctypes as C
+    from monolith_mi355.runtime import hip
+    lib = hip.load()
+    base = dict(t=1, heads=24, kv_heads=4, head_dim=128, rotary_dim=64, pos=10, ctx_max=1024, gate=1, proj=256,
+                ld_proj=7168, rope_cos=256, rope_sin=256, k_codes=256, k_scales=256, v_codes=256, v_scales=256,
+                y=256, ld_y=3072, eps=1e-6, scaling=0.088)
+    bad = [dict(head_dim=64), dict(t=0), dict(t=17), dict(heads=25), dict(t=11), dict(pos=1024),
+           dict(ctx_max=1020, pos=10), dict(rotary_dim=129), dict(proj=0), dict(qk_norm=1), dict(k_codes=8)]
+    for kw in bad:
+        d = hip.MiGqaDesc(**{**base, **kw})
+        assert lib.mi_gqa_decode(C.byref(d), None) == 1, kw
+        assert hip.last_error().startswith("mi_gqa_decode")
+    assert lib.mi_gqa_workspace_bytes(C.byref(hip.MiGqaDesc(**base))) > 0
