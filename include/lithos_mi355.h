@@ -146,8 +146,9 @@ int mi_gdn_step(const mi_gdn_desc* d, void* stream);
  *      nn/attention.py:215-243; kernels/common/gqa_decode.metal:32-302; GqaParams kernels.py:604-611) ----------
  * proj [T][heads·(gate ? 2 : 1)·D + 2·kv·D] BF16 in checkpoint column order (q|gate per head, then k, v). The new
  * tokens are normed (qk_norm), roped (cos/sin [ctx_max][rotary_dim] BF16, cat(freqs, freqs)), quantized and
- * appended at pos..pos+T. Cache (this backend's layout): k_codes [kv][ctx_max][D] int8, v_codes [kv][D][ctx_max]
- * int8, k_scales / v_scales [kv][ctx_max] f16 bits (scale = f16(absmax/127) per token and KV head).
+ * appended at pos..pos+T. Cache (this backend's layout): k_codes [kv][ctx_max][D] int8, v_codes
+ * [kv][ctx_max/64][D][64] int8 (transposed inside 64-key blocks), k_scales / v_scales [kv][ctx_max] f16 bits
+ * (scale = f16(absmax/127) per token and KV head); ctx_max a multiple of 64.
  * y [T][heads·D] BF16 (× bf16(σ(gate)) when gate). D = 128, T <= 16, heads/kv·T <= 64 rows per KV head. */
 typedef struct mi_gqa_desc {
   int32_t t, heads, kv_heads, head_dim, rotary_dim, pos, ctx_max, gate, qk_norm;

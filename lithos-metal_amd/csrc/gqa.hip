@@ -7,18 +7,22 @@
 // dequantized cache, causal inside the step; softmax in FP32 with P rounded to BF16; P·V in FP32 → BF16;
 // × bf16(σ(gate)).
 //
-// MI355X design:
-//  * Cache layout (this backend's): K codes [kv][ctx][D] int8, V codes transposed [kv][D][ctx] int8, scales
-//    [kv][ctx] f16 — each operand an MFMA B tile read with 16- or 8-byte loads.
-//  * gqa_decode: one wave per (KV head, split of the keys); the rep·T query rows of the KV head are A tiles of
-//    v_mfma_f32_16x16x32_f16 (Q prescaled by a power of two into F16 range); int8 codes become exact F16 with
-//    an XOR / byte-permute / packed subtract. QKᵀ and P·V run on MFMA, the softmax online per 64-key chunk; the
-//    V scale folds into P (with a per-chunk power of two so it stays in F16 range). Each split writes
-//    (O, m, l) partials. The split holding the new tokens also quantizes and appends them.
-//  * gqa_merge: one wave per (head, token) folds the splits in order and applies the gate — deterministic.
+// MI355X design, three launches:
+//  * Cache layout (this backend's): K codes [kv][ctx][D] int8; V codes [kv][ctx/64][D][64] int8 — transposed inside
+//    blocks of 64 keys, so a P·V B tile is 8 consecutive keys of one dim and a 64-key chunk is 8 KB contiguous, like
+//    K's; scales [kv][ctx] f16. Every chunk is two contiguous 8 KB streams read with 16- and 8-byte loads.
+//  * gqa_prep: one wave per (head or KV head, token), all in parallel: q rows normed, roped and prescaled by a power
+//    of two into F16 (the MFMA A operand, in the workspace); k/v quantized and appended to the cache.
+//  * gqa_decode: a workgroup of 4 waves per (KV head, key range); each wave streams its share of the range in
+//    64-key chunks with the next chunk's codes prefetched into registers. The rep·T query rows of the KV head are A
+//    tiles of v_mfma_f32_16x16x32_f16; int8 codes become exact F16 with an XOR / byte-permute / packed subtract;
+//    QKᵀ and P·V run on MFMA, the softmax online; the V scale folds into P (with a per-chunk power of two so it
+//    stays in F16 range). The 4 waves fold their (O, m, l) in LDS; the workgroup writes one partial.
+//  * gqa_merge: one wave per (head, token) folds the partials in key order and applies the gate — deterministic.
 #include "mi_common.h"
 
 #include <algorithm>
+#include <cstdlib>
 #include <mutex>
 #include <vector>
 
@@ -29,13 +33,15 @@ constexpr int CHUNK = 64;       // keys per inner step
 constexpr int TMAX = 16;
 
 struct GqaArgs {
-  int t, heads, kv, rot, pos, ctx, gate, qk_norm, rep, rows, n_splits, split_len;
+  int t, heads, kv, rot, pos, ctx, gate, qk_norm, rep, rows;
+  int n_groups, group_len;                      // decode workgroups per KV head, keys per workgroup
   const uint16_t* proj; int ldp;
   const uint16_t* cosb; const uint16_t* sinb;   // [ctx][rot] BF16
   const float* q_norm; const float* k_norm;     // (1 + w), [D]
   float eps, scaling;
   int8_t* kc; uint16_t* ks; int8_t* vc; uint16_t* vs;
-  float* part_o; float* part_ml;                // [kv][split][rows][D], [kv][split][rows][2]
+  f16_t* qf; float* qsc;                        // [kv][64][D] prescaled F16 query rows, [kv][64] their 2^p
+  float* part_o; float* part_ml;                // [kv][group][rows][D], [kv][group][rows][2]
   uint16_t* y; int ldy;
 };
 
@@ -108,243 +114,338 @@ __device__ void quant_store(const float* src, int8_t* codes, long long stride, u
   if (lane == 0) *scale_out = __builtin_bit_cast(uint16_t, sh);
 }
 
-template <int RT>
-__global__ __launch_bounds__(64) void gqa_decode(GqaArgs a) {
-  // the KV head's query rows (BF16 values, row = t·rep + r) while the A tiles are built; then P'' of the chunk,
-  // the P·V A-operand source
-  __shared__ __attribute__((aligned(16))) float qbuf[RT * 16 * D];
+constexpr int MAXROWS = 64;     // query rows per KV head (rep·T)
+constexpr int NW = 4;           // waves per decode workgroup
+
+__device__ __forceinline__ float pow2f(int e) { return __uint_as_float((uint32_t)(127 + e) << 23); }
+
+__device__ __forceinline__ int prescale_exp(float mx) {   // 2^-p·mx in [2^14, 2^15): F16 keeps 11 bits of each value
+  if (mx == 0.0f) return 0;
+  const int p = (int)((__float_as_uint(mx) >> 23) & 0xFF) - 127 - 14;
+  return min(max(p, -100), 100);
+}
+
+// Position of key k (0..63) inside its V block: the P·V MFMA sums over keys in any order, so the order is the one
+// in which the score tile already holds them — lane (kg, m16) holds keys 16·kt + 4·kg + i of score tile kt, and as
+// the B operand of k-block ks its 8 values are tiles 2·ks, 2·ks + 1 — and those 8 keys sit together.
+__device__ __forceinline__ int vblock_pos(int k) { return (k >> 5) * 32 + ((k & 15) >> 2) * 8 + ((k >> 4) & 1) * 4 + (k & 3); }
+
+__global__ __launch_bounds__(64) void gqa_prep(GqaArgs a) {
   __shared__ float tmp[D];
-  float (*qv)[D] = reinterpret_cast<float (*)[D]>(qbuf);
-  f16_t (*pl)[CHUNK + 8] = reinterpret_cast<f16_t (*)[CHUNK + 8]>(qbuf);
-  const int lane = threadIdx.x;
-  const int j = blockIdx.y;                    // KV head
-  const int sp = blockIdx.x;                   // split
-  const int n_keys = a.pos + a.t;
-  const int k_begin = sp * a.split_len;
-  const bool last = sp == a.n_splits - 1;     // splits cut the cached keys; the last also takes the new tokens
-  const int k_end = last ? n_keys : k_begin + a.split_len;
+  const int lane = threadIdx.x, x = blockIdx.x, t = blockIdx.y;
   const int q_cols = a.gate ? 2 * D : D;
-  const int k_col0 = a.heads * q_cols + j * D;
-  const int v_col0 = a.heads * q_cols + a.kv * D + j * D;
-
-  // ---- the new tokens' k / v: quantized into the cache by the split that holds them ---------------------------
-  if (last) {
-    for (int t = 0; t < a.t; ++t) {
-      const uint16_t* row = a.proj + (long long)t * a.ldp;
-      const int p = a.pos + t;
-      prep_vec(a, row + k_col0, a.k_norm, t, tmp, lane);
-      quant_store(tmp, a.kc + ((long long)j * a.ctx + p) * D, 1, a.ks + (long long)j * a.ctx + p, lane);
-      tmp[lane] = bfv(row + v_col0, lane);
-      tmp[lane + 64] = bfv(row + v_col0, lane + 64);
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      quant_store(tmp, a.vc + (long long)j * D * a.ctx + p, a.ctx, a.vs + (long long)j * a.ctx + p, lane);
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-    }
-    __threadfence_block();                     // the appended rows are read back below by this wave
+  const uint16_t* row = a.proj + (long long)t * a.ldp;
+  if (x < a.heads) {
+    const int j = x / a.rep, qrow = t * a.rep + (x - j * a.rep);
+    prep_vec(a, row + x * q_cols, a.q_norm, t, tmp, lane);
+    const float x0 = tmp[lane], x1 = tmp[lane + 64];
+    const int p = prescale_exp(wave_max(fmaxf(fabsf(x0), fabsf(x1))));
+    const float inv = pow2f(-p);
+    f16_t* dst = a.qf + ((long long)j * MAXROWS + qrow) * D;
+    dst[lane] = (f16_t)(x0 * inv);
+    dst[lane + 64] = (f16_t)(x1 * inv);
+    if (lane == 0) a.qsc[j * MAXROWS + qrow] = pow2f(p);
+  } else {
+    const int j = x - a.heads, p = a.pos + t;
+    prep_vec(a, row + a.heads * q_cols + j * D, a.k_norm, t, tmp, lane);
+    quant_store(tmp, a.kc + ((long long)j * a.ctx + p) * D, 1, a.ks + (long long)j * a.ctx + p, lane);
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    const uint16_t* v = row + a.heads * q_cols + a.kv * D + j * D;
+    tmp[lane] = bfv(v, lane);
+    tmp[lane + 64] = bfv(v, lane + 64);
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    quant_store(tmp, a.vc + ((long long)j * a.ctx + (p & ~(CHUNK - 1))) * D + vblock_pos(p & (CHUNK - 1)), CHUNK,
+                a.vs + (long long)j * a.ctx + p, lane);
   }
+}
 
-  // ---- the query rows: norm + RoPE, then per-row power-of-two prescale into F16 A tiles -----------------------
-  for (int row = 0; row < a.rows; ++row) {
-    const int t = row / a.rep, h = j * a.rep + (row - t * a.rep);
-    prep_vec(a, a.proj + (long long)t * a.ldp + h * q_cols, a.q_norm, t, qv[row], lane);
+// a chunk's K side as this lane holds it: codes of key 16·kt + m16, dims 32·kg + [0, 32); scales of keys
+// 16·kt + 4·kg + [0, 4)
+struct KChunk {
+  uint4 k[4][2];
+  uint2 ksc[4], vsc[4];
+};
+
+__device__ __forceinline__ void load_k(const int8_t* kbase, const uint16_t* ksb, const uint16_t* vsb, int k0, int m16,
+                                       int kg, KChunk& c) {
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt) {
+    const int8_t* kp = kbase + (long long)(k0 + kt * 16 + m16) * D + 32 * kg;
+    c.k[kt][0] = *reinterpret_cast<const uint4*>(kp);
+    c.k[kt][1] = *reinterpret_cast<const uint4*>(kp + 16);
+    c.ksc[kt] = *reinterpret_cast<const uint2*>(ksb + k0 + kt * 16 + 4 * kg);
+    c.vsc[kt] = *reinterpret_cast<const uint2*>(vsb + k0 + kt * 16 + 4 * kg);
   }
-  for (int row = a.rows; row < RT * 16; ++row) { qv[row][lane] = 0.0f; qv[row][lane + 64] = 0.0f; }
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  __builtin_amdgcn_wave_barrier();
+}
+
+__device__ __forceinline__ float f16_lo(uint32_t u) { return (float)__builtin_bit_cast(f16_t, (uint16_t)(u & 0xFFFF)); }
+__device__ __forceinline__ float f16_hi(uint32_t u) { return (float)__builtin_bit_cast(f16_t, (uint16_t)(u >> 16)); }
+
+// The decode workgroup: NW waves over one key range of KV head j. Everything is computed transposed so that a
+// lane owns one query row (row = 16·rt + m16): Sᵀ = K·Qᵀ (A = K codes as F16, B = the prescaled F16 query rows),
+// softmax over the lane's 16 keys plus the lanes l ^ 16, l ^ 32, l ^ 48 of the same row, and Oᵀ += Vᵀ·Pᵀ with
+// Pᵀ straight from the score registers (no LDS round trip) — every per-row quantity is lane-local.
+template <int RT>
+__global__ __launch_bounds__(64 * NW, RT == 1 ? 2 : 1) void gqa_decode(GqaArgs a) {   // RT = 1: 2 waves / SIMD
+  __shared__ __attribute__((aligned(16))) float red[RT * 16][D + 4];   // the workgroup's O, row-major
+  __shared__ float mls[NW][RT * 16][2];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int j = blockIdx.y, g = blockIdx.x;
+  const int n_keys = a.pos + a.t;
+  const int kb = g * a.group_len;
+  const int ke = g == a.n_groups - 1 ? n_keys : kb + a.group_len;   // the last group also takes the new tokens
+  const int nch = (ke - kb + CHUNK - 1) / CHUNK;
+  const int k_begin = kb + (w * nch / NW) * CHUNK;
+  const int k_end = min(ke, kb + ((w + 1) * nch / NW) * CHUNK);
   const int m16 = lane & 15, kg = lane >> 4;
-  f16x8 qa[RT][4];
-  float qscale[RT];                            // 2^p of this lane's A row (row = 16·rt + m16)
+
+  const int8_t* kbase = a.kc + (long long)j * a.ctx * D;
+  const int8_t* vbase = a.vc + (long long)j * a.ctx * D;
+  const uint16_t* ksb = a.ks + (long long)j * a.ctx;
+  const uint16_t* vsb = a.vs + (long long)j * a.ctx;
+  KChunk cur, nxt;
+  if (k_begin < k_end) load_k(kbase, ksb, vsb, k_begin, m16, kg, cur);   // chunks lie inside the cache: ctx % 64 == 0
+
+  // the query rows as B tiles (k-permuted: lane holds dims 32·kg + 8·s + i of row 16·rt + m16), zero past rows
+  f16x8 qb[RT][4];
+  float rsc[RT];                                        // the lane's row: 2^p of its prescale
+  int qlim[RT];                                         // the lane's row: last key it may see (causal)
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
-    const float* qr = qv[rt * 16 + m16];
-    float mx = 0.0f;
-    for (int i = 0; i < D; ++i) mx = fmaxf(mx, fabsf(qr[i]));
-    const int p = mx == 0.0f ? 0 : (int)((__float_as_uint(mx) >> 23) & 0xFF) - 127 - 14;
-    const float inv = __uint_as_float((uint32_t)(127 - p) << 23);
-    qscale[rt] = __uint_as_float((uint32_t)(127 + p) << 23);
+    const int row = rt * 16 + m16;
+    const bool ok = row < a.rows;
+    const f16_t* src = a.qf + ((long long)j * MAXROWS + (ok ? row : 0)) * D + 32 * kg;
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
+    for (int s = 0; s < 4; ++s) {
+      const f16x8 v = *reinterpret_cast<const f16x8*>(src + 8 * s);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) qa[rt][s][i] = (f16_t)(qr[32 * kg + 8 * s + i] * inv);
+      for (int i = 0; i < 8; ++i) qb[rt][s][i] = ok ? v[i] : (f16_t)0.0f;
+    }
+    rsc[rt] = ok ? a.qsc[j * MAXROWS + row] : 1.0f;
+    qlim[rt] = ok ? a.pos + row / a.rep : n_keys;       // rows past `rows` hold q = 0: finite, never written
   }
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");   // qv reads done before pl (same LDS) is written
-  __builtin_amdgcn_wave_barrier();
 
-  // ---- online softmax over the split's keys, 64 per chunk ---------------------------------------------------
-  f32x4 o[RT][8];
-  float m_run[RT][4], l_run[RT][4];
+  f32x4 o[RT][8];                                       // o[rt][ct][i] = O[row 16·rt + m16][dim 16·ct + 4·kg + i]
+  float m_run[RT], l_run[RT];                           // l_run: this lane's share (its 16 keys per chunk)
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
 #pragma unroll
     for (int ct = 0; ct < 8; ++ct) o[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) { m_run[rt][i] = -INFINITY; l_run[rt][i] = 0.0f; }
+    m_run[rt] = -INFINITY;
+    l_run[rt] = 0.0f;
   }
-  int pv_cur = 0;                              // O is held in units of 2^pv_cur
-  const int8_t* kbase = a.kc + (long long)j * a.ctx * D;
-  const int8_t* vbase = a.vc + (long long)j * D * a.ctx;
-  const uint16_t* ksb = a.ks + (long long)j * a.ctx;
-  const uint16_t* vsb = a.vs + (long long)j * a.ctx;
-  // the row of this lane's D element i (rows 4·kg + i of each row tile) and its token
+  int pv_cur = 0;                                       // O is held in units of 2^pv_cur
+
   for (int k0 = k_begin; k0 < k_end; k0 += CHUNK) {
-    // scores: S[row][key] for 4 key tiles of 16
-    f32x4 sacc[RT][4];
-    float kscale[4], vscale[4];
-    bool kvalid[4];
+    // this chunk's V codes, then the next chunk's K side (the last iteration reloads its own, in bounds)
+    uint2 vr[2][8];
+    const int8_t* vp = vbase + (long long)k0 * D + 8 * kg;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int ct = 0; ct < 8; ++ct) vr[ks][ct] = *reinterpret_cast<const uint2*>(vp + (ct * 16 + m16) * CHUNK + ks * 32);
+    load_k(kbase, ksb, vsb, k0 + CHUNK < k_end ? k0 + CHUNK : k0, m16, kg, nxt);
+
+    const bool full = k0 + CHUNK <= k_end && k0 + CHUNK - 1 <= a.pos;   // every key valid and visible to every row
+    float ksc[4][4], vsc[4][4];
+    float vmax = 0.0f;
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
-      const int key = k0 + kt * 16 + m16;
-      kvalid[kt] = key < k_end;
-      const int kk = kvalid[kt] ? key : k_begin;
-      const uint4 c0 = *reinterpret_cast<const uint4*>(kbase + (long long)kk * D + 32 * kg);
-      const uint4 c1 = *reinterpret_cast<const uint4*>(kbase + (long long)kk * D + 32 * kg + 16);
-      kscale[kt] = (float)__builtin_bit_cast(f16_t, ksb[kk]);
-      vscale[kt] = kvalid[kt] ? (float)__builtin_bit_cast(f16_t, vsb[kk]) : 0.0f;
-      const f16x8 b0 = i8x8_to_f16(c0.x, c0.y), b1 = i8x8_to_f16(c0.z, c0.w);
-      const f16x8 b2 = i8x8_to_f16(c1.x, c1.y), b3 = i8x8_to_f16(c1.z, c1.w);
+      const uint2 kq = cur.ksc[kt], vq = cur.vsc[kt];
+      ksc[kt][0] = f16_lo(kq.x); ksc[kt][1] = f16_hi(kq.x); ksc[kt][2] = f16_lo(kq.y); ksc[kt][3] = f16_hi(kq.y);
+      vsc[kt][0] = f16_lo(vq.x); vsc[kt][1] = f16_hi(vq.x); vsc[kt][2] = f16_lo(vq.y); vsc[kt][3] = f16_hi(vq.y);
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[rt][0], b0, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[rt][1], b1, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[rt][2], b2, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[rt][3], b3, acc, 0, 0, 0);
-        sacc[rt][kt] = acc;
+      for (int i = 0; i < 4; ++i) {
+        if (!full && k0 + kt * 16 + 4 * kg + i >= k_end) vsc[kt][i] = 0.0f;
+        vmax = fmaxf(vmax, vsc[kt][i]);
       }
     }
-    // the chunk's V-scale prescale 2^-pv (keeps P'' = p·v_scale·2^-pv in F16 range)
-    float vmax = fmaxf(fmaxf(vscale[0], vscale[1]), fmaxf(vscale[2], vscale[3]));
+    vmax = max_xor32(max_xor16(vmax));
+    // the chunk's V-scale prescale 2^-pv keeps P'' = p·v_scale·2^-pv in F16 range
+    const int pv = vmax == 0.0f ? pv_cur : prescale_exp(vmax);
+    const float pv_inv = pow2f(-pv), resc = pow2f(pv_cur - pv);
 #pragma unroll
-    for (int off = 1; off < 16; off <<= 1) vmax = fmaxf(vmax, __shfl_xor(vmax, off, 64));
-    const int pv = vmax == 0.0f ? pv_cur : (int)((__float_as_uint(vmax) >> 23) & 0xFF) - 127 - 14;
-    const float pv_inv = __uint_as_float((uint32_t)(127 - pv) << 23);
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vsc[kt][i] *= pv_inv;
+
+    f16x8 kb4[4][4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      kb4[kt][0] = i8x8_to_f16(cur.k[kt][0].x, cur.k[kt][0].y);
+      kb4[kt][1] = i8x8_to_f16(cur.k[kt][0].z, cur.k[kt][0].w);
+      kb4[kt][2] = i8x8_to_f16(cur.k[kt][1].x, cur.k[kt][1].y);
+      kb4[kt][3] = i8x8_to_f16(cur.k[kt][1].z, cur.k[kt][1].w);
+    }
+    f16x8 pb[RT][2];                                    // Pᵀ B tiles: element i of k-block ks = key tile 2·ks + i/4
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      // the row scales of this lane's D rows (4·kg + i): 2^p of the query row, via the A-row owner lanes
-      float rs[4];
+      float sc[4][4];
+      float mx = -INFINITY;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) rs[i] = __shfl(qscale[rt], (lane & 48) | (4 * kg + i), 64);
-      float mc[4];
+      for (int kt = 0; kt < 4; ++kt) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = rt * 16 + 4 * kg + i;
-        const int t = row / a.rep;
-        const int qpos = a.pos + t;
-        float mx = -INFINITY;
+        for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb4[kt][s], qb[rt][s], acc, 0, 0, 0);
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-          const int key = k0 + kt * 16 + m16;
-          float sc = round_bf16(sacc[rt][kt][i] * rs[i] * kscale[kt]);
-          sc = round_bf16(sc * a.scaling);
-          const bool ok = kvalid[kt] && key <= qpos && row < a.rows;
-          sacc[rt][kt][i] = ok ? sc : -INFINITY;
-          mx = fmaxf(mx, sacc[rt][kt][i]);
+        for (int i = 0; i < 4; ++i) {
+          float v = round_bf16(round_bf16(acc[i] * (rsc[rt] * ksc[kt][i])) * a.scaling);
+          if (!full) {
+            const int key = k0 + kt * 16 + 4 * kg + i;
+            v = (key < k_end && key <= qlim[rt]) ? v : -INFINITY;
+          }
+          sc[kt][i] = v;
+          mx = fmaxf(mx, v);
         }
-#pragma unroll
-        for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-        mc[i] = mx;
       }
-      float alpha[4];
+      mx = max_xor32(max_xor16(mx));
+      const float mnew = fmaxf(m_run[rt], mx);
+      const float alpha = m_run[rt] == -INFINITY ? 0.0f : __expf(m_run[rt] - mnew);
+      float psum = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float mnew = fmaxf(m_run[rt][i], mc[i]);
-        const float ex = (m_run[rt][i] == -INFINITY) ? 0.0f : __expf(m_run[rt][i] - mnew);
-        alpha[i] = (mnew == -INFINITY) ? 1.0f : ex;
-        float psum = 0.0f;
+      for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-          const float s = sacc[rt][kt][i];
-          const float p = (s == -INFINITY) ? 0.0f : __expf(s - mnew);
+        for (int i = 0; i < 4; ++i) {
+          const float p = sc[kt][i] == -INFINITY ? 0.0f : __expf(sc[kt][i] - mnew);
           psum += p;
-          const float pp = round_bf16(p) * vscale[kt] * pv_inv;
-          pl[rt * 16 + 4 * kg + i][kt * 16 + m16] = (f16_t)pp;
+          pb[rt][kt >> 1][(kt & 1) * 4 + i] = (f16_t)(round_bf16(p) * vsc[kt][i]);
         }
-#pragma unroll
-        for (int off = 1; off < 16; off <<= 1) psum += __shfl_xor(psum, off, 64);
-        l_run[rt][i] = l_run[rt][i] * alpha[i] + psum;
-        m_run[rt][i] = mnew;
-      }
-      const float resc = __uint_as_float((uint32_t)(127 + pv_cur - pv) << 23);   // 2^(pv_cur - pv)
+      l_run[rt] = l_run[rt] * alpha + psum;
+      m_run[rt] = mnew;
+      const float f = alpha * resc;
 #pragma unroll
       for (int ct = 0; ct < 8; ++ct)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o[rt][ct][i] *= alpha[i] * resc;
+        for (int i = 0; i < 4; ++i) o[rt][ct][i] *= f;
     }
     pv_cur = pv;
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    // O += P''·V
+    // Oᵀ += Vᵀ·Pᵀ
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      f16x8 pa[RT];
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) pa[rt] = *reinterpret_cast<const f16x8*>(&pl[rt * 16 + m16][ks * 32 + 8 * kg]);
-      const int key8 = k0 + ks * 32 + 8 * kg;
-      const int keyc = key8 + 8 <= a.ctx ? key8 : 0;
+    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
       for (int ct = 0; ct < 8; ++ct) {
-        const uint2 c = *reinterpret_cast<const uint2*>(vbase + (long long)(ct * 16 + m16) * a.ctx + keyc);
-        const f16x8 bv = i8x8_to_f16(c.x, c.y);
+        const f16x8 va = i8x8_to_f16(vr[ks][ct].x, vr[ks][ct].y);
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) o[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[rt], bv, o[rt][ct], 0, 0, 0);
+        for (int rt = 0; rt < RT; ++rt) o[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[rt][ks], o[rt][ct], 0, 0, 0);
       }
-    }
-    __builtin_amdgcn_wave_barrier();
+    cur = nxt;
   }
 
-  // ---- partials: O (in units of 2^pv_cur → scaled back), m, l -------------------------------------------------
-  const float unscale = __uint_as_float((uint32_t)(127 + pv_cur) << 23);
-  const long long base = ((long long)j * a.n_splits + sp) * a.rows;
+  // ---- fold the workgroup's waves: common max, O summed in LDS in wave order, one partial per workgroup ---------
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = rt * 16 + 4 * kg + i;
-      if (row >= a.rows) continue;
-#pragma unroll
-      for (int ct = 0; ct < 8; ++ct) a.part_o[(base + row) * D + ct * 16 + m16] = o[rt][ct][i] * unscale;
-      if (m16 == 0) {
-        a.part_ml[(base + row) * 2] = m_run[rt][i];
-        a.part_ml[(base + row) * 2 + 1] = l_run[rt][i];
-      }
+  for (int rt = 0; rt < RT; ++rt) {
+    const float l = quad16_sum(l_run[rt]);
+    if (kg == 0) {
+      mls[w][rt * 16 + m16][0] = m_run[rt];
+      mls[w][rt * 16 + m16][1] = l;
     }
+  }
+  __syncthreads();
+  const float unscale = pow2f(pv_cur);
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const int row = rt * 16 + m16;
+    float M = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, mls[ww][row][0]);
+    const float f = m_run[rt] == -INFINITY ? 0.0f : __expf(m_run[rt] - M) * unscale;
+#pragma unroll
+    for (int ct = 0; ct < 8; ++ct)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[rt][ct][i] *= f;
+  }
+  for (int ww = 0; ww < NW; ++ww) {
+    if (w == ww) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < 8; ++ct) {
+          f32x4* dst = reinterpret_cast<f32x4*>(&red[rt * 16 + m16][ct * 16 + 4 * kg]);
+          *dst = ww == 0 ? o[rt][ct] : *dst + o[rt][ct];
+        }
+    }
+    __syncthreads();
+  }
+  const long long base = ((long long)j * a.n_groups + g) * a.rows;
+  for (int idx = threadIdx.x; idx < a.rows * D; idx += 64 * NW) a.part_o[base * D + idx] = red[idx / D][idx % D];
+  for (int row = threadIdx.x; row < a.rows; row += 64 * NW) {
+    float M = -INFINITY, L = 0.0f;
+    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, mls[ww][row][0]);
+    for (int ww = 0; ww < NW; ++ww)
+      if (mls[ww][row][0] != -INFINITY) L += __expf(mls[ww][row][0] - M) * mls[ww][row][1];
+    a.part_ml[(base + row) * 2] = M;
+    a.part_ml[(base + row) * 2 + 1] = L;
+  }
 }
 
-// one wave per (query head, token): fold the splits in order, normalize, BF16, × bf16(σ(gate))
-__global__ __launch_bounds__(64) void gqa_merge(GqaArgs a) {
-  const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+// one workgroup of MW waves per (query head, token): wave w folds partials w, w + MW, … (all its loads in flight
+// at once), then wave 0 adds the MW sums in wave order — deterministic; normalize, BF16, × bf16(σ(gate))
+constexpr int MW = 8;
+__global__ __launch_bounds__(64 * MW) void gqa_merge(GqaArgs a) {
+  __shared__ float red[MW][D + 1];
+  const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int j = h / a.rep;
   const int row = t * a.rep + (h - j * a.rep);
+  const long long b0 = (long long)j * a.n_groups * a.rows + row;      // partial g at b0 + g·rows
   float M = -INFINITY;
-  for (int s = 0; s < a.n_splits; ++s) M = fmaxf(M, a.part_ml[(((long long)j * a.n_splits + s) * a.rows + row) * 2]);
+  for (int g = lane; g < a.n_groups; g += 64) M = fmaxf(M, a.part_ml[(b0 + (long long)g * a.rows) * 2]);
+  M = wave_max(M);
   float l = 0.0f, o0 = 0.0f, o1 = 0.0f;
-  for (int s = 0; s < a.n_splits; ++s) {
-    const long long b = ((long long)j * a.n_splits + s) * a.rows + row;
-    const float m = a.part_ml[b * 2];
-    if (m == -INFINITY) continue;
-    const float w = __expf(m - M);
-    l += w * a.part_ml[b * 2 + 1];
-    o0 += w * a.part_o[b * D + lane];
-    o1 += w * a.part_o[b * D + lane + 64];
+#pragma unroll 8
+  for (int g = w; g < a.n_groups; g += MW) {
+    const long long b = b0 + (long long)g * a.rows;
+    const float m = a.part_ml[b * 2], lg = a.part_ml[b * 2 + 1];
+    const float x0 = a.part_o[b * D + lane], x1 = a.part_o[b * D + lane + 64];
+    const float wgt = m == -INFINITY ? 0.0f : __expf(m - M);
+    l += wgt * lg;
+    o0 += wgt * x0;
+    o1 += wgt * x1;
   }
+  red[w][lane] = o0;
+  red[w][lane + 64] = o1;
+  if (lane == 0) red[w][D] = l;
+  __syncthreads();
+  if (w != 0) return;
+  o0 = red[0][lane]; o1 = red[0][lane + 64]; l = red[0][D];
+#pragma unroll
+  for (int ww = 1; ww < MW; ++ww) { o0 += red[ww][lane]; o1 += red[ww][lane + 64]; l += red[ww][D]; }
   float y0 = round_bf16(o0 / l), y1 = round_bf16(o1 / l);
   if (a.gate) {
-    const uint16_t* g = a.proj + (long long)t * a.ldp + h * 2 * D + D;
-    y0 = round_bf16(y0 * round_bf16(1.0f / (1.0f + __expf(-bfv(g, lane)))));
-    y1 = round_bf16(y1 * round_bf16(1.0f / (1.0f + __expf(-bfv(g, lane + 64)))));
+    const uint16_t* gp = a.proj + (long long)t * a.ldp + h * 2 * D + D;
+    y0 = round_bf16(y0 * round_bf16(1.0f / (1.0f + __expf(-bfv(gp, lane)))));
+    y1 = round_bf16(y1 * round_bf16(1.0f / (1.0f + __expf(-bfv(gp, lane + 64)))));
   }
   a.y[(long long)t * a.ldy + h * D + lane] = f32_to_bf16_bits(y0);
   a.y[(long long)t * a.ldy + h * D + lane + 64] = f32_to_bf16_bits(y1);
 }
 
-// splits of the pos cached keys, CHUNK-multiple lengths, about 512 waves in all; the last split also covers the
-// t new tokens, so the wave that appends them is the only one that reads them
-int plan_splits(int pos, int kv, int* split_len) {
-  int len = ((pos * kv + 511) / 512 + CHUNK - 1) / CHUNK * CHUNK;
-  len = std::max(len, CHUNK);
-  *split_len = len;
-  return std::max(1, (pos + len - 1) / len);
+// Key ranges: a workgroup covers NW·cw chunks of the pos cached keys (the last one also the t new tokens), cw chosen
+// for about 1024 waves over the cache — one workgroup per CU, each wave streaming its chunks with one in flight.
+struct Plan { int n_groups, group_len; };
+Plan plan(int pos, int kv, int rows) {
+  (void)rows;
+  static const long long waves_target = [] {            // MI_GQA_WAVES: tuning override
+    const char* e = getenv("MI_GQA_WAVES");
+    return e ? std::max(64LL, atoll(e)) : 1024LL;
+  }();
+  const int cw = (int)std::max<long long>(1, ((long long)pos * kv + waves_target * CHUNK - 1) / (waves_target * CHUNK));
+  const int len = NW * cw * CHUNK;
+  return {std::max(1, (pos + len - 1) / len), len};
+}
+
+size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+
+struct Layout { size_t qf, qsc, part_o, part_ml, total; };
+Layout layout(int kv, int n_groups, int rows) {
+  Layout l{};
+  l.qf = 0;
+  l.qsc = align256((size_t)kv * MAXROWS * D * sizeof(f16_t));
+  l.part_o = l.qsc + align256((size_t)kv * MAXROWS * sizeof(float));
+  l.part_ml = l.part_o + align256((size_t)kv * n_groups * rows * D * sizeof(float));
+  l.total = l.part_ml + align256((size_t)kv * n_groups * rows * 2 * sizeof(float));
+  return l;
 }
 
 std::mutex g_mu;
@@ -370,10 +471,8 @@ int workspace(size_t bytes, void** out) {
 
 extern "C" size_t mi_gqa_workspace_bytes(const mi_gqa_desc* d) {
   if (!d || d->t < 1 || d->kv_heads < 1 || d->heads % d->kv_heads) return 0;
-  int len = 0;
-  const int splits = plan_splits(d->pos, d->kv_heads, &len);
-  const size_t rows = (size_t)(d->heads / d->kv_heads) * d->t;
-  return (size_t)d->kv_heads * splits * rows * (D + 2) * sizeof(float);
+  const int rows = d->heads / d->kv_heads * d->t;
+  return layout(d->kv_heads, plan(d->pos, d->kv_heads, rows).n_groups, rows).total;
 }
 
 extern "C" int mi_gqa_decode(const mi_gqa_desc* d, void* stream) {
@@ -386,7 +485,7 @@ extern "C" int mi_gqa_decode(const mi_gqa_desc* d, void* stream) {
   MI_REQUIRE(rows <= 64, "mi_gqa_decode: rep·t = %d query rows per KV head exceeds 64", rows);
   MI_REQUIRE(d->rotary_dim >= 0 && d->rotary_dim <= D && d->rotary_dim % 2 == 0, "mi_gqa_decode: bad rotary_dim");
   MI_REQUIRE(d->pos >= 0 && d->pos + d->t <= d->ctx_max, "mi_gqa_decode: pos + t exceeds the cache (%d)", d->ctx_max);
-  MI_REQUIRE(d->ctx_max % 8 == 0, "mi_gqa_decode: ctx_max must be a multiple of 8");
+  MI_REQUIRE(d->ctx_max % CHUNK == 0, "mi_gqa_decode: ctx_max must be a multiple of %d", CHUNK);
   MI_REQUIRE(d->proj && d->k_codes && d->k_scales && d->v_codes && d->v_scales && d->y, "mi_gqa_decode: null pointer");
   MI_REQUIRE(d->rotary_dim == 0 || (d->rope_cos && d->rope_sin), "mi_gqa_decode: RoPE tables missing");
   MI_REQUIRE(!d->qk_norm || (d->q_norm && d->k_norm), "mi_gqa_decode: qk_norm needs q_norm and k_norm");
@@ -394,7 +493,9 @@ extern "C" int mi_gqa_decode(const mi_gqa_desc* d, void* stream) {
   GqaArgs a{};
   a.t = d->t; a.heads = d->heads; a.kv = d->kv_heads; a.rot = d->rotary_dim; a.pos = d->pos; a.ctx = d->ctx_max;
   a.gate = d->gate; a.qk_norm = d->qk_norm; a.rep = rep; a.rows = rows;
-  a.n_splits = plan_splits(d->pos, d->kv_heads, &a.split_len);
+  const Plan pl = plan(d->pos, d->kv_heads, rows);
+  a.n_groups = pl.n_groups;
+  a.group_len = pl.group_len;
   a.proj = d->proj; a.ldp = d->ld_proj; a.cosb = d->rope_cos; a.sinb = d->rope_sin;
   a.q_norm = d->q_norm; a.k_norm = d->k_norm; a.eps = d->eps; a.scaling = d->scaling;
   a.kc = d->k_codes; a.ks = d->k_scales; a.vc = d->v_codes; a.vs = d->v_scales;
@@ -406,17 +507,23 @@ extern "C" int mi_gqa_decode(const mi_gqa_desc* d, void* stream) {
   } else if (int rc = workspace(need, &ws)) {
     return rc;
   }
-  a.part_o = static_cast<float*>(ws);
-  a.part_ml = a.part_o + (size_t)d->kv_heads * a.n_splits * rows * D;
+  const Layout L = layout(d->kv_heads, a.n_groups, rows);
+  char* wb = static_cast<char*>(ws);
+  a.qf = reinterpret_cast<f16_t*>(wb + L.qf);
+  a.qsc = reinterpret_cast<float*>(wb + L.qsc);
+  a.part_o = reinterpret_cast<float*>(wb + L.part_o);
+  a.part_ml = reinterpret_cast<float*>(wb + L.part_ml);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(a.n_splits, d->kv_heads);
+  hipLaunchKernelGGL(gqa_prep, dim3(d->heads + d->kv_heads, d->t), dim3(64), 0, s, a);
+  MI_TRY_HIP(hipGetLastError(), "gqa_prep launch");
+  const dim3 grid(a.n_groups, d->kv_heads), block(64 * NW);
   const int rt = (rows + 15) / 16;
-  if (rt == 1) hipLaunchKernelGGL(gqa_decode<1>, grid, dim3(64), 0, s, a);
-  else if (rt == 2) hipLaunchKernelGGL(gqa_decode<2>, grid, dim3(64), 0, s, a);
-  else if (rt == 3) hipLaunchKernelGGL(gqa_decode<3>, grid, dim3(64), 0, s, a);
-  else hipLaunchKernelGGL(gqa_decode<4>, grid, dim3(64), 0, s, a);
+  if (rt == 1) hipLaunchKernelGGL(gqa_decode<1>, grid, block, 0, s, a);
+  else if (rt == 2) hipLaunchKernelGGL(gqa_decode<2>, grid, block, 0, s, a);
+  else if (rt == 3) hipLaunchKernelGGL(gqa_decode<3>, grid, block, 0, s, a);
+  else hipLaunchKernelGGL(gqa_decode<4>, grid, block, 0, s, a);
   MI_TRY_HIP(hipGetLastError(), "gqa_decode launch");
-  hipLaunchKernelGGL(gqa_merge, dim3(d->heads, d->t), dim3(64), 0, s, a);
+  hipLaunchKernelGGL(gqa_merge, dim3(d->heads, d->t), dim3(64 * MW), 0, s, a);
   MI_TRY_HIP(hipGetLastError(), "gqa_merge launch");
   return MI_OK;
 }

@@ -33,32 +33,59 @@ int mi_check_hip(hipError_t e, const char* what);         // 0 on success, else 
 // ---- BF16 / F16 bit helpers ---------------------------------------------------------------------------------------
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t u16) { return __uint_as_float(u16 << 16); }
 
-// round-to-nearest-even, NaN kept quiet (the reference's f32_to_bf16)
-__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+// round-to-nearest-even, NaN kept quiet (the reference's f32_to_bf16): gfx950's v_cvt_pk_bf16_f32, branch-free
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+
+__device__ __forceinline__ float round_bf16(float f) { return (float)(__bf16)f; }
+
+// ---- wave64 cross-lane exchanges without LDS: DPP inside a row of 16 lanes, gfx950's permlane16/32 swaps across
+// rows. They read every lane of the wave: call them with the whole wave active. ---------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
 }
+constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // lane i of 8 ↔ 7 − i
+constexpr int kDppMirror = 0x140;      // lane i of 16 ↔ 15 − i
 
-__device__ __forceinline__ float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
-
-// ---- wave64 reductions (DPP/permute via the compiler's cross-lane builtins) ----------------------------------------
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+// sum / max over the 16 lanes of a row, result in every lane of the row
+__device__ __forceinline__ float sum16(float v) {
+  v += dpp_f<kDppXor1>(v);
+  v += dpp_f<kDppXor2>(v);
+  v += dpp_f<kDppHalfMirror>(v);
+  v += dpp_f<kDppMirror>(v);
+  return v;
+}
+__device__ __forceinline__ float max16(float v) {
+  v = fmaxf(v, dpp_f<kDppXor1>(v));
+  v = fmaxf(v, dpp_f<kDppXor2>(v));
+  v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp_f<kDppMirror>(v));
   return v;
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+// v(l) + v(l ^ 16) and v(l) + v(l ^ 32): a swap leaves each lane holding its own value in one half of the pair and
+// its partner's in the other, so the pair's sum (max) is the same in both lanes
+__device__ __forceinline__ float add_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false);
+  return __int_as_float(r[0]) + __int_as_float(r[1]);
+}
+__device__ __forceinline__ float add_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+  return __int_as_float(r[0]) + __int_as_float(r[1]);
+}
+__device__ __forceinline__ float max_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false);
+  return fmaxf(__int_as_float(r[0]), __int_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+  return fmaxf(__int_as_float(r[0]), __int_as_float(r[1]));
 }
 
 // sum over the four lanes l, l^16, l^32, l^48 (the k-groups of an MFMA operand)
-__device__ __forceinline__ float quad16_sum(float v) {
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
-}
+__device__ __forceinline__ float quad16_sum(float v) { return add_xor32(add_xor16(v)); }
+
+__device__ __forceinline__ float wave_sum(float v) { return quad16_sum(sum16(v)); }
+__device__ __forceinline__ float wave_max(float v) { return max_xor32(max_xor16(max16(v))); }

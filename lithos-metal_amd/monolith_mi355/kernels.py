@@ -39,6 +39,19 @@ class PackedWeight:
     def n_pad(self) -> int:
         return -(-self.n // 16) * 16
 
+    def v_codes_token_major(self):
+        """``v_codes`` as ``[kv, ctx_max, D]`` (a copy)."""
+        torch = _torch()
+        kv, nb, d, b = self.v_codes.shape
+        idx = torch.as_tensor(self.V_POS, device=self.v_codes.device)
+        return self.v_codes.index_select(3, idx).permute(0, 1, 3, 2).reshape(kv, nb * b, d)
+
+    def set_v_token_major(self, codes):
+        """Store ``codes [kv, ctx_max, D]`` int8 into the blocked ``v_codes``."""
+        kv, nb, d, b = self.v_codes.shape
+        blocks = codes.reshape(kv, nb, b, d).permute(0, 1, 3, 2)           # [kv, nb, D, key]
+        self.v_codes[..., torch_index(self.V_POS, self.v_codes.device)] = blocks
+
     @property
     def nbytes(self) -> int:
         return int(self.data.numel())
@@ -167,22 +180,44 @@ def rope_tables(theta: float, rotary_dim: int, ctx: int, device="cuda"):
     return emb.cos().to(torch.bfloat16).to(device), emb.sin().to(torch.bfloat16).to(device)
 
 
+def torch_index(a, device):
+    return _torch().as_tensor(np.asarray(a), device=device)
+
+
 class KVCache:
     """One attention layer's int8 KV cache in this backend's layout (the reference keeps BF16 ``[ctx_max, Hkv, D]``,
-    ``nn/attention.py:207-209``): ``k_codes [kv, ctx_max, D]`` int8, ``v_codes [kv, D, ctx_max]`` int8 (transposed,
-    so a P·V B tile is 8 consecutive keys of one dim), ``k_scales`` / ``v_scales [kv, ctx_max]`` float16 —
-    ``scale = f16(absmax / 127)`` per token and KV head. 288 GB of HBM holds a 262 144-token context for all 16
+    ``nn/attention.py:207-209``): ``k_codes [kv, ctx_max, D]`` int8, ``v_codes [kv, ctx_max/64, D, 64]`` int8
+    (transposed inside blocks of 64 keys — key k of a block at position ``V_POS[k]``, the order in which the
+    kernel's score tiles hold the keys — so each 64-key block is 8 KB contiguous), ``k_scales`` / ``v_scales [kv, ctx_max]`` float16 — ``scale = f16(absmax / 127)`` per token
+    and KV head. 288 GB of HBM holds a 262 144-token context for all 16
     attention layers of the 27B model at 4 KV heads × 128 dims many times over."""
+
+    BLOCK = 64
+    V_POS = np.array([(k >> 5) * 32 + ((k & 15) >> 2) * 8 + ((k >> 4) & 1) * 4 + (k & 3) for k in range(64)])
 
     def __init__(self, kv_heads: int, ctx_max: int, head_dim: int = 128, device="cuda"):
         torch = _torch()
-        if ctx_max % 8:
-            raise ValueError("KVCache: ctx_max must be a multiple of 8")
+        if ctx_max % self.BLOCK:
+            raise ValueError(f"KVCache: ctx_max must be a multiple of {self.BLOCK}")
         self.kv_heads, self.ctx_max, self.head_dim = kv_heads, ctx_max, head_dim
         self.k_codes = torch.zeros((kv_heads, ctx_max, head_dim), dtype=torch.int8, device=device)
-        self.v_codes = torch.zeros((kv_heads, head_dim, ctx_max), dtype=torch.int8, device=device)
+        self.v_codes = torch.zeros((kv_heads, ctx_max // self.BLOCK, head_dim, self.BLOCK), dtype=torch.int8,
+                                   device=device)
         self.k_scales = torch.zeros((kv_heads, ctx_max), dtype=torch.float16, device=device)
         self.v_scales = torch.zeros((kv_heads, ctx_max), dtype=torch.float16, device=device)
+
+    def v_codes_token_major(self):
+        """``v_codes`` as ``[kv, ctx_max, D]`` (a copy)."""
+        torch = _torch()
+        kv, nb, d, b = self.v_codes.shape
+        idx = torch.as_tensor(self.V_POS, device=self.v_codes.device)
+        return self.v_codes.index_select(3, idx).permute(0, 1, 3, 2).reshape(kv, nb * b, d)
+
+    def set_v_token_major(self, codes):
+        """Store ``codes [kv, ctx_max, D]`` int8 into the blocked ``v_codes``."""
+        kv, nb, d, b = self.v_codes.shape
+        blocks = codes.reshape(kv, nb, b, d).permute(0, 1, 3, 2)           # [kv, nb, D, key]
+        self.v_codes[..., torch_index(self.V_POS, self.v_codes.device)] = blocks
 
     @property
     def nbytes(self) -> int:

@@ -44,14 +44,14 @@ def _filled_cache(rng, ctx, pos):
 
 def _upload(torch, cache, kc, ks, vc, vs):
     cache.k_codes.copy_(torch.from_numpy(np.ascontiguousarray(kc.transpose(1, 0, 2))))
-    cache.v_codes.copy_(torch.from_numpy(np.ascontiguousarray(vc.transpose(1, 2, 0))))
+    cache.set_v_token_major(torch.from_numpy(np.ascontiguousarray(vc.transpose(1, 0, 2))).cuda())
     cache.k_scales.copy_(torch.from_numpy(np.ascontiguousarray(ks.T)))
     cache.v_scales.copy_(torch.from_numpy(np.ascontiguousarray(vs.T)))
 
 
 def _download(cache):
     return (cache.k_codes.cpu().numpy().transpose(1, 0, 2), cache.k_scales.cpu().numpy().T,
-            cache.v_codes.cpu().numpy().transpose(2, 0, 1), cache.v_scales.cpu().numpy().T)
+            cache.v_codes_token_major().cpu().numpy().transpose(1, 0, 2), cache.v_scales.cpu().numpy().T)
 
 
 def _check_out(y, ref):
@@ -144,6 +144,18 @@ def test_gqa_decode_deterministic(torch_gpu):
     assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
 
 
+def test_v_block_layout_round_trip():
+    """The blocked V layout is a permutation inside each 64-key block, and the two accessors invert each other."""
+    torch = pytest.importorskip("torch")
+    from monolith_mi355 import kernels
+    assert sorted(kernels.KVCache.V_POS) == list(range(64))
+    c = kernels.KVCache(2, 128, device="cpu")
+    codes = torch.randint(-127, 128, (2, 128, 128), dtype=torch.int8)
+    c.set_v_token_major(codes)
+    assert torch.equal(c.v_codes_token_major(), codes)
+    assert c.v_codes[1, 1, 5, kernels.KVCache.V_POS[7]] == codes[1, 64 + 7, 5]
+
+
 def test_rope_tables_match_oracle():
     """The product's BF16 tables against numpy's FP32 ``cos``/``sin``: at most one BF16 step apart, rarely."""
     torch = pytest.importorskip("torch")
@@ -168,7 +180,7 @@ def test_gqa_rejects_bad_descriptors():
                 ld_proj=7168, rope_cos=256, rope_sin=256, k_codes=256, k_scales=256, v_codes=256, v_scales=256,
                 y=256, ld_y=3072, eps=1e-6, scaling=0.088)
     bad = [dict(head_dim=64), dict(t=0), dict(t=17), dict(heads=25), dict(t=11), dict(pos=1024),
-           dict(ctx_max=1020, pos=10), dict(rotary_dim=129), dict(proj=0), dict(qk_norm=1), dict(k_codes=8)]
+           dict(ctx_max=1000, pos=10), dict(rotary_dim=129), dict(proj=0), dict(qk_norm=1), dict(k_codes=8)]
     for kw in bad:
         d = hip.MiGqaDesc(**{**base, **kw})
         assert lib.mi_gqa_decode(C.byref(d), None) == 1, kw
