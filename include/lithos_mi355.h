@@ -171,6 +171,43 @@ typedef struct mi_gqa_desc {
 size_t mi_gqa_workspace_bytes(const mi_gqa_desc* d);
 int mi_gqa_decode(const mi_gqa_desc* d, void* stream);
 
+/* ---- MoE routing and combine (ops/moe.py `moe_route`, `moe_combine`; nn/moe.py:108-135;
+ *      kernels/common/moe_route.metal:20-66, moe_combine.metal:19-49, moe_group.metal:8-47) -----------------------
+ * Route: logits [t][ld_logits] BF16 → ids [t][top_k] int32, weights [t][top_k] float (BF16-valued): softmax in FP32,
+ * top-k with ties to the lowest expert index, renormalized over the k when renorm. With `groups` non-NULL the same
+ * launch writes the expert groups of the grouped GEMV (mi_gemv_desc.groups): max_groups records of 18 int32 —
+ * expert, count, then the count pair ids p = t·top_k + slot ascending — one per distinct expert in order of first
+ * use, the rest expert = -1, count = 0. t <= 16, n_experts <= 512, top_k <= 16. */
+typedef struct mi_moe_route_desc {
+  int32_t t, n_experts, top_k, renorm;
+  const uint16_t* logits;
+  int32_t ld_logits;
+  int32_t* ids;
+  float* weights;
+  int32_t* groups;
+  int32_t max_groups;
+} mi_moe_route_desc;
+int mi_moe_route(const mi_moe_route_desc* d, void* stream);
+
+/* Combine: out[t] = Σ_j w[t][j]·h[t·top_k + j] (+ bf16(σ(shared_gate[t]))·shared[t]) (+ residual[t]), FP32, one BF16
+ * rounding. h [t·top_k][ldh], shared [t][ld_shared], shared_gate [t] at stride ld_gate, residual [t][ldr], out [t][ldo],
+ * all BF16; hidden and the row strides multiples of 8, rows 16-byte aligned. shared/shared_gate/residual may be NULL. */
+typedef struct mi_moe_combine_desc {
+  int32_t t, hidden, top_k;
+  const uint16_t* h;
+  int32_t ldh;
+  const float* weights;
+  const uint16_t* shared;
+  int32_t ld_shared;
+  const uint16_t* shared_gate;
+  int32_t ld_gate;
+  const uint16_t* residual;
+  int32_t ldr;
+  uint16_t* out;
+  int32_t ldo;
+} mi_moe_combine_desc;
+int mi_moe_combine(const mi_moe_combine_desc* d, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,210 @@
+// MoE router top-k + expert grouping, and the weighted combine (ops/moe.py `moe_route`, `moe_combine`;
+// nn/moe.py:108-135; kernels/common/moe_route.metal:20-66, moe_combine.metal:19-49, moe_group.metal:8-47).
+//
+// Semantics: softmax in FP32 over the BF16 logits, k rounds of argmax over the probabilities with ties to the lowest
+// expert index, the chosen probabilities optionally renormalized by their sum (taken in pick order), weights rounded
+// to BF16 and stored as FP32. Combine: Σ_j w_j·h_j (fused multiply-adds in slot order) (+ bf16(σ(gate))·shared)
+// (+ residual) in FP32, one BF16 rounding.
+//
+// MI355X design:
+//  * moe_route: one workgroup, one wave per token (T <= 16): each lane holds E/64 logits; max / sum / argmax are
+//    DPP + permlane reductions. The same launch then turns the ids into expert groups for the grouped GEMV — one
+//    record per distinct expert, in order of first use, holding the ≤ 16 (token, slot) pairs routed to it (pair
+//    p = t·k + j, ascending) — so the expert GEMVs stream exactly the chosen experts, each once per step.
+//  * moe_combine: one workgroup per token, 8 columns per lane with 16-byte loads.
+#include "mi_common.h"
+
+namespace {
+
+constexpr int MAX_PER_LANE = 8;      // E <= 512
+constexpr int MAX_K = 16;
+constexpr int MAX_T = 16;
+constexpr int GROUP_REC = 18;        // expert, count, 16 pair ids (the grouped GEMV's record)
+
+struct RouteArgs {
+  int t, n_experts, top_k, renorm, ld_logits, max_groups;
+  const uint16_t* logits;
+  int32_t* ids;
+  float* weights;
+  int32_t* groups;
+};
+
+__device__ __forceinline__ float wave_min(float v) { return -wave_max(-v); }
+
+__global__ __launch_bounds__(64 * MAX_T) void moe_route(RouteArgs a) {
+  __shared__ int sel[MAX_T * MAX_K];
+  const int lane = threadIdx.x & 63, t = threadIdx.x >> 6;
+  const int E = a.n_experts, k = a.top_k;
+  if (t < a.t) {                                    // wave-uniform
+    float v[MAX_PER_LANE];
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < MAX_PER_LANE; ++i) {
+      const int e = lane + 64 * i;
+      v[i] = e < E ? bf16_bits_to_f32(a.logits[(long long)t * a.ld_logits + e]) : -INFINITY;
+      m = fmaxf(m, v[i]);
+    }
+    m = wave_max(m);
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < MAX_PER_LANE; ++i) {
+      const int e = lane + 64 * i;
+      v[i] = e < E ? expf(v[i] - m) : 0.0f;
+      s += v[i];
+    }
+    s = wave_sum(s);
+#pragma unroll
+    for (int i = 0; i < MAX_PER_LANE; ++i) v[i] = lane + 64 * i < E ? v[i] / s : -1.0f;   // -1: absent or taken
+    float cw[MAX_K];
+    int ce[MAX_K];
+    float wsum = 0.0f;
+    for (int r = 0; r < k; ++r) {
+      float best = -1.0f;
+      int bi = 1 << 20;
+#pragma unroll
+      for (int i = 0; i < MAX_PER_LANE; ++i)
+        if (v[i] > best) { best = v[i]; bi = lane + 64 * i; }        // strictly greater: the lane's lowest index
+      const float gmax = wave_max(best);
+      const int e = (int)wave_min(best == gmax ? (float)bi : (float)(1 << 20));
+#pragma unroll
+      for (int i = 0; i < MAX_PER_LANE; ++i)
+        if (lane + 64 * i == e) v[i] = -1.0f;
+      ce[r] = e;
+      cw[r] = gmax;
+      wsum += gmax;
+    }
+    for (int r = 0; r < k; ++r) {
+      const float w = a.renorm ? cw[r] / wsum : cw[r];
+      if (lane == 0) {
+        a.ids[t * k + r] = ce[r];
+        a.weights[t * k + r] = round_bf16(w);
+      }
+      sel[t * k + r] = ce[r];
+    }
+  }
+  if (!a.groups) return;                            // workgroup-uniform
+  __syncthreads();
+  // groups: record g = the g-th distinct expert in pair order; pairs of a record ascending
+  const int P = a.t * k;
+  for (int p = threadIdx.x; p < P; p += blockDim.x) {
+    const int e = sel[p];
+    int first = p, rank = 0, count = 0;
+    for (int q = 0; q < P; ++q) {
+      if (sel[q] != e) continue;
+      if (q < first) first = q;
+      if (q < p) ++rank;
+      ++count;
+    }
+    int g = 0;                                      // distinct experts first used before `first`
+    for (int q = 0; q < first; ++q) {
+      bool seen = false;
+      for (int r = 0; r < q; ++r) seen |= sel[r] == sel[q];
+      g += !seen;
+    }
+    int32_t* rec = a.groups + (long long)g * GROUP_REC;
+    rec[2 + rank] = p;
+    if (rank == 0) { rec[0] = e; rec[1] = count; }
+  }
+  // the records past the distinct experts: empty
+  int distinct = 0;
+  for (int q = 0; q < P; ++q) {
+    bool seen = false;
+    for (int r = 0; r < q; ++r) seen |= sel[r] == sel[q];
+    distinct += !seen;
+  }
+  for (int g = distinct + (int)threadIdx.x; g < a.max_groups; g += blockDim.x) {
+    a.groups[(long long)g * GROUP_REC] = -1;
+    a.groups[(long long)g * GROUP_REC + 1] = 0;
+  }
+}
+
+struct CombineArgs {
+  int t, hidden, top_k, ldh, ld_shared, ld_gate, ldr, ldo;
+  const uint16_t* h;
+  const float* weights;
+  const uint16_t* shared;
+  const uint16_t* shared_gate;
+  const uint16_t* residual;
+  uint16_t* out;
+};
+
+__device__ __forceinline__ void bf16x8_to_f32(uint4 u, float* f) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(w[i] << 16);
+    f[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+  }
+}
+
+__global__ __launch_bounds__(256) void moe_combine(CombineArgs a) {
+  const int t = blockIdx.y;
+  const int c = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (c >= a.hidden) return;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, x[8];
+  for (int j = 0; j < a.top_k; ++j) {
+    const float w = a.weights[t * a.top_k + j];
+    bf16x8_to_f32(*reinterpret_cast<const uint4*>(a.h + (long long)(t * a.top_k + j) * a.ldh + c), x);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = fmaf(w, x[i], acc[i]);
+  }
+  if (a.shared) {
+    const float g = 1.0f / (1.0f + expf(-bf16_bits_to_f32(a.shared_gate[(long long)t * a.ld_gate])));
+    const float gb = round_bf16(g);
+    bf16x8_to_f32(*reinterpret_cast<const uint4*>(a.shared + (long long)t * a.ld_shared + c), x);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = fmaf(gb, x[i], acc[i]);
+  }
+  if (a.residual) {
+    bf16x8_to_f32(*reinterpret_cast<const uint4*>(a.residual + (long long)t * a.ldr + c), x);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] += x[i];
+  }
+  uint4 o;
+  o.x = f32_to_bf16_bits(acc[0]) | ((uint32_t)f32_to_bf16_bits(acc[1]) << 16);
+  o.y = f32_to_bf16_bits(acc[2]) | ((uint32_t)f32_to_bf16_bits(acc[3]) << 16);
+  o.z = f32_to_bf16_bits(acc[4]) | ((uint32_t)f32_to_bf16_bits(acc[5]) << 16);
+  o.w = f32_to_bf16_bits(acc[6]) | ((uint32_t)f32_to_bf16_bits(acc[7]) << 16);
+  *reinterpret_cast<uint4*>(a.out + (long long)t * a.ldo + c) = o;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+
+extern "C" int mi_moe_route(const mi_moe_route_desc* d, void* stream) {
+  MI_REQUIRE(d, "mi_moe_route: null descriptor");
+  MI_REQUIRE(d->t >= 1 && d->t <= MAX_T, "mi_moe_route: t=%d must be in 1..%d", d->t, MAX_T);
+  MI_REQUIRE(d->n_experts >= 1 && d->n_experts <= 64 * MAX_PER_LANE, "mi_moe_route: n_experts=%d must be in 1..%d",
+             d->n_experts, 64 * MAX_PER_LANE);
+  MI_REQUIRE(d->top_k >= 1 && d->top_k <= MAX_K && d->top_k <= d->n_experts, "mi_moe_route: top_k=%d out of range",
+             d->top_k);
+  MI_REQUIRE(d->logits && d->ids && d->weights && d->ld_logits >= d->n_experts, "mi_moe_route: bad logits / outputs");
+  MI_REQUIRE(!d->groups || d->max_groups >= d->t * d->top_k || d->max_groups >= d->n_experts,
+             "mi_moe_route: max_groups=%d cannot hold every distinct expert", d->max_groups);
+  RouteArgs a{d->t, d->n_experts, d->top_k, d->renorm, d->ld_logits, d->max_groups, d->logits, d->ids, d->weights,
+              d->groups};
+  hipLaunchKernelGGL(moe_route, dim3(1), dim3(64 * d->t), 0, static_cast<hipStream_t>(stream), a);
+  MI_TRY_HIP(hipGetLastError(), "moe_route launch");
+  return MI_OK;
+}
+
+extern "C" int mi_moe_combine(const mi_moe_combine_desc* d, void* stream) {
+  MI_REQUIRE(d, "mi_moe_combine: null descriptor");
+  MI_REQUIRE(d->t >= 1 && d->top_k >= 1 && d->hidden >= 8 && d->hidden % 8 == 0,
+             "mi_moe_combine: t, top_k >= 1 and hidden a multiple of 8 (t=%d k=%d hidden=%d)", d->t, d->top_k, d->hidden);
+  MI_REQUIRE(d->h && d->weights && d->out, "mi_moe_combine: null pointer");
+  MI_REQUIRE(!d->shared == !d->shared_gate, "mi_moe_combine: shared and shared_gate go together");
+  MI_REQUIRE(d->ldh % 8 == 0 && d->ldo % 8 == 0 && (!d->shared || d->ld_shared % 8 == 0) &&
+                 (!d->residual || d->ldr % 8 == 0),
+             "mi_moe_combine: row strides must be multiples of 8");
+  MI_REQUIRE(aligned16(d->h) && aligned16(d->out) && (!d->shared || aligned16(d->shared)) &&
+                 (!d->residual || aligned16(d->residual)),
+             "mi_moe_combine: 16-byte aligned rows");
+  CombineArgs a{d->t, d->hidden, d->top_k, d->ldh, d->ld_shared, d->ld_gate, d->ldr, d->ldo,
+                d->h, d->weights, d->shared, d->shared_gate, d->residual, d->out};
+  const dim3 grid((d->hidden / 8 + 255) / 256, d->t);
+  hipLaunchKernelGGL(moe_combine, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  MI_TRY_HIP(hipGetLastError(), "moe_combine launch");
+  return MI_OK;
+}

@@ -262,3 +262,84 @@ def gqa_decode(proj, cache: KVCache, pos: int, *, heads: int, rope_cos, rope_sin
                          workspace_bytes=0 if workspace is None else workspace.numel() * workspace.element_size())
     hip.call("mi_gqa_decode", C.byref(desc), hip.stream_handle(stream))
     return out
+
+
+# ---- MoE: route (+ expert groups), grouped expert GEMV, combine -------------------------------------------------------
+GROUP_REC = 18
+
+
+def moe_route(logits, top_k: int, *, renorm: bool = True, groups: bool = True, stream=None):
+    """``moe_route`` (``ops/moe.py``): ``logits [T, E]`` bf16 → ``(ids [T, k] int32, weights [T, k] float32,
+    groups [max_groups, 18] int32 or None)``; ``max_groups = min(E, T·k)``. The groups feed ``moe_gemv``."""
+    torch = _torch()
+    _bf16_2d(logits, "moe_route logits", aligned=False)
+    t, e = logits.shape
+    dev = logits.device
+    ids = torch.empty((t, top_k), dtype=torch.int32, device=dev)
+    w = torch.empty((t, top_k), dtype=torch.float32, device=dev)
+    max_groups = min(e, t * top_k)
+    g = torch.empty((max_groups, GROUP_REC), dtype=torch.int32, device=dev) if groups else None
+    d = hip.MiMoeRouteDesc(t=t, n_experts=e, top_k=top_k, renorm=int(renorm), logits=hip.ptr(logits),
+                           ld_logits=logits.stride(0), ids=hip.ptr(ids), weights=hip.ptr(w), groups=hip.ptr(g),
+                           max_groups=max_groups if groups else 0)
+    hip.call("mi_moe_route", C.byref(d), hip.stream_handle(stream))
+    return ids, w, g
+
+
+def moe_gemv(w: PackedWeight, x, groups, *, tokens: int, top_k: int, x_per_slot: bool, epilogue=None, norm_w=None,
+             eps: float = 1e-6, out=None, stream=None):
+    """``moe_gemv`` (``ops/moe.py``; the grouped mode of ``gemv``): for every group record (expert e, its pairs
+    p = t·k + j), ``out[p] = x_row · W_eᵀ`` with ``x_row = x[p]`` (``x_per_slot``) or ``x[p // k]``; ``w`` holds the
+    experts back to back. ``out [T·k, n_out]`` bf16."""
+    torch = _torch()
+    _bf16_2d(x, "moe_gemv x")
+    if x.shape[1] != w.k:
+        raise ValueError(f"moe_gemv: x has {x.shape[1]} columns, the experts take K={w.k}")
+    if x.shape[0] < (tokens * top_k if x_per_slot else tokens):
+        raise ValueError("moe_gemv: x has too few rows")
+    if groups.dtype != torch.int32 or groups.dim() != 2 or groups.shape[1] != GROUP_REC:
+        raise ValueError("moe_gemv: groups must be int32 [max_groups, 18] (moe_route)")
+    if not 1 <= tokens <= 16:
+        raise ValueError("moe_gemv: 1..16 tokens")
+    n_out = w.n // 2 if epilogue in ("silu_mul", "silu_mul_rounded") else w.n
+    if out is None:
+        out = torch.empty((tokens * top_k, n_out), dtype=torch.bfloat16, device=x.device)
+    _bf16_2d(out, "moe_gemv out", aligned=False)
+    if norm_w is not None and (norm_w.dtype != torch.float32 or norm_w.numel() != w.k):
+        raise ValueError("moe_gemv: norm_w must be float32 [K]")
+    d = hip.MiGemvDesc(format=hip.MI_FMT[w.format], n=w.n, k=w.k, m=tokens, w=hip.ptr(w.data),
+                       row_scale=hip.ptr(w.row_scale), x=hip.ptr(x), ldx=x.stride(0), y=hip.ptr(out),
+                       ldy=out.stride(0), epilogue=hip.MI_EPI[epilogue], residual=0, ldr=0, norm_w=hip.ptr(norm_w),
+                       eps=eps, groups=hip.ptr(groups), max_groups=groups.shape[0], top_k=top_k,
+                       x_per_slot=int(x_per_slot), workspace=0, workspace_bytes=0, out_f32=0)
+    hip.call("mi_gemv", C.byref(d), hip.stream_handle(stream))
+    return out
+
+
+def moe_combine(h, weights, *, top_k: int, shared=None, shared_gate=None, residual=None, out=None, stream=None):
+    """``moe_combine`` (``ops/moe.py``): ``out[t] = Σ_j w[t, j]·h[t·k + j] (+ bf16(σ(shared_gate[t]))·shared[t])
+    (+ residual[t])``, FP32, one BF16 rounding. ``h [T·k, H]``, ``weights [T, k]`` float32."""
+    torch = _torch()
+    _bf16_2d(h, "moe_combine h")
+    t = weights.shape[0]
+    hidden = h.shape[1]
+    if weights.dtype != torch.float32 or tuple(weights.shape) != (t, top_k) or not weights.is_contiguous():
+        raise ValueError("moe_combine: weights must be contiguous float32 [T, k]")
+    if h.shape[0] < t * top_k:
+        raise ValueError("moe_combine: h has too few rows")
+    for name, a in (("shared", shared), ("residual", residual)):
+        if a is not None:
+            _bf16_2d(a, f"moe_combine {name}")
+    if shared_gate is not None:
+        _bf16_2d(shared_gate, "moe_combine shared_gate", aligned=False)
+    if out is None:
+        out = torch.empty((t, hidden), dtype=torch.bfloat16, device=h.device)
+    _bf16_2d(out, "moe_combine out")
+    d = hip.MiMoeCombineDesc(t=t, hidden=hidden, top_k=top_k, h=hip.ptr(h), ldh=h.stride(0), weights=hip.ptr(weights),
+                             shared=hip.ptr(shared), ld_shared=shared.stride(0) if shared is not None else 0,
+                             shared_gate=hip.ptr(shared_gate),
+                             ld_gate=shared_gate.stride(0) if shared_gate is not None else 0,
+                             residual=hip.ptr(residual), ldr=residual.stride(0) if residual is not None else 0,
+                             out=hip.ptr(out), ldo=out.stride(0))
+    hip.call("mi_moe_combine", C.byref(d), hip.stream_handle(stream))
+    return out

@@ -56,6 +56,19 @@ class MiGqaDesc(C.Structure):
                 ("workspace_bytes", C.c_size_t)]
 
 
+class MiMoeRouteDesc(C.Structure):
+    _fields_ = [("t", C.c_int32), ("n_experts", C.c_int32), ("top_k", C.c_int32), ("renorm", C.c_int32),
+                ("logits", C.c_void_p), ("ld_logits", C.c_int32), ("ids", C.c_void_p), ("weights", C.c_void_p),
+                ("groups", C.c_void_p), ("max_groups", C.c_int32)]
+
+
+class MiMoeCombineDesc(C.Structure):
+    _fields_ = [("t", C.c_int32), ("hidden", C.c_int32), ("top_k", C.c_int32), ("h", C.c_void_p), ("ldh", C.c_int32),
+                ("weights", C.c_void_p), ("shared", C.c_void_p), ("ld_shared", C.c_int32), ("shared_gate", C.c_void_p),
+                ("ld_gate", C.c_int32), ("residual", C.c_void_p), ("ldr", C.c_int32), ("out", C.c_void_p),
+                ("ldo", C.c_int32)]
+
+
 # name -> (restype, argtypes); every int-returning entry point is error-checked
 _VP, _I32, _SZ, _F = C.c_void_p, C.c_int32, C.c_size_t, C.c_float
 SIGNATURES = {
@@ -90,6 +103,8 @@ SIGNATURES = {
     "mi_gdn_step": (C.c_int, [C.POINTER(MiGdnDesc), _VP]),
     "mi_gqa_workspace_bytes": (_SZ, [C.POINTER(MiGqaDesc)]),
     "mi_gqa_decode": (C.c_int, [C.POINTER(MiGqaDesc), _VP]),
+    "mi_moe_route": (C.c_int, [C.POINTER(MiMoeRouteDesc), _VP]),
+    "mi_moe_combine": (C.c_int, [C.POINTER(MiMoeCombineDesc), _VP]),
 }
 
 

@@ -1,0 +1,210 @@
+"""The HIP MoE path against the oracle (the reference's ``tests/kernels/test_moe_ops.py`` strategy and bars):
+
+* ``moe_route``: ids bit-exact against the oracle's routing (ties to the lowest index, a forced tie included), weights
+  BF16-valued and within 2^-8 of the largest weight (``test_moe_ops.py:66-67``), at the reference's test shapes and
+  the BASELINE 256 experts / top-8; the expert groups cover every (token, slot) pair exactly once;
+* the grouped expert GEMV (``moe_gemv``): every pair's row against a float64 matmul of that expert's exact
+  dequantized matrix (per-slot and per-token inputs, plain and silu·mul), one BF16 ULP of its own magnitude;
+* ``moe_combine`` within one BF16 ULP (``test_moe_ops.py:119-144``);
+* the whole sparse MoE block at the BASELINE geometry (hidden 2048, expert intermediate 512, NVFP4 experts, top-8,
+  a shared expert, fused input RMSNorm) for M = 1 and 8, against ``SparseMoE.forward``'s restatement fed the same
+  router logits (``ok_rounded``).
+"""
+
+import numpy as np
+import pytest
+
+from helpers import from_dev_bf16, spec_of, to_dev_bf16
+from oracle import formats as OF
+from oracle import nn as ON
+from oracle.fp import bf16_to_f32, f32_to_bf16, rbf
+from oracle.gates import check_against_oracle
+
+GROUP_REC = 18
+
+
+def _check_groups(groups, ids, t, k):
+    g = groups.cpu().numpy()
+    ids = ids.cpu().numpy()
+    seen = []
+    for rec in g:
+        e, cnt = int(rec[0]), int(rec[1])
+        if cnt == 0:
+            assert e == -1
+            continue
+        pairs = rec[2: 2 + cnt]
+        assert np.all(np.diff(pairs) > 0)
+        for p in pairs:
+            assert ids[p // k, p % k] == e
+        seen += list(pairs)
+    assert sorted(seen) == list(range(t * k))
+    used = [int(r[0]) for r in g if r[1] > 0]
+    assert len(used) == len(set(used)) == len(np.unique(ids))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n_experts,k,renorm", [(8, 2, True), (60, 4, False), (128, 8, True), (5, 5, False),
+                                                (256, 8, True), (256, 8, False)])
+@pytest.mark.parametrize("t", [1, 5, 8, 16])
+def test_moe_route(torch_gpu, n_experts, k, renorm, t):
+    from monolith_mi355 import kernels
+    rng = np.random.default_rng(n_experts * 10 + t)
+    logits = rbf(rng.standard_normal((t, n_experts)) * 2)
+    if t > 1:
+        logits[1, 3] = logits[1, 0]                         # a tie: the lower index wins
+    ids, w, groups = kernels.moe_route(to_dev_bf16(torch_gpu, logits), k, renorm=renorm)
+    ref_ids, ref_w = ON.moe_route(logits, k, renorm)
+    got_w = w.cpu().numpy()
+    assert np.array_equal(ids.cpu().numpy(), ref_ids)
+    assert np.allclose(got_w, ref_w, rtol=0, atol=2 ** -8 * ref_w.max()) and np.array_equal(got_w, rbf(got_w))
+    _check_groups(groups, ids, t, k)
+
+
+@pytest.mark.gpu
+def test_moe_route_tied_logits_and_underflow(torch_gpu):
+    """Exact ties among the top probabilities and probabilities that underflow to 0 both resolve by index."""
+    from monolith_mi355 import kernels
+    logits = np.zeros((3, 256), np.float32)
+    logits[0, [6, 7, 9]] = 1.0                                # three-way tie at the top
+    logits[1, :] = -120.0
+    logits[1, 2] = logits[1, 9] = 0.0                         # everything else underflows to p = 0
+    logits[2] = rbf(np.linspace(-3, 3, 256))[::-1]
+    logits = rbf(logits)
+    ids, w, _ = kernels.moe_route(to_dev_bf16(torch_gpu, logits), 8, renorm=False)
+    ref_ids, ref_w = ON.moe_route(logits, 8, renorm=False)
+    assert np.array_equal(ids.cpu().numpy(), ref_ids)
+    assert list(ids.cpu().numpy()[1, :4]) == [2, 9, 0, 1]
+
+
+def _experts(rng, n_exp, inter, hidden):
+    """Per expert: gate|up slab (chunk-interleaved by 8, per-row tensor scales) and down, plus their exact
+    dequantized float32 matrices ([gate; up] un-interleaved)."""
+    perm = ON.interleave_chunks(inter, inter, 8)
+    gu_specs, gu_scales, dn_specs, dn_scales, w_gu, w_dn = [], [], [], [], [], []
+    for _ in range(n_exp):
+        gate, up, down = OF.nvfp4_random(inter, hidden, rng), OF.nvfp4_random(inter, hidden, rng), OF.nvfp4_random(hidden, inter, rng)
+        slab = OF.permute_rows(OF.stack_rows([gate, up]), perm)
+        gu_specs.append(spec_of(dict(slab, weight_scale_2=1.0)))
+        gu_scales.append(slab["row_scale"])
+        dn_specs.append(spec_of(dict(down, weight_scale_2=1.0)))
+        dn_scales.append(np.full(hidden, down["weight_scale_2"], np.float32))
+        w_gu.append(np.concatenate([OF.dequantize(gate), OF.dequantize(up)]))
+        w_dn.append(OF.dequantize(down))
+    return gu_specs, gu_scales, dn_specs, dn_scales, np.stack(w_gu), np.stack(w_dn)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("x_per_slot,epilogue", [(False, None), (True, None), (False, "silu_mul_rounded"),
+                                                 (False, "silu_mul")])
+@pytest.mark.parametrize("t", [1, 3, 8])
+def test_moe_gemv_pairs_stream_the_chosen_experts(torch_gpu, x_per_slot, epilogue, t):
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    rng = np.random.default_rng(t + 7 * x_per_slot)
+    n_exp, inter, hidden, k = 6, 64, 256, 2
+    gu_specs, gu_scales, _, _, w_gu, _ = _experts(rng, n_exp, inter, hidden)
+    w = kernels.upload(gu_specs, row_scales=gu_scales)
+    ids = rng.integers(0, n_exp, (t, k)).astype(np.int32)
+    for row in ids:                                           # distinct experts per token, as top-k gives
+        while row[0] == row[1]:
+            row[1] = rng.integers(0, n_exp)
+    logits = np.full((t, n_exp), -4.0, np.float32)            # route logits that pick exactly `ids`
+    for tt in range(t):
+        logits[tt, ids[tt, 0]], logits[tt, ids[tt, 1]] = 2.0, 1.0
+    rid, _, groups = kernels.moe_route(to_dev_bf16(torch, rbf(logits)), k, renorm=False)
+    assert np.array_equal(rid.cpu().numpy(), ids)
+    x = rbf(rng.uniform(-1, 1, (t * k if x_per_slot else t, hidden)))
+    got = from_dev_bf16(kernels.moe_gemv(w, to_dev_bf16(torch, x), groups, tokens=t, top_k=k, x_per_slot=x_per_slot,
+                                         epilogue=epilogue))
+    for p in range(t * k):
+        e = ids[p // k, p % k]
+        xr = x[p] if x_per_slot else x[p // k]
+        if epilogue:
+            ref = ON.linear(xr[None], w_gu[e], epilogue="silu_mul", round_silu=epilogue == "silu_mul_rounded")[0]
+        else:
+            ref = ON.linear(xr[None], np.concatenate([w_gu[e][ON.interleave_chunks(inter, inter, 8)]]))[0]
+        chk = check_against_oracle(got[p], ref)
+        assert chk.ok_rounded() and chk.max_ulp_elementwise <= 1, (p, chk)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shared,residual", [(False, True), (True, True), (True, False), (False, False)])
+def test_moe_combine(torch_gpu, shared, residual):
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    rng = np.random.default_rng(3)
+    t, k, hidden = 4, 3, 96
+    h = rbf(rng.standard_normal((t * k, hidden)))
+    w = rbf(rng.uniform(0, 1, (t, k)))
+    sh = rbf(rng.standard_normal((t, hidden)))
+    gate = rbf(rng.standard_normal((t, 1)))
+    res = rbf(rng.standard_normal((t, hidden)))
+    got = from_dev_bf16(kernels.moe_combine(to_dev_bf16(torch, h), torch.from_numpy(w).cuda(), top_k=k,
+                                            shared=to_dev_bf16(torch, sh) if shared else None,
+                                            shared_gate=to_dev_bf16(torch, gate) if shared else None,
+                                            residual=to_dev_bf16(torch, res) if residual else None))
+    ref = ON.moe_combine(h.reshape(t, k, hidden), w, residual=res if residual else None,
+                         shared=sh if shared else None, shared_gate=gate if shared else None)
+    chk = check_against_oracle(got, ref)
+    assert chk.ok_rounded() and chk.max_ulp_elementwise <= 1, chk
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("t", [1, 8])
+def test_sparse_moe_block_baseline_geometry(torch_gpu, t):
+    """hidden 2048, expert intermediate 512 (NVFP4), top-8 of 32 experts (256 in the routing tests: the grouped GEMV
+    streams only the chosen experts, so E changes nothing but the slab size), shared expert 512, fused RMSNorm."""
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    rng = np.random.default_rng(100 + t)
+    n_exp, k, inter, hidden, si, eps = 32, 8, 512, 2048, 512, 1e-6
+    gu_specs, gu_scales, dn_specs, dn_scales, w_gu, w_dn = _experts(rng, n_exp, inter, hidden)
+    w_gu_d = kernels.upload(gu_specs, row_scales=gu_scales)
+    w_dn_d = kernels.upload(dn_specs, row_scales=dn_scales)
+    sgu_specs, sgu_scales, sdn_specs, sdn_scales, s_gu, s_dn = _experts(rng, 1, si, hidden)
+    s_gu_d = kernels.upload(sgu_specs, row_scales=sgu_scales)
+    s_dn_d = kernels.upload(sdn_specs, row_scales=sdn_scales)
+    router = {"format": "bf16", "weight": f32_to_bf16((rng.standard_normal((n_exp, hidden)) * 0.02).astype(np.float32))}
+    sgate = {"format": "bf16", "weight": f32_to_bf16((rng.standard_normal((1, hidden)) * 0.02).astype(np.float32))}
+    r_d, sg_d = kernels.upload(spec_of(router)), kernels.upload(spec_of(sgate))
+    h = rbf(rng.standard_normal((t, hidden)))
+    wn = rbf(rng.standard_normal(hidden) * 0.1)
+    nw = torch.from_numpy((1 + wn).astype(np.float32)).cuda()
+    hd = to_dev_bf16(torch, h)
+
+    logits = kernels.gemv(r_d, hd, norm_w=nw, eps=eps)
+    ids, wts, groups = kernels.moe_route(logits, k, renorm=True)
+    act = kernels.moe_gemv(w_gu_d, hd, groups, tokens=t, top_k=k, x_per_slot=False, epilogue="silu_mul_rounded",
+                           norm_w=nw, eps=eps)
+    hk = kernels.moe_gemv(w_dn_d, act, groups, tokens=t, top_k=k, x_per_slot=True)
+    s_act = kernels.gemv(s_gu_d, hd, epilogue="silu_mul", norm_w=nw, eps=eps)
+    s_out = kernels.gemv(s_dn_d, s_act)
+    s_gate = kernels.gemv(sg_d, hd, norm_w=nw, eps=eps)
+    y = kernels.moe_combine(hk, wts, top_k=k, shared=s_out, shared_gate=s_gate, residual=hd)
+    torch.cuda.synchronize()
+
+    xn = ON.rms_norm(h, wn, eps)
+    got_logits = from_dev_bf16(logits)
+    chk = check_against_oracle(got_logits, ON.linear(xn, bf16_to_f32(router["weight"])))
+    assert chk.ok_rounded(), chk
+    ref, ref_ids, _ = ON.moe_forward(xn, h, got_logits, k, w_gu, w_dn, renorm=True,
+                                     shared=(s_gu[0], s_dn[0], bf16_to_f32(sgate["weight"])))
+    assert np.array_equal(ids.cpu().numpy(), ref_ids)
+    chk = check_against_oracle(from_dev_bf16(y), ref)
+    assert chk.ok_rounded(), chk
+
+
+def test_moe_rejects_bad_descriptors():
+    import ctypes as C
+    from monolith_mi355.runtime import hip
+    lib = hip.load()
+    base = dict(t=2, n_experts=256, top_k=8, renorm=1, logits=256, ld_logits=256, ids=256, weights=256, groups=0,
+                max_groups=0)
+    for kw in (dict(t=0), dict(t=17), dict(n_experts=513), dict(top_k=17), dict(top_k=0), dict(ld_logits=100),
+               dict(groups=256, max_groups=10), dict(logits=0)):
+        assert lib.mi_moe_route(C.byref(hip.MiMoeRouteDesc(**{**base, **kw})), None) == 1, kw
+        assert hip.last_error().startswith("mi_moe_route")
+    cb = dict(t=2, hidden=2048, top_k=8, h=256, ldh=2048, weights=256, out=256, ldo=2048)
+    for kw in (dict(hidden=2044), dict(ldh=2047), dict(h=8), dict(shared=256, ld_shared=2048), dict(out=0)):
+        assert lib.mi_moe_combine(C.byref(hip.MiMoeCombineDesc(**{**cb, **kw})), None) == 1, kw
+        assert hip.last_error().startswith("mi_moe_combine")
