@@ -1,0 +1,227 @@
+"""Decode layers composed from the HIP kernels: ``h += mixer(norm1(h)); h += mlp(norm2(h))`` (``nn/decoder.py:14-26``)
+with a Gated DeltaNet (``nn/gdn.py:21-120``) or gated GQA (``nn/attention.py:27-155``) mixer and the gated MLP
+(``nn/mlp.py:14-30``), every projection an NVFP4 GEMV with its RMSNorm fused on load and its residual add fused in
+the epilogue. A step is 5 launches for the GDN layer and 7 for the attention layer; nothing allocates inside
+``step`` when ``out`` buffers are given, so a step can be captured into a HIP graph.
+
+Weights are synthetic (N(0, 0.02) quantized on the GPU with the reference NVFP4 rule) — there is no network for
+checkpoints; ``export()`` hands the quantized codes to a checker. Each layer owns its state (GDN conv + recurrent
+state, attention KV cache), so several instances are several layers of one model.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Dict, Optional
+
+import numpy as np
+
+from . import kernels
+from .formats import device as DV
+
+
+def _torch():
+    import torch
+    return torch
+
+
+@dataclass
+class QuantizedMatrix:
+    """NVFP4 codes as the reference's format holds them (``weight`` [N, K/2] u8, ``weight_scale`` [N, K/16] E4M3,
+    per-row tensor scale) plus the packed device weight."""
+
+    codes: "object"
+    scales: "object"
+    row_scale: "object"
+    packed: kernels.PackedWeight
+
+
+def nvfp4_matrix(n: int, k: int, gen, device, *, gate_up: bool = False, std: float = 0.02) -> QuantizedMatrix:
+    """A random N(0, std) matrix quantized to NVFP4 on the device and packed. ``gate_up``: [gate; up] halves of n/2
+    rows each (own tensor scales), rows interleaved by 8 for the silu·mul epilogue (``packs/transforms.py:16-24``)."""
+    torch = _torch()
+    if gate_up:
+        half = n // 2
+        gc, gs, g2 = DV.nvfp4_quantize(torch.randn(half, k, generator=gen, device=device) * std)
+        uc, us, u2 = DV.nvfp4_quantize(torch.randn(half, k, generator=gen, device=device) * std)
+        codes, scales = DV.interleave_rows(gc, uc), DV.interleave_rows(gs, us)
+        rs = DV.interleave_rows(torch.full((half, 1), g2, device=device),
+                                torch.full((half, 1), u2, device=device)).reshape(-1)
+    else:
+        codes, scales, s2 = DV.nvfp4_quantize(torch.randn(n, k, generator=gen, device=device) * std)
+        rs = torch.full((n,), s2, device=device)
+    n_pad = -(-n // 16) * 16
+    rs_pad = torch.cat([rs, rs.new_ones(n_pad - n)]) if n_pad != n else rs
+    packed = kernels.PackedWeight("nvfp4", n, k, 1, DV.pack_nvfp4(codes, scales), rs_pad.contiguous())
+    return QuantizedMatrix(codes, scales, rs, packed)
+
+
+def _gemv_bytes(n: int, k: int, m: int, *, n_out: Optional[int] = None, residual: bool = False) -> int:
+    """Algorithmic HBM bytes of one NVFP4 GEMV: codes + block scales (9/16 B per weight), x in, y out (+ residual in)."""
+    n_out = n if n_out is None else n_out
+    return n * k * 9 // 16 + m * k * 2 + m * n_out * 2 + (m * n_out * 2 if residual else 0)
+
+
+class GatedMLP:
+    """``down(silu(gate·x)·(up·x)) + residual`` with x = RMSNorm(h)(1 + w) fused into the gate|up GEMV."""
+
+    def __init__(self, hidden: int, inter: int, gen, device, eps: float = 1e-6):
+        torch = _torch()
+        self.hidden, self.inter, self.eps = hidden, inter, eps
+        self.norm_w = 1.0 + torch.randn(hidden, generator=gen, device=device) * 0.1     # (1 + w), float32
+        self.gate_up = nvfp4_matrix(2 * inter, hidden, gen, device, gate_up=True)
+        self.down = nvfp4_matrix(hidden, inter, gen, device)
+
+    def __call__(self, h, act=None, out=None):
+        act = kernels.gemv(self.gate_up.packed, h, epilogue="silu_mul", norm_w=self.norm_w, eps=self.eps, out=act)
+        return kernels.gemv(self.down.packed, act, epilogue="residual", residual=h, out=out)
+
+    def bytes_per_step(self, m: int) -> int:
+        return (_gemv_bytes(2 * self.inter, self.hidden, m, n_out=self.inter) + self.hidden * 4
+                + _gemv_bytes(self.hidden, self.inter, m, residual=True))
+
+
+class GdnDecoderLayer:
+    """Gated DeltaNet layer (27B geometry by default: hidden 5120, 16 key / 48 value heads of 128, conv 4, MLP
+    17408). Projection rows z|q|k|v|a|b (``nn/gdn.py:48-52``)."""
+
+    def __init__(self, *, hidden=5120, k_heads=16, v_heads=48, dk=128, dv=128, conv=4, inter=17408, eps=1e-6,
+                 device="cuda", seed=0):
+        torch = _torch()
+        gen = torch.Generator(device=device)
+        gen.manual_seed(seed)
+        self.hidden, self.hk, self.hv, self.dk, self.dv, self.conv, self.eps = hidden, k_heads, v_heads, dk, dv, conv, eps
+        self.conv_dim = 2 * k_heads * dk + v_heads * dv
+        self.n_proj = v_heads * dv + self.conv_dim + 2 * v_heads
+        self.norm_w = 1.0 + torch.randn(hidden, generator=gen, device=device) * 0.1
+        self.w_in = nvfp4_matrix(self.n_proj, hidden, gen, device)
+        self.w_out = nvfp4_matrix(hidden, v_heads * dv, gen, device)
+        self.conv_w = (torch.randn(self.conv_dim, conv, generator=gen, device=device) * 0.3).to(torch.bfloat16)
+        self.a_log = (torch.rand(v_heads, generator=gen, device=device) * 3 - 2).to(torch.bfloat16).float()
+        self.neg_exp_a = -torch.exp(self.a_log)
+        self.dt_bias = torch.randn(v_heads, generator=gen, device=device).to(torch.bfloat16).float()
+        self.gdn_norm_w = (1.0 + torch.randn(dv, generator=gen, device=device) * 0.2).to(torch.bfloat16).float()
+        self.mlp = GatedMLP(hidden, inter, gen, device, eps)
+        self.conv_state = [(torch.randn(self.conv_dim, conv - 1, generator=gen, device=device) * 0.5).to(torch.bfloat16),
+                           torch.zeros(self.conv_dim, conv - 1, dtype=torch.bfloat16, device=device)]
+        self.rec_state = torch.randn(v_heads, dk, dv, generator=gen, device=device) * 0.1
+        self.parity = 0
+        self._bufs: Dict[int, tuple] = {}
+
+    def buffers(self, m: int):
+        torch = _torch()
+        if m not in self._bufs:
+            dev = self.rec_state.device
+            self._bufs[m] = (torch.empty(m, self.n_proj, dtype=torch.bfloat16, device=dev),
+                             torch.empty(m, self.hv * self.dv, dtype=torch.bfloat16, device=dev),
+                             torch.empty(m, self.hidden, dtype=torch.bfloat16, device=dev),
+                             torch.empty(m, self.mlp.inter, dtype=torch.bfloat16, device=dev),
+                             torch.empty(m, self.hidden, dtype=torch.bfloat16, device=dev))
+        return self._bufs[m]
+
+    def step(self, h, out=None):
+        """One decode step over ``h [M, hidden]`` bf16 (M ≤ 16 tokens): returns the layer output; advances the state."""
+        proj, o, h1, act, h2 = self.buffers(h.shape[0])
+        out = h2 if out is None else out
+        kernels.gemv(self.w_in.packed, h, norm_w=self.norm_w, eps=self.eps, out=proj)
+        cin, cout = self.conv_state[self.parity], self.conv_state[1 - self.parity]
+        kernels.gdn_step(proj, cin, cout, self.rec_state, self.rec_state, conv_w=self.conv_w, neg_exp_a=self.neg_exp_a,
+                         dt_bias=self.dt_bias, norm_w=self.gdn_norm_w, k_heads=self.hk, v_heads=self.hv, dk=self.dk,
+                         dv=self.dv, conv_width=self.conv, eps=self.eps, out=o)
+        self.parity ^= 1
+        kernels.gemv(self.w_out.packed, o, epilogue="residual", residual=h, out=h1)
+        return self.mlp(h1, act=act, out=out)
+
+    def mixer_bytes(self, m: int) -> int:
+        state = 2 * self.hv * self.dk * self.dv * 4 + 2 * self.conv_dim * (self.conv - 1) * 2
+        params = self.conv_dim * self.conv * 2 + 3 * self.hv * 4 + self.dv * 4
+        return state + params + m * self.n_proj * 2 + m * self.hv * self.dv * 2
+
+    def bytes_per_step(self, m: int) -> int:
+        return (_gemv_bytes(self.n_proj, self.hidden, m) + self.hidden * 4 + self.mixer_bytes(m)
+                + _gemv_bytes(self.hidden, self.hv * self.dv, m, residual=True) + self.mlp.bytes_per_step(m))
+
+    def export(self) -> dict:
+        """Host copies of everything the checker needs (quantized codes, parameters, state)."""
+        def q(mat):
+            return {"weight": mat.codes.cpu().numpy(), "weight_scale": mat.scales.cpu().numpy(),
+                    "row_scale": mat.row_scale.cpu().numpy()}
+        return {"w_in": q(self.w_in), "w_out": q(self.w_out), "gate_up": q(self.mlp.gate_up), "down": q(self.mlp.down),
+                "norm1": self.norm_w.cpu().numpy(), "norm2": self.mlp.norm_w.cpu().numpy(),
+                "conv_w": self.conv_w.float().cpu().numpy(), "a_log": self.a_log.cpu().numpy(),
+                "dt_bias": self.dt_bias.cpu().numpy(), "gdn_norm_w": self.gdn_norm_w.cpu().numpy(),
+                "conv_state": self.conv_state[self.parity].float().cpu().numpy(),
+                "rec_state": self.rec_state.cpu().numpy()}
+
+
+class AttnDecoderLayer:
+    """Gated GQA layer (hidden 5120, 24 query / 4 KV heads of 128, partial RoPE 64 at θ = 1e6, q/k norm, output
+    gate, int8 KV cache of ``ctx`` tokens, MLP 17408). Projection rows q|gate per head, then k, v."""
+
+    def __init__(self, *, hidden=5120, heads=24, kv_heads=4, head_dim=128, rotary_dim=64, theta=1e6, ctx=32768,
+                 inter=17408, eps=1e-6, device="cuda", seed=0):
+        torch = _torch()
+        gen = torch.Generator(device=device)
+        gen.manual_seed(seed)
+        self.hidden, self.heads, self.kv, self.d, self.eps = hidden, heads, kv_heads, head_dim, eps
+        self.n_proj = heads * 2 * head_dim + 2 * kv_heads * head_dim
+        self.norm_w = 1.0 + torch.randn(hidden, generator=gen, device=device) * 0.1
+        self.w_qkv = nvfp4_matrix(self.n_proj, hidden, gen, device)
+        self.w_o = nvfp4_matrix(hidden, heads * head_dim, gen, device)
+        self.q_norm = (1.0 + torch.randn(head_dim, generator=gen, device=device) * 0.1).to(torch.bfloat16).float()
+        self.k_norm = (1.0 + torch.randn(head_dim, generator=gen, device=device) * 0.1).to(torch.bfloat16).float()
+        self.cos, self.sin = kernels.rope_tables(theta, rotary_dim, ctx, device=device)
+        self.cache = kernels.KVCache(kv_heads, ctx, head_dim, device=device)
+        self.mlp = GatedMLP(hidden, inter, gen, device, eps)
+        self._bufs: Dict[int, tuple] = {}
+
+    def fill_cache(self, n: int, gen=None):
+        """Random int8 codes and f16 scales (N(0, 1) K/V quantized per token) in the first ``n`` positions."""
+        torch = _torch()
+        c = self.cache
+        c.k_codes[:, :n].random_(-127, 128, generator=gen)
+        c.v_codes[:, : -(-n // 64)].random_(-127, 128, generator=gen)
+        c.k_scales[:, :n] = 3.0 / 127
+        c.v_scales[:, :n] = 3.0 / 127
+
+    def buffers(self, m: int):
+        torch = _torch()
+        if m not in self._bufs:
+            dev = self.norm_w.device
+            self._bufs[m] = (torch.empty(m, self.n_proj, dtype=torch.bfloat16, device=dev),
+                             torch.empty(m, self.heads * self.d, dtype=torch.bfloat16, device=dev),
+                             torch.empty(m, self.hidden, dtype=torch.bfloat16, device=dev),
+                             torch.empty(m, self.mlp.inter, dtype=torch.bfloat16, device=dev),
+                             torch.empty(m, self.hidden, dtype=torch.bfloat16, device=dev))
+        return self._bufs[m]
+
+    def step(self, h, pos: int, out=None):
+        """One decode step over ``h [M, hidden]`` at positions ``pos..pos+M-1``; the new k/v enter the cache."""
+        proj, o, h1, act, h2 = self.buffers(h.shape[0])
+        out = h2 if out is None else out
+        kernels.gemv(self.w_qkv.packed, h, norm_w=self.norm_w, eps=self.eps, out=proj)
+        kernels.gqa_decode(proj, self.cache, pos, heads=self.heads, rope_cos=self.cos, rope_sin=self.sin, gate=True,
+                           q_norm=self.q_norm, k_norm=self.k_norm, eps=self.eps, out=o)
+        kernels.gemv(self.w_o.packed, o, epilogue="residual", residual=h, out=h1)
+        return self.mlp(h1, act=act, out=out)
+
+    def mixer_bytes(self, m: int, pos: int) -> int:
+        n = pos + m
+        return (n * self.kv * (2 * self.d + 4) + m * self.n_proj * 2 + m * self.heads * self.d * 2
+                + m * self.kv * (2 * self.d + 4))
+
+    def bytes_per_step(self, m: int, pos: int) -> int:
+        return (_gemv_bytes(self.n_proj, self.hidden, m) + self.hidden * 4 + self.mixer_bytes(m, pos)
+                + _gemv_bytes(self.hidden, self.heads * self.d, m, residual=True) + self.mlp.bytes_per_step(m))
+
+    def export(self) -> dict:
+        def q(mat):
+            return {"weight": mat.codes.cpu().numpy(), "weight_scale": mat.scales.cpu().numpy(),
+                    "row_scale": mat.row_scale.cpu().numpy()}
+        c = self.cache
+        return {"w_qkv": q(self.w_qkv), "w_o": q(self.w_o), "gate_up": q(self.mlp.gate_up), "down": q(self.mlp.down),
+                "norm1": self.norm_w.cpu().numpy(), "norm2": self.mlp.norm_w.cpu().numpy(),
+                "q_norm": self.q_norm.cpu().numpy(), "k_norm": self.k_norm.cpu().numpy(),
+                "cos": self.cos.float().cpu().numpy(), "sin": self.sin.float().cpu().numpy(),
+                "k_codes": c.k_codes.cpu().numpy(), "k_scales": c.k_scales.cpu().numpy(),
+                "v_codes": c.v_codes_token_major().cpu().numpy(), "v_scales": c.v_scales.cpu().numpy()}
