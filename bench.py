@@ -1,21 +1,28 @@
 #!/usr/bin/env python3
-"""Decode-layer benchmark on one MI355X — BASELINE.json's metric on configs[1]: the 27B-class NVFP4 gated MLP
-(gate|up 2×[17408×5120] with the silu·mul epilogue, then down [5120×17408] with the residual add) at M = 1 decode,
-with the M = 8 verify step measured beside it.
+"""Decode-layer benchmark on one MI355X — BASELINE.json's metric: decode-layer HBM GB/s (% of the 8 TB/s peak) and
+tokens/s at M = 1 and M = 8.
 
-One step = one MLP forward over one token batch. Inputs and weights are resident in HBM before the timed region;
-the weights rotate through ≥ 2 GB of distinct copies so the 256 MB MALL cannot serve them. Synthetic data:
-weights N(0, 0.02) quantized with the reference NVFP4 rule, activations N(0, 1) in BF16.
+The workload (``config.workload``) is one 27B-class decode layer, ``h += mixer(norm1(h)); h += mlp(norm2(h))``:
+a Gated DeltaNet mixer (16 key / 48 value heads of 128, conv 4; in_proj 16480×5120 and out_proj 5120×6144 NVFP4)
+and the NVFP4 gated MLP of BASELINE configs[1] (gate|up 2×17408×5120 with silu·mul, down 5120×17408 with the
+residual). ``value`` is that layer's algorithmic HBM bytes ÷ its step time at M = 1. Beside it: the same layer at
+M = 8, the gated-GQA layer (24 q / 4 KV heads of 128, int8 KV cache at a 32K context; configs[2]) at M = 1 and 8,
+and the MLP alone.
 
-Prints ONE JSON line. ``value`` is the MLP's algorithmic HBM GB/s at M = 1; ``roofline`` is for the dominant kernel
-(the gate|up GEMV); ``cpu_baseline`` times the C/OpenMP restatement of the reference's CPU oracle GEMV on the host.
+One step = one layer forward over one token batch. Weights, states and KV caches are resident in HBM before the
+timed region; the step rotates over ``--layers`` distinct layer instances (≥ 2 GB in all), so the 256 MB MALL
+cannot serve them — like consecutive layers of one model. The timed steps are one HIP graph (host launch cost is
+not in the number), bracketed by HIP events on the stream they run on. Synthetic data: weights N(0, 0.02) quantized
+with the reference NVFP4 rule on the GPU, activations N(0, 1) BF16, GDN state N(0, 0.1), KV codes uniform int8.
+
+Prints ONE JSON line. ``roofline`` is for the dominant kernel (the gate|up GEMV, 34816×5120 NVFP4 at M = 1) timed
+alone the same way; ``cpu_baseline`` times the C/OpenMP restatement of the reference's CPU oracle GEMV on the host.
 """
 
 from __future__ import annotations
 
 import argparse
 import json
-import os
 import sys
 import time
 from pathlib import Path
@@ -23,26 +30,43 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "lithos-metal_amd"))
 
-HIDDEN, INTER = 5120, 17408
 HBM_PEAK_GBS = 8000.0
+CTX = 32768
 
 
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=200)
-    p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--copies-gb", type=float, default=2.2)
+    p.add_argument("--steps", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--layers", type=int, default=10, help="distinct layer instances the steps rotate over")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--only", choices=["gdn", "attn", "mlp", "gateup"], default=None,
+                   help="time one workload only (profiling runs)")
     return p.parse_args()
 
 
-def mlp_bytes(m: int) -> int:
-    w = 3 * INTER * HIDDEN * 9 // 16                   # three NVFP4 matrices: 0.5 B codes + 1/16 B scales per weight
-    act = m * HIDDEN * 2 + m * INTER * 2                 # gate|up: x in, act out
-    act += m * INTER * 2 + m * HIDDEN * 2 * 2            # down: act in, residual in, y out
-    return w + act
+def timed_graph(fn, steps, warmup, stream):
+    """Run ``fn(i)`` for ``warmup`` steps eagerly, capture ``steps`` of them as one graph, replay twice and time the
+    second replay with HIP events on ``stream``. Returns ms per step."""
+    import torch
+    from monolith_mi355.runtime import hip
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(steps):
+            fn(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    t0, t1 = hip.Event(), hip.Event()
+    t0.record(stream)
+    graph.replay()
+    t1.record(stream)
+    t1.synchronize()
+    return t0.elapsed_ms(t1) / steps
 
 
 def main():
@@ -53,93 +77,76 @@ def main():
         sys.exit(2)
     import torch
     from monolith_mi355 import kernels
-    from monolith_mi355.formats import device as DV
+    from monolith_mi355.layers import AttnDecoderLayer, GdnDecoderLayer
     from monolith_mi355.runtime import hip
 
     hip.load()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    g = torch.Generator(device=dev)
-    g.manual_seed(1)
+    stream = torch.cuda.Stream(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1)
+    n = args.layers
+    out = {}
 
-    # ---- weights: quantize once, replicate into distinct HBM copies --------------------------------------------
-    def quant(n, k):
-        w = torch.randn(n, k, generator=g, device=dev) * 0.02
-        return DV.nvfp4_quantize(w)
-    gc, gs, g2 = quant(INTER, HIDDEN)
-    uc, us, u2 = quant(INTER, HIDDEN)
-    dc, ds, d2 = quant(HIDDEN, INTER)
-    gu_codes = DV.interleave_rows(gc, uc)
-    gu_scales = DV.interleave_rows(gs, us)
-    gu_rs = DV.interleave_rows(torch.full((INTER, 1), g2, device=dev), torch.full((INTER, 1), u2, device=dev)).reshape(-1)
-    gu_pack = DV.pack_nvfp4(gu_codes, gu_scales)
-    dn_pack = DV.pack_nvfp4(dc, ds)
-    dn_rs = torch.full((HIDDEN,), d2, device=dev)
-    del gc, gs, uc, us, dc, ds, gu_codes, gu_scales
-    per_copy = gu_pack.numel() + dn_pack.numel()
-    copies = max(2, int(args.copies_gb * 1e9 // per_copy) + 1)
-    gu_w = [kernels.PackedWeight("nvfp4", 2 * INTER, HIDDEN, 1, gu_pack.clone(), gu_rs) for _ in range(copies)]
-    dn_w = [kernels.PackedWeight("nvfp4", HIDDEN, INTER, 1, dn_pack.clone(), dn_rs) for _ in range(copies)]
+    def xin(m):
+        return torch.randn(m, 5120, generator=gen, device=dev).to(torch.bfloat16)
 
-    def run(m, steps, warmup):
-        x = torch.randn(m, HIDDEN, generator=g, device=dev).to(torch.bfloat16)
-        h = torch.randn(m, HIDDEN, generator=g, device=dev).to(torch.bfloat16)
-        act = torch.empty(m, INTER, dtype=torch.bfloat16, device=dev)
-        y = torch.empty(m, HIDDEN, dtype=torch.bfloat16, device=dev)
-        stream = torch.cuda.current_stream()
+    with torch.cuda.stream(stream):
+        gdn = [GdnDecoderLayer(seed=10 + i, device=dev) for i in range(n)] if args.only in (None, "gdn", "mlp", "gateup") else []
+        for m in (1, 8):
+            if args.only not in (None, "gdn"):
+                break
+            x = xin(m)
+            ms = timed_graph(lambda i: gdn[i % n].step(x), args.steps, args.warmup, stream)
+            out[f"gdn_m{m}"] = (ms, gdn[0].bytes_per_step(m))
+        for m in (1, 8):
+            if args.only not in (None, "mlp"):
+                break
+            x = xin(m)
+            ms = timed_graph(lambda i: gdn[i % n].mlp(x), args.steps, args.warmup, stream)
+            out[f"mlp_m{m}"] = (ms, gdn[0].mlp.bytes_per_step(m))
+        if args.only in (None, "gateup"):
+            x = xin(1)
+            act = torch.empty(1, 17408, dtype=torch.bfloat16, device=dev)
+            ms = timed_graph(lambda i: kernels.gemv(gdn[i % n].mlp.gate_up.packed, x, epilogue="silu_mul", out=act),
+                             args.steps, args.warmup, stream)
+            out["gateup_m1"] = (ms, 34816 * 5120 * 9 // 16 + 5120 * 2 + 17408 * 2)
+        del gdn
+        torch.cuda.empty_cache()
+        if args.only in (None, "attn"):
+            attn = [AttnDecoderLayer(seed=40 + i, ctx=CTX, device=dev) for i in range(n)]
+            for layer in attn:
+                layer.fill_cache(CTX, gen)
+            pos = CTX - 16
+            for m in (1, 8):
+                x = xin(m)
+                ms = timed_graph(lambda i: attn[i % n].step(x, pos), args.steps, args.warmup, stream)
+                out[f"attn_m{m}"] = (ms, attn[0].bytes_per_step(m, pos))
+            del attn
 
-        def step(i):
-            kernels.gemv(gu_w[i % copies], x, epilogue="silu_mul", out=act)
-            kernels.gemv(dn_w[i % copies], act, epilogue="residual", residual=h, out=y)
+    def rate(key):
+        ms, b = out[key]
+        gbs = b / (ms * 1e-3) / 1e9
+        return ms, b, gbs
 
-        for i in range(warmup):
-            step(i)
-        torch.cuda.synchronize()
-        # the timed steps as one HIP graph, so host launch cost is not in the number
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            for i in range(steps):
-                step(i)
-        graph.replay()
-        torch.cuda.synchronize()
-        t0 = hip.Event(); t1 = hip.Event()
-        torch.cuda.synchronize()
-        t0.record(stream)
-        graph.replay()
-        t1.record(stream)
-        t1.synchronize()
-        ms = t0.elapsed_ms(t1) / steps
-        # the dominant kernel alone (gate|up GEMV), HIP events on the stream it is launched on
-        kg = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(kg):
-            for i in range(steps):
-                kernels.gemv(gu_w[i % copies], x, epilogue="silu_mul", out=act)
-        kg.replay()
-        torch.cuda.synchronize()
-        t0.record(stream)
-        kg.replay()
-        t1.record(stream)
-        t1.synchronize()
-        k_ms = t0.elapsed_ms(t1) / steps
-        return ms, k_ms
-
-    ms1, kms1 = run(1, args.steps, args.warmup)
-    ms8, kms8 = run(8, args.steps, args.warmup)
-    b1, b8 = mlp_bytes(1), mlp_bytes(8)
-    gbs1 = b1 / (ms1 * 1e-3) / 1e9
-    gbs8 = b8 / (ms8 * 1e-3) / 1e9
-    gu_bytes = 2 * INTER * HIDDEN * 9 // 16 + HIDDEN * 2 + INTER * 2
-    k_gbs = gu_bytes / (kms1 * 1e-3) / 1e9
+    if args.only:
+        print(json.dumps({k: {"ms": round(v[0], 5), "bytes": v[1], "GB/s": round(rate(k)[2], 1)} for k, v in out.items()}))
+        return
 
     traffic = None
     prof = ROOT / "profiles" / "gemv_nvfp4_gateup_m1_traffic.json"
     if prof.exists():
         traffic = json.loads(prof.read_text()).get("hbm_bytes_per_launch")
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
 
-    cpu = None
-    if not args.no_cpu:
-        cpu = cpu_baseline(args.cpu_seconds)
+    def entry(key, m):
+        ms, b, gbs = rate(key)
+        return {"ms_per_step": round(ms, 5), "GB/s": round(gbs, 1), "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+                "tokens_per_s": round(m * 1e3 / ms, 1), "bytes_per_step": b}
 
+    ms1, b1, gbs1 = rate("gdn_m1")
+    k_ms, k_bytes, k_gbs = rate("gateup_m1")
     line = {
         "metric": "decode-layer HBM GB/s (% of peak) + tokens/s at M=1 and M=8, one MI355X",
         "value": round(gbs1, 1),
@@ -151,20 +158,24 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "nvfp4 weights x bf16 activations, fp32 accumulate",
-        "data": "synthetic: weights N(0,0.02) quantized to NVFP4 (reference rule), activations N(0,1) bf16",
-        "config": {"workload": "27B NVFP4 gated MLP decode step: gate|up 2x[17408x5120] silu_mul + down "
-                               "[5120x17408] residual (BASELINE configs[1])", "m": 1, "hidden": HIDDEN,
-                   "intermediate": INTER, "weight_copies": copies, "bytes_per_step": b1},
+        "dtype": "nvfp4 weights x bf16 activations, fp32 accumulate; fp32 GDN state; int8 KV cache",
+        "data": "synthetic: weights N(0,0.02) quantized to NVFP4 (reference rule), activations N(0,1) bf16, "
+                "GDN state N(0,0.1), KV int8",
+        "config": {"workload": "27B decode layer, M=1: GDN mixer (hk16/hv48 x128, in_proj 16480x5120, out_proj "
+                               "5120x6144) + NVFP4 gated MLP (gate|up 2x17408x5120, down 5120x17408), fused norms "
+                               "and residuals", "m": 1, "hidden": 5120, "layers_rotated": args.layers,
+                   "bytes_per_step": b1},
         "pct_of_hbm_peak": round(100 * gbs1 / HBM_PEAK_GBS, 2),
         "tokens_per_s_m1": round(1e3 / ms1, 1),
-        "m8": {"ms_per_step": round(ms8, 5), "GB/s": round(gbs8, 1), "pct_of_hbm_peak": round(100 * gbs8 / HBM_PEAK_GBS, 2),
-               "tokens_per_s": round(8e3 / ms8, 1), "bytes_per_step": b8},
-        "roofline": {"kernel": "gemv (NVFP4 gate|up 34816x5120, silu_mul, M=1)", "bound": "hbm",
+        "gdn_layer_m8": entry("gdn_m8", 8),
+        "attn_layer_ctx32k_m1": entry("attn_m1", 1),
+        "attn_layer_ctx32k_m8": entry("attn_m8", 8),
+        "mlp_m1": entry("mlp_m1", 1),
+        "mlp_m8": entry("mlp_m8", 8),
+        "roofline": {"kernel": "gemv_dot (NVFP4 gate|up 34816x5120, silu_mul, M=1)", "bound": "hbm",
                      "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "algorithmic_bytes": gu_bytes, "avg_launch_us": round(kms1 * 1e3, 3),
-                     "m8_avg_launch_us": round(kms8 * 1e3, 3)},
+                     "algorithmic_bytes": k_bytes, "avg_launch_us": round(k_ms * 1e3, 3)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
@@ -172,16 +183,16 @@ def main():
 
 def cpu_baseline(seconds: float):
     """The C/OpenMP restatement of the reference's oracle GEMV (dequantize to FP32, multiply) on this host's cores,
-    over the down projection [5120×17408] at M = 1, repeated for about ``seconds``; reported as the same MLP GB/s
-    figure (the MLP's bytes ÷ three GEMVs' time at that rate)."""
+    over the layer's down projection [5120×17408] at M = 1, repeated for about ``seconds``."""
     import numpy as np
     sys.path.insert(0, str(ROOT))
     from oracle import cpu as OC
+    hidden, inter = 5120, 17408
     rng = np.random.default_rng(0)
-    m = {"weight": rng.integers(0, 256, size=(HIDDEN, INTER // 2), dtype=np.uint8),
-         "weight_scale": rng.integers(0x20, 0x48, size=(HIDDEN, INTER // 16), dtype=np.uint8),
+    m = {"weight": rng.integers(0, 256, size=(hidden, inter // 2), dtype=np.uint8),
+         "weight_scale": rng.integers(0x20, 0x48, size=(hidden, inter // 16), dtype=np.uint8),
          "weight_scale_2": 0.02 / (6 * 448) * 64}
-    x = rng.standard_normal((1, INTER)).astype(np.float32)
+    x = rng.standard_normal((1, inter)).astype(np.float32)
     nt = OC.threads()
     OC.nvfp4_gemv(m, x, nt)
     reps, t0 = 0, time.perf_counter()
@@ -189,11 +200,10 @@ def cpu_baseline(seconds: float):
         OC.nvfp4_gemv(m, x, nt)
         reps += 1
     dt = (time.perf_counter() - t0) / reps
-    w_bytes = HIDDEN * INTER * 9 // 16
-    gbs = w_bytes / dt / 1e9
-    return {"value": round(gbs, 2), "unit": "GB/s", "cores": nt, "kind": "port",
-            "sample": f"{reps} runs of the NVFP4 down GEMV [5120x17408] at M=1 ({seconds:.0f} s), "
-                      f"{dt * 1e3:.2f} ms each; MLP step at this rate = {3 * dt * 1e3:.1f} ms"}
+    w_bytes = hidden * inter * 9 // 16
+    return {"value": round(w_bytes / dt / 1e9, 2), "unit": "GB/s", "cores": nt, "kind": "port",
+            "sample": f"{reps} runs of the layer's NVFP4 down GEMV [5120x17408] at M=1 ({seconds:.0f} s), "
+                      f"{dt * 1e3:.2f} ms each, GB/s of its weight bytes"}
 
 
 if __name__ == "__main__":
