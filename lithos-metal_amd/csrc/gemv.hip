@@ -5,23 +5,23 @@
 // ops/norm.py:1-6) and a residual / silu·mul epilogue. Grouped mode is the MoE expert GEMV (ops/moe.py `moe_gemv`):
 // a group is one expert with the ≤ 16 (token, slot) pairs routed to it, so a step streams exactly the chosen experts.
 //
-// MI355X design:
-//  * One wave64 owns RT 16-row tiles over a run of 128-column chunks. Each chunk of a tile is one 1152-byte unit: a
-//    fully coalesced 1 KiB load of 16-byte code words (lane l: row l%16, 32 codes) plus 128 B of block scales.
-//  * The products run on MFMA v_mfma_f32_16x16x32_{f16,bf16} with A = activations (16 token rows, padded with an LDS
-//    zero row) and B = decoded weights. NVFP4 decodes to exact F16: v_cvt_scalef32_pk_f16_fp4 applies the power-of-two
-//    part of the E4M3 block scale, a packed F16 multiply its 3-bit mantissa (e2m1·e4m3 has ≤ 6 significant bits and
-//    lies in [2^-10, 2688], so every decoded weight is exact). INT4 codes become exact F16 integers (0x6400|c − 1024)
-//    and the affine term is applied per group of 64 as scale·Σcx + bias·Σx.
-//  * F16 activations: each token row staged in LDS is multiplied by a power of two 2^-P that brings its max into
-//    [2^14, 2^15), converted BF16 → F16 (exact above 2^-14, i.e. everything within 2^28 of the row max), and the
-//    partial sums are multiplied back by 2^P — BF16 range without F16 overflow.
-//  * Each wave keeps 8/RT chunks of loads in flight (a register ring), issued before the activations are staged, so
-//    the staging prologue and the LDS barriers hide under HBM traffic.
-//  * K is split across the waves of a workgroup (reduced through LDS in a fixed order, deterministic). When the
-//    staged activations of the whole K would not fit LDS (M = 8 over K = 17408), the workgroup walks K in windows,
-//    restaging per window. There is no cross-workgroup reduction: on gfx950 the agent-scope fences it needs
-//    (an L2 writeback + invalidate per workgroup) cost more than the GEMV.
+// MI355X design. The pack streams 16-row tiles in 128-column chunks; lane l of a wave owns row l%16 and the 32
+// columns 32·(l/16)… of a chunk, one fully coalesced 1 KiB load per chunk (NVFP4 block scales: one 16-byte load per
+// 8 chunks). What sets the speed is how many of those loads are in flight per CU and how cheaply the activations
+// reach every wave; two kernels:
+//  * gemv_row (M <= 2): a workgroup per tile, its waves splitting K into slices of KW = 4/8/16 chunks; each wave
+//    issues its activation slice, the slice's scales and all KW weight chunks at once, stages the activations in its
+//    own LDS region, and computes on the VALU: NVFP4 → BF16 pairs with v_cvt_scalef32_pk_bf16_fp4 (e2m1 × the power-
+//    of-two part of the E4M3 block scale, exact), v_dot2_f32_bf16 against the BF16 activations as they are, the
+//    scale's 3-bit mantissa applied once per block of 16; INT4 as BF16 128 + c corrected by 128·Σx per segment. The
+//    K slices meet in LDS (fixed order). Many short waves keep ~all weight bytes of the CU's share in flight.
+//  * gemv_tk (M ≤ 16): MFMA v_mfma_f32_16x16x32_{f16,bf16} with the activations as the A operand (token rows,
+//    power-of-two prescaled into F16 range: exact above 2^-14 of the row max) and the decoded weights as B (NVFP4 →
+//    exact F16 by v_cvt_scalef32_pk_f16_fp4 and a packed multiply by the mantissa factor). A workgroup stages one K
+//    split of the activations once and streams many tiles against it, so the activations are re-read per workgroup,
+//    not per tile; long K is split across workgroups with FP32 partials added in order by gemv_tk_reduce.
+// There is no cross-workgroup reduction inside a kernel: on gfx950 the agent-scope fences it needs (an L2 write-
+// back + invalidate per workgroup) cost more than the GEMV.
 #include "mi_common.h"
 
 #include <algorithm>
@@ -38,12 +38,27 @@ constexpr int FMT_NVFP4 = MI_FMT_NVFP4;
 constexpr int FMT_INT4 = MI_FMT_INT4_AFFINE;
 constexpr int FMT_BF16 = MI_FMT_BF16;
 
-constexpr int UNIT_Q = 1152;   // nvfp4 / int4 unit: 1024 B codes + 128 B scales
+constexpr int UNIT_Q = 1152;   // int4 unit: 1024 B codes + 128 B (scale, bias) pairs
 constexpr int UNIT_B = 1024;   // bf16 unit: 16 rows × 32 columns
 constexpr int GROUP_REC = 18;  // grouped-mode record: expert, count, 16 pair ids
 
 __host__ __device__ constexpr int unit_bytes(int fmt) { return fmt == FMT_BF16 ? UNIT_B : UNIT_Q; }
 __host__ __device__ constexpr int chunk_cols(int fmt) { return fmt == FMT_BF16 ? 32 : 128; }
+
+// NVFP4 tile layout: groups of 8 chunks, each [g × 1 KiB codes][scale block: 64 pieces of 16 B (8 B if g <= 4)]
+__host__ __device__ inline int nv_group_chunks(int gi, int chunks) { return min(8, chunks - 8 * gi); }
+__host__ __device__ inline int nv_piece(int g) { return g > 4 ? 16 : 8; }
+__host__ __device__ inline long long nv_tile_bytes(int chunks) {
+  const int r = chunks & 7;
+  return (long long)(chunks >> 3) * 9216 + (r ? r * 1024 + 64 * nv_piece(r) : 0);
+}
+__host__ __device__ inline long long nv_code_off(int c) { return (long long)(c >> 3) * 9216 + (c & 7) * 1024; }
+__host__ __device__ inline long long nv_scale_off(int gi, int chunks) {
+  return (long long)gi * 9216 + nv_group_chunks(gi, chunks) * 1024;
+}
+__host__ __device__ inline long long tile_bytes(int fmt, int chunks) {
+  return fmt == FMT_NVFP4 ? nv_tile_bytes(chunks) : (long long)chunks * unit_bytes(fmt);
+}
 
 struct Args {
   const uint8_t* w;
@@ -54,13 +69,18 @@ struct Args {
   const float* norm_w;
   const int32_t* groups;
   long long expert_stride;  // bytes between experts' packs
+  long long tile_stride;    // bytes per tile
   float eps;
   int ldx, ldy, ldr;
   int n, k, m;
-  int n_tiles, chunks, row_blocks;
-  int kw, win, wave_lds;    // chunks per wave (its K slice), chunks per staged window, LDS bytes per wave
+  int n_tiles, chunks;
   int epilogue, top_k, x_per_slot, out_f32;
-  int lds_rows, lds_ld;     // staged token rows, LDS row stride (elements)
+  int lds_rows;             // gemv_tk: staged token rows
+  int tb;                   // gemv_tk: 16-row tiles per workgroup
+  int ks, kc;               // gemv_tk: K splits, chunks per split
+  float* part;              // gemv_tk with ks > 1: FP32 partials [ks][m][n_tiles·16]
+  int row_ld;               // gemv_row: LDS row stride of a wave's staged slice (elements)
+  int row_wave_lds;         // gemv_row: LDS bytes per wave
 };
 
 // ---- weight decode ---------------------------------------------------------------------------------------------
@@ -151,449 +171,140 @@ __device__ __forceinline__ void emit(const Args& a, const int32_t* pairs, int cn
   }
 }
 
-// ---- the kernel ------------------------------------------------------------------------------------------------
+
+// ---- one chunk of one tile in registers ---------------------------------------------------------------------
 template <int FMT>
-struct Units {               // one chunk of one tile, in registers
-  uint4 q;
-  uint32_t s;                // nvfp4: two E4M3 block-scale bytes
-  uint2 sb;                  // int4: (scale, bias) pairs of the chunk's two groups
+struct Units {
+  uint4 q;                   // lane l: 16 bytes of codes (NVFP4 / INT4) or 8 BF16 values
+  uint32_t s;                // NVFP4 (gemv_tk): the lane's two E4M3 block-scale bytes
+  uint2 sb;                  // INT4: (scale, bias) pairs of the chunk's two groups
 };
 
-template <int FMT>
-__device__ __forceinline__ void load_unit(Units<FMT>& u, const uint8_t* p, int lane) {
-  u.q = *reinterpret_cast<const uint4*>(p + 16 * lane);
-  if constexpr (FMT == FMT_NVFP4) u.s = *reinterpret_cast<const uint16_t*>(p + 1024 + 2 * lane);
-  if constexpr (FMT == FMT_INT4) u.sb = *reinterpret_cast<const uint2*>(p + 1024 + 8 * (lane & 15));
+// chunk c of the tile at `tb`; NVFP4 scales for gemv_tk from the group's scale block (gemv_row loads whole pieces)
+template <int FMT, bool SCALE>
+__device__ __forceinline__ void load_chunk(Units<FMT>& u, const uint8_t* tb, int c, int chunks, int lane) {
+  if constexpr (FMT == FMT_NVFP4) {
+    u.q = *reinterpret_cast<const uint4*>(tb + nv_code_off(c) + 16 * lane);
+    if constexpr (SCALE) {
+      const int gi = c >> 3;
+      u.s = *reinterpret_cast<const uint16_t*>(tb + nv_scale_off(gi, chunks) + nv_piece(nv_group_chunks(gi, chunks)) * lane +
+                                               2 * (c & 7));
+    }
+  } else {
+    const uint8_t* p = tb + (long long)c * unit_bytes(FMT);
+    u.q = *reinterpret_cast<const uint4*>(p + 16 * lane);
+    if constexpr (FMT == FMT_INT4) u.sb = *reinterpret_cast<const uint2*>(p + 1024 + 8 * (lane & 15));
+  }
 }
 
 // orders this wave's LDS writes before its later LDS reads by other lanes (one wave's LDS requests complete in
 // order; this keeps the compiler from moving them)
 __device__ __forceinline__ void wave_lds_sync() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); __builtin_amdgcn_wave_barrier(); }
 
-// Per-wave LDS region (2-byte elements): xs[lds_rows][lds_ld] staged activations of the wave's current window,
-// then pscale[16], and (int4) gsum[win/64][16]. After the regions: stat[waves][16] (fused-norm partial sums).
-template <int FMT, int RT>
-__global__ __launch_bounds__(512) void gemv_t16(Args a) {
-  constexpr int D = 8 / RT;                      // prefetch depth in chunks
+// ---- gemv_row: M <= 2 ------------------------------------------------------------------------------------------
+// Workgroup = one 16-row tile (blockIdx.x) of one group (blockIdx.y, MoE); wave w = K slice [w·KW, w·KW + KW).
+// LDS: per wave xs[MT][row_ld] (INT4: then seg[MT][KW][8]) | stat[S][2] | red[S][MT][16].
+template <int FMT, int MT, int KW>
+__global__ __launch_bounds__(KW == 16 ? 640 : 1024) void gemv_row(Args a) {
   constexpr int KC = chunk_cols(FMT);
-  constexpr int UB = unit_bytes(FMT);
-  constexpr int XV = 4;                          // activation vectors per lane loaded ahead of the weights
+  constexpr int NPL = MT * KW * KC / 8 / 64 > 0 ? MT * KW * KC / 8 / 64 : 1;   // activation vectors per lane
+  constexpr int NG = FMT == FMT_NVFP4 ? (KW + 7) / 8 : 0;                         // scale pieces per wave
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int nwaves = blockDim.x >> 6;
-  const int rb = blockIdx.x;
-  const int grp = blockIdx.y;
-
-  // ---- group: which matrix and which token rows ---------------------------------------------------------------
+  const int S = blockDim.x >> 6;
+  const int tile = blockIdx.x;
   int expert = 0, cnt = a.m;
   const int32_t* pairs = nullptr;
   if (a.groups) {
-    const int32_t* g = a.groups + grp * GROUP_REC;
+    const int32_t* g = a.groups + blockIdx.y * GROUP_REC;
     expert = g[0];
     cnt = g[1];
     pairs = g + 2;
-    if (cnt <= 0 || expert < 0) return;      // the whole workgroup leaves together: no barrier is skipped
-  }
-  if (cnt > a.lds_rows) cnt = a.lds_rows;
-  auto xrow_of = [&](int j) -> long long {     // activation row of token j (grouped mode: the pair's row)
-    if (!pairs) return j;
-    const int p = pairs[j];
-    return a.x_per_slot ? p : p / a.top_k;
-  };
-
-  // ---- this wave: K slice [c0, c0 + kw) chunks, windows of `win` chunks --------------------------------------
-  const int c0 = wave * a.kw;
-  const int win = a.win;                      // chunks per window
-  const int wcols = win * KC;
-  uint8_t* wbase_lds = smem + (size_t)wave * a.wave_lds;
-  uint16_t* xs = reinterpret_cast<uint16_t*>(wbase_lds);
-  float* pscale = reinterpret_cast<float*>(wbase_lds + (size_t)a.lds_rows * a.lds_ld * 2);   // [16] 2^p
-  float* pinv = pscale + 16;                                                                  // [16] 2^-p
-  float* rstd = pinv + 16;                                                                    // [16]
-  float* gsum = rstd + 16;                                                                    // [win·KC/64][16]
-  float* stat = reinterpret_cast<float*>(smem + (size_t)nwaves * a.wave_lds);   // [nwaves][16]
-  const uint8_t* zero = reinterpret_cast<const uint8_t*>(stat + nwaves * 16); // 64 zero bytes
-  if (threadIdx.x < 16) reinterpret_cast<uint32_t*>(stat + nwaves * 16)[threadIdx.x] = 0u;
-  if (lane < 16) { rstd[lane] = 1.0f; pscale[lane] = 1.0f; pinv[lane] = 1.0f; }
-
-  const int tile0 = rb * RT;
-  bool tile_ok[RT];
-  const uint8_t* tbase[RT];
-  const uint8_t* wmat = a.w + (long long)expert * a.expert_stride;
-#pragma unroll
-  for (int r = 0; r < RT; ++r) {
-    tile_ok[r] = (tile0 + r) < a.n_tiles;
-    tbase[r] = wmat + (long long)(tile_ok[r] ? tile0 + r : 0) * a.chunks * UB;
-  }
-
-  // activations of window w: cnt rows × wcols columns from column (c0 + w·win)·KC (clamped at the row end)
-  uint4 xv[XV];
-  auto x_issue = [&](int w) {
-    const int per_row = wcols / 8;
-    const int n_units = cnt * per_row;
-    const int kbase = (c0 + w * win) * KC;
-#pragma unroll
-    for (int i = 0; i < XV; ++i) {
-      const int idx = min(lane + 64 * i, n_units - 1);
-      const int j = idx / per_row, e = (idx - j * per_row) * 8;
-      const int col = min(kbase + e, a.k - 8);
-      xv[i] = *reinterpret_cast<const uint4*>(a.x + xrow_of(j) * a.ldx + col);
-    }
-  };
-
-  // ---- weights: the first D chunks of every tile --------------------------------------------------------------
-  x_issue(0);
-  Units<FMT> ring[D][RT];
-#pragma unroll
-  for (int i = 0; i < D; ++i) {
-    const int c = c0 + min(i, a.kw - 1);
-#pragma unroll
-    for (int r = 0; r < RT; ++r) load_unit<FMT>(ring[i][r], tbase[r] + (long long)c * UB, lane);
-  }
-
-  // ---- fused RMSNorm: Σh² over the row from every wave's slice, one workgroup barrier -------------------------
-  if (a.norm_w) {
-    const int per_row = a.kw * KC / 8;
-    for (int j = 0; j < cnt; ++j) {
-      float s = 0.0f;
-      for (int u = lane; u < per_row; u += 64) {
-        const uint4 v = *reinterpret_cast<const uint4*>(a.x + xrow_of(j) * a.ldx + c0 * KC + u * 8);
-        const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float lo = bf16_bits_to_f32(vv[q] & 0xFFFFu), hi = bf16_bits_to_f32(vv[q] >> 16);
-          s = fmaf(lo, lo, fmaf(hi, hi, s));
-        }
-      }
-      s = wave_sum(s);
-      if (lane == 0) stat[wave * 16 + j] = s;
-    }
-    __syncthreads();
-    if (lane < cnt) {
-      float s = 0.0f;
-      for (int wv = 0; wv < nwaves; ++wv) s += stat[wv * 16 + lane];          // fixed order: bit-repeatable
-      rstd[lane] = 1.0f / sqrtf(s / (float)a.k + a.eps);
-    }
-    wave_lds_sync();
-  }
-
-  // ---- stage window w of this wave's slice into its LDS region (wave-local: no workgroup barrier) -------------
-  // x = bf16(h·r·w) when the norm is fused; for F16 operands a per-token power of two 2^-p taken from this window's
-  // max brings the row into [2^14, 2^15) before BF16 → F16 (exact from 2^-14 up); the window's products are scaled
-  // back by 2^p when folded into the accumulator.
-  auto stage = [&](int w) {
-    const int per_row = wcols / 8;
-    const int n_units = cnt * per_row;
-    const int kbase = (c0 + w * win) * KC;
-    auto put = [&](int idx, uint4 v) {
-      const int j = idx / per_row, e = (idx - j * per_row) * 8;
-      const int col = kbase + e;
-      if (col >= a.k) {
-        v = uint4{0u, 0u, 0u, 0u};                                   // window past the row end
-      } else if (a.norm_w) {
-        const float4 w0 = *reinterpret_cast<const float4*>(a.norm_w + col);
-        const float4 w1 = *reinterpret_cast<const float4*>(a.norm_w + col + 4);
-        const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-        const float rr = rstd[j];
-        uint32_t* vv = reinterpret_cast<uint32_t*>(&v);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float lo = round_bf16((bf16_bits_to_f32(vv[q] & 0xFFFFu) * rr) * wv[2 * q]);
-          const float hi = round_bf16((bf16_bits_to_f32(vv[q] >> 16) * rr) * wv[2 * q + 1]);
-          vv[q] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
-        }
-      }
-      *reinterpret_cast<uint4*>(xs + (size_t)j * a.lds_ld + e) = v;
-    };
-#pragma unroll
-    for (int i = 0; i < XV; ++i)
-      if (lane + 64 * i < n_units) put(lane + 64 * i, xv[i]);
-    for (int idx = lane + 64 * XV; idx < n_units; idx += 64) {
-      const int j = idx / per_row, e = (idx - j * per_row) * 8;
-      const int col = min(kbase + e, a.k - 8);
-      put(idx, *reinterpret_cast<const uint4*>(a.x + xrow_of(j) * a.ldx + col));
-    }
-    wave_lds_sync();
-    if constexpr (FMT == FMT_BF16) return;
-    // per-token prescale from the staged window
-    for (int j = 0; j < cnt; ++j) {
-      float m = 0.0f;
-      for (int u = lane; u < per_row; u += 64) {
-        const uint4 v = *reinterpret_cast<const uint4*>(xs + (size_t)j * a.lds_ld + u * 8);
-        const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) m = fmaxf(m, fmaxf(fabsf(bf16_bits_to_f32(vv[q] & 0xFFFFu)), fabsf(bf16_bits_to_f32(vv[q] >> 16))));
-      }
-      m = wave_max(m);
-      if (lane == 0) {
-        const int p = (m == 0.0f) ? 0 : (int)((__float_as_uint(m) >> 23) & 0xFF) - 127 - 14;
-        pscale[j] = __uint_as_float((uint32_t)(127 + p) << 23);   // 2^p
-        pinv[j] = __uint_as_float((uint32_t)(127 - p) << 23);     // 2^-p
-      }
-    }
-    wave_lds_sync();
-    for (int idx = lane; idx < n_units; idx += 64) {
-      const int j = idx / per_row, e = (idx - j * per_row) * 8;
-      uint16_t* p = xs + (size_t)j * a.lds_ld + e;
-      const uint4 v = *reinterpret_cast<const uint4*>(p);
-      const uint16_t* hv = reinterpret_cast<const uint16_t*>(&v);
-      const float sc = pinv[j];
-      f16x8 o;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = (f16_t)(bf16_bits_to_f32(hv[(FMT == FMT_INT4) ? int4_perm8(i) : i]) * sc);
-      *reinterpret_cast<f16x8*>(p) = o;
-    }
-    wave_lds_sync();
-    if constexpr (FMT == FMT_INT4) {
-      const int ng = wcols / 64;
-      for (int idx = lane; idx < 16 * ng; idx += 64) {
-        const int g = idx >> 4, j = idx & 15;
-        float sum = 0.0f;
-        if (j < cnt) {
-          const f16_t* p = reinterpret_cast<const f16_t*>(xs + (size_t)j * a.lds_ld + g * 64);
-          for (int i = 0; i < 64; ++i) sum += (float)p[i];
-        }
-        gsum[g * 16 + j] = sum;
-      }
-      wave_lds_sync();
-    }
-  };
-
-  const int g4 = lane >> 4;        // k-group of the operands / token quad of the result
-  const int m_row = lane & 15;     // A row = token
-  const bool a_real = m_row < cnt;
-  const uint8_t* a_row = a_real ? reinterpret_cast<const uint8_t*>(xs + (size_t)m_row * a.lds_ld) : zero;
-  const int a_mask = a_real ? ~0 : 0;    // a padding token reads the same 16 zero bytes at every step
-
-  // one chunk of RT tiles on MFMA, the activations of window-local column kl
-  auto compute = [&](const Units<FMT>* u, int kl, f32x4* acc) {
-    if constexpr (FMT == FMT_BF16) {
-      const bf16x8 av = *reinterpret_cast<const bf16x8*>(a_row + (((kl + 8 * g4) * 2) & a_mask));
-#pragma unroll
-      for (int r = 0; r < RT; ++r) {
-        union { uint4 u; bf16x8 b; } wv;
-        wv.u = u[r].q;
-        acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, wv.b, acc[r], 0, 0, 0);
-      }
-    } else if constexpr (FMT == FMT_NVFP4) {
-      f16x8 av[4];
-#pragma unroll
-      for (int s = 0; s < 4; ++s) av[s] = *reinterpret_cast<const f16x8*>(a_row + (((kl + 32 * g4 + 8 * s) * 2) & a_mask));
-#pragma unroll
-      for (int r = 0; r < RT; ++r) {
-        const ScalePair sp = nvfp4_scales(u[r].s);
-        const uint32_t dw[4] = {u[r].q.x, u[r].q.y, u[r].q.z, u[r].q.w};
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const f16x8 bv = nvfp4_decode8(dw[s], s < 2 ? sp.e0 : sp.e1, s < 2 ? sp.m0 : sp.m1);
-          acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[s], bv, acc[r], 0, 0, 0);
-        }
-      }
-    } else {  // INT4: steps 0,1 = group 2c, steps 2,3 = group 2c+1
-      f16x8 av[4];
-#pragma unroll
-      for (int s = 0; s < 4; ++s) av[s] = *reinterpret_cast<const f16x8*>(a_row + (((kl + 32 * s + 8 * g4) * 2) & a_mask));
-      const int gl = kl / 64;
-      const f32x4 sxa = *reinterpret_cast<const f32x4*>(gsum + gl * 16 + 4 * g4);
-      const f32x4 sxb = *reinterpret_cast<const f32x4*>(gsum + (gl + 1) * 16 + 4 * g4);
-#pragma unroll
-      for (int r = 0; r < RT; ++r) {
-        const uint32_t dw[4] = {u[r].q.x, u[r].q.y, u[r].q.z, u[r].q.w};
-        f32x4 da = {0.f, 0.f, 0.f, 0.f}, db = {0.f, 0.f, 0.f, 0.f};
-        da = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[0], int4_decode8(dw[0]), da, 0, 0, 0);
-        da = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[1], int4_decode8(dw[1]), da, 0, 0, 0);
-        db = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[2], int4_decode8(dw[2]), db, 0, 0, 0);
-        db = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[3], int4_decode8(dw[3]), db, 0, 0, 0);
-        const float sca = bf16_bits_to_f32(u[r].sb.x & 0xFFFFu), bia = bf16_bits_to_f32(u[r].sb.x >> 16);
-        const float scb = bf16_bits_to_f32(u[r].sb.y & 0xFFFFu), bib = bf16_bits_to_f32(u[r].sb.y >> 16);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          acc[r][i] = fmaf(sca, da[i], fmaf(bia, sxa[i], acc[r][i]));
-          acc[r][i] = fmaf(scb, db[i], fmaf(bib, sxb[i], acc[r][i]));
-        }
-      }
-    }
-  };
-
-  // ---- main loop: the wave's K slice window by window, D chunks of every tile in flight -------------------------
-  f32x4 acc[RT], wacc[RT];
-#pragma unroll
-  for (int r = 0; r < RT; ++r) { acc[r] = f32x4{0.f, 0.f, 0.f, 0.f}; wacc[r] = acc[r]; }
-  auto fold = [&]() {                          // acc += window accumulator · 2^p (per token)
-#pragma unroll
-    for (int r = 0; r < RT; ++r)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc[r][i] = fmaf(wacc[r][i], pscale[4 * g4 + i], acc[r][i]);
-        wacc[r][i] = 0.0f;
-      }
-  };
-  stage(0);
-  for (int base = 0; base < a.kw; base += D) {
-#pragma unroll
-    for (int i = 0; i < D; ++i) {
-      const int cc = base + i;
-      if (cc < a.kw) {
-        const int w = cc / win, cw = cc - w * win;
-        if (cw == 0 && w > 0) {                 // next window of this wave's slice (multi-window plans only)
-          fold();
-          x_issue(w);
-          stage(w);
-        }
-        compute(ring[i], cw * KC, wacc);
-      }
-      const int c = c0 + min(cc + D, a.kw - 1);
-#pragma unroll
-      for (int r = 0; r < RT; ++r) load_unit<FMT>(ring[i][r], tbase[r] + (long long)c * UB, lane);
-    }
-  }
-  fold();
-
-  // ---- reduce the K-slices through LDS, in wave order ------------------------------------------------------------
-  if (nwaves > 1) {
-    f32x4* red = reinterpret_cast<f32x4*>(smem);     // aliases the staged activations: all reads are done
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < RT; ++r) red[(wave * RT + r) * 64 + lane] = acc[r];
-    __syncthreads();
-    if (wave != 0) return;
-#pragma unroll
-    for (int r = 0; r < RT; ++r) {
-      f32x4 s = red[r * 64 + lane];
-      for (int w = 1; w < nwaves; ++w) {
-        const f32x4 o = red[(w * RT + r) * 64 + lane];
-        s[0] += o[0]; s[1] += o[1]; s[2] += o[2]; s[3] += o[3];
-      }
-      acc[r] = s;
-    }
-  }
-
-
-  // ---- epilogue ------------------------------------------------------------------------------------------------
-  const int n_pad = a.n_tiles * 16;
-#pragma unroll
-  for (int r = 0; r < RT; ++r) {
-    const int row = (tile0 + r) * 16 + m_row;
-    const float rs = (a.row_scale != nullptr) ? a.row_scale[(long long)expert * n_pad + (tile_ok[r] ? row : 0)] : 1.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float v = acc[r][i] * rs;
-      const float up = __shfl_down(v, 8, 16);                     // rows 8..15 of a silu·mul tile are the up rows
-      emit(a, pairs, cnt, tile0 + r, tile_ok[r], m_row, 4 * g4 + i, v, up);
-    }
-  }
-}
-
-// ---- the M ≤ 2 kernel: VALU dot products on BF16 activations ---------------------------------------------------
-// At one or two tokens the MFMA tile would be 15/16 padding and the activations would need the F16 staging; here
-// the weights decode to BF16 (v_cvt_scalef32_pk_bf16_fp4: e2m1·2^E exactly), v_dot2_f32_bf16 multiplies them with
-// the BF16 activations as they are, and each E4M3 block's 3-bit mantissa factor is applied once per block of 16.
-// INT4 codes become BF16 128 + c (0x4300|c, exact) and the dot product is corrected by 128·Σx per 16-column
-// segment; the affine pair is applied as scale·Σcx + bias·Σx. Lane (r = l%16, g = l/16) owns row r of each tile
-// and 32 of each chunk's 128 columns; the four g-lanes of a row are summed at the end.
-template <int FMT, int RT, int MT>
-__global__ __launch_bounds__(512) void gemv_dot(Args a) {
-  constexpr int D = 8 / RT;
-  constexpr int KC = chunk_cols(FMT);
-  constexpr int UB = unit_bytes(FMT);
-  constexpr int XV = 4;
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int nwaves = blockDim.x >> 6;
-  const int rb = blockIdx.x;
-  const int grp = blockIdx.y;
-  int expert = 0, cnt = a.m;
-  const int32_t* pairs = nullptr;
-  if (a.groups) {
-    const int32_t* g = a.groups + grp * GROUP_REC;
-    expert = g[0];
-    cnt = g[1];
-    pairs = g + 2;
-    if (cnt <= 0 || expert < 0) return;
+    if (cnt <= 0 || expert < 0) return;       // the whole workgroup leaves together
   }
   if (cnt > MT) cnt = MT;
-  auto xrow_of = [&](int j) -> long long {
-    if (!pairs) return j;
-    const int p = pairs[j];
-    return a.x_per_slot ? p : p / a.top_k;
-  };
-  // this wave's K slice: chunks [c0, c1) (slices differ by at most one chunk)
-  const int c0 = (int)((long long)wave * a.chunks / nwaves);
-  const int c1 = (int)((long long)(wave + 1) * a.chunks / nwaves);
-  const int kw = c1 - c0;
-  const int scols = kw * KC;
-  // LDS per wave: xs[MT][slice cols] BF16 (INT4: permuted in 8s) | (INT4) seg[MT][kw][2][4] Σx per 16-col segment
-  uint8_t* wl = smem + (size_t)wave * a.wave_lds;
+  const long long xr0 = pairs ? (a.x_per_slot ? pairs[0] : pairs[0] / a.top_k) : 0;
+  const long long xr1 = MT > 1 ? (pairs ? (a.x_per_slot ? pairs[cnt - 1] : pairs[cnt - 1] / a.top_k) : cnt - 1) : 0;
+  const int c0 = wave * KW;
+  const int kw = min(KW, a.chunks - c0);
+  const int cols = kw * KC;
+  const uint8_t* tbase = a.w + (long long)expert * a.expert_stride + (long long)tile * a.tile_stride;
+
+  // ---- loads: activations, norm weights, scale pieces, then every weight chunk of the slice --------------------
+  const int per_row = cols / 8;
+  uint4 xv[NPL];
+  float4 nv[NPL][2];
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const int idx = min(lane + 64 * i, MT * per_row - 1);
+    const int j = MT > 1 && idx >= per_row ? 1 : 0;
+    const int e = (idx - j * per_row) * 8;
+    xv[i] = *reinterpret_cast<const uint4*>(a.x + (j ? xr1 : xr0) * a.ldx + c0 * KC + e);
+    if (a.norm_w) {
+      nv[i][0] = *reinterpret_cast<const float4*>(a.norm_w + c0 * KC + e);
+      nv[i][1] = *reinterpret_cast<const float4*>(a.norm_w + c0 * KC + e + 4);
+    }
+  }
+  uint4 sv[NG > 0 ? NG : 1];
+  if constexpr (FMT == FMT_NVFP4) {
+#pragma unroll
+    for (int q = 0; q < NG; ++q) {
+      const int gi = min((c0 >> 3) + q, (a.chunks - 1) >> 3);
+      const int gsz = nv_group_chunks(gi, a.chunks);
+      const uint8_t* p = tbase + nv_scale_off(gi, a.chunks);
+      if (nv_piece(gsz) == 16) {
+        sv[q] = *reinterpret_cast<const uint4*>(p + 16 * lane);
+      } else {
+        const uint2 t = *reinterpret_cast<const uint2*>(p + 8 * lane);
+        sv[q] = uint4{t.x, t.y, 0u, 0u};
+      }
+    }
+  }
+  Units<FMT> u[KW];
+#pragma unroll
+  for (int cc = 0; cc < KW; ++cc) load_chunk<FMT, false>(u[cc], tbase, c0 + min(cc, kw - 1), a.chunks, lane);
+
+  // ---- stage the slice (normalized when the norm is fused: Σh² over the row from every wave's slice) ----------
+  uint8_t* wl = smem + (size_t)wave * a.row_wave_lds;
   uint16_t* xs = reinterpret_cast<uint16_t*>(wl);
-  const int ld = a.lds_ld;
+  const int ld = a.row_ld;
   float* seg = reinterpret_cast<float*>(wl + (size_t)MT * ld * 2);
-  float* stat = reinterpret_cast<float*>(smem + (size_t)nwaves * a.wave_lds);   // [nwaves][16]
-  float* red = stat + nwaves * 16;                                             // [nwaves][RT][MT][16]
-
-  const int tile0 = rb * RT;
-  bool tile_ok[RT];
-  const uint8_t* tbase[RT];
-  const uint8_t* wmat = a.w + (long long)expert * a.expert_stride;
-#pragma unroll
-  for (int r = 0; r < RT; ++r) {
-    tile_ok[r] = (tile0 + r) < a.n_tiles;
-    tbase[r] = wmat + (long long)(tile_ok[r] ? tile0 + r : 0) * a.chunks * UB;
-  }
-
-  // activation slice loads first, then the weight ring: the wait for the activations counts the weights behind them
-  const int per_row = scols / 8;
-  const int n_units = cnt * per_row;
-  uint4 xv[XV];
-#pragma unroll
-  for (int i = 0; i < XV; ++i) {
-    const int idx = min(lane + 64 * i, n_units - 1);
-    const int j = idx / per_row, e = (idx - j * per_row) * 8;
-    xv[i] = *reinterpret_cast<const uint4*>(a.x + xrow_of(j) * a.ldx + c0 * KC + e);
-  }
-  Units<FMT> ring[D][RT];
-#pragma unroll
-  for (int i = 0; i < D; ++i) {
-    const int c = c0 + min(i, kw - 1);
-#pragma unroll
-    for (int r = 0; r < RT; ++r) load_unit<FMT>(ring[i][r], tbase[r] + (long long)c * UB, lane);
-  }
-
-  // fused RMSNorm statistic over the full row: per-wave partial sums, one barrier, fixed summation order
-  float rstd0 = 1.0f, rstd1 = 1.0f;
+  float* stat = reinterpret_cast<float*>(smem + (size_t)S * a.row_wave_lds);   // [S][2]
+  float* red = stat + 2 * S;                                                  // [S][MT][16]
   if (a.norm_w) {
-    for (int j = 0; j < cnt; ++j) {
-      float s = 0.0f;
-      for (int u = lane; u < per_row; u += 64) {
-        const uint4 v = *reinterpret_cast<const uint4*>(a.x + xrow_of(j) * a.ldx + c0 * KC + u * 8);
-        const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+    float sq[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      const int idx = lane + 64 * i;
+      if (idx < MT * per_row) {
+        const uint32_t vv[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+        float t = 0.0f;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const float lo = bf16_bits_to_f32(vv[q] & 0xFFFFu), hi = bf16_bits_to_f32(vv[q] >> 16);
-          s = fmaf(lo, lo, fmaf(hi, hi, s));
+          t = fmaf(lo, lo, fmaf(hi, hi, t));
         }
+        sq[MT > 1 && idx >= per_row ? 1 : 0] += t;
       }
-      s = wave_sum(s);
-      if (lane == 0) stat[wave * 16 + j] = s;
     }
+    sq[0] = wave_sum(sq[0]);
+    if (MT > 1) sq[1] = wave_sum(sq[1]);
+    if (lane == 0) { stat[2 * wave] = sq[0]; stat[2 * wave + 1] = sq[1]; }
     __syncthreads();
-    float s0 = 0.0f, s1 = 0.0f;
-    for (int wv = 0; wv < nwaves; ++wv) { s0 += stat[wv * 16]; if (MT > 1) s1 += stat[wv * 16 + 1]; }
-    rstd0 = 1.0f / sqrtf(s0 / (float)a.k + a.eps);
-    rstd1 = 1.0f / sqrtf(s1 / (float)a.k + a.eps);
-  }
-
-  // stage the slice (BF16; normalized when fused; INT4: the (0,4,1,5,2,6,3,7) order inside each 8)
-  auto put = [&](int idx, uint4 v) {
-    const int j = idx / per_row, e = (idx - j * per_row) * 8;
-    uint32_t* vv = reinterpret_cast<uint32_t*>(&v);
-    if (a.norm_w) {
-      const int col = c0 * KC + e;
-      const float4 w0 = *reinterpret_cast<const float4*>(a.norm_w + col);
-      const float4 w1 = *reinterpret_cast<const float4*>(a.norm_w + col + 4);
-      const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-      const float rr = j == 0 ? rstd0 : rstd1;
+    float rstd[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      float t = 0.0f;
+      for (int w = 0; w < S; ++w) t += stat[2 * w + j];
+      rstd[j] = 1.0f / sqrtf(t / (float)a.k + a.eps);
+    }
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      const int idx = lane + 64 * i;
+      const float rr = rstd[MT > 1 && idx >= per_row ? 1 : 0];
+      const float wv[8] = {nv[i][0].x, nv[i][0].y, nv[i][0].z, nv[i][0].w, nv[i][1].x, nv[i][1].y, nv[i][1].z, nv[i][1].w};
+      uint32_t* vv = reinterpret_cast<uint32_t*>(&xv[i]);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const float lo = round_bf16((bf16_bits_to_f32(vv[q] & 0xFFFFu) * rr) * wv[2 * q]);
@@ -601,87 +312,85 @@ __global__ __launch_bounds__(512) void gemv_dot(Args a) {
         vv[q] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
       }
     }
-    if constexpr (FMT == FMT_INT4) {        // (x0,x1)(x2,x3)(x4,x5)(x6,x7) → (x0,x4)(x1,x5)(x2,x6)(x3,x7)
-      const uint32_t a0 = vv[0], a1 = vv[1], a2 = vv[2], a3 = vv[3];
-      vv[0] = __builtin_amdgcn_perm(a2, a0, 0x05040100u);
-      vv[1] = __builtin_amdgcn_perm(a2, a0, 0x07060302u);
-      vv[2] = __builtin_amdgcn_perm(a3, a1, 0x05040100u);
-      vv[3] = __builtin_amdgcn_perm(a3, a1, 0x07060302u);
-    }
-    *reinterpret_cast<uint4*>(xs + (size_t)j * ld + e) = v;
-  };
+  }
 #pragma unroll
-  for (int i = 0; i < XV; ++i)
-    if (lane + 64 * i < n_units) put(lane + 64 * i, xv[i]);
-  for (int idx = lane + 64 * XV; idx < n_units; idx += 64) {
-    const int j = idx / per_row, e = (idx - j * per_row) * 8;
-    put(idx, *reinterpret_cast<const uint4*>(a.x + xrow_of(j) * a.ldx + c0 * KC + e));
+  for (int i = 0; i < NPL; ++i) {
+    const int idx = lane + 64 * i;
+    if (idx < MT * per_row) {
+      const int j = MT > 1 && idx >= per_row ? 1 : 0;
+      uint4 v = xv[i];
+      if constexpr (FMT == FMT_INT4) {        // (x0,x1)(x2,x3)(x4,x5)(x6,x7) → (x0,x4)(x1,x5)(x2,x6)(x3,x7)
+        const uint32_t a0 = v.x, a1 = v.y, a2 = v.z, a3 = v.w;
+        v.x = __builtin_amdgcn_perm(a2, a0, 0x05040100u);
+        v.y = __builtin_amdgcn_perm(a2, a0, 0x07060302u);
+        v.z = __builtin_amdgcn_perm(a3, a1, 0x05040100u);
+        v.w = __builtin_amdgcn_perm(a3, a1, 0x07060302u);
+      }
+      *reinterpret_cast<uint4*>(xs + (size_t)j * ld + (idx - j * per_row) * 8) = v;
+    }
   }
   wave_lds_sync();
   if constexpr (FMT == FMT_INT4) {
     // Σx over each (chunk, g, group) segment of 16 columns: steps {0,1} (group A) / {2,3} (group B) of k-group g
-    const int nseg = MT * kw * 8;
-    for (int idx = lane; idx < nseg; idx += 64) {
-      const int j = idx / (kw * 8), rem = idx - j * kw * 8;
+    for (int idx = lane; idx < MT * KW * 8; idx += 64) {
+      const int j = idx / (KW * 8), rem = idx - j * KW * 8;
       const int cc = rem >> 3, g = (rem >> 1) & 3, gp = rem & 1;
-      float s = 0.0f;
-      if (j < cnt) {
+      float sx = 0.0f;
+      if (cc < kw) {
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
           const uint4 v = *reinterpret_cast<const uint4*>(xs + (size_t)j * ld + cc * 128 + 32 * (2 * gp + st) + 8 * g);
           const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-          for (int q = 0; q < 4; ++q) s += bf16_bits_to_f32(vv[q] & 0xFFFFu) + bf16_bits_to_f32(vv[q] >> 16);
+          for (int q = 0; q < 4; ++q) sx += bf16_bits_to_f32(vv[q] & 0xFFFFu) + bf16_bits_to_f32(vv[q] >> 16);
         }
       }
-      seg[idx] = s;
+      seg[idx] = sx;
     }
     wave_lds_sync();
   }
 
+  // ---- the slice's dot products --------------------------------------------------------------------------------
   const int g = lane >> 4, m_row = lane & 15;
-  float acc[RT][MT];
+  float acc[MT];
 #pragma unroll
-  for (int r = 0; r < RT; ++r)
-#pragma unroll
-    for (int t = 0; t < MT; ++t) acc[r][t] = 0.0f;
-
-  auto compute = [&](const Units<FMT>* u, int cc) {
+  for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
+  auto slice_chunk = [&](int cc) {
+    const uint32_t dw[4] = {u[cc].q.x, u[cc].q.y, u[cc].q.z, u[cc].q.w};
     if constexpr (FMT == FMT_NVFP4) {
-      uint4 xq[MT][4];                          // this lane's 32 activations of the chunk, per token
+      uint4 xq[MT][4];
 #pragma unroll
       for (int t = 0; t < MT; ++t)
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-          xq[t][s] = *reinterpret_cast<const uint4*>(xs + (size_t)t * ld + cc * 128 + 32 * g + 8 * s);
+        for (int s = 0; s < 4; ++s) xq[t][s] = *reinterpret_cast<const uint4*>(xs + (size_t)t * ld + cc * 128 + 32 * g + 8 * s);
+      const int ci = ((c0 + cc) & 7);                // chunk in its group; KW >= 8 slices start on a group
+      const uint4 pv = sv[KW >= 8 ? cc >> 3 : 0];
+      const uint32_t word = KW >= 8 ? (cc & 6) == 0 ? pv.x : (cc & 6) == 2 ? pv.y : (cc & 6) == 4 ? pv.z : pv.w
+                                    : (ci >> 1) == 0 ? pv.x : (ci >> 1) == 1 ? pv.y : (ci >> 1) == 2 ? pv.z : pv.w;
+      const uint32_t two = (KW >= 8 ? (cc & 1) : (ci & 1)) ? word >> 16 : word & 0xFFFFu;
+      const f32x2 f = __builtin_amdgcn_cvt_pk_f32_fp8((int)two, false);
+      const uint32_t u0 = __float_as_uint(f.x), u1 = __float_as_uint(f.y);
+      const float e[2] = {__uint_as_float(u0 & 0x7F800000u), __uint_as_float(u1 & 0x7F800000u)};
+      const float mant[2] = {__uint_as_float((u0 & 0x807FFFFFu) | 0x3F800000u),
+                             __uint_as_float((u1 & 0x807FFFFFu) | 0x3F800000u)};
 #pragma unroll
-      for (int r = 0; r < RT; ++r) {
-        const f32x2 f = __builtin_amdgcn_cvt_pk_f32_fp8((int)u[r].s, false);
-        const uint32_t u0 = __float_as_uint(f.x), u1 = __float_as_uint(f.y);
-        const float e[2] = {__uint_as_float(u0 & 0x7F800000u), __uint_as_float(u1 & 0x7F800000u)};
-        const float mant[2] = {__uint_as_float((u0 & 0x807FFFFFu) | 0x3F800000u),
-                               __uint_as_float((u1 & 0x807FFFFFu) | 0x3F800000u)};
-        const uint32_t dw[4] = {u[r].q.x, u[r].q.y, u[r].q.z, u[r].q.w};
+      for (int b = 0; b < 2; ++b) {
+        float part[MT];
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-          float part[MT];
+        for (int t = 0; t < MT; ++t) part[t] = 0.0f;
 #pragma unroll
-          for (int t = 0; t < MT; ++t) part[t] = 0.0f;
+        for (int s = 2 * b; s < 2 * b + 2; ++s)
 #pragma unroll
-          for (int s = 2 * b; s < 2 * b + 2; ++s) {
+          for (int j = 0; j < 4; ++j) {
+            const bf16x2 w2 = cvt_fp4x2_bf16(dw[s], e[b], j);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const bf16x2 w2 = cvt_fp4x2_bf16(dw[s], e[b], j);
-#pragma unroll
-              for (int t = 0; t < MT; ++t) {
-                const uint32_t xw = j == 0 ? xq[t][s].x : j == 1 ? xq[t][s].y : j == 2 ? xq[t][s].z : xq[t][s].w;
-                part[t] = __builtin_amdgcn_fdot2_f32_bf16(w2, __builtin_bit_cast(bf16x2, xw), part[t], false);
-              }
+            for (int t = 0; t < MT; ++t) {
+              const uint32_t xw = j == 0 ? xq[t][s].x : j == 1 ? xq[t][s].y : j == 2 ? xq[t][s].z : xq[t][s].w;
+              part[t] = __builtin_amdgcn_fdot2_f32_bf16(w2, __builtin_bit_cast(bf16x2, xw), part[t], false);
             }
           }
 #pragma unroll
-          for (int t = 0; t < MT; ++t) acc[r][t] = fmaf(part[t], mant[b], acc[r][t]);
-        }
+        for (int t = 0; t < MT; ++t) acc[t] = fmaf(part[t], mant[b], acc[t]);
       }
     } else if constexpr (FMT == FMT_INT4) {
       uint4 xq[MT][4];
@@ -689,102 +398,495 @@ __global__ __launch_bounds__(512) void gemv_dot(Args a) {
 #pragma unroll
       for (int t = 0; t < MT; ++t) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-          xq[t][s] = *reinterpret_cast<const uint4*>(xs + (size_t)t * ld + cc * 128 + 32 * s + 8 * g);
-        sa[t] = seg[(t * kw + cc) * 8 + g * 2];
-        sb[t] = seg[(t * kw + cc) * 8 + g * 2 + 1];
+        for (int s = 0; s < 4; ++s) xq[t][s] = *reinterpret_cast<const uint4*>(xs + (size_t)t * ld + cc * 128 + 32 * s + 8 * g);
+        sa[t] = seg[(t * KW + cc) * 8 + g * 2];
+        sb[t] = seg[(t * KW + cc) * 8 + g * 2 + 1];
       }
+      float d[2][MT];
 #pragma unroll
-      for (int r = 0; r < RT; ++r) {
-        const uint32_t dw[4] = {u[r].q.x, u[r].q.y, u[r].q.z, u[r].q.w};
-        float d[2][MT];
+      for (int t = 0; t < MT; ++t) d[0][t] = d[1][t] = 0.0f;
 #pragma unroll
-        for (int t = 0; t < MT; ++t) d[0][t] = d[1][t] = 0.0f;
+      for (int s = 0; s < 4; ++s)
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t w2 = ((dw[s] >> (4 * j)) & 0x000F000Fu) | 0x43004300u;   // BF16 (128 + n_j, 128 + n_j+4)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const uint32_t w2 = ((dw[s] >> (4 * j)) & 0x000F000Fu) | 0x43004300u;   // BF16 (128 + n_j, 128 + n_j+4)
-#pragma unroll
-            for (int t = 0; t < MT; ++t) {
-              const uint32_t xw = j == 0 ? xq[t][s].x : j == 1 ? xq[t][s].y : j == 2 ? xq[t][s].z : xq[t][s].w;
-              d[s >> 1][t] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w2), __builtin_bit_cast(bf16x2, xw),
-                                                             d[s >> 1][t], false);
-            }
+          for (int t = 0; t < MT; ++t) {
+            const uint32_t xw = j == 0 ? xq[t][s].x : j == 1 ? xq[t][s].y : j == 2 ? xq[t][s].z : xq[t][s].w;
+            d[s >> 1][t] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w2), __builtin_bit_cast(bf16x2, xw),
+                                                           d[s >> 1][t], false);
           }
         }
-        const float sca = bf16_bits_to_f32(u[r].sb.x & 0xFFFFu), bia = bf16_bits_to_f32(u[r].sb.x >> 16);
-        const float scb = bf16_bits_to_f32(u[r].sb.y & 0xFFFFu), bib = bf16_bits_to_f32(u[r].sb.y >> 16);
+      const float sca = bf16_bits_to_f32(u[cc].sb.x & 0xFFFFu), bia = bf16_bits_to_f32(u[cc].sb.x >> 16);
+      const float scb = bf16_bits_to_f32(u[cc].sb.y & 0xFFFFu), bib = bf16_bits_to_f32(u[cc].sb.y >> 16);
 #pragma unroll
-        for (int t = 0; t < MT; ++t) {
-          acc[r][t] = fmaf(sca, fmaf(-128.0f, sa[t], d[0][t]), fmaf(bia, sa[t], acc[r][t]));
-          acc[r][t] = fmaf(scb, fmaf(-128.0f, sb[t], d[1][t]), fmaf(bib, sb[t], acc[r][t]));
-        }
+      for (int t = 0; t < MT; ++t) {
+        acc[t] = fmaf(sca, fmaf(-128.0f, sa[t], d[0][t]), fmaf(bia, sa[t], acc[t]));
+        acc[t] = fmaf(scb, fmaf(-128.0f, sb[t], d[1][t]), fmaf(bib, sb[t], acc[t]));
       }
-    } else {  // BF16 weights: 8 values of row r at columns 32·cc + 8·g
+    } else {
       uint4 xq[MT];
 #pragma unroll
       for (int t = 0; t < MT; ++t) xq[t] = *reinterpret_cast<const uint4*>(xs + (size_t)t * ld + cc * 32 + 8 * g);
 #pragma unroll
-      for (int r = 0; r < RT; ++r) {
-        const uint32_t dw[4] = {u[r].q.x, u[r].q.y, u[r].q.z, u[r].q.w};
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int t = 0; t < MT; ++t) {
+          const uint32_t xw = j == 0 ? xq[t].x : j == 1 ? xq[t].y : j == 2 ? xq[t].z : xq[t].w;
+          acc[t] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, dw[j]), __builtin_bit_cast(bf16x2, xw),
+                                                   acc[t], false);
+        }
+    }
+  };
+#pragma unroll
+  for (int cc = 0; cc < KW; ++cc)
+    if (cc < kw) slice_chunk(cc);
+
+  // ---- the four k-groups of each row, then the K slices in wave order, then the epilogue ------------------------
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const float v = quad16_sum(acc[t]);
+    if (g == 0) red[(wave * MT + t) * 16 + m_row] = v;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  const int row = tile * 16 + m_row;
+  const float rs = a.row_scale != nullptr ? a.row_scale[(long long)expert * a.n_tiles * 16 + row] : 1.0f;
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    float v = red[t * 16 + m_row];
+    for (int w = 1; w < S; ++w) v += red[(w * MT + t) * 16 + m_row];
+    v *= rs;
+    const float up = __shfl_down(v, 8, 16);
+    if (g == 0) emit(a, pairs, cnt, tile, true, m_row, t, v, up);
+  }
+}
+
+// ---- the tile × K-split kernel ----------------------------------------------------------------------------------
+// Work item: (group of TB consecutive 16-row tiles, K split s = chunks [s·kc, min(chunks, (s+1)·kc))). A workgroup
+// of S waves stages the split's activations once — BF16 for the VALU path (M <= 2), per-token power-of-two
+// prescaled F16 for MFMA (M <= 16) — and wave w takes tiles w, w + S, … of the group over the whole split, streaming
+// its units through a D-deep register ring that runs on across tile boundaries. Every tile ends in the wave that
+// computed it: with one split the epilogue runs from its registers; with several the wave writes FP32 partials and
+// gemv_tk_reduce adds them in split order (deterministic). The activations are read once per workgroup, so the
+// L2 traffic they cost is (workgroups × split width) rather than (tiles × K) — the difference between the two at
+// M = 8 is several times the weight bytes.
+// LDS: xs[rows][kw·KC + 8] | pscale[16] (MFMA) | (INT4) seg / gsum.
+template <int FMT, int MT, int D, bool PIECES>
+__global__ __launch_bounds__(512) void gemv_tk(Args a) {
+  constexpr bool MF = MT > 2;
+  constexpr int KC = chunk_cols(FMT);
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int S = blockDim.x >> 6;
+  const int split = blockIdx.y;
+  int expert = 0, cnt = a.m;
+  const int32_t* pairs = nullptr;
+  if (a.groups) {
+    const int32_t* g = a.groups + blockIdx.z * GROUP_REC;
+    expert = g[0];
+    cnt = g[1];
+    pairs = g + 2;
+    if (cnt <= 0 || expert < 0) return;       // the whole workgroup leaves together
+  }
+  if (cnt > MT) cnt = MT;
+  auto xrow_of = [&](int j) -> long long {
+    if (!pairs) return j;
+    const int p = pairs[j];
+    return a.x_per_slot ? p : p / a.top_k;
+  };
+  const int kb = split * a.kc;
+  const int kw = min(a.chunks, kb + a.kc) - kb;
+  const int cols = kw * KC;
+  const int ld = cols + 8;
+  uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
+  const int xrows = cnt;
+  float* pscale = reinterpret_cast<float*>(smem + (size_t)a.lds_rows * ld * 2);   // [16]
+  float* extra = pscale + 16;                                             // INT4: seg [MT][kw][8] / gsum [kw·2][16]
+  const uint8_t* zero = reinterpret_cast<const uint8_t*>(extra + (FMT == FMT_INT4 ? (MF ? kw * 2 * 16 : MT * kw * 8) : 0));
+
+  // ---- this wave's tiles and the ring: the weights start streaming before anything else ---------------------
+  const int tile0 = blockIdx.x * a.tb;
+  const int ntl = min(a.tb, a.n_tiles - tile0);
+  const int nt_w = ntl > wave ? (ntl - wave + S - 1) / S : 0;   // tiles wave, wave + S, … < ntl
+  const int total = nt_w * kw;
+  const uint8_t* wmat = a.w + (long long)expert * a.expert_stride;
+  int lt = 0, lc = 0, left = total;
+  // NVFP4 block scales (PIECES): one 16-byte piece per group of 8 chunks. The split width is a multiple of 8, so
+  // every 8th unit of the stream starts a group; the stream runs in steps of 16 units with the ring (D = 8) and a
+  // 2-slot piece ring both indexed statically. Without PIECES each unit brings its two scale bytes itself.
+  uint4 spc[2] = {uint4{0u, 0u, 0u, 0u}, uint4{0u, 0u, 0u, 0u}};
+  auto load_next = [&](Units<FMT>& u) {
+    load_chunk<FMT, !PIECES>(u, wmat + (long long)(tile0 + wave + lt * S) * a.tile_stride, kb + lc, a.chunks, lane);
+    if (left > 1) {
+      --left;
+      if (++lc == kw) { lc = 0; ++lt; }
+    }
+  };
+  auto piece_of = [&](const uint8_t* tb, int c) {
+    const int gi = c >> 3;
+    const uint8_t* pp = tb + nv_scale_off(gi, a.chunks);
+    return *reinterpret_cast<const uint4*>(pp + 16 * lane);
+  };
+  Units<FMT> ring[D];
+  if (total > 0) {
+    if constexpr (PIECES) spc[0] = piece_of(wmat + (long long)(tile0 + wave) * a.tile_stride, kb);
+#pragma unroll
+    for (int i = 0; i < D; ++i) load_next(ring[i]);
+  }
+
+  // ---- stage the split's activations: wave j stages token rows j, j + S, … -------------------------------------
+  if (threadIdx.x < 16) reinterpret_cast<uint32_t*>(const_cast<uint8_t*>(zero))[threadIdx.x] = 0u;
+  for (int j = wave; j < xrows; j += S) {
+    const uint16_t* src = a.x + xrow_of(j) * a.ldx + kb * KC;
+    uint16_t* dst = xs + (size_t)j * ld;
+    const int nv = cols / 8;
+    float sq = 0.0f;
+    for (int v = lane; v < nv; v += 64) {
+      const uint4 q = *reinterpret_cast<const uint4*>(src + v * 8);
+      if (a.norm_w) {
+        const uint32_t qq[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float lo = bf16_bits_to_f32(qq[i] & 0xFFFFu), hi = bf16_bits_to_f32(qq[i] >> 16);
+          sq = fmaf(lo, lo, fmaf(hi, hi, sq));
+        }
+      }
+      *reinterpret_cast<uint4*>(dst + v * 8) = q;
+    }
+    float rr = 1.0f;
+    if (a.norm_w) rr = 1.0f / sqrtf(wave_sum(sq) / (float)a.k + a.eps);   // one split covers the row here
+    float mx = 0.0f;
+    if (a.norm_w || MF || FMT == FMT_INT4) {
+      wave_lds_sync();
+      for (int v = lane; v < nv; v += 64) {
+        uint4 q = *reinterpret_cast<const uint4*>(dst + v * 8);
+        uint32_t* qq = reinterpret_cast<uint32_t*>(&q);
+        if (a.norm_w) {
+          const int col = kb * KC + v * 8;
+          const float4 w0 = *reinterpret_cast<const float4*>(a.norm_w + col);
+          const float4 w1 = *reinterpret_cast<const float4*>(a.norm_w + col + 4);
+          const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float lo = round_bf16((bf16_bits_to_f32(qq[i] & 0xFFFFu) * rr) * wv[2 * i]);
+            const float hi = round_bf16((bf16_bits_to_f32(qq[i] >> 16) * rr) * wv[2 * i + 1]);
+            qq[i] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+          }
+        }
+        if (MF) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            mx = fmaxf(mx, fmaxf(fabsf(bf16_bits_to_f32(qq[i] & 0xFFFFu)), fabsf(bf16_bits_to_f32(qq[i] >> 16))));
+        }
+        if (!MF && FMT == FMT_INT4) {       // (x0,x1)(x2,x3)(x4,x5)(x6,x7) → (x0,x4)(x1,x5)(x2,x6)(x3,x7)
+          const uint32_t a0 = qq[0], a1 = qq[1], a2 = qq[2], a3 = qq[3];
+          qq[0] = __builtin_amdgcn_perm(a2, a0, 0x05040100u);
+          qq[1] = __builtin_amdgcn_perm(a2, a0, 0x07060302u);
+          qq[2] = __builtin_amdgcn_perm(a3, a1, 0x05040100u);
+          qq[3] = __builtin_amdgcn_perm(a3, a1, 0x07060302u);
+        }
+        *reinterpret_cast<uint4*>(dst + v * 8) = q;
+      }
+    }
+    if constexpr (MF && FMT == FMT_BF16) {
+      if (lane == 0) pscale[j] = 1.0f;                // BF16 weights: the MFMA takes the BF16 activations as they are
+    } else if constexpr (MF) {
+      // F16 operands: 2^-p brings the row max into [2^14, 2^15) (exact for everything within 2^28 of the max)
+      mx = wave_max(mx);
+      const int p = mx == 0.0f ? 0 : (int)((__float_as_uint(mx) >> 23) & 0xFF) - 127 - 14;
+      const float inv = __uint_as_float((uint32_t)(127 - p) << 23);
+      if (lane == 0) pscale[j] = __uint_as_float((uint32_t)(127 + p) << 23);
+      wave_lds_sync();
+      for (int v = lane; v < nv; v += 64) {
+        const uint4 q = *reinterpret_cast<const uint4*>(dst + v * 8);
+        const uint16_t* hv = reinterpret_cast<const uint16_t*>(&q);
+        f16x8 o;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = (f16_t)(bf16_bits_to_f32(hv[FMT == FMT_INT4 ? int4_perm8(i) : i]) * inv);
+        *reinterpret_cast<f16x8*>(dst + v * 8) = o;
+      }
+    }
+    wave_lds_sync();
+    if constexpr (FMT == FMT_INT4) {
+      if constexpr (MF) {
+        // Σx (prescaled F16) per 64 columns: the bias term of the affine groups
+        for (int gi = lane; gi < kw * 2; gi += 64) {
+          const f16_t* px = reinterpret_cast<const f16_t*>(dst + gi * 64);
+          float sx = 0.0f;
+          for (int i = 0; i < 64; ++i) sx += (float)px[i];
+          extra[gi * 16 + j] = sx;
+        }
+      } else {
+        // Σx over each (chunk, g, group) segment of 16 columns: steps {0,1} (group A) / {2,3} (group B) of k-group g
+        for (int idx = lane; idx < kw * 8; idx += 64) {
+          const int cc = idx >> 3, g = (idx >> 1) & 3, gp = idx & 1;
+          float sx = 0.0f;
+#pragma unroll
+          for (int st = 0; st < 2; ++st) {
+            const uint4 v = *reinterpret_cast<const uint4*>(dst + cc * 128 + 32 * (2 * gp + st) + 8 * g);
+            const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) sx += bf16_bits_to_f32(vv[q] & 0xFFFFu) + bf16_bits_to_f32(vv[q] >> 16);
+          }
+          extra[(j * kw + cc) * 8 + g * 2 + gp] = sx;
+        }
+      }
+    }
+  }
+  if constexpr (MF && FMT == FMT_INT4) {   // padding token rows: zero sums
+    for (int idx = threadIdx.x; idx < kw * 2 * 16; idx += blockDim.x)
+      if ((idx & 15) >= xrows) extra[idx] = 0.0f;
+  }
+  __syncthreads();
+
+  const int g = lane >> 4, m_row = lane & 15;
+  // MFMA: A row = token m_row (a padding token reads the 16 zero bytes at every step)
+  const bool a_real = m_row < cnt;
+  const uint8_t* a_row = a_real ? reinterpret_cast<const uint8_t*>(xs + (size_t)m_row * ld) : zero;
+  const int a_mask = a_real ? ~0 : 0;
+
+  float acc_v[MT > 2 ? 1 : MT];
+  f32x4 acc_m = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < (MT > 2 ? 1 : MT); ++t) acc_v[t] = 0.0f;
+
+  auto compute = [&](const Units<FMT>& u, int cc, int par, uint32_t s_unit) {
+    if constexpr (MF) {
+      const int kl = cc * KC;
+      if constexpr (FMT == FMT_BF16) {
+        const bf16x8 av = *reinterpret_cast<const bf16x8*>(a_row + (((kl + 8 * g) * 2) & a_mask));
+        union { uint4 u; bf16x8 b; } wv;
+        wv.u = u.q;
+        acc_m = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, wv.b, acc_m, 0, 0, 0);
+      } else if constexpr (FMT == FMT_NVFP4) {
+        f16x8 av[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) av[s] = *reinterpret_cast<const f16x8*>(a_row + (((kl + 32 * g + 8 * s) * 2) & a_mask));
+        uint32_t two = s_unit;
+        if constexpr (PIECES) {
+          const uint4 pv = spc[par];
+          const int ci = cc & 7;
+          const uint32_t word = (ci >> 1) == 0 ? pv.x : (ci >> 1) == 1 ? pv.y : (ci >> 1) == 2 ? pv.z : pv.w;
+          two = (ci & 1) ? word >> 16 : word & 0xFFFFu;
+        }
+        const ScalePair sp = nvfp4_scales(two);
+        const uint32_t dw[4] = {u.q.x, u.q.y, u.q.z, u.q.w};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const f16x8 bv = nvfp4_decode8(dw[s], s < 2 ? sp.e0 : sp.e1, s < 2 ? sp.m0 : sp.m1);
+          acc_m = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[s], bv, acc_m, 0, 0, 0);
+        }
+      } else {
+        f16x8 av[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) av[s] = *reinterpret_cast<const f16x8*>(a_row + (((kl + 32 * s + 8 * g) * 2) & a_mask));
+        const f32x4 sxa = *reinterpret_cast<const f32x4*>(extra + (cc * 2) * 16 + 4 * g);
+        const f32x4 sxb = *reinterpret_cast<const f32x4*>(extra + (cc * 2 + 1) * 16 + 4 * g);
+        const uint32_t dw[4] = {u.q.x, u.q.y, u.q.z, u.q.w};
+        f32x4 da = {0.f, 0.f, 0.f, 0.f}, db = {0.f, 0.f, 0.f, 0.f};
+        da = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[0], int4_decode8(dw[0]), da, 0, 0, 0);
+        da = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[1], int4_decode8(dw[1]), da, 0, 0, 0);
+        db = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[2], int4_decode8(dw[2]), db, 0, 0, 0);
+        db = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[3], int4_decode8(dw[3]), db, 0, 0, 0);
+        const float sca = bf16_bits_to_f32(u.sb.x & 0xFFFFu), bia = bf16_bits_to_f32(u.sb.x >> 16);
+        const float scb = bf16_bits_to_f32(u.sb.y & 0xFFFFu), bib = bf16_bits_to_f32(u.sb.y >> 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc_m[i] = fmaf(sca, da[i], fmaf(bia, sxa[i], acc_m[i]));
+          acc_m[i] = fmaf(scb, db[i], fmaf(bib, sxb[i], acc_m[i]));
+        }
+      }
+    } else if constexpr (FMT == FMT_NVFP4) {
+      uint4 xq[MT][4];
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) xq[t][s] = *reinterpret_cast<const uint4*>(xs + (size_t)t * ld + cc * 128 + 32 * g + 8 * s);
+      uint32_t two = s_unit;
+      if constexpr (PIECES) {
+        const uint4 pv = spc[par];
+        const int ci = cc & 7;
+        const uint32_t word = (ci >> 1) == 0 ? pv.x : (ci >> 1) == 1 ? pv.y : (ci >> 1) == 2 ? pv.z : pv.w;
+        two = (ci & 1) ? word >> 16 : word & 0xFFFFu;
+      }
+      const f32x2 f = __builtin_amdgcn_cvt_pk_f32_fp8((int)two, false);
+      const uint32_t u0 = __float_as_uint(f.x), u1 = __float_as_uint(f.y);
+      const float e[2] = {__uint_as_float(u0 & 0x7F800000u), __uint_as_float(u1 & 0x7F800000u)};
+      const float mant[2] = {__uint_as_float((u0 & 0x807FFFFFu) | 0x3F800000u),
+                             __uint_as_float((u1 & 0x807FFFFFu) | 0x3F800000u)};
+      const uint32_t dw[4] = {u.q.x, u.q.y, u.q.z, u.q.w};
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        float part[MT];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) part[t] = 0.0f;
+#pragma unroll
+        for (int s = 2 * b; s < 2 * b + 2; ++s)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const bf16x2 w2 = cvt_fp4x2_bf16(dw[s], e[b], j);
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+              const uint32_t xw = j == 0 ? xq[t][s].x : j == 1 ? xq[t][s].y : j == 2 ? xq[t][s].z : xq[t][s].w;
+              part[t] = __builtin_amdgcn_fdot2_f32_bf16(w2, __builtin_bit_cast(bf16x2, xw), part[t], false);
+            }
+          }
+#pragma unroll
+        for (int t = 0; t < MT; ++t) acc_v[t] = fmaf(part[t], mant[b], acc_v[t]);
+      }
+    } else if constexpr (FMT == FMT_INT4) {
+      uint4 xq[MT][4];
+      float sa[MT], sb[MT];
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) xq[t][s] = *reinterpret_cast<const uint4*>(xs + (size_t)t * ld + cc * 128 + 32 * s + 8 * g);
+        sa[t] = extra[(t * kw + cc) * 8 + g * 2];
+        sb[t] = extra[(t * kw + cc) * 8 + g * 2 + 1];
+      }
+      const uint32_t dw[4] = {u.q.x, u.q.y, u.q.z, u.q.w};
+      float d[2][MT];
+#pragma unroll
+      for (int t = 0; t < MT; ++t) d[0][t] = d[1][t] = 0.0f;
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t w2 = ((dw[s] >> (4 * j)) & 0x000F000Fu) | 0x43004300u;   // BF16 (128 + n_j, 128 + n_j+4)
 #pragma unroll
           for (int t = 0; t < MT; ++t) {
-            const uint32_t xw = j == 0 ? xq[t].x : j == 1 ? xq[t].y : j == 2 ? xq[t].z : xq[t].w;
-            acc[r][t] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, dw[j]), __builtin_bit_cast(bf16x2, xw),
-                                                         acc[r][t], false);
+            const uint32_t xw = j == 0 ? xq[t][s].x : j == 1 ? xq[t][s].y : j == 2 ? xq[t][s].z : xq[t][s].w;
+            d[s >> 1][t] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w2), __builtin_bit_cast(bf16x2, xw),
+                                                           d[s >> 1][t], false);
           }
+        }
+      const float sca = bf16_bits_to_f32(u.sb.x & 0xFFFFu), bia = bf16_bits_to_f32(u.sb.x >> 16);
+      const float scb = bf16_bits_to_f32(u.sb.y & 0xFFFFu), bib = bf16_bits_to_f32(u.sb.y >> 16);
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        acc_v[t] = fmaf(sca, fmaf(-128.0f, sa[t], d[0][t]), fmaf(bia, sa[t], acc_v[t]));
+        acc_v[t] = fmaf(scb, fmaf(-128.0f, sb[t], d[1][t]), fmaf(bib, sb[t], acc_v[t]));
+      }
+    } else {
+      uint4 xq[MT];
+#pragma unroll
+      for (int t = 0; t < MT; ++t) xq[t] = *reinterpret_cast<const uint4*>(xs + (size_t)t * ld + cc * 32 + 8 * g);
+      const uint32_t dw[4] = {u.q.x, u.q.y, u.q.z, u.q.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          const uint32_t xw = j == 0 ? xq[t].x : j == 1 ? xq[t].y : j == 2 ? xq[t].z : xq[t].w;
+          acc_v[t] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, dw[j]), __builtin_bit_cast(bf16x2, xw),
+                                                     acc_v[t], false);
+        }
+    }
+  };
+
+  // a finished tile: scale, then the epilogue (one split) or the FP32 partial (several)
+  const int n_pad = a.n_tiles * 16;
+  auto finish = [&](int tile) {
+    const int row = tile * 16 + m_row;
+    const float rs = a.row_scale != nullptr ? a.row_scale[(long long)expert * n_pad + row] : 1.0f;
+    if constexpr (MF) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 4 * g + i;
+        const float v = acc_m[i] * pscale[t & 15];
+        if (a.ks == 1) {
+          const float vs = v * rs;
+          const float up = __shfl_down(vs, 8, 16);
+          emit(a, pairs, cnt, tile, true, m_row, t, vs, up);
+        } else if (t < cnt) {
+          a.part[((long long)split * a.m + t) * n_pad + row] = v;
+        }
+        acc_m[i] = 0.0f;
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const float v = quad16_sum(acc_v[t]);
+        if (a.ks == 1) {
+          const float vs = v * rs;
+          const float up = __shfl_down(vs, 8, 16);
+          if (g == 0) emit(a, pairs, cnt, tile, true, m_row, t, vs, up);
+        } else if (g == 0 && t < cnt) {
+          a.part[((long long)split * a.m + t) * n_pad + row] = v;
+        }
+        acc_v[t] = 0.0f;
       }
     }
   };
 
-  for (int base = 0; base < kw; base += D) {
+  // ---- the stream: compute unit i, refill its ring slot with unit i + D ----------------------------------------
+  int ct = 0, cc = 0;
+  if constexpr (PIECES) {
+    // steps of 16 units = two scale groups: unit base + i computes with piece i / 8; the piece of the group two
+    // ahead is loaded when that group's first unit is issued (i = 0 → slot 1 … no: slot of group (base+i+8)/8)
+    for (int base = 0; base < total; base += 16) {
 #pragma unroll
-    for (int i = 0; i < D; ++i) {
-      const int cc = base + i;
-      if (cc < kw) compute(ring[i], cc);
-      const int c = c0 + min(cc + D, kw - 1);
-#pragma unroll
-      for (int r = 0; r < RT; ++r) load_unit<FMT>(ring[i][r], tbase[r] + (long long)c * UB, lane);
-    }
-  }
-
-  // the four k-groups of each row, then the K-slices (waves) in order
-#pragma unroll
-  for (int r = 0; r < RT; ++r)
-#pragma unroll
-    for (int t = 0; t < MT; ++t) acc[r][t] = quad16_sum(acc[r][t]);
-  if (nwaves > 1) {
-    if (g == 0) {
-#pragma unroll
-      for (int r = 0; r < RT; ++r)
-#pragma unroll
-        for (int t = 0; t < MT; ++t) red[((wave * RT + r) * MT + t) * 16 + m_row] = acc[r][t];
-    }
-    __syncthreads();
-    if (wave != 0) return;
-#pragma unroll
-    for (int r = 0; r < RT; ++r)
-#pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        float s = red[((0 * RT + r) * MT + t) * 16 + m_row];
-        for (int w = 1; w < nwaves; ++w) s += red[((w * RT + r) * MT + t) * 16 + m_row];
-        acc[r][t] = s;
+      for (int i = 0; i < 16; ++i) {
+        if (base + i < total) {
+          compute(ring[i & 7], cc, i >> 3, 0u);
+          if (++cc == kw) {
+            finish(tile0 + wave + ct * S);
+            cc = 0;
+            ++ct;
+          }
+        }
+        if ((i & 7) == 0 && base + i + 8 < total) {
+          // unit base + i + 8 starts a group (split width a multiple of 8): its piece goes to the slot of its
+          // group parity, ((base + i + 8) / 8) & 1 = (i >> 3) ^ 1, free since group (base + i) / 8 - 1 is done
+          const uint8_t* tb = wmat + (long long)(tile0 + wave + lt * S) * a.tile_stride;
+          spc[(i >> 3) ^ 1] = piece_of(tb, kb + lc);
+        }
+        load_next(ring[i & 7]);
       }
-  }
-  const int n_pad = a.n_tiles * 16;
-#pragma unroll
-  for (int r = 0; r < RT; ++r) {
-    const int row = (tile0 + r) * 16 + m_row;
-    const float rs = (a.row_scale != nullptr) ? a.row_scale[(long long)expert * n_pad + (tile_ok[r] ? row : 0)] : 1.0f;
-#pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      const float v = acc[r][t] * rs;
-      const float up = __shfl_down(v, 8, 16);
-      if (g == 0) emit(a, pairs, cnt, tile0 + r, tile_ok[r], m_row, t, v, up);
     }
+  } else {
+    for (int base = 0; base < total; base += D) {
+#pragma unroll
+      for (int i = 0; i < D; ++i) {
+        if (base + i < total) {
+          compute(ring[i], cc, 0, ring[i].s);
+          if (++cc == kw) {
+            finish(tile0 + wave + ct * S);
+            cc = 0;
+            ++ct;
+          }
+        }
+        load_next(ring[i]);
+      }
+    }
+  }
+}
+
+// the K splits of gemv_tk added in split order, scaled by the row scale, through the epilogue
+__global__ __launch_bounds__(256) void gemv_tk_reduce(Args a) {
+  const int t = blockIdx.y;
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  const bool silu = a.epilogue == MI_EPI_SILU_MUL || a.epilogue == MI_EPI_SILU_MUL_ROUNDED;
+  const int n_out = silu ? a.n / 2 : a.n;
+  if (c >= n_out) return;
+  const int n_pad = a.n_tiles * 16;
+  auto sum = [&](int row) {
+    float v = 0.0f;
+    for (int s = 0; s < a.ks; ++s) v += a.part[((long long)s * a.m + t) * n_pad + row];
+    return v * (a.row_scale != nullptr ? a.row_scale[row] : 1.0f);
+  };
+  if (silu) {
+    const int tile = c / 8, i = c % 8;
+    const float gv = sum(tile * 16 + i), uv = sum(tile * 16 + 8 + i);
+    float o;
+    if (a.epilogue == MI_EPI_SILU_MUL_ROUNDED) o = silu_f(round_bf16(gv)) * round_bf16(uv);
+    else o = silu_f(gv) * uv;
+    store_out(a, (long long)t * a.ldy + c, o);
+  } else {
+    float o = sum(c);
+    if (a.epilogue == MI_EPI_RESIDUAL) o += bf16_bits_to_f32(a.res[(long long)t * a.ldr + c]);
+    store_out(a, (long long)t * a.ldy + c, o);
   }
 }
 
@@ -794,25 +896,23 @@ __global__ __launch_bounds__(64) void dequant_t16(const uint8_t* w, const float*
                                                    float* out) {
   const int lane = threadIdx.x;
   const int tile = blockIdx.x / chunks, c = blockIdx.x % chunks;
-  constexpr int UB = unit_bytes(FMT);
-  const uint8_t* u = w + ((long long)tile * chunks + c) * UB;
-  const uint4 q = *reinterpret_cast<const uint4*>(u + 16 * lane);
+  Units<FMT> u;
+  load_chunk<FMT, true>(u, w + (long long)tile * tile_bytes(FMT, chunks), c, chunks, lane);
   const int row = tile * 16 + (lane & 15), g = lane >> 4;
   if (row >= n) return;
   float* o = out + (long long)row * k;
-  const uint32_t dw[4] = {q.x, q.y, q.z, q.w};
+  const uint32_t dw[4] = {u.q.x, u.q.y, u.q.z, u.q.w};
   if constexpr (FMT == FMT_NVFP4) {
-    const ScalePair sp = nvfp4_scales(*reinterpret_cast<const uint16_t*>(u + 1024 + 2 * lane));
+    const ScalePair sp = nvfp4_scales(u.s);
     const float rs = row_scale ? row_scale[row] : 1.0f;
     for (int s = 0; s < 4; ++s) {
       const f16x8 v = nvfp4_decode8(dw[s], s < 2 ? sp.e0 : sp.e1, s < 2 ? sp.m0 : sp.m1);
       for (int i = 0; i < 8; ++i) o[c * 128 + 32 * g + 8 * s + i] = (float)v[i] * rs;
     }
   } else if constexpr (FMT == FMT_INT4) {
-    const uint2 sb = *reinterpret_cast<const uint2*>(u + 1024 + 8 * (lane & 15));
     for (int s = 0; s < 4; ++s) {
       const f16x8 v = int4_decode8(dw[s]);
-      const uint32_t pr = s < 2 ? sb.x : sb.y;
+      const uint32_t pr = s < 2 ? u.sb.x : u.sb.y;
       const float sc = bf16_bits_to_f32(pr & 0xFFFFu), bi = bf16_bits_to_f32(pr >> 16);
       for (int i = 0; i < 8; ++i) o[c * 128 + 32 * s + 8 * g + int4_perm8(i)] = fmaf((float)v[i], sc, bi);
     }
@@ -826,10 +926,12 @@ __global__ __launch_bounds__(64) void dequant_t16(const uint8_t* w, const float*
 
 // ---- planning --------------------------------------------------------------------------------------------------
 struct Plan {
-  int dot;                 // 1: the VALU kernel (M <= 2), 0: MFMA
-  int rt, wk, kw, win;
-  int lds_rows, lds_ld, wave_lds;
-  size_t lds_bytes;
+  int kernel = 0;          // 1: gemv_row, 2: gemv_tk
+  int S = 1;               // waves per workgroup
+  int kw = 0;              // gemv_row: KW (chunks per wave); gemv_tk: chunks per split
+  int tb = 1, ks = 1, depth = 8;   // gemv_tk: tiles per workgroup, K splits, ring depth
+  int lds_rows = 1, row_ld = 0, row_wave_lds = 0;
+  size_t lds_bytes = 0;
 };
 
 int check_desc(const mi_gemv_desc* d) {
@@ -853,110 +955,170 @@ int check_desc(const mi_gemv_desc* d) {
   return MI_OK;
 }
 
-constexpr size_t kLdsBudget = 64 * 1024;
+constexpr size_t kMaxLds = 160 * 1024;
 
-size_t wave_lds_for(int fmt, int rows, int win_cols) {
-  size_t b = (size_t)rows * (win_cols + 8) * 2 + 3 * 16 * 4 + (fmt == FMT_INT4 ? (size_t)(win_cols / 64) * 16 * 4 : 0);
-  return (b + 15) / 16 * 16;
+// gemv_row for M <= 2: KW = 4 while K fits 16 slices of 4 chunks, else 8, else 16 (more, shorter waves keep more
+// loads in flight); gemv_tk otherwise
+Plan plan_row(const mi_gemv_desc* d, int fmt, int chunks, int rows) {
+  Plan p{};
+  int kw = chunks <= 64 ? 4 : chunks <= 128 ? 8 : chunks <= 160 ? 16 : 0;
+  if (const char* env = getenv("MI_GEMV_ROW")) kw = atoi(env);      // tuning sweeps
+  if (fmt == FMT_NVFP4 && kw < 8 && kw != 4) kw = 4;
+  if (kw <= 0) return p;
+  const int S = (chunks + kw - 1) / kw;
+  if (S > (kw == 16 ? 10 : 16)) return p;
+  const int kc = chunk_cols(fmt);
+  const int ld = kw * kc + 8;
+  size_t wl = (size_t)rows * ld * 2 + (fmt == FMT_INT4 ? (size_t)rows * kw * 8 * 4 : 0);
+  wl = (wl + 15) / 16 * 16;
+  const size_t lds = (size_t)S * wl + (size_t)S * 2 * 4 + (size_t)S * rows * 16 * 4;
+  if (lds > kMaxLds) return p;
+  p.kernel = 1; p.S = S; p.kw = kw; p.lds_rows = rows; p.row_ld = ld; p.row_wave_lds = (int)wl; p.lds_bytes = lds;
+  return p;
 }
 
-Plan make_plan(const mi_gemv_desc* d) {
-  const int fmt = d->format;
-  int force[3] = {0, 0, 0};   // MI_GEMV_PLAN="rt,wk,win" pins a plan (tuning sweeps)
-  if (const char* env = getenv("MI_GEMV_PLAN")) sscanf(env, "%d,%d,%d", &force[0], &force[1], &force[2]);
-  const int kc = chunk_cols(fmt);
-  const int chunks = d->k / kc;
-  const int n_tiles = (d->n + 15) / 16;
-  const int groups = d->groups ? d->max_groups : 1;
-  const int rows = d->groups ? std::min(16, d->m) : d->m;   // a group holds at most one pair per token
+int tk_lds(int fmt, int rows, int kc, bool mf) {
+  const int kcols = chunk_cols(fmt);
+  size_t b = (size_t)rows * (kc * kcols + 8) * 2 + 16 * 4;
+  if (fmt == FMT_INT4) b += mf ? (size_t)kc * 2 * 16 * 4 : (size_t)rows * kc * 8 * 4;
+  b += 64;
+  return (int)((b + 15) / 16 * 16);
+}
+
+// gemv_tk: K splits (ks), tiles per workgroup (tb), waves per workgroup (S), ring depth (D ∈ {4, 8, 12}), chosen by
+// a bytes-over-rate model: the rate falls off below ~96 KB of weights in flight per CU; the activations cost their
+// re-reads (workgroups × split bytes), split K its partials and a second launch; a fused norm needs one split.
+Plan plan_tk(const mi_gemv_desc* d, int fmt, int chunks, int n_tiles, int groups, int rows) {
   Plan best{};
-  double best_score = -1e30;
-  const char* fk = getenv("MI_GEMV_KERNEL");                 // "dot" / "mfma" pins the kernel (tuning sweeps)
-  const bool dot_ok = rows <= 2 && !(fk && fk[0] == 'm');
-  if (dot_ok) {
-    for (int rt : {1, 2, 4}) {
-      if (force[0] && rt != force[0]) continue;
-      for (int wk = 1; wk <= 8; ++wk) {
-        if (force[0] && wk != force[1]) continue;
-        const int kwmax = (chunks + wk - 1) / wk;
-        if (kwmax < 1 || chunks < wk) continue;
-        size_t wl = (size_t)rows * (kwmax * kc + 8) * 2 + (fmt == FMT_INT4 ? (size_t)rows * kwmax * 8 * 4 : 0);
-        wl = (wl + 15) / 16 * 16;
-        const size_t lds = (size_t)wk * wl + (size_t)wk * 16 * 4 + (size_t)wk * rt * rows * 16 * 4;
-        if (lds > kLdsBudget) continue;
-        const int row_blocks = (n_tiles + rt - 1) / rt;
-        const double wgs = (double)row_blocks * groups;
-        const double waves = wgs * wk;
-        const int per_cu = std::max(1, std::min((int)(160 * 1024 / lds), 16 / wk));
-        const double rounds = wgs / (256.0 * per_cu);
-        const double tail = std::ceil(rounds) / std::max(rounds, 1e-9);
-        const double pad = (double)row_blocks * rt / n_tiles;
-        const int depth = 8 / rt;
-        double score = 0.0;
-        score -= (waves < 4096 ? (4096.0 / waves) : 1.0) * 2.0;
-        score -= (rounds >= 1.0 ? (tail - 1.0) * 3.0 : 0.0);
-        score -= (pad - 1.0) * 4.0;
-        score -= (kwmax < depth ? (depth - kwmax) * 0.3 : 0.0);
-        score -= (kwmax > 16 ? (kwmax - 16) * 0.02 : 0.0);
-        score -= 0.2 * (rows * 2.0) / (rt * 16.0 * 0.5625);
-        if (score > best_score) {
-          best_score = score;
-          best.dot = 1; best.rt = rt; best.wk = wk; best.kw = kwmax; best.win = kwmax;
-          best.lds_rows = rows; best.lds_ld = kwmax * kc + 8; best.wave_lds = (int)wl; best.lds_bytes = lds;
+  const bool mf = rows > 2;
+  int force[4] = {0, 0, 0, 0};           // MI_GEMV_TK="ks,tb,S,D" pins a plan (tuning sweeps)
+  if (const char* env = getenv("MI_GEMV_TK")) sscanf(env, "%d,%d,%d,%d", &force[0], &force[1], &force[2], &force[3]);
+  const int ub = unit_bytes(fmt);
+  double best_cost = 1e30;
+  for (int ks = 1; ks <= 16; ++ks) {
+    if (force[0] && ks != force[0]) continue;
+    if (ks > 1 && (d->norm_w || d->groups)) break;
+    int kc = (chunks + ks - 1) / ks;
+    if (fmt == FMT_NVFP4 && ks > 1) kc = (kc + 7) / 8 * 8;   // splits on scale-group boundaries
+    if (ks > 1 && (ks - 1) * kc >= chunks) continue;    // no empty split
+    const int lrows = mf ? std::min(16, rows) : rows;
+    const int lds = tk_lds(fmt, lrows, kc, mf);
+    if (lds > 96 * 1024) continue;
+    for (int S : {1, 2, 4, 8}) {
+      if (force[2] && S != force[2]) continue;
+      for (int tb = S; tb <= 8 * S; tb += S) {
+        if (force[1] && tb != force[1]) continue;
+        if (tb > n_tiles && tb != S) break;
+        for (int D : {4, 8, 12}) {
+          if (force[3] && D != force[3]) continue;
+          // NVFP4 on whole scale groups streams with D = 8 (the piece ring); otherwise any depth
+          if (fmt == FMT_NVFP4 && chunks % 8 == 0 && kc % 8 == 0 && D != 8) continue;
+          const double wgs = (double)((n_tiles + tb - 1) / tb) * ks * groups;
+          const int per_cu_lds = std::max(1, (int)(kMaxLds / lds));
+          const int per_cu = std::min(per_cu_lds, 32 / S);
+          const double resident_waves = std::min(wgs, 256.0 * per_cu) * S / 256.0;
+          const double inflight = resident_waves * D * ub;
+          const double rounds = wgs / (256.0 * per_cu);
+          const double tail = rounds > 1.0 ? std::ceil(rounds) / rounds : 1.0;
+          const double w_bytes = (double)n_tiles * chunks * ub * groups;
+          const double x_bytes = wgs * lrows * kc * chunk_cols(fmt) * 2.0;
+          const double p_bytes = ks > 1 ? 2.0 * ks * rows * n_tiles * 16 * 4 : 0.0;
+          const double rate = std::min(1.0, inflight / (96.0 * 1024));
+          double cost = (w_bytes + 0.5 * x_bytes + p_bytes) / std::max(rate, 1e-3) * tail;
+          cost += ks > 1 ? w_bytes * 0.12 : 0.0;
+          const int lw = ((n_tiles + tb - 1) / tb) * tb - n_tiles;
+          cost *= 1.0 + (double)lw / n_tiles;
+          if (cost < best_cost) {
+            best_cost = cost;
+            best.kernel = 2; best.S = S; best.kw = kc; best.tb = tb; best.ks = ks; best.depth = D;
+            best.lds_rows = lrows; best.lds_bytes = lds;
+          }
         }
-      }
-    }
-    return best;
-  }
-  for (int rt : {1, 2, 4}) {
-    if (force[0] && rt != force[0]) continue;
-    for (int wk = 1; wk <= 8; ++wk) {
-      if (chunks % wk) continue;
-      if (force[0] && wk != force[1]) continue;
-      const int kw = chunks / wk;
-      for (int win = kw; win >= 1; --win) {
-        if (force[0] && win != std::min(force[2], kw)) continue;
-        const size_t wl = wave_lds_for(fmt, rows, win * kc);
-        const size_t lds = std::max((size_t)wk * wl, (size_t)wk * rt * 64 * 16) + (size_t)wk * 16 * 4 + 64;
-        if (lds > kLdsBudget) continue;
-        const int nwin = (kw + win - 1) / win;
-        const int row_blocks = (n_tiles + rt - 1) / rt;
-        const double wgs = (double)row_blocks * groups;
-        const double waves = wgs * wk;
-        const int per_cu = std::max(1, std::min((int)(160 * 1024 / lds), 16 / wk));
-        const double rounds = wgs / (256.0 * per_cu);
-        const double tail = std::ceil(rounds) / std::max(rounds, 1e-9);
-        const double pad = (double)row_blocks * rt / n_tiles;
-        const int depth = 8 / rt;
-        double score = 0.0;
-        score -= (waves < 4096 ? (4096.0 / waves) : 1.0) * 2.0;          // starved for parallelism
-        score -= (rounds >= 1.0 ? (tail - 1.0) * 3.0 : 0.0);
-        score -= (pad - 1.0) * 4.0;
-        score -= (nwin - 1) * 0.4;                                        // each extra window drains the ring
-        score -= (kw < depth ? (depth - kw) * 0.3 : 0.0);                 // prefetch ring not filled
-        score -= (kw > 16 ? (kw - 16) * 0.02 : 0.0);                      // long slices: coarse tail
-        // activation staging relative to weight bytes streamed per wave: rows·2 per column vs rt·16·0.5625
-        score -= 0.6 * (rows * 2.0) / (rt * 16.0 * 0.5625);
-        if (score > best_score) {
-          best_score = score;
-          best.dot = 0; best.rt = rt; best.wk = wk; best.kw = kw; best.win = win;
-          best.lds_rows = rows; best.lds_ld = win * kc + 8; best.wave_lds = (int)wl; best.lds_bytes = lds;
-        }
-        break;   // the widest window that fits is the one to use for this (rt, wk)
       }
     }
   }
   return best;
 }
 
-template <int FMT, int RT>
-void launch(const Args& a, const Plan& p, dim3 grid, hipStream_t s) {
-  if (p.dot) {
-    if (p.lds_rows <= 1) hipLaunchKernelGGL((gemv_dot<FMT, RT, 1>), grid, dim3(64 * p.wk), p.lds_bytes, s, a);
-    else hipLaunchKernelGGL((gemv_dot<FMT, RT, 2>), grid, dim3(64 * p.wk), p.lds_bytes, s, a);
-  } else {
-    hipLaunchKernelGGL((gemv_t16<FMT, RT>), grid, dim3(64 * p.wk), p.lds_bytes, s, a);
+Plan make_plan(const mi_gemv_desc* d) {
+  const int fmt = d->format;
+  const int chunks = d->k / chunk_cols(fmt);
+  const int n_tiles = (d->n + 15) / 16;
+  const int groups = d->groups ? d->max_groups : 1;
+  const int rows = d->groups ? std::min(16, d->m) : d->m;   // a group holds at most one pair per token
+  const char* fk = getenv("MI_GEMV_KERNEL");                 // "row" / "tk" pins the kernel (tuning sweeps)
+  if (rows <= 2 && !(fk && fk[0] == 't')) {
+    const Plan p = plan_row(d, fmt, chunks, rows);
+    if (p.kernel) return p;
   }
+  return plan_tk(d, fmt, chunks, n_tiles, groups, rows);
+}
+
+// dynamic LDS above 64 KB must be allowed per kernel once
+template <typename K>
+void allow_lds(K kernel) {
+  static std::once_flag once;
+  std::call_once(once, [&] {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)kMaxLds);
+    (void)hipGetLastError();
+  });
+}
+
+template <int FMT, int MT>
+void launch_tk_d(const Args& a, const Plan& p, dim3 g, hipStream_t s) {
+  const bool pieces = FMT == FMT_NVFP4 && a.chunks % 8 == 0 && p.kw % 8 == 0;
+  if (pieces) { allow_lds(gemv_tk<FMT, MT, 8, true>); hipLaunchKernelGGL((gemv_tk<FMT, MT, 8, true>), g, dim3(64 * p.S), p.lds_bytes, s, a); }
+  else if (p.depth == 4) { allow_lds(gemv_tk<FMT, MT, 4, false>); hipLaunchKernelGGL((gemv_tk<FMT, MT, 4, false>), g, dim3(64 * p.S), p.lds_bytes, s, a); }
+  else if (p.depth == 8) { allow_lds(gemv_tk<FMT, MT, 8, false>); hipLaunchKernelGGL((gemv_tk<FMT, MT, 8, false>), g, dim3(64 * p.S), p.lds_bytes, s, a); }
+  else { allow_lds(gemv_tk<FMT, MT, 12, false>); hipLaunchKernelGGL((gemv_tk<FMT, MT, 12, false>), g, dim3(64 * p.S), p.lds_bytes, s, a); }
+}
+
+template <int FMT, int MT>
+void launch_row_k(const Args& a, const Plan& p, dim3 g, hipStream_t s) {
+  if (p.kw == 4) { allow_lds(gemv_row<FMT, MT, 4>); hipLaunchKernelGGL((gemv_row<FMT, MT, 4>), g, dim3(64 * p.S), p.lds_bytes, s, a); }
+  else if (p.kw == 8) { allow_lds(gemv_row<FMT, MT, 8>); hipLaunchKernelGGL((gemv_row<FMT, MT, 8>), g, dim3(64 * p.S), p.lds_bytes, s, a); }
+  else { allow_lds(gemv_row<FMT, MT, 16>); hipLaunchKernelGGL((gemv_row<FMT, MT, 16>), g, dim3(64 * p.S), p.lds_bytes, s, a); }
+}
+
+template <int FMT>
+void launch(const Args& a, const Plan& p, int groups, hipStream_t s) {
+  if (p.kernel == 1) {
+    const dim3 g(a.n_tiles, groups);
+    if (p.lds_rows == 2) launch_row_k<FMT, 2>(a, p, g, s);
+    else launch_row_k<FMT, 1>(a, p, g, s);
+    return;
+  }
+  const dim3 g((a.n_tiles + p.tb - 1) / p.tb, p.ks, groups);
+  if (p.lds_rows > 2) launch_tk_d<FMT, 16>(a, p, g, s);
+  else if (p.lds_rows == 2) launch_tk_d<FMT, 2>(a, p, g, s);
+  else launch_tk_d<FMT, 1>(a, p, g, s);
+  if (p.ks > 1) {
+    const bool silu = a.epilogue == MI_EPI_SILU_MUL || a.epilogue == MI_EPI_SILU_MUL_ROUNDED;
+    const int n_out = silu ? a.n / 2 : a.n;
+    hipLaunchKernelGGL(gemv_tk_reduce, dim3((n_out + 255) / 256, a.m), dim3(256), 0, s, a);
+  }
+}
+
+// the library's FP32 partials buffer for split-K plans (per device, grown on demand; a caller that cannot allocate
+// passes its own through mi_gemv_desc.workspace)
+std::mutex g_ws_mu;
+std::vector<std::pair<void*, size_t>> g_ws;
+
+int partials_workspace(size_t bytes, void** out) {
+  int dev = 0;
+  MI_TRY_HIP(hipGetDevice(&dev), "hipGetDevice");
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  if ((int)g_ws.size() <= dev) g_ws.resize(dev + 1, {nullptr, 0});
+  auto& w = g_ws[dev];
+  if (w.second < bytes) {
+    if (w.first) MI_TRY_HIP(hipFree(w.first), "hipFree(gemv partials)");
+    w = {nullptr, 0};
+    MI_TRY_HIP(hipMalloc(&w.first, bytes), "hipMalloc(gemv partials)");
+    w.second = bytes;
+  }
+  *out = w.first;
+  return MI_OK;
 }
 
 }  // namespace
@@ -965,32 +1127,35 @@ extern "C" {
 
 size_t mi_pack_bytes(int32_t format, int32_t n, int32_t k) {
   if (n <= 0 || k <= 0) return 0;
+  if (format != FMT_NVFP4 && format != FMT_INT4 && format != FMT_BF16) return 0;
   const int kc = chunk_cols(format);
   if (k % kc) return 0;
-  return (size_t)((n + 15) / 16) * (k / kc) * unit_bytes(format);
+  return (size_t)((n + 15) / 16) * (size_t)tile_bytes(format, k / kc);
 }
 
 size_t mi_gemv_workspace_bytes(const mi_gemv_desc* d) {
-  (void)d;
-  return 0;
+  if (check_desc(d) != MI_OK) return 0;
+  const Plan p = make_plan(d);
+  return p.kernel == 2 && p.ks > 1 ? (size_t)p.ks * d->m * ((d->n + 15) / 16) * 16 * sizeof(float) : 0;
 }
 
 int mi_gemv_plan(const mi_gemv_desc* d, int32_t out[7]) {
   if (int rc = check_desc(d)) return rc;
   MI_REQUIRE(out, "mi_gemv_plan: null output");
   const Plan p = make_plan(d);
-  MI_REQUIRE(p.kw > 0, "mi_gemv_plan: no launch plan fits (k=%d, m=%d)", d->k, d->m);
+  MI_REQUIRE(p.kernel, "mi_gemv_plan: no launch plan fits (k=%d, m=%d)", d->k, d->m);
   const int n_tiles = (d->n + 15) / 16;
-  const int row_blocks = (n_tiles + p.rt - 1) / p.rt;
-  out[0] = p.rt; out[1] = p.wk; out[2] = p.kw; out[3] = p.win; out[4] = p.dot ? -1 : (p.kw + p.win - 1) / p.win;
-  out[5] = (int32_t)p.lds_bytes; out[6] = row_blocks * (d->groups ? d->max_groups : 1);
+  const int groups = d->groups ? d->max_groups : 1;
+  out[0] = p.kernel; out[1] = p.S; out[2] = p.kw;
+  out[3] = p.kernel == 1 ? 1 : p.tb; out[4] = p.kernel == 1 ? 1 : p.ks; out[5] = (int32_t)p.lds_bytes;
+  out[6] = (p.kernel == 1 ? n_tiles : (n_tiles + p.tb - 1) / p.tb * p.ks) * groups;
   return MI_OK;
 }
 
 int mi_gemv(const mi_gemv_desc* d, void* stream) {
   if (int rc = check_desc(d)) return rc;
   const Plan p = make_plan(d);
-  MI_REQUIRE(p.kw > 0, "mi_gemv: no launch plan fits (k=%d, m=%d)", d->k, d->m);
+  MI_REQUIRE(p.kernel, "mi_gemv: no launch plan fits (k=%d, m=%d)", d->k, d->m);
   Args a{};
   a.w = static_cast<const uint8_t*>(d->w);
   a.row_scale = d->row_scale;
@@ -1004,29 +1169,34 @@ int mi_gemv(const mi_gemv_desc* d, void* stream) {
   a.n = d->n; a.k = d->k; a.m = d->m;
   a.n_tiles = (d->n + 15) / 16;
   a.chunks = d->k / chunk_cols(d->format);
-  a.row_blocks = (a.n_tiles + p.rt - 1) / p.rt;
-  a.kw = p.kw; a.win = p.win; a.wave_lds = p.wave_lds;
+  a.tile_stride = tile_bytes(d->format, a.chunks);
+  a.expert_stride = (long long)a.n_tiles * a.tile_stride;
   a.epilogue = d->epilogue;
   a.top_k = d->top_k;
   a.x_per_slot = d->x_per_slot;
   a.out_f32 = d->out_f32;
   a.lds_rows = p.lds_rows;
-  a.lds_ld = p.lds_ld;
-  a.expert_stride = (long long)a.n_tiles * a.chunks * unit_bytes(d->format);
-  const dim3 grid(a.row_blocks, d->groups ? d->max_groups : 1);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  switch (d->format * 8 + p.rt) {
-    case FMT_NVFP4 * 8 + 1: launch<FMT_NVFP4, 1>(a, p, grid, s); break;
-    case FMT_NVFP4 * 8 + 2: launch<FMT_NVFP4, 2>(a, p, grid, s); break;
-    case FMT_NVFP4 * 8 + 4: launch<FMT_NVFP4, 4>(a, p, grid, s); break;
-    case FMT_INT4 * 8 + 1: launch<FMT_INT4, 1>(a, p, grid, s); break;
-    case FMT_INT4 * 8 + 2: launch<FMT_INT4, 2>(a, p, grid, s); break;
-    case FMT_INT4 * 8 + 4: launch<FMT_INT4, 4>(a, p, grid, s); break;
-    case FMT_BF16 * 8 + 1: launch<FMT_BF16, 1>(a, p, grid, s); break;
-    case FMT_BF16 * 8 + 2: launch<FMT_BF16, 2>(a, p, grid, s); break;
-    default: launch<FMT_BF16, 4>(a, p, grid, s); break;
+  a.tb = p.tb;
+  a.ks = p.ks;
+  a.kc = p.kw;
+  a.row_ld = p.row_ld;
+  a.row_wave_lds = p.row_wave_lds;
+  if (p.kernel == 2 && p.ks > 1) {
+    const size_t need = (size_t)p.ks * d->m * ((d->n + 15) / 16) * 16 * sizeof(float);
+    void* ws = d->workspace;
+    if (ws) {
+      MI_REQUIRE(d->workspace_bytes >= need, "mi_gemv: workspace %zu B < %zu B", d->workspace_bytes, need);
+    } else if (int rc = partials_workspace(need, &ws)) {
+      return rc;
+    }
+    a.part = static_cast<float*>(ws);
   }
-  MI_TRY_HIP(hipGetLastError(), "gemv_t16 launch");
+  const int groups = d->groups ? d->max_groups : 1;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (d->format == FMT_NVFP4) launch<FMT_NVFP4>(a, p, groups, s);
+  else if (d->format == FMT_INT4) launch<FMT_INT4>(a, p, groups, s);
+  else launch<FMT_BF16>(a, p, groups, s);
+  MI_TRY_HIP(hipGetLastError(), "gemv launch");
   return MI_OK;
 }
 

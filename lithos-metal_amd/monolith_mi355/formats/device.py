@@ -69,6 +69,7 @@ def nvfp4_quantize(w: torch.Tensor):
 
 def pack_nvfp4(codes: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
     """The T16 NVFP4 layout (see :mod:`.pack`) of ``codes [N, K/2]``, ``scales [N, K/16]`` → uint8 [bytes]."""
+    from .pack import nvfp4_groups
     n, kh = codes.shape
     k = kh * 2
     nt, c = -(-n // 16), k // 128
@@ -77,8 +78,14 @@ def pack_nvfp4(codes: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
         codes = torch.cat([codes, codes.new_zeros(rows - n, kh)])
         scales = torch.cat([scales, scales.new_zeros(rows - n, k // 16)])
     cw = codes.reshape(nt, 16, c, 4, 16).permute(0, 2, 3, 1, 4).reshape(nt, c, 1024)
-    sw = scales.reshape(nt, 16, c, 4, 2).permute(0, 2, 3, 1, 4).reshape(nt, c, 128)
-    return torch.cat([cw, sw], dim=-1).reshape(-1).contiguous()
+    sw = scales.reshape(nt, 16, c, 4, 2).permute(0, 2, 3, 1, 4).reshape(nt, c, 64, 2)
+    parts = []
+    for c0, g, _, sb in nvfp4_groups(c)[0]:
+        parts.append(cw[:, c0: c0 + g].reshape(nt, g * 1024))
+        piece = sw.new_zeros(nt, 64, sb // 64)
+        piece[:, :, : 2 * g] = sw[:, c0: c0 + g].permute(0, 2, 1, 3).reshape(nt, 64, 2 * g)
+        parts.append(piece.reshape(nt, sb))
+    return torch.cat(parts, dim=-1).reshape(-1).contiguous()
 
 
 def interleave_rows(gate: torch.Tensor, up: torch.Tensor, chunk: int = 8) -> torch.Tensor:

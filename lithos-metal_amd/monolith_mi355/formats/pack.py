@@ -5,15 +5,19 @@ stripes.
 A matrix ``[N, K]`` is cut into 16-row tiles (the last one zero-padded) and 128-column chunks (32 for BF16). Each
 (tile, chunk) is one unit, tile-major then chunk, so one wave walking a tile's K reads a contiguous stream:
 
-* NVFP4 (1152 B): bytes ``[16·l, 16·l+16)`` for lane ``l`` (row ``r = l % 16``, k-group ``g = l // 16``) hold the 32
-  codes of row ``r`` at columns ``128·c + 32·g + [0, 32)`` — the checkpoint's own bytes, low nibble first; bytes
-  ``[1024 + 2·l, +2)`` the two E4M3 block scales of those 32 columns.
+* NVFP4: the chunks of a tile come in groups of 8 (the last group holds the rest): the group's 1 KiB code blocks,
+  then one scale block. In the code block of chunk ``c``, bytes ``[16·l, 16·l+16)`` for lane ``l`` (row
+  ``r = l % 16``, k-group ``g = l // 16``) hold the 32 codes of row ``r`` at columns ``128·c + 32·g + [0, 32)`` —
+  the checkpoint's own bytes, low nibble first. The scale block gives lane ``l`` a piece of 16 bytes (8 bytes when
+  the group has at most 4 chunks) whose bytes ``2·i, 2·i + 1`` are the two E4M3 block scales of chunk ``i`` of the
+  group for that lane's 32 columns — one 16-byte load per lane brings the scales of 8 chunks.
 * INT4 affine (1152 B): lane ``l``'s dword ``s`` (``s = 0..3``) holds the 8 codes of row ``r`` at columns
   ``128·c + 32·s + 8·g + [0, 8)``; bytes ``[1024 + 8·r, +8)`` the BF16 (scale, bias) pairs of groups ``2c`` and
   ``2c + 1`` of row ``r`` (scale in the low half, as the reference's pairs, ``formats/int4_affine.py:460``).
 * BF16 (1024 B): lane ``l``'s 16 bytes are the 8 values of row ``r`` at columns ``32·c + 8·g + [0, 8)``.
 
-The byte count per weight is the format's own (0.5625 B for NVFP4 and INT4): no padding inside a unit.
+The byte count per weight is the format's own (0.5625 B for NVFP4 and INT4) except for the scale block of a short
+last NVFP4 group (K not a multiple of 1024 columns), padded to 8 or 16 bytes per lane.
 """
 
 from __future__ import annotations
@@ -39,7 +43,20 @@ def unit_bytes(fmt: str) -> int:
     return UNIT_B if fmt == "bf16" else UNIT_Q
 
 
+def nvfp4_groups(chunks: int):
+    """``[(first chunk, chunks in the group, byte offset in the tile, scale-block bytes), …]`` and the tile bytes."""
+    out, off = [], 0
+    for c0 in range(0, chunks, 8):
+        g = min(8, chunks - c0)
+        sb = 1024 if g > 4 else 512
+        out.append((c0, g, off, sb))
+        off += g * 1024 + sb
+    return out, off
+
+
 def pack_bytes(fmt: str, n: int, k: int) -> int:
+    if fmt == "nvfp4":
+        return -(-n // 16) * nvfp4_groups(k // 128)[1]
     return -(-n // 16) * (k // chunk_cols(fmt)) * unit_bytes(fmt)
 
 
@@ -76,8 +93,14 @@ def pack(spec: DequantSpec, row_scale: Optional[np.ndarray] = None) -> Tuple[np.
         w = _pad_rows(np.asarray(spec.tensors["weight"], np.uint8), rows)            # [rows, K/2]
         sc = _pad_rows(np.asarray(spec.tensors["weight_scale"], np.uint8), rows)     # [rows, K/16]
         codes = w.reshape(nt, 16, c, 4, 16).transpose(0, 2, 3, 1, 4).reshape(nt, c, 1024)
-        scales = sc.reshape(nt, 16, c, 4, 2).transpose(0, 2, 3, 1, 4).reshape(nt, c, 128)
-        data = np.concatenate([codes, scales], axis=-1)
+        scales = sc.reshape(nt, 16, c, 4, 2).transpose(0, 2, 3, 1, 4).reshape(nt, c, 64, 2)      # [nt, c, lane, 2]
+        parts = []
+        for c0, g, _, sb in nvfp4_groups(c)[0]:
+            parts.append(codes[:, c0: c0 + g].reshape(nt, g * 1024))
+            piece = np.zeros((nt, 64, sb // 64), np.uint8)
+            piece[:, :, : 2 * g] = scales[:, c0: c0 + g].transpose(0, 2, 1, 3).reshape(nt, 64, 2 * g)
+            parts.append(piece.reshape(nt, sb))
+        data = np.concatenate(parts, axis=-1)
         if row_scale is None:
             row_scale = np.full(n, spec.params["weight_scale_2"], np.float32)
         rs = np.zeros(rows, np.float32)
@@ -105,9 +128,16 @@ def unpack(data: np.ndarray, info: PackInfo) -> DequantSpec:
     nt, c, n, k = info.n_tiles, info.chunks, info.n, info.k
     d = np.asarray(data, np.uint8)
     if info.format == "nvfp4":
-        d = d.reshape(nt, c, UNIT_Q)
-        w = d[..., :1024].reshape(nt, c, 4, 16, 16).transpose(0, 3, 1, 2, 4).reshape(nt * 16, k // 2)
-        sc = d[..., 1024:].reshape(nt, c, 4, 16, 2).transpose(0, 3, 1, 2, 4).reshape(nt * 16, k // 16)
+        groups, tile = nvfp4_groups(c)
+        d = d.reshape(nt, tile)
+        codes = np.empty((nt, c, 1024), np.uint8)
+        scales = np.empty((nt, c, 64, 2), np.uint8)
+        for c0, g, off, sb in groups:
+            codes[:, c0: c0 + g] = d[:, off: off + g * 1024].reshape(nt, g, 1024)
+            piece = d[:, off + g * 1024: off + g * 1024 + sb].reshape(nt, 64, sb // 64)[:, :, : 2 * g]
+            scales[:, c0: c0 + g] = piece.reshape(nt, 64, g, 2).transpose(0, 2, 1, 3)
+        w = codes.reshape(nt, c, 4, 16, 16).transpose(0, 3, 1, 2, 4).reshape(nt * 16, k // 2)
+        sc = scales.reshape(nt, c, 4, 16, 2).transpose(0, 3, 1, 2, 4).reshape(nt * 16, k // 16)
         rs = info.row_scale[:n] if info.row_scale is not None else np.ones(n, np.float32)
         s2 = float(rs[0]) if n else 1.0
         return DequantSpec("nvfp4", (n, k), {"weight": w[:n], "weight_scale": sc[:n]}, {"weight_scale_2": s2})

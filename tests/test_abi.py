@@ -53,15 +53,21 @@ def _desc(hip, **kw):
 
 
 @pytest.mark.parametrize("n,k,m", [(34816, 5120, 1), (5120, 17408, 1), (34816, 5120, 8), (5120, 17408, 8),
-                                   (4096, 4096, 1), (1024, 2048, 16), (16, 128, 3)])
+                                   (4096, 4096, 1), (1024, 2048, 16), (16, 128, 3), (5120, 17408, 2)])
 def test_gemv_plans_fit_the_hardware(n, k, m):
     from monolith_mi355.runtime import hip
     out = (C.c_int32 * 7)()
     hip.call("mi_gemv_plan", C.byref(_desc(hip, n=n, k=k, m=m, ldx=k, ldy=n)), out)
-    rt, wk, kw, win, nwin, lds, wgs = list(out)
-    assert rt in (1, 2, 4) and 1 <= wk <= 8 and kw >= 1 and lds <= 64 * 1024 and wgs >= 1
-    assert (nwin == -1) == (m <= 2)                      # the VALU kernel for M <= 2, MFMA above
-    assert wk * kw >= k // 128
+    kernel, waves, kw, tb, ks, lds, wgs = list(out)
+    assert kernel == (1 if m <= 2 else 2)                  # gemv_row (VALU) for M <= 2, gemv_tk (MFMA) above
+    assert 1 <= waves <= 16 and kw >= 1 and lds <= 160 * 1024 and wgs >= 1 and ks >= 1 and tb >= 1
+    chunks = k // 128
+    if kernel == 1:
+        assert kw in (4, 8, 16) and waves * kw >= chunks and (waves - 1) * kw < chunks
+    else:
+        assert ks * kw >= chunks and (ks - 1) * kw < chunks
+    ws = hip.load().mi_gemv_workspace_bytes(C.byref(_desc(hip, n=n, k=k, m=m, ldx=k, ldy=n)))
+    assert (ws > 0) == (kernel == 2 and ks > 1)
 
 
 def test_gemv_rejects_bad_descriptors_before_launch():

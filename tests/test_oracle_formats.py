@@ -161,7 +161,7 @@ def test_device_quantizer_and_pack_match_host():
 
 
 @pytest.mark.parametrize("fmt", ["nvfp4", "int4_affine", "bf16"])
-@pytest.mark.parametrize("n,k", [(37, 512), (16, 128), (100, 1024)])
+@pytest.mark.parametrize("n,k", [(37, 512), (16, 128), (100, 1024), (20, 1664), (33, 2304)])
 def test_t16_pack_round_trip_and_unit_map(fmt, n, k):
     from monolith_mi355.formats import FORMATS
     from monolith_mi355.formats import pack as P
@@ -173,8 +173,14 @@ def test_t16_pack_round_trip_and_unit_map(fmt, n, k):
     assert data.size == P.pack_bytes(fmt, n, k) == info.nbytes
     back = P.unpack(data, info)
     assert np.array_equal(FORMATS[fmt].dequantize(back), FORMATS[fmt].dequantize(spec))
-    # lane 21 of tile 1, chunk 0: row 16 + 5, k-group 1
+    # lane 21 of tile 1, chunk 0: row 16 + 5, k-group 1 (codes in the chunk's block, scales in the group's piece)
     if fmt == "nvfp4" and n > 21:
-        unit = data[(1 * info.chunks + 0) * P.UNIT_Q:][:P.UNIT_Q]
-        assert np.array_equal(unit[16 * 21: 16 * 22], spec.tensors["weight"][21, 16:32])
-        assert np.array_equal(unit[1024 + 2 * 21: 1024 + 2 * 22], spec.tensors["weight_scale"][21, 2:4])
+        groups, tile_b = P.nvfp4_groups(info.chunks)
+        tile = data[tile_b:][:tile_b]
+        g0 = groups[0][1]
+        piece = 16 if g0 > 4 else 8
+        assert np.array_equal(tile[16 * 21: 16 * 22], spec.tensors["weight"][21, 16:32])
+        assert np.array_equal(tile[g0 * 1024 + piece * 21: g0 * 1024 + piece * 21 + 2], spec.tensors["weight_scale"][21, 2:4])
+        if info.chunks > 1:      # chunk 1 of the group: the next two bytes of the same piece
+            assert np.array_equal(tile[g0 * 1024 + piece * 21 + 2: g0 * 1024 + piece * 21 + 4],
+                                  spec.tensors["weight_scale"][21, 10:12])
