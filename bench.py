@@ -42,8 +42,8 @@ def parse():
     p.add_argument("--layers", type=int, default=10, help="distinct layer instances the steps rotate over")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--only", choices=["gdn", "attn", "mlp", "gateup"], default=None,
-                   help="time one workload only (profiling runs)")
+    p.add_argument("--only", choices=["gdn", "attn", "mlp", "gateup", "copy"], default=None,
+                   help="time one workload only (profiling runs; copy = a 256 MiB device copy, the counter reference)")
     return p.parse_args()
 
 
@@ -91,6 +91,15 @@ def main():
 
     def xin(m):
         return torch.randn(m, 5120, generator=gen, device=dev).to(torch.bfloat16)
+
+    if args.only == "copy":
+        # a plain device-to-device copy of known size: what HBM counters read for 256 MiB in + 256 MiB out
+        with torch.cuda.stream(stream):
+            srcs = [torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0) for _ in range(4)]
+            dst = torch.empty(64 << 20, dtype=torch.float32, device=dev)
+            ms = timed_graph(lambda i: dst.copy_(srcs[i % 4]), 20, 2, stream)
+        print(json.dumps({"copy": {"ms": round(ms, 5), "bytes_read": 256 << 20, "bytes_written": 256 << 20}}))
+        return
 
     with torch.cuda.stream(stream):
         gdn = [GdnDecoderLayer(seed=10 + i, device=dev) for i in range(n)] if args.only in (None, "gdn", "mlp", "gateup") else []
@@ -172,7 +181,7 @@ def main():
         "attn_layer_ctx32k_m8": entry("attn_m8", 8),
         "mlp_m1": entry("mlp_m1", 1),
         "mlp_m8": entry("mlp_m8", 8),
-        "roofline": {"kernel": "gemv_dot (NVFP4 gate|up 34816x5120, silu_mul, M=1)", "bound": "hbm",
+        "roofline": {"kernel": "gemv_row (NVFP4 gate|up 34816x5120, silu_mul, M=1)", "bound": "hbm",
                      "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes": k_bytes, "avg_launch_us": round(k_ms * 1e3, 3)},

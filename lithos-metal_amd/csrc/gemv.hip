@@ -226,9 +226,12 @@ __global__ __launch_bounds__(KW == 16 ? 640 : 1024) void gemv_row(Args a) {
   if (cnt > MT) cnt = MT;
   const long long xr0 = pairs ? (a.x_per_slot ? pairs[0] : pairs[0] / a.top_k) : 0;
   const long long xr1 = MT > 1 ? (pairs ? (a.x_per_slot ? pairs[cnt - 1] : pairs[cnt - 1] / a.top_k) : cnt - 1) : 0;
-  const int c0 = wave * KW;
-  const int kw = min(KW, a.chunks - c0);
-  const int cols = kw * KC;
+  const int split = blockIdx.z;                  // K split (a.ks of a.kc chunks each; FP32 partials when > 1)
+  const int c0_raw = split * a.kc + wave * KW;
+  const int kw = min(KW, min(a.chunks, (split + 1) * a.kc) - c0_raw);   // <= 0: a wave past a short last split
+  const int c0 = kw > 0 ? c0_raw : 0;           // such a wave reads chunk 0 (in bounds) and adds nothing
+  const int kwl = max(kw, 1);
+  const int cols = kwl * KC;
   const uint8_t* tbase = a.w + (long long)expert * a.expert_stride + (long long)tile * a.tile_stride;
 
   // ---- loads: activations, norm weights, scale pieces, then every weight chunk of the slice --------------------
@@ -263,7 +266,7 @@ __global__ __launch_bounds__(KW == 16 ? 640 : 1024) void gemv_row(Args a) {
   }
   Units<FMT> u[KW];
 #pragma unroll
-  for (int cc = 0; cc < KW; ++cc) load_chunk<FMT, false>(u[cc], tbase, c0 + min(cc, kw - 1), a.chunks, lane);
+  for (int cc = 0; cc < KW; ++cc) load_chunk<FMT, false>(u[cc], tbase, c0 + min(cc, kwl - 1), a.chunks, lane);
 
   // ---- stage the slice (normalized when the norm is fused: Σh² over the row from every wave's slice) ----------
   uint8_t* wl = smem + (size_t)wave * a.row_wave_lds;
@@ -451,6 +454,15 @@ __global__ __launch_bounds__(KW == 16 ? 640 : 1024) void gemv_row(Args a) {
   __syncthreads();
   if (wave != 0) return;
   const int row = tile * 16 + m_row;
+  if (a.ks > 1) {                               // this split's partial; gemv_tk_reduce adds the splits in order
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      float v = red[t * 16 + m_row];
+      for (int w = 1; w < S; ++w) v += red[(w * MT + t) * 16 + m_row];
+      if (g == 0 && t < cnt) a.part[((long long)split * a.m + t) * a.n_tiles * 16 + row] = v;
+    }
+    return;
+  }
   const float rs = a.row_scale != nullptr ? a.row_scale[(long long)expert * a.n_tiles * 16 + row] : 1.0f;
 #pragma unroll
   for (int t = 0; t < MT; ++t) {
@@ -957,24 +969,43 @@ int check_desc(const mi_gemv_desc* d) {
 
 constexpr size_t kMaxLds = 160 * 1024;
 
-// gemv_row for M <= 2: KW = 4 while K fits 16 slices of 4 chunks, else 8, else 16 (more, shorter waves keep more
-// loads in flight); gemv_tk otherwise
-Plan plan_row(const mi_gemv_desc* d, int fmt, int chunks, int rows) {
-  Plan p{};
-  int kw = chunks <= 64 ? 4 : chunks <= 128 ? 8 : chunks <= 160 ? 16 : 0;
-  if (const char* env = getenv("MI_GEMV_ROW")) kw = atoi(env);      // tuning sweeps
-  if (fmt == FMT_NVFP4 && kw < 8 && kw != 4) kw = 4;
-  if (kw <= 0) return p;
-  const int S = (chunks + kw - 1) / kw;
-  if (S > (kw == 16 ? 10 : 16)) return p;
-  const int kc = chunk_cols(fmt);
-  const int ld = kw * kc + 8;
-  size_t wl = (size_t)rows * ld * 2 + (fmt == FMT_INT4 ? (size_t)rows * kw * 8 * 4 : 0);
-  wl = (wl + 15) / 16 * 16;
-  const size_t lds = (size_t)S * wl + (size_t)S * 2 * 4 + (size_t)S * rows * 16 * 4;
-  if (lds > kMaxLds) return p;
-  p.kernel = 1; p.S = S; p.kw = kw; p.lds_rows = rows; p.row_ld = ld; p.row_wave_lds = (int)wl; p.lds_bytes = lds;
-  return p;
+// gemv_row for M <= 2: KW = 4 while a split's K fits 16 slices of 4 chunks, else 8, else 16 (more, shorter waves keep
+// more loads in flight). One K split, except long K over few tiles (N = 5120, K = 17408: 320 workgroups leave a
+// quarter of the CUs a second round) where three splits with FP32 partials measured ~10 % faster; a fused norm or
+// a grouped (MoE) launch always takes one split.
+Plan plan_row(const mi_gemv_desc* d, int fmt, int chunks, int rows, int n_tiles, int groups) {
+  Plan best{};
+  double best_cost = 1e30;
+  int force_ks = 0, force_kw = 0;
+  if (const char* env = getenv("MI_GEMV_ROW")) sscanf(env, "%d,%d", &force_kw, &force_ks);   // tuning sweeps
+  for (int ks : {1, 3, 2, 4}) {
+    if (force_ks && ks != force_ks) continue;
+    if (ks > 1 && (d->norm_w || d->groups)) break;
+    int kc = (chunks + ks - 1) / ks;
+    if (fmt == FMT_NVFP4 && ks > 1) kc = (kc + 7) / 8 * 8;      // splits on scale-group boundaries
+    if (ks > 1 && (ks - 1) * kc >= chunks) continue;
+    int kw = kc <= 64 ? 4 : kc <= 128 ? 8 : kc <= 160 ? 16 : 0;
+    if (force_kw) kw = force_kw;
+    if (fmt == FMT_NVFP4 && ks > 1 && kw == 4 && kc % 4) continue;
+    if (kw <= 0) continue;
+    const int S = (kc + kw - 1) / kw;
+    if (S > (kw == 16 ? 10 : 16)) continue;
+    const int kcols = chunk_cols(fmt);
+    const int ld = kw * kcols + 8;
+    size_t wl = (size_t)rows * ld * 2 + (fmt == FMT_INT4 ? (size_t)rows * kw * 8 * 4 : 0);
+    wl = (wl + 15) / 16 * 16;
+    const size_t lds = (size_t)S * wl + (size_t)S * 2 * 4 + (size_t)S * rows * 16 * 4;
+    if (lds > kMaxLds) continue;
+    const int want_ks = (chunks >= 96 && n_tiles * groups <= 512 && !d->norm_w && !d->groups) ? 3 : 1;
+    const double cost = force_ks ? 0.0 : std::abs(ks - want_ks);
+    if (cost < best_cost) {
+      best_cost = cost;
+      best = Plan{};
+      best.kernel = 1; best.S = S; best.kw = kw; best.ks = ks; best.tb = kc; best.lds_rows = rows; best.row_ld = ld;
+      best.row_wave_lds = (int)wl; best.lds_bytes = lds;
+    }
+  }
+  return best;
 }
 
 int tk_lds(int fmt, int rows, int kc, bool mf) {
@@ -1048,7 +1079,7 @@ Plan make_plan(const mi_gemv_desc* d) {
   const int rows = d->groups ? std::min(16, d->m) : d->m;   // a group holds at most one pair per token
   const char* fk = getenv("MI_GEMV_KERNEL");                 // "row" / "tk" pins the kernel (tuning sweeps)
   if (rows <= 2 && !(fk && fk[0] == 't')) {
-    const Plan p = plan_row(d, fmt, chunks, rows);
+    const Plan p = plan_row(d, fmt, chunks, rows, n_tiles, groups);
     if (p.kernel) return p;
   }
   return plan_tk(d, fmt, chunks, n_tiles, groups, rows);
@@ -1084,9 +1115,14 @@ void launch_row_k(const Args& a, const Plan& p, dim3 g, hipStream_t s) {
 template <int FMT>
 void launch(const Args& a, const Plan& p, int groups, hipStream_t s) {
   if (p.kernel == 1) {
-    const dim3 g(a.n_tiles, groups);
+    const dim3 g(a.n_tiles, groups, p.ks);
     if (p.lds_rows == 2) launch_row_k<FMT, 2>(a, p, g, s);
     else launch_row_k<FMT, 1>(a, p, g, s);
+    if (p.ks > 1) {
+      const bool silu = a.epilogue == MI_EPI_SILU_MUL || a.epilogue == MI_EPI_SILU_MUL_ROUNDED;
+      const int n_out = silu ? a.n / 2 : a.n;
+      hipLaunchKernelGGL(gemv_tk_reduce, dim3((n_out + 255) / 256, a.m), dim3(256), 0, s, a);
+    }
     return;
   }
   const dim3 g((a.n_tiles + p.tb - 1) / p.tb, p.ks, groups);
@@ -1136,7 +1172,7 @@ size_t mi_pack_bytes(int32_t format, int32_t n, int32_t k) {
 size_t mi_gemv_workspace_bytes(const mi_gemv_desc* d) {
   if (check_desc(d) != MI_OK) return 0;
   const Plan p = make_plan(d);
-  return p.kernel == 2 && p.ks > 1 ? (size_t)p.ks * d->m * ((d->n + 15) / 16) * 16 * sizeof(float) : 0;
+  return p.ks > 1 ? (size_t)p.ks * d->m * ((d->n + 15) / 16) * 16 * sizeof(float) : 0;
 }
 
 int mi_gemv_plan(const mi_gemv_desc* d, int32_t out[7]) {
@@ -1147,8 +1183,8 @@ int mi_gemv_plan(const mi_gemv_desc* d, int32_t out[7]) {
   const int n_tiles = (d->n + 15) / 16;
   const int groups = d->groups ? d->max_groups : 1;
   out[0] = p.kernel; out[1] = p.S; out[2] = p.kw;
-  out[3] = p.kernel == 1 ? 1 : p.tb; out[4] = p.kernel == 1 ? 1 : p.ks; out[5] = (int32_t)p.lds_bytes;
-  out[6] = (p.kernel == 1 ? n_tiles : (n_tiles + p.tb - 1) / p.tb * p.ks) * groups;
+  out[3] = p.kernel == 1 ? 1 : p.tb; out[4] = p.ks; out[5] = (int32_t)p.lds_bytes;
+  out[6] = (p.kernel == 1 ? n_tiles * p.ks : (n_tiles + p.tb - 1) / p.tb * p.ks) * groups;
   return MI_OK;
 }
 
@@ -1178,10 +1214,10 @@ int mi_gemv(const mi_gemv_desc* d, void* stream) {
   a.lds_rows = p.lds_rows;
   a.tb = p.tb;
   a.ks = p.ks;
-  a.kc = p.kw;
+  a.kc = p.kernel == 1 ? p.tb : p.kw;     // chunks per K split
   a.row_ld = p.row_ld;
   a.row_wave_lds = p.row_wave_lds;
-  if (p.kernel == 2 && p.ks > 1) {
+  if (p.ks > 1) {
     const size_t need = (size_t)p.ks * d->m * ((d->n + 15) / 16) * 16 * sizeof(float);
     void* ws = d->workspace;
     if (ws) {

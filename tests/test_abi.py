@@ -62,12 +62,12 @@ def test_gemv_plans_fit_the_hardware(n, k, m):
     assert kernel == (1 if m <= 2 else 2)                  # gemv_row (VALU) for M <= 2, gemv_tk (MFMA) above
     assert 1 <= waves <= 16 and kw >= 1 and lds <= 160 * 1024 and wgs >= 1 and ks >= 1 and tb >= 1
     chunks = k // 128
-    if kernel == 1:
-        assert kw in (4, 8, 16) and waves * kw >= chunks and (waves - 1) * kw < chunks
+    if kernel == 1:                                      # K splits of ≤ waves·kw chunks each
+        assert kw in (4, 8, 16) and waves * kw * ks >= chunks
     else:
         assert ks * kw >= chunks and (ks - 1) * kw < chunks
     ws = hip.load().mi_gemv_workspace_bytes(C.byref(_desc(hip, n=n, k=k, m=m, ldx=k, ldy=n)))
-    assert (ws > 0) == (kernel == 2 and ks > 1)
+    assert (ws > 0) == (ks > 1)
 
 
 def test_gemv_rejects_bad_descriptors_before_launch():
