@@ -108,8 +108,9 @@ typedef struct mi_gemv_desc {
 } mi_gemv_desc;
 size_t mi_gemv_workspace_bytes(const mi_gemv_desc* d);   /* 0 when the plan needs none */
 int mi_gemv(const mi_gemv_desc* d, void* stream);
-/* the launch plan mi_gemv would use (host only, no device call): tiles per wave, waves per workgroup (K slices),
- * chunks per wave, chunks per staged window, windows (-1: the VALU kernel for M <= 2), LDS bytes, workgroups */
+/* the launch plan mi_gemv would use (host only, no device call): out = [kernel (1: gemv_row, the M <= 2 kernel with
+ * one tile per workgroup; 2: gemv_tk, the tile-streaming kernel), waves per workgroup, chunks per wave (row) or
+ * chunks per K split (tk), tiles per workgroup (tk) or 1, K splits, LDS bytes, workgroups] */
 int mi_gemv_plan(const mi_gemv_desc* d, int32_t out[7]);
 
 /* exact dequantization of a T16 pack to FP32 [n, k] through the kernels' own decode (the bit-exact check of
