@@ -15,6 +15,9 @@
 //    of-two part of the E4M3 block scale, exact), v_dot2_f32_bf16 against the BF16 activations as they are, the
 //    scale's 3-bit mantissa applied once per block of 16; INT4 as BF16 128 + c corrected by 128·Σx per segment. The
 //    K slices meet in LDS (fixed order). Many short waves keep ~all weight bytes of the CU's share in flight.
+//    gemv_rowp is the same wave layout looping over several tiles per workgroup, for a fused input norm over many
+//    tiles: the norm's statistic (a workgroup barrier on the critical path of every workgroup) is then paid once
+//    per workgroup instead of once per tile.
 //  * gemv_tk (M ≤ 16): MFMA v_mfma_f32_16x16x32_{f16,bf16} with the activations as the A operand (token rows,
 //    power-of-two prescaled into F16 range: exact above 2^-14 of the row max) and the decoded weights as B (NVFP4 →
 //    exact F16 by v_cvt_scalef32_pk_f16_fp4 and a packed multiply by the mantissa factor). A workgroup stages one K
@@ -29,7 +32,9 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <mutex>
+#include <tuple>
 #include <vector>
 
 namespace {
@@ -471,6 +476,321 @@ __global__ __launch_bounds__(KW == 16 ? 640 : 1024) void gemv_row(Args a) {
     v *= rs;
     const float up = __shfl_down(v, 8, 16);
     if (g == 0) emit(a, pairs, cnt, tile, true, m_row, t, v, up);
+  }
+}
+
+// ---- gemv_rowp: M = 1, a workgroup over several tiles ------------------------------------------------------------------------------------------
+// Workgroup = S waves over tiles blockIdx.x, blockIdx.x + G, … (G = gridDim.x, at most a.rt tiles; G is sized so
+// every workgroup is resident at once) of one group (blockIdx.y, MoE) and one K split (blockIdx.z); wave w owns the
+// K slice [w·KW, w·KW + KW) of every one of those tiles. The activations (normalized when the norm is fused) are
+// staged once per workgroup; each wave keeps two tiles' weight chunks in flight, issuing tile j + 2 as soon as
+// tile j is consumed, so the stream never waits on the arithmetic. A tile's K slices meet in LDS in wave order
+// after the last tile.
+// LDS: per wave xs[MT][row_ld] (INT4: then seg[MT][KW][8]) | stat[S][2] | red[rt][S][MT][16].
+template <int FMT, int MT, int KW>
+__global__ __launch_bounds__(KW == 16 ? 640 : 1024) __attribute__((amdgpu_waves_per_eu(KW == 4 && MT == 1 ? 8 : 1)))
+void gemv_rowp(Args a) {
+  constexpr int KC = chunk_cols(FMT);
+  constexpr int NPL = MT * KW * KC / 8 / 64 > 0 ? MT * KW * KC / 8 / 64 : 1;   // activation vectors per lane
+  constexpr int NG = FMT == FMT_NVFP4 ? (KW + 7) / 8 : 1;                         // scale pieces per wave and tile
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int S = blockDim.x >> 6;
+  const int G = gridDim.x;
+  const int ntl = (a.n_tiles - 1 - (int)blockIdx.x) / G + 1;   // this workgroup's tiles (gridDim.x <= n_tiles)
+  int expert = 0, cnt = a.m;
+  const int32_t* pairs = nullptr;
+  if (a.groups) {
+    const int32_t* g = a.groups + blockIdx.y * GROUP_REC;
+    expert = g[0];
+    cnt = g[1];
+    pairs = g + 2;
+    if (cnt <= 0 || expert < 0) return;       // the whole workgroup leaves together
+  }
+  if (cnt > MT) cnt = MT;
+  const long long xr0 = pairs ? (a.x_per_slot ? pairs[0] : pairs[0] / a.top_k) : 0;
+  const long long xr1 = MT > 1 ? (pairs ? (a.x_per_slot ? pairs[cnt - 1] : pairs[cnt - 1] / a.top_k) : cnt - 1) : 0;
+  const int split = blockIdx.z;                  // K split (a.ks of a.kc chunks each; FP32 partials when > 1)
+  const int c0_raw = split * a.kc + wave * KW;
+  const int kw = min(KW, min(a.chunks, (split + 1) * a.kc) - c0_raw);   // <= 0: a wave past a short last split
+  const int c0 = kw > 0 ? c0_raw : 0;           // such a wave reads chunk 0 (in bounds) and adds nothing
+  const int kwl = max(kw, 1);
+  const int cols = kwl * KC;
+  const uint8_t* wmat = a.w + (long long)expert * a.expert_stride;
+  auto tile_of = [&](int j) { return (int)blockIdx.x + j * G; };
+
+  // ---- loads: activations, norm weights, then the first two tiles' scale pieces and weight chunks -------------
+  const int per_row = cols / 8;
+  uint4 xv[NPL];
+  float4 nv[NPL][2];
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const int idx = min(lane + 64 * i, MT * per_row - 1);
+    const int j = MT > 1 && idx >= per_row ? 1 : 0;
+    const int e = (idx - j * per_row) * 8;
+    xv[i] = *reinterpret_cast<const uint4*>(a.x + (j ? xr1 : xr0) * a.ldx + c0 * KC + e);
+    if (a.norm_w) {
+      nv[i][0] = *reinterpret_cast<const float4*>(a.norm_w + c0 * KC + e);
+      nv[i][1] = *reinterpret_cast<const float4*>(a.norm_w + c0 * KC + e + 4);
+    }
+  }
+  // chunk cc of the slice at a compile-time offset from chunk c0 (NVFP4: KW = 4 slices lie in one group of 8,
+  // longer ones start on a group); chunks past a short slice are not loaded (their arithmetic is skipped)
+  const long long c0_off = FMT == FMT_NVFP4 ? nv_code_off(c0) : (long long)c0 * unit_bytes(FMT);
+  auto issue = [&](Units<FMT> (&u)[KW], uint4 (&sv)[NG], int j) {
+    const uint8_t* tbase = wmat + (long long)tile_of(j) * a.tile_stride;
+    if constexpr (FMT == FMT_NVFP4) {
+#pragma unroll
+      for (int q = 0; q < NG; ++q) {
+        const int gi = min((c0 >> 3) + q, (a.chunks - 1) >> 3);
+        const int gsz = nv_group_chunks(gi, a.chunks);
+        const uint8_t* p = tbase + nv_scale_off(gi, a.chunks);
+        if (nv_piece(gsz) == 16) {
+          sv[q] = *reinterpret_cast<const uint4*>(p + 16 * lane);
+        } else {
+          const uint2 t = *reinterpret_cast<const uint2*>(p + 8 * lane);
+          sv[q] = uint4{t.x, t.y, 0u, 0u};
+        }
+      }
+    }
+    const uint8_t* cb = tbase + c0_off;
+    auto one = [&](int cc) {
+      if constexpr (FMT == FMT_NVFP4) {
+        const int off = KW <= 4 ? cc * 1024 : (cc >> 3) * 9216 + (cc & 7) * 1024;
+        u[cc].q = *reinterpret_cast<const uint4*>(cb + off + 16 * lane);
+      } else {
+        const uint8_t* p = cb + cc * unit_bytes(FMT);
+        u[cc].q = *reinterpret_cast<const uint4*>(p + 16 * lane);
+        if constexpr (FMT == FMT_INT4) u[cc].sb = *reinterpret_cast<const uint2*>(p + 1024 + 8 * (lane & 15));
+      }
+    };
+    if (kwl == KW) {                          // the common case: straight-line loads
+#pragma unroll
+      for (int cc = 0; cc < KW; ++cc) one(cc);
+    } else {
+#pragma unroll
+      for (int cc = 0; cc < KW; ++cc)
+        if (cc < kwl) one(cc);
+    }
+  };
+  Units<FMT> u0[KW];
+  uint4 s0[NG];
+  issue(u0, s0, 0);
+
+  // ---- stage the slice (normalized when the norm is fused: Σh² over the row from every wave's slice) ----------
+  uint8_t* wl = smem + (size_t)wave * a.row_wave_lds;
+  uint16_t* xs = reinterpret_cast<uint16_t*>(wl);
+  const int ld = a.row_ld;
+  float* seg = reinterpret_cast<float*>(wl + (size_t)MT * ld * 2);
+  float* stat = reinterpret_cast<float*>(smem + (size_t)S * a.row_wave_lds);   // [S][2]
+  float* red = stat + 2 * S;                                                  // [rt][S][MT][16]
+  if (a.norm_w) {
+    float sq[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      const int idx = lane + 64 * i;
+      if (idx < MT * per_row) {
+        const uint32_t vv[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+        float t = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float lo = bf16_bits_to_f32(vv[q] & 0xFFFFu), hi = bf16_bits_to_f32(vv[q] >> 16);
+          t = fmaf(lo, lo, fmaf(hi, hi, t));
+        }
+        sq[MT > 1 && idx >= per_row ? 1 : 0] += t;
+      }
+    }
+    sq[0] = wave_sum(sq[0]);
+    if (MT > 1) sq[1] = wave_sum(sq[1]);
+    if (lane == 0) { stat[2 * wave] = sq[0]; stat[2 * wave + 1] = sq[1]; }
+    __syncthreads();
+    float rstd[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      float t = 0.0f;
+      for (int w = 0; w < S; ++w) t += stat[2 * w + j];
+      rstd[j] = 1.0f / sqrtf(t / (float)a.k + a.eps);
+    }
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      const int idx = lane + 64 * i;
+      const float rr = rstd[MT > 1 && idx >= per_row ? 1 : 0];
+      const float wv[8] = {nv[i][0].x, nv[i][0].y, nv[i][0].z, nv[i][0].w, nv[i][1].x, nv[i][1].y, nv[i][1].z, nv[i][1].w};
+      uint32_t* vv = reinterpret_cast<uint32_t*>(&xv[i]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float lo = round_bf16((bf16_bits_to_f32(vv[q] & 0xFFFFu) * rr) * wv[2 * q]);
+        const float hi = round_bf16((bf16_bits_to_f32(vv[q] >> 16) * rr) * wv[2 * q + 1]);
+        vv[q] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const int idx = lane + 64 * i;
+    if (idx < MT * per_row) {
+      const int j = MT > 1 && idx >= per_row ? 1 : 0;
+      uint4 v = xv[i];
+      if constexpr (FMT == FMT_INT4) {        // (x0,x1)(x2,x3)(x4,x5)(x6,x7) → (x0,x4)(x1,x5)(x2,x6)(x3,x7)
+        const uint32_t a0 = v.x, a1 = v.y, a2 = v.z, a3 = v.w;
+        v.x = __builtin_amdgcn_perm(a2, a0, 0x05040100u);
+        v.y = __builtin_amdgcn_perm(a2, a0, 0x07060302u);
+        v.z = __builtin_amdgcn_perm(a3, a1, 0x05040100u);
+        v.w = __builtin_amdgcn_perm(a3, a1, 0x07060302u);
+      }
+      *reinterpret_cast<uint4*>(xs + (size_t)j * ld + (idx - j * per_row) * 8) = v;
+    }
+  }
+  wave_lds_sync();
+  if constexpr (FMT == FMT_INT4) {
+    // Σx over each (chunk, g, group) segment of 16 columns: steps {0,1} (group A) / {2,3} (group B) of k-group g
+    for (int idx = lane; idx < MT * KW * 8; idx += 64) {
+      const int j = idx / (KW * 8), rem = idx - j * KW * 8;
+      const int cc = rem >> 3, g = (rem >> 1) & 3, gp = rem & 1;
+      float sx = 0.0f;
+      if (cc < kw) {
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+          const uint4 v = *reinterpret_cast<const uint4*>(xs + (size_t)j * ld + cc * 128 + 32 * (2 * gp + st) + 8 * g);
+          const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) sx += bf16_bits_to_f32(vv[q] & 0xFFFFu) + bf16_bits_to_f32(vv[q] >> 16);
+        }
+      }
+      seg[idx] = sx;
+    }
+    wave_lds_sync();
+  }
+
+  // ---- the slice's dot products, tile by tile --------------------------------------------------------------------
+  const int g = lane >> 4, m_row = lane & 15;
+  auto tile_dot = [&](const Units<FMT> (&uu)[KW], const uint4 (&ss)[NG], int jt) {
+    float acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
+    auto slice_chunk = [&](int cc) {
+      const uint32_t dw[4] = {uu[cc].q.x, uu[cc].q.y, uu[cc].q.z, uu[cc].q.w};
+      if constexpr (FMT == FMT_NVFP4) {
+        uint4 xq[MT][4];
+  #pragma unroll
+        for (int t = 0; t < MT; ++t)
+  #pragma unroll
+          for (int s = 0; s < 4; ++s) xq[t][s] = *reinterpret_cast<const uint4*>(xs + (size_t)t * ld + cc * 128 + 32 * g + 8 * s);
+        const int ci = ((c0 + cc) & 7);                // chunk in its group; KW >= 8 slices start on a group
+        const uint4 pv = ss[KW >= 8 ? cc >> 3 : 0];
+        const uint32_t word = KW >= 8 ? (cc & 6) == 0 ? pv.x : (cc & 6) == 2 ? pv.y : (cc & 6) == 4 ? pv.z : pv.w
+                                      : (ci >> 1) == 0 ? pv.x : (ci >> 1) == 1 ? pv.y : (ci >> 1) == 2 ? pv.z : pv.w;
+        const uint32_t two = (KW >= 8 ? (cc & 1) : (ci & 1)) ? word >> 16 : word & 0xFFFFu;
+        const f32x2 f = __builtin_amdgcn_cvt_pk_f32_fp8((int)two, false);
+        const uint32_t u0 = __float_as_uint(f.x), u1 = __float_as_uint(f.y);
+        const float e[2] = {__uint_as_float(u0 & 0x7F800000u), __uint_as_float(u1 & 0x7F800000u)};
+        const float mant[2] = {__uint_as_float((u0 & 0x807FFFFFu) | 0x3F800000u),
+                               __uint_as_float((u1 & 0x807FFFFFu) | 0x3F800000u)};
+  #pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          float part[MT];
+  #pragma unroll
+          for (int t = 0; t < MT; ++t) part[t] = 0.0f;
+  #pragma unroll
+          for (int s = 2 * b; s < 2 * b + 2; ++s)
+  #pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const bf16x2 w2 = cvt_fp4x2_bf16(dw[s], e[b], j);
+  #pragma unroll
+              for (int t = 0; t < MT; ++t) {
+                const uint32_t xw = j == 0 ? xq[t][s].x : j == 1 ? xq[t][s].y : j == 2 ? xq[t][s].z : xq[t][s].w;
+                part[t] = __builtin_amdgcn_fdot2_f32_bf16(w2, __builtin_bit_cast(bf16x2, xw), part[t], false);
+              }
+            }
+  #pragma unroll
+          for (int t = 0; t < MT; ++t) acc[t] = fmaf(part[t], mant[b], acc[t]);
+        }
+      } else if constexpr (FMT == FMT_INT4) {
+        uint4 xq[MT][4];
+        float sa[MT], sb[MT];
+  #pragma unroll
+        for (int t = 0; t < MT; ++t) {
+  #pragma unroll
+          for (int s = 0; s < 4; ++s) xq[t][s] = *reinterpret_cast<const uint4*>(xs + (size_t)t * ld + cc * 128 + 32 * s + 8 * g);
+          sa[t] = seg[(t * KW + cc) * 8 + g * 2];
+          sb[t] = seg[(t * KW + cc) * 8 + g * 2 + 1];
+        }
+        float d[2][MT];
+  #pragma unroll
+        for (int t = 0; t < MT; ++t) d[0][t] = d[1][t] = 0.0f;
+  #pragma unroll
+        for (int s = 0; s < 4; ++s)
+  #pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const uint32_t w2 = ((dw[s] >> (4 * j)) & 0x000F000Fu) | 0x43004300u;   // BF16 (128 + n_j, 128 + n_j+4)
+  #pragma unroll
+            for (int t = 0; t < MT; ++t) {
+              const uint32_t xw = j == 0 ? xq[t][s].x : j == 1 ? xq[t][s].y : j == 2 ? xq[t][s].z : xq[t][s].w;
+              d[s >> 1][t] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w2), __builtin_bit_cast(bf16x2, xw),
+                                                             d[s >> 1][t], false);
+            }
+          }
+        const float sca = bf16_bits_to_f32(uu[cc].sb.x & 0xFFFFu), bia = bf16_bits_to_f32(uu[cc].sb.x >> 16);
+        const float scb = bf16_bits_to_f32(uu[cc].sb.y & 0xFFFFu), bib = bf16_bits_to_f32(uu[cc].sb.y >> 16);
+  #pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          acc[t] = fmaf(sca, fmaf(-128.0f, sa[t], d[0][t]), fmaf(bia, sa[t], acc[t]));
+          acc[t] = fmaf(scb, fmaf(-128.0f, sb[t], d[1][t]), fmaf(bib, sb[t], acc[t]));
+        }
+      } else {
+        uint4 xq[MT];
+  #pragma unroll
+        for (int t = 0; t < MT; ++t) xq[t] = *reinterpret_cast<const uint4*>(xs + (size_t)t * ld + cc * 32 + 8 * g);
+  #pragma unroll
+        for (int j = 0; j < 4; ++j)
+  #pragma unroll
+          for (int t = 0; t < MT; ++t) {
+            const uint32_t xw = j == 0 ? xq[t].x : j == 1 ? xq[t].y : j == 2 ? xq[t].z : xq[t].w;
+            acc[t] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, dw[j]), __builtin_bit_cast(bf16x2, xw),
+                                                     acc[t], false);
+          }
+      }
+    };
+    if (kw == KW) {
+#pragma unroll
+      for (int cc = 0; cc < KW; ++cc) slice_chunk(cc);
+    } else {
+#pragma unroll
+      for (int cc = 0; cc < KW; ++cc)
+        if (cc < kw) slice_chunk(cc);
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const float v = quad16_sum(acc[t]);
+      if (g == 0) red[((jt * S + wave) * MT + t) * 16 + m_row] = v;
+    }
+  };
+  for (int j = 0; j < ntl; ++j) {
+    tile_dot(u0, s0, j);
+    if (j + 1 < ntl) issue(u0, s0, j + 1);
+  }
+
+  // ---- per tile: the K slices in wave order, then the epilogue (16-lane groups hold one tile's rows) -----------
+  __syncthreads();
+  if (wave != 0) return;
+  const int total = ntl * MT * 16;
+  for (int base = 0; base < total; base += 64) {
+    const int idx = base + threadIdx.x;
+    const bool ok = idx < total;
+    const int q = ok ? idx >> 4 : 0, r = idx & 15;
+    const int jt = q / MT, t = q - jt * MT;
+    float v = red[(jt * S * MT + t) * 16 + r];
+    for (int w = 1; w < S; ++w) v += red[((jt * S + w) * MT + t) * 16 + r];
+    const int tile = tile_of(jt);
+    const int row = tile * 16 + r;
+    if (a.ks > 1) {                             // this split's partial; gemv_tk_reduce adds the splits in order
+      if (ok && t < cnt) a.part[((long long)split * a.m + t) * a.n_tiles * 16 + row] = v;
+      continue;
+    }
+    v *= a.row_scale != nullptr ? a.row_scale[(long long)expert * a.n_tiles * 16 + row] : 1.0f;
+    const float up = __shfl_down(v, 8, 16);
+    if (ok) emit(a, pairs, cnt, tile, true, r, t, v, up);
   }
 }
 
@@ -942,6 +1262,7 @@ struct Plan {
   int S = 1;               // waves per workgroup
   int kw = 0;              // gemv_row: KW (chunks per wave); gemv_tk: chunks per split
   int tb = 1, ks = 1, depth = 8;   // gemv_tk: tiles per workgroup, K splits, ring depth
+  int rt = 1, G = 0;       // gemv_row: tiles per workgroup (at most), workgroups along the tiles
   int lds_rows = 1, row_ld = 0, row_wave_lds = 0;
   size_t lds_bytes = 0;
 };
@@ -969,6 +1290,55 @@ int check_desc(const mi_gemv_desc* d) {
 
 constexpr size_t kMaxLds = 160 * 1024;
 
+template <int FMT, int MT, int KW> __global__ void gemv_rowp(Args a);
+
+// compute units of the current device (256 on MI355X; also the answer where no device is visible)
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 && cached[dev] > 0) return cached[dev];
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
+      hipSuccess || n <= 0) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  if (dev >= 0 && dev < 64) cached[dev] = n;
+  return n;
+}
+
+// resident gemv_rowp workgroups per CU for this instantiation, block size and LDS (the occupancy calculator; without
+// a device, the wave-slot bound of 32 waves per CU)
+int row_blocks_query(int fmt, int kw, int threads, size_t lds) {
+  const void* k = nullptr;
+#define MI_ROW_K(F, W) if (fmt == F && kw == W) k = reinterpret_cast<const void*>(gemv_rowp<F, 1, W>);
+  MI_ROW_K(FMT_NVFP4, 4) MI_ROW_K(FMT_NVFP4, 8) MI_ROW_K(FMT_NVFP4, 16)
+  MI_ROW_K(FMT_INT4, 4) MI_ROW_K(FMT_INT4, 8) MI_ROW_K(FMT_INT4, 16)
+  MI_ROW_K(FMT_BF16, 4) MI_ROW_K(FMT_BF16, 8) MI_ROW_K(FMT_BF16, 16)
+#undef MI_ROW_K
+  int n = 0;
+  if (k && hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, threads, lds) == hipSuccess && n > 0) return n;
+  (void)hipGetLastError();
+  return std::max(1, 32 / (threads / 64));
+}
+
+int row_blocks_per_cu(int fmt, int kw, int threads, size_t lds) {
+  static std::mutex mu;
+  static std::map<std::tuple<int, int, int, size_t, int>, int> cache;
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  (void)hipGetLastError();
+  const auto key = std::make_tuple(fmt, kw, threads, lds, dev);
+  {
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+  }
+  const int n = row_blocks_query(fmt, kw, threads, lds);
+  std::lock_guard<std::mutex> lk(mu);
+  cache[key] = n;
+  return n;
+}
+
 // gemv_row for M <= 2: KW = 4 while a split's K fits 16 slices of 4 chunks, else 8, else 16 (more, shorter waves keep
 // more loads in flight). One K split, except long K over few tiles (N = 5120, K = 17408: 320 workgroups leave a
 // quarter of the CUs a second round) where three splits with FP32 partials measured ~10 % faster; a fused norm or
@@ -976,8 +1346,9 @@ constexpr size_t kMaxLds = 160 * 1024;
 Plan plan_row(const mi_gemv_desc* d, int fmt, int chunks, int rows, int n_tiles, int groups) {
   Plan best{};
   double best_cost = 1e30;
-  int force_ks = 0, force_kw = 0;
-  if (const char* env = getenv("MI_GEMV_ROW")) sscanf(env, "%d,%d", &force_kw, &force_ks);   // tuning sweeps
+  int force_ks = 0, force_kw = 0, force_rt = 0;
+  if (const char* env = getenv("MI_GEMV_ROW"))                                   // tuning sweeps
+    sscanf(env, "%d,%d,%d", &force_kw, &force_ks, &force_rt);
   for (int ks : {1, 3, 2, 4}) {
     if (force_ks && ks != force_ks) continue;
     if (ks > 1 && (d->norm_w || d->groups)) break;
@@ -994,8 +1365,20 @@ Plan plan_row(const mi_gemv_desc* d, int fmt, int chunks, int rows, int n_tiles,
     const int ld = kw * kcols + 8;
     size_t wl = (size_t)rows * ld * 2 + (fmt == FMT_INT4 ? (size_t)rows * kw * 8 * 4 : 0);
     wl = (wl + 15) / 16 * 16;
-    const size_t lds = (size_t)S * wl + (size_t)S * 2 * 4 + (size_t)S * rows * 16 * 4;
-    if (lds > kMaxLds) continue;
+    const size_t lds1 = (size_t)S * wl + (size_t)S * 2 * 4;     // + red[rt][S][rows][16]
+    const size_t red1 = (size_t)S * rows * 16 * 4;
+    if (lds1 + red1 > kMaxLds) continue;
+    // gemv_rowp (rt > 1 tiles per workgroup) where the input norm is fused: its statistic then costs once per
+    // workgroup instead of once per tile; rt is what keeps ~every workgroup resident at once
+    int rt = 1;
+    if (rows == 1 && !d->groups && (d->norm_w || force_rt)) {
+      const int per_cu = row_blocks_per_cu(fmt, kw, 64 * S, lds1 + 4 * red1);
+      const long long slots = (long long)cu_count() * std::max(per_cu, 1);
+      rt = (int)std::min<long long>(4, std::max<long long>(1, ((long long)n_tiles * ks + slots - 1) / slots));
+      if (rt < 3) rt = 1;          // measured: at two tiles per workgroup the loop costs what the statistic saves
+      if (force_rt) rt = force_rt;
+    }
+    const size_t lds = lds1 + (size_t)rt * red1;
     const int want_ks = (chunks >= 96 && n_tiles * groups <= 512 && !d->norm_w && !d->groups) ? 3 : 1;
     const double cost = force_ks ? 0.0 : std::abs(ks - want_ks);
     if (cost < best_cost) {
@@ -1003,6 +1386,7 @@ Plan plan_row(const mi_gemv_desc* d, int fmt, int chunks, int rows, int n_tiles,
       best = Plan{};
       best.kernel = 1; best.S = S; best.kw = kw; best.ks = ks; best.tb = kc; best.lds_rows = rows; best.row_ld = ld;
       best.row_wave_lds = (int)wl; best.lds_bytes = lds;
+      best.rt = rt; best.G = rt > 1 ? (n_tiles + rt - 1) / rt : n_tiles;
     }
   }
   return best;
@@ -1105,17 +1489,23 @@ void launch_tk_d(const Args& a, const Plan& p, dim3 g, hipStream_t s) {
   else { allow_lds(gemv_tk<FMT, MT, 12, false>); hipLaunchKernelGGL((gemv_tk<FMT, MT, 12, false>), g, dim3(64 * p.S), p.lds_bytes, s, a); }
 }
 
+template <int FMT, int MT, int KW>
+void launch_row_kw(const Args& a, const Plan& p, dim3 g, hipStream_t s) {
+  if (MT == 1 && p.rt > 1) { allow_lds(gemv_rowp<FMT, 1, KW>); hipLaunchKernelGGL((gemv_rowp<FMT, 1, KW>), g, dim3(64 * p.S), p.lds_bytes, s, a); }
+  else { allow_lds(gemv_row<FMT, MT, KW>); hipLaunchKernelGGL((gemv_row<FMT, MT, KW>), g, dim3(64 * p.S), p.lds_bytes, s, a); }
+}
+
 template <int FMT, int MT>
 void launch_row_k(const Args& a, const Plan& p, dim3 g, hipStream_t s) {
-  if (p.kw == 4) { allow_lds(gemv_row<FMT, MT, 4>); hipLaunchKernelGGL((gemv_row<FMT, MT, 4>), g, dim3(64 * p.S), p.lds_bytes, s, a); }
-  else if (p.kw == 8) { allow_lds(gemv_row<FMT, MT, 8>); hipLaunchKernelGGL((gemv_row<FMT, MT, 8>), g, dim3(64 * p.S), p.lds_bytes, s, a); }
-  else { allow_lds(gemv_row<FMT, MT, 16>); hipLaunchKernelGGL((gemv_row<FMT, MT, 16>), g, dim3(64 * p.S), p.lds_bytes, s, a); }
+  if (p.kw == 4) launch_row_kw<FMT, MT, 4>(a, p, g, s);
+  else if (p.kw == 8) launch_row_kw<FMT, MT, 8>(a, p, g, s);
+  else launch_row_kw<FMT, MT, 16>(a, p, g, s);
 }
 
 template <int FMT>
 void launch(const Args& a, const Plan& p, int groups, hipStream_t s) {
   if (p.kernel == 1) {
-    const dim3 g(a.n_tiles, groups, p.ks);
+    const dim3 g(p.G, groups, p.ks);
     if (p.lds_rows == 2) launch_row_k<FMT, 2>(a, p, g, s);
     else launch_row_k<FMT, 1>(a, p, g, s);
     if (p.ks > 1) {
@@ -1183,8 +1573,8 @@ int mi_gemv_plan(const mi_gemv_desc* d, int32_t out[7]) {
   const int n_tiles = (d->n + 15) / 16;
   const int groups = d->groups ? d->max_groups : 1;
   out[0] = p.kernel; out[1] = p.S; out[2] = p.kw;
-  out[3] = p.kernel == 1 ? 1 : p.tb; out[4] = p.ks; out[5] = (int32_t)p.lds_bytes;
-  out[6] = (p.kernel == 1 ? n_tiles * p.ks : (n_tiles + p.tb - 1) / p.tb * p.ks) * groups;
+  out[3] = p.kernel == 1 ? p.rt : p.tb; out[4] = p.ks; out[5] = (int32_t)p.lds_bytes;
+  out[6] = (p.kernel == 1 ? p.G * p.ks : (n_tiles + p.tb - 1) / p.tb * p.ks) * groups;
   return MI_OK;
 }
 

@@ -173,3 +173,38 @@ def test_gemv_repeat_is_bit_identical(torch_gpu, rng):
     a = kernels.gemv(w, x).clone()
     b = kernels.gemv(w, x)
     assert torch_gpu.equal(a, b)
+
+
+@pytest.mark.parametrize("fmt", ["nvfp4", "int4_affine", "bf16"])
+@pytest.mark.parametrize("n,k", [(1040, 2048), (336, 1664)])
+@pytest.mark.parametrize("epi", [None, "residual", "silu_mul"])
+def test_gemv_tiles_per_workgroup(torch_gpu, fmt, n, k, epi, rng, monkeypatch):
+    """M = 1 with a workgroup streaming 1..5 tiles (the fused-norm plan): every tile's K slices are added in the
+    same order, so the output is bit-identical to one tile per workgroup, and within the oracle bar."""
+    from monolith_mi355 import kernels
+    if epi == "silu_mul":
+        n = n // 16 * 16
+    m = _matrix(fmt, n, k, rng)
+    w = _upload(torch_gpu, m)
+    h = rbf(rng.standard_normal((1, k)) * 3)
+    wn = rbf(rng.standard_normal(k) * 0.2)
+    nw = torch_gpu.from_numpy((1.0 + wn).astype(np.float32)).cuda()
+    res = rbf(rng.standard_normal((1, n)))
+    kw = dict(norm_w=nw, eps=1e-6, epilogue=epi)
+    if epi == "residual":
+        kw["residual"] = to_dev_bf16(torch_gpu, res)
+    outs = {}
+    for rt in (1, 2, 3, 5):
+        monkeypatch.setenv("MI_GEMV_ROW", f"4,1,{rt}")
+        outs[rt] = from_dev_bf16(kernels.gemv(w, to_dev_bf16(torch_gpu, h), **kw))
+    monkeypatch.delenv("MI_GEMV_ROW")
+    for rt in (2, 3, 5):
+        assert np.array_equal(outs[rt].view(np.uint16), outs[1].view(np.uint16)), rt
+    xn = ON.rms_norm(h, wn, 1e-6)
+    wd = _dequant(m)
+    if epi == "silu_mul":
+        ref = ON.linear(xn, wd[np.argsort(ON.interleave_chunks(n // 2, n // 2, 8))], epilogue="silu_mul")
+    else:
+        ref = ON.linear(xn, wd, epilogue=epi, residual=res if epi else None)
+    chk = check_against_oracle(outs[1], ref)
+    assert chk.ok_rounded(), chk
