@@ -105,12 +105,21 @@ typedef struct mi_gemv_desc {
                                 calls overlapping in time need distinct workspaces); NULL = the library's own */
   size_t workspace_bytes;
   int32_t out_f32;           /* 1: y is FP32 (the lm_head / kernel-test output, ops/gemv.py:12), unrounded */
+  /* gated head RMSNorm applied to x while it is staged — the Gated DeltaNet output norm (ops/gdn.py `gdn_norm`,
+   * nn/gdn.py:86-93) fused into the output projection: per 128-column head of each x row,
+   * x' = bf16(bf16(bf16(w)·bf16(x·r))·silu(z)), r = rsqrt(mean over the head of x² + eps). NVFP4 / INT4 only;
+   * exclusive with norm_w. NULL = off. */
+  const float* gnorm_w;      /* [128] BF16-valued weights */
+  const uint16_t* gnorm_z;   /* z [m][ld_gnorm_z] BF16, same rows as x */
+  int32_t ld_gnorm_z;
+  float gnorm_eps;
 } mi_gemv_desc;
 size_t mi_gemv_workspace_bytes(const mi_gemv_desc* d);   /* 0 when the plan needs none */
 int mi_gemv(const mi_gemv_desc* d, void* stream);
-/* the launch plan mi_gemv would use (host only, no device call): out = [kernel (1: gemv_row, the M <= 2 kernel with
- * one tile per workgroup; 2: gemv_tk, the tile-streaming kernel), waves per workgroup, chunks per wave (row) or
- * chunks per K split (tk), tiles per workgroup (tk) or 1, K splits, LDS bytes, workgroups] */
+/* the launch plan mi_gemv would use (host only; the tiles per workgroup of a fused-norm M = 1 plan follow the
+ * current device's occupancy): out = [kernel (1: gemv_row, the M <= 2 kernel whose waves split a tile's K; 2:
+ * gemv_tk, the tile-streaming kernel), waves per workgroup, chunks per wave (row) or chunks per K split (tk),
+ * tiles per workgroup, K splits, LDS bytes, workgroups] */
 int mi_gemv_plan(const mi_gemv_desc* d, int32_t out[7]);
 
 /* exact dequantization of a T16 pack to FP32 [n, k] through the kernels' own decode (the bit-exact check of
@@ -140,6 +149,8 @@ typedef struct mi_gdn_desc {
   uint16_t* y;
   int32_t ld_y;
   float eps;
+  int32_t defer_norm;        /* 1: y gets the BF16 read-out o and the gated RMSNorm is left to the consumer (the
+                                output projection's mi_gemv, gnorm_* fields); 0: y is the normed, gated output */
 } mi_gdn_desc;
 int mi_gdn_step(const mi_gdn_desc* d, void* stream);
 

@@ -3,19 +3,26 @@
 // β = bf16(σ(b)), g = −exp(A_log)·softplus(a + dt_bias), the delta-rule recurrence on the FP32 state
 // S ← S·e^g; Δ = (v − Sᵀk)·β; S += k⊗Δ; o = Sᵀq, then the gated RMSNorm y = bf16(bf16(w·bf16(o·r))·silu(z)).
 //
-// MI355X design: one workgroup per value head, eight wave64s, wave w owning state columns [16w, 16w+16). Lane
-// (c = l%16, rg = l/16) holds S[32·rg .. 32·rg+32][16w + c] in 32 VGPRs for all T tokens; the Σ over dk is 32 FMAs
-// in-lane plus a 4-lane shuffle reduction, so the sequential token loop never touches memory or a barrier. The
-// conv for the head's q/k (its key head) and v channels is computed once per workgroup into LDS. Conv state is
-// read from one buffer and written to another (several value heads read the same key head's channels: the
-// reference solves the same race with two slots by step parity, gdn_mixer.metal:25-37); the recurrent state may be
-// updated in place (each workgroup owns its head).
+// MI355X design: the state columns of a head are independent through the whole step (the Σ over dk stays inside a
+// column), so a workgroup takes one value head's 32-column slice (grid hv × 4: 192 workgroups, enough to spread the
+// 6 MB state stream over the chip), two state waves of 16 columns each plus two waves that compute the conv while
+// the state streams in. Lane (c = l%16, rg = l/16) of a state wave holds
+// S[32·rg .. 32·rg+32][col] in 32 VGPRs for all T tokens; the Σ over dk is 32 FMAs in-lane plus a 4-lane shuffle
+// reduction, so the sequential token loop never touches memory or a barrier. Each workgroup computes the conv,
+// SiLU and L2 norms of its key head's q/k (256 channels, repeated per slice: cheap) and of its own 32 v channels.
+// Conv state is read from one buffer and written to another (several value heads read the same key head's
+// channels: the reference solves the same race with two slots by step parity, gdn_mixer.metal:25-37); the
+// recurrent state may be updated in place (each workgroup owns its slice). The gated RMSNorm needs the head's
+// whole output, so it is a second small kernel (gdn_gated_norm), or — with defer_norm — left to the consumer: the
+// output projection's GEMV applies it while staging its input.
 #include "mi_common.h"
 
 namespace {
 
 constexpr int DK = 128, DV = 128, CW = 4, TMAX = 16;
-constexpr int WAVES = 8, COLS = DV / WAVES;   // 16 columns per wave
+constexpr int WAVES = 2, COLS = 16;            // per workgroup: 2 state waves of 16 columns …
+constexpr int CONV_WAVES = 2;                  // … and 2 waves that compute the conv while the state streams in
+constexpr int SLICE = WAVES * COLS, NSLICE = DV / SLICE;
 
 struct GdnArgs {
   int t, hk, hv;
@@ -38,36 +45,44 @@ __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)
 __device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : log1pf(__expf(x)); }
 __device__ __forceinline__ float bf(const uint16_t* p, long long i) { return bf16_bits_to_f32(p[i]); }
 
-__global__ __launch_bounds__(512) void gdn_step(GdnArgs a) {
+__global__ __launch_bounds__(64 * (WAVES + CONV_WAVES)) void gdn_step(GdnArgs a) {
   __shared__ float qs[TMAX][DK];   // conv → silu → L2-norm (q also /√dk)
   __shared__ float ks[TMAX][DK];
-  __shared__ float vs[TMAX][DV];
-  __shared__ float os[TMAX][DV];   // BF16-valued read-out
-  __shared__ float beta_s[TMAX], eg_s[TMAX], rstd_s[TMAX];
-  const int h = blockIdx.x;
+  __shared__ float vs[TMAX][SLICE];
+  __shared__ float beta_s[TMAX], eg_s[TMAX];
+  const int h = blockIdx.x, sl = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int T = a.t;
   const int rep = a.hv / a.hk;
   const int kh = h / rep;
   const int key_dim = a.hk * DK;
 
-  // ---- the state slice into registers first (its latency hides under the conv) ---------------------------------
+  // ---- waves 0..WAVES-1 load the state slice; the CONV_WAVES after them compute the conv meanwhile (the vector
+  // memory counter is per wave, so the conv's loads do not queue behind the state's) ------------------------------
   const int c = lane & 15, rg = lane >> 4;
-  const int col = wave * COLS + c;
+  const int col = sl * SLICE + wave * COLS + c;   // column in the head
+  const int lcol = wave * COLS + c;               // column in the slice
   float s[32];
-  const float* sin = a.rec_in + (long long)h * DK * DV;
+  if (wave < WAVES) {
+    const float* sin = a.rec_in + (long long)h * DK * DV;
 #pragma unroll
-  for (int i = 0; i < 32; ++i) s[i] = sin[(long long)(32 * rg + i) * DV + col];
+    for (int i = 0; i < 32; ++i) s[i] = sin[(long long)(32 * rg + i) * DV + col];
+  }
 
-  // ---- causal conv1d + SiLU over the head's q, k (key head kh) and v channels --------------------------------
-  if (tid < 2 * DK + DV) {
+  // ---- causal conv1d + SiLU over the head's q, k (key head kh) and this slice's v channels ---------------------
+  const bool kw_writer = (h % rep) == 0 && sl == 0;   // the workgroup that writes its key head's q/k conv state
+  for (int cidx = tid - 64 * WAVES; cidx >= 0 && cidx < 2 * DK + SLICE; cidx += 64 * CONV_WAVES) {
     int ch;           // channel index in the conv input order q | k | v
     int src_off;      // column of that channel in proj
     float* dst;
+    int ld;           // LDS row stride of dst
     bool writer;      // which workgroup writes this channel's new conv state
-    if (tid < DK) { ch = kh * DK + tid; src_off = a.q_off + kh * DK + tid; dst = &qs[0][tid]; writer = (h % rep) == 0; }
-    else if (tid < 2 * DK) { const int i = tid - DK; ch = key_dim + kh * DK + i; src_off = a.k_off + kh * DK + i; dst = &ks[0][i]; writer = (h % rep) == 0; }
-    else { const int i = tid - 2 * DK; ch = 2 * key_dim + h * DV + i; src_off = a.v_off + h * DV + i; dst = &vs[0][i]; writer = true; }
+    if (cidx < DK) { ch = kh * DK + cidx; src_off = a.q_off + kh * DK + cidx; dst = &qs[0][cidx]; ld = DK; writer = kw_writer; }
+    else if (cidx < 2 * DK) { const int i = cidx - DK; ch = key_dim + kh * DK + i; src_off = a.k_off + kh * DK + i; dst = &ks[0][i]; ld = DK; writer = kw_writer; }
+    else {
+      const int i = cidx - 2 * DK, hc = sl * SLICE + i;
+      ch = 2 * key_dim + h * DV + hc; src_off = a.v_off + h * DV + hc; dst = &vs[0][i]; ld = SLICE; writer = true;
+    }
     float w[CW], xs[CW - 1 + TMAX];
 #pragma unroll
     for (int j = 0; j < CW; ++j) w[j] = bf(a.conv_w, (long long)ch * CW + j);
@@ -81,7 +96,7 @@ __global__ __launch_bounds__(512) void gdn_step(GdnArgs a) {
       float y = 0.0f;
 #pragma unroll
       for (int j = 0; j < CW; ++j) y = __fadd_rn(y, __fmul_rn(w[j], xs[j + t]));   // the oracle's y += w·x
-      dst[t * DK] = round_bf16(silu_f(round_bf16(y)));
+      dst[t * ld] = round_bf16(silu_f(round_bf16(y)));
     }
     if (writer) {                 // the last CW-1 inputs of [state | x]
 #pragma unroll
@@ -94,16 +109,17 @@ __global__ __launch_bounds__(512) void gdn_step(GdnArgs a) {
     }
   }
   // gates per token: β = bf16(σ(b)), e^g with g = −exp(A_log)·softplus(a + dt_bias)
-  if (tid < T) {
-    const float bv = bf(a.ab, (long long)tid * a.ldab + a.b_off + h);
-    const float av = bf(a.ab, (long long)tid * a.ldab + a.a_off + h);
-    beta_s[tid] = round_bf16(sigmoid_f(bv));
-    eg_s[tid] = expf(a.neg_exp_a[h] * softplus_f(av + a.dt_bias[h]));
+  if (tid >= 64 * WAVES && tid - 64 * WAVES < T) {
+    const int t = tid - 64 * WAVES;
+    const float bv = bf(a.ab, (long long)t * a.ldab + a.b_off + h);
+    const float av = bf(a.ab, (long long)t * a.ldab + a.a_off + h);
+    beta_s[t] = round_bf16(sigmoid_f(bv));
+    eg_s[t] = expf(a.neg_exp_a[h] * softplus_f(av + a.dt_bias[h]));
   }
   __syncthreads();
 
-  // ---- L2 norms: wave w takes tokens w, w + 8 ------------------------------------------------------------------
-  for (int t = wave; t < T; t += WAVES) {
+  // ---- L2 norms: wave w takes tokens w, w + 4, … -----------------------------------------------------------------
+  for (int t = wave; t < T; t += WAVES + CONV_WAVES) {
     const float q0 = qs[t][lane], q1 = qs[t][lane + 64];
     const float k0 = ks[t][lane], k1 = ks[t][lane + 64];
     const float rq = 1.0f / sqrtf(wave_sum(q0 * q0 + q1 * q1) + 1e-6f);
@@ -114,6 +130,7 @@ __global__ __launch_bounds__(512) void gdn_step(GdnArgs a) {
     ks[t][lane + 64] = k1 * rk;
   }
   __syncthreads();
+  if (wave >= WAVES) return;
 
   // ---- the recurrence, token by token, state in registers --------------------------------------------------------
   for (int t = 0; t < T; ++t) {
@@ -136,7 +153,7 @@ __global__ __launch_bounds__(512) void gdn_step(GdnArgs a) {
       m2 = fmaf(s[i + 2], kk[i + 2], m2); m3 = fmaf(s[i + 3], kk[i + 3], m3);
     }
     const float kv_mem = quad16_sum((m0 + m1) + (m2 + m3));
-    const float delta = (vs[t][col] - kv_mem) * beta_s[t];
+    const float delta = (vs[t][lcol] - kv_mem) * beta_s[t];
     float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
 #pragma unroll
     for (int i = 0; i < 32; i += 4) {
@@ -148,26 +165,27 @@ __global__ __launch_bounds__(512) void gdn_step(GdnArgs a) {
       o2 = fmaf(s[i + 2], qq[i + 2], o2); o3 = fmaf(s[i + 3], qq[i + 3], o3);
     }
     const float o = quad16_sum((o0 + o1) + (o2 + o3));
-    if (rg == 0) os[t][col] = round_bf16(o);
+    if (rg == 0) a.y[(long long)t * a.ldy + h * DV + col] = f32_to_bf16_bits(o);   // the BF16 read-out
   }
   float* sout = a.rec_out + (long long)h * DK * DV;
 #pragma unroll
   for (int i = 0; i < 32; ++i) sout[(long long)(32 * rg + i) * DV + col] = s[i];
-  __syncthreads();
+}
 
-  // ---- gated RMSNorm over the head's dv outputs of each token ------------------------------------------------------
-  for (int t = wave; t < T; t += WAVES) {
-    const float v0 = os[t][lane], v1 = os[t][lane + 64];
-    const float ms = wave_sum(v0 * v0 + v1 * v1) / (float)DV;
-    if (lane == 0) rstd_s[t] = 1.0f / sqrtf(ms + a.eps);
-  }
-  __syncthreads();
-  for (int idx = tid; idx < T * DV; idx += blockDim.x) {
-    const int t = idx / DV, cc = idx - t * DV;
-    const float n = round_bf16(os[t][cc] * rstd_s[t]);
+// gated RMSNorm over each head's dv read-outs, in place: y = bf16(bf16(bf16(w)·bf16(o·r))·silu(z)); one wave per
+// (head, token)
+__global__ __launch_bounds__(64) void gdn_gated_norm(GdnArgs a) {
+  const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+  uint16_t* y = a.y + (long long)t * a.ldy + h * DV;
+  const float v0 = bf16_bits_to_f32(y[lane]), v1 = bf16_bits_to_f32(y[lane + 64]);
+  const float r = 1.0f / sqrtf(wave_sum(v0 * v0 + v1 * v1) / (float)DV + a.eps);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int cc = lane + 64 * j;
+    const float n = round_bf16((j ? v1 : v0) * r);
     const float nw = round_bf16(round_bf16(a.norm_w[cc]) * n);
     const float z = bf(a.proj, (long long)t * a.ldp + a.z_off + h * DV + cc);
-    a.y[(long long)t * a.ldy + h * DV + cc] = f32_to_bf16_bits(nw * silu_f(z));
+    y[cc] = f32_to_bf16_bits(nw * silu_f(z));
   }
 }
 
@@ -188,7 +206,12 @@ extern "C" int mi_gdn_step(const mi_gdn_desc* d, void* stream) {
   a.conv_w = d->conv_w; a.neg_exp_a = d->neg_exp_a; a.dt_bias = d->dt_bias; a.norm_w = d->norm_w;
   a.conv_in = d->conv_in; a.conv_out = d->conv_out; a.rec_in = d->rec_in; a.rec_out = d->rec_out;
   a.y = d->y; a.ldy = d->ld_y; a.eps = d->eps;
-  hipLaunchKernelGGL(gdn_step, dim3(d->v_heads), dim3(512), 0, static_cast<hipStream_t>(stream), a);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(gdn_step, dim3(d->v_heads, NSLICE), dim3(64 * (WAVES + CONV_WAVES)), 0, s, a);
   MI_TRY_HIP(hipGetLastError(), "gdn_step launch");
+  if (!d->defer_norm) {
+    hipLaunchKernelGGL(gdn_gated_norm, dim3(d->v_heads, d->t), dim3(64), 0, s, a);
+    MI_TRY_HIP(hipGetLastError(), "gdn_gated_norm launch");
+  }
   return MI_OK;
 }

@@ -84,6 +84,10 @@ struct Args {
   int tb;                   // gemv_tk: 16-row tiles per workgroup
   int ks, kc;               // gemv_tk: K splits, chunks per split
   float* part;              // gemv_tk with ks > 1: FP32 partials [ks][m][n_tiles·16]
+  const float* gnorm_w;     // gated head RMSNorm on the input (Gated DeltaNet output norm), or null
+  const uint16_t* gnorm_z;
+  int ld_gnorm_z;
+  float gnorm_eps;
   int row_ld;               // gemv_row: LDS row stride of a wave's staged slice (elements)
   int row_wave_lds;         // gemv_row: LDS bytes per wave
 };
@@ -149,6 +153,34 @@ __device__ __forceinline__ void store_out(const Args& a, long long idx, float v)
   else a.y[idx] = f32_to_bf16_bits(v);
 }
 
+
+// the Gated DeltaNet output norm (nn/gdn.py:86-93, the gdn_norm op) on one lane's 8 consecutive input values at
+// `col` of token row `xrow`, whose 128-column head spans this lane's 16-lane row (every lane of the wave calls it):
+// x ← bf16(bf16(bf16(w)·bf16(x·r))·silu(z)), r = rsqrt(mean over the head of x² + eps)
+__device__ __forceinline__ void gated_head_norm8(uint32_t (&qq)[4], const uint4 zv, const float4 w0, const float4 w1,
+                                                 float eps) {
+  float sq = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float lo = bf16_bits_to_f32(qq[i] & 0xFFFFu), hi = bf16_bits_to_f32(qq[i] >> 16);
+    sq = fmaf(lo, lo, fmaf(hi, hi, sq));
+  }
+  const float r = 1.0f / sqrtf(sum16(sq) / 128.0f + eps);
+  const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+  const uint32_t zz[4] = {zv.x, zv.y, zv.z, zv.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float o[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float x = bf16_bits_to_f32(h ? qq[i] >> 16 : qq[i] & 0xFFFFu);
+      const float z = bf16_bits_to_f32(h ? zz[i] >> 16 : zz[i] & 0xFFFFu);
+      const float nw = round_bf16(round_bf16(wv[2 * i + h]) * round_bf16(x * r));
+      o[h] = nw * silu_f(z);
+    }
+    qq[i] = (uint32_t)f32_to_bf16_bits(o[0]) | ((uint32_t)f32_to_bf16_bits(o[1]) << 16);
+  }
+}
 
 // one output value: row tile·16 + m_row of token t, already scaled by its row scale; `up` is the value of the row
 // 8 below it (the up half of a silu·mul tile), fetched by the caller with a shuffle every lane executes
@@ -241,7 +273,7 @@ __global__ __launch_bounds__(KW == 16 ? 640 : 1024) void gemv_row(Args a) {
 
   // ---- loads: activations, norm weights, scale pieces, then every weight chunk of the slice --------------------
   const int per_row = cols / 8;
-  uint4 xv[NPL];
+  uint4 xv[NPL], zv[NPL];
   float4 nv[NPL][2];
 #pragma unroll
   for (int i = 0; i < NPL; ++i) {
@@ -252,6 +284,10 @@ __global__ __launch_bounds__(KW == 16 ? 640 : 1024) void gemv_row(Args a) {
     if (a.norm_w) {
       nv[i][0] = *reinterpret_cast<const float4*>(a.norm_w + c0 * KC + e);
       nv[i][1] = *reinterpret_cast<const float4*>(a.norm_w + c0 * KC + e + 4);
+    } else if (a.gnorm_w) {
+      zv[i] = *reinterpret_cast<const uint4*>(a.gnorm_z + (j ? xr1 : xr0) * a.ld_gnorm_z + c0 * KC + e);
+      nv[i][0] = *reinterpret_cast<const float4*>(a.gnorm_w + ((c0 * KC + e) & 127));
+      nv[i][1] = *reinterpret_cast<const float4*>(a.gnorm_w + ((c0 * KC + e) & 127) + 4);
     }
   }
   uint4 sv[NG > 0 ? NG : 1];
@@ -320,6 +356,9 @@ __global__ __launch_bounds__(KW == 16 ? 640 : 1024) void gemv_row(Args a) {
         vv[q] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
       }
     }
+  } else if (a.gnorm_w) {
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) gated_head_norm8(reinterpret_cast<uint32_t(&)[4]>(xv[i]), zv[i], nv[i][0], nv[i][1], a.gnorm_eps);
   }
 #pragma unroll
   for (int i = 0; i < NPL; ++i) {
@@ -522,7 +561,7 @@ void gemv_rowp(Args a) {
 
   // ---- loads: activations, norm weights, then the first two tiles' scale pieces and weight chunks -------------
   const int per_row = cols / 8;
-  uint4 xv[NPL];
+  uint4 xv[NPL], zv[NPL];
   float4 nv[NPL][2];
 #pragma unroll
   for (int i = 0; i < NPL; ++i) {
@@ -533,6 +572,10 @@ void gemv_rowp(Args a) {
     if (a.norm_w) {
       nv[i][0] = *reinterpret_cast<const float4*>(a.norm_w + c0 * KC + e);
       nv[i][1] = *reinterpret_cast<const float4*>(a.norm_w + c0 * KC + e + 4);
+    } else if (a.gnorm_w) {
+      zv[i] = *reinterpret_cast<const uint4*>(a.gnorm_z + (j ? xr1 : xr0) * a.ld_gnorm_z + c0 * KC + e);
+      nv[i][0] = *reinterpret_cast<const float4*>(a.gnorm_w + ((c0 * KC + e) & 127));
+      nv[i][1] = *reinterpret_cast<const float4*>(a.gnorm_w + ((c0 * KC + e) & 127) + 4);
     }
   }
   // chunk cc of the slice at a compile-time offset from chunk c0 (NVFP4: KW = 4 slices lie in one group of 8,
@@ -625,6 +668,9 @@ void gemv_rowp(Args a) {
         vv[q] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
       }
     }
+  } else if (a.gnorm_w) {
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) gated_head_norm8(reinterpret_cast<uint32_t(&)[4]>(xv[i]), zv[i], nv[i][0], nv[i][1], a.gnorm_eps);
   }
 #pragma unroll
   for (int i = 0; i < NPL; ++i) {
@@ -890,11 +936,18 @@ __global__ __launch_bounds__(512) void gemv_tk(Args a) {
     float rr = 1.0f;
     if (a.norm_w) rr = 1.0f / sqrtf(wave_sum(sq) / (float)a.k + a.eps);   // one split covers the row here
     float mx = 0.0f;
-    if (a.norm_w || MF || FMT == FMT_INT4) {
+    if (a.norm_w || a.gnorm_w || MF || FMT == FMT_INT4) {
       wave_lds_sync();
-      for (int v = lane; v < nv; v += 64) {
+      for (int v = lane; v < nv; v += 64) {      // nv is a multiple of 16: whole 16-lane rows stay active
         uint4 q = *reinterpret_cast<const uint4*>(dst + v * 8);
         uint32_t* qq = reinterpret_cast<uint32_t*>(&q);
+        if (a.gnorm_w) {
+          const int col = kb * KC + v * 8;
+          const uint4 zv = *reinterpret_cast<const uint4*>(a.gnorm_z + xrow_of(j) * a.ld_gnorm_z + col);
+          const float4 w0 = *reinterpret_cast<const float4*>(a.gnorm_w + (col & 127));
+          const float4 w1 = *reinterpret_cast<const float4*>(a.gnorm_w + (col & 127) + 4);
+          gated_head_norm8(reinterpret_cast<uint32_t(&)[4]>(q), zv, w0, w1, a.gnorm_eps);
+        }
         if (a.norm_w) {
           const int col = kb * KC + v * 8;
           const float4 w0 = *reinterpret_cast<const float4*>(a.norm_w + col);
@@ -1285,6 +1338,14 @@ int check_desc(const mi_gemv_desc* d) {
   MI_REQUIRE(((uintptr_t)d->x & 15) == 0 && d->ldx % 8 == 0, "mi_gemv: x must be 16-byte aligned with ldx %% 8 == 0");
   MI_REQUIRE(((uintptr_t)d->w & 15) == 0, "mi_gemv: weight pack must be 16-byte aligned");
   MI_REQUIRE(!d->norm_w || ((uintptr_t)d->norm_w & 15) == 0, "mi_gemv: norm_w must be 16-byte aligned");
+  if (d->gnorm_w) {
+    MI_REQUIRE(!d->norm_w, "mi_gemv: norm_w and gnorm_w are exclusive");
+    MI_REQUIRE(d->format != FMT_BF16, "mi_gemv: the gated head norm is built for 128-column chunks (NVFP4, INT4)");
+    MI_REQUIRE(d->k % 128 == 0, "mi_gemv: gated head norm needs k %% 128 == 0");
+    MI_REQUIRE(d->gnorm_z && ((uintptr_t)d->gnorm_z & 15) == 0 && d->ld_gnorm_z % 8 == 0 && d->ld_gnorm_z >= d->k,
+               "mi_gemv: gnorm_z must be 16-byte aligned with ld_gnorm_z %% 8 == 0 and >= k");
+    MI_REQUIRE(((uintptr_t)d->gnorm_w & 15) == 0, "mi_gemv: gnorm_w must be 16-byte aligned");
+  }
   return MI_OK;
 }
 
@@ -1589,6 +1650,10 @@ int mi_gemv(const mi_gemv_desc* d, void* stream) {
   a.y = d->y;
   a.res = d->residual;
   a.norm_w = d->norm_w;
+  a.gnorm_w = d->gnorm_w;
+  a.gnorm_z = d->gnorm_z;
+  a.ld_gnorm_z = d->ld_gnorm_z;
+  a.gnorm_eps = d->gnorm_eps;
   a.groups = d->groups;
   a.eps = d->eps;
   a.ldx = d->ldx; a.ldy = d->ldy; a.ldr = d->ldr;

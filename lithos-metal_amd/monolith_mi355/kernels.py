@@ -84,10 +84,12 @@ def _bf16_2d(t, name, aligned=True):
 
 
 def gemv(w: PackedWeight, x, *, epilogue=None, residual=None, norm_w=None, eps: float = 1e-6, out=None,
-         stream=None, workspace=None, out_f32: bool = False):
+         stream=None, workspace=None, out_f32: bool = False, gated_norm=None):
     """``gemv`` (``ops/gemv.py:1-12``): ``y = x·Wᵀ`` for ``x [M, K]`` bf16, M ≤ 16; ``epilogue`` None | "residual" |
     "silu_mul" (rows gate|up interleaved by 8, output N/2 columns) | "silu_mul_rounded"; ``norm_w`` = the (1 + w)
-    float32 weight of a fused input RMSNorm; ``out_f32`` writes the unrounded FP32 result (``lm_head``)."""
+    float32 weight of a fused input RMSNorm; ``out_f32`` writes the unrounded FP32 result (``lm_head``).
+    ``gated_norm = (w [128] float32, z [M, K] bf16 view, eps)`` applies the Gated DeltaNet output norm
+    (``gdn_norm``, ``nn/gdn.py:86-93``) to x per 128-column head while staging it."""
     torch = _torch()
     _bf16_2d(x, "gemv x")
     m, k = x.shape
@@ -107,6 +109,13 @@ def gemv(w: PackedWeight, x, *, epilogue=None, residual=None, norm_w=None, eps: 
             raise ValueError("gemv: residual too small")
     if norm_w is not None and (norm_w.dtype != torch.float32 or norm_w.numel() != k):
         raise ValueError("gemv: norm_w must be float32 [K]")
+    gw, gz, geps = gated_norm if gated_norm is not None else (None, None, 0.0)
+    if gated_norm is not None:
+        if gw.dtype != torch.float32 or gw.numel() != 128:
+            raise ValueError("gemv: gated_norm weight must be float32 [128]")
+        _bf16_2d(gz, "gemv gated_norm z")
+        if gz.shape[0] < m or gz.shape[1] < k:
+            raise ValueError("gemv: gated_norm z too small")
     d = hip.MiGemvDesc(format=hip.MI_FMT[w.format], n=w.n, k=w.k, m=m, w=hip.ptr(w.data),
                        row_scale=hip.ptr(w.row_scale), x=hip.ptr(x), ldx=x.stride(0), y=hip.ptr(out),
                        ldy=out.stride(0), epilogue=hip.MI_EPI[epilogue],
@@ -114,7 +123,8 @@ def gemv(w: PackedWeight, x, *, epilogue=None, residual=None, norm_w=None, eps: 
                        ldr=residual.stride(0) if epilogue == "residual" else 0, norm_w=hip.ptr(norm_w), eps=eps,
                        groups=0, max_groups=0, top_k=0, x_per_slot=0,
                        workspace=hip.ptr(workspace), workspace_bytes=0 if workspace is None else workspace.numel(),
-                       out_f32=int(out_f32))
+                       out_f32=int(out_f32), gnorm_w=hip.ptr(gw), gnorm_z=hip.ptr(gz),
+                       ld_gnorm_z=gz.stride(0) if gz is not None else 0, gnorm_eps=geps)
     hip.call("mi_gemv", C.byref(d), hip.stream_handle(stream))
     return out
 
@@ -131,12 +141,14 @@ def dequant(w: PackedWeight, expert: int = 0, stream=None):
 
 
 def gdn_step(proj, conv_in, conv_out, rec_in, rec_out, *, conv_w, neg_exp_a, dt_bias, norm_w, k_heads, v_heads,
-             dk=128, dv=128, conv_width=4, eps=1e-6, ab=None, offsets=None, out=None, stream=None):
+             dk=128, dv=128, conv_width=4, eps=1e-6, ab=None, offsets=None, out=None, stream=None,
+             defer_norm: bool = False):
     """``gdn_mixer`` + ``gdn_norm`` (``ops/gdn.py:1-24``) for ``proj [T, N1]`` bf16 in part order
     ``z | q | k | v | a | b`` (``nn/gdn.py:48-52``) unless ``offsets`` (z, q, k, v, a, b) says otherwise.
     Conv state ``[conv_dim, W-1]`` bf16 is read from ``conv_in`` and written to ``conv_out`` (distinct); the FP32
     recurrent state ``[hv, dk, dv]`` is read from ``rec_in`` and written to ``rec_out`` (may be the same tensor).
-    Returns ``[T, hv·dv]`` bf16."""
+    Returns ``[T, hv·dv]`` bf16: the gated-norm output, or with ``defer_norm`` the BF16 read-out ``o`` for a
+    consumer that applies the norm itself (``gemv(..., gated_norm=...)``)."""
     torch = _torch()
     _bf16_2d(proj, "gdn proj", aligned=False)
     t = proj.shape[0]
@@ -163,7 +175,8 @@ def gdn_step(proj, conv_in, conv_out, rec_in, rec_out, *, conv_w, neg_exp_a, dt_
                       ld_ab=ab.stride(0) if ab is not None else 0, a_off=a_off, b_off=b_off, conv_w=hip.ptr(conv_w),
                       neg_exp_a=hip.ptr(neg_exp_a), dt_bias=hip.ptr(dt_bias), norm_w=hip.ptr(norm_w),
                       conv_in=hip.ptr(conv_in), conv_out=hip.ptr(conv_out), rec_in=hip.ptr(rec_in),
-                      rec_out=hip.ptr(rec_out), y=hip.ptr(out), ld_y=out.stride(0), eps=eps)
+                      rec_out=hip.ptr(rec_out), y=hip.ptr(out), ld_y=out.stride(0), eps=eps,
+                      defer_norm=int(defer_norm))
     hip.call("mi_gdn_step", C.byref(d), hip.stream_handle(stream))
     return out
 

@@ -124,12 +124,15 @@ class GdnDecoderLayer:
         proj, o, h1, act, h2 = self.buffers(h.shape[0])
         out = h2 if out is None else out
         kernels.gemv(self.w_in.packed, h, norm_w=self.norm_w, eps=self.eps, out=proj)
+        defer = proj.stride(0) % 8 == 0            # z must be a 16-byte aligned view for the fused norm
         cin, cout = self.conv_state[self.parity], self.conv_state[1 - self.parity]
         kernels.gdn_step(proj, cin, cout, self.rec_state, self.rec_state, conv_w=self.conv_w, neg_exp_a=self.neg_exp_a,
                          dt_bias=self.dt_bias, norm_w=self.gdn_norm_w, k_heads=self.hk, v_heads=self.hv, dk=self.dk,
-                         dv=self.dv, conv_width=self.conv, eps=self.eps, out=o)
+                         dv=self.dv, conv_width=self.conv, eps=self.eps, out=o, defer_norm=defer)
         self.parity ^= 1
-        kernels.gemv(self.w_out.packed, o, epilogue="residual", residual=h, out=h1)
+        # the gated RMSNorm (gdn_norm) is applied by the output projection while it stages o; z = proj[:, :hv·dv]
+        kernels.gemv(self.w_out.packed, o, epilogue="residual", residual=h, out=h1,
+                     gated_norm=(self.gdn_norm_w, proj[:, : self.hv * self.dv], self.eps) if defer else None)
         return self.mlp(h1, act=act, out=out)
 
     def mixer_bytes(self, m: int) -> int:

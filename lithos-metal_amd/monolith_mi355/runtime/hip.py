@@ -33,7 +33,8 @@ class MiGemvDesc(C.Structure):
                 ("y", C.c_void_p), ("ldy", C.c_int32), ("epilogue", C.c_int32), ("residual", C.c_void_p),
                 ("ldr", C.c_int32), ("norm_w", C.c_void_p), ("eps", C.c_float), ("groups", C.c_void_p),
                 ("max_groups", C.c_int32), ("top_k", C.c_int32), ("x_per_slot", C.c_int32),
-                ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t), ("out_f32", C.c_int32)]
+                ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t), ("out_f32", C.c_int32),
+                ("gnorm_w", C.c_void_p), ("gnorm_z", C.c_void_p), ("ld_gnorm_z", C.c_int32), ("gnorm_eps", C.c_float)]
 
 
 class MiGdnDesc(C.Structure):
@@ -43,7 +44,7 @@ class MiGdnDesc(C.Structure):
                 ("ld_ab", C.c_int32), ("a_off", C.c_int32), ("b_off", C.c_int32), ("conv_w", C.c_void_p),
                 ("neg_exp_a", C.c_void_p), ("dt_bias", C.c_void_p), ("norm_w", C.c_void_p), ("conv_in", C.c_void_p),
                 ("conv_out", C.c_void_p), ("rec_in", C.c_void_p), ("rec_out", C.c_void_p), ("y", C.c_void_p),
-                ("ld_y", C.c_int32), ("eps", C.c_float)]
+                ("ld_y", C.c_int32), ("eps", C.c_float), ("defer_norm", C.c_int32)]
 
 
 class MiGqaDesc(C.Structure):

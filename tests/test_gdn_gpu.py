@@ -102,3 +102,29 @@ def test_gdn_rejects_aliased_conv_state(torch_gpu):
     proj = torch.zeros(1, 256 + 768 + 4, dtype=torch.bfloat16, device="cuda")
     with pytest.raises(MiError):
         kernels.gdn_step(proj, conv, conv, rec, rec, k_heads=2, v_heads=2, **p)
+
+
+@pytest.mark.parametrize("t", [1, 8])
+def test_gdn_deferred_norm_read_out(torch_gpu, t):
+    """defer_norm: y holds the BF16 read-out o; the oracle's gated RMSNorm of it is the mixer output."""
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    hk, hv = 4, 12
+    rng = np.random.default_rng(7 + t)
+    p = _params(rng, hk, hv)
+    dp = _dev_params(torch, p)
+    conv_dim = 2 * hk * 128 + hv * 128
+    n1 = hv * 128 + conv_dim + 2 * hv
+    conv = rbf(rng.standard_normal((conv_dim, 3)) * 0.5)
+    rec = (rng.standard_normal((hv, 128, 128)) * 0.1).astype(np.float32)
+    proj = rbf(rng.standard_normal((t, n1)))
+    ref, conv_ref, rec_ref = ON.gdn_mix(proj, conv, rec, k_heads=hk, v_heads=hv, dk=128, dv=128, eps=EPS, **p)
+    rec_d = torch.from_numpy(rec).cuda()
+    conv_out = torch.empty(conv_dim, 3, dtype=torch.bfloat16, device="cuda")
+    o = kernels.gdn_step(to_dev_bf16(torch, proj), to_dev_bf16(torch, conv), conv_out, rec_d, rec_d, k_heads=hk,
+                         v_heads=hv, eps=EPS, defer_norm=True, **dp)
+    torch.cuda.synchronize()
+    o = from_dev_bf16(o).reshape(t, hv, 128)
+    z = proj[:, : hv * 128].reshape(t, hv, 128)
+    got = ON.gated_rms_norm(o, z, p["norm_w"], EPS).reshape(t, hv * 128)
+    _check(got, ref, from_dev_bf16(conv_out), conv_ref, rec_d.cpu().numpy(), rec_ref)

@@ -208,3 +208,29 @@ def test_gemv_tiles_per_workgroup(torch_gpu, fmt, n, k, epi, rng, monkeypatch):
         ref = ON.linear(xn, wd, epilogue=epi, residual=res if epi else None)
     chk = check_against_oracle(outs[1], ref)
     assert chk.ok_rounded(), chk
+
+
+@pytest.mark.parametrize("fmt", ["nvfp4", "int4_affine"])
+@pytest.mark.parametrize("mtok", [1, 2, 8])
+@pytest.mark.parametrize("plan", [None, "4,3", "tk"])
+def test_gemv_gated_head_norm(torch_gpu, fmt, mtok, plan, rng, monkeypatch):
+    """The Gated DeltaNet output norm fused into the output projection's input staging: per 128-column head,
+    bf16(bf16(bf16(w)·bf16(o·r))·silu(z)), then the GEMV — against the oracle's gated_rms_norm and matmul."""
+    from monolith_mi355 import kernels
+    if plan == "tk":
+        monkeypatch.setenv("MI_GEMV_KERNEL", "tk")
+    elif plan:
+        monkeypatch.setenv("MI_GEMV_ROW", plan)
+    heads, n = 12, 320
+    k = heads * 128
+    m = _matrix(fmt, n, k, rng)
+    o = rbf(rng.standard_normal((mtok, k)) * 0.3)
+    zfull = rbf(rng.standard_normal((mtok, k + 64)) * 2)       # z as a view with its own row stride
+    wn = rbf(1 + rng.standard_normal(128) * 0.2).astype(np.float32)
+    zd = to_dev_bf16(torch_gpu, zfull)[:, 32: 32 + k]
+    got = kernels.gemv(_upload(torch_gpu, m), to_dev_bf16(torch_gpu, o), out_f32=True,
+                       gated_norm=(torch_gpu.from_numpy(wn).cuda(), zd, 1e-6)).cpu().numpy()
+    xn = ON.gated_rms_norm(o.reshape(mtok, heads, 128), zfull[:, 32: 32 + k].reshape(mtok, heads, 128), wn, 1e-6)
+    ref = ON.matmul_acc(xn.reshape(mtok, k), _dequant(m))
+    chk = check_against_oracle(got, ref)
+    assert chk.ok_rounded(), (fmt, mtok, plan, chk)
