@@ -246,9 +246,10 @@ __global__ __launch_bounds__(KW == 16 ? 640 : 1024) void gemv_row(Args a) {
   constexpr int KC = chunk_cols(FMT);
   constexpr int NPL = MT * KW * KC / 8 / 64 > 0 ? MT * KW * KC / 8 / 64 : 1;   // activation vectors per lane
   constexpr int NG = FMT == FMT_NVFP4 ? (KW + 7) / 8 : 0;                         // scale pieces per wave
+  static_assert(KW == 4 || KW % 8 == 0, "NVFP4 slices: half a scale group or whole groups");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform (scalar) in the compiler's view
   const int S = blockDim.x >> 6;
   const int tile = blockIdx.x;
   int expert = 0, cnt = a.m;
@@ -410,12 +411,12 @@ __global__ __launch_bounds__(KW == 16 ? 640 : 1024) void gemv_row(Args a) {
       for (int t = 0; t < MT; ++t)
 #pragma unroll
         for (int s = 0; s < 4; ++s) xq[t][s] = *reinterpret_cast<const uint4*>(xs + (size_t)t * ld + cc * 128 + 32 * g + 8 * s);
-      const int ci = ((c0 + cc) & 7);                // chunk in its group; KW >= 8 slices start on a group
+      // chunk in its group: KW >= 8 slices start on a group, KW = 4 slices on one of its halves (c0 % 4 == 0)
       const uint4 pv = sv[KW >= 8 ? cc >> 3 : 0];
       const uint32_t word = KW >= 8 ? (cc & 6) == 0 ? pv.x : (cc & 6) == 2 ? pv.y : (cc & 6) == 4 ? pv.z : pv.w
-                                    : (ci >> 1) == 0 ? pv.x : (ci >> 1) == 1 ? pv.y : (ci >> 1) == 2 ? pv.z : pv.w;
-      const uint32_t two = (KW >= 8 ? (cc & 1) : (ci & 1)) ? word >> 16 : word & 0xFFFFu;
-      const f32x2 f = __builtin_amdgcn_cvt_pk_f32_fp8((int)two, false);
+                                    : (c0 & 4) ? (cc < 2 ? pv.z : pv.w) : (cc < 2 ? pv.x : pv.y);
+      const f32x2 f = (cc & 1) ? __builtin_amdgcn_cvt_pk_f32_fp8((int)word, true)
+                               : __builtin_amdgcn_cvt_pk_f32_fp8((int)word, false);
       const uint32_t u0 = __float_as_uint(f.x), u1 = __float_as_uint(f.y);
       const float e[2] = {__uint_as_float(u0 & 0x7F800000u), __uint_as_float(u1 & 0x7F800000u)};
       const float mant[2] = {__uint_as_float((u0 & 0x807FFFFFu) | 0x3F800000u),
@@ -532,9 +533,10 @@ void gemv_rowp(Args a) {
   constexpr int KC = chunk_cols(FMT);
   constexpr int NPL = MT * KW * KC / 8 / 64 > 0 ? MT * KW * KC / 8 / 64 : 1;   // activation vectors per lane
   constexpr int NG = FMT == FMT_NVFP4 ? (KW + 7) / 8 : 1;                         // scale pieces per wave and tile
+  static_assert(KW == 4 || KW % 8 == 0, "NVFP4 slices: half a scale group or whole groups");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform (scalar) in the compiler's view
   const int S = blockDim.x >> 6;
   const int G = gridDim.x;
   const int ntl = (a.n_tiles - 1 - (int)blockIdx.x) / G + 1;   // this workgroup's tiles (gridDim.x <= n_tiles)
@@ -723,12 +725,12 @@ void gemv_rowp(Args a) {
         for (int t = 0; t < MT; ++t)
   #pragma unroll
           for (int s = 0; s < 4; ++s) xq[t][s] = *reinterpret_cast<const uint4*>(xs + (size_t)t * ld + cc * 128 + 32 * g + 8 * s);
-        const int ci = ((c0 + cc) & 7);                // chunk in its group; KW >= 8 slices start on a group
+        // chunk in its group: KW >= 8 slices start on a group, KW = 4 slices on one of its halves (c0 % 4 == 0)
         const uint4 pv = ss[KW >= 8 ? cc >> 3 : 0];
         const uint32_t word = KW >= 8 ? (cc & 6) == 0 ? pv.x : (cc & 6) == 2 ? pv.y : (cc & 6) == 4 ? pv.z : pv.w
-                                      : (ci >> 1) == 0 ? pv.x : (ci >> 1) == 1 ? pv.y : (ci >> 1) == 2 ? pv.z : pv.w;
-        const uint32_t two = (KW >= 8 ? (cc & 1) : (ci & 1)) ? word >> 16 : word & 0xFFFFu;
-        const f32x2 f = __builtin_amdgcn_cvt_pk_f32_fp8((int)two, false);
+                                      : (c0 & 4) ? (cc < 2 ? pv.z : pv.w) : (cc < 2 ? pv.x : pv.y);
+        const f32x2 f = (cc & 1) ? __builtin_amdgcn_cvt_pk_f32_fp8((int)word, true)
+                                 : __builtin_amdgcn_cvt_pk_f32_fp8((int)word, false);
         const uint32_t u0 = __float_as_uint(f.x), u1 = __float_as_uint(f.y);
         const float e[2] = {__uint_as_float(u0 & 0x7F800000u), __uint_as_float(u1 & 0x7F800000u)};
         const float mant[2] = {__uint_as_float((u0 & 0x807FFFFFu) | 0x3F800000u),
@@ -856,7 +858,7 @@ __global__ __launch_bounds__(512) void gemv_tk(Args a) {
   constexpr int KC = chunk_cols(FMT);
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform (scalar) in the compiler's view
   const int S = blockDim.x >> 6;
   const int split = blockIdx.y;
   int expert = 0, cnt = a.m;
