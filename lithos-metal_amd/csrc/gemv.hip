@@ -238,6 +238,26 @@ __device__ __forceinline__ void load_chunk(Units<FMT>& u, const uint8_t* tb, int
 // order; this keeps the compiler from moving them)
 __device__ __forceinline__ void wave_lds_sync() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); __builtin_amdgcn_wave_barrier(); }
 
+// Σ over the S K slices of one tile row in the order every M = 1 kernel uses: four partial sums p_q over slices
+// q, q + 4, … (q = 0..3) in increasing order, then (p0 + p1) + (p2 + p3). slice_sum runs it on a whole wave — lane
+// (r = l % 16, q = l / 16) forms p_q of row r and the rows meet through two lane exchanges — and returns the row's
+// total in every lane; slice_sum_lane is the same sum in one lane.
+__device__ __forceinline__ float slice_sum(const float* red, int stride, int S, int lane) {
+  const int r = lane & 15, q = lane >> 4;
+  float v = 0.0f;
+  for (int w = q; w < S; w += 4) v += red[w * stride + r];
+  return add_xor32(add_xor16(v));
+}
+__device__ __forceinline__ float slice_sum_lane(const float* red, int stride, int S, int r) {
+  float p[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    p[q] = 0.0f;
+    for (int w = q; w < S; w += 4) p[q] += red[w * stride + r];
+  }
+  return (p[0] + p[1]) + (p[2] + p[3]);
+}
+
 // ---- gemv_row: M <= 2 ------------------------------------------------------------------------------------------
 // Workgroup = one 16-row tile (blockIdx.x) of one group (blockIdx.y, MoE); wave w = K slice [w·KW, w·KW + KW).
 // LDS: per wave xs[MT][row_ld] (INT4: then seg[MT][KW][8]) | stat[S][2] | red[S][MT][16].
@@ -502,8 +522,7 @@ __global__ __launch_bounds__(KW == 16 ? 640 : 1024) void gemv_row(Args a) {
   if (a.ks > 1) {                               // this split's partial; gemv_tk_reduce adds the splits in order
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
-      float v = red[t * 16 + m_row];
-      for (int w = 1; w < S; ++w) v += red[(w * MT + t) * 16 + m_row];
+      const float v = slice_sum(red + t * 16, MT * 16, S, lane);
       if (g == 0 && t < cnt) a.part[((long long)split * a.m + t) * a.n_tiles * 16 + row] = v;
     }
     return;
@@ -511,8 +530,7 @@ __global__ __launch_bounds__(KW == 16 ? 640 : 1024) void gemv_row(Args a) {
   const float rs = a.row_scale != nullptr ? a.row_scale[(long long)expert * a.n_tiles * 16 + row] : 1.0f;
 #pragma unroll
   for (int t = 0; t < MT; ++t) {
-    float v = red[t * 16 + m_row];
-    for (int w = 1; w < S; ++w) v += red[(w * MT + t) * 16 + m_row];
+    float v = slice_sum(red + t * 16, MT * 16, S, lane);
     v *= rs;
     const float up = __shfl_down(v, 8, 16);
     if (g == 0) emit(a, pairs, cnt, tile, true, m_row, t, v, up);
@@ -523,9 +541,8 @@ __global__ __launch_bounds__(KW == 16 ? 640 : 1024) void gemv_row(Args a) {
 // Workgroup = S waves over tiles blockIdx.x, blockIdx.x + G, … (G = gridDim.x, at most a.rt tiles; G is sized so
 // every workgroup is resident at once) of one group (blockIdx.y, MoE) and one K split (blockIdx.z); wave w owns the
 // K slice [w·KW, w·KW + KW) of every one of those tiles. The activations (normalized when the norm is fused) are
-// staged once per workgroup; each wave keeps two tiles' weight chunks in flight, issuing tile j + 2 as soon as
-// tile j is consumed, so the stream never waits on the arithmetic. A tile's K slices meet in LDS in wave order
-// after the last tile.
+// staged once per workgroup; each wave issues tile j + 1 as soon as tile j is consumed. A tile's K slices meet in
+// LDS after the last tile, in the order of gemv_row.
 // LDS: per wave xs[MT][row_ld] (INT4: then seg[MT][KW][8]) | stat[S][2] | red[rt][S][MT][16].
 template <int FMT, int MT, int KW>
 __global__ __launch_bounds__(KW == 16 ? 640 : 1024) __attribute__((amdgpu_waves_per_eu(KW == 4 && MT == 1 ? 8 : 1)))
@@ -828,8 +845,7 @@ void gemv_rowp(Args a) {
     const bool ok = idx < total;
     const int q = ok ? idx >> 4 : 0, r = idx & 15;
     const int jt = q / MT, t = q - jt * MT;
-    float v = red[(jt * S * MT + t) * 16 + r];
-    for (int w = 1; w < S; ++w) v += red[((jt * S + w) * MT + t) * 16 + r];
+    float v = slice_sum_lane(red + (jt * S * MT + t) * 16, MT * 16, S, r);
     const int tile = tile_of(jt);
     const int row = tile * 16 + r;
     if (a.ks > 1) {                             // this split's partial; gemv_tk_reduce adds the splits in order
