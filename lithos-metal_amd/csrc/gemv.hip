@@ -858,6 +858,184 @@ void gemv_rowp(Args a) {
   }
 }
 
+// ---- gemv_rowm: 3 <= M <= 16, NVFP4 -----------------------------------------------------------------------------
+// The gemv_row wave layout on the matrix cores, over several tiles per workgroup. Workgroup = S waves over tiles
+// blockIdx.x + j·G (j < ntl) and K split blockIdx.z; wave w owns chunks [c0, c0 + 4) of every one of them. The
+// wave's activations for those chunks stay in VGPRs for the whole launch as the F16 A operands of
+// v_mfma_f32_16x16x32_f16 (token = A row; each token power-of-two scaled into F16 range over the wave's slice;
+// normalized first when the input norm is fused); the weights are the B operand, decoded exactly to F16. Each wave
+// issues tile j + 1 as soon as tile j is consumed (the operands leave no VGPRs for a second tile in flight). A
+// tile's K slices meet in LDS after the last tile, in the gemv_row order.
+// LDS: nw[K] (fused norm) | stat[S][16] | red[rt][S][16 tokens][16 rows].
+__global__ __launch_bounds__(768) void gemv_rowm(Args a) {
+  constexpr int KW = 4, KC = 128;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int S = blockDim.x >> 6;
+  const int G = gridDim.x;
+  const int ntl = (a.n_tiles - 1 - (int)blockIdx.x) / G + 1;
+  const int cnt = a.m;
+  const int split = blockIdx.z;
+  const int c0_raw = split * a.kc + wave * KW;
+  const bool active = c0_raw < min(a.chunks, (split + 1) * a.kc);   // slices are whole: kc % 4 == 0, chunks % 4 == 0
+  const int c0 = active ? c0_raw : 0;
+  const int g = lane >> 4, m_row = lane & 15;
+  const uint8_t* wmat = a.w;
+  auto tile_of = [&](int j) { return (int)blockIdx.x + j * G; };
+  float* nws = reinterpret_cast<float*>(smem);                                  // [K] when the norm is fused
+  float* stat = nws + (a.norm_w ? a.k : 0);                                    // [S][16]
+  float* red = stat + S * 16;                                                  // [rt][S][16][16]
+
+  // ---- the first tile's weights, then the activations ------------------------------------------------------------
+  const long long c0_off = nv_code_off(c0);
+  auto issue = [&](uint4 (&u)[KW], uint4& sv, int j) {
+    const uint8_t* tbase = wmat + (long long)tile_of(j) * a.tile_stride;
+    const int gi = c0 >> 3;
+    const uint8_t* p = tbase + nv_scale_off(gi, a.chunks);
+    if (nv_piece(nv_group_chunks(gi, a.chunks)) == 16) {
+      sv = *reinterpret_cast<const uint4*>(p + 16 * lane);
+    } else {
+      const uint2 t = *reinterpret_cast<const uint2*>(p + 8 * lane);
+      sv = uint4{t.x, t.y, 0u, 0u};
+    }
+#pragma unroll
+    for (int cc = 0; cc < KW; ++cc) u[cc] = *reinterpret_cast<const uint4*>(tbase + c0_off + cc * 1024 + 16 * lane);
+  };
+  uint4 u0[KW], s0;
+  issue(u0, s0, 0);
+
+  // x[token m_row][c0·128 + cc·128 + 32g + 8s + (0..7)]: the A operand of step s of chunk cc
+  const bool real = m_row < cnt;
+  uint4 xa[KW][4];
+  const uint16_t* xrow = a.x + (long long)(real ? m_row : 0) * a.ldx + c0 * KC + 32 * g;
+#pragma unroll
+  for (int cc = 0; cc < KW; ++cc)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) xa[cc][s] = *reinterpret_cast<const uint4*>(xrow + cc * KC + 8 * s);
+  if (!real) {                                // padding token rows: zero operands (their loads read row 0)
+#pragma unroll
+    for (int cc = 0; cc < KW; ++cc)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) xa[cc][s] = uint4{0u, 0u, 0u, 0u};
+  }
+
+  if (a.norm_w) {
+    // the norm weights into LDS once; Σx² per token over the row from every wave's slice
+    for (int i = threadIdx.x; i < a.k / 4; i += blockDim.x)
+      reinterpret_cast<float4*>(nws)[i] = reinterpret_cast<const float4*>(a.norm_w)[i];
+    float sq = 0.0f;
+#pragma unroll
+    for (int cc = 0; cc < KW; ++cc)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint32_t vv[4] = {xa[cc][s].x, xa[cc][s].y, xa[cc][s].z, xa[cc][s].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float lo = bf16_bits_to_f32(vv[q] & 0xFFFFu), hi = bf16_bits_to_f32(vv[q] >> 16);
+          sq = fmaf(lo, lo, fmaf(hi, hi, sq));
+        }
+      }
+    sq = add_xor32(add_xor16(active ? sq : 0.0f));    // the four lanes of token m_row
+    if (g == 0) stat[wave * 16 + m_row] = sq;
+    __syncthreads();
+    float t = 0.0f;
+    for (int w = 0; w < S; ++w) t += stat[w * 16 + m_row];
+    const float rr = 1.0f / sqrtf(t / (float)a.k + a.eps);
+#pragma unroll
+    for (int cc = 0; cc < KW; ++cc)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const float* wv = nws + (c0 + cc) * KC + 32 * g + 8 * s;
+        const float4 w0 = *reinterpret_cast<const float4*>(wv), w1 = *reinterpret_cast<const float4*>(wv + 4);
+        const float ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        uint32_t* vv = reinterpret_cast<uint32_t*>(&xa[cc][s]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float lo = round_bf16((bf16_bits_to_f32(vv[q] & 0xFFFFu) * rr) * ww[2 * q]);
+          const float hi = round_bf16((bf16_bits_to_f32(vv[q] >> 16) * rr) * ww[2 * q + 1]);
+          vv[q] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+        }
+        __builtin_amdgcn_sched_barrier(0);    // one step's weights at a time (the operands already hold 64 VGPRs)
+      }
+  }
+  // F16 operands: per token, 2^-p brings the slice max into [2^14, 2^15) (exact within 2^28 of the max)
+  float mx = 0.0f;
+#pragma unroll
+  for (int cc = 0; cc < KW; ++cc)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const uint32_t vv[4] = {xa[cc][s].x, xa[cc][s].y, xa[cc][s].z, xa[cc][s].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        mx = fmaxf(mx, fmaxf(fabsf(bf16_bits_to_f32(vv[q] & 0xFFFFu)), fabsf(bf16_bits_to_f32(vv[q] >> 16))));
+    }
+  mx = max_xor32(max_xor16(mx));
+  const int pe = mx == 0.0f ? 0 : (int)((__float_as_uint(mx) >> 23) & 0xFF) - 127 - 14;
+  const float inv = __uint_as_float((uint32_t)(127 - pe) << 23);
+  const float psc = __uint_as_float((uint32_t)(127 + pe) << 23);
+#pragma unroll
+  for (int cc = 0; cc < KW; ++cc)             // in place: xa now holds the F16 operands
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      uint32_t* vv = reinterpret_cast<uint32_t*>(&xa[cc][s]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f16x2 h = {(f16_t)(bf16_bits_to_f32(vv[q] & 0xFFFFu) * inv), (f16_t)(bf16_bits_to_f32(vv[q] >> 16) * inv)};
+        vv[q] = __builtin_bit_cast(uint32_t, h);
+      }
+    }
+  // the output rows of lane l are tokens 4g + i: their scales from the lanes that hold those tokens' A rows
+  float ps[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ps[i] = __shfl(psc, 4 * g + i, 64);
+
+  // ---- tile by tile: 16 MFMAs over the slice, the partial (tokens × rows) into LDS ----------------------------------
+  auto tile_mma = [&](const uint4 (&u)[KW], const uint4 sv, int jt) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int cc = 0; cc < KW; ++cc) {
+      const uint32_t word = (c0 & 4) ? (cc < 2 ? sv.z : sv.w) : (cc < 2 ? sv.x : sv.y);
+      const f32x2 f = (cc & 1) ? __builtin_amdgcn_cvt_pk_f32_fp8((int)word, true)
+                               : __builtin_amdgcn_cvt_pk_f32_fp8((int)word, false);
+      const uint32_t b0 = __float_as_uint(f.x), b1 = __float_as_uint(f.y);
+      const float e0 = __uint_as_float(b0 & 0x7F800000u), e1 = __uint_as_float(b1 & 0x7F800000u);
+      const f16_t m0 = (f16_t)__uint_as_float((b0 & 0x807FFFFFu) | 0x3F800000u);
+      const f16_t m1 = (f16_t)__uint_as_float((b1 & 0x807FFFFFu) | 0x3F800000u);
+      const uint32_t dw[4] = {u[cc].x, u[cc].y, u[cc].z, u[cc].w};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const f16x8 bv = nvfp4_decode8(dw[s], s < 2 ? e0 : e1, s < 2 ? m0 : m1);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, xa[cc][s]), bv, acc, 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);      // decode chunk by chunk: keeps the decoded operands' registers few
+    }
+    float* rp = red + ((jt * S + wave) * 16) * 16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rp[(4 * g + i) * 16 + m_row] = active ? acc[i] * ps[i] : 0.0f;
+  };
+  for (int j = 0; j < ntl; ++j) {
+    tile_mma(u0, s0, j);
+    if (j + 1 < ntl) issue(u0, s0, j + 1);
+  }
+
+  // ---- per (tile, token): the K slices in the gemv_row order, then the epilogue --------------------------------
+  __syncthreads();
+  for (int pi = wave; pi < ntl * cnt; pi += S) {
+    const int jt = pi / cnt, t = pi - jt * cnt;
+    const int tile = tile_of(jt);
+    float v = slice_sum(red + (jt * S * 16 + t) * 16, 16 * 16, S, lane);
+    const int row = tile * 16 + m_row;
+    if (a.ks > 1) {
+      if (g == 0) a.part[((long long)split * a.m + t) * a.n_tiles * 16 + row] = v;
+      continue;
+    }
+    v *= a.row_scale != nullptr ? a.row_scale[row] : 1.0f;
+    const float up = __shfl_down(v, 8, 16);
+    if (g == 0) emit(a, nullptr, cnt, tile, true, m_row, t, v, up);
+  }
+}
+
 // ---- the tile × K-split kernel ----------------------------------------------------------------------------------
 // Work item: (group of TB consecutive 16-row tiles, K split s = chunks [s·kc, min(chunks, (s+1)·kc))). A workgroup
 // of S waves stages the split's activations once — BF16 for the VALU path (M <= 2), per-token power-of-two
@@ -1329,7 +1507,7 @@ __global__ __launch_bounds__(64) void dequant_t16(const uint8_t* w, const float*
 
 // ---- planning --------------------------------------------------------------------------------------------------
 struct Plan {
-  int kernel = 0;          // 1: gemv_row, 2: gemv_tk
+  int kernel = 0;          // 1: gemv_row (gemv_rowp when rt > 1), 2: gemv_tk, 3: gemv_rowm
   int S = 1;               // waves per workgroup
   int kw = 0;              // gemv_row: KW (chunks per wave); gemv_tk: chunks per split
   int tb = 1, ks = 1, depth = 8;   // gemv_tk: tiles per workgroup, K splits, ring depth
@@ -1465,7 +1643,13 @@ Plan plan_row(const mi_gemv_desc* d, int fmt, int chunks, int rows, int n_tiles,
       best = Plan{};
       best.kernel = 1; best.S = S; best.kw = kw; best.ks = ks; best.tb = kc; best.lds_rows = rows; best.row_ld = ld;
       best.row_wave_lds = (int)wl; best.lds_bytes = lds;
-      best.rt = rt; best.G = rt > 1 ? (n_tiles + rt - 1) / rt : n_tiles;
+      best.rt = rt; best.G = n_tiles;
+      if (rt > 1) {                            // every resident slot takes tiles (strided): no idle CUs
+        best.G = force_rt ? (n_tiles + rt - 1) / rt : (int)std::min<long long>(n_tiles, (long long)cu_count() *
+                 std::max(row_blocks_per_cu(fmt, kw, 64 * S, lds1 + 4 * red1), 1));
+        best.rt = (n_tiles + best.G - 1) / best.G;
+        best.lds_bytes = lds1 + (size_t)best.rt * red1;
+      }
     }
   }
   return best;
@@ -1534,6 +1718,59 @@ Plan plan_tk(const mi_gemv_desc* d, int fmt, int chunks, int n_tiles, int groups
   return best;
 }
 
+// gemv_rowm (3 <= M <= 16, NVFP4): waves of 4 chunks over K splits of at most 48 chunks (12 waves); as many
+// workgroups as are resident at once, each over rt tiles
+__global__ void gemv_rowm(Args a);
+int rowm_blocks_per_cu(int threads, size_t lds) {
+  static std::mutex mu;
+  static std::map<std::tuple<int, size_t, int>, int> cache;
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  (void)hipGetLastError();
+  const auto key = std::make_tuple(threads, lds, dev);
+  {
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+  }
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(gemv_rowm), threads, lds) !=
+          hipSuccess || n <= 0) {
+    (void)hipGetLastError();
+    n = std::max(1, 12 / (threads / 64));      // no device: the 3 waves per SIMD of the kernel's VGPR budget
+  }
+  std::lock_guard<std::mutex> lk(mu);
+  cache[key] = n;
+  return n;
+}
+
+Plan plan_rowm(const mi_gemv_desc* d, int chunks, int n_tiles) {
+  Plan best{};
+  if (d->format != FMT_NVFP4 || d->groups || d->gnorm_w || d->m < 3 || d->m > 16 || chunks % 4) return best;
+  int ks = (chunks + 47) / 48;                   // at most 12 waves: the kernel's VGPR budget is 3 waves per SIMD
+  if (d->norm_w && ks > 1) return best;          // the fused norm needs the whole row in one workgroup
+  int force_ks = 0, force_rt = 0;
+  if (const char* env = getenv("MI_GEMV_ROWM")) sscanf(env, "%d,%d", &force_ks, &force_rt);   // tuning sweeps
+  if (force_ks) ks = force_ks;
+  int kc = (chunks + ks - 1) / ks;
+  if (ks > 1) kc = (kc + 7) / 8 * 8;             // splits on scale-group boundaries
+  if (kc > 48 || (ks > 1 && (ks - 1) * kc >= chunks)) return best;
+  const int S = kc / 4;
+  const size_t fixed = (d->norm_w ? (size_t)d->k * 4 : 0) + (size_t)S * 16 * 4;
+  const size_t per_tile = (size_t)S * 16 * 16 * 4;
+  const int per_cu = rowm_blocks_per_cu(64 * S, fixed + 4 * per_tile);
+  const long long slots = std::max<long long>(1, (long long)cu_count() * std::max(per_cu, 1) / ks);
+  // every resident slot takes tiles (strided), so no CU idles for the rounding of tiles per workgroup
+  int G = (int)std::min<long long>(n_tiles, slots);
+  if (force_rt) G = (n_tiles + force_rt - 1) / force_rt;
+  const int rt = (n_tiles + G - 1) / G;
+  const size_t lds = fixed + (size_t)rt * per_tile;
+  if (lds > kMaxLds) return best;
+  best.kernel = 3; best.S = S; best.kw = kc; best.ks = ks; best.rt = rt; best.G = G;
+  best.tb = rt; best.lds_rows = 16; best.lds_bytes = lds;
+  return best;
+}
+
 Plan make_plan(const mi_gemv_desc* d) {
   const int fmt = d->format;
   const int chunks = d->k / chunk_cols(fmt);
@@ -1543,6 +1780,10 @@ Plan make_plan(const mi_gemv_desc* d) {
   const char* fk = getenv("MI_GEMV_KERNEL");                 // "row" / "tk" pins the kernel (tuning sweeps)
   if (rows <= 2 && !(fk && fk[0] == 't')) {
     const Plan p = plan_row(d, fmt, chunks, rows, n_tiles, groups);
+    if (p.kernel) return p;
+  }
+  if (rows > 2 && !(fk && fk[0] == 't')) {
+    const Plan p = plan_rowm(d, chunks, n_tiles);
     if (p.kernel) return p;
   }
   return plan_tk(d, fmt, chunks, n_tiles, groups, rows);
@@ -1583,6 +1824,16 @@ void launch_row_k(const Args& a, const Plan& p, dim3 g, hipStream_t s) {
 
 template <int FMT>
 void launch(const Args& a, const Plan& p, int groups, hipStream_t s) {
+  if (p.kernel == 3) {
+    allow_lds(gemv_rowm);
+    hipLaunchKernelGGL(gemv_rowm, dim3(p.G, 1, p.ks), dim3(64 * p.S), p.lds_bytes, s, a);
+    if (p.ks > 1) {
+      const bool silu = a.epilogue == MI_EPI_SILU_MUL || a.epilogue == MI_EPI_SILU_MUL_ROUNDED;
+      const int n_out = silu ? a.n / 2 : a.n;
+      hipLaunchKernelGGL(gemv_tk_reduce, dim3((n_out + 255) / 256, a.m), dim3(256), 0, s, a);
+    }
+    return;
+  }
   if (p.kernel == 1) {
     const dim3 g(p.G, groups, p.ks);
     if (p.lds_rows == 2) launch_row_k<FMT, 2>(a, p, g, s);
@@ -1653,7 +1904,7 @@ int mi_gemv_plan(const mi_gemv_desc* d, int32_t out[7]) {
   const int groups = d->groups ? d->max_groups : 1;
   out[0] = p.kernel; out[1] = p.S; out[2] = p.kw;
   out[3] = p.kernel == 1 ? p.rt : p.tb; out[4] = p.ks; out[5] = (int32_t)p.lds_bytes;
-  out[6] = (p.kernel == 1 ? p.G * p.ks : (n_tiles + p.tb - 1) / p.tb * p.ks) * groups;
+  out[6] = (p.kernel != 2 ? p.G * p.ks : (n_tiles + p.tb - 1) / p.tb * p.ks) * groups;
   return MI_OK;
 }
 

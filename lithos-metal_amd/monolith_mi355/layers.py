@@ -124,7 +124,9 @@ class GdnDecoderLayer:
         proj, o, h1, act, h2 = self.buffers(h.shape[0])
         out = h2 if out is None else out
         kernels.gemv(self.w_in.packed, h, norm_w=self.norm_w, eps=self.eps, out=proj)
-        defer = proj.stride(0) % 8 == 0            # z must be a 16-byte aligned view for the fused norm
+        # the gated norm rides on the output projection at M <= 2 (gemv_row); at M >= 3 its GEMV kernel keeps the
+        # activations in registers and the norm stays a small kernel of its own. z must be a 16-byte aligned view.
+        defer = h.shape[0] <= 2 and proj.stride(0) % 8 == 0
         cin, cout = self.conv_state[self.parity], self.conv_state[1 - self.parity]
         kernels.gdn_step(proj, cin, cout, self.rec_state, self.rec_state, conv_w=self.conv_w, neg_exp_a=self.neg_exp_a,
                          dt_bias=self.dt_bias, norm_w=self.gdn_norm_w, k_heads=self.hk, v_heads=self.hv, dk=self.dk,

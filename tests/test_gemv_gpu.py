@@ -234,3 +234,29 @@ def test_gemv_gated_head_norm(torch_gpu, fmt, mtok, plan, rng, monkeypatch):
     ref = ON.matmul_acc(xn.reshape(mtok, k), _dequant(m))
     chk = check_against_oracle(got, ref)
     assert chk.ok_rounded(), (fmt, mtok, plan, chk)
+
+
+@pytest.mark.parametrize("mtok", [3, 8, 16])
+@pytest.mark.parametrize("n,k,plan", [(1040, 2048, None), (1040, 2048, "1,3"), (336, 6144, "2,1"),
+                                      (336, 6144, "3,2"), (5120, 17408, None)])
+@pytest.mark.parametrize("epi", [None, "residual", "silu_mul"])
+def test_gemv_rowm_plans(torch_gpu, mtok, n, k, plan, epi, rng, monkeypatch):
+    """The M >= 3 NVFP4 kernel (K slices per wave on the matrix cores, several tiles per workgroup) over forced
+    K splits and tiles per workgroup, against the oracle."""
+    from monolith_mi355 import kernels
+    if plan:
+        monkeypatch.setenv("MI_GEMV_ROWM", plan)
+    m = _matrix("nvfp4", n, k, rng)
+    x = rbf(rng.standard_normal((mtok, k)))
+    res = rbf(rng.standard_normal((mtok, n)))
+    kw = dict(epilogue=epi)
+    if epi == "residual":
+        kw["residual"] = to_dev_bf16(torch_gpu, res)
+    got = from_dev_bf16(kernels.gemv(_upload(torch_gpu, m), to_dev_bf16(torch_gpu, x), **kw))
+    wd = _dequant(m)
+    if epi == "silu_mul":
+        ref = ON.linear(x, wd[np.argsort(ON.interleave_chunks(n // 2, n // 2, 8))], epilogue="silu_mul")
+    else:
+        ref = ON.linear(x, wd, epilogue=epi, residual=res if epi else None)
+    chk = check_against_oracle(got, ref)
+    assert chk.ok_rounded(), (mtok, n, k, plan, epi, chk)
