@@ -59,11 +59,15 @@ def test_gemv_plans_fit_the_hardware(n, k, m):
     out = (C.c_int32 * 7)()
     hip.call("mi_gemv_plan", C.byref(_desc(hip, n=n, k=k, m=m, ldx=k, ldy=n)), out)
     kernel, waves, kw, tb, ks, lds, wgs = list(out)
-    assert kernel == (1 if m <= 2 else 2)                  # gemv_row (VALU) for M <= 2, gemv_tk (MFMA) above
-    assert 1 <= waves <= 16 and kw >= 1 and lds <= 160 * 1024 and wgs >= 1 and ks >= 1 and tb >= 1
     chunks = k // 128
+    # gemv_row (VALU) for M <= 2; gemv_rowm (MFMA, 4-chunk K slices) above when its slices fit, else gemv_tk
+    assert kernel == (1 if m <= 2 else 3 if chunks % 4 == 0 else 2)
+    assert 1 <= waves <= 16 and kw >= 1 and lds <= 160 * 1024 and wgs >= 1 and ks >= 1 and tb >= 1
     if kernel == 1:                                      # K splits of ≤ waves·kw chunks each
         assert kw in (4, 8, 16) and waves * kw * ks >= chunks
+    elif kernel == 3:                                    # 4 chunks per wave, ≤ 12 waves per K split
+        assert waves * 4 == kw and waves <= 12 and ks * kw >= chunks and (ks - 1) * kw < chunks
+        assert tb * wgs >= -(-n // 16) * ks              # tiles per workgroup × workgroups cover every tile
     else:
         assert ks * kw >= chunks and (ks - 1) * kw < chunks
     ws = hip.load().mi_gemv_workspace_bytes(C.byref(_desc(hip, n=n, k=k, m=m, ldx=k, ldy=n)))
