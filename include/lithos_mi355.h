@@ -27,6 +27,8 @@ extern "C" {
 #define MI_FMT_NVFP4 1       /* "nvfp4": E2M1 codes, E4M3 scale per 16, FP32 tensor scale (formats/nvfp4.py) */
 #define MI_FMT_INT4_AFFINE 2 /* "int4_affine": u4 codes, BF16 (scale, bias) per 64 (formats/int4_affine.py) */
 #define MI_FMT_BF16 3        /* "bf16": plain BF16 rows (formats/bf16.py) — the router / gate projections */
+#define MI_FMT_FP8_E4M3 4    /* "fp8_e4m3": E4M3 codes, FP32 tensor scale (formats/fp8_e4m3.py) — M <= 2, or NVFP4-like
+                                dense plans above (no grouped / gated-norm launches) */
 
 /* GEMV epilogues (ops/gemv.py:1-12, nn/linear.py:114-135) */
 #define MI_EPI_NONE 0
@@ -87,7 +89,7 @@ typedef struct mi_gemv_desc {
   int32_t n, k;              /* rows and columns of one matrix (one expert in grouped mode) */
   int32_t m;                 /* tokens (dense mode, 1..16); in grouped mode the token count of the step */
   const void* w;             /* T16 pack; grouped mode: n_experts packs back to back */
-  const float* row_scale;    /* NVFP4 tensor scale per row [experts·n_pad] (the reference's row-scale table); NULL=1 */
+  const float* row_scale;    /* NVFP4 / FP8 tensor scale per row [experts·n_pad] (the reference's row-scale table); NULL=1 */
   const uint16_t* x;         /* BF16 activations, row stride ldx */
   int32_t ldx;
   uint16_t* y;               /* BF16 output, row stride ldy */

@@ -42,13 +42,14 @@ namespace {
 constexpr int FMT_NVFP4 = MI_FMT_NVFP4;
 constexpr int FMT_INT4 = MI_FMT_INT4_AFFINE;
 constexpr int FMT_BF16 = MI_FMT_BF16;
+constexpr int FMT_FP8 = MI_FMT_FP8_E4M3;
 
 constexpr int UNIT_Q = 1152;   // int4 unit: 1024 B codes + 128 B (scale, bias) pairs
 constexpr int UNIT_B = 1024;   // bf16 unit: 16 rows × 32 columns
 constexpr int GROUP_REC = 18;  // grouped-mode record: expert, count, 16 pair ids
 
-__host__ __device__ constexpr int unit_bytes(int fmt) { return fmt == FMT_BF16 ? UNIT_B : UNIT_Q; }
-__host__ __device__ constexpr int chunk_cols(int fmt) { return fmt == FMT_BF16 ? 32 : 128; }
+__host__ __device__ constexpr int unit_bytes(int fmt) { return fmt == FMT_BF16 || fmt == FMT_FP8 ? UNIT_B : UNIT_Q; }
+__host__ __device__ constexpr int chunk_cols(int fmt) { return fmt == FMT_BF16 ? 32 : fmt == FMT_FP8 ? 64 : 128; }
 
 // NVFP4 tile layout: groups of 8 chunks, each [g × 1 KiB codes][scale block: 64 pieces of 16 B (8 B if g <= 4)]
 __host__ __device__ inline int nv_group_chunks(int gi, int chunks) { return min(8, chunks - 8 * gi); }
@@ -142,6 +143,16 @@ __device__ __forceinline__ bf16x2 cvt_fp4x2_bf16(uint32_t dw, float e, int j) {
     case 2: return __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(dw, e, 2);
     default: return __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(dw, e, 3);
   }
+}
+
+// FP8 E4M3: codes 2j, 2j+1 of a dword (hi: 2, 3) → exact BF16 / F16 pairs (scale 1: the tensor scale is the row's)
+__device__ __forceinline__ bf16x2 cvt_fp8x2_bf16(uint32_t dw, bool hi) {
+  return hi ? __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(dw, 1.0f, true) : __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(dw, 1.0f, false);
+}
+__device__ __forceinline__ f16x8 fp8_decode8(uint32_t d0, uint32_t d1) {
+  const f16x2 a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, false), b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, true);
+  const f16x2 c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, false), e = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, true);
+  return f16x8{a.x, a.y, b.x, b.y, c.x, c.y, e.x, e.y};
 }
 
 __device__ __forceinline__ int int4_perm8(int i) { return (i & 1) ? 4 + (i >> 1) : (i >> 1); }
@@ -492,6 +503,25 @@ __global__ __launch_bounds__(KW == 16 ? 640 : 1024) void gemv_row(Args a) {
         acc[t] = fmaf(sca, fmaf(-128.0f, sa[t], d[0][t]), fmaf(bia, sa[t], acc[t]));
         acc[t] = fmaf(scb, fmaf(-128.0f, sb[t], d[1][t]), fmaf(bib, sb[t], acc[t]));
       }
+    } else if constexpr (FMT == FMT_FP8) {
+      uint4 xq[MT][2];                      // the lane's 16 columns 64·cc + 16·g + [0, 16)
+    #pragma unroll
+      for (int t = 0; t < MT; ++t)
+    #pragma unroll
+        for (int h = 0; h < 2; ++h) xq[t][h] = *reinterpret_cast<const uint4*>(xs + (size_t)t * ld + cc * 64 + 16 * g + 8 * h);
+    #pragma unroll
+      for (int q = 0; q < 4; ++q)
+    #pragma unroll
+        for (int hi = 0; hi < 2; ++hi) {
+          const bf16x2 w2 = cvt_fp8x2_bf16(dw[q], hi);   // columns 4q + 2hi, +1 of the lane's 16
+    #pragma unroll
+          for (int t = 0; t < MT; ++t) {
+            const uint4 xv4 = xq[t][q >> 1];
+            const int e = 2 * (q & 1) + hi;
+            const uint32_t xw = e == 0 ? xv4.x : e == 1 ? xv4.y : e == 2 ? xv4.z : xv4.w;
+            acc[t] = __builtin_amdgcn_fdot2_f32_bf16(w2, __builtin_bit_cast(bf16x2, xw), acc[t], false);
+          }
+        }
     } else {
       uint4 xq[MT];
 #pragma unroll
@@ -803,6 +833,25 @@ void gemv_rowp(Args a) {
           acc[t] = fmaf(sca, fmaf(-128.0f, sa[t], d[0][t]), fmaf(bia, sa[t], acc[t]));
           acc[t] = fmaf(scb, fmaf(-128.0f, sb[t], d[1][t]), fmaf(bib, sb[t], acc[t]));
         }
+      } else if constexpr (FMT == FMT_FP8) {
+        uint4 xq[MT][2];                      // the lane's 16 columns 64·cc + 16·g + [0, 16)
+      #pragma unroll
+        for (int t = 0; t < MT; ++t)
+      #pragma unroll
+          for (int h = 0; h < 2; ++h) xq[t][h] = *reinterpret_cast<const uint4*>(xs + (size_t)t * ld + cc * 64 + 16 * g + 8 * h);
+      #pragma unroll
+        for (int q = 0; q < 4; ++q)
+      #pragma unroll
+          for (int hi = 0; hi < 2; ++hi) {
+            const bf16x2 w2 = cvt_fp8x2_bf16(dw[q], hi);   // columns 4q + 2hi, +1 of the lane's 16
+      #pragma unroll
+            for (int t = 0; t < MT; ++t) {
+              const uint4 xv4 = xq[t][q >> 1];
+              const int e = 2 * (q & 1) + hi;
+              const uint32_t xw = e == 0 ? xv4.x : e == 1 ? xv4.y : e == 2 ? xv4.z : xv4.w;
+              acc[t] = __builtin_amdgcn_fdot2_f32_bf16(w2, __builtin_bit_cast(bf16x2, xw), acc[t], false);
+            }
+          }
       } else {
         uint4 xq[MT];
   #pragma unroll
@@ -867,8 +916,11 @@ void gemv_rowp(Args a) {
 // issues tile j + 1 as soon as tile j is consumed (the operands leave no VGPRs for a second tile in flight). A
 // tile's K slices meet in LDS after the last tile, in the gemv_row order.
 // LDS: nw[K] (fused norm) | stat[S][16] | red[rt][S][16 tokens][16 rows].
+template <int FMT>
 __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
-  constexpr int KW = 4, KC = 128;
+  constexpr int KW = 4, KC = chunk_cols(FMT);
+  constexpr int SPC = KC / 32;                  // MFMA steps per chunk: the lane's KC/4 columns, 8 per step
+  static_assert(FMT == FMT_NVFP4 || FMT == FMT_FP8, "gemv_rowm: NVFP4 or FP8");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -888,36 +940,40 @@ __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
   float* red = stat + S * 16;                                                  // [rt][S][16][16]
 
   // ---- the first tile's weights, then the activations ------------------------------------------------------------
-  const long long c0_off = nv_code_off(c0);
+  const long long c0_off = FMT == FMT_NVFP4 ? nv_code_off(c0) : (long long)c0 * UNIT_B;
   auto issue = [&](uint4 (&u)[KW], uint4& sv, int j) {
     const uint8_t* tbase = wmat + (long long)tile_of(j) * a.tile_stride;
-    const int gi = c0 >> 3;
-    const uint8_t* p = tbase + nv_scale_off(gi, a.chunks);
-    if (nv_piece(nv_group_chunks(gi, a.chunks)) == 16) {
-      sv = *reinterpret_cast<const uint4*>(p + 16 * lane);
+    if constexpr (FMT == FMT_NVFP4) {
+      const int gi = c0 >> 3;
+      const uint8_t* p = tbase + nv_scale_off(gi, a.chunks);
+      if (nv_piece(nv_group_chunks(gi, a.chunks)) == 16) {
+        sv = *reinterpret_cast<const uint4*>(p + 16 * lane);
+      } else {
+        const uint2 t = *reinterpret_cast<const uint2*>(p + 8 * lane);
+        sv = uint4{t.x, t.y, 0u, 0u};
+      }
     } else {
-      const uint2 t = *reinterpret_cast<const uint2*>(p + 8 * lane);
-      sv = uint4{t.x, t.y, 0u, 0u};
+      sv = uint4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
-    for (int cc = 0; cc < KW; ++cc) u[cc] = *reinterpret_cast<const uint4*>(tbase + c0_off + cc * 1024 + 16 * lane);
+    for (int cc = 0; cc < KW; ++cc) u[cc] = *reinterpret_cast<const uint4*>(tbase + c0_off + cc * 1024 + 16 * lane);  // units of 1 KiB codes
   };
   uint4 u0[KW], s0;
   issue(u0, s0, 0);
 
-  // x[token m_row][c0·128 + cc·128 + 32g + 8s + (0..7)]: the A operand of step s of chunk cc
+  // x[token m_row][c0·KC + cc·KC + (KC/4)·g + 8s + (0..7)]: the A operand of step s of chunk cc
   const bool real = m_row < cnt;
-  uint4 xa[KW][4];
-  const uint16_t* xrow = a.x + (long long)(real ? m_row : 0) * a.ldx + c0 * KC + 32 * g;
+  uint4 xa[KW][SPC];
+  const uint16_t* xrow = a.x + (long long)(real ? m_row : 0) * a.ldx + c0 * KC + (KC / 4) * g;
 #pragma unroll
   for (int cc = 0; cc < KW; ++cc)
 #pragma unroll
-    for (int s = 0; s < 4; ++s) xa[cc][s] = *reinterpret_cast<const uint4*>(xrow + cc * KC + 8 * s);
+    for (int s = 0; s < SPC; ++s) xa[cc][s] = *reinterpret_cast<const uint4*>(xrow + cc * KC + 8 * s);
   if (!real) {                                // padding token rows: zero operands (their loads read row 0)
 #pragma unroll
     for (int cc = 0; cc < KW; ++cc)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) xa[cc][s] = uint4{0u, 0u, 0u, 0u};
+      for (int s = 0; s < SPC; ++s) xa[cc][s] = uint4{0u, 0u, 0u, 0u};
   }
 
   if (a.norm_w) {
@@ -928,7 +984,7 @@ __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
 #pragma unroll
     for (int cc = 0; cc < KW; ++cc)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
+      for (int s = 0; s < SPC; ++s) {
         const uint32_t vv[4] = {xa[cc][s].x, xa[cc][s].y, xa[cc][s].z, xa[cc][s].w};
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -945,8 +1001,8 @@ __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
 #pragma unroll
     for (int cc = 0; cc < KW; ++cc)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const float* wv = nws + (c0 + cc) * KC + 32 * g + 8 * s;
+      for (int s = 0; s < SPC; ++s) {
+        const float* wv = nws + (c0 + cc) * KC + (KC / 4) * g + 8 * s;
         const float4 w0 = *reinterpret_cast<const float4*>(wv), w1 = *reinterpret_cast<const float4*>(wv + 4);
         const float ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
         uint32_t* vv = reinterpret_cast<uint32_t*>(&xa[cc][s]);
@@ -964,7 +1020,7 @@ __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
 #pragma unroll
   for (int cc = 0; cc < KW; ++cc)
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s = 0; s < SPC; ++s) {
       const uint32_t vv[4] = {xa[cc][s].x, xa[cc][s].y, xa[cc][s].z, xa[cc][s].w};
 #pragma unroll
       for (int q = 0; q < 4; ++q)
@@ -977,7 +1033,7 @@ __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
 #pragma unroll
   for (int cc = 0; cc < KW; ++cc)             // in place: xa now holds the F16 operands
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s = 0; s < SPC; ++s) {
       uint32_t* vv = reinterpret_cast<uint32_t*>(&xa[cc][s]);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -995,18 +1051,26 @@ __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int cc = 0; cc < KW; ++cc) {
-      const uint32_t word = (c0 & 4) ? (cc < 2 ? sv.z : sv.w) : (cc < 2 ? sv.x : sv.y);
-      const f32x2 f = (cc & 1) ? __builtin_amdgcn_cvt_pk_f32_fp8((int)word, true)
-                               : __builtin_amdgcn_cvt_pk_f32_fp8((int)word, false);
-      const uint32_t b0 = __float_as_uint(f.x), b1 = __float_as_uint(f.y);
-      const float e0 = __uint_as_float(b0 & 0x7F800000u), e1 = __uint_as_float(b1 & 0x7F800000u);
-      const f16_t m0 = (f16_t)__uint_as_float((b0 & 0x807FFFFFu) | 0x3F800000u);
-      const f16_t m1 = (f16_t)__uint_as_float((b1 & 0x807FFFFFu) | 0x3F800000u);
       const uint32_t dw[4] = {u[cc].x, u[cc].y, u[cc].z, u[cc].w};
+      if constexpr (FMT == FMT_NVFP4) {
+        const uint32_t word = (c0 & 4) ? (cc < 2 ? sv.z : sv.w) : (cc < 2 ? sv.x : sv.y);
+        const f32x2 f = (cc & 1) ? __builtin_amdgcn_cvt_pk_f32_fp8((int)word, true)
+                                 : __builtin_amdgcn_cvt_pk_f32_fp8((int)word, false);
+        const uint32_t b0 = __float_as_uint(f.x), b1 = __float_as_uint(f.y);
+        const float e0 = __uint_as_float(b0 & 0x7F800000u), e1 = __uint_as_float(b1 & 0x7F800000u);
+        const f16_t m0 = (f16_t)__uint_as_float((b0 & 0x807FFFFFu) | 0x3F800000u);
+        const f16_t m1 = (f16_t)__uint_as_float((b1 & 0x807FFFFFu) | 0x3F800000u);
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const f16x8 bv = nvfp4_decode8(dw[s], s < 2 ? e0 : e1, s < 2 ? m0 : m1);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, xa[cc][s]), bv, acc, 0, 0, 0);
+        for (int s = 0; s < 4; ++s) {
+          const f16x8 bv = nvfp4_decode8(dw[s], s < 2 ? e0 : e1, s < 2 ? m0 : m1);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, xa[cc][s]), bv, acc, 0, 0, 0);
+        }
+      } else {                                  // FP8: the lane's 16 codes, 8 per step
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          const f16x8 bv = fp8_decode8(dw[2 * s], dw[2 * s + 1]);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, xa[cc][s]), bv, acc, 0, 0, 0);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);      // decode chunk by chunk: keeps the decoded operands' registers few
     }
@@ -1497,6 +1561,12 @@ __global__ __launch_bounds__(64) void dequant_t16(const uint8_t* w, const float*
       const float sc = bf16_bits_to_f32(pr & 0xFFFFu), bi = bf16_bits_to_f32(pr >> 16);
       for (int i = 0; i < 8; ++i) o[c * 128 + 32 * s + 8 * g + int4_perm8(i)] = fmaf((float)v[i], sc, bi);
     }
+  } else if constexpr (FMT == FMT_FP8) {
+    const float rs = row_scale ? row_scale[row] : 1.0f;
+    for (int s = 0; s < 2; ++s) {
+      const f16x8 v = fp8_decode8(dw[2 * s], dw[2 * s + 1]);
+      for (int i = 0; i < 8; ++i) o[c * 64 + 16 * g + 8 * s + i] = (float)v[i] * rs;
+    }
   } else {
     for (int i = 0; i < 8; ++i) {
       const uint32_t h = (dw[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
@@ -1518,7 +1588,8 @@ struct Plan {
 
 int check_desc(const mi_gemv_desc* d) {
   MI_REQUIRE(d, "mi_gemv: null descriptor");
-  MI_REQUIRE(d->format == FMT_NVFP4 || d->format == FMT_INT4 || d->format == FMT_BF16, "mi_gemv: unknown format %d",
+  MI_REQUIRE(d->format == FMT_NVFP4 || d->format == FMT_INT4 || d->format == FMT_BF16 || d->format == FMT_FP8,
+             "mi_gemv: unknown format %d",
              d->format);
   const int kc = chunk_cols(d->format);
   MI_REQUIRE(d->n > 0 && d->k > 0 && d->k % kc == 0, "mi_gemv: k=%d must be a positive multiple of %d", d->k, kc);
@@ -1536,7 +1607,8 @@ int check_desc(const mi_gemv_desc* d) {
   MI_REQUIRE(!d->norm_w || ((uintptr_t)d->norm_w & 15) == 0, "mi_gemv: norm_w must be 16-byte aligned");
   if (d->gnorm_w) {
     MI_REQUIRE(!d->norm_w, "mi_gemv: norm_w and gnorm_w are exclusive");
-    MI_REQUIRE(d->format != FMT_BF16, "mi_gemv: the gated head norm is built for 128-column chunks (NVFP4, INT4)");
+    MI_REQUIRE(d->format == FMT_NVFP4 || d->format == FMT_INT4,
+               "mi_gemv: the gated head norm is built for 128-column chunks (NVFP4, INT4)");
     MI_REQUIRE(d->k % 128 == 0, "mi_gemv: gated head norm needs k %% 128 == 0");
     MI_REQUIRE(d->gnorm_z && ((uintptr_t)d->gnorm_z & 15) == 0 && d->ld_gnorm_z % 8 == 0 && d->ld_gnorm_z >= d->k,
                "mi_gemv: gnorm_z must be 16-byte aligned with ld_gnorm_z %% 8 == 0 and >= k");
@@ -1571,6 +1643,7 @@ int row_blocks_query(int fmt, int kw, int threads, size_t lds) {
   MI_ROW_K(FMT_NVFP4, 4) MI_ROW_K(FMT_NVFP4, 8) MI_ROW_K(FMT_NVFP4, 16)
   MI_ROW_K(FMT_INT4, 4) MI_ROW_K(FMT_INT4, 8) MI_ROW_K(FMT_INT4, 16)
   MI_ROW_K(FMT_BF16, 4) MI_ROW_K(FMT_BF16, 8) MI_ROW_K(FMT_BF16, 16)
+  MI_ROW_K(FMT_FP8, 4) MI_ROW_K(FMT_FP8, 8) MI_ROW_K(FMT_FP8, 16)
 #undef MI_ROW_K
   int n = 0;
   if (k && hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, threads, lds) == hipSuccess && n > 0) return n;
@@ -1668,6 +1741,7 @@ int tk_lds(int fmt, int rows, int kc, bool mf) {
 // re-reads (workgroups × split bytes), split K its partials and a second launch; a fused norm needs one split.
 Plan plan_tk(const mi_gemv_desc* d, int fmt, int chunks, int n_tiles, int groups, int rows) {
   Plan best{};
+  if (fmt == FMT_FP8) return best;            // no FP8 path in gemv_tk
   const bool mf = rows > 2;
   int force[4] = {0, 0, 0, 0};           // MI_GEMV_TK="ks,tb,S,D" pins a plan (tuning sweeps)
   if (const char* env = getenv("MI_GEMV_TK")) sscanf(env, "%d,%d,%d,%d", &force[0], &force[1], &force[2], &force[3]);
@@ -1720,21 +1794,23 @@ Plan plan_tk(const mi_gemv_desc* d, int fmt, int chunks, int n_tiles, int groups
 
 // gemv_rowm (3 <= M <= 16, NVFP4): waves of 4 chunks over K splits of at most 48 chunks (12 waves); as many
 // workgroups as are resident at once, each over rt tiles
-__global__ void gemv_rowm(Args a);
-int rowm_blocks_per_cu(int threads, size_t lds) {
+template <int FMT> __global__ void gemv_rowm(Args a);
+int rowm_blocks_per_cu(int fmt, int threads, size_t lds) {
   static std::mutex mu;
   static std::map<std::tuple<int, size_t, int>, int> cache;
   int dev = 0;
   (void)hipGetDevice(&dev);
   (void)hipGetLastError();
-  const auto key = std::make_tuple(threads, lds, dev);
+  const auto key = std::make_tuple(threads * 8 + fmt, lds, dev);
   {
     std::lock_guard<std::mutex> lk(mu);
     auto it = cache.find(key);
     if (it != cache.end()) return it->second;
   }
   int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(gemv_rowm), threads, lds) !=
+  const void* kern = fmt == FMT_FP8 ? reinterpret_cast<const void*>(gemv_rowm<FMT_FP8>)
+                                    : reinterpret_cast<const void*>(gemv_rowm<FMT_NVFP4>);
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, threads, lds) !=
           hipSuccess || n <= 0) {
     (void)hipGetLastError();
     n = std::max(1, 12 / (threads / 64));      // no device: the 3 waves per SIMD of the kernel's VGPR budget
@@ -1746,7 +1822,9 @@ int rowm_blocks_per_cu(int threads, size_t lds) {
 
 Plan plan_rowm(const mi_gemv_desc* d, int chunks, int n_tiles) {
   Plan best{};
-  if (d->format != FMT_NVFP4 || d->groups || d->gnorm_w || d->m < 3 || d->m > 16 || chunks % 4) return best;
+  if ((d->format != FMT_NVFP4 && d->format != FMT_FP8) || d->groups || d->gnorm_w || d->m < 3 || d->m > 16 ||
+      chunks % 4)
+    return best;
   int ks = (chunks + 47) / 48;                   // at most 12 waves: the kernel's VGPR budget is 3 waves per SIMD
   if (d->norm_w && ks > 1) return best;          // the fused norm needs the whole row in one workgroup
   int force_ks = 0, force_rt = 0;
@@ -1758,7 +1836,7 @@ Plan plan_rowm(const mi_gemv_desc* d, int chunks, int n_tiles) {
   const int S = kc / 4;
   const size_t fixed = (d->norm_w ? (size_t)d->k * 4 : 0) + (size_t)S * 16 * 4;
   const size_t per_tile = (size_t)S * 16 * 16 * 4;
-  const int per_cu = rowm_blocks_per_cu(64 * S, fixed + 4 * per_tile);
+  const int per_cu = rowm_blocks_per_cu(d->format, 64 * S, fixed + 4 * per_tile);
   const long long slots = std::max<long long>(1, (long long)cu_count() * std::max(per_cu, 1) / ks);
   // every resident slot takes tiles (strided), so no CU idles for the rounding of tiles per workgroup
   int G = (int)std::min<long long>(n_tiles, slots);
@@ -1824,15 +1902,17 @@ void launch_row_k(const Args& a, const Plan& p, dim3 g, hipStream_t s) {
 
 template <int FMT>
 void launch(const Args& a, const Plan& p, int groups, hipStream_t s) {
-  if (p.kernel == 3) {
-    allow_lds(gemv_rowm);
-    hipLaunchKernelGGL(gemv_rowm, dim3(p.G, 1, p.ks), dim3(64 * p.S), p.lds_bytes, s, a);
-    if (p.ks > 1) {
-      const bool silu = a.epilogue == MI_EPI_SILU_MUL || a.epilogue == MI_EPI_SILU_MUL_ROUNDED;
-      const int n_out = silu ? a.n / 2 : a.n;
-      hipLaunchKernelGGL(gemv_tk_reduce, dim3((n_out + 255) / 256, a.m), dim3(256), 0, s, a);
+  if constexpr (FMT == FMT_NVFP4 || FMT == FMT_FP8) {
+    if (p.kernel == 3) {
+      allow_lds(gemv_rowm<FMT>);
+      hipLaunchKernelGGL(gemv_rowm<FMT>, dim3(p.G, 1, p.ks), dim3(64 * p.S), p.lds_bytes, s, a);
+      if (p.ks > 1) {
+        const bool silu = a.epilogue == MI_EPI_SILU_MUL || a.epilogue == MI_EPI_SILU_MUL_ROUNDED;
+        const int n_out = silu ? a.n / 2 : a.n;
+        hipLaunchKernelGGL(gemv_tk_reduce, dim3((n_out + 255) / 256, a.m), dim3(256), 0, s, a);
+      }
+      return;
     }
-    return;
   }
   if (p.kernel == 1) {
     const dim3 g(p.G, groups, p.ks);
@@ -1845,14 +1925,16 @@ void launch(const Args& a, const Plan& p, int groups, hipStream_t s) {
     }
     return;
   }
-  const dim3 g((a.n_tiles + p.tb - 1) / p.tb, p.ks, groups);
-  if (p.lds_rows > 2) launch_tk_d<FMT, 16>(a, p, g, s);
-  else if (p.lds_rows == 2) launch_tk_d<FMT, 2>(a, p, g, s);
-  else launch_tk_d<FMT, 1>(a, p, g, s);
-  if (p.ks > 1) {
-    const bool silu = a.epilogue == MI_EPI_SILU_MUL || a.epilogue == MI_EPI_SILU_MUL_ROUNDED;
-    const int n_out = silu ? a.n / 2 : a.n;
-    hipLaunchKernelGGL(gemv_tk_reduce, dim3((n_out + 255) / 256, a.m), dim3(256), 0, s, a);
+  if constexpr (FMT != FMT_FP8) {                // FP8 runs on gemv_row / gemv_rowm only (the planner's choice)
+    const dim3 g((a.n_tiles + p.tb - 1) / p.tb, p.ks, groups);
+    if (p.lds_rows > 2) launch_tk_d<FMT, 16>(a, p, g, s);
+    else if (p.lds_rows == 2) launch_tk_d<FMT, 2>(a, p, g, s);
+    else launch_tk_d<FMT, 1>(a, p, g, s);
+    if (p.ks > 1) {
+      const bool silu = a.epilogue == MI_EPI_SILU_MUL || a.epilogue == MI_EPI_SILU_MUL_ROUNDED;
+      const int n_out = silu ? a.n / 2 : a.n;
+      hipLaunchKernelGGL(gemv_tk_reduce, dim3((n_out + 255) / 256, a.m), dim3(256), 0, s, a);
+    }
   }
 }
 
@@ -1883,7 +1965,7 @@ extern "C" {
 
 size_t mi_pack_bytes(int32_t format, int32_t n, int32_t k) {
   if (n <= 0 || k <= 0) return 0;
-  if (format != FMT_NVFP4 && format != FMT_INT4 && format != FMT_BF16) return 0;
+  if (format != FMT_NVFP4 && format != FMT_INT4 && format != FMT_BF16 && format != FMT_FP8) return 0;
   const int kc = chunk_cols(format);
   if (k % kc) return 0;
   return (size_t)((n + 15) / 16) * (size_t)tile_bytes(format, k / kc);
@@ -1955,6 +2037,7 @@ int mi_gemv(const mi_gemv_desc* d, void* stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (d->format == FMT_NVFP4) launch<FMT_NVFP4>(a, p, groups, s);
   else if (d->format == FMT_INT4) launch<FMT_INT4>(a, p, groups, s);
+  else if (d->format == FMT_FP8) launch<FMT_FP8>(a, p, groups, s);
   else launch<FMT_BF16>(a, p, groups, s);
   MI_TRY_HIP(hipGetLastError(), "gemv launch");
   return MI_OK;
@@ -1962,7 +2045,8 @@ int mi_gemv(const mi_gemv_desc* d, void* stream) {
 
 int mi_dequant(int32_t format, const void* w, const float* row_scale, int32_t n, int32_t k, float* out, void* stream) {
   MI_REQUIRE(w && out, "mi_dequant: null pointer");
-  MI_REQUIRE(format == FMT_NVFP4 || format == FMT_INT4 || format == FMT_BF16, "mi_dequant: unknown format");
+  MI_REQUIRE(format == FMT_NVFP4 || format == FMT_INT4 || format == FMT_BF16 || format == FMT_FP8,
+             "mi_dequant: unknown format");
   const int kc = chunk_cols(format);
   MI_REQUIRE(n > 0 && k > 0 && k % kc == 0, "mi_dequant: bad shape");
   const int chunks = k / kc, tiles = (n + 15) / 16;
@@ -1972,6 +2056,8 @@ int mi_dequant(int32_t format, const void* w, const float* row_scale, int32_t n,
     hipLaunchKernelGGL(dequant_t16<FMT_NVFP4>, dim3(tiles * chunks), dim3(64), 0, s, wb, row_scale, n, k, chunks, out);
   else if (format == FMT_INT4)
     hipLaunchKernelGGL(dequant_t16<FMT_INT4>, dim3(tiles * chunks), dim3(64), 0, s, wb, row_scale, n, k, chunks, out);
+  else if (format == FMT_FP8)
+    hipLaunchKernelGGL(dequant_t16<FMT_FP8>, dim3(tiles * chunks), dim3(64), 0, s, wb, row_scale, n, k, chunks, out);
   else
     hipLaunchKernelGGL(dequant_t16<FMT_BF16>, dim3(tiles * chunks), dim3(64), 0, s, wb, row_scale, n, k, chunks, out);
   MI_TRY_HIP(hipGetLastError(), "dequant_t16 launch");

@@ -202,7 +202,32 @@ class BF16:
         return bf16_to_f32(spec.tensors["weight"])
 
 
-FORMATS = {"nvfp4": NVFP4(), "int4_affine": INT4Affine(), "bf16": BF16()}
+class FP8E4M3:
+    """FP8 E4M3 codes with one FP32 tensor scale (ModelOpt ``FP8``: ``weight`` F8_E4M3 ``[N, K]``, ``weight_scale``
+    F32 ``[]``; ``input_scale`` ignored) — ``formats/fp8_e4m3.py:1-79``."""
+    name = "fp8_e4m3"
+    bytes_per_weight = 1.0
 
-__all__ = ["DequantSpec", "FORMATS", "NVFP4", "INT4Affine", "BF16", "e4m3_encode", "e4m3_decode", "e2m1_encode",
+    def unpack(self, tensors: Mapping[str, Any], *, shape: Tuple[int, int]) -> DequantSpec:
+        n, k = shape
+        w = np.asarray(tensors["weight"])
+        w = w.view(np.uint8) if w.dtype.itemsize == 1 else w.astype(np.uint8)
+        s = float(np.asarray(tensors["weight_scale"], np.float32).reshape(()))
+        if w.shape != (n, k):
+            raise ValueError(f"fp8_e4m3: weight {w.shape} does not match shape {shape}")
+        return DequantSpec("fp8_e4m3", (n, k), {"weight": w}, {"weight_scale": s})
+
+    def quantize(self, w) -> DequantSpec:
+        w = np.asarray(w, dtype=np.float32)
+        amax = float(np.abs(w).max()) or 1.0
+        s = np.float32(amax / E4M3_MAX)
+        return DequantSpec("fp8_e4m3", w.shape, {"weight": e4m3_encode(w / s)}, {"weight_scale": float(s)})
+
+    def dequantize(self, spec: DequantSpec) -> np.ndarray:
+        return (e4m3_decode(spec.tensors["weight"]) * np.float32(spec.params["weight_scale"])).astype(np.float32)
+
+
+FORMATS = {"nvfp4": NVFP4(), "int4_affine": INT4Affine(), "bf16": BF16(), "fp8_e4m3": FP8E4M3()}
+
+__all__ = ["DequantSpec", "FORMATS", "NVFP4", "INT4Affine", "BF16", "FP8E4M3", "e4m3_encode", "e4m3_decode", "e2m1_encode",
            "e2m1_decode", "f32_to_bf16", "bf16_to_f32", "to_bf16_values"]

@@ -15,6 +15,8 @@ A matrix ``[N, K]`` is cut into 16-row tiles (the last one zero-padded) and 128-
   ``128·c + 32·s + 8·g + [0, 8)``; bytes ``[1024 + 8·r, +8)`` the BF16 (scale, bias) pairs of groups ``2c`` and
   ``2c + 1`` of row ``r`` (scale in the low half, as the reference's pairs, ``formats/int4_affine.py:460``).
 * BF16 (1024 B): lane ``l``'s 16 bytes are the 8 values of row ``r`` at columns ``32·c + 8·g + [0, 8)``.
+* FP8 E4M3 (1024 B, 64-column chunks): lane ``l``'s 16 bytes are the codes of row ``r`` at columns
+  ``64·c + 16·g + [0, 16)``; the FP32 tensor scale is the per-row table, as for NVFP4.
 
 The byte count per weight is the format's own (0.5625 B for NVFP4 and INT4) except for the scale block of a short
 last NVFP4 group (K not a multiple of 1024 columns), padded to 8 or 16 bytes per lane.
@@ -32,15 +34,15 @@ from .fp import bf16_to_f32, f32_to_bf16
 
 UNIT_Q = 1152
 UNIT_B = 1024
-FORMAT_IDS = {"nvfp4": 1, "int4_affine": 2, "bf16": 3}
+FORMAT_IDS = {"nvfp4": 1, "int4_affine": 2, "bf16": 3, "fp8_e4m3": 4}
 
 
 def chunk_cols(fmt: str) -> int:
-    return 32 if fmt == "bf16" else 128
+    return {"bf16": 32, "fp8_e4m3": 64}.get(fmt, 128)
 
 
 def unit_bytes(fmt: str) -> int:
-    return UNIT_B if fmt == "bf16" else UNIT_Q
+    return UNIT_B if fmt in ("bf16", "fp8_e4m3") else UNIT_Q
 
 
 def nvfp4_groups(chunks: int):
@@ -68,7 +70,7 @@ class PackInfo:
     n_tiles: int
     chunks: int
     nbytes: int
-    row_scale: Optional[np.ndarray] = None     # NVFP4: per-row tensor scale [n_tiles·16] float32
+    row_scale: Optional[np.ndarray] = None     # NVFP4 / FP8: per-row tensor scale [n_tiles·16] float32
 
 
 def _pad_rows(a: np.ndarray, rows: int) -> np.ndarray:
@@ -80,8 +82,8 @@ def _pad_rows(a: np.ndarray, rows: int) -> np.ndarray:
 
 
 def pack(spec: DequantSpec, row_scale: Optional[np.ndarray] = None) -> Tuple[np.ndarray, PackInfo]:
-    """``(bytes as uint8 array, PackInfo)`` of the T16 layout. ``row_scale`` overrides the NVFP4 per-row tensor scale
-    (stacked slabs whose parts carry different ``weight_scale_2``)."""
+    """``(bytes as uint8 array, PackInfo)`` of the T16 layout. ``row_scale`` overrides the NVFP4 / FP8 per-row tensor
+    scale (stacked slabs whose parts carry different tensor scales)."""
     fmt = spec.format
     n, k = spec.shape
     kc = chunk_cols(fmt)
@@ -118,6 +120,14 @@ def pack(spec: DequantSpec, row_scale: Optional[np.ndarray] = None) -> Tuple[np.
         w = _pad_rows(np.asarray(spec.tensors["weight"], np.uint16), rows)           # [rows, K]
         data = np.ascontiguousarray(w.reshape(nt, 16, c, 4, 8).transpose(0, 2, 3, 1, 4)).reshape(nt, c, 512).view(np.uint8)
         info = PackInfo(fmt, n, k, nt, c, data.size)
+    elif fmt == "fp8_e4m3":
+        w = _pad_rows(np.asarray(spec.tensors["weight"], np.uint8), rows)            # [rows, K]
+        data = np.ascontiguousarray(w.reshape(nt, 16, c, 4, 16).transpose(0, 2, 3, 1, 4)).reshape(nt, c, 1024)
+        if row_scale is None:
+            row_scale = np.full(n, spec.params["weight_scale"], np.float32)
+        rs = np.zeros(rows, np.float32)
+        rs[:n] = np.asarray(row_scale, np.float32)
+        info = PackInfo(fmt, n, k, nt, c, data.size, rs)
     else:
         raise ValueError(f"T16 pack: unknown format {fmt!r}")
     return np.ascontiguousarray(data).reshape(-1), info
@@ -148,6 +158,10 @@ def unpack(data: np.ndarray, info: PackInfo) -> DequantSpec:
         pairs = pairs.reshape(nt * 16, k // 64, 2)
         return DequantSpec("int4_affine", (n, k), {"weight": w[:n], "scales": bf16_to_f32(pairs[:n, :, 0]),
                                                    "biases": bf16_to_f32(pairs[:n, :, 1])}, {"group": 64})
+    if info.format == "fp8_e4m3":
+        w = d.reshape(nt, c, 4, 16, 16).transpose(0, 3, 1, 2, 4).reshape(nt * 16, k)
+        s = float(info.row_scale[0]) if info.row_scale is not None and n else 1.0
+        return DequantSpec("fp8_e4m3", (n, k), {"weight": w[:n]}, {"weight_scale": s})
     d = d.reshape(nt, c, UNIT_B).view(np.uint16).reshape(nt, c, 4, 16, 8)
     w = d.transpose(0, 3, 1, 2, 4).reshape(nt * 16, k)
     return DequantSpec("bf16", (n, k), {"weight": w[:n]})

@@ -25,7 +25,7 @@ def _torch():
 
 @dataclass
 class PackedWeight:
-    """A T16 pack resident in HBM: ``data`` uint8 ``[experts·nbytes]``, NVFP4 ``row_scale`` float32
+    """A T16 pack resident in HBM: ``data`` uint8 ``[experts·nbytes]``, NVFP4 / FP8 ``row_scale`` float32
     ``[experts·n_pad]``."""
 
     format: str

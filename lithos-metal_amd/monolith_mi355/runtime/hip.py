@@ -17,7 +17,7 @@ LIB_NAME = "libmi355.so"
 _PKG_ROOT = Path(__file__).resolve().parents[2]          # lithos-metal_amd/
 LIB_PATH = Path(os.environ.get("LITHOS_MI355_LIB", _PKG_ROOT / "lib" / LIB_NAME))
 
-MI_FMT = {"nvfp4": 1, "int4_affine": 2, "bf16": 3}
+MI_FMT = {"nvfp4": 1, "int4_affine": 2, "bf16": 3, "fp8_e4m3": 4}
 MI_EPI = {None: 0, "none": 0, "residual": 1, "silu_mul": 2, "silu_mul_rounded": 3}
 
 

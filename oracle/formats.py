@@ -5,7 +5,9 @@ A quantized matrix is a plain dict of checkpoint-shaped arrays, in the reference
 * ``nvfp4``: ``weight`` U8 ``[N, K/2]`` (E2M1 codes, low nibble first), ``weight_scale`` U8 ``[N, K/16]`` (E4M3),
   ``weight_scale_2`` float (the FP32 tensor scale) — ``formats/nvfp4.py:122-161``;
 * ``int4_affine``: ``weight`` U8 ``[N, K/2]`` (unsigned codes, low nibble first), ``scales`` / ``biases`` F32
-  ``[N, K/64]`` holding BF16-valued numbers — ``formats/int4_affine.py:73-119``.
+  ``[N, K/64]`` holding BF16-valued numbers — ``formats/int4_affine.py:73-119``;
+* ``fp8_e4m3``: ``weight`` U8 ``[N, K]`` (E4M3 codes), ``weight_scale`` float (the FP32 tensor scale) —
+  ``formats/fp8_e4m3.py:62-79``.
 """
 
 from __future__ import annotations
@@ -109,12 +111,33 @@ def int4_random(n: int, k: int, rng: np.random.Generator) -> dict:
             "biases": bf16_to_f32(f32_to_bf16(biases))}
 
 
+# ---- FP8 E4M3 with a tensor scale ----------------------------------------------------------------------------------
+def fp8_dequantize(m: dict) -> np.ndarray:
+    """``w = e4m3(code) · weight_scale`` in float32, one rounding (``formats/fp8_e4m3.py:69-70``)."""
+    return (e4m3_to_f32(m["weight"]) * np.float32(m["weight_scale"])).astype(np.float32)
+
+
+def fp8_quantize(w: np.ndarray) -> dict:
+    """The reference quantizer (``formats/fp8_e4m3.py:72-76``): ``s = amax / 448``, codes = E4M3 of ``w / s``."""
+    w = np.asarray(w, dtype=np.float32)
+    amax = float(np.abs(w).max()) or 1.0
+    s = np.float32(amax / E4M3_MAX)
+    return {"format": "fp8_e4m3", "weight": f32_to_e4m3(w / s), "weight_scale": float(s)}
+
+
+def fp8_random(n: int, k: int, rng: np.random.Generator, s: float = 0.02 / E4M3_MAX * 8) -> dict:
+    """Random finite codes (every code but the NaNs 0x7F / 0xFF) and a tensor scale."""
+    codes = rng.integers(0, 254, size=(n, k), dtype=np.uint8)
+    codes = np.where(codes >= 0x7F, codes + 1, codes).astype(np.uint8)          # skip 0x7F; 0xFF is never drawn
+    return {"format": "fp8_e4m3", "weight": codes, "weight_scale": float(np.float32(s))}
+
+
 def dequantize(m: dict) -> np.ndarray:
-    return nvfp4_dequantize(m) if m["format"] == "nvfp4" else int4_dequantize(m)
+    return {"nvfp4": nvfp4_dequantize, "fp8_e4m3": fp8_dequantize}.get(m["format"], int4_dequantize)(m)
 
 
 def quantize(fmt: str, w: np.ndarray) -> dict:
-    return nvfp4_quantize(w) if fmt == "nvfp4" else int4_quantize(w)
+    return {"nvfp4": nvfp4_quantize, "fp8_e4m3": fp8_quantize}.get(fmt, int4_quantize)(w)
 
 
 def stack_rows(mats) -> dict:
@@ -127,6 +150,9 @@ def stack_rows(mats) -> dict:
         out["weight_scale"] = np.concatenate([m["weight_scale"] for m in mats], axis=0)
         out["row_scale"] = np.concatenate([np.full(m["weight"].shape[0], m["weight_scale_2"], np.float32) for m in mats])
         out["weight_scale_2"] = 1.0
+    elif fmt == "fp8_e4m3":
+        out["row_scale"] = np.concatenate([np.full(m["weight"].shape[0], m["weight_scale"], np.float32) for m in mats])
+        out["weight_scale"] = 1.0
     else:
         out["scales"] = np.concatenate([m["scales"] for m in mats], axis=0)
         out["biases"] = np.concatenate([m["biases"] for m in mats], axis=0)
@@ -138,12 +164,14 @@ def dequantize_rows(m: dict) -> np.ndarray:
     if m["format"] == "nvfp4" and "row_scale" in m:
         base = dict(m, weight_scale_2=1.0)
         return (nvfp4_dequantize(base) * m["row_scale"][:, None].astype(np.float32)).astype(np.float32)
+    if m["format"] == "fp8_e4m3" and "row_scale" in m:
+        return (e4m3_to_f32(m["weight"]) * m["row_scale"][:, None].astype(np.float32)).astype(np.float32)
     return dequantize(m)
 
 
 def permute_rows(m: dict, perm: np.ndarray) -> dict:
     out = dict(m)
     for key in ("weight", "weight_scale", "scales", "biases", "row_scale"):
-        if key in m:
+        if key in m and np.ndim(m[key]) > 0:                  # per-row arrays; a tensor scale stays as it is
             out[key] = np.ascontiguousarray(np.asarray(m[key])[perm])
     return out

@@ -19,6 +19,8 @@ def spec_of(m: dict) -> DequantSpec:
         k = m["weight"].shape[1] * 2
         return DequantSpec("int4_affine", (n, k), {"weight": m["weight"], "scales": m["scales"], "biases": m["biases"]},
                            {"group": 64})
+    if m["format"] == "fp8_e4m3":
+        return DequantSpec("fp8_e4m3", m["weight"].shape, {"weight": m["weight"]}, {"weight_scale": m["weight_scale"]})
     return DequantSpec("bf16", m["weight"].shape, {"weight": m["weight"]})
 
 

@@ -1,7 +1,7 @@
 """The HIP GEMV / skinny GEMM against the oracle (the reference's ``tests/kernels/test_gemv_T.py`` strategy):
 
 * dequantized weights decoded by the kernels' own decode path are bit-identical to the oracle's ``dequantize``
-  (all three formats, including every E4M3 block-scale code);
+  (all four formats, including every E4M3 block-scale code and every finite FP8 code, signed zero included);
 * ``y = x·Wᵀ`` within the reference's leaf gate (``OracleCheck.ok``: ≤ 2 BF16 ULP at the output RMS, relative error
   < 1e-4) against a float64 matmul of the exact dequantized matrix, for M = 1, 2, 8, 16, ragged N, the residual and
   silu·mul epilogues (rounded chains gated by ``ok_rounded``) and the fused input RMSNorm;
@@ -23,6 +23,8 @@ pytestmark = pytest.mark.gpu
 def _matrix(fmt, n, k, rng):
     if fmt == "nvfp4":
         return OF.nvfp4_random(n, k, rng)
+    if fmt == "fp8_e4m3":
+        return OF.fp8_random(n, k, rng)
     if fmt == "int4_affine":
         return OF.int4_random(n, k, rng)
     from oracle.fp import f32_to_bf16
@@ -41,7 +43,7 @@ def _upload(torch, m):
     return kernels.upload(spec_of(m))
 
 
-@pytest.mark.parametrize("fmt", ["nvfp4", "int4_affine", "bf16"])
+@pytest.mark.parametrize("fmt", ["nvfp4", "int4_affine", "bf16", "fp8_e4m3"])
 @pytest.mark.parametrize("n,k", [(16, 128), (37, 512), (300, 1024)])
 def test_dequant_bit_exact(torch_gpu, fmt, n, k, rng):
     from monolith_mi355 import kernels
@@ -76,7 +78,7 @@ def _run(torch, m, x, **kw):
     return y.cpu().numpy()
 
 
-@pytest.mark.parametrize("fmt", ["nvfp4", "int4_affine", "bf16"])
+@pytest.mark.parametrize("fmt", ["nvfp4", "int4_affine", "bf16", "fp8_e4m3"])
 @pytest.mark.parametrize("mtok", [1, 2, 8, 16])
 @pytest.mark.parametrize("n,k", [(48, 256), (77, 1024), (1040, 2048)])
 def test_gemv_matches_oracle(torch_gpu, fmt, mtok, n, k, rng):
@@ -91,7 +93,7 @@ def test_gemv_matches_oracle(torch_gpu, fmt, mtok, n, k, rng):
     assert np.array_equal(yb, rbf(got))
 
 
-@pytest.mark.parametrize("fmt", ["nvfp4", "int4_affine"])
+@pytest.mark.parametrize("fmt", ["nvfp4", "int4_affine", "fp8_e4m3"])
 @pytest.mark.parametrize("mtok", [1, 8])
 def test_gemv_residual(torch_gpu, fmt, mtok, rng):
     n, k = 160, 1024
@@ -107,7 +109,7 @@ def test_gemv_residual(torch_gpu, fmt, mtok, rng):
     assert chk.ok_rounded() and chk.max_ulp_elementwise <= 1, chk
 
 
-@pytest.mark.parametrize("fmt", ["nvfp4", "int4_affine"])
+@pytest.mark.parametrize("fmt", ["nvfp4", "int4_affine", "fp8_e4m3"])
 @pytest.mark.parametrize("rounded", [False, True])
 @pytest.mark.parametrize("mtok", [1, 8])
 def test_gemv_silu_mul(torch_gpu, fmt, rounded, mtok, rng):
@@ -115,13 +117,15 @@ def test_gemv_silu_mul(torch_gpu, fmt, rounded, mtok, rng):
     gate, up = _matrix(fmt, inter, k, rng), _matrix(fmt, inter, k, rng)
     if fmt == "nvfp4":
         up["weight_scale_2"] = gate["weight_scale_2"] * 1.5              # distinct tensor scales per part
+    if fmt == "fp8_e4m3":
+        up["weight_scale"] = gate["weight_scale"] * 1.5
     slab = OF.stack_rows([gate, up])
     perm = ON.interleave_chunks(inter, inter, 8)
     slab = OF.permute_rows(slab, perm)
     from monolith_mi355 import kernels
     from monolith_mi355.formats import DequantSpec
-    spec = spec_of(dict(slab, weight_scale_2=1.0))
-    w = kernels.upload(spec, row_scales=[slab["row_scale"]] if fmt == "nvfp4" else None)
+    spec = spec_of(dict(slab, weight_scale=1.0) if fmt == "fp8_e4m3" else dict(slab, weight_scale_2=1.0))
+    w = kernels.upload(spec, row_scales=[slab["row_scale"]] if fmt in ("nvfp4", "fp8_e4m3") else None)
     x = rbf(rng.standard_normal((mtok, k)))
     epi = "silu_mul_rounded" if rounded else "silu_mul"
     got = from_dev_bf16(kernels.gemv(w, to_dev_bf16(torch_gpu, x), epilogue=epi))
@@ -132,7 +136,7 @@ def test_gemv_silu_mul(torch_gpu, fmt, rounded, mtok, rng):
     assert chk.ok_rounded(), chk
 
 
-@pytest.mark.parametrize("fmt", ["nvfp4", "int4_affine", "bf16"])
+@pytest.mark.parametrize("fmt", ["nvfp4", "int4_affine", "bf16", "fp8_e4m3"])
 @pytest.mark.parametrize("mtok", [1, 8])
 def test_gemv_fused_norm(torch_gpu, fmt, mtok, rng):
     n, k = 200, 2048
@@ -175,7 +179,7 @@ def test_gemv_repeat_is_bit_identical(torch_gpu, rng):
     assert torch_gpu.equal(a, b)
 
 
-@pytest.mark.parametrize("fmt", ["nvfp4", "int4_affine", "bf16"])
+@pytest.mark.parametrize("fmt", ["nvfp4", "int4_affine", "bf16", "fp8_e4m3"])
 @pytest.mark.parametrize("n,k", [(1040, 2048), (336, 1664)])
 @pytest.mark.parametrize("epi", [None, "residual", "silu_mul"])
 def test_gemv_tiles_per_workgroup(torch_gpu, fmt, n, k, epi, rng, monkeypatch):
@@ -236,17 +240,18 @@ def test_gemv_gated_head_norm(torch_gpu, fmt, mtok, plan, rng, monkeypatch):
     assert chk.ok_rounded(), (fmt, mtok, plan, chk)
 
 
+@pytest.mark.parametrize("fmt", ["nvfp4", "fp8_e4m3"])
 @pytest.mark.parametrize("mtok", [3, 8, 16])
 @pytest.mark.parametrize("n,k,plan", [(1040, 2048, None), (1040, 2048, "1,3"), (336, 6144, "2,1"),
                                       (336, 6144, "3,2"), (5120, 17408, None)])
 @pytest.mark.parametrize("epi", [None, "residual", "silu_mul"])
-def test_gemv_rowm_plans(torch_gpu, mtok, n, k, plan, epi, rng, monkeypatch):
+def test_gemv_rowm_plans(torch_gpu, fmt, mtok, n, k, plan, epi, rng, monkeypatch):
     """The M >= 3 NVFP4 kernel (K slices per wave on the matrix cores, several tiles per workgroup) over forced
     K splits and tiles per workgroup, against the oracle."""
     from monolith_mi355 import kernels
     if plan:
         monkeypatch.setenv("MI_GEMV_ROWM", plan)
-    m = _matrix("nvfp4", n, k, rng)
+    m = _matrix(fmt, n, k, rng)
     x = rbf(rng.standard_normal((mtok, k)))
     res = rbf(rng.standard_normal((mtok, n)))
     kw = dict(epilogue=epi)
@@ -260,3 +265,16 @@ def test_gemv_rowm_plans(torch_gpu, mtok, n, k, plan, epi, rng, monkeypatch):
         ref = ON.linear(x, wd, epilogue=epi, residual=res if epi else None)
     chk = check_against_oracle(got, ref)
     assert chk.ok_rounded(), (mtok, n, k, plan, epi, chk)
+
+
+def test_fp8_dequant_every_code(torch_gpu):
+    """Every finite E4M3 code (signed zero, subnormals, ±448) decodes bit-exactly; the tensor scale multiplies once."""
+    from monolith_mi355 import kernels
+    from oracle.fp import e4m3_to_f32
+    codes = np.array([c for c in range(256) if c & 0x7F != 0x7F], np.uint8)
+    w = np.resize(codes, (32, 256)).astype(np.uint8)
+    for s in (1.0, 0.0123):
+        m = {"format": "fp8_e4m3", "weight": w, "weight_scale": float(np.float32(s))}
+        got = kernels.dequant(_upload(torch_gpu, m)).cpu().numpy()
+        ref = (e4m3_to_f32(w) * np.float32(s)).astype(np.float32)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), s

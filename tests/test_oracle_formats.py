@@ -184,3 +184,61 @@ def test_t16_pack_round_trip_and_unit_map(fmt, n, k):
         if info.chunks > 1:      # chunk 1 of the group: the next two bytes of the same piece
             assert np.array_equal(tile[g0 * 1024 + piece * 21 + 2: g0 * 1024 + piece * 21 + 4],
                                   spec.tensors["weight_scale"][21, 10:12])
+
+
+# ---- FP8 E4M3 (formats/fp8_e4m3.py) --------------------------------------------------------------------------------
+def test_fp8_dequantize_is_code_times_scale():
+    """``w = e4m3(code) · s`` with one rounding; e4m3 itself is pinned by the code-table tests above."""
+    from oracle.fp import e4m3_to_f32
+    codes = np.arange(256, dtype=np.uint8).reshape(4, 64)
+    s = 0.0123
+    got = OF.fp8_dequantize({"format": "fp8_e4m3", "weight": codes, "weight_scale": s})
+    fin = (codes & 0x7F) != 0x7F
+    ref = e4m3_to_f32(codes).astype(np.float64) * np.float64(np.float32(s))
+    assert np.array_equal(got[fin], ref[fin].astype(np.float32))          # one rounding of the exact product
+    assert np.signbit(got[0, 0]) == False and np.signbit(got[2, 0]) == True and got[2, 0] == 0.0   # ±0
+
+
+def test_fp8_quantize_closed_form(rng):
+    """s = amax / 448 exactly; the largest |w| maps to ±448 (code 0x7E / 0xFE); every code is the nearest E4M3 of
+    w / s (within half an E4M3 step); quantize∘dequantize is idempotent on the codes."""
+    from oracle.fp import e4m3_to_f32
+    w = (rng.standard_normal((64, 128)) * 0.05).astype(np.float32)
+    m = OF.fp8_quantize(w)
+    amax = float(np.abs(w).max())
+    assert m["weight_scale"] == float(np.float32(amax / 448.0))
+    i = np.unravel_index(np.argmax(np.abs(w)), w.shape)
+    assert m["weight"][i] in (0x7E, 0xFE)
+    v = e4m3_to_f32(m["weight"])
+    x = w / np.float32(m["weight_scale"])
+    step = np.maximum(2.0 ** (np.floor(np.log2(np.maximum(np.abs(x), 2.0 ** -6))) - 3), 2.0 ** -9)
+    assert np.all(np.abs(v - x) <= step / 2 + 1e-12)
+    again = OF.fp8_quantize(OF.fp8_dequantize(m))
+    assert np.array_equal(again["weight"], m["weight"])
+
+
+def test_fp8_host_format_matches_oracle(rng):
+    from monolith_mi355.formats import FORMATS
+    w = (rng.standard_normal((32, 256)) * 0.03).astype(np.float32)
+    spec = FORMATS["fp8_e4m3"].quantize(w)
+    m = OF.fp8_quantize(w)
+    assert np.array_equal(spec.tensors["weight"], m["weight"]) and spec.params["weight_scale"] == m["weight_scale"]
+    assert np.array_equal(FORMATS["fp8_e4m3"].dequantize(spec), OF.fp8_dequantize(m))
+
+
+@pytest.mark.parametrize("n,k", [(16, 64), (37, 512), (300, 1024)])
+def test_fp8_pack_round_trip(n, k, rng):
+    """The T16 FP8 pack: lane l of chunk c holds row l % 16, columns 64c + 16(l // 16) + [0, 16); unpack inverts it."""
+    from monolith_mi355.formats import pack as P
+    from monolith_mi355.formats import DequantSpec
+    m = OF.fp8_random(n, k, rng)
+    data, info = P.pack(DequantSpec("fp8_e4m3", (n, k), {"weight": m["weight"]}, {"weight_scale": m["weight_scale"]}))
+    assert data.size == P.pack_bytes("fp8_e4m3", n, k) == -(-n // 16) * (k // 64) * 1024
+    back = P.unpack(data, info)
+    assert np.array_equal(back.tensors["weight"], m["weight"]) and back.params["weight_scale"] == m["weight_scale"]
+    t, c, lane = (n - 1) // 16, (k // 64) - 1, 37
+    r, g = lane % 16, lane // 16
+    unit = data.reshape(-1, k // 64, 1024)[t, c]
+    row = t * 16 + r
+    if row < n:
+        assert np.array_equal(unit[16 * lane: 16 * lane + 16], m["weight"][row, 64 * c + 16 * g: 64 * c + 16 * g + 16])
