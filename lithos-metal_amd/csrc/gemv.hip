@@ -1015,17 +1015,18 @@ __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
         __builtin_amdgcn_sched_barrier(0);    // one step's weights at a time (the operands already hold 64 VGPRs)
       }
   }
-  // F16 operands: per token, 2^-p brings the slice max into [2^14, 2^15) (exact within 2^28 of the max)
-  float mx = 0.0f;
+  // F16 operands: per token, 2^-p brings the slice max into [2^14, 2^15) (exact within 2^28 of the max). The max
+  // is taken on the BF16 magnitudes as integers (same order for finite values), so no FP32 copy of the slice exists.
+  uint32_t mb = 0;
 #pragma unroll
   for (int cc = 0; cc < KW; ++cc)
 #pragma unroll
     for (int s = 0; s < SPC; ++s) {
       const uint32_t vv[4] = {xa[cc][s].x, xa[cc][s].y, xa[cc][s].z, xa[cc][s].w};
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        mx = fmaxf(mx, fmaxf(fabsf(bf16_bits_to_f32(vv[q] & 0xFFFFu)), fabsf(bf16_bits_to_f32(vv[q] >> 16))));
+      for (int q = 0; q < 4; ++q) mb = max(mb, max(vv[q] & 0x7FFFu, (vv[q] >> 16) & 0x7FFFu));
     }
+  float mx = bf16_bits_to_f32(mb);
   mx = max_xor32(max_xor16(mx));
   const int pe = mx == 0.0f ? 0 : (int)((__float_as_uint(mx) >> 23) & 0xFF) - 127 - 14;
   const float inv = __uint_as_float((uint32_t)(127 - pe) << 23);
@@ -1040,6 +1041,7 @@ __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
         const f16x2 h = {(f16_t)(bf16_bits_to_f32(vv[q] & 0xFFFFu) * inv), (f16_t)(bf16_bits_to_f32(vv[q] >> 16) * inv)};
         vv[q] = __builtin_bit_cast(uint32_t, h);
       }
+      __builtin_amdgcn_sched_barrier(0);      // one operand at a time: no FP32 copies of the whole slice
     }
   // the output rows of lane l are tokens 4g + i: their scales from the lanes that hold those tokens' A rows
   float ps[4];
