@@ -7,7 +7,8 @@ a Gated DeltaNet mixer (16 key / 48 value heads of 128, conv 4; in_proj 16480×5
 and the NVFP4 gated MLP of BASELINE configs[1] (gate|up 2×17408×5120 with silu·mul, down 5120×17408 with the
 residual). ``value`` is that layer's algorithmic HBM bytes ÷ its step time at M = 1. Beside it: the same layer at
 M = 8, the gated-GQA layer (24 q / 4 KV heads of 128, int8 KV cache at a 32K context; configs[2]) at M = 1 and 8,
-and the MLP alone.
+and the MLP alone; and the FP8 E4M3 GEMV (the 27B checkpoint's format for its mixer projections) at the
+GDN in_proj shape with its fused norm, M = 1 and 8.
 
 One step = one layer forward over one token batch. Weights, states and KV caches are resident in HBM before the
 timed region; the step rotates over ``--layers`` distinct layer instances (≥ 2 GB in all), so the 256 MB MALL
@@ -42,7 +43,7 @@ def parse():
     p.add_argument("--layers", type=int, default=10, help="distinct layer instances the steps rotate over")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--only", choices=["gdn", "attn", "mlp", "gateup", "copy"], default=None,
+    p.add_argument("--only", choices=["gdn", "attn", "mlp", "gateup", "fp8", "copy"], default=None,
                    help="time one workload only (profiling runs; copy = a 256 MiB device copy, the counter reference)")
     return p.parse_args()
 
@@ -123,6 +124,25 @@ def main():
             out["gateup_m1"] = (ms, 34816 * 5120 * 9 // 16 + 5120 * 2 + 17408 * 2)
         del gdn
         torch.cuda.empty_cache()
+        if args.only in (None, "fp8"):
+            # the 27B checkpoint's mixer projections are FP8 E4M3: the GDN in_proj shape (16480×5120) with its fused
+            # norm, M = 1 and 8; random finite codes drawn straight in the packed layout, a per-row tensor scale
+            n8, k8 = 16480, 5120
+            nb = (n8 + 15) // 16 * 16 * k8
+            mats = []
+            for i in range(n):
+                c = torch.randint(0, 253, (nb,), dtype=torch.int16, generator=gen, device=dev)
+                c = (c + (c >= 0x7F).to(torch.int16)).to(torch.uint8)            # every code but the NaNs
+                rs = torch.full(((n8 + 15) // 16 * 16,), 1e-3, dtype=torch.float32, device=dev)
+                mats.append(kernels.PackedWeight("fp8_e4m3", n8, k8, 1, c, rs))
+            nw = 1.0 + torch.randn(k8, generator=gen, device=dev) * 0.1
+            for m in (1, 8):
+                x = xin(m)
+                y8 = torch.empty(m, n8, dtype=torch.bfloat16, device=dev)
+                ms = timed_graph(lambda i: kernels.gemv(mats[i % n], x, norm_w=nw, out=y8), args.steps, args.warmup,
+                                 stream)
+                out[f"fp8_m{m}"] = (ms, nb + m * k8 * 2 + m * n8 * 2)
+            del mats
         if args.only in (None, "attn"):
             attn = [AttnDecoderLayer(seed=40 + i, ctx=CTX, device=dev) for i in range(n)]
             for layer in attn:
@@ -181,6 +201,8 @@ def main():
         "attn_layer_ctx32k_m8": entry("attn_m8", 8),
         "mlp_m1": entry("mlp_m1", 1),
         "mlp_m8": entry("mlp_m8", 8),
+        "fp8_in_proj_m1": entry("fp8_m1", 1),
+        "fp8_in_proj_m8": entry("fp8_m8", 8),
         "roofline": {"kernel": "gemv_row (NVFP4 gate|up 34816x5120, silu_mul, M=1)", "bound": "hbm",
                      "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,

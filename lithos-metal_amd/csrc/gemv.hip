@@ -907,9 +907,10 @@ void gemv_rowp(Args a) {
   }
 }
 
-// ---- gemv_rowm: 3 <= M <= 16, NVFP4 -----------------------------------------------------------------------------
+// ---- gemv_rowm: 3 <= M <= 16, NVFP4 and FP8 --------------------------------------------------------------------
 // The gemv_row wave layout on the matrix cores, over several tiles per workgroup. Workgroup = S waves over tiles
-// blockIdx.x + j·G (j < ntl) and K split blockIdx.z; wave w owns chunks [c0, c0 + 4) of every one of them. The
+// blockIdx.x + j·G (j < ntl) and K split blockIdx.z; wave w owns a 512-column slice (4 NVFP4 / 8 FP8 chunks) of
+// every one of them. The
 // wave's activations for those chunks stay in VGPRs for the whole launch as the F16 A operands of
 // v_mfma_f32_16x16x32_f16 (token = A row; each token power-of-two scaled into F16 range over the wave's slice;
 // normalized first when the input norm is fused); the weights are the B operand, decoded exactly to F16. Each wave
@@ -918,7 +919,7 @@ void gemv_rowp(Args a) {
 // LDS: nw[K] (fused norm) | stat[S][16] | red[rt][S][16 tokens][16 rows].
 template <int FMT>
 __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
-  constexpr int KW = 4, KC = chunk_cols(FMT);
+  constexpr int KC = chunk_cols(FMT), KW = 512 / KC;   // a wave's slice is 512 columns: 4 NVFP4 / 8 FP8 chunks
   constexpr int SPC = KC / 32;                  // MFMA steps per chunk: the lane's KC/4 columns, 8 per step
   static_assert(FMT == FMT_NVFP4 || FMT == FMT_FP8, "gemv_rowm: NVFP4 or FP8");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -930,8 +931,9 @@ __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
   const int cnt = a.m;
   const int split = blockIdx.z;
   const int c0_raw = split * a.kc + wave * KW;
-  const bool active = c0_raw < min(a.chunks, (split + 1) * a.kc);   // slices are whole: kc % 4 == 0, chunks % 4 == 0
+  const bool active = c0_raw < min(a.chunks, (split + 1) * a.kc);
   const int c0 = active ? c0_raw : 0;
+  const int kw = active ? min(KW, min(a.chunks, (split + 1) * a.kc) - c0) : 0;   // chunks this wave holds (≤ KW)
   const int g = lane >> 4, m_row = lane & 15;
   const uint8_t* wmat = a.w;
   auto tile_of = [&](int j) { return (int)blockIdx.x + j * G; };
@@ -956,7 +958,8 @@ __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
       sv = uint4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
-    for (int cc = 0; cc < KW; ++cc) u[cc] = *reinterpret_cast<const uint4*>(tbase + c0_off + cc * 1024 + 16 * lane);  // units of 1 KiB codes
+    for (int cc = 0; cc < KW; ++cc)             // units of 1 KiB codes
+      if (cc < kw) u[cc] = *reinterpret_cast<const uint4*>(tbase + c0_off + cc * 1024 + 16 * lane);
   };
   uint4 u0[KW], s0;
   issue(u0, s0, 0);
@@ -968,7 +971,8 @@ __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
 #pragma unroll
   for (int cc = 0; cc < KW; ++cc)
 #pragma unroll
-    for (int s = 0; s < SPC; ++s) xa[cc][s] = *reinterpret_cast<const uint4*>(xrow + cc * KC + 8 * s);
+    for (int s = 0; s < SPC; ++s)
+      xa[cc][s] = cc < kw ? *reinterpret_cast<const uint4*>(xrow + cc * KC + 8 * s) : uint4{0u, 0u, 0u, 0u};
   if (!real) {                                // padding token rows: zero operands (their loads read row 0)
 #pragma unroll
     for (int cc = 0; cc < KW; ++cc)
@@ -987,10 +991,8 @@ __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
       for (int s = 0; s < SPC; ++s) {
         const uint32_t vv[4] = {xa[cc][s].x, xa[cc][s].y, xa[cc][s].z, xa[cc][s].w};
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float lo = bf16_bits_to_f32(vv[q] & 0xFFFFu), hi = bf16_bits_to_f32(vv[q] >> 16);
-          sq = fmaf(lo, lo, fmaf(hi, hi, sq));
-        }
+        for (int q = 0; q < 4; ++q)           // x0² + x1² straight from the BF16 pair: no FP32 copies of the slice
+          sq = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, vv[q]), __builtin_bit_cast(bf16x2, vv[q]), sq, false);
       }
     sq = add_xor32(add_xor16(active ? sq : 0.0f));    // the four lanes of token m_row
     if (g == 0) stat[wave * 16 + m_row] = sq;
@@ -1002,6 +1004,7 @@ __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
     for (int cc = 0; cc < KW; ++cc)
 #pragma unroll
       for (int s = 0; s < SPC; ++s) {
+        if (cc >= kw) break;
         const float* wv = nws + (c0 + cc) * KC + (KC / 4) * g + 8 * s;
         const float4 w0 = *reinterpret_cast<const float4*>(wv), w1 = *reinterpret_cast<const float4*>(wv + 4);
         const float ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
@@ -1053,6 +1056,7 @@ __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int cc = 0; cc < KW; ++cc) {
+      if (cc >= kw) break;
       const uint32_t dw[4] = {u[cc].x, u[cc].y, u[cc].z, u[cc].w};
       if constexpr (FMT == FMT_NVFP4) {
         const uint32_t word = (c0 & 4) ? (cc < 2 ? sv.z : sv.w) : (cc < 2 ? sv.x : sv.y);
@@ -1794,7 +1798,7 @@ Plan plan_tk(const mi_gemv_desc* d, int fmt, int chunks, int n_tiles, int groups
   return best;
 }
 
-// gemv_rowm (3 <= M <= 16, NVFP4): waves of 4 chunks over K splits of at most 48 chunks (12 waves); as many
+// gemv_rowm (3 <= M <= 16, NVFP4 / FP8): waves of 512 columns over K splits of at most 12 waves; as many
 // workgroups as are resident at once, each over rt tiles
 template <int FMT> __global__ void gemv_rowm(Args a);
 int rowm_blocks_per_cu(int fmt, int threads, size_t lds) {
@@ -1825,17 +1829,18 @@ int rowm_blocks_per_cu(int fmt, int threads, size_t lds) {
 Plan plan_rowm(const mi_gemv_desc* d, int chunks, int n_tiles) {
   Plan best{};
   if ((d->format != FMT_NVFP4 && d->format != FMT_FP8) || d->groups || d->gnorm_w || d->m < 3 || d->m > 16 ||
-      chunks % 4)
+      (d->format == FMT_NVFP4 && chunks % 4))     // NVFP4 slices start on half scale groups
     return best;
-  int ks = (chunks + 47) / 48;                   // at most 12 waves: the kernel's VGPR budget is 3 waves per SIMD
+  const int kw = 512 / chunk_cols(d->format);    // chunks per wave (512 columns)
+  int ks = (chunks + 12 * kw - 1) / (12 * kw);   // at most 12 waves: the kernel's VGPR budget is 3 waves per SIMD
   if (d->norm_w && ks > 1) return best;          // the fused norm needs the whole row in one workgroup
   int force_ks = 0, force_rt = 0;
   if (const char* env = getenv("MI_GEMV_ROWM")) sscanf(env, "%d,%d", &force_ks, &force_rt);   // tuning sweeps
   if (force_ks) ks = force_ks;
   int kc = (chunks + ks - 1) / ks;
-  if (ks > 1) kc = (kc + 7) / 8 * 8;             // splits on scale-group boundaries
-  if (kc > 48 || (ks > 1 && (ks - 1) * kc >= chunks)) return best;
-  const int S = kc / 4;
+  if (ks > 1) kc = (kc + 7) / 8 * 8;             // splits on scale-group boundaries (whole waves for FP8)
+  if (kc > 12 * kw || (ks > 1 && (ks - 1) * kc >= chunks)) return best;
+  const int S = (kc + kw - 1) / kw;
   const size_t fixed = (d->norm_w ? (size_t)d->k * 4 : 0) + (size_t)S * 16 * 4;
   const size_t per_tile = (size_t)S * 16 * 16 * 4;
   const int per_cu = rowm_blocks_per_cu(d->format, 64 * S, fixed + 4 * per_tile);
