@@ -39,19 +39,6 @@ class PackedWeight:
     def n_pad(self) -> int:
         return -(-self.n // 16) * 16
 
-    def v_codes_token_major(self):
-        """``v_codes`` as ``[kv, ctx_max, D]`` (a copy)."""
-        torch = _torch()
-        kv, nb, d, b = self.v_codes.shape
-        idx = torch.as_tensor(self.V_POS, device=self.v_codes.device)
-        return self.v_codes.index_select(3, idx).permute(0, 1, 3, 2).reshape(kv, nb * b, d)
-
-    def set_v_token_major(self, codes):
-        """Store ``codes [kv, ctx_max, D]`` int8 into the blocked ``v_codes``."""
-        kv, nb, d, b = self.v_codes.shape
-        blocks = codes.reshape(kv, nb, b, d).permute(0, 1, 3, 2)           # [kv, nb, D, key]
-        self.v_codes[..., torch_index(self.V_POS, self.v_codes.device)] = blocks
-
     @property
     def nbytes(self) -> int:
         return int(self.data.numel())
