@@ -153,6 +153,10 @@ typedef struct mi_gdn_desc {
   float eps;
   int32_t defer_norm;        /* 1: y gets the BF16 read-out o and the gated RMSNorm is left to the consumer (the
                                 output projection's mi_gemv, gnorm_* fields); 0: y is the normed, gated output */
+  int32_t commit;            /* 1: the speculative commit pass (ops/gdn.py `gdn_commit`, gdn_mixer.metal:331-347):
+                                replay the committed tokens from the step's input state (rec_in != rec_out) into the
+                                output slot; no read-out (y may be NULL) */
+  const int32_t* t_dev;      /* device-resident token count 0..t (the accept scan's committed count), or NULL = t */
 } mi_gdn_desc;
 int mi_gdn_step(const mi_gdn_desc* d, void* stream);
 

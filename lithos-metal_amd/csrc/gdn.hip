@@ -38,6 +38,8 @@ struct GdnArgs {
   float* rec_out;
   uint16_t* y; int ldy;
   float eps;
+  int commit;               // the speculative commit pass: state only, no read-out
+  const int32_t* t_dev;     // device-resident token count (<= t), or null
 };
 
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + __expf(-x)); }
@@ -52,7 +54,7 @@ __global__ __launch_bounds__(64 * (WAVES + CONV_WAVES)) void gdn_step(GdnArgs a)
   __shared__ float beta_s[TMAX], eg_s[TMAX];
   const int h = blockIdx.x, sl = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int T = a.t;
+  const int T = a.t_dev ? min(max(*a.t_dev, 0), a.t) : a.t;
   const int rep = a.hv / a.hk;
   const int kh = h / rep;
   const int key_dim = a.hk * DK;
@@ -165,7 +167,7 @@ __global__ __launch_bounds__(64 * (WAVES + CONV_WAVES)) void gdn_step(GdnArgs a)
       o2 = fmaf(s[i + 2], qq[i + 2], o2); o3 = fmaf(s[i + 3], qq[i + 3], o3);
     }
     const float o = quad16_sum((o0 + o1) + (o2 + o3));
-    if (rg == 0) a.y[(long long)t * a.ldy + h * DV + col] = f32_to_bf16_bits(o);   // the BF16 read-out
+    if (rg == 0 && !a.commit) a.y[(long long)t * a.ldy + h * DV + col] = f32_to_bf16_bits(o);   // the BF16 read-out
   }
   float* sout = a.rec_out + (long long)h * DK * DV;
 #pragma unroll
@@ -176,6 +178,7 @@ __global__ __launch_bounds__(64 * (WAVES + CONV_WAVES)) void gdn_step(GdnArgs a)
 // (head, token)
 __global__ __launch_bounds__(64) void gdn_gated_norm(GdnArgs a) {
   const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+  if (a.t_dev && t >= *a.t_dev) return;
   uint16_t* y = a.y + (long long)t * a.ldy + h * DV;
   const float v0 = bf16_bits_to_f32(y[lane]), v1 = bf16_bits_to_f32(y[lane + 64]);
   const float r = 1.0f / sqrtf(wave_sum(v0 * v0 + v1 * v1) / (float)DV + a.eps);
@@ -197,8 +200,10 @@ extern "C" int mi_gdn_step(const mi_gdn_desc* d, void* stream) {
   MI_REQUIRE(d->dk == DK && d->dv == DV && d->conv_width == CW, "mi_gdn_step: built for dk=dv=%d, conv width %d", DK, CW);
   MI_REQUIRE(d->k_heads > 0 && d->v_heads > 0 && d->v_heads % d->k_heads == 0, "mi_gdn_step: v_heads must be a multiple of k_heads");
   MI_REQUIRE(d->proj && d->conv_w && d->neg_exp_a && d->dt_bias && d->norm_w && d->conv_in && d->conv_out && d->rec_in &&
-             d->rec_out && d->y, "mi_gdn_step: null pointer");
+             d->rec_out && (d->y || d->commit), "mi_gdn_step: null pointer");
   MI_REQUIRE(d->conv_in != d->conv_out, "mi_gdn_step: conv_in and conv_out must be distinct buffers (shared key heads)");
+  MI_REQUIRE(!d->commit || d->rec_in != d->rec_out, "mi_gdn_step: the commit pass replays from the step's input state: "
+             "rec_in and rec_out must be distinct");
   GdnArgs a{};
   a.t = d->t; a.hk = d->k_heads; a.hv = d->v_heads;
   a.proj = d->proj; a.ldp = d->ld_proj; a.z_off = d->z_off; a.q_off = d->q_off; a.k_off = d->k_off; a.v_off = d->v_off;
@@ -206,10 +211,11 @@ extern "C" int mi_gdn_step(const mi_gdn_desc* d, void* stream) {
   a.conv_w = d->conv_w; a.neg_exp_a = d->neg_exp_a; a.dt_bias = d->dt_bias; a.norm_w = d->norm_w;
   a.conv_in = d->conv_in; a.conv_out = d->conv_out; a.rec_in = d->rec_in; a.rec_out = d->rec_out;
   a.y = d->y; a.ldy = d->ld_y; a.eps = d->eps;
+  a.commit = d->commit; a.t_dev = d->t_dev;
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(gdn_step, dim3(d->v_heads, NSLICE), dim3(64 * (WAVES + CONV_WAVES)), 0, s, a);
   MI_TRY_HIP(hipGetLastError(), "gdn_step launch");
-  if (!d->defer_norm) {
+  if (!d->defer_norm && !d->commit) {
     hipLaunchKernelGGL(gdn_gated_norm, dim3(d->v_heads, d->t), dim3(64), 0, s, a);
     MI_TRY_HIP(hipGetLastError(), "gdn_gated_norm launch");
   }

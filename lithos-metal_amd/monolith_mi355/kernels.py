@@ -129,13 +129,15 @@ def dequant(w: PackedWeight, expert: int = 0, stream=None):
 
 def gdn_step(proj, conv_in, conv_out, rec_in, rec_out, *, conv_w, neg_exp_a, dt_bias, norm_w, k_heads, v_heads,
              dk=128, dv=128, conv_width=4, eps=1e-6, ab=None, offsets=None, out=None, stream=None,
-             defer_norm: bool = False):
+             defer_norm: bool = False, commit: bool = False, t_dev=None):
     """``gdn_mixer`` + ``gdn_norm`` (``ops/gdn.py:1-24``) for ``proj [T, N1]`` bf16 in part order
     ``z | q | k | v | a | b`` (``nn/gdn.py:48-52``) unless ``offsets`` (z, q, k, v, a, b) says otherwise.
     Conv state ``[conv_dim, W-1]`` bf16 is read from ``conv_in`` and written to ``conv_out`` (distinct); the FP32
     recurrent state ``[hv, dk, dv]`` is read from ``rec_in`` and written to ``rec_out`` (may be the same tensor).
     Returns ``[T, hv·dv]`` bf16: the gated-norm output, or with ``defer_norm`` the BF16 read-out ``o`` for a
-    consumer that applies the norm itself (``gemv(..., gated_norm=...)``)."""
+    consumer that applies the norm itself (``gemv(..., gated_norm=...)``). ``commit`` is ``gdn_commit``
+    (``ops/gdn.py:13-17``): the speculative commit pass re-runs the first ``t_dev`` (device int32, ≤ T; None = all)
+    tokens from the step's input state into ``rec_out`` / ``conv_out`` and returns None (no read-out)."""
     torch = _torch()
     _bf16_2d(proj, "gdn proj", aligned=False)
     t = proj.shape[0]
@@ -155,15 +157,19 @@ def gdn_step(proj, conv_in, conv_out, rec_in, rec_out, *, conv_w, neg_exp_a, dt_
             raise ValueError(f"gdn_step: {name} must be a contiguous {dt} {shape}, got {tns.dtype} {tuple(tns.shape)}")
     if max(offsets[:4]) + dk > proj.shape[1] and ab is None:
         raise ValueError("gdn_step: proj is narrower than the z|q|k|v|a|b offsets")
-    if out is None:
+    if commit and rec_in.data_ptr() == rec_out.data_ptr():
+        raise ValueError("gdn_step: the commit pass needs distinct rec_in / rec_out (two state slots)")
+    if t_dev is not None and (t_dev.dtype != torch.int32 or t_dev.numel() != 1):
+        raise ValueError("gdn_step: t_dev must be a one-element int32 device tensor")
+    if out is None and not commit:
         out = torch.empty((t, vd), dtype=torch.bfloat16, device=proj.device)
     d = hip.MiGdnDesc(t=t, k_heads=k_heads, v_heads=v_heads, dk=dk, dv=dv, conv_width=conv_width, proj=hip.ptr(proj),
                       ld_proj=proj.stride(0), z_off=z_off, q_off=q_off, k_off=k_off, v_off=v_off, ab=hip.ptr(ab),
                       ld_ab=ab.stride(0) if ab is not None else 0, a_off=a_off, b_off=b_off, conv_w=hip.ptr(conv_w),
                       neg_exp_a=hip.ptr(neg_exp_a), dt_bias=hip.ptr(dt_bias), norm_w=hip.ptr(norm_w),
                       conv_in=hip.ptr(conv_in), conv_out=hip.ptr(conv_out), rec_in=hip.ptr(rec_in),
-                      rec_out=hip.ptr(rec_out), y=hip.ptr(out), ld_y=out.stride(0), eps=eps,
-                      defer_norm=int(defer_norm))
+                      rec_out=hip.ptr(rec_out), y=hip.ptr(out), ld_y=out.stride(0) if out is not None else 0, eps=eps,
+                      defer_norm=int(defer_norm), commit=int(commit), t_dev=hip.ptr(t_dev))
     hip.call("mi_gdn_step", C.byref(d), hip.stream_handle(stream))
     return out
 

@@ -1,7 +1,7 @@
 """The hot-path op kinds with their gfx950 bindings (names as in ``monolith/ops/{gemv,norm,attention,gdn,moe}.py``).
 
-``gdn_commit`` (the speculative verify's state commit, ``ops/gdn.py``) is defined without a binding: this backend
-does not implement it yet, and a program that uses it fails the coverage check instead of running wrong."""
+``gdn_commit`` (the speculative verify's state commit, ``ops/gdn.py:13-17``) is the GDN step entry point with
+``commit = 1``: the committed tokens replayed from the step's input slot into its output slot, no read-out."""
 
 from .registry import PROFILE, KernelBinding, OpClass, OpDef, register_op
 
@@ -21,10 +21,10 @@ GQA_DECODE = _op("gqa_decode", OpClass.MAP, "heads", "mi_gqa_decode")
 GQA_MERGE = _op("gqa_merge", OpClass.MAP, "heads", "mi_gqa_decode", fused_into="gqa_decode")
 GDN_MIXER = _op("gdn_mixer", OpClass.MAP, "heads", "mi_gdn_step")
 GDN_NORM = _op("gdn_norm", OpClass.MAP, "heads", "mi_gdn_step", fused_into="gdn_mixer")
-GDN_COMMIT = _op("gdn_commit", OpClass.MAP, "heads")
+GDN_COMMIT = _op("gdn_commit", OpClass.MAP, "heads", "mi_gdn_step", commit=1)
 MOE_ROUTE = _op("moe_route", OpClass.MAP, "rows", "mi_moe_route")
 MOE_GEMV = _op("moe_gemv", OpClass.MAP, "rows", "mi_gemv", grouped=1)
 MOE_COMBINE = _op("moe_combine", OpClass.MAP, "rows", "mi_moe_combine")
 
 DECODE_LAYER_OPS = ("gemv", "rmsnorm_stat", "norm_apply", "gqa_decode", "gqa_merge", "gdn_mixer", "gdn_norm",
-                    "moe_route", "moe_gemv", "moe_combine", "lm_head")
+                    "gdn_commit", "moe_route", "moe_gemv", "moe_combine", "lm_head")

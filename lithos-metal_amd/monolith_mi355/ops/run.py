@@ -32,6 +32,15 @@ def _gdn(proj, conv_in, conv_out, rec_in, rec_out, *, conv_w, neg_exp_a, dt_bias
                             conv_width=conv_width, eps=eps, ab=ab, offsets=offsets, out=out, stream=stream)
 
 
+def _gdn_commit(proj, conv_in, conv_out, rec_in, rec_out, *, conv_w, neg_exp_a, dt_bias, norm_w, k_heads, v_heads,
+                dk=128, dv=128, conv_width=4, eps=1e-6, ab=None, offsets=None, committed=None, stream=None, **_):
+    """``committed``: the accept scan's count of committed tokens as a device int32 (None: every row of proj)."""
+    return kernels.gdn_step(proj, conv_in, conv_out, rec_in, rec_out, conv_w=conv_w, neg_exp_a=neg_exp_a,
+                            dt_bias=dt_bias, norm_w=norm_w, k_heads=k_heads, v_heads=v_heads, dk=dk, dv=dv,
+                            conv_width=conv_width, eps=eps, ab=ab, offsets=offsets, commit=True, t_dev=committed,
+                            stream=stream)
+
+
 def _route(logits, *, top_k, renorm=True, stream=None, **_):
     return kernels.moe_route(logits, top_k, renorm=renorm, stream=stream)
 
@@ -47,8 +56,8 @@ def _combine(h, weights, shared=None, shared_gate=None, residual=None, *, top_k,
                                out=out, stream=stream)
 
 
-HANDLERS = {"gemv": _gemv, "lm_head": _lm_head, "gqa_decode": _gqa, "gdn_mixer": _gdn, "moe_route": _route,
-            "moe_gemv": _moe_gemv, "moe_combine": _combine}
+HANDLERS = {"gemv": _gemv, "lm_head": _lm_head, "gqa_decode": _gqa, "gdn_mixer": _gdn, "gdn_commit": _gdn_commit,
+            "moe_route": _route, "moe_gemv": _moe_gemv, "moe_combine": _combine}
 
 
 def run(kind: str, *inputs, **attrs):

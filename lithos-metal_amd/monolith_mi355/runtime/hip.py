@@ -44,7 +44,8 @@ class MiGdnDesc(C.Structure):
                 ("ld_ab", C.c_int32), ("a_off", C.c_int32), ("b_off", C.c_int32), ("conv_w", C.c_void_p),
                 ("neg_exp_a", C.c_void_p), ("dt_bias", C.c_void_p), ("norm_w", C.c_void_p), ("conv_in", C.c_void_p),
                 ("conv_out", C.c_void_p), ("rec_in", C.c_void_p), ("rec_out", C.c_void_p), ("y", C.c_void_p),
-                ("ld_y", C.c_int32), ("eps", C.c_float), ("defer_norm", C.c_int32)]
+                ("ld_y", C.c_int32), ("eps", C.c_float), ("defer_norm", C.c_int32), ("commit", C.c_int32),
+                ("t_dev", C.c_void_p)]
 
 
 class MiGqaDesc(C.Structure):

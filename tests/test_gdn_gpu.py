@@ -128,3 +128,57 @@ def test_gdn_deferred_norm_read_out(torch_gpu, t):
     z = proj[:, : hv * 128].reshape(t, hv, 128)
     got = ON.gated_rms_norm(o, z, p["norm_w"], EPS).reshape(t, hv * 128)
     _check(got, ref, from_dev_bf16(conv_out), conv_ref, rec_d.cpu().numpy(), rec_ref)
+
+
+@pytest.mark.parametrize("n_commit,via_device", [(3, True), (8, True), (0, True), (5, False)])
+def test_gdn_commit_replays_the_accepted_prefix(torch_gpu, n_commit, via_device):
+    """``gdn_commit`` (ops/gdn.py:13-17): after a verify step of 8 tokens wrote the output slot, the commit pass
+    recomputes the state for the first n accepted tokens from the step's input slot — the output slot then equals
+    the oracle's state after those n tokens, conv window included, and no read-out is written."""
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    hk, hv, t = 4, 12, 8
+    rng = np.random.default_rng(100 + n_commit)
+    p = _params(rng, hk, hv)
+    dp = _dev_params(torch, p)
+    conv_dim = 2 * hk * 128 + hv * 128
+    n1 = hv * 128 + conv_dim + 2 * hv
+    conv = rbf(rng.standard_normal((conv_dim, 3)) * 0.5)
+    rec = (rng.standard_normal((hv, 128, 128)) * 0.1).astype(np.float32)
+    proj = rbf(rng.standard_normal((t, n1)))
+    conv_a, conv_b = to_dev_bf16(torch, conv), torch.empty(conv_dim, 3, dtype=torch.bfloat16, device="cuda")
+    rec_a, rec_b = torch.from_numpy(rec).cuda(), torch.empty(hv, 128, 128, device="cuda")
+    pd = to_dev_bf16(torch, proj)
+    kernels.gdn_step(pd, conv_a, conv_b, rec_a, rec_b, k_heads=hk, v_heads=hv, eps=EPS, **dp)    # the verify step
+    if via_device:
+        tdev = torch.tensor([n_commit], dtype=torch.int32, device="cuda")
+        r = kernels.gdn_step(pd, conv_a, conv_b, rec_a, rec_b, k_heads=hk, v_heads=hv, eps=EPS, commit=True,
+                             t_dev=tdev, **dp)
+    else:
+        r = kernels.gdn_step(pd[:n_commit], conv_a, conv_b, rec_a, rec_b, k_heads=hk, v_heads=hv, eps=EPS,
+                             commit=True, **dp)
+    torch.cuda.synchronize()
+    assert r is None
+    if n_commit:
+        _, conv_ref, rec_ref = ON.gdn_mix(proj[:n_commit], conv, rec, k_heads=hk, v_heads=hv, dk=128, dv=128,
+                                          eps=EPS, **p)
+    else:
+        conv_ref, rec_ref = conv, rec
+    assert np.array_equal(from_dev_bf16(conv_b), conv_ref)
+    got = rec_b.cpu().numpy()
+    assert float(np.abs(got - rec_ref).max()) <= 8 * 2.0 ** -23 * float(np.abs(rec_ref).max())
+    assert np.array_equal(rec_a.cpu().numpy(), rec)                          # the input slot is untouched
+
+
+def test_gdn_commit_needs_two_slots(torch_gpu):
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    hk, hv = 2, 2
+    rng = np.random.default_rng(3)
+    dp = _dev_params(torch, _params(rng, hk, hv))
+    conv_dim = 2 * hk * 128 + hv * 128
+    proj = to_dev_bf16(torch, rbf(rng.standard_normal((1, hv * 128 + conv_dim + 2 * hv))))
+    rec = torch.zeros(hv, 128, 128, device="cuda")
+    c0, c1 = torch.zeros(conv_dim, 3, dtype=torch.bfloat16, device="cuda"), torch.zeros(conv_dim, 3, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError):
+        kernels.gdn_step(proj, c0, c1, rec, rec, k_heads=hk, v_heads=hv, commit=True, **dp)
