@@ -185,6 +185,8 @@ typedef struct mi_gqa_desc {
   int32_t ld_y;
   void* workspace;           /* split partials; NULL = the library's own */
   size_t workspace_bytes;
+  const int32_t* pos_dev;    /* device-resident position (a step program's mi_step_state.position) or NULL = pos;
+                                the key ranges are then planned for ctx_max - t and the kernels read the position */
 } mi_gqa_desc;
 size_t mi_gqa_workspace_bytes(const mi_gqa_desc* d);
 int mi_gqa_decode(const mi_gqa_desc* d, void* stream);

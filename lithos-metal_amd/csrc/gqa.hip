@@ -43,7 +43,11 @@ struct GqaArgs {
   f16_t* qf; float* qsc;                        // [kv][64][D] prescaled F16 query rows, [kv][64] their 2^p
   float* part_o; float* part_ml;                // [kv][group][rows][D], [kv][group][rows][2]
   uint16_t* y; int ldy;
+  const int32_t* pos_dev;                       // device-resident position (a step program's StepState), or null
 };
+
+// the cache position of the step's first new token: the descriptor's, or the one a step program keeps on the device
+__device__ __forceinline__ int cur_pos(const GqaArgs& a) { return a.pos_dev ? *a.pos_dev : a.pos; }
 
 __device__ __forceinline__ float bfv(const uint16_t* p, long long i) { return bf16_bits_to_f32(p[i]); }
 
@@ -76,7 +80,7 @@ __device__ void prep_vec(const GqaArgs& a, const uint16_t* src, const float* nw,
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   __builtin_amdgcn_wave_barrier();
   const int half = a.rot / 2;
-  const int p = a.pos + t;
+  const int p = cur_pos(a) + t;
   float o[2];
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
@@ -146,7 +150,8 @@ __global__ __launch_bounds__(64) void gqa_prep(GqaArgs a) {
     dst[lane + 64] = (f16_t)(x1 * inv);
     if (lane == 0) a.qsc[j * MAXROWS + qrow] = pow2f(p);
   } else {
-    const int j = x - a.heads, p = a.pos + t;
+    const int j = x - a.heads, p = cur_pos(a) + t;
+    if (p >= a.ctx) return;                       // past the cache (a device position the host cannot check)
     prep_vec(a, row + a.heads * q_cols + j * D, a.k_norm, t, tmp, lane);
     quant_store(tmp, a.kc + ((long long)j * a.ctx + p) * D, 1, a.ks + (long long)j * a.ctx + p, lane);
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -193,10 +198,13 @@ __global__ __launch_bounds__(64 * NW, RT == 1 ? 2 : 1) void gqa_decode(GqaArgs a
   __shared__ float mls[NW][RT * 16][2];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int j = blockIdx.y, g = blockIdx.x;
-  const int n_keys = a.pos + a.t;
+  const int pos = cur_pos(a);
+  const int n_keys = min(pos + a.t, a.ctx);
   const int kb = g * a.group_len;
-  const int ke = g == a.n_groups - 1 ? n_keys : kb + a.group_len;   // the last group also takes the new tokens
-  const int nch = (ke - kb + CHUNK - 1) / CHUNK;
+  // the last group also takes the new tokens; with a device position the groups cover the planned bound and the
+  // ones past the position are empty (their partials fold in with weight 0)
+  const int ke = g == a.n_groups - 1 ? n_keys : min(kb + a.group_len, n_keys);
+  const int nch = max(0, (ke - kb + CHUNK - 1) / CHUNK);
   const int k_begin = kb + (w * nch / NW) * CHUNK;
   const int k_end = min(ke, kb + ((w + 1) * nch / NW) * CHUNK);
   const int m16 = lane & 15, kg = lane >> 4;
@@ -224,7 +232,7 @@ __global__ __launch_bounds__(64 * NW, RT == 1 ? 2 : 1) void gqa_decode(GqaArgs a
       for (int i = 0; i < 8; ++i) qb[rt][s][i] = ok ? v[i] : (f16_t)0.0f;
     }
     rsc[rt] = ok ? a.qsc[j * MAXROWS + row] : 1.0f;
-    qlim[rt] = ok ? a.pos + row / a.rep : n_keys;       // rows past `rows` hold q = 0: finite, never written
+    qlim[rt] = ok ? pos + row / a.rep : n_keys;         // rows past `rows` hold q = 0: finite, never written
   }
 
   f32x4 o[RT][8];                                       // o[rt][ct][i] = O[row 16·rt + m16][dim 16·ct + 4·kg + i]
@@ -248,7 +256,7 @@ __global__ __launch_bounds__(64 * NW, RT == 1 ? 2 : 1) void gqa_decode(GqaArgs a
       for (int ct = 0; ct < 8; ++ct) vr[ks][ct] = *reinterpret_cast<const uint2*>(vp + (ct * 16 + m16) * CHUNK + ks * 32);
     load_k(kbase, ksb, vsb, k0 + CHUNK < k_end ? k0 + CHUNK : k0, m16, kg, nxt);
 
-    const bool full = k0 + CHUNK <= k_end && k0 + CHUNK - 1 <= a.pos;   // every key valid and visible to every row
+    const bool full = k0 + CHUNK <= k_end && k0 + CHUNK - 1 <= pos;     // every key valid and visible to every row
     float ksc[4][4], vsc[4][4];
     float vmax = 0.0f;
 #pragma unroll
@@ -469,10 +477,14 @@ int workspace(size_t bytes, void** out) {
 
 }  // namespace
 
+// the position the key ranges are planned for: the descriptor's, or — with a device position — the largest one the
+// cache allows
+int plan_pos(const mi_gqa_desc* d) { return d->pos_dev ? std::max(0, d->ctx_max - d->t) : d->pos; }
+
 extern "C" size_t mi_gqa_workspace_bytes(const mi_gqa_desc* d) {
   if (!d || d->t < 1 || d->kv_heads < 1 || d->heads % d->kv_heads) return 0;
   const int rows = d->heads / d->kv_heads * d->t;
-  return layout(d->kv_heads, plan(d->pos, d->kv_heads, rows).n_groups, rows).total;
+  return layout(d->kv_heads, plan(plan_pos(d), d->kv_heads, rows).n_groups, rows).total;
 }
 
 extern "C" int mi_gqa_decode(const mi_gqa_desc* d, void* stream) {
@@ -484,7 +496,8 @@ extern "C" int mi_gqa_decode(const mi_gqa_desc* d, void* stream) {
   const int rows = rep * d->t;
   MI_REQUIRE(rows <= 64, "mi_gqa_decode: rep·t = %d query rows per KV head exceeds 64", rows);
   MI_REQUIRE(d->rotary_dim >= 0 && d->rotary_dim <= D && d->rotary_dim % 2 == 0, "mi_gqa_decode: bad rotary_dim");
-  MI_REQUIRE(d->pos >= 0 && d->pos + d->t <= d->ctx_max, "mi_gqa_decode: pos + t exceeds the cache (%d)", d->ctx_max);
+  MI_REQUIRE(d->pos_dev || (d->pos >= 0 && d->pos + d->t <= d->ctx_max), "mi_gqa_decode: pos + t exceeds the cache (%d)",
+             d->ctx_max);
   MI_REQUIRE(d->ctx_max % CHUNK == 0, "mi_gqa_decode: ctx_max must be a multiple of %d", CHUNK);
   MI_REQUIRE(d->proj && d->k_codes && d->k_scales && d->v_codes && d->v_scales && d->y, "mi_gqa_decode: null pointer");
   MI_REQUIRE(d->rotary_dim == 0 || (d->rope_cos && d->rope_sin), "mi_gqa_decode: RoPE tables missing");
@@ -493,7 +506,8 @@ extern "C" int mi_gqa_decode(const mi_gqa_desc* d, void* stream) {
   GqaArgs a{};
   a.t = d->t; a.heads = d->heads; a.kv = d->kv_heads; a.rot = d->rotary_dim; a.pos = d->pos; a.ctx = d->ctx_max;
   a.gate = d->gate; a.qk_norm = d->qk_norm; a.rep = rep; a.rows = rows;
-  const Plan pl = plan(d->pos, d->kv_heads, rows);
+  const Plan pl = plan(plan_pos(d), d->kv_heads, rows);
+  a.pos_dev = d->pos_dev;
   a.n_groups = pl.n_groups;
   a.group_len = pl.group_len;
   a.proj = d->proj; a.ldp = d->ld_proj; a.cosb = d->rope_cos; a.sinb = d->rope_sin;

@@ -230,13 +230,15 @@ class KVCache:
         return sum(int(t.numel() * t.element_size()) for t in (self.k_codes, self.v_codes, self.k_scales, self.v_scales))
 
 
-def gqa_decode(proj, cache: KVCache, pos: int, *, heads: int, rope_cos, rope_sin, gate: bool = True,
+def gqa_decode(proj, cache: KVCache, pos, *, heads: int, rope_cos, rope_sin, gate: bool = True,
                q_norm=None, k_norm=None, eps: float = 1e-6, scaling: Optional[float] = None, out=None, stream=None,
                workspace=None):
     """``gqa_decode`` + ``gqa_merge`` (``ops/attention.py``; ``GQAAttention.mix``, ``nn/attention.py:215-243``) for
     ``proj [T, N1]`` bf16 (``q|gate`` per head, then ``k``, ``v``): q/k norm (``q_norm``/``k_norm`` = the (1 + w)
     float32 weights, both or neither), partial RoPE from the BF16 tables ``[ctx_max, rotary_dim]``, the new k/v
-    quantized into ``cache`` at ``pos..pos+T``, attention over the cache, × σ(gate). Returns ``[T, heads·D]`` bf16."""
+    quantized into ``cache`` at ``pos..pos+T``, attention over the cache, × σ(gate). Returns ``[T, heads·D]`` bf16.
+    ``pos`` is an int, or a one-element int32 device tensor the kernels read (a step program's StepState position:
+    the same launch serves every step of a replayed graph)."""
     torch = _torch()
     _bf16_2d(proj, "gqa proj", aligned=False)
     t = proj.shape[0]
@@ -257,6 +259,11 @@ def gqa_decode(proj, cache: KVCache, pos: int, *, heads: int, rope_cos, rope_sin
     _bf16_2d(out, "gqa out", aligned=False)
     if out.shape[0] < t or out.shape[1] < heads * d:
         raise ValueError("gqa_decode: out too small")
+    pos_dev = None
+    if not isinstance(pos, int):
+        if pos.dtype != torch.int32 or pos.numel() != 1 or pos.device.type != "cuda":
+            raise ValueError("gqa_decode: pos must be an int or a one-element int32 device tensor")
+        pos_dev, pos = pos, 0
     desc = hip.MiGqaDesc(t=t, heads=heads, kv_heads=kv, head_dim=d, rotary_dim=rope_cos.shape[1], pos=pos,
                          ctx_max=cache.ctx_max, gate=int(gate), qk_norm=int(q_norm is not None), proj=hip.ptr(proj),
                          ld_proj=proj.stride(0), rope_cos=hip.ptr(rope_cos), rope_sin=hip.ptr(rope_sin),
@@ -265,7 +272,8 @@ def gqa_decode(proj, cache: KVCache, pos: int, *, heads: int, rope_cos, rope_sin
                          k_scales=hip.ptr(cache.k_scales), v_codes=hip.ptr(cache.v_codes),
                          v_scales=hip.ptr(cache.v_scales), y=hip.ptr(out), ld_y=out.stride(0),
                          workspace=hip.ptr(workspace),
-                         workspace_bytes=0 if workspace is None else workspace.numel() * workspace.element_size())
+                         workspace_bytes=0 if workspace is None else workspace.numel() * workspace.element_size(),
+                         pos_dev=hip.ptr(pos_dev))
     hip.call("mi_gqa_decode", C.byref(desc), hip.stream_handle(stream))
     return out
 

@@ -55,7 +55,7 @@ class MiGqaDesc(C.Structure):
                 ("rope_sin", C.c_void_p), ("q_norm", C.c_void_p), ("k_norm", C.c_void_p), ("eps", C.c_float),
                 ("scaling", C.c_float), ("k_codes", C.c_void_p), ("k_scales", C.c_void_p), ("v_codes", C.c_void_p),
                 ("v_scales", C.c_void_p), ("y", C.c_void_p), ("ld_y", C.c_int32), ("workspace", C.c_void_p),
-                ("workspace_bytes", C.c_size_t)]
+                ("workspace_bytes", C.c_size_t), ("pos_dev", C.c_void_p)]
 
 
 class MiMoeRouteDesc(C.Structure):

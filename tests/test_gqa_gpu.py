@@ -75,7 +75,7 @@ def _check_cache(got, want, pos, t, exact):
             assert np.all(np.abs(gn.astype(np.float32) - wn.astype(np.float32)) <= 2 ** -9 * np.abs(wn.astype(np.float32)))
 
 
-def _run(torch, rng, ctx, pos, t, rot=64, gate=True, qk_norm=False, steps=1):
+def _run(torch, rng, ctx, pos, t, rot=64, gate=True, qk_norm=False, steps=1, device_pos=False):
     from monolith_mi355 import kernels
     cfg = _cfg(rot, gate, qk_norm, rng)
     cos, sin = kernels.rope_tables(1e6, rot, ctx)
@@ -89,7 +89,8 @@ def _run(torch, rng, ctx, pos, t, rot=64, gate=True, qk_norm=False, steps=1):
     for _ in range(steps):
         proj = rbf(rng.standard_normal((t, n1)))
         ref = ON.gqa_mix(proj, kc, ks, vc, vs, pos, **cfg)
-        y = kernels.gqa_decode(to_dev_bf16(torch, proj), cache, pos, heads=H, rope_cos=cos, rope_sin=sin, gate=gate,
+        p_arg = torch.tensor([pos], dtype=torch.int32, device="cuda") if device_pos else pos
+        y = kernels.gqa_decode(to_dev_bf16(torch, proj), cache, p_arg, heads=H, rope_cos=cos, rope_sin=sin, gate=gate,
                                q_norm=qn, k_norm=kn, eps=EPS)
         torch.cuda.synchronize()
         _check_cache(_download(cache), (kc, ks, vc, vs), pos, t, exact=not qk_norm)
@@ -120,6 +121,15 @@ def test_gqa_decode_variants(torch_gpu, gate, qk_norm, rot):
     print(f"gqa variant gate={gate} qk_norm={qk_norm} rot={rot}", flush=True)
     _run(torch_gpu, np.random.default_rng(rot + 2 * gate + qk_norm), 2048, 1500, 8, rot=rot, gate=gate,
          qk_norm=qk_norm)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("ctx,pos,t", [(4096, 0, 1), (4096, 1000, 1), (4096, 4088, 8), (16384, 300, 8)])
+def test_gqa_decode_device_position(torch_gpu, ctx, pos, t):
+    """The position read from device memory (a step program's StepState): key ranges planned for the whole cache,
+    the ones past the position empty — same bars as the host position."""
+    _run(torch_gpu, np.random.default_rng(ctx + pos + t), ctx, pos, t, steps=2 if pos + 2 * t <= ctx else 1,
+         device_pos=True)
 
 
 @pytest.mark.gpu
