@@ -228,6 +228,104 @@ typedef struct mi_moe_combine_desc {
 } mi_moe_combine_desc;
 int mi_moe_combine(const mi_moe_combine_desc* d, void* stream);
 
+/* ---- The GPU-resident token loop (runtime/engine.py:47-122, core/step_state.py:28-73, ops/embed.py, ops/sample.py
+ *      `argmax`, the advance op of runtime/src/metal_core.mm:256-386) ------------------------------------------------
+ * A step program replays one captured step (embed → layers → final norm + lm_head → argmax → advance) as a HIP graph;
+ * everything that changes between steps lives in mi_step_state in device memory, written by the serial ops at the
+ * end of the step, so the graph never changes. Emitted tokens go to a ring in pinned host memory as
+ * (sequence << 32) | token; the host drains it between launches. */
+#define MI_STEP_T_MAX 16
+#define MI_STEP_GAMMA_MAX 15
+/* Field order and meaning are the reference's StepStateLayout (core/step_state.py:38-63) at t_max = 16,
+ * gamma_max = 15: every field a 4-byte scalar or an array of them, 272 bytes. */
+typedef struct mi_step_state {
+  uint32_t step;                               /* steps completed */
+  uint32_t position;                           /* position of the first token of this step */
+  uint32_t kv_len;                             /* committed context length */
+  uint32_t t_this_step;                        /* tokens in this step */
+  int32_t pending_tokens[MI_STEP_T_MAX];       /* token ids fed to this step (embed reads them) */
+  uint32_t rng_lo, rng_hi;
+  int32_t anchor;
+  uint32_t gamma;
+  int32_t draft_tokens[MI_STEP_GAMMA_MAX];
+  float confidence[MI_STEP_GAMMA_MAX];
+  uint32_t verify_len, accepted, checkpoint_index, drafter_ctx_len;
+  uint32_t done;                               /* stop condition met: later steps' serial ops do nothing */
+  uint32_t error;                              /* 1 token ring overflow, 2 context capacity reached */
+  uint32_t ring_head;                          /* next ring slot the GPU writes */
+  uint32_t ring_tail;                          /* next slot the host reads (host-written) */
+  uint32_t prefill_left;                       /* prompt chunks still to feed; the advance emits only at 0 */
+  uint32_t n_inject;
+  uint32_t stop_at;                            /* host-written: ring head at which done is set (0 = never) */
+  uint32_t n_chain;
+  uint32_t pad_[2];
+} mi_step_state;
+
+/* embed (ops/embed.py:1-7, kernels/common/embed.metal): out[i] = table[tokens[i]] for i < t, BF16 [vocab][hidden]
+ * rows; an id outside [0, vocab) reads row 0 */
+typedef struct mi_embed_desc {
+  int32_t t, vocab, hidden;
+  const int32_t* tokens;      /* device: usually mi_step_state.pending_tokens */
+  const uint16_t* table;
+  uint16_t* out;
+  int32_t ldo;
+} mi_embed_desc;
+int mi_embed(const mi_embed_desc* d, void* stream);
+
+/* argmax (ops/sample.py:1-9, kernels/common/argmax.metal): ids[i] = the index of the largest logit of row i; ties →
+ * the lowest index; NaN never wins; a row with no number gives -1 */
+typedef struct mi_argmax_desc {
+  int32_t t, vocab;
+  const void* logits;
+  int32_t ld, f32;            /* f32: 1 FP32 logits, 0 BF16 */
+  int32_t* ids;               /* device [t] */
+} mi_argmax_desc;
+int mi_argmax(const mi_argmax_desc* d, void* stream);
+
+/* advance (kernels/common/advance.metal:15-37): the serial op that closes a step. Unless done: while prefill_left > 0
+ * only position += t_this_step and step += 1; otherwise the last row's token (tokens[t_this_step - 1]) goes to ring
+ * slot head % ring_cap as ((head + 1) << 32) | token (ring full: error 1 + done, nothing else changes), becomes
+ * pending_tokens[0], position += t_this_step, step += 1, t_this_step = 1; done at the ring head stop_at, at an EOS
+ * token, and (error 2) when ctx_cap > 0 and the new position reaches it. */
+typedef struct mi_advance_desc {
+  mi_step_state* state;       /* device */
+  const int32_t* tokens;      /* device: the argmax ids of this step */
+  uint64_t* ring;             /* pinned host memory (mi_host_alloc), ring_cap slots */
+  uint32_t ring_cap, ctx_cap;
+  int32_t n_eos, eos[8];      /* the EOS token ids (n_eos = 0: none) */
+  uint32_t* host_ctl;         /* optional pinned host words: [0] the host's ring tail (host-written), [1] done and
+                                 [2] error (written by every advance so the host polls them without a copy) */
+} mi_advance_desc;
+int mi_advance(const mi_advance_desc* d, void* stream);
+
+/* The host pump (runtime/src/metal_core.mm:256-386 `Runner::run` / `drain`): replay a captured step graph up to
+ * max_launches times, launches_per_batch per batch with at most in_flight batches queued; after each completed batch
+ * drain the ring by sequence tag into tokens[] and publish the tail (host_ctl[0], copied into state->ring_tail ahead
+ * of every batch); stop submitting once host_ctl[1] (done) is set, max_tokens tokens arrived (0 = no limit) or the
+ * token buffer is full. n_tokens counts what tokens[] holds (in: already there; out: after the run). */
+typedef struct mi_runner_desc {
+  void* graph_exec;           /* from mi_graph_end */
+  void* stream;
+  mi_step_state* state;       /* device */
+  const uint64_t* ring;       /* pinned host (mi_host_alloc) */
+  uint32_t ring_capacity;
+  uint32_t* host_ctl;         /* pinned host, the words the advance writes */
+  uint32_t max_launches, launches_per_batch, in_flight;
+  uint64_t max_tokens;
+  int32_t* tokens;            /* host */
+  uint64_t tokens_capacity, n_tokens;
+} mi_runner_desc;
+typedef struct mi_runner_stats {
+  uint64_t launches, batches, tokens;
+  double wall_ms, gpu_ms, launch_ms, wait_ms, host_busy_ms;
+  uint32_t done, error;
+} mi_runner_stats;
+int mi_runner_run(mi_runner_desc* d, mi_runner_stats* stats);
+
+/* pinned, device-accessible host memory for the token ring (hipHostMalloc); freed with mi_host_free */
+void* mi_host_alloc(size_t bytes);
+int mi_host_free(void* p);
+
 #ifdef __cplusplus
 }
 #endif

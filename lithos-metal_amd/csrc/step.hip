@@ -1,0 +1,240 @@
+// The serial ops of a GPU-resident decode loop (ops/embed.py `embed`, ops/sample.py `argmax`, the advance of
+// runtime/src/metal_core.mm:256-386 with the StepState fields of core/step_state.py:28-73): small kernels that run
+// once per step so a captured step replays unchanged; everything that varies lives in mi_step_state.
+#include "mi_common.h"
+
+#include <time.h>
+
+#include <chrono>
+#include <deque>
+#include <vector>
+
+static_assert(sizeof(mi_step_state) == 272, "mi_step_state: the 272-byte layout");
+
+namespace {
+
+constexpr int EMBED_THREADS = 256;
+constexpr int ARGMAX_THREADS = 1024;
+
+// one block per (token, 2048-column span): 8 BF16 per thread, 16-byte loads
+__global__ __launch_bounds__(EMBED_THREADS) void embed_rows(mi_embed_desc d) {
+  const int i = blockIdx.y;
+  const int col = (blockIdx.x * EMBED_THREADS + threadIdx.x) * 8;
+  if (col >= d.hidden) return;
+  const int tok = d.tokens[i];
+  const long long row = (tok >= 0 && tok < d.vocab) ? tok : 0;
+  const uint4 v = *reinterpret_cast<const uint4*>(d.table + row * d.hidden + col);
+  *reinterpret_cast<uint4*>(d.out + (long long)i * d.ldo + col) = v;
+}
+
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+  return v > bv || (v == bv && i < bi);          // NaN compares false: never replaces a number
+}
+
+// one block per row: strided scan, then a tree over the block in LDS (deterministic: the order is fixed)
+__global__ __launch_bounds__(ARGMAX_THREADS) void argmax_rows(mi_argmax_desc d) {
+  __shared__ float sv[ARGMAX_THREADS];
+  __shared__ int si[ARGMAX_THREADS];
+  const int row = blockIdx.x, tid = threadIdx.x;
+  float bv = -INFINITY;
+  int bi = 0x7FFFFFFF;
+  if (d.f32) {
+    const float* p = static_cast<const float*>(d.logits) + (long long)row * d.ld;
+    for (int i = tid; i < d.vocab; i += ARGMAX_THREADS)
+      if (better(p[i], i, bv, bi)) { bv = p[i]; bi = i; }
+  } else {
+    const uint16_t* p = static_cast<const uint16_t*>(d.logits) + (long long)row * d.ld;
+    for (int i = tid; i < d.vocab; i += ARGMAX_THREADS) {
+      const float v = bf16_bits_to_f32(p[i]);
+      if (better(v, i, bv, bi)) { bv = v; bi = i; }
+    }
+  }
+  sv[tid] = bv;
+  si[tid] = bi;
+  __syncthreads();
+  for (int s = ARGMAX_THREADS / 2; s > 0; s >>= 1) {
+    if (tid < s && better(sv[tid + s], si[tid + s], sv[tid], si[tid])) {
+      sv[tid] = sv[tid + s];
+      si[tid] = si[tid + s];
+    }
+    __syncthreads();
+  }
+  if (tid == 0) d.ids[row] = si[0] == 0x7FFFFFFF ? -1 : si[0];  // no number in the row
+}
+
+__device__ __forceinline__ void publish(const mi_advance_desc& d, const mi_step_state* st) {
+  if (d.host_ctl) {                                 // posted writes to pinned host memory: the pump polls these
+    __atomic_store_n(&d.host_ctl[2], st->error, __ATOMIC_RELAXED);
+    __atomic_store_n(&d.host_ctl[1], st->done, __ATOMIC_RELEASE);
+  }
+}
+
+// one thread: the ring, the position and the stop conditions
+__global__ __launch_bounds__(64) void advance_step(mi_advance_desc d) {
+  if (threadIdx.x != 0) return;
+  mi_step_state* st = d.state;
+  if (st->done) return;
+  const uint32_t t = st->t_this_step;
+  if (st->prefill_left > 0) {                       // a prompt chunk: no token leaves the step
+    st->position += t;
+    st->step += 1;
+    if (d.ctx_cap && st->position >= d.ctx_cap) { st->error = 2; st->done = 1; }
+    publish(d, st);
+    return;
+  }
+  const int32_t tok = d.tokens[t > 0 ? t - 1 : 0];
+  const uint32_t head = st->ring_head;
+  if (head - st->ring_tail >= d.ring_cap) {         // the host has not drained: overflow
+    st->error = 1;
+    st->done = 1;
+    publish(d, st);
+    return;
+  }
+  d.ring[head % d.ring_cap] = ((uint64_t)(head + 1) << 32) | (uint32_t)tok;
+  st->ring_head = head + 1;
+  if (st->stop_at && head + 1 >= st->stop_at) st->done = 1;
+  st->pending_tokens[0] = tok;
+  st->position += t;
+  st->step += 1;
+  st->t_this_step = 1;
+  for (int i = 0; i < d.n_eos; ++i)
+    if (tok == d.eos[i]) st->done = 1;
+  if (d.ctx_cap && st->position >= d.ctx_cap) { st->error = 2; st->done = 1; }
+  publish(d, st);
+}
+
+double now_ms() {
+  return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+double thread_cpu_ms() {
+  timespec ts;
+  clock_gettime(CLOCK_THREAD_CPUTIME_ID, &ts);
+  return ts.tv_sec * 1e3 + ts.tv_nsec / 1e6;
+}
+
+// take slots while the next expected sequence number is present (slots of batches still running may be written in
+// any order, so the GPU's head is never trusted), then publish the tail
+bool drain_ring(mi_runner_desc* d) {
+  const volatile uint64_t* slots = d->ring;
+  uint32_t tail = __atomic_load_n(&d->host_ctl[0], __ATOMIC_RELAXED);
+  bool full = false;
+  for (;;) {
+    const uint64_t v = slots[tail % d->ring_capacity];
+    if ((uint32_t)(v >> 32) != tail + 1) break;
+    if (d->n_tokens >= d->tokens_capacity) { full = true; break; }
+    d->tokens[d->n_tokens++] = (int32_t)(uint32_t)v;
+    ++tail;
+  }
+  __atomic_store_n(&d->host_ctl[0], tail, __ATOMIC_RELEASE);
+  return full;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mi_runner_run(mi_runner_desc* d, mi_runner_stats* st) {
+  MI_REQUIRE(d && st && d->graph_exec && d->state && d->ring && d->host_ctl && (d->tokens || !d->tokens_capacity),
+             "mi_runner_run: null pointer");
+  MI_REQUIRE(d->ring_capacity > 0 && d->launches_per_batch > 0 && d->in_flight > 0,
+             "mi_runner_run: ring_capacity, launches_per_batch and in_flight must be >= 1");
+  MI_REQUIRE(d->n_tokens <= d->tokens_capacity, "mi_runner_run: n_tokens exceeds tokens_capacity");
+  *st = mi_runner_stats{};
+  hipStream_t s = static_cast<hipStream_t>(d->stream);
+  auto exec = static_cast<hipGraphExec_t>(d->graph_exec);
+  struct Batch { hipEvent_t a, b; };
+  std::vector<Batch> pool(d->in_flight);
+  for (auto& b : pool) {
+    MI_TRY_HIP(hipEventCreate(&b.a), "hipEventCreate");
+    MI_TRY_HIP(hipEventCreate(&b.b), "hipEventCreate");
+  }
+  auto release = [&]() { for (auto& b : pool) { (void)hipEventDestroy(b.a); (void)hipEventDestroy(b.b); } };
+  const double t0 = now_ms(), c0 = thread_cpu_ms();
+  const uint64_t first = d->n_tokens;
+  std::deque<size_t> pending;
+  size_t next = 0;
+  bool full = false;
+  hipError_t err = hipSuccess;
+  auto observe = [&]() {
+    Batch& b = pool[pending.front()];
+    pending.pop_front();
+    const double w = now_ms();
+    hipError_t e = hipEventSynchronize(b.b);
+    st->wait_ms += now_ms() - w;
+    if (e != hipSuccess && err == hipSuccess) err = e;
+    float ms = 0.f;
+    if (e == hipSuccess && hipEventElapsedTime(&ms, b.a, b.b) == hipSuccess) st->gpu_ms += ms;
+    st->batches++;
+    full = drain_ring(d) || full;
+    st->done = __atomic_load_n(&d->host_ctl[1], __ATOMIC_ACQUIRE);
+    st->error = __atomic_load_n(&d->host_ctl[2], __ATOMIC_RELAXED);
+  };
+  while (st->launches < d->max_launches && !st->done && !full && err == hipSuccess &&
+         (d->max_tokens == 0 || d->n_tokens - first < d->max_tokens)) {
+    const double l = now_ms();
+    const uint32_t n = (uint32_t)std::min<uint64_t>(d->launches_per_batch, d->max_launches - st->launches);
+    Batch& b = pool[next];
+    // the tail the GPU checks for overflow: the host's value when the copy runs (it only grows)
+    err = hipMemcpyAsync(&d->state->ring_tail, &d->host_ctl[0], sizeof(uint32_t), hipMemcpyHostToDevice, s);
+    if (err == hipSuccess) err = hipEventRecord(b.a, s);
+    for (uint32_t i = 0; i < n && err == hipSuccess; ++i) err = hipGraphLaunch(exec, s);
+    if (err == hipSuccess) err = hipEventRecord(b.b, s);
+    st->launch_ms += now_ms() - l;
+    if (err != hipSuccess) break;
+    pending.push_back(next);
+    next = (next + 1) % pool.size();
+    st->launches += n;
+    while (pending.size() >= d->in_flight) observe();
+  }
+  while (!pending.empty()) observe();
+  st->wall_ms = now_ms() - t0;
+  st->host_busy_ms = thread_cpu_ms() - c0;
+  st->tokens = d->n_tokens - first;
+  release();
+  MI_TRY_HIP(err, "mi_runner_run");
+  return MI_OK;
+}
+
+int mi_embed(const mi_embed_desc* d, void* stream) {
+  MI_REQUIRE(d && d->tokens && d->table && d->out, "mi_embed: null pointer");
+  MI_REQUIRE(d->t >= 1 && d->t <= 16 && d->vocab > 0 && d->hidden > 0 && d->hidden % 8 == 0 && d->ldo >= d->hidden &&
+             d->ldo % 8 == 0, "mi_embed: bad shape");
+  MI_REQUIRE(((uintptr_t)d->table & 15) == 0 && ((uintptr_t)d->out & 15) == 0, "mi_embed: table / out alignment");
+  const dim3 grid((d->hidden / 8 + EMBED_THREADS - 1) / EMBED_THREADS, d->t);
+  hipLaunchKernelGGL(embed_rows, grid, dim3(EMBED_THREADS), 0, static_cast<hipStream_t>(stream), *d);
+  MI_TRY_HIP(hipGetLastError(), "embed launch");
+  return MI_OK;
+}
+
+int mi_argmax(const mi_argmax_desc* d, void* stream) {
+  MI_REQUIRE(d && d->logits && d->ids, "mi_argmax: null pointer");
+  MI_REQUIRE(d->t >= 1 && d->t <= 16 && d->vocab > 0 && d->ld >= d->vocab, "mi_argmax: bad shape");
+  hipLaunchKernelGGL(argmax_rows, dim3(d->t), dim3(ARGMAX_THREADS), 0, static_cast<hipStream_t>(stream), *d);
+  MI_TRY_HIP(hipGetLastError(), "argmax launch");
+  return MI_OK;
+}
+
+int mi_advance(const mi_advance_desc* d, void* stream) {
+  MI_REQUIRE(d && d->state && d->tokens && d->ring, "mi_advance: null pointer");
+  MI_REQUIRE(d->ring_cap >= 1 && d->n_eos >= 0 && d->n_eos <= 8, "mi_advance: ring_cap >= 1, n_eos in 0..8");
+  hipLaunchKernelGGL(advance_step, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), *d);
+  MI_TRY_HIP(hipGetLastError(), "advance launch");
+  return MI_OK;
+}
+
+void* mi_host_alloc(size_t bytes) {
+  void* p = nullptr;
+  if (hipHostMalloc(&p, bytes, hipHostMallocCoherent) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  return p;
+}
+
+int mi_host_free(void* p) {
+  if (p) MI_TRY_HIP(hipHostFree(p), "hipHostFree");
+  return MI_OK;
+}
+
+}  // extern "C"

@@ -92,3 +92,15 @@ def interleave_rows(gate: torch.Tensor, up: torch.Tensor, chunk: int = 8) -> tor
     """``[gate; up]`` rows reordered ``chunk`` gate rows then ``chunk`` up rows (``packs/transforms.py:16-24``)."""
     n = gate.shape[0]
     return torch.stack([gate.reshape(n // chunk, chunk, -1), up.reshape(n // chunk, chunk, -1)], dim=1).reshape(2 * n, -1)
+
+
+def pack_bf16(w: torch.Tensor) -> torch.Tensor:
+    """The T16 BF16 layout (see :mod:`.pack`) of ``w [N, K]`` bfloat16 (K a multiple of 32) → uint8 [bytes]."""
+    n, k = w.shape
+    if k % 32:
+        raise ValueError("pack_bf16: K must be a multiple of 32")
+    nt = -(-n // 16)
+    if nt * 16 != n:
+        w = torch.cat([w, w.new_zeros(nt * 16 - n, k)])
+    u = w.contiguous().view(torch.int16).reshape(nt, 16, k // 32, 4, 8).permute(0, 2, 3, 1, 4)
+    return u.contiguous().view(torch.uint8).reshape(-1)

@@ -357,3 +357,58 @@ def moe_combine(h, weights, *, top_k: int, shared=None, shared_gate=None, residu
                              out=hip.ptr(out), ldo=out.stride(0))
     hip.call("mi_moe_combine", C.byref(d), hip.stream_handle(stream))
     return out
+
+
+def embed(table, tokens, *, t: Optional[int] = None, out=None, stream=None):
+    """``embed`` (``ops/embed.py:1-7``): ``out[i] = table[tokens[i]]`` for ``i < t`` over a BF16 ``table
+    [vocab, hidden]``; ``tokens`` is a device int32 vector (a view of the step state's ``pending_tokens`` in a step
+    program); an id outside ``[0, vocab)`` reads row 0."""
+    torch = _torch()
+    _bf16_2d(table, "embed table")
+    vocab, hidden = table.shape
+    t = tokens.numel() if t is None else t
+    if tokens.dtype != torch.int32 or tokens.numel() < t or not 1 <= t <= 16:
+        raise ValueError("embed: tokens must be a device int32 vector of 1..16 ids")
+    if out is None:
+        out = torch.empty((t, hidden), dtype=torch.bfloat16, device=table.device)
+    _bf16_2d(out, "embed out")
+    if out.shape[0] < t or out.shape[1] != hidden:
+        raise ValueError("embed: out must be [t, hidden]")
+    d = hip.MiEmbedDesc(t=t, vocab=vocab, hidden=hidden, tokens=hip.ptr(tokens), table=hip.ptr(table),
+                        out=hip.ptr(out), ldo=out.stride(0))
+    hip.call("mi_embed", C.byref(d), hip.stream_handle(stream))
+    return out
+
+
+def argmax(logits, *, out=None, stream=None):
+    """``argmax`` (``ops/sample.py:1-9``): ``logits [T, V]`` float32 or bf16 → ``ids [T]`` int32; ties → the lowest
+    index, NaN never wins, a row without a number gives -1."""
+    torch = _torch()
+    if logits.dim() != 2 or logits.stride(1) != 1 or logits.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("argmax: logits must be a row-major 2-D float32 or bfloat16 tensor")
+    t, v = logits.shape
+    if not 1 <= t <= 16:
+        raise ValueError("argmax: 1..16 rows")
+    if out is None:
+        out = torch.empty(t, dtype=torch.int32, device=logits.device)
+    if out.dtype != torch.int32 or out.numel() < t:
+        raise ValueError("argmax: out must be int32 [t]")
+    d = hip.MiArgmaxDesc(t=t, vocab=v, logits=hip.ptr(logits), ld=logits.stride(0),
+                         f32=int(logits.dtype == torch.float32), ids=hip.ptr(out))
+    hip.call("mi_argmax", C.byref(d), hip.stream_handle(stream))
+    return out
+
+
+def advance(state, tokens, ring, ring_cap: int, *, eos=(), ctx_cap: int = 0, host_ctl=None, stream=None):
+    """``advance`` (``kernels/common/advance.metal:15-37``): close a step — publish the last row's token to the ring,
+    make it the next step's pending token, move position and step, stop at EOS / ``stop_at`` / the context capacity.
+    ``state``: the device step state (int32 tensor of 68 words); ``ring`` / ``host_ctl``: pinned host addresses."""
+    torch = _torch()
+    if state.dtype != torch.int32 or state.numel() * 4 < C.sizeof(hip.MiStepState) or not state.is_cuda:
+        raise ValueError("advance: state must be a device int32 tensor of the step-state size")
+    eos = [int(e) for e in ([eos] if isinstance(eos, int) else eos) if e is not None and int(e) >= 0]
+    if len(eos) > 8:
+        raise ValueError("advance: at most 8 EOS ids")
+    d = hip.MiAdvanceDesc(state=hip.ptr(state), tokens=hip.ptr(tokens), ring=hip.ptr(ring), ring_cap=ring_cap,
+                          ctx_cap=ctx_cap, n_eos=len(eos), eos=(C.c_int32 * 8)(*eos), host_ctl=hip.ptr(host_ctl))
+    hip.call("mi_advance", C.byref(d), hip.stream_handle(stream))

@@ -119,8 +119,11 @@ class GdnDecoderLayer:
                              torch.empty(m, self.hidden, dtype=torch.bfloat16, device=dev))
         return self._bufs[m]
 
-    def step(self, h, out=None):
-        """One decode step over ``h [M, hidden]`` bf16 (M ≤ 16 tokens): returns the layer output; advances the state."""
+    ping_pong = True          # the conv state alternates between two buffers: a captured program holds step pairs
+
+    def step(self, h, out=None, pos=None):
+        """One decode step over ``h [M, hidden]`` bf16 (M ≤ 16 tokens): returns the layer output; advances the state.
+        ``pos`` is accepted for a uniform layer interface (the recurrence needs no position)."""
         proj, o, h1, act, h2 = self.buffers(h.shape[0])
         out = h2 if out is None else out
         kernels.gemv(self.w_in.packed, h, norm_w=self.norm_w, eps=self.eps, out=proj)
@@ -201,7 +204,8 @@ class AttnDecoderLayer:
         return self._bufs[m]
 
     def step(self, h, pos: int, out=None):
-        """One decode step over ``h [M, hidden]`` at positions ``pos..pos+M-1``; the new k/v enter the cache."""
+        """One decode step over ``h [M, hidden]`` at positions ``pos..pos+M-1``; the new k/v enter the cache. ``pos``
+        is an int or a one-element device int32 tensor (the step state's position in a captured program)."""
         proj, o, h1, act, h2 = self.buffers(h.shape[0])
         out = h2 if out is None else out
         kernels.gemv(self.w_qkv.packed, h, norm_w=self.norm_w, eps=self.eps, out=proj)
@@ -230,3 +234,25 @@ class AttnDecoderLayer:
                 "cos": self.cos.float().cpu().numpy(), "sin": self.sin.float().cpu().numpy(),
                 "k_codes": c.k_codes.cpu().numpy(), "k_scales": c.k_scales.cpu().numpy(),
                 "v_codes": c.v_codes_token_major().cpu().numpy(), "v_scales": c.v_scales.cpu().numpy()}
+
+
+class DecoderModel:
+    """Embedding, decoder layers, final RMSNorm and LM head (``nn/decoder.py``, ``models/*``): what a step program
+    runs once per token. ``lm_head`` is BF16 (the reference's unquantized head), its RMSNorm fused on load."""
+
+    def __init__(self, layers, *, vocab: int, hidden: int, eps: float = 1e-6, device="cuda", seed=0):
+        torch = _torch()
+        gen = torch.Generator(device=device)
+        gen.manual_seed(seed + 7919)
+        self.layers, self.vocab, self.hidden, self.eps = list(layers), vocab, hidden, eps
+        self.embed_table = (torch.randn(vocab, hidden, generator=gen, device=device) * 0.5).to(torch.bfloat16)
+        self.norm_w = 1.0 + torch.randn(hidden, generator=gen, device=device) * 0.1
+        self.lm_w = (torch.randn(vocab, hidden, generator=gen, device=device) * 0.02).to(torch.bfloat16)
+        self.lm_head = kernels.PackedWeight("bf16", vocab, hidden, 1, DV.pack_bf16(self.lm_w), None)
+
+    def step_bytes(self, pos: int) -> int:
+        """Algorithmic HBM bytes of one token step (M = 1)."""
+        total = self.hidden * 2 + self.vocab * self.hidden * 2 + self.hidden * 4 + self.vocab * 4
+        for layer in self.layers:
+            total += layer.bytes_per_step(1) if getattr(layer, "ping_pong", False) else layer.bytes_per_step(1, pos)
+        return total

@@ -71,6 +71,46 @@ class MiMoeCombineDesc(C.Structure):
                 ("ldo", C.c_int32)]
 
 
+class MiStepState(C.Structure):
+    """``mi_step_state``: the reference's StepStateLayout order (``core/step_state.py:38-63``) at t_max 16,
+    gamma_max 15."""
+    _u = C.c_uint32
+    _fields_ = [("step", _u), ("position", _u), ("kv_len", _u), ("t_this_step", _u),
+                ("pending_tokens", C.c_int32 * 16), ("rng_lo", _u), ("rng_hi", _u), ("anchor", C.c_int32),
+                ("gamma", _u), ("draft_tokens", C.c_int32 * 15), ("confidence", C.c_float * 15),
+                ("verify_len", _u), ("accepted", _u), ("checkpoint_index", _u), ("drafter_ctx_len", _u),
+                ("done", _u), ("error", _u), ("ring_head", _u), ("ring_tail", _u), ("prefill_left", _u),
+                ("n_inject", _u), ("stop_at", _u), ("n_chain", _u), ("pad_", _u * 2)]
+
+
+class MiEmbedDesc(C.Structure):
+    _fields_ = [("t", C.c_int32), ("vocab", C.c_int32), ("hidden", C.c_int32), ("tokens", C.c_void_p),
+                ("table", C.c_void_p), ("out", C.c_void_p), ("ldo", C.c_int32)]
+
+
+class MiArgmaxDesc(C.Structure):
+    _fields_ = [("t", C.c_int32), ("vocab", C.c_int32), ("logits", C.c_void_p), ("ld", C.c_int32),
+                ("f32", C.c_int32), ("ids", C.c_void_p)]
+
+
+class MiAdvanceDesc(C.Structure):
+    _fields_ = [("state", C.c_void_p), ("tokens", C.c_void_p), ("ring", C.c_void_p), ("ring_cap", C.c_uint32),
+                ("ctx_cap", C.c_uint32), ("n_eos", C.c_int32), ("eos", C.c_int32 * 8), ("host_ctl", C.c_void_p)]
+
+
+class MiRunnerDesc(C.Structure):
+    _fields_ = [("graph_exec", C.c_void_p), ("stream", C.c_void_p), ("state", C.c_void_p), ("ring", C.c_void_p),
+                ("ring_capacity", C.c_uint32), ("host_ctl", C.c_void_p), ("max_launches", C.c_uint32),
+                ("launches_per_batch", C.c_uint32), ("in_flight", C.c_uint32), ("max_tokens", C.c_uint64),
+                ("tokens", C.c_void_p), ("tokens_capacity", C.c_uint64), ("n_tokens", C.c_uint64)]
+
+
+class MiRunnerStats(C.Structure):
+    _fields_ = [("launches", C.c_uint64), ("batches", C.c_uint64), ("tokens", C.c_uint64), ("wall_ms", C.c_double),
+                ("gpu_ms", C.c_double), ("launch_ms", C.c_double), ("wait_ms", C.c_double),
+                ("host_busy_ms", C.c_double), ("done", C.c_uint32), ("error", C.c_uint32)]
+
+
 # name -> (restype, argtypes); every int-returning entry point is error-checked
 _VP, _I32, _SZ, _F = C.c_void_p, C.c_int32, C.c_size_t, C.c_float
 SIGNATURES = {
@@ -107,6 +147,12 @@ SIGNATURES = {
     "mi_gqa_decode": (C.c_int, [C.POINTER(MiGqaDesc), _VP]),
     "mi_moe_route": (C.c_int, [C.POINTER(MiMoeRouteDesc), _VP]),
     "mi_moe_combine": (C.c_int, [C.POINTER(MiMoeCombineDesc), _VP]),
+    "mi_embed": (C.c_int, [C.POINTER(MiEmbedDesc), _VP]),
+    "mi_argmax": (C.c_int, [C.POINTER(MiArgmaxDesc), _VP]),
+    "mi_advance": (C.c_int, [C.POINTER(MiAdvanceDesc), _VP]),
+    "mi_runner_run": (C.c_int, [C.POINTER(MiRunnerDesc), C.POINTER(MiRunnerStats)]),
+    "mi_host_alloc": (_VP, [_SZ]),
+    "mi_host_free": (C.c_int, [_VP]),
 }
 
 

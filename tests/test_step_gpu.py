@@ -1,0 +1,269 @@
+"""The GPU-resident token loop on the MI355X: ``embed`` / ``argmax`` / ``advance`` against the oracle, the native
+pump over a captured step graph (the reference's ``tests/runtime/test_toy_program.py`` cases: many steps from one
+capture, graph ≡ eager, early exit with ring wrap, overflow as an error), and a decoder with Gated DeltaNet and
+attention layers whose replayed tokens equal a launch-by-launch host loop."""
+
+import numpy as np
+import pytest
+
+from helpers import from_dev_bf16, to_dev_bf16
+from oracle import step as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+@pytest.mark.parametrize("vocab", [248320, 1000, 300])
+@pytest.mark.parametrize("f32", [True, False])
+def test_argmax(torch_gpu, vocab, f32):
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    _say("argmax", vocab, f32)
+    rng = np.random.default_rng(vocab)
+    x = rng.standard_normal((5, vocab)).astype(np.float32) * 4
+    x[0, vocab - 1] = 100.0
+    x[1, 5] = x[1, 7] = 50.0
+    x[2] = -np.abs(x[2]) - 1
+    x[3, ::3] = np.nan
+    x[3, 11] = 60.0
+    x[4] = np.nan
+    x[4, vocab // 2] = -np.inf
+    if f32:
+        logits = torch.from_numpy(x).cuda()
+        ref = O.argmax(x)
+    else:
+        logits = to_dev_bf16(torch, x)
+        ref = O.argmax(from_dev_bf16(logits))
+    got = kernels.argmax(logits).cpu().numpy()
+    assert got.tolist() == ref.tolist()
+    assert got[1] == 5 and got[0] == vocab - 1 and got[3] == 11 and got[4] == vocab // 2
+
+
+def test_argmax_all_nan_row(torch_gpu):
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    x = torch.full((2, 300), float("nan"), device="cuda")
+    x[1, 17] = 0.0
+    assert kernels.argmax(x).cpu().tolist() == [-1, 17]
+
+
+def test_embed(torch_gpu):
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    rng = np.random.default_rng(3)
+    table = rng.standard_normal((1000, 5120)).astype(np.float32)
+    tdev = to_dev_bf16(torch, table)
+    ids = [999, -3, 1000, 0, 17, 512]
+    out = kernels.embed(tdev, torch.tensor(ids, dtype=torch.int32, device="cuda"))
+    assert np.array_equal(from_dev_bf16(out), O.embed(from_dev_bf16(tdev), ids))
+
+
+def _advance_once(torch, state, token, **kw):
+    """One advance over 16 token rows (``tokens[t_this_step - 1]`` is read), all holding ``token``."""
+    from monolith_mi355 import kernels
+    tokens = torch.full((16,), token, dtype=torch.int32, device="cuda")
+    kernels.advance(state.buf, tokens, state.ring.addr, state.ring_capacity, host_ctl=state.ctl.addr, **kw)
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("token,stops,done", [(2, [2, 9, 11], 1), (9, [2, 9, 11], 1), (11, [2, 9, 11], 1),
+                                              (7, [2, 9, 11], 0), (9, [], 0), (9, [-1], 0), (9, [9], 1)])
+def test_advance_stop_tokens(torch_gpu, token, stops, done):
+    """The reference's ``tests/kernels/test_eos_set.py`` table, through the kernel."""
+    from monolith_mi355.runtime.step import StepState
+    st = StepState(ring_capacity=16)
+    st.write(t_this_step=1, position=5)
+    _advance_once(torch_gpu, st, token, eos=stops)
+    got = st.read()
+    assert got["done"] == done and got["ring_head"] == 1 and got["position"] == 6 and got["step"] == 1
+    assert int(st.ring.array[0]) & 0xFFFFFFFF == token and int(st.ring.array[0]) >> 32 == 1
+    assert got["pending_tokens"][0] == token and st.done == bool(done) and st.error == 0
+
+
+def test_advance_matches_oracle_over_a_sequence(torch_gpu):
+    """Prefill chunk, tokens, ring wrap with drains, stop_at, then context capacity: field by field."""
+    torch = torch_gpu
+    from monolith_mi355.runtime.step import StepState
+    st = StepState(ring_capacity=8)
+    st.write(t_this_step=4, position=0, prefill_left=1, stop_at=30)
+    ref, ring_ref, tail_ref = O.new_state(t_this_step=4, position=0, prefill_left=1, stop_at=30), np.zeros(8, np.uint64), 0
+    got_tokens, ref_tokens = [], []
+    for s in range(40):
+        if s == 1:
+            st.write(prefill_left=0)
+            ref["prefill_left"] = 0
+        tok = (s * 37 + 5) % 101
+        _advance_once(torch, st, tok, ctx_cap=64)
+        O.advance(ref, [tok] * 16, ring_ref, ctx_cap=64)
+        if s % 3 == 2:
+            st.drain(got_tokens)
+            st.write(ring_tail=int(st.ctl.array[0]))
+            tail_ref = O.drain(ring_ref, tail_ref, ref_tokens)
+            ref["ring_tail"] = tail_ref
+        g = st.read()
+        for k in ("step", "position", "t_this_step", "done", "error", "ring_head"):
+            assert g[k] == ref[k], (s, k)
+    st.drain(got_tokens)
+    O.drain(ring_ref, tail_ref, ref_tokens)
+    assert got_tokens == ref_tokens and len(got_tokens) == 30
+
+
+def test_advance_context_capacity(torch_gpu):
+    from monolith_mi355.runtime.step import StepState
+    st = StepState(ring_capacity=4)
+    st.write(t_this_step=1, position=9)
+    _advance_once(torch_gpu, st, 3, ctx_cap=10)
+    g = st.read()
+    assert g["error"] == 2 and g["done"] == 1 and st.error == 2 and st.done
+
+
+# ---- the pump over a captured graph: a toy program of this library's own ops --------------------------------------
+
+class _ToyModel:
+    """No layers; the embedding table's row v is one-hot at f(v) = (7·v + 3) mod V and the LM head is the identity,
+    so the step maps token v to f(v) (the RMSNorm of a one-hot row keeps its argmax)."""
+
+    def __init__(self, torch, vocab=256):
+        from monolith_mi355 import kernels
+        from monolith_mi355.formats import device as DV
+        self.layers, self.eps = [], 1e-6
+        t = torch.zeros(vocab, vocab, device="cuda")
+        t[torch.arange(vocab), (torch.arange(vocab) * 7 + 3) % vocab] = 1.0
+        self.embed_table = t.to(torch.bfloat16)
+        self.norm_w = torch.ones(vocab, device="cuda")
+        eye = torch.eye(vocab, device="cuda").to(torch.bfloat16)
+        self.lm_head = kernels.PackedWeight("bf16", vocab, vocab, 1, DV.pack_bf16(eye), None)
+        self.vocab = vocab
+
+    def chain(self, tok, n):
+        out = []
+        for _ in range(n):
+            tok = (tok * 7 + 3) % self.vocab
+            out.append(tok)
+        return out
+
+
+def _toy_program(torch, *, ring=256, stop_at=0, steps_per_graph=2):
+    from monolith_mi355.runtime.step import StepProgram, StepState
+    model = _ToyModel(torch)
+    st = StepState(ring_capacity=ring)
+    prog = StepProgram(model, st, steps_per_graph=steps_per_graph)
+    return model, st, prog
+
+
+def test_pump_replays_1000_steps_from_one_capture(torch_gpu):
+    torch = torch_gpu
+    _say("pump 1000")
+    model, st, prog = _toy_program(torch, stop_at=0)
+    st.start(position=0, token=1, stop_at=1)
+    prog.step_eager(1)                                   # grows the workspaces; emits one token
+    st.start(position=0, token=1, stop_at=1000)
+    prog.capture()
+    rep = prog.run(1000, launches_per_batch=25, in_flight=3)
+    assert rep.done and rep.error == 0 and rep.steps_submitted == 1000 and rep.batches == 20
+    assert rep.tokens == model.chain(1, 1000)
+    g = st.read()
+    assert g["step"] == 1000 and g["position"] == 1000 and g["ring_head"] == 1000
+    _say(f"1000 steps: gpu {rep.gpu_ms:.2f} ms wall {rep.wall_ms:.2f} ms host busy {rep.host_busy_ms:.2f} ms")
+
+
+def test_pump_matches_eager(torch_gpu):
+    torch = torch_gpu
+    model, st, prog = _toy_program(torch)
+    st.start(position=0, token=5)
+    eager = prog.step_eager(60)
+    st.start(position=0, token=5)
+    rep = prog.run(60, launches_per_batch=5, in_flight=2)
+    assert eager == rep.tokens == model.chain(5, 60)
+
+
+def test_pump_early_exit_and_ring_wrap(torch_gpu):
+    torch = torch_gpu
+    model, st, prog = _toy_program(torch, ring=64)
+    st.start(position=0, token=2)
+    prog.step_eager(1)
+    st.start(position=0, token=2, stop_at=100)
+    rep = prog.run(1000, launches_per_batch=2, in_flight=2)
+    g = st.read()
+    assert rep.done and rep.steps_submitted <= 100 + 2 * 2 * 2 and g["step"] == 100 and g["error"] == 0
+    assert rep.tokens == model.chain(2, 100)
+
+
+def test_pump_ring_overflow_is_an_error_not_corruption(torch_gpu):
+    torch = torch_gpu
+    model, st, prog = _toy_program(torch, ring=16)
+    st.start(position=0, token=3)
+    prog.step_eager(1)
+    st.start(position=0, token=3)
+    rep = prog.run(1000, launches_per_batch=25, in_flight=3)     # 50 steps per batch: the GPU outruns the host
+    g = st.read()
+    assert g["error"] == 1 and g["done"] == 1 and rep.error == 1
+    assert rep.tokens == model.chain(3, len(rep.tokens)) and len(rep.tokens) == 16
+
+
+def test_pump_max_tokens(torch_gpu):
+    torch = torch_gpu
+    model, st, prog = _toy_program(torch)
+    st.start(position=0, token=4)
+    prog.step_eager(1)
+    st.start(position=0, token=4)
+    rep = prog.run(200, launches_per_batch=4, in_flight=1, max_tokens=20)
+    assert 20 <= len(rep.tokens) < 40 and rep.tokens == model.chain(4, len(rep.tokens)) and not rep.done
+
+
+# ---- a decoder: GDN + attention layers, graph replay ≡ a launch-by-launch host loop --------------------------------
+
+def _decoder(torch, seed):
+    from monolith_mi355.layers import AttnDecoderLayer, DecoderModel, GdnDecoderLayer
+    hidden = 1024
+    layers = [GdnDecoderLayer(hidden=hidden, k_heads=2, v_heads=4, inter=1024, seed=seed),
+              AttnDecoderLayer(hidden=hidden, heads=4, kv_heads=1, ctx=256, inter=1024, seed=seed + 1)]
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    layers[1].fill_cache(40, gen)
+    return DecoderModel(layers, vocab=4096, hidden=hidden, seed=seed)
+
+
+def test_decoder_program_matches_host_loop(torch_gpu):
+    """Model A: host loop with int positions, torch argmax of the FP32 logits. Model B (same seeds): two eager steps
+    then graph replay through the pump. Same tokens; B's state matches A's step count and position."""
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    from monolith_mi355.runtime.step import StepProgram, StepState
+    _say("decoder program")
+    steps = 24
+    a = _decoder(torch, 11)
+    tok, pos, host = 7, 40, []
+    for _ in range(steps):
+        h = kernels.embed(a.embed_table, torch.tensor([tok], dtype=torch.int32, device="cuda"))
+        for layer in a.layers:
+            h = layer.step(h, pos=pos)
+        logits = kernels.gemv(a.lm_head, h, norm_w=a.norm_w, eps=a.eps, out_f32=True)
+        tok = int(torch.argmax(logits[0]).item())
+        host.append(tok)
+        pos += 1
+    b = _decoder(torch, 11)
+    st = StepState(ring_capacity=64)
+    prog = StepProgram(b, st, ctx_cap=256, steps_per_graph=2)
+    st.start(position=40, token=7)
+    first = prog.step_eager(2)
+    rep = prog.run(steps - 2, launches_per_batch=3, in_flight=2)
+    assert first + rep.tokens == host
+    g = st.read()
+    assert g["step"] == steps and g["position"] == 40 + steps and g["error"] == 0
+
+
+def test_decoder_program_stops_at_context_capacity(torch_gpu):
+    torch = torch_gpu
+    from monolith_mi355.runtime.step import StepProgram, StepState
+    b = _decoder(torch, 5)
+    st = StepState(ring_capacity=64)
+    prog = StepProgram(b, st, ctx_cap=50, steps_per_graph=2)
+    st.start(position=40, token=1)
+    prog.step_eager(2)
+    rep = prog.run(40, launches_per_batch=2, in_flight=2)
+    g = st.read()
+    assert g["error"] == 2 and g["done"] == 1 and g["position"] == 50 and len(rep.tokens) == 8
