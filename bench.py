@@ -7,8 +7,10 @@ a Gated DeltaNet mixer (16 key / 48 value heads of 128, conv 4; in_proj 16480×5
 and the NVFP4 gated MLP of BASELINE configs[1] (gate|up 2×17408×5120 with silu·mul, down 5120×17408 with the
 residual). ``value`` is that layer's algorithmic HBM bytes ÷ its step time at M = 1. Beside it: the same layer at
 M = 8, the gated-GQA layer (24 q / 4 KV heads of 128, int8 KV cache at a 32K context; configs[2]) at M = 1 and 8,
-and the MLP alone; and the FP8 E4M3 GEMV (the 27B checkpoint's format for its mixer projections) at the
-GDN in_proj shape with its fused norm, M = 1 and 8.
+and the MLP alone; the FP8 E4M3 GEMV (the 27B checkpoint's format for its mixer projections) at the
+GDN in_proj shape with its fused norm, M = 1 and 8; and the GPU-resident token loop (embedding, a GDN and an
+attention layer, the BF16 LM head over a 248320-token vocabulary, argmax and advance, replayed as a graph by the
+native pump; wall time per token).
 
 One step = one layer forward over one token batch. Weights, states and KV caches are resident in HBM before the
 timed region; the step rotates over ``--layers`` distinct layer instances (≥ 2 GB in all), so the 256 MB MALL
@@ -43,7 +45,7 @@ def parse():
     p.add_argument("--layers", type=int, default=10, help="distinct layer instances the steps rotate over")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--only", choices=["gdn", "attn", "mlp", "gateup", "fp8", "copy"], default=None,
+    p.add_argument("--only", choices=["gdn", "attn", "mlp", "gateup", "fp8", "loop", "copy"], default=None,
                    help="time one workload only (profiling runs; copy = a 256 MiB device copy, the counter reference)")
     return p.parse_args()
 
@@ -154,6 +156,29 @@ def main():
                 out[f"attn_m{m}"] = (ms, attn[0].bytes_per_step(m, pos))
             del attn
 
+        if args.only in (None, "loop"):
+            # the GPU-resident token loop: embed → GDN layer → attention layer (32K context) → final norm + BF16
+            # lm_head (248320×5120) → argmax → advance, replayed as a graph of 2 steps by the native pump
+            from monolith_mi355.layers import DecoderModel
+            from monolith_mi355.runtime.step import StepProgram, StepState
+            layers = [GdnDecoderLayer(seed=70, device=dev), AttnDecoderLayer(seed=71, ctx=CTX, device=dev)]
+            layers[1].fill_cache(CTX - 512, gen)
+            model = DecoderModel(layers, vocab=248320, hidden=5120, device=dev)
+            st = StepState(ring_capacity=4096, device=dev)
+            prog = StepProgram(model, st, ctx_cap=CTX, steps_per_graph=2)
+            start = CTX - 512
+            st.start(position=start, token=11)
+            prog.step_eager(2)
+            st.start(position=start, token=11)
+            prog.run(32, launches_per_batch=8, in_flight=2)                    # warm
+            st.start(position=start, token=11)
+            rep = prog.run(256, launches_per_batch=8, in_flight=2)
+            loop_ms = rep.wall_ms / rep.steps_submitted
+            out["loop"] = (loop_ms, model.step_bytes(start + 128))
+            loop_info = {"tokens": len(rep.tokens), "gpu_ms_per_token": round(rep.gpu_ms / rep.steps_submitted, 5),
+                         "host_busy_fraction": round(rep.host_busy_ms / rep.wall_ms, 4)}
+            del prog, model, layers
+
     def rate(key):
         ms, b = out[key]
         gbs = b / (ms * 1e-3) / 1e9
@@ -203,6 +228,9 @@ def main():
         "mlp_m8": entry("mlp_m8", 8),
         "fp8_in_proj_m1": entry("fp8_m1", 1),
         "fp8_in_proj_m8": entry("fp8_m8", 8),
+        "token_loop_2layers_ctx32k": dict(entry("loop", 1), **loop_info,
+                                          workload="embed + GDN layer + attention layer (32K) + BF16 lm_head 248320 "
+                                                   "+ argmax + advance, graph replay through the native pump"),
         "roofline": {"kernel": "gemv_row (NVFP4 gate|up 34816x5120, silu_mul, M=1)", "bound": "hbm",
                      "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,

@@ -279,7 +279,11 @@ typedef struct mi_argmax_desc {
   const void* logits;
   int32_t ld, f32;            /* f32: 1 FP32 logits, 0 BF16 */
   int32_t* ids;               /* device [t] */
+  void* workspace;            /* optional device buffer of mi_argmax_workspace_bytes, zeroed once before its first use
+                                 (its arrival counters return to zero after every call); NULL: the library's own */
+  size_t workspace_bytes;
 } mi_argmax_desc;
+size_t mi_argmax_workspace_bytes(const mi_argmax_desc* d);
 int mi_argmax(const mi_argmax_desc* d, void* stream);
 
 /* advance (kernels/common/advance.metal:15-37): the serial op that closes a step. Unless done: while prefill_left > 0

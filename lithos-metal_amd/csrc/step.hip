@@ -7,6 +7,7 @@
 
 #include <chrono>
 #include <deque>
+#include <mutex>
 #include <vector>
 
 static_assert(sizeof(mi_step_state) == 272, "mi_step_state: the 272-byte layout");
@@ -14,7 +15,7 @@ static_assert(sizeof(mi_step_state) == 272, "mi_step_state: the 272-byte layout"
 namespace {
 
 constexpr int EMBED_THREADS = 256;
-constexpr int ARGMAX_THREADS = 1024;
+constexpr int ARGMAX_THREADS = 256;
 
 // one block per (token, 2048-column span): 8 BF16 per thread, 16-byte loads
 __global__ __launch_bounds__(EMBED_THREADS) void embed_rows(mi_embed_desc d) {
@@ -31,35 +32,97 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
   return v > bv || (v == bv && i < bi);          // NaN compares false: never replaces a number
 }
 
-// one block per row: strided scan, then a tree over the block in LDS (deterministic: the order is fixed)
-__global__ __launch_bounds__(ARGMAX_THREADS) void argmax_rows(mi_argmax_desc d) {
-  __shared__ float sv[ARGMAX_THREADS];
-  __shared__ int si[ARGMAX_THREADS];
-  const int row = blockIdx.x, tid = threadIdx.x;
+// The order "larger value, then lower index" over the numbers is total, so combining partial results in any order
+// gives the same answer: the spans of a row run in parallel and the last one to finish folds them.
+constexpr int ARGMAX_SPAN = ARGMAX_THREADS * 16;   // logits per workgroup
+constexpr int ARGMAX_MAX_SPANS = 256;
+constexpr size_t ARGMAX_COUNTERS = 256;            // bytes: 16 per-row arrival counters, padded
+
+struct ArgmaxPartial { float v; int i; };
+
+__device__ __forceinline__ void block_best(float& bv, int& bi, float* sv, int* si) {
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o);
+    const int oi = __shfl_xor(bi, o);
+    if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  }
+  const int w = threadIdx.x / 64;
+  if ((threadIdx.x & 63) == 0) { sv[w] = bv; si[w] = bi; }
+  __syncthreads();
+  bv = sv[0];
+  bi = si[0];
+  for (int k = 1; k < ARGMAX_THREADS / 64; ++k)
+    if (better(sv[k], si[k], bv, bi)) { bv = sv[k]; bi = si[k]; }
+}
+
+// grid (spans, rows): each workgroup scans ARGMAX_SPAN logits of one row with 16-byte loads, publishes its best,
+// and the last workgroup of the row to arrive folds the row's partials and resets the row's counter
+__global__ __launch_bounds__(ARGMAX_THREADS) void argmax_spans(mi_argmax_desc d, uint32_t* counters,
+                                                               ArgmaxPartial* part) {
+  __shared__ float sv[ARGMAX_THREADS / 64];
+  __shared__ int si[ARGMAX_THREADS / 64];
+  __shared__ int last;
+  const int row = blockIdx.y, nb = gridDim.x, tid = threadIdx.x;
+  const int lo = blockIdx.x * ARGMAX_SPAN, hi = min(lo + ARGMAX_SPAN, d.vocab);
   float bv = -INFINITY;
   int bi = 0x7FFFFFFF;
   if (d.f32) {
     const float* p = static_cast<const float*>(d.logits) + (long long)row * d.ld;
-    for (int i = tid; i < d.vocab; i += ARGMAX_THREADS)
-      if (better(p[i], i, bv, bi)) { bv = p[i]; bi = i; }
+    const bool vec = ((reinterpret_cast<uintptr_t>(p) | (uintptr_t)lo * 4) & 15) == 0;
+    for (int c = lo + tid * 4; c < hi; c += ARGMAX_THREADS * 4) {
+      float v[4];
+      if (vec && c + 4 <= hi) {
+        const float4 q = *reinterpret_cast<const float4*>(p + c);
+        v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+      } else {
+        for (int e = 0; e < 4; ++e) v[e] = c + e < hi ? p[c + e] : NAN;
+      }
+      for (int e = 0; e < 4; ++e)
+        if (better(v[e], c + e, bv, bi)) { bv = v[e]; bi = c + e; }
+    }
   } else {
     const uint16_t* p = static_cast<const uint16_t*>(d.logits) + (long long)row * d.ld;
-    for (int i = tid; i < d.vocab; i += ARGMAX_THREADS) {
-      const float v = bf16_bits_to_f32(p[i]);
-      if (better(v, i, bv, bi)) { bv = v; bi = i; }
+    const bool vec = ((reinterpret_cast<uintptr_t>(p) | (uintptr_t)lo * 2) & 15) == 0;
+    for (int c = lo + tid * 8; c < hi; c += ARGMAX_THREADS * 8) {
+      uint32_t w[4];
+      if (vec && c + 8 <= hi) {
+        const uint4 q = *reinterpret_cast<const uint4*>(p + c);
+        w[0] = q.x; w[1] = q.y; w[2] = q.z; w[3] = q.w;
+      } else {
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t a = c + 2 * e < hi ? p[c + 2 * e] : 0x7FC0u;          // past the end: NaN
+          const uint32_t b = c + 2 * e + 1 < hi ? p[c + 2 * e + 1] : 0x7FC0u;
+          w[e] = a | (b << 16);
+        }
+      }
+      for (int e = 0; e < 4; ++e) {
+        const float v0 = __uint_as_float(w[e] << 16), v1 = __uint_as_float(w[e] & 0xFFFF0000u);
+        if (better(v0, c + 2 * e, bv, bi)) { bv = v0; bi = c + 2 * e; }
+        if (better(v1, c + 2 * e + 1, bv, bi)) { bv = v1; bi = c + 2 * e + 1; }
+      }
     }
   }
-  sv[tid] = bv;
-  si[tid] = bi;
+  block_best(bv, bi, sv, si);
+  if (tid == 0) {
+    part[row * nb + blockIdx.x] = ArgmaxPartial{bv, bi};
+    __threadfence();
+    last = atomicAdd(&counters[row], 1u) == (uint32_t)(nb - 1);
+  }
   __syncthreads();
-  for (int s = ARGMAX_THREADS / 2; s > 0; s >>= 1) {
-    if (tid < s && better(sv[tid + s], si[tid + s], sv[tid], si[tid])) {
-      sv[tid] = sv[tid + s];
-      si[tid] = si[tid + s];
-    }
-    __syncthreads();
+  if (!last) return;
+  __threadfence();
+  bv = -INFINITY;
+  bi = 0x7FFFFFFF;
+  for (int k = tid; k < nb; k += ARGMAX_THREADS) {
+    const ArgmaxPartial q = part[row * nb + k];
+    if (better(q.v, q.i, bv, bi)) { bv = q.v; bi = q.i; }
   }
-  if (tid == 0) d.ids[row] = si[0] == 0x7FFFFFFF ? -1 : si[0];  // no number in the row
+  __syncthreads();                                  // sv / si are reused
+  block_best(bv, bi, sv, si);
+  if (tid == 0) {
+    d.ids[row] = bi == 0x7FFFFFFF ? -1 : bi;        // no number in the row
+    atomicExch(&counters[row], 0u);
+  }
 }
 
 __device__ __forceinline__ void publish(const mi_advance_desc& d, const mi_step_state* st) {
@@ -101,6 +164,31 @@ __global__ __launch_bounds__(64) void advance_step(mi_advance_desc d) {
     if (tok == d.eos[i]) st->done = 1;
   if (d.ctx_cap && st->position >= d.ctx_cap) { st->error = 2; st->done = 1; }
   publish(d, st);
+}
+
+int argmax_spans_of(int vocab) { return (vocab + ARGMAX_SPAN - 1) / ARGMAX_SPAN; }
+
+// the library's argmax workspace (per device, grown on demand, zeroed when allocated: the kernels keep its counters
+// at zero); calls sharing it must be ordered on one stream
+std::mutex g_am_mu;
+std::vector<std::pair<void*, size_t>> g_am;
+
+int argmax_workspace(size_t bytes, void** out) {
+  int dev = 0;
+  MI_TRY_HIP(hipGetDevice(&dev), "hipGetDevice");
+  std::lock_guard<std::mutex> lk(g_am_mu);
+  if ((int)g_am.size() <= dev) g_am.resize(dev + 1, {nullptr, 0});
+  auto& w = g_am[dev];
+  if (w.second < bytes) {
+    const size_t grow = bytes < 64 * 1024 ? 64 * 1024 : bytes;
+    if (w.first) MI_TRY_HIP(hipFree(w.first), "hipFree(argmax workspace)");
+    w = {nullptr, 0};
+    MI_TRY_HIP(hipMalloc(&w.first, grow), "hipMalloc(argmax workspace)");
+    MI_TRY_HIP(hipMemset(w.first, 0, grow), "hipMemset(argmax workspace)");
+    w.second = grow;
+  }
+  *out = w.first;
+  return MI_OK;
 }
 
 double now_ms() {
@@ -160,7 +248,12 @@ int mi_runner_run(mi_runner_desc* d, mi_runner_stats* st) {
     Batch& b = pool[pending.front()];
     pending.pop_front();
     const double w = now_ms();
-    hipError_t e = hipEventSynchronize(b.b);
+    // poll with short sleeps: the pump thread stays idle while the GPU works (hipEventSynchronize spins)
+    hipError_t e;
+    while ((e = hipEventQuery(b.b)) == hipErrorNotReady) {
+      const timespec nap{0, 20000};
+      nanosleep(&nap, nullptr);
+    }
     st->wait_ms += now_ms() - w;
     if (e != hipSuccess && err == hipSuccess) err = e;
     float ms = 0.f;
@@ -207,10 +300,27 @@ int mi_embed(const mi_embed_desc* d, void* stream) {
   return MI_OK;
 }
 
+size_t mi_argmax_workspace_bytes(const mi_argmax_desc* d) {
+  if (!d || d->t < 1 || d->vocab < 1) return 0;
+  return ARGMAX_COUNTERS + (size_t)d->t * argmax_spans_of(d->vocab) * sizeof(ArgmaxPartial);
+}
+
 int mi_argmax(const mi_argmax_desc* d, void* stream) {
   MI_REQUIRE(d && d->logits && d->ids, "mi_argmax: null pointer");
   MI_REQUIRE(d->t >= 1 && d->t <= 16 && d->vocab > 0 && d->ld >= d->vocab, "mi_argmax: bad shape");
-  hipLaunchKernelGGL(argmax_rows, dim3(d->t), dim3(ARGMAX_THREADS), 0, static_cast<hipStream_t>(stream), *d);
+  const int nb = argmax_spans_of(d->vocab);
+  MI_REQUIRE(nb <= ARGMAX_MAX_SPANS, "mi_argmax: vocab %d exceeds %d", d->vocab, ARGMAX_MAX_SPANS * ARGMAX_SPAN);
+  const size_t need = mi_argmax_workspace_bytes(d);
+  void* ws = d->workspace;
+  if (ws) {
+    MI_REQUIRE(d->workspace_bytes >= need, "mi_argmax: workspace %zu B < %zu B", d->workspace_bytes, need);
+  } else if (int rc = argmax_workspace(need, &ws)) {
+    return rc;
+  }
+  auto* counters = static_cast<uint32_t*>(ws);
+  auto* part = reinterpret_cast<ArgmaxPartial*>(static_cast<char*>(ws) + ARGMAX_COUNTERS);
+  hipLaunchKernelGGL(argmax_spans, dim3(nb, d->t), dim3(ARGMAX_THREADS), 0, static_cast<hipStream_t>(stream), *d,
+                     counters, part);
   MI_TRY_HIP(hipGetLastError(), "argmax launch");
   return MI_OK;
 }

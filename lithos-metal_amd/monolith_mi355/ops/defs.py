@@ -25,6 +25,11 @@ GDN_COMMIT = _op("gdn_commit", OpClass.MAP, "heads", "mi_gdn_step", commit=1)
 MOE_ROUTE = _op("moe_route", OpClass.MAP, "rows", "mi_moe_route")
 MOE_GEMV = _op("moe_gemv", OpClass.MAP, "rows", "mi_gemv", grouped=1)
 MOE_COMBINE = _op("moe_combine", OpClass.MAP, "rows", "mi_moe_combine")
+EMBED = _op("embed", OpClass.MAP, "rows", "mi_embed")                       # ops/embed.py:1-7
+ARGMAX = _op("argmax", OpClass.REDUCE, "span", "mi_argmax")                 # ops/sample.py:9
 
 DECODE_LAYER_OPS = ("gemv", "rmsnorm_stat", "norm_apply", "gqa_decode", "gqa_merge", "gdn_mixer", "gdn_norm",
                     "gdn_commit", "moe_route", "moe_gemv", "moe_combine", "lm_head")
+
+# the token loop around the layers; the program's tail (the advance, compiler/emit.py:1459-1462) is mi_advance
+STEP_OPS = ("embed", "argmax")

@@ -56,7 +56,15 @@ def _combine(h, weights, shared=None, shared_gate=None, residual=None, *, top_k,
                                out=out, stream=stream)
 
 
-HANDLERS = {"gemv": _gemv, "lm_head": _lm_head, "gqa_decode": _gqa, "gdn_mixer": _gdn, "gdn_commit": _gdn_commit,
+def _embed(tokens, table, *, t=None, out=None, stream=None, **_):
+    return kernels.embed(table, tokens, t=t, out=out, stream=stream)
+
+
+def _argmax(logits, *, out=None, stream=None, **_):
+    return kernels.argmax(logits, out=out, stream=stream)
+
+
+HANDLERS = {"embed": _embed, "argmax": _argmax, "gemv": _gemv, "lm_head": _lm_head, "gqa_decode": _gqa, "gdn_mixer": _gdn, "gdn_commit": _gdn_commit,
             "moe_route": _route, "moe_gemv": _moe_gemv, "moe_combine": _combine}
 
 

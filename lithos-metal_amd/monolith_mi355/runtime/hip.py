@@ -90,7 +90,7 @@ class MiEmbedDesc(C.Structure):
 
 class MiArgmaxDesc(C.Structure):
     _fields_ = [("t", C.c_int32), ("vocab", C.c_int32), ("logits", C.c_void_p), ("ld", C.c_int32),
-                ("f32", C.c_int32), ("ids", C.c_void_p)]
+                ("f32", C.c_int32), ("ids", C.c_void_p), ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t)]
 
 
 class MiAdvanceDesc(C.Structure):
@@ -148,6 +148,7 @@ SIGNATURES = {
     "mi_moe_route": (C.c_int, [C.POINTER(MiMoeRouteDesc), _VP]),
     "mi_moe_combine": (C.c_int, [C.POINTER(MiMoeCombineDesc), _VP]),
     "mi_embed": (C.c_int, [C.POINTER(MiEmbedDesc), _VP]),
+    "mi_argmax_workspace_bytes": (_SZ, [C.POINTER(MiArgmaxDesc)]),
     "mi_argmax": (C.c_int, [C.POINTER(MiArgmaxDesc), _VP]),
     "mi_advance": (C.c_int, [C.POINTER(MiAdvanceDesc), _VP]),
     "mi_runner_run": (C.c_int, [C.POINTER(MiRunnerDesc), C.POINTER(MiRunnerStats)]),

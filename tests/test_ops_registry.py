@@ -25,11 +25,11 @@ def test_hot_path_ops_bound_to_exported_entry_points():
     import re
     from pathlib import Path
     from monolith_mi355.ops import OPS, PROFILE, check_coverage
-    from monolith_mi355.ops.defs import DECODE_LAYER_OPS
-    check_coverage(DECODE_LAYER_OPS)
+    from monolith_mi355.ops.defs import DECODE_LAYER_OPS, STEP_OPS
+    check_coverage(DECODE_LAYER_OPS + STEP_OPS)
     header = (Path(__file__).resolve().parents[1] / "include" / "lithos_mi355.h").read_text()
     declared = set(re.findall(r"\b(mi_[a-z0-9_]+)\s*\(", header))
-    for kind in DECODE_LAYER_OPS:
+    for kind in DECODE_LAYER_OPS + STEP_OPS:
         assert OPS[kind].binding_for(PROFILE).kernel in declared, kind
 
 

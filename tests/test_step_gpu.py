@@ -50,6 +50,35 @@ def test_argmax_all_nan_row(torch_gpu):
     assert kernels.argmax(x).cpu().tolist() == [-1, 17]
 
 
+def test_argmax_repeated_calls_and_caller_workspace(torch_gpu):
+    """The arrival counters return to zero: consecutive calls (rows, vocab and dtype varying) stay exact, also with
+    a caller-owned zeroed workspace."""
+    torch = torch_gpu
+    import ctypes as C
+    from monolith_mi355 import kernels
+    from monolith_mi355.runtime import hip
+    rng = np.random.default_rng(9)
+    for i, (t, v) in enumerate([(1, 248320), (16, 70000), (3, 4097), (8, 248320), (1, 5)]):
+        x = rng.standard_normal((t, v)).astype(np.float32)
+        logits = torch.from_numpy(x).cuda() if i % 2 == 0 else to_dev_bf16(torch, x)
+        ref = O.argmax(x if i % 2 == 0 else from_dev_bf16(logits))
+        assert kernels.argmax(logits).cpu().numpy().tolist() == ref.tolist(), (t, v)
+    x = torch.randn(4, 100000, device="cuda")
+    ids = torch.empty(4, dtype=torch.int32, device="cuda")
+    d = hip.MiArgmaxDesc(t=4, vocab=100000, logits=hip.ptr(x), ld=100000, f32=1, ids=hip.ptr(ids))
+    need = hip.load().mi_argmax_workspace_bytes(C.byref(d))
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    d.workspace, d.workspace_bytes = hip.ptr(ws), need
+    for _ in range(3):
+        x.normal_()
+        hip.call("mi_argmax", C.byref(d), hip.stream_handle(None))
+        assert ids.cpu().tolist() == O.argmax(x.cpu().numpy()).tolist()
+    assert int(ws[:64].view(torch.int32).abs().sum()) == 0          # counters back at zero
+    d.workspace_bytes = need - 1
+    with pytest.raises(hip.MiError):
+        hip.call("mi_argmax", C.byref(d), hip.stream_handle(None))
+
+
 def test_embed(torch_gpu):
     torch = torch_gpu
     from monolith_mi355 import kernels
