@@ -302,6 +302,45 @@ typedef struct mi_advance_desc {
 } mi_advance_desc;
 int mi_advance(const mi_advance_desc* d, void* stream);
 
+/* verify_select (kernels/common/spec_ops.metal:108-146): one thread. Unless done: the drafter's context grows by the
+ * injected rows (lm: becomes position + gamma, or position in a prefill chunk), n_inject = 0; outside a prefill chunk
+ * the block's drafts and confidences go into the state (and conf_log[(step % log_cap) * 16 + k] when log_cap > 0),
+ * and the verify length L ≤ min(gamma, t_max − 1) (and ≤ ctx_cap − position − 1; position ≥ ctx_cap: error 2 + done)
+ * is chosen — mode 0: the leading drafts with confidence ≥ threshold (threshold ≤ 0: all), mode 1: argmax over l of
+ * (1 + Σ_{i≤l} Π_{j≤i} c_j) / cost[l], mode 2: L = threshold — then pending_tokens = [anchor, d_0 … d_{L−1}],
+ * t_this_step = 1 + L, gamma and verify_len recorded. */
+typedef struct mi_verify_select_desc {
+  mi_step_state* state;       /* device */
+  const int32_t* drafts;      /* device [gamma] */
+  const float* conf;          /* device [gamma] */
+  uint32_t gamma, t_max, mode;
+  float threshold;
+  float cost[16];
+  float* conf_log;            /* device [log_cap][16], optional */
+  uint32_t log_cap, ctx_cap, lm;
+} mi_verify_select_desc;
+int mi_verify_select(const mi_verify_select_desc* d, void* stream);
+
+/* accept_scan (kernels/common/spec_ops.metal:148-195): one thread, the closing serial op of a speculative step (in
+ * place of the advance). Unless done: a prefill chunk advances the position by t_this_step and marks its rows for
+ * injection; otherwise the target's tokens are compared with the drafts the step fed (pending_tokens =
+ * [prompt tail …, anchor, d_0 … d_{L−1}], base = t − 1 − L): the matching prefix and the bonus token after it go to
+ * the ring (stopping after the first EOS; not enough ring room: error 1 + done, nothing written), position advances
+ * by base + committed, anchor = the last committed token, n_inject = checkpoint_index = base + committed (lm: the
+ * committed rows the drafter has not seen), verify_len = 0, t_this_step = 1; log[step % log_cap] = (committed << 16)
+ * | (L << 8) | accepted ((t << 16) | 0xFFFF for a prefill chunk); done at EOS / stop_at, error 2 at ctx_cap. */
+typedef struct mi_accept_scan_desc {
+  mi_step_state* state;       /* device */
+  const int32_t* tokens;      /* device: the target's argmax per row */
+  uint64_t* ring;             /* pinned host, ring_cap slots */
+  uint32_t ring_cap, ctx_cap, lm;
+  int32_t n_eos, eos[8];
+  uint32_t* log;              /* device [log_cap], optional */
+  uint32_t log_cap;
+  uint32_t* host_ctl;         /* optional pinned host words, as for mi_advance */
+} mi_accept_scan_desc;
+int mi_accept_scan(const mi_accept_scan_desc* d, void* stream);
+
 /* The host pump (runtime/src/metal_core.mm:256-386 `Runner::run` / `drain`): replay a captured step graph up to
  * max_launches times, launches_per_batch per batch with at most in_flight batches queued; after each completed batch
  * drain the ring by sequence tag into tokens[] and publish the tail (host_ctl[0], copied into state->ring_tail ahead

@@ -125,10 +125,10 @@ __global__ __launch_bounds__(ARGMAX_THREADS) void argmax_spans(mi_argmax_desc d,
   }
 }
 
-__device__ __forceinline__ void publish(const mi_advance_desc& d, const mi_step_state* st) {
-  if (d.host_ctl) {                                 // posted writes to pinned host memory: the pump polls these
-    __atomic_store_n(&d.host_ctl[2], st->error, __ATOMIC_RELAXED);
-    __atomic_store_n(&d.host_ctl[1], st->done, __ATOMIC_RELEASE);
+__device__ __forceinline__ void publish_ctl(uint32_t* ctl, const mi_step_state* st) {
+  if (ctl) {                                        // posted writes to pinned host memory: the pump polls these
+    __atomic_store_n(&ctl[2], st->error, __ATOMIC_RELAXED);
+    __atomic_store_n(&ctl[1], st->done, __ATOMIC_RELEASE);
   }
 }
 
@@ -142,7 +142,7 @@ __global__ __launch_bounds__(64) void advance_step(mi_advance_desc d) {
     st->position += t;
     st->step += 1;
     if (d.ctx_cap && st->position >= d.ctx_cap) { st->error = 2; st->done = 1; }
-    publish(d, st);
+    publish_ctl(d.host_ctl, st);
     return;
   }
   const int32_t tok = d.tokens[t > 0 ? t - 1 : 0];
@@ -150,7 +150,7 @@ __global__ __launch_bounds__(64) void advance_step(mi_advance_desc d) {
   if (head - st->ring_tail >= d.ring_cap) {         // the host has not drained: overflow
     st->error = 1;
     st->done = 1;
-    publish(d, st);
+    publish_ctl(d.host_ctl, st);
     return;
   }
   d.ring[head % d.ring_cap] = ((uint64_t)(head + 1) << 32) | (uint32_t)tok;
@@ -163,7 +163,7 @@ __global__ __launch_bounds__(64) void advance_step(mi_advance_desc d) {
   for (int i = 0; i < d.n_eos; ++i)
     if (tok == d.eos[i]) st->done = 1;
   if (d.ctx_cap && st->position >= d.ctx_cap) { st->error = 2; st->done = 1; }
-  publish(d, st);
+  publish_ctl(d.host_ctl, st);
 }
 
 int argmax_spans_of(int vocab) { return (vocab + ARGMAX_SPAN - 1) / ARGMAX_SPAN; }
@@ -189,6 +189,110 @@ int argmax_workspace(size_t bytes, void** out) {
   }
   *out = w.first;
   return MI_OK;
+}
+
+__global__ __launch_bounds__(64) void verify_select_step(mi_verify_select_desc d) {
+  if (threadIdx.x != 0) return;
+  mi_step_state* st = d.state;
+  if (st->done) return;
+  if (d.lm) st->drafter_ctx_len = st->position + (st->prefill_left > 0 ? 0u : d.gamma);
+  else st->drafter_ctx_len += st->n_inject;
+  st->n_inject = 0;
+  if (st->prefill_left > 0) return;                 // the host feeds the next prompt chunk
+  for (uint32_t k = 0; k < d.gamma; ++k) {
+    st->draft_tokens[k] = d.drafts[k];
+    st->confidence[k] = d.conf[k];
+    if (d.log_cap) d.conf_log[(st->step % d.log_cap) * 16 + k] = d.conf[k];
+  }
+  uint32_t lmax = min(d.gamma, d.t_max - 1);
+  if (d.ctx_cap) {                                  // the verify rows position … position + L must fit the caches
+    if (st->position >= d.ctx_cap) { st->error = 2; st->done = 1; return; }
+    lmax = min(lmax, d.ctx_cap - st->position - 1);
+  }
+  uint32_t L = 0;
+  if (d.mode == 2) {
+    L = min((uint32_t)fmaxf(d.threshold, 0.f), lmax);
+  } else if (d.mode == 1) {
+    float survive = 1.f, expected = 1.f, best = 1.f / d.cost[0];
+    for (uint32_t l = 1; l <= lmax; ++l) {
+      survive *= d.conf[l - 1];
+      expected += survive;
+      const float score = expected / d.cost[l];
+      if (score > best) { best = score; L = l; }
+    }
+  } else if (d.threshold <= 0.f) {
+    L = lmax;
+  } else {
+    while (L < lmax && d.conf[L] >= d.threshold) ++L;
+  }
+  st->gamma = d.gamma;
+  st->verify_len = L;
+  st->pending_tokens[0] = st->anchor;
+  for (uint32_t k = 0; k < L; ++k) st->pending_tokens[k + 1] = d.drafts[k];
+  st->t_this_step = 1 + L;
+}
+
+__device__ __forceinline__ bool is_eos(const int32_t* eos, int n, int32_t tok) {
+  bool hit = false;
+  for (int i = 0; i < n; ++i) hit |= tok == eos[i];
+  return hit;
+}
+
+__global__ __launch_bounds__(64) void accept_scan_step(mi_accept_scan_desc d) {
+  if (threadIdx.x != 0) return;
+  mi_step_state* st = d.state;
+  if (st->done) return;
+  const uint32_t t = st->t_this_step;
+  if (st->prefill_left > 0) {                       // a prompt chunk: nothing to verify; its rows are injected next
+    if (d.log_cap) d.log[st->step % d.log_cap] = (t << 16) | 0xFFFFu;
+    st->position += t;
+    st->step += 1;
+    st->n_inject = t;
+    st->checkpoint_index = t;
+    st->n_chain = 0;
+    if (d.ctx_cap && st->position >= d.ctx_cap) { st->error = 2; st->done = 1; }
+    publish_ctl(d.host_ctl, st);
+    return;
+  }
+  const uint32_t L = st->verify_len;
+  const uint32_t base = t - 1 - L;                  // the anchor's row
+  uint32_t acc = 0;
+  while (acc < L && d.tokens[base + acc] == st->pending_tokens[base + acc + 1]) ++acc;
+  const int32_t bonus = d.tokens[base + acc];
+  uint32_t head = st->ring_head;
+  if (head + acc + 1 - st->ring_tail > d.ring_cap) {  // not enough ring room: the host fell behind
+    st->error = 1;
+    st->done = 1;
+    publish_ctl(d.host_ctl, st);
+    return;
+  }
+  uint32_t committed = 0;
+  int32_t last = bonus;
+  bool stop = false;
+  for (uint32_t k = 0; k <= acc; ++k) {
+    const int32_t tok = k < acc ? st->pending_tokens[base + k + 1] : bonus;
+    d.ring[head % d.ring_cap] = ((uint64_t)(head + 1) << 32) | (uint32_t)tok;
+    ++head;
+    ++committed;
+    last = tok;
+    if (is_eos(d.eos, d.n_eos, tok)) { stop = true; break; }   // nothing after the first EOS is committed
+  }
+  if (d.log_cap) d.log[st->step % d.log_cap] = (committed << 16) | (L << 8) | acc;
+  st->ring_head = head;
+  if (st->stop_at && head >= st->stop_at) stop = true;
+  st->accepted = acc;
+  st->anchor = last;
+  st->position += base + committed;
+  st->step += 1;
+  st->verify_len = 0;
+  st->t_this_step = 1;
+  st->n_inject = base + committed;
+  st->checkpoint_index = base + committed;
+  st->n_chain = 1;
+  if (d.lm) st->n_inject = st->position > st->drafter_ctx_len ? st->position - st->drafter_ctx_len : 0;
+  if (stop) st->done = 1;
+  if (d.ctx_cap && st->position >= d.ctx_cap) { st->error = 2; st->done = 1; }
+  publish_ctl(d.host_ctl, st);
 }
 
 double now_ms() {
@@ -330,6 +434,28 @@ int mi_advance(const mi_advance_desc* d, void* stream) {
   MI_REQUIRE(d->ring_cap >= 1 && d->n_eos >= 0 && d->n_eos <= 8, "mi_advance: ring_cap >= 1, n_eos in 0..8");
   hipLaunchKernelGGL(advance_step, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), *d);
   MI_TRY_HIP(hipGetLastError(), "advance launch");
+  return MI_OK;
+}
+
+int mi_verify_select(const mi_verify_select_desc* d, void* stream) {
+  MI_REQUIRE(d && d->state && (d->gamma == 0 || (d->drafts && d->conf)), "mi_verify_select: null pointer");
+  MI_REQUIRE(d->gamma <= MI_STEP_GAMMA_MAX && d->t_max >= 1 && d->t_max <= MI_STEP_T_MAX && d->mode <= 2,
+             "mi_verify_select: gamma <= %d, t_max in 1..%d, mode 0..2", MI_STEP_GAMMA_MAX, MI_STEP_T_MAX);
+  MI_REQUIRE(!d->log_cap || d->conf_log, "mi_verify_select: log_cap without conf_log");
+  if (d->mode == 1)
+    for (uint32_t l = 0; l <= d->gamma && l < 16; ++l)
+      MI_REQUIRE(d->cost[l] > 0.f, "mi_verify_select: cost[%u] must be positive", l);
+  hipLaunchKernelGGL(verify_select_step, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), *d);
+  MI_TRY_HIP(hipGetLastError(), "verify_select launch");
+  return MI_OK;
+}
+
+int mi_accept_scan(const mi_accept_scan_desc* d, void* stream) {
+  MI_REQUIRE(d && d->state && d->tokens && d->ring, "mi_accept_scan: null pointer");
+  MI_REQUIRE(d->ring_cap >= 1 && d->n_eos >= 0 && d->n_eos <= 8, "mi_accept_scan: ring_cap >= 1, n_eos in 0..8");
+  MI_REQUIRE(!d->log_cap || d->log, "mi_accept_scan: log_cap without log");
+  hipLaunchKernelGGL(accept_scan_step, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), *d);
+  MI_TRY_HIP(hipGetLastError(), "accept_scan launch");
   return MI_OK;
 }
 

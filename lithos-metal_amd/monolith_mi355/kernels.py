@@ -403,12 +403,58 @@ def advance(state, tokens, ring, ring_cap: int, *, eos=(), ctx_cap: int = 0, hos
     """``advance`` (``kernels/common/advance.metal:15-37``): close a step — publish the last row's token to the ring,
     make it the next step's pending token, move position and step, stop at EOS / ``stop_at`` / the context capacity.
     ``state``: the device step state (int32 tensor of 68 words); ``ring`` / ``host_ctl``: pinned host addresses."""
-    torch = _torch()
-    if state.dtype != torch.int32 or state.numel() * 4 < C.sizeof(hip.MiStepState) or not state.is_cuda:
-        raise ValueError("advance: state must be a device int32 tensor of the step-state size")
+    _check_state(state, "advance")
+    n_eos, eos_arr = _eos_list(eos)
+    d = hip.MiAdvanceDesc(state=hip.ptr(state), tokens=hip.ptr(tokens), ring=hip.ptr(ring), ring_cap=ring_cap,
+                          ctx_cap=ctx_cap, n_eos=n_eos, eos=eos_arr, host_ctl=hip.ptr(host_ctl))
+    hip.call("mi_advance", C.byref(d), hip.stream_handle(stream))
+
+
+def _eos_list(eos):
     eos = [int(e) for e in ([eos] if isinstance(eos, int) else eos) if e is not None and int(e) >= 0]
     if len(eos) > 8:
-        raise ValueError("advance: at most 8 EOS ids")
-    d = hip.MiAdvanceDesc(state=hip.ptr(state), tokens=hip.ptr(tokens), ring=hip.ptr(ring), ring_cap=ring_cap,
-                          ctx_cap=ctx_cap, n_eos=len(eos), eos=(C.c_int32 * 8)(*eos), host_ctl=hip.ptr(host_ctl))
-    hip.call("mi_advance", C.byref(d), hip.stream_handle(stream))
+        raise ValueError("at most 8 EOS ids")
+    return len(eos), (C.c_int32 * 8)(*eos)
+
+
+def _check_state(state, name):
+    torch = _torch()
+    if state.dtype != torch.int32 or state.numel() * 4 < C.sizeof(hip.MiStepState) or not state.is_cuda:
+        raise ValueError(f"{name}: state must be a device int32 tensor of the step-state size")
+
+
+def verify_select(state, drafts, conf, *, gamma: int, threshold: float = 0.0, t_max: int = 8, mode: int = 0,
+                  cost=None, conf_log=None, ctx_cap: int = 0, lm: bool = False, stream=None):
+    """``verify_select`` (``ops/draft.py:13-15,27``; ``spec_ops.metal:108-146``): choose the verify length of the next
+    step from the drafter's block (``drafts [γ]`` int32, ``conf [γ]`` float32 on the device) and set its pending
+    tokens. ``mode`` 0 confident prefix (``threshold``), 1 cost-aware (``cost [16]``), 2 fixed L = ``threshold``;
+    ``conf_log [log_cap, 16]`` float32 receives the block's confidences."""
+    torch = _torch()
+    _check_state(state, "verify_select")
+    if not 0 <= gamma <= 15 or not 1 <= t_max <= 16 or mode not in (0, 1, 2):
+        raise ValueError("verify_select: gamma 0..15, t_max 1..16, mode 0..2")
+    if gamma and (drafts.dtype != torch.int32 or drafts.numel() < gamma or conf.dtype != torch.float32
+                  or conf.numel() < gamma):
+        raise ValueError("verify_select: drafts int32 [gamma], conf float32 [gamma]")
+    c = list(cost) if cost is not None else [1.0] * 16
+    if mode == 1 and (len(c) < min(gamma, t_max - 1) + 1 or any(v <= 0 for v in c[: gamma + 1])):
+        raise ValueError("verify_select: cost needs a positive entry per length 0..gamma")
+    log_cap = 0 if conf_log is None else conf_log.numel() // 16
+    d = hip.MiVerifySelectDesc(state=hip.ptr(state), drafts=hip.ptr(drafts), conf=hip.ptr(conf), gamma=gamma,
+                               t_max=t_max, mode=mode, threshold=threshold, cost=(C.c_float * 16)(*c[:16]),
+                               conf_log=hip.ptr(conf_log), log_cap=log_cap, ctx_cap=ctx_cap, lm=int(lm))
+    hip.call("mi_verify_select", C.byref(d), hip.stream_handle(stream))
+
+
+def accept_scan(state, tokens, ring, ring_cap: int, *, eos=(), log=None, ctx_cap: int = 0, lm: bool = False,
+                host_ctl=None, stream=None):
+    """``accept_scan`` (``ops/draft.py:16-18,28``; ``spec_ops.metal:148-195``): the closing serial op of a
+    speculative step — commit the accepted drafts and the bonus token to the ring, advance the state.
+    ``tokens``: the target's argmax per row (device int32); ``ring`` / ``host_ctl``: pinned host addresses;
+    ``log [log_cap]`` int32 receives ``(committed << 16) | (L << 8) | accepted`` per step."""
+    _check_state(state, "accept_scan")
+    n_eos, eos_arr = _eos_list(eos)
+    d = hip.MiAcceptScanDesc(state=hip.ptr(state), tokens=hip.ptr(tokens), ring=hip.ptr(ring), ring_cap=ring_cap,
+                             ctx_cap=ctx_cap, lm=int(lm), n_eos=n_eos, eos=eos_arr, log=hip.ptr(log),
+                             log_cap=0 if log is None else log.numel(), host_ctl=hip.ptr(host_ctl))
+    hip.call("mi_accept_scan", C.byref(d), hip.stream_handle(stream))

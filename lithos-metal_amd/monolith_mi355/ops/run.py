@@ -64,7 +64,19 @@ def _argmax(logits, *, out=None, stream=None, **_):
     return kernels.argmax(logits, out=out, stream=stream)
 
 
-HANDLERS = {"embed": _embed, "argmax": _argmax, "gemv": _gemv, "lm_head": _lm_head, "gqa_decode": _gqa, "gdn_mixer": _gdn, "gdn_commit": _gdn_commit,
+def _verify_select(drafts, conf, *, state, gamma, threshold=0.0, t_max=8, mode=0, cost=None, conf_log=None, ctx_cap=0,
+                   lm=False, stream=None, **_):
+    return kernels.verify_select(state, drafts, conf, gamma=gamma, threshold=threshold, t_max=t_max, mode=mode,
+                                 cost=cost, conf_log=conf_log, ctx_cap=ctx_cap, lm=lm, stream=stream)
+
+
+def _accept_scan(token, *, state, ring, ring_cap, eos=(), log=None, ctx_cap=0, lm=False, host_ctl=None, stream=None,
+                 **_):
+    return kernels.accept_scan(state, token, ring, ring_cap, eos=eos, log=log, ctx_cap=ctx_cap, lm=lm,
+                               host_ctl=host_ctl, stream=stream)
+
+
+HANDLERS = {"embed": _embed, "argmax": _argmax, "verify_select": _verify_select, "accept_scan": _accept_scan, "gemv": _gemv, "lm_head": _lm_head, "gqa_decode": _gqa, "gdn_mixer": _gdn, "gdn_commit": _gdn_commit,
             "moe_route": _route, "moe_gemv": _moe_gemv, "moe_combine": _combine}
 
 

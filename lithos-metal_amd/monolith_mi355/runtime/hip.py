@@ -98,6 +98,18 @@ class MiAdvanceDesc(C.Structure):
                 ("ctx_cap", C.c_uint32), ("n_eos", C.c_int32), ("eos", C.c_int32 * 8), ("host_ctl", C.c_void_p)]
 
 
+class MiVerifySelectDesc(C.Structure):
+    _fields_ = [("state", C.c_void_p), ("drafts", C.c_void_p), ("conf", C.c_void_p), ("gamma", C.c_uint32),
+                ("t_max", C.c_uint32), ("mode", C.c_uint32), ("threshold", C.c_float), ("cost", C.c_float * 16),
+                ("conf_log", C.c_void_p), ("log_cap", C.c_uint32), ("ctx_cap", C.c_uint32), ("lm", C.c_uint32)]
+
+
+class MiAcceptScanDesc(C.Structure):
+    _fields_ = [("state", C.c_void_p), ("tokens", C.c_void_p), ("ring", C.c_void_p), ("ring_cap", C.c_uint32),
+                ("ctx_cap", C.c_uint32), ("lm", C.c_uint32), ("n_eos", C.c_int32), ("eos", C.c_int32 * 8),
+                ("log", C.c_void_p), ("log_cap", C.c_uint32), ("host_ctl", C.c_void_p)]
+
+
 class MiRunnerDesc(C.Structure):
     _fields_ = [("graph_exec", C.c_void_p), ("stream", C.c_void_p), ("state", C.c_void_p), ("ring", C.c_void_p),
                 ("ring_capacity", C.c_uint32), ("host_ctl", C.c_void_p), ("max_launches", C.c_uint32),
@@ -151,6 +163,8 @@ SIGNATURES = {
     "mi_argmax_workspace_bytes": (_SZ, [C.POINTER(MiArgmaxDesc)]),
     "mi_argmax": (C.c_int, [C.POINTER(MiArgmaxDesc), _VP]),
     "mi_advance": (C.c_int, [C.POINTER(MiAdvanceDesc), _VP]),
+    "mi_verify_select": (C.c_int, [C.POINTER(MiVerifySelectDesc), _VP]),
+    "mi_accept_scan": (C.c_int, [C.POINTER(MiAcceptScanDesc), _VP]),
     "mi_runner_run": (C.c_int, [C.POINTER(MiRunnerDesc), C.POINTER(MiRunnerStats)]),
     "mi_host_alloc": (_VP, [_SZ]),
     "mi_host_free": (C.c_int, [_VP]),

@@ -1,13 +1,17 @@
 """CPU restatement of the serial ops that close a decode step — TEST INFRASTRUCTURE ONLY.
 
 ``embed`` (``kernels/common/embed.metal:1-12``, row-major BF16 table), ``argmax`` (``kernels/common/argmax.metal:1-99``),
-``advance`` (``kernels/common/advance.metal:1-37``) and the host ring drain (``runtime/src/metal_core.mm:304-318``),
+``advance`` (``kernels/common/advance.metal:1-37``), the speculative round's ``verify_select`` and ``accept_scan``
+(``kernels/common/spec_ops.metal:108-195``) and the host ring drain (``runtime/src/metal_core.mm:304-318``),
 over a step state held as a dict with the reference's field names (``core/step_state.py:38-63``).
 
 Pinning: ``argmax`` against ``numpy.argmax`` (first occurrence on ties) on NaN-free rows and brute force over tiny
 rows with NaN / ±inf; ``advance`` against the known answers of the reference's ``tests/kernels/test_eos_set.py``
 (stop-token table: done, ring head 1, position 6, slot token) and the toy-program invariants of
-``tests/runtime/test_toy_program.py`` (every token once, in order; overflow → error 1 with a clean prefix).
+``tests/runtime/test_toy_program.py`` (every token once, in order; overflow → error 1 with a clean prefix);
+``verify_select`` and ``accept_scan`` against the known answers of the reference's ``tests/kernels/test_draft_ops.py``
+(``test_verify_select``'s lengths, tokens and bookkeeping; ``test_accept_scan``'s per-case fields) and
+``tests/kernels/test_eos_set.py``'s EOS cases.
 """
 
 from __future__ import annotations
@@ -37,10 +41,20 @@ def argmax(logits: np.ndarray) -> np.ndarray:
     return out
 
 
+STATE_FIELDS = {"step": 0, "position": 0, "kv_len": 0, "t_this_step": 0, "pending_tokens": [0] * 16, "rng_lo": 0,
+                "rng_hi": 0, "anchor": 0, "gamma": 0, "draft_tokens": [0] * 15, "confidence": [0.0] * 15,
+                "verify_len": 0, "accepted": 0, "checkpoint_index": 0, "drafter_ctx_len": 0, "done": 0, "error": 0,
+                "ring_head": 0, "ring_tail": 0, "prefill_left": 0, "n_inject": 0, "stop_at": 0, "n_chain": 0}
+
+
 def new_state(**fields) -> Dict[str, object]:
-    st = {"step": 0, "position": 0, "t_this_step": 1, "pending_tokens": [0] * 16, "done": 0, "error": 0,
-          "ring_head": 0, "ring_tail": 0, "prefill_left": 0, "stop_at": 0}
-    st.update(fields)
+    """A step state with every field of the reference's layout (zero unless given; t_this_step defaults to 1)."""
+    st = {k: (list(v) if isinstance(v, list) else v) for k, v in STATE_FIELDS.items()}
+    st["t_this_step"] = 1
+    for k, v in fields.items():
+        if isinstance(st[k], list):
+            v = list(v) + [0] * (len(st[k]) - len(v))
+        st[k] = v
     return st
 
 
@@ -86,3 +100,112 @@ def drain(ring: np.ndarray, tail: int, out: List[int]) -> int:
             return tail
         out.append(int(np.uint32(v & 0xFFFFFFFF).view(np.int32)))
         tail += 1
+
+
+def verify_select(st: Dict[str, object], drafts: Sequence[int], conf: Sequence[float], *, gamma: int,
+                  threshold: float = 0.0, t_max: int = 8, mode: int = 0, cost: Sequence[float] = (),
+                  conf_log: np.ndarray = None, ctx_cap: int = 0, lm: bool = False) -> None:
+    """``spec_ops.metal:108-146``: the drafter's bookkeeping, then the verify length and the next step's tokens.
+    ``conf`` is taken as float32 (the kernel's arithmetic)."""
+    if st["done"]:
+        return
+    f32 = np.float32
+    if lm:
+        st["drafter_ctx_len"] = st["position"] + (0 if st["prefill_left"] > 0 else gamma)
+    else:
+        st["drafter_ctx_len"] += st["n_inject"]
+    st["n_inject"] = 0
+    if st["prefill_left"] > 0:
+        return
+    c = [f32(v) for v in conf]
+    for k in range(gamma):
+        st["draft_tokens"][k] = int(drafts[k])
+        st["confidence"][k] = float(c[k])
+        if conf_log is not None and conf_log.shape[0]:
+            conf_log[st["step"] % conf_log.shape[0], k] = c[k]
+    lmax = min(gamma, t_max - 1)
+    if ctx_cap:
+        if st["position"] >= ctx_cap:
+            st["error"], st["done"] = 2, 1
+            return
+        lmax = min(lmax, ctx_cap - st["position"] - 1)
+    L = 0
+    if mode == 2:
+        L = min(int(max(f32(threshold), f32(0))), lmax)
+    elif mode == 1:
+        a, e = f32(1), f32(1)
+        best = f32(1) / f32(cost[0])
+        for l in range(1, lmax + 1):
+            a = f32(a * c[l - 1])
+            e = f32(e + a)
+            score = f32(e / f32(cost[l]))
+            if score > best:
+                best, L = score, l
+    elif f32(threshold) <= 0:
+        L = lmax
+    else:
+        while L < lmax and c[L] >= f32(threshold):
+            L += 1
+    st["gamma"], st["verify_len"] = gamma, L
+    st["pending_tokens"][0] = st["anchor"]
+    for k in range(L):
+        st["pending_tokens"][k + 1] = int(drafts[k])
+    st["t_this_step"] = 1 + L
+
+
+def accept_scan(st: Dict[str, object], tokens: Sequence[int], ring: np.ndarray, *, eos: Sequence[int] = (),
+                log: np.ndarray = None, ctx_cap: int = 0, lm: bool = False) -> None:
+    """``spec_ops.metal:148-195``: commit the matching prefix of the drafts and the bonus token, advance the state."""
+    if st["done"]:
+        return
+    t = st["t_this_step"]
+    cap = ring.shape[0]
+    log_cap = 0 if log is None else log.shape[0]
+    if st["prefill_left"] > 0:
+        if log_cap:
+            log[st["step"] % log_cap] = (t << 16) | 0xFFFF
+        st["position"] += t
+        st["step"] += 1
+        st["n_inject"] = st["checkpoint_index"] = t
+        st["n_chain"] = 0
+        if ctx_cap and st["position"] >= ctx_cap:
+            st["error"], st["done"] = 2, 1
+        return
+    L = st["verify_len"]
+    base = t - 1 - L
+    acc = 0
+    while acc < L and int(tokens[base + acc]) == st["pending_tokens"][base + acc + 1]:
+        acc += 1
+    bonus = int(tokens[base + acc])
+    head = st["ring_head"]
+    if head + acc + 1 - st["ring_tail"] > cap:
+        st["error"], st["done"] = 1, 1
+        return
+    stops = set(int(e) for e in eos)
+    committed, last, stop = 0, bonus, False
+    for k in range(acc + 1):
+        tok = st["pending_tokens"][base + k + 1] if k < acc else bonus
+        ring[head % cap] = np.uint64(((head + 1) << 32) | (tok & 0xFFFFFFFF))
+        head += 1
+        committed += 1
+        last = tok
+        if tok in stops:
+            stop = True
+            break
+    if log_cap:
+        log[st["step"] % log_cap] = (committed << 16) | (L << 8) | acc
+    st["ring_head"] = head
+    if st["stop_at"] and head >= st["stop_at"]:
+        stop = True
+    st["accepted"], st["anchor"] = acc, last
+    st["position"] += base + committed
+    st["step"] += 1
+    st["verify_len"], st["t_this_step"] = 0, 1
+    st["n_inject"] = st["checkpoint_index"] = base + committed
+    st["n_chain"] = 1
+    if lm:
+        st["n_inject"] = st["position"] - st["drafter_ctx_len"] if st["position"] > st["drafter_ctx_len"] else 0
+    if stop:
+        st["done"] = 1
+    if ctx_cap and st["position"] >= ctx_cap:
+        st["error"], st["done"] = 2, 1

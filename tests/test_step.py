@@ -98,3 +98,126 @@ def test_embed_oracle_out_of_range_reads_row_zero(rng):
     table = rng.standard_normal((5, 8)).astype(np.float32)
     h = O.embed(table, [3, -1, 5, 0])
     assert np.array_equal(h, table[[3, 0, 0, 0]])
+
+
+# ---- the speculative round's serial ops: the reference's known answers (tests/kernels/test_draft_ops.py:280-317,
+#      378-420 and tests/kernels/test_eos_set.py:27-42) ----------------------------------------------------------------
+
+DRAFTS, CONF = [11, 12, 13, 14, 15], [0.9, 0.6, 0.4, 0.8, 0.1]
+SELECT_BASE = {"anchor": 7, "drafter_ctx_len": 10, "n_inject": 3, "t_this_step": 1}
+
+
+def _select(base=SELECT_BASE, **kw):
+    st = O.new_state(**base)
+    O.verify_select(st, DRAFTS, CONF, gamma=5, **kw)
+    return st
+
+
+def test_verify_select_oracle_known_answers():
+    s = _select(threshold=0.0)
+    assert s["drafter_ctx_len"] == 13 and s["n_inject"] == 0 and s["gamma"] == 5 and s["verify_len"] == 5
+    assert s["t_this_step"] == 6 and s["pending_tokens"][:8] == [7, 11, 12, 13, 14, 15, 0, 0]
+    assert s["draft_tokens"][:5] == DRAFTS and s["confidence"][:5] == pytest.approx(CONF)
+    s = _select(threshold=0.5)
+    assert s["verify_len"] == 2 and s["t_this_step"] == 3 and s["pending_tokens"][:4] == [7, 11, 12, 0]
+    s = _select(threshold=0.0, t_max=3)
+    assert s["verify_len"] == 2 and s["t_this_step"] == 3
+    s = _select(dict(SELECT_BASE, prefill_left=2, t_this_step=8, pending_tokens=[1, 2, 3, 4, 5, 6, 7, 8]))
+    assert s["drafter_ctx_len"] == 13 and s["n_inject"] == 0 and s["t_this_step"] == 8
+    assert s["pending_tokens"][:8] == [1, 2, 3, 4, 5, 6, 7, 8]
+    s = _select(dict(SELECT_BASE, done=1))
+    assert s["drafter_ctx_len"] == 10 and s["n_inject"] == 3
+    cost = [1.0, 1.28, 1.535, 1.79, 2.67, 3.55, 4.4, 5.3]
+    assert _select(mode=1, cost=cost)["verify_len"] == 2
+    log = np.zeros((4, 16), np.float32)
+    s = _select(dict(SELECT_BASE, step=6), threshold=2.0, mode=2, conf_log=log)
+    assert s["verify_len"] == 2 and log[6 % 4, :5].tolist() == pytest.approx(CONF)
+    assert _select(threshold=9.0, mode=2)["verify_len"] == 5 and _select(threshold=9.0, t_max=4, mode=2)["verify_len"] == 3
+    at = dict(SELECT_BASE, position=10)
+    s = _select(at, ctx_cap=13)
+    assert s["verify_len"] == 2 and s["t_this_step"] == 3 and s["error"] == 0 and s["done"] == 0
+    s = _select(at, ctx_cap=11)
+    assert s["verify_len"] == 0 and s["t_this_step"] == 1 and s["error"] == 0
+    s = _select(at, ctx_cap=10)
+    assert s["error"] == 2 and s["done"] == 1 and s["t_this_step"] == 1
+    assert _select(at, ctx_cap=64)["verify_len"] == 5
+
+
+ACCEPT_BASE = dict(position=40, step=5, ring_head=3, ring_tail=1, anchor=9, t_this_step=4, verify_len=3,
+                   pending_tokens=[9, 21, 22, 23])
+
+
+def accept_case(case):
+    """(state fields, tokens, eos, ctx_cap) of the reference's ``test_accept_scan`` cases; ring capacity 16."""
+    st, tokens, eos, ctx_cap = dict(ACCEPT_BASE), [21, 22, 23, 24], [], 0
+    if case == "context_full":
+        ctx_cap = 44
+    elif case == "context_room":
+        ctx_cap = 45
+    elif case == "partial":
+        tokens = [21, 50, 23, 24]
+    elif case == "none":
+        tokens = [51, 22, 23, 24]
+    elif case == "eos_draft":
+        eos = [22]
+    elif case == "eos_bonus":
+        tokens, eos = [21, 50, 23, 24], [50]
+    elif case == "first_token":
+        st.update(t_this_step=3, verify_len=0, pending_tokens=[101, 102, 103], ring_head=0, ring_tail=0)
+        tokens = [31, 32, 33]
+    elif case == "overflow":
+        st.update(ring_head=17, ring_tail=0)
+    elif case == "wrap":
+        st.update(ring_head=15, ring_tail=13)
+    return st, tokens, eos, ctx_cap
+
+
+ACCEPT_CASES = ["all", "partial", "none", "eos_draft", "eos_bonus", "first_token", "overflow", "wrap",
+                "context_full", "context_room"]
+
+
+@pytest.mark.parametrize("case", ACCEPT_CASES)
+def test_accept_scan_oracle_known_answers(case):
+    fields, tokens, eos, ctx_cap = accept_case(case)
+    st, ring, log = O.new_state(**fields), np.zeros(16, np.uint64), np.zeros(64, np.uint32)
+    O.accept_scan(st, tokens, ring, eos=eos, log=log, ctx_cap=ctx_cap)
+    vals = [int(v) & 0xFFFFFFFF for v in ring if v]
+    if case == "context_full":
+        assert st["error"] == 2 and st["done"] == 1 and st["position"] == 44 and st["ring_head"] == 7 and len(vals) == 4
+    if case == "context_room":
+        assert st["error"] == 0 and st["done"] == 0 and st["position"] == 44
+    if case == "all":
+        assert st["accepted"] == 3 and st["position"] == 44 and st["anchor"] == 24 and st["n_inject"] == 4
+        assert st["ring_head"] == 7 and log[5] == (4 << 16) | (3 << 8) | 3
+    if case == "partial":
+        assert st["accepted"] == 1 and st["position"] == 42 and st["anchor"] == 50 and st["n_inject"] == 2
+        assert vals == [21, 50]
+    if case == "eos_draft":
+        assert st["done"] == 1 and st["ring_head"] == 5 and st["anchor"] == 22 and st["position"] == 42
+    if case == "first_token":
+        assert st["position"] == 43 and st["n_inject"] == 3 and st["anchor"] == 33 and st["ring_head"] == 1
+        assert st["step"] == 6
+    if case == "overflow":
+        assert st["error"] == 1 and st["done"] == 1 and not vals
+    if case == "wrap":                                   # slots 15 and 0 hold sequences 16 and 17
+        assert int(ring[15]) >> 32 == 16 and int(ring[0]) >> 32 == 17 and st["ring_head"] == 19
+    # a prefill chunk only advances and marks its rows for injection
+    st = O.new_state(**dict(fields, prefill_left=2, t_this_step=4))
+    O.accept_scan(st, tokens, np.zeros(16, np.uint64), eos=eos, log=log, ctx_cap=ctx_cap)
+    assert st["position"] == fields["position"] + 4 and st["n_inject"] == 4 and st["n_chain"] == 0
+    assert log[fields["step"] % 64] == (4 << 16) | 0xFFFF
+
+
+@pytest.mark.parametrize("token,stops,done", [(2, [2, 9, 11], 1), (9, [2, 9, 11], 1), (7, [2, 9, 11], 0), (9, [], 0)])
+def test_accept_scan_oracle_stop_tokens(token, stops, done):
+    st = O.new_state(t_this_step=1, position=5)
+    O.accept_scan(st, [token], np.zeros(16, np.uint64), eos=stops)
+    assert st["done"] == done and st["ring_head"] == 1 and st["position"] == 6
+
+
+def test_accept_scan_oracle_stops_after_the_first_eos():
+    st = O.new_state(t_this_step=4, verify_len=3, position=5, pending_tokens=[1, 7, 9, 8])
+    ring = np.zeros(16, np.uint64)
+    O.accept_scan(st, [7, 9, 8, 12], ring, eos=[2, 9])
+    assert st["done"] == 1 and st["ring_head"] == 2 and st["position"] == 7 and st["checkpoint_index"] == 2
+    assert [int(v) & 0xFFFFFFFF for v in ring[:3]] == [7, 9, 0]

@@ -296,3 +296,80 @@ def test_decoder_program_stops_at_context_capacity(torch_gpu):
     rep = prog.run(40, launches_per_batch=2, in_flight=2)
     g = st.read()
     assert g["error"] == 2 and g["done"] == 1 and g["position"] == 50 and len(rep.tokens) == 8
+
+
+# ---- the speculative round's serial ops through the kernels, state compared field by field with the oracle ---------
+
+from test_step import ACCEPT_CASES, CONF, DRAFTS, SELECT_BASE, accept_case  # noqa: E402
+
+
+def _fresh(fields, ring=16):
+    from monolith_mi355.runtime.step import StepState
+    st = StepState(ring_capacity=ring)
+    st.write(**O.new_state(**fields))
+    return st
+
+
+def _same_state(got, ref):
+    for k, v in ref.items():
+        g = got[k]
+        if k == "confidence":
+            assert np.array_equal(np.float32(g), np.float32(v)), k
+        else:
+            assert g == v, k
+
+
+SELECT_CALLS = [(SELECT_BASE, dict(threshold=0.0)), (SELECT_BASE, dict(threshold=0.5)),
+                (SELECT_BASE, dict(threshold=0.0, t_max=3)),
+                (dict(SELECT_BASE, prefill_left=2, t_this_step=8, pending_tokens=[1, 2, 3, 4, 5, 6, 7, 8]), {}),
+                (dict(SELECT_BASE, done=1), {}),
+                (SELECT_BASE, dict(mode=1, cost=[1.0, 1.28, 1.535, 1.79, 2.67, 3.55, 4.4, 5.3])),
+                (dict(SELECT_BASE, step=6), dict(threshold=2.0, mode=2, log=True)),
+                (SELECT_BASE, dict(threshold=9.0, t_max=4, mode=2)),
+                (dict(SELECT_BASE, position=10), dict(ctx_cap=13)), (dict(SELECT_BASE, position=10), dict(ctx_cap=10)),
+                (dict(SELECT_BASE, position=30), dict(lm=True)),
+                (dict(SELECT_BASE, position=30, prefill_left=1), dict(lm=True))]
+
+
+@pytest.mark.parametrize("i", range(len(SELECT_CALLS)))
+def test_verify_select_matches_oracle(torch_gpu, i):
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    base, kw = SELECT_CALLS[i]
+    kw = dict(kw)
+    want_log = kw.pop("log", False)
+    st = _fresh(base)
+    log = torch.zeros(4, 16, dtype=torch.float32, device="cuda") if want_log else None
+    kernels.verify_select(st.buf, torch.tensor(DRAFTS, dtype=torch.int32, device="cuda"),
+                          torch.tensor(CONF, dtype=torch.float32, device="cuda"), gamma=5, conf_log=log, **kw)
+    torch.cuda.synchronize()
+    ref = O.new_state(**base)
+    ref_log = np.zeros((4, 16), np.float32) if want_log else None
+    O.verify_select(ref, DRAFTS, CONF, gamma=5, conf_log=ref_log, **kw)
+    _same_state(st.read(), ref)
+    if want_log:
+        assert np.array_equal(log.cpu().numpy(), ref_log)
+
+
+@pytest.mark.parametrize("case", ACCEPT_CASES + ["prefill", "stop_at", "lm"])
+def test_accept_scan_matches_oracle(torch_gpu, case):
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    fields, tokens, eos, ctx_cap = accept_case(case if case in ACCEPT_CASES else "all")
+    lm = case == "lm"
+    if case == "prefill":
+        fields = dict(fields, prefill_left=2)
+    if case == "stop_at":
+        fields = dict(fields, stop_at=5)
+    if lm:
+        fields = dict(fields, drafter_ctx_len=41)
+    st = _fresh(fields)
+    log = torch.zeros(64, dtype=torch.int32, device="cuda")
+    kernels.accept_scan(st.buf, torch.tensor(tokens, dtype=torch.int32, device="cuda"), st.ring.addr, 16, eos=eos,
+                        log=log, ctx_cap=ctx_cap, lm=lm, host_ctl=st.ctl.addr)
+    torch.cuda.synchronize()
+    ref, ring, ref_log = O.new_state(**fields), np.zeros(16, np.uint64), np.zeros(64, np.uint32)
+    O.accept_scan(ref, tokens, ring, eos=eos, log=ref_log, ctx_cap=ctx_cap, lm=lm)
+    _same_state(st.read(), ref)
+    assert np.array_equal(st.ring.array, ring) and np.array_equal(log.cpu().numpy().view(np.uint32), ref_log)
+    assert st.done == bool(ref["done"]) and st.error == ref["error"]
