@@ -85,6 +85,8 @@ struct Args {
   int tb;                   // gemv_tk: 16-row tiles per workgroup
   int ks, kc;               // gemv_tk: K splits, chunks per split
   float* part;              // gemv_tk with ks > 1: FP32 partials [ks][m][n_tiles·16]
+  uint32_t* fold_cnt;       // gemv_row with ks > 1: per-tile arrival counters (zero between calls): the last split
+                            // of a tile folds the partials in the kernel; null: gemv_tk_reduce does it
   const float* gnorm_w;     // gated head RMSNorm on the input (Gated DeltaNet output norm), or null
   const uint16_t* gnorm_z;
   int ld_gnorm_z;
@@ -549,18 +551,50 @@ __global__ __launch_bounds__(KW == 16 ? 640 : 1024) void gemv_row(Args a) {
   __syncthreads();
   if (wave != 0) return;
   const int row = tile * 16 + m_row;
-  if (a.ks > 1) {                               // this split's partial; gemv_tk_reduce adds the splits in order
+  float vt[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) vt[t] = slice_sum(red + t * 16, MT * 16, S, lane);
+  if (a.ks > 1) {
+    const long long pstride = (long long)a.n_tiles * 16;
+    if (!a.fold_cnt) {                          // this split's partial; gemv_tk_reduce adds the splits in order
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+        if (g == 0 && t < cnt) a.part[((long long)split * a.m + t) * pstride + row] = vt[t];
+      return;
+    }
+    // The splits of a tile meet without a memory fence (an agent-scope release writes back the whole L2 — about
+    // 0.15 us per workgroup, serialized): partials and counter are device-scope atomic read-modify-writes, performed
+    // at the device's coherence point in the order each lane issues them; every exchange has returned before the
+    // counter moves, and the last split reads the partials back with read-modify-writes issued after it saw the
+    // count. It adds the splits in split order (the result of gemv_tk_reduce, bit for bit) and re-arms the counter.
+    auto* pu = reinterpret_cast<uint32_t*>(a.part);
+    uint32_t seen = 0;
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+      if (g == 0 && t < cnt)
+        seen |= __hip_atomic_exchange(pu + ((long long)split * a.m + t) * pstride + row, __float_as_uint(vt[t]),
+                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("" ::"v"(seen) : "memory");     // the exchanges have returned
+    uint32_t prev = 0;
+    if (lane == 0)
+      prev = __hip_atomic_fetch_add(a.fold_cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    prev = __shfl(prev, 0);
+    if (prev != (uint32_t)(a.ks - 1)) return;
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
-      const float v = slice_sum(red + t * 16, MT * 16, S, lane);
-      if (g == 0 && t < cnt) a.part[((long long)split * a.m + t) * a.n_tiles * 16 + row] = v;
+      float v = 0.0f;
+      if (g == 0 && t < cnt)
+        for (int sp = 0; sp < a.ks; ++sp)
+          v += __uint_as_float(__hip_atomic_fetch_or(pu + ((long long)sp * a.m + t) * pstride + row, 0u,
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+      vt[t] = v;
     }
-    return;
+    if (lane == 0) __hip_atomic_store(a.fold_cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   const float rs = a.row_scale != nullptr ? a.row_scale[(long long)expert * a.n_tiles * 16 + row] : 1.0f;
 #pragma unroll
   for (int t = 0; t < MT; ++t) {
-    float v = slice_sum(red + t * 16, MT * 16, S, lane);
+    float v = vt[t];
     v *= rs;
     const float up = __shfl_down(v, 8, 16);
     if (g == 0) emit(a, pairs, cnt, tile, true, m_row, t, v, up);
@@ -1925,7 +1959,7 @@ void launch(const Args& a, const Plan& p, int groups, hipStream_t s) {
     const dim3 g(p.G, groups, p.ks);
     if (p.lds_rows == 2) launch_row_k<FMT, 2>(a, p, g, s);
     else launch_row_k<FMT, 1>(a, p, g, s);
-    if (p.ks > 1) {
+    if (p.ks > 1 && !a.fold_cnt) {
       const bool silu = a.epilogue == MI_EPI_SILU_MUL || a.epilogue == MI_EPI_SILU_MUL_ROUNDED;
       const int n_out = silu ? a.n / 2 : a.n;
       hipLaunchKernelGGL(gemv_tk_reduce, dim3((n_out + 255) / 256, a.m), dim3(256), 0, s, a);
@@ -1945,6 +1979,12 @@ void launch(const Args& a, const Plan& p, int groups, hipStream_t s) {
   }
 }
 
+// split-K workspace: a fixed region of per-tile arrival counters (the same for every shape, so partials of one call
+// never land on the counters of another), then the FP32 partials [ks][m][n_tiles·16]
+constexpr int kFoldTiles = 16384;
+constexpr size_t kFoldCounterBytes = kFoldTiles * sizeof(uint32_t);
+size_t fold_counter_bytes(int) { return kFoldCounterBytes; }
+
 // the library's FP32 partials buffer for split-K plans (per device, grown on demand; a caller that cannot allocate
 // passes its own through mi_gemv_desc.workspace)
 std::mutex g_ws_mu;
@@ -1960,6 +2000,7 @@ int partials_workspace(size_t bytes, void** out) {
     if (w.first) MI_TRY_HIP(hipFree(w.first), "hipFree(gemv partials)");
     w = {nullptr, 0};
     MI_TRY_HIP(hipMalloc(&w.first, bytes), "hipMalloc(gemv partials)");
+    MI_TRY_HIP(hipMemset(w.first, 0, bytes), "hipMemset(gemv partials)");   // the arrival counters start at zero
     w.second = bytes;
   }
   *out = w.first;
@@ -1981,7 +2022,7 @@ size_t mi_pack_bytes(int32_t format, int32_t n, int32_t k) {
 size_t mi_gemv_workspace_bytes(const mi_gemv_desc* d) {
   if (check_desc(d) != MI_OK) return 0;
   const Plan p = make_plan(d);
-  return p.ks > 1 ? (size_t)p.ks * d->m * ((d->n + 15) / 16) * 16 * sizeof(float) : 0;
+  return p.ks > 1 ? fold_counter_bytes(d->n) + (size_t)p.ks * d->m * ((d->n + 15) / 16) * 16 * sizeof(float) : 0;
 }
 
 int mi_gemv_plan(const mi_gemv_desc* d, int32_t out[7]) {
@@ -2031,14 +2072,18 @@ int mi_gemv(const mi_gemv_desc* d, void* stream) {
   a.row_ld = p.row_ld;
   a.row_wave_lds = p.row_wave_lds;
   if (p.ks > 1) {
-    const size_t need = (size_t)p.ks * d->m * ((d->n + 15) / 16) * 16 * sizeof(float);
+    const size_t cb = fold_counter_bytes(d->n);
+    const size_t need = cb + (size_t)p.ks * d->m * ((d->n + 15) / 16) * 16 * sizeof(float);
     void* ws = d->workspace;
     if (ws) {
       MI_REQUIRE(d->workspace_bytes >= need, "mi_gemv: workspace %zu B < %zu B", d->workspace_bytes, need);
     } else if (int rc = partials_workspace(need, &ws)) {
       return rc;
     }
-    a.part = static_cast<float*>(ws);
+    a.part = reinterpret_cast<float*>(static_cast<char*>(ws) + cb);
+    // gemv_row folds its splits in the kernel (MI_GEMV_FOLD=0: the separate reduction launch, for comparisons)
+    static const bool fold = !(getenv("MI_GEMV_FOLD") && getenv("MI_GEMV_FOLD")[0] == '0');
+    if (p.kernel == 1 && fold && a.n_tiles <= kFoldTiles) a.fold_cnt = static_cast<uint32_t*>(ws);
   }
   const int groups = d->groups ? d->max_groups : 1;
   hipStream_t s = static_cast<hipStream_t>(stream);

@@ -278,3 +278,45 @@ def test_fp8_dequant_every_code(torch_gpu):
         got = kernels.dequant(_upload(torch_gpu, m)).cpu().numpy()
         ref = (e4m3_to_f32(w) * np.float32(s)).astype(np.float32)
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), s
+
+
+def test_gemv_split_k_fold_in_kernel(torch_gpu):
+    """M ≤ 2 split-K plans fold their splits inside the kernel (arrival counters in the workspace): shapes with
+    different tile counts interleaved, each repeated — the counters re-arm, the partials of one shape never disturb
+    another's, the results repeat bit for bit, match the oracle, and a caller's zeroed workspace gives the same bits."""
+    torch = torch_gpu
+    import ctypes as C
+    from monolith_mi355 import kernels
+    from monolith_mi355.runtime import hip
+    rng = np.random.default_rng(77)
+    cases = []
+    for n, k, mtok in [(4096, 12288, 1), (5120, 17408, 1), (1040, 17408, 2), (5120, 12288, 2)]:
+        m = _matrix("nvfp4", n, k, rng)
+        w = _upload(torch, m)
+        x = rbf(rng.standard_normal((mtok, k)))
+        xd = to_dev_bf16(torch, x)
+        yd = torch.empty(mtok, n, dtype=torch.float32, device="cuda")
+        d = hip.MiGemvDesc(format=1, n=n, k=k, m=mtok, w=hip.ptr(w.data), row_scale=hip.ptr(w.row_scale),
+                           x=hip.ptr(xd), ldx=k, y=hip.ptr(yd), ldy=n, out_f32=1)
+        plan = (C.c_int32 * 7)()
+        hip.call("mi_gemv_plan", C.byref(d), plan)
+        assert plan[0] == 1 and plan[4] > 1, (n, k, list(plan))          # gemv_row with K splits
+        cases.append((m, w, x, xd, d))
+    first = []
+    for rep in range(3):
+        for i, (m, w, x, xd, d) in enumerate(cases):
+            y = kernels.gemv(w, xd, out_f32=True)
+            torch.cuda.synchronize()
+            y = y.cpu().numpy()
+            if rep == 0:
+                chk = check_against_oracle(y, ON.matmul_acc(x, _dequant(m)))
+                assert chk.ok(), (i, chk)
+                first.append(y)
+            else:
+                assert np.array_equal(y, first[i]), (rep, i)
+    ws_bytes = max(hip.load().mi_gemv_workspace_bytes(C.byref(d)) for *_, d in cases)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device="cuda")
+    for i, (m, w, x, xd, d) in enumerate(cases * 2):
+        y = kernels.gemv(w, xd, out_f32=True, workspace=ws)
+        torch.cuda.synchronize()
+        assert np.array_equal(y.cpu().numpy(), first[i % len(cases)]), i
