@@ -286,6 +286,29 @@ typedef struct mi_argmax_desc {
 size_t mi_argmax_workspace_bytes(const mi_argmax_desc* d);
 int mi_argmax(const mi_argmax_desc* d, void* stream);
 
+/* sample (ops/sample.py:1-10, kernels/common/sample.metal, nn/sampling_ref.py): per row of BF16 logits, the token
+ * argmax over the kept logits (v >= tau) of v / temperature − log(−log u), u from a splitmix64 hash of (seed, step,
+ * row, index); tau = the most restrictive of top-k (k-th largest, ties kept; top_k > 0), top-p (0 < top_p < 1: the
+ * value where the descending cumulative softmax mass first reaches top_p — of the top-k set with topp_in_topk) and
+ * min-p (min_p > 0: max + temperature · log(min_p)). temperature > 0 (greedy is mi_argmax). With state set, the seed
+ * is (rng_hi << 32 | rng_lo) and the step is state->step, read on the device. */
+typedef struct mi_sample_desc {
+  int32_t t, vocab;
+  const uint16_t* logits;     /* device BF16 [t][ld] */
+  int32_t ld;
+  int32_t* ids;               /* device [t] */
+  float temperature, top_p, min_p;
+  int32_t top_k, topp_in_topk;
+  uint64_t seed;
+  uint32_t step;
+  const mi_step_state* state; /* optional: seed and step from the step state */
+  void* workspace;            /* optional, mi_sample_workspace_bytes, zeroed once before its first use (the
+                                 histograms and counters are left at zero by every call); NULL: the library's own */
+  size_t workspace_bytes;
+} mi_sample_desc;
+size_t mi_sample_workspace_bytes(const mi_sample_desc* d);
+int mi_sample(const mi_sample_desc* d, void* stream);
+
 /* advance (kernels/common/advance.metal:15-37): the serial op that closes a step. Unless done: while prefill_left > 0
  * only position += t_this_step and step += 1; otherwise the last row's token (tokens[t_this_step - 1]) goes to ring
  * slot head % ring_cap as ((head + 1) << 32) | token (ring full: error 1 + done, nothing else changes), becomes

@@ -55,10 +55,171 @@ __device__ __forceinline__ void block_best(float& bv, int& bi, float* sv, int* s
     if (better(sv[k], si[k], bv, bi)) { bv = sv[k]; bi = si[k]; }
 }
 
+// ---- stochastic sampling (kernels/common/sample.metal, nn/sampling_ref.py) -------------------------------------
+// The draw is argmax over the kept logits (v >= tau) of v / temperature + g_i, g_i = −log(−log(u_i)), u_i from a
+// splitmix64 hash of (seed, step, token row, index): the reference's counter-based noise, so a draw is reproducible
+// bit for bit and checkable against the host restatement.
+struct SampleCtx {
+  const float* tau;                // per row: the logit threshold (select_thresholds)
+  float inv_t;
+  uint32_t seed_lo, seed_hi, step;
+  const mi_step_state* st;         // when set: seed = (rng_hi, rng_lo) and step come from the step state
+};
+
+__device__ __forceinline__ float uniform01(uint32_t seed_lo, uint32_t seed_hi, uint32_t step, uint32_t t, uint32_t i) {
+  uint64_t x = ((uint64_t)seed_hi << 32) | seed_lo;
+  x += (uint64_t)step * 0x9E3779B97F4A7C15ull + (uint64_t)t * 0xC2B2AE3D27D4EB4Full + (uint64_t)i * 0x165667B19E3779F9ull;
+  x ^= x >> 30;                    // the splitmix64 finalizer
+  x *= 0xBF58476D1CE4E5B9ull;
+  x ^= x >> 27;
+  x *= 0x94D049BB133111EBull;
+  x ^= x >> 31;
+  return ((float)((x >> 41) & 0x7FFFFFull) + 0.5f) * (1.0f / 8388608.0f);   // 23 bits: u in (0, 1), never 1
+}
+
+// BF16 bits → a 16-bit key that orders like the value (sign flipped: negative values reversed)
+__device__ __forceinline__ uint32_t key16(uint32_t bits) { return bits & 0x8000u ? (~bits) & 0xFFFFu : bits | 0x8000u; }
+__device__ __forceinline__ float key_val(uint32_t key) {
+  const uint32_t bits = key & 0x8000u ? key & 0x7FFFu : (~key) & 0xFFFFu;
+  return __uint_as_float(bits << 16);
+}
+
+constexpr uint32_t HIST_KEYS = 65536;
+constexpr int SELECT_THREADS = 1024;
+constexpr int SELECT_WAVES = SELECT_THREADS / 64;
+constexpr uint32_t WAVE_KEYS = HIST_KEYS / SELECT_WAVES;   // keys per wave, descending from 65535 − 4096·w
+
+// grid (spans, rows): the histogram of each row's logit keys (device-scope atomic adds; select clears it again)
+__global__ __launch_bounds__(ARGMAX_THREADS) void sample_hist(const uint16_t* logits, int ld, int vocab, uint32_t* hist) {
+  const int row = blockIdx.y;
+  const uint16_t* p = logits + (long long)row * ld;
+  uint32_t* h = hist + (size_t)row * HIST_KEYS;
+  const int lo = blockIdx.x * ARGMAX_SPAN, hi = min(lo + ARGMAX_SPAN, vocab);
+  for (int c = lo + (int)threadIdx.x; c < hi; c += ARGMAX_THREADS) atomicAdd(h + key16(p[c]), 1u);
+}
+
+// inclusive prefix over the 64 lanes of a wave (lane order)
+template <typename T>
+__device__ __forceinline__ T wave_scan_incl(T v, int lane) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const T u = __shfl_up(v, off);
+    if (lane >= off) v += u;
+  }
+  return v;
+}
+template <typename T>
+__device__ __forceinline__ T wave_total(T v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+// the key where a descending cumulative sum starting at `run` first reaches `target`, walking this wave's keys
+// (chunks of 64, lane 0 the highest key of a chunk); -inf when the wave's keys do not get there
+template <bool MASS>
+__device__ float walk_to(const uint32_t* h, uint32_t hi, float vmax, float inv_t, double run_in, double target, int lane) {
+  float run = (float)run_in;
+  float last = -INFINITY;                           // the lowest key with a count walked so far
+  for (int q = 0; q < WAVE_KEYS / 64; ++q) {
+    const uint32_t k = hi - 64 * q - lane;
+    const uint32_t cnt = h[k];
+    const float x = MASS ? (cnt ? (float)cnt * expf((key_val(k) - vmax) * inv_t) : 0.0f) : (float)cnt;
+    const float incl = run + wave_scan_incl(x, lane);
+    const unsigned long long hit = __ballot(cnt != 0u && incl >= (float)target);
+    if (hit) return key_val(hi - 64 * q - (uint32_t)__builtin_ctzll(hit));
+    const unsigned long long nz = __ballot(cnt != 0u);
+    if (nz) last = key_val(hi - 64 * q - (63u - (uint32_t)__builtin_clzll(nz)));
+    run = __shfl(incl, 63);
+  }
+  return last;                                      // the sums' order left the target a rounding short: the last key
+}
+
+// one workgroup per row (sample.metal `sample_select`): wave w owns the keys 65535 − 4096·w − [0, 4096), walked
+// 64 at a time from the top (lane = key), so wave order is descending key order. tau = the most restrictive of
+// top-k (the k-th largest logit, ties kept), top-p (the key at which the descending cumulative softmax mass of
+// logits / temperature first reaches p of the total — of the top-k set's mass with flag 8) and min-p (max +
+// temperature · log(min_p)). Per-wave sums (fixed lane order), then a sequential sum over the waves decides which
+// wave walks to the key; the row's histogram is cleared after.
+__global__ __launch_bounds__(SELECT_THREADS) void sample_select(uint32_t* hist, float* tau, int top_k, float temperature,
+                                                                float top_p, float min_p, uint32_t flags) {
+  __shared__ uint32_t wmax[SELECT_WAVES];
+  __shared__ uint32_t wcnt[SELECT_WAVES];
+  __shared__ float wmass[SELECT_WAVES], wmass_k[SELECT_WAVES];
+  __shared__ float res[2];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, row = blockIdx.x;
+  uint32_t* h = hist + (size_t)row * HIST_KEYS;
+  const uint32_t hi = HIST_KEYS - 1 - (uint32_t)w * WAVE_KEYS;
+  uint32_t km = 0;
+  for (int q = 0; q < WAVE_KEYS / 64; ++q) {
+    const uint32_t k = hi - 64 * q - lane;
+    if (h[k]) km = max(km, k);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) km = max(km, (uint32_t)__shfl_xor((int)km, off));
+  if (lane == 0) wmax[w] = km;
+  if (threadIdx.x == 0) { res[0] = -INFINITY; res[1] = -INFINITY; }
+  __syncthreads();
+  uint32_t gmax = 0;
+  for (int i = 0; i < SELECT_WAVES; ++i) gmax = max(gmax, wmax[i]);
+  const float vmax = key_val(gmax), inv_t = 1.0f / temperature;
+  float tau_k = -INFINITY, tau_p = -INFINITY, tau_m = -INFINITY;
+  if (flags & 1u) {                                 // top-k: counts are exact
+    uint32_t cnt = 0;
+    for (int q = 0; q < WAVE_KEYS / 64; ++q) cnt += h[hi - 64 * q - lane];
+    cnt = wave_total(cnt);
+    if (lane == 0) wcnt[w] = cnt;
+    __syncthreads();
+    uint32_t before = 0;
+    for (int i = 0; i < w; ++i) before += wcnt[i];
+    if (before < (uint32_t)top_k && before + wcnt[w] >= (uint32_t)top_k) {
+      const float kk = walk_to<false>(h, hi, vmax, inv_t, (double)before, (double)top_k, lane);
+      if (lane == 0) res[0] = kk;
+    }
+    __syncthreads();
+    tau_k = res[0];                                 // k beyond the vocabulary: every logit kept (−inf)
+  }
+  if (flags & 2u) {
+    float m = 0.0f, mk = 0.0f;
+    for (int q = 0; q < WAVE_KEYS / 64; ++q) {
+      const uint32_t k = hi - 64 * q - lane;
+      const uint32_t cnt = h[k];
+      if (cnt) {
+        const float x = (float)cnt * expf((key_val(k) - vmax) * inv_t);
+        m += x;
+        if (key_val(k) >= tau_k) mk += x;
+      }
+    }
+    m = wave_total(m);
+    mk = wave_total(mk);
+    if (lane == 0) { wmass[w] = m; wmass_k[w] = mk; }
+    __syncthreads();
+    float total = 0.0f, before = 0.0f;
+    for (int i = 0; i < SELECT_WAVES; ++i) total += (flags & 9u) == 9u ? wmass_k[i] : wmass[i];
+    for (int i = 0; i < w; ++i) before += wmass[i];
+    const float target = top_p * total;
+    if (before < target && before + wmass[w] >= target) {
+      const float kp = walk_to<true>(h, hi, vmax, inv_t, (double)before, (double)target, lane);
+      if (lane == 0) res[1] = kp;
+    }
+    __syncthreads();
+    tau_p = res[1];
+  }
+  if (flags & 4u) tau_m = vmax + temperature * logf(min_p);
+  if (threadIdx.x == 0) tau[row] = fmaxf(fmaxf(tau_k, tau_p), tau_m);
+  __syncthreads();                                  // every wave's reads before the clearing stores
+  for (int q = 0; q < WAVE_KEYS / 64; ++q) {
+    const uint32_t k = hi - 64 * q - lane;
+    if (h[k]) h[k] = 0u;                            // clear for the next call
+  }
+}
+
 // grid (spans, rows): each workgroup scans ARGMAX_SPAN logits of one row with 16-byte loads, publishes its best,
-// and the last workgroup of the row to arrive folds the row's partials and resets the row's counter
+// and the last workgroup of the row to arrive folds the row's partials and resets the row's counter. SAMPLE: the
+// value of a BF16 logit v >= tau is v / temperature + its Gumbel noise, any other logit is left out.
+template <bool SAMPLE>
 __global__ __launch_bounds__(ARGMAX_THREADS) void argmax_spans(mi_argmax_desc d, uint32_t* counters,
-                                                               ArgmaxPartial* part) {
+                                                               ArgmaxPartial* part, SampleCtx sc) {
   __shared__ float sv[ARGMAX_THREADS / 64];
   __shared__ int si[ARGMAX_THREADS / 64];
   __shared__ int last;
@@ -66,7 +227,15 @@ __global__ __launch_bounds__(ARGMAX_THREADS) void argmax_spans(mi_argmax_desc d,
   const int lo = blockIdx.x * ARGMAX_SPAN, hi = min(lo + ARGMAX_SPAN, d.vocab);
   float bv = -INFINITY;
   int bi = 0x7FFFFFFF;
-  if (d.f32) {
+  float th = 0.0f;
+  uint32_t seed_lo = 0, seed_hi = 0, step = 0;
+  if constexpr (SAMPLE) {
+    th = sc.tau[row];
+    seed_lo = sc.st ? (uint32_t)sc.st->rng_lo : sc.seed_lo;
+    seed_hi = sc.st ? (uint32_t)sc.st->rng_hi : sc.seed_hi;
+    step = sc.st ? sc.st->step : sc.step;
+  }
+  if (!SAMPLE && d.f32) {
     const float* p = static_cast<const float*>(d.logits) + (long long)row * d.ld;
     const bool vec = ((reinterpret_cast<uintptr_t>(p) | (uintptr_t)lo * 4) & 15) == 0;
     for (int c = lo + tid * 4; c < hi; c += ARGMAX_THREADS * 4) {
@@ -96,7 +265,11 @@ __global__ __launch_bounds__(ARGMAX_THREADS) void argmax_spans(mi_argmax_desc d,
         }
       }
       for (int e = 0; e < 4; ++e) {
-        const float v0 = __uint_as_float(w[e] << 16), v1 = __uint_as_float(w[e] & 0xFFFF0000u);
+        float v0 = __uint_as_float(w[e] << 16), v1 = __uint_as_float(w[e] & 0xFFFF0000u);
+        if constexpr (SAMPLE) {
+          v0 = v0 >= th ? v0 * sc.inv_t - logf(-logf(uniform01(seed_lo, seed_hi, step, row, c + 2 * e))) : NAN;
+          v1 = v1 >= th ? v1 * sc.inv_t - logf(-logf(uniform01(seed_lo, seed_hi, step, row, c + 2 * e + 1))) : NAN;
+        }
         if (better(v0, c + 2 * e, bv, bi)) { bv = v0; bi = c + 2 * e; }
         if (better(v1, c + 2 * e + 1, bv, bi)) { bv = v1; bi = c + 2 * e + 1; }
       }
@@ -167,6 +340,10 @@ __global__ __launch_bounds__(64) void advance_step(mi_advance_desc d) {
 }
 
 int argmax_spans_of(int vocab) { return (vocab + ARGMAX_SPAN - 1) / ARGMAX_SPAN; }
+
+__global__ void fill_neg_inf(float* p, int n) {
+  if ((int)threadIdx.x < n) p[threadIdx.x] = -INFINITY;
+}
 
 // the library's argmax workspace (per device, grown on demand, zeroed when allocated: the kernels keep its counters
 // at zero); calls sharing it must be ordered on one stream
@@ -423,9 +600,64 @@ int mi_argmax(const mi_argmax_desc* d, void* stream) {
   }
   auto* counters = static_cast<uint32_t*>(ws);
   auto* part = reinterpret_cast<ArgmaxPartial*>(static_cast<char*>(ws) + ARGMAX_COUNTERS);
-  hipLaunchKernelGGL(argmax_spans, dim3(nb, d->t), dim3(ARGMAX_THREADS), 0, static_cast<hipStream_t>(stream), *d,
-                     counters, part);
+  hipLaunchKernelGGL(argmax_spans<false>, dim3(nb, d->t), dim3(ARGMAX_THREADS), 0, static_cast<hipStream_t>(stream),
+                     *d, counters, part, SampleCtx{});
   MI_TRY_HIP(hipGetLastError(), "argmax launch");
+  return MI_OK;
+}
+
+// workspace: argmax counters | partials | tau[16] | histograms [t][65536] u32
+size_t sample_layout(int t, int vocab, size_t* off_tau, size_t* off_hist) {
+  const size_t part = ARGMAX_COUNTERS + (size_t)t * argmax_spans_of(vocab) * sizeof(ArgmaxPartial);
+  *off_tau = (part + 255) / 256 * 256;
+  *off_hist = *off_tau + 256;
+  return *off_hist + (size_t)t * HIST_KEYS * sizeof(uint32_t);
+}
+
+size_t mi_sample_workspace_bytes(const mi_sample_desc* d) {
+  if (!d || d->t < 1 || d->vocab < 1) return 0;
+  size_t a, b;
+  return sample_layout(d->t, d->vocab, &a, &b);
+}
+
+int mi_sample(const mi_sample_desc* d, void* stream) {
+  MI_REQUIRE(d && d->logits && d->ids, "mi_sample: null pointer");
+  MI_REQUIRE(d->t >= 1 && d->t <= 16 && d->vocab > 0 && d->ld >= d->vocab, "mi_sample: bad shape");
+  MI_REQUIRE(d->temperature > 0.0f && d->top_k >= 0 && d->top_p >= 0.0f && d->min_p >= 0.0f,
+             "mi_sample: temperature > 0, top_k / top_p / min_p >= 0 (temperature 0 is mi_argmax)");
+  const int nb = argmax_spans_of(d->vocab);
+  MI_REQUIRE(nb <= ARGMAX_MAX_SPANS, "mi_sample: vocab %d exceeds %d", d->vocab, ARGMAX_MAX_SPANS * ARGMAX_SPAN);
+  size_t off_tau, off_hist;
+  const size_t need = sample_layout(d->t, d->vocab, &off_tau, &off_hist);
+  void* ws = d->workspace;
+  if (ws) {
+    MI_REQUIRE(d->workspace_bytes >= need, "mi_sample: workspace %zu B < %zu B", d->workspace_bytes, need);
+  } else if (int rc = argmax_workspace(need, &ws)) {
+    return rc;
+  }
+  char* wb = static_cast<char*>(ws);
+  auto* counters = reinterpret_cast<uint32_t*>(wb);
+  auto* part = reinterpret_cast<ArgmaxPartial*>(wb + ARGMAX_COUNTERS);
+  auto* tau = reinterpret_cast<float*>(wb + off_tau);
+  auto* hist = reinterpret_cast<uint32_t*>(wb + off_hist);
+  uint32_t flags = 0;
+  if (d->top_k > 0) flags |= 1u;
+  if (d->top_p > 0.0f && d->top_p < 1.0f) flags |= 2u;
+  if (d->min_p > 0.0f) flags |= 4u;
+  if (d->topp_in_topk) flags |= 8u;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (flags & 7u) {
+    hipLaunchKernelGGL(sample_hist, dim3(nb, d->t), dim3(ARGMAX_THREADS), 0, s, d->logits, d->ld, d->vocab, hist);
+    hipLaunchKernelGGL(sample_select, dim3(d->t), dim3(SELECT_THREADS), 0, s, hist, tau, d->top_k, d->temperature,
+                       d->top_p, d->min_p, flags);
+  } else {
+    hipLaunchKernelGGL(fill_neg_inf, dim3(1), dim3(64), 0, s, tau, d->t);        // nothing to cut: keep every logit
+  }
+  mi_argmax_desc am{};
+  am.t = d->t; am.vocab = d->vocab; am.logits = d->logits; am.ld = d->ld; am.f32 = 0; am.ids = d->ids;
+  SampleCtx sc{tau, 1.0f / d->temperature, (uint32_t)d->seed, (uint32_t)(d->seed >> 32), d->step, d->state};
+  hipLaunchKernelGGL(argmax_spans<true>, dim3(nb, d->t), dim3(ARGMAX_THREADS), 0, s, am, counters, part, sc);
+  MI_TRY_HIP(hipGetLastError(), "sample launch");
   return MI_OK;
 }
 

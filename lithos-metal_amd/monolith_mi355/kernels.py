@@ -399,6 +399,33 @@ def argmax(logits, *, out=None, stream=None):
     return out
 
 
+def sample(logits, *, temperature: float = 1.0, top_k: int = 0, top_p: float = 0.0, min_p: float = 0.0,
+           topp_in_topk: bool = False, seed: int = 0, step: int = 0, state=None, out=None, stream=None):
+    """``sample`` (``ops/sample.py:1-10``): ``logits [T, V]`` bf16 → ``ids [T]`` int32 drawn from the warped softmax
+    (top-k / top-p / min-p thresholds, temperature) by Gumbel-max with the reference's counter-based noise, so the
+    draw for (seed, step, row) is reproducible. ``state``: a step state whose ``rng_lo/rng_hi`` and ``step`` give the
+    seed and step on the device (a captured program). Temperature 0 is greedy: :func:`argmax`."""
+    torch = _torch()
+    _bf16_2d(logits, "sample logits", aligned=False)
+    t, v = logits.shape
+    if not 1 <= t <= 16:
+        raise ValueError("sample: 1..16 rows")
+    if temperature <= 0:
+        return argmax(logits, out=out, stream=stream)
+    if out is None:
+        out = torch.empty(t, dtype=torch.int32, device=logits.device)
+    if out.dtype != torch.int32 or out.numel() < t:
+        raise ValueError("sample: out must be int32 [t]")
+    if state is not None:
+        _check_state(state, "sample")
+    d = hip.MiSampleDesc(t=t, vocab=v, logits=hip.ptr(logits), ld=logits.stride(0), ids=hip.ptr(out),
+                         temperature=temperature, top_p=top_p, min_p=min_p, top_k=top_k,
+                         topp_in_topk=int(topp_in_topk), seed=seed & 0xFFFFFFFFFFFFFFFF, step=step,
+                         state=hip.ptr(state))
+    hip.call("mi_sample", C.byref(d), hip.stream_handle(stream))
+    return out
+
+
 def advance(state, tokens, ring, ring_cap: int, *, eos=(), ctx_cap: int = 0, host_ctl=None, stream=None):
     """``advance`` (``kernels/common/advance.metal:15-37``): close a step — publish the last row's token to the ring,
     make it the next step's pending token, move position and step, stop at EOS / ``stop_at`` / the context capacity.

@@ -27,6 +27,7 @@ MOE_GEMV = _op("moe_gemv", OpClass.MAP, "rows", "mi_gemv", grouped=1)
 MOE_COMBINE = _op("moe_combine", OpClass.MAP, "rows", "mi_moe_combine")
 EMBED = _op("embed", OpClass.MAP, "rows", "mi_embed")                       # ops/embed.py:1-7
 ARGMAX = _op("argmax", OpClass.REDUCE, "span", "mi_argmax")                 # ops/sample.py:9
+SAMPLE = _op("sample", OpClass.REDUCE, "span", "mi_sample")                 # ops/sample.py:10
 VERIFY_SELECT = _op("verify_select", OpClass.SERIAL, "span", "mi_verify_select")   # ops/draft.py:27
 ACCEPT_SCAN = _op("accept_scan", OpClass.SERIAL, "span", "mi_accept_scan")         # ops/draft.py:28
 
@@ -34,4 +35,4 @@ DECODE_LAYER_OPS = ("gemv", "rmsnorm_stat", "norm_apply", "gqa_decode", "gqa_mer
                     "gdn_commit", "moe_route", "moe_gemv", "moe_combine", "lm_head")
 
 # the token loop around the layers; the program's tail (the advance, compiler/emit.py:1459-1462) is mi_advance
-STEP_OPS = ("embed", "argmax", "verify_select", "accept_scan")
+STEP_OPS = ("embed", "argmax", "sample", "verify_select", "accept_scan")

@@ -64,6 +64,12 @@ def _argmax(logits, *, out=None, stream=None, **_):
     return kernels.argmax(logits, out=out, stream=stream)
 
 
+def _sample(logits, *, temperature=1.0, top_k=0, top_p=0.0, min_p=0.0, topp_in_topk=False, seed=0, step=0,
+            state=None, out=None, stream=None, **_):
+    return kernels.sample(logits, temperature=temperature, top_k=top_k, top_p=top_p, min_p=min_p,
+                          topp_in_topk=topp_in_topk, seed=seed, step=step, state=state, out=out, stream=stream)
+
+
 def _verify_select(drafts, conf, *, state, gamma, threshold=0.0, t_max=8, mode=0, cost=None, conf_log=None, ctx_cap=0,
                    lm=False, stream=None, **_):
     return kernels.verify_select(state, drafts, conf, gamma=gamma, threshold=threshold, t_max=t_max, mode=mode,
@@ -76,7 +82,7 @@ def _accept_scan(token, *, state, ring, ring_cap, eos=(), log=None, ctx_cap=0, l
                                host_ctl=host_ctl, stream=stream)
 
 
-HANDLERS = {"embed": _embed, "argmax": _argmax, "verify_select": _verify_select, "accept_scan": _accept_scan, "gemv": _gemv, "lm_head": _lm_head, "gqa_decode": _gqa, "gdn_mixer": _gdn, "gdn_commit": _gdn_commit,
+HANDLERS = {"embed": _embed, "argmax": _argmax, "sample": _sample, "verify_select": _verify_select, "accept_scan": _accept_scan, "gemv": _gemv, "lm_head": _lm_head, "gqa_decode": _gqa, "gdn_mixer": _gdn, "gdn_commit": _gdn_commit,
             "moe_route": _route, "moe_gemv": _moe_gemv, "moe_combine": _combine}
 
 

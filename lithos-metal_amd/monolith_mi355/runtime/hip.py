@@ -93,6 +93,13 @@ class MiArgmaxDesc(C.Structure):
                 ("f32", C.c_int32), ("ids", C.c_void_p), ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t)]
 
 
+class MiSampleDesc(C.Structure):
+    _fields_ = [("t", C.c_int32), ("vocab", C.c_int32), ("logits", C.c_void_p), ("ld", C.c_int32), ("ids", C.c_void_p),
+                ("temperature", C.c_float), ("top_p", C.c_float), ("min_p", C.c_float), ("top_k", C.c_int32),
+                ("topp_in_topk", C.c_int32), ("seed", C.c_uint64), ("step", C.c_uint32), ("state", C.c_void_p),
+                ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t)]
+
+
 class MiAdvanceDesc(C.Structure):
     _fields_ = [("state", C.c_void_p), ("tokens", C.c_void_p), ("ring", C.c_void_p), ("ring_cap", C.c_uint32),
                 ("ctx_cap", C.c_uint32), ("n_eos", C.c_int32), ("eos", C.c_int32 * 8), ("host_ctl", C.c_void_p)]
@@ -162,6 +169,8 @@ SIGNATURES = {
     "mi_embed": (C.c_int, [C.POINTER(MiEmbedDesc), _VP]),
     "mi_argmax_workspace_bytes": (_SZ, [C.POINTER(MiArgmaxDesc)]),
     "mi_argmax": (C.c_int, [C.POINTER(MiArgmaxDesc), _VP]),
+    "mi_sample_workspace_bytes": (_SZ, [C.POINTER(MiSampleDesc)]),
+    "mi_sample": (C.c_int, [C.POINTER(MiSampleDesc), _VP]),
     "mi_advance": (C.c_int, [C.POINTER(MiAdvanceDesc), _VP]),
     "mi_verify_select": (C.c_int, [C.POINTER(MiVerifySelectDesc), _VP]),
     "mi_accept_scan": (C.c_int, [C.POINTER(MiAcceptScanDesc), _VP]),

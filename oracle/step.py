@@ -11,7 +11,10 @@ rows with NaN / ±inf; ``advance`` against the known answers of the reference's 
 ``tests/runtime/test_toy_program.py`` (every token once, in order; overflow → error 1 with a clean prefix);
 ``verify_select`` and ``accept_scan`` against the known answers of the reference's ``tests/kernels/test_draft_ops.py``
 (``test_verify_select``'s lengths, tokens and bookkeeping; ``test_accept_scan``'s per-case fields) and
-``tests/kernels/test_eos_set.py``'s EOS cases.
+``tests/kernels/test_eos_set.py``'s EOS cases; the sampler's ``thresholds`` against the Hugging Face logits warpers
+(``TopKLogitsWarper``, ``TopPLogitsWarper``, ``MinPLogitsWarper``, as the reference's ``tests/kernels/test_sampling.py``
+does), ``splitmix64_mix`` against the published splitmix64 output for seed 0, and ``sample``'s draws against the
+warped softmax in distribution.
 """
 
 from __future__ import annotations
@@ -209,3 +212,75 @@ def accept_scan(st: Dict[str, object], tokens: Sequence[int], ring: np.ndarray, 
         st["done"] = 1
     if ctx_cap and st["position"] >= ctx_cap:
         st["error"], st["done"] = 2, 1
+
+
+# ---- stochastic sampling (nn/sampling_ref.py:19-71, kernels/common/sample.metal:22-30) ------------------------------
+
+_M64 = 0xFFFFFFFFFFFFFFFF
+
+
+def splitmix64_mix(x: int) -> int:
+    """The splitmix64 finalizer (Steele, Lea & Flood 2014; ``sample.metal:25``)."""
+    x &= _M64
+    x ^= x >> 30
+    x = (x * 0xBF58476D1CE4E5B9) & _M64
+    x ^= x >> 27
+    x = (x * 0x94D049BB133111EB) & _M64
+    return x ^ (x >> 31)
+
+
+def gumbel_noise(seed: int, step: int, t: int, idx) -> np.ndarray:
+    """``−log(−log u)`` per index, ``u = ((h >> 41) + 0.5) / 2^23`` with ``h`` the finalizer of
+    ``seed + step·φ64 + t·c2 + i·c3`` (``sampling_ref.py:44-55``); float32 arithmetic."""
+    idx = np.asarray(idx, np.uint64)
+    with np.errstate(over="ignore"):
+        x = (np.uint64(seed & _M64) + np.uint64(step) * np.uint64(0x9E3779B97F4A7C15)
+             + np.uint64(t) * np.uint64(0xC2B2AE3D27D4EB4F) + idx * np.uint64(0x165667B19E3779F9))
+        x ^= x >> np.uint64(30)
+        x *= np.uint64(0xBF58476D1CE4E5B9)
+        x ^= x >> np.uint64(27)
+        x *= np.uint64(0x94D049BB133111EB)
+        x ^= x >> np.uint64(31)
+    u = ((x >> np.uint64(41)) & np.uint64(0x7FFFFF)).astype(np.float32)
+    u = (u + np.float32(0.5)) * np.float32(1.0 / 8388608.0)
+    return (-np.log(-np.log(u))).astype(np.float32)
+
+
+def thresholds(logits, *, temperature: float = 1.0, top_k: int = 0, top_p: float = 0.0, min_p: float = 0.0,
+               topp_in_topk: bool = False) -> float:
+    """The logit threshold τ (``sampling_ref.py:19-41``): the largest of the enabled top-k (k-th largest value, ties
+    kept), top-p (the distinct value at which the descending cumulative softmax mass of v / T first reaches p of the
+    total — of the top-k set with ``topp_in_topk``) and min-p (max + T·log min_p); −inf when none is enabled."""
+    v = np.asarray(logits, np.float32)
+    taus = []
+    tau_k = -np.inf
+    if top_k > 0:
+        tau_k = float(np.sort(v)[::-1][min(top_k, v.size) - 1])
+        taus.append(tau_k)
+    if 0.0 < top_p < 1.0:
+        vals = np.unique(v)[::-1]
+        counts = np.array([(v == x).sum() for x in vals], np.float64)
+        cum = np.cumsum(counts * np.exp((vals.astype(np.float64) - vals[0]) / temperature))
+        total = cum[vals >= tau_k][-1] if topp_in_topk and top_k > 0 else cum[-1]
+        taus.append(float(vals[int(np.argmax(cum >= top_p * total))]))
+    if min_p > 0.0:
+        taus.append(float(v.max() + temperature * np.log(min_p)))
+    return max(taus) if taus else -np.inf
+
+
+def sample(logits, *, seed: int, step: int, t: int = 0, temperature: float = 1.0, **opts) -> int:
+    """The token drawn for one row (``sampling_ref.py:58-64``): argmax over the kept logits of v / T + noise."""
+    v = np.asarray(logits, np.float32)
+    tau = thresholds(v, temperature=temperature, **opts)
+    keys = v * np.float32(1.0 / temperature) + gumbel_noise(seed, step, t, np.arange(v.size))
+    keys = np.where(v >= tau, keys, -np.inf).astype(np.float32)
+    return int(np.argmax(keys))
+
+
+def warped_probabilities(logits, *, temperature: float = 1.0, **opts) -> np.ndarray:
+    """The distribution the draws follow: the softmax of v / T over the kept logits (``sampling_ref.py:67-71``)."""
+    v = np.asarray(logits, np.float64)
+    tau = thresholds(v.astype(np.float32), temperature=temperature, **opts)
+    z = np.where(v >= tau, (v - v.max()) / temperature, -np.inf)
+    p = np.exp(z)
+    return p / p.sum()

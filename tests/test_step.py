@@ -221,3 +221,52 @@ def test_accept_scan_oracle_stops_after_the_first_eos():
     O.accept_scan(st, [7, 9, 8, 12], ring, eos=[2, 9])
     assert st["done"] == 1 and st["ring_head"] == 2 and st["position"] == 7 and st["checkpoint_index"] == 2
     assert [int(v) & 0xFFFFFFFF for v in ring[:3]] == [7, 9, 0]
+
+
+# ---- the sampler's oracle ----------------------------------------------------------------------------------------
+
+def test_splitmix64_known_answers():
+    """The published splitmix64 sequence for seed 0 (state advanced by the golden gamma before each mix)."""
+    g = 0x9E3779B97F4A7C15
+    assert O.splitmix64_mix(g) == 0xE220A8397B1DCDAF
+    assert O.splitmix64_mix(2 * g & 0xFFFFFFFFFFFFFFFF) == 0x6E789E6AA1B965F4
+    # the noise hashes seed + step·gamma + …: seed 0, step 1, row 0, index 0 is that first output
+    u = ((0xE220A8397B1DCDAF >> 41) + 0.5) / 8388608.0
+    assert O.gumbel_noise(0, 1, 0, [0])[0] == np.float32(-np.log(-np.log(np.float32(u))))
+
+
+def _bf16_logits(rng, t, vocab, scale):
+    from oracle.fp import rbf
+    return rbf((rng.standard_normal((t, vocab)) * scale).astype(np.float32))
+
+
+def test_thresholds_match_the_hf_warpers():
+    """τ keeps exactly what the Hugging Face warpers keep (the reference's tests/kernels/test_sampling.py check)."""
+    torch = pytest.importorskip("torch")
+    tf = pytest.importorskip("transformers")
+    rng = np.random.default_rng(3)
+    lf = _bf16_logits(rng, 2, 4096, 3.0)
+    cases = [(dict(top_k=25), tf.TopKLogitsWarper(25)), (dict(top_p=0.8), tf.TopPLogitsWarper(0.8)),
+             (dict(min_p=0.1), tf.MinPLogitsWarper(0.1)),
+             (dict(top_k=25, top_p=0.8, topp_in_topk=True),
+              lambda ids, sc: tf.TopPLogitsWarper(0.8)(ids, tf.TopKLogitsWarper(25)(ids, sc)))]
+    for opts, warper in cases:
+        for i in range(2):
+            tau = O.thresholds(lf[i], temperature=1.0, **opts)
+            hf = warper(None, torch.from_numpy(lf[i:i + 1]).clone())[0].numpy()
+            assert np.array_equal(np.isfinite(hf), lf[i] >= tau), (opts, i)
+
+
+def test_sample_oracle_follows_the_warped_softmax():
+    rng = np.random.default_rng(11)
+    lf = np.full(512, -60.0, np.float32)
+    lf[:16] = rng.standard_normal(16) * 1.5
+    from oracle.fp import rbf
+    lf = rbf(lf)
+    n = 3000
+    counts = np.zeros(512)
+    for step in range(n):
+        counts[O.sample(lf, seed=99, step=step, temperature=0.9)] += 1
+    p = O.warped_probabilities(lf, temperature=0.9)
+    sigma = np.sqrt(p * (1 - p) / n)
+    assert np.all(np.abs(counts / n - p)[:16] <= 4 * sigma[:16] + 1e-9) and counts[16:].sum() == 0

@@ -373,3 +373,60 @@ def test_accept_scan_matches_oracle(torch_gpu, case):
     _same_state(st.read(), ref)
     assert np.array_equal(st.ring.array, ring) and np.array_equal(log.cpu().numpy().view(np.uint32), ref_log)
     assert st.done == bool(ref["done"]) and st.error == ref["error"]
+
+
+# ---- stochastic sampling: draws equal to the oracle's (same hash, same thresholds) -------------------------------
+
+SAMPLE_OPTS = [dict(temperature=1.0), dict(temperature=0.7, top_k=40), dict(temperature=1.0, top_p=0.9),
+               dict(temperature=1.3, min_p=0.05), dict(temperature=0.8, top_k=50, top_p=0.95, min_p=0.02),
+               dict(temperature=0.8, top_k=50, top_p=0.9, topp_in_topk=True)]
+
+
+@pytest.mark.parametrize("vocab", [248320, 1000])
+@pytest.mark.parametrize("oi", range(len(SAMPLE_OPTS)))
+def test_sample_draws_equal_the_oracle(torch_gpu, vocab, oi):
+    """The reference's tests/kernels/test_sampling.py case: three rows, steps 0, 1, 7; every token equals the host
+    restatement's draw."""
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    opts = SAMPLE_OPTS[oi]
+    _say("sample", vocab, opts)
+    rng = np.random.default_rng(vocab + len(opts))
+    lb = to_dev_bf16(torch, (rng.standard_normal((3, vocab)) * 4.0).astype(np.float32))
+    lf = from_dev_bf16(lb)
+    for step in (0, 1, 7):
+        tok = kernels.sample(lb, seed=12345, step=step, **opts).cpu().tolist()
+        for i in range(3):
+            assert tok[i] == O.sample(lf[i], seed=12345, step=step, t=i, **opts), (step, i)
+
+
+def test_sample_distribution_determinism_and_device_seed(torch_gpu):
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    from monolith_mi355.runtime.step import StepState
+    from oracle.fp import rbf
+    rng = np.random.default_rng(11)
+    lf = np.full(512, -60.0, np.float32)
+    lf[:16] = rng.standard_normal(16) * 1.5
+    lf = rbf(lf)
+    lb = to_dev_bf16(torch, lf[None, :])
+    n = 2000
+    counts = np.zeros(512)
+    out = torch.empty(1, dtype=torch.int32, device="cuda")
+    for step in range(n):
+        kernels.sample(lb, seed=99, step=step, temperature=0.9, out=out)
+        counts[int(out.item())] += 1
+    p = O.warped_probabilities(lf, temperature=0.9)
+    sigma = np.sqrt(p * (1 - p) / n)
+    assert np.all(np.abs(counts / n - p)[:16] <= 4 * sigma[:16] + 1e-9) and counts[16:].sum() == 0
+    a = kernels.sample(lb, seed=99, step=5, temperature=0.9).item()
+    assert a == kernels.sample(lb, seed=99, step=5, temperature=0.9).item() == O.sample(lf, seed=99, step=5,
+                                                                                           temperature=0.9)
+    # seed and step from a step state, read on the device
+    st = StepState(ring_capacity=4)
+    seed = 0x0123456789ABCDEF
+    st.write(rng_lo=seed & 0xFFFFFFFF, rng_hi=seed >> 32, step=17)
+    lb3 = to_dev_bf16(torch, (rng.standard_normal((3, 5000)) * 3).astype(np.float32))
+    got = kernels.sample(lb3, state=st.buf, temperature=1.1, top_k=100).cpu().tolist()
+    l3 = from_dev_bf16(lb3)
+    assert got == [O.sample(l3[i], seed=seed, step=17, t=i, temperature=1.1, top_k=100) for i in range(3)]
