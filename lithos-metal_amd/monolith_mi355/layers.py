@@ -252,7 +252,7 @@ class DecoderModel:
 
     def step_bytes(self, pos: int) -> int:
         """Algorithmic HBM bytes of one token step (M = 1)."""
-        total = self.hidden * 2 + self.vocab * self.hidden * 2 + self.hidden * 4 + self.vocab * 4
+        total = self.hidden * 2 + self.vocab * self.hidden * 2 + self.hidden * 4 + self.vocab * 2   # BF16 logits
         for layer in self.layers:
             total += layer.bytes_per_step(1) if getattr(layer, "ping_pong", False) else layer.bytes_per_step(1, pos)
         return total

@@ -8,8 +8,8 @@ command buffers of ``steps_per_cb`` steps with ``in_flight`` of them queued; her
 changes between steps lives in :class:`StepState` (the reference's StepState layout, ``core/step_state.py:28-73``)
 and is written by the serial ops that close a step (``argmax``, ``advance``), so the graph never changes.
 
-A step of :class:`StepProgram`: ``embed(pending_tokens) → layers → lm_head (final RMSNorm fused, FP32 logits) →
-argmax → advance``. Attention layers read the position from the step state (``pos_dev``); Gated DeltaNet layers
+A step of :class:`StepProgram`: ``embed(pending_tokens) → layers → lm_head (final RMSNorm fused, BF16 logits as
+the reference's argmax and sampler take them) → argmax or sample → advance``. Attention layers read the position from the step state (``pos_dev``); Gated DeltaNet layers
 ping-pong their conv state between two buffers, so a graph holds an even number of steps.
 """
 
@@ -169,7 +169,10 @@ class StepProgram:
     """
 
     def __init__(self, model, state: StepState, *, eos: Sequence[int] = (), ctx_cap: int = 0,
-                 steps_per_graph: int = 2, stream=None):
+                 steps_per_graph: int = 2, stream=None, sampling: Optional[dict] = None):
+        """``sampling``: ``dict(temperature=…, top_k=…, top_p=…, min_p=…, topp_in_topk=…)`` draws each token with
+        :func:`kernels.sample`, seeded by the state's ``rng_lo``/``rng_hi`` and its step (set them with
+        ``state.write``); None (or temperature 0) is greedy."""
         torch = _torch()
         if steps_per_graph < 1:
             raise ValueError("steps_per_graph must be >= 1")
@@ -181,7 +184,8 @@ class StepProgram:
         self.stream = stream if stream is not None else torch.cuda.Stream(device=dev)
         vocab, hidden = model.embed_table.shape
         self.h0 = torch.empty(1, hidden, dtype=torch.bfloat16, device=dev)
-        self.logits = torch.empty(1, vocab, dtype=torch.float32, device=dev)
+        self.logits = torch.empty(1, vocab, dtype=torch.bfloat16, device=dev)
+        self.sampling = dict(sampling) if sampling and sampling.get("temperature", 1.0) > 0 else None
         self.ids = torch.empty(T_MAX, dtype=torch.int32, device=dev)
         self.graph: Optional[hip.Graph] = None
 
@@ -196,8 +200,11 @@ class StepProgram:
         with torch.cuda.stream(s):
             for layer in m.layers:
                 h = layer.step(h, pos=pos)
-        kernels.gemv(m.lm_head, h, norm_w=m.norm_w, eps=m.eps, out=self.logits, out_f32=True, stream=s)
-        kernels.argmax(self.logits, out=self.ids, stream=s)
+        kernels.gemv(m.lm_head, h, norm_w=m.norm_w, eps=m.eps, out=self.logits, stream=s)
+        if self.sampling:
+            kernels.sample(self.logits, state=st.buf, out=self.ids, stream=s, **self.sampling)
+        else:
+            kernels.argmax(self.logits, out=self.ids, stream=s)
         kernels.advance(st.buf, self.ids, st.ring.addr, st.ring_capacity, eos=self.eos, ctx_cap=self.ctx_cap,
                         host_ctl=st.ctl.addr, stream=s)
 

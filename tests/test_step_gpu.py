@@ -257,8 +257,8 @@ def _decoder(torch, seed):
 
 
 def test_decoder_program_matches_host_loop(torch_gpu):
-    """Model A: host loop with int positions, torch argmax of the FP32 logits. Model B (same seeds): two eager steps
-    then graph replay through the pump. Same tokens; B's state matches A's step count and position."""
+    """Model A: host loop with int positions, the oracle's argmax of the BF16 logits. Model B (same seeds): two eager
+    steps then graph replay through the pump. Same tokens; B's state matches A's step count and position."""
     torch = torch_gpu
     from monolith_mi355 import kernels
     from monolith_mi355.runtime.step import StepProgram, StepState
@@ -270,8 +270,8 @@ def test_decoder_program_matches_host_loop(torch_gpu):
         h = kernels.embed(a.embed_table, torch.tensor([tok], dtype=torch.int32, device="cuda"))
         for layer in a.layers:
             h = layer.step(h, pos=pos)
-        logits = kernels.gemv(a.lm_head, h, norm_w=a.norm_w, eps=a.eps, out_f32=True)
-        tok = int(torch.argmax(logits[0]).item())
+        logits = kernels.gemv(a.lm_head, h, norm_w=a.norm_w, eps=a.eps)            # BF16, as the program's
+        tok = int(O.argmax(from_dev_bf16(logits))[0])
         host.append(tok)
         pos += 1
     b = _decoder(torch, 11)
@@ -430,3 +430,31 @@ def test_sample_distribution_determinism_and_device_seed(torch_gpu):
     got = kernels.sample(lb3, state=st.buf, temperature=1.1, top_k=100).cpu().tolist()
     l3 = from_dev_bf16(lb3)
     assert got == [O.sample(l3[i], seed=seed, step=17, t=i, temperature=1.1, top_k=100) for i in range(3)]
+
+
+def test_decoder_program_sampling_matches_host_loop(torch_gpu):
+    """The program with a sampler: the host loop draws each token with the oracle from the same BF16 logits, seed
+    and step; the replayed program (seed in the state's rng words, step from the state) draws the same tokens."""
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    from monolith_mi355.runtime.step import StepProgram, StepState
+    steps, seed = 12, 0xFEEDFACE12345
+    opts = dict(temperature=0.9, top_k=64, top_p=0.95)
+    a = _decoder(torch, 21)
+    tok, pos, host = 3, 40, []
+    for s in range(steps):
+        h = kernels.embed(a.embed_table, torch.tensor([tok], dtype=torch.int32, device="cuda"))
+        for layer in a.layers:
+            h = layer.step(h, pos=pos)
+        logits = from_dev_bf16(kernels.gemv(a.lm_head, h, norm_w=a.norm_w, eps=a.eps))
+        tok = O.sample(logits[0], seed=seed, step=s, t=0, **opts)
+        host.append(tok)
+        pos += 1
+    b = _decoder(torch, 21)
+    st = StepState(ring_capacity=64)
+    prog = StepProgram(b, st, ctx_cap=256, steps_per_graph=2, sampling=opts)
+    st.start(position=40, token=3)
+    st.write(rng_lo=seed & 0xFFFFFFFF, rng_hi=seed >> 32)
+    first = prog.step_eager(2)
+    rep = prog.run(steps - 2, launches_per_batch=2, in_flight=2)
+    assert first + rep.tokens == host
