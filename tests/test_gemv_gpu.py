@@ -215,14 +215,17 @@ def test_gemv_tiles_per_workgroup(torch_gpu, fmt, n, k, epi, rng, monkeypatch):
 
 
 @pytest.mark.parametrize("fmt", ["nvfp4", "int4_affine"])
-@pytest.mark.parametrize("mtok", [1, 2, 8])
-@pytest.mark.parametrize("plan", [None, "4,3", "tk"])
+@pytest.mark.parametrize("mtok", [1, 2, 3, 8, 16])
+@pytest.mark.parametrize("plan", [None, "4,3", "tk", "rowm2"])
 def test_gemv_gated_head_norm(torch_gpu, fmt, mtok, plan, rng, monkeypatch):
     """The Gated DeltaNet output norm fused into the output projection's input staging: per 128-column head,
-    bf16(bf16(bf16(w)·bf16(o·r))·silu(z)), then the GEMV — against the oracle's gated_rms_norm and matmul."""
+    bf16(bf16(bf16(w)·bf16(o·r))·silu(z)), then the GEMV — against the oracle's gated_rms_norm and matmul (M ≥ 3:
+    gemv_tk, whatever gemv_rowm split is asked for)."""
     from monolith_mi355 import kernels
     if plan == "tk":
         monkeypatch.setenv("MI_GEMV_KERNEL", "tk")
+    elif plan == "rowm2":
+        monkeypatch.setenv("MI_GEMV_ROWM", "2,0")
     elif plan:
         monkeypatch.setenv("MI_GEMV_ROW", plan)
     heads, n = 12, 320
