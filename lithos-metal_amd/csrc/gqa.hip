@@ -80,7 +80,8 @@ __device__ void prep_vec(const GqaArgs& a, const uint16_t* src, const float* nw,
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   __builtin_amdgcn_wave_barrier();
   const int half = a.rot / 2;
-  const int p = cur_pos(a) + t;
+  const int p = min(cur_pos(a) + t, a.ctx - 1);     // a device position past the cache (a stopped program's queued
+                                                   // steps) must not read past the RoPE tables
   float o[2];
 #pragma unroll
   for (int u = 0; u < 2; ++u) {

@@ -105,6 +105,8 @@ class GdnDecoderLayer:
         self.conv_state = [(torch.randn(self.conv_dim, conv - 1, generator=gen, device=device) * 0.5).to(torch.bfloat16),
                            torch.zeros(self.conv_dim, conv - 1, dtype=torch.bfloat16, device=device)]
         self.rec_state = torch.randn(v_heads, dk, dv, generator=gen, device=device) * 0.1
+        self.rec_slots = [self.rec_state, None]    # the second recurrent-state slot of a speculative verify pass
+        self.slot = 0
         self.parity = 0
         self._bufs: Dict[int, tuple] = {}
 
@@ -121,20 +123,50 @@ class GdnDecoderLayer:
 
     ping_pong = True          # the conv state alternates between two buffers: a captured program holds step pairs
 
-    def step(self, h, out=None, pos=None):
+    def _second_slot(self):
+        if self.rec_slots[1 - self.slot] is None:
+            self.rec_slots[1 - self.slot] = self.rec_slots[self.slot].clone()
+        return self.rec_slots[1 - self.slot]
+
+    def commit(self, t_dev):
+        """``gdn_commit`` after a verify pass (``step(..., verify=True)``): replay the first ``t_dev`` (device int32:
+        the accept scan's committed rows) tokens of that pass from its input state into the other slots, which
+        become the layer's state."""
+        kernels.gdn_step(self._verify_proj, self.conv_state[self.parity], self.conv_state[1 - self.parity],
+                         self.rec_slots[self.slot], self._second_slot(), conv_w=self.conv_w, neg_exp_a=self.neg_exp_a,
+                         dt_bias=self.dt_bias, norm_w=self.gdn_norm_w, k_heads=self.hk, v_heads=self.hv, dk=self.dk,
+                         dv=self.dv, conv_width=self.conv, eps=self.eps, commit=True, t_dev=t_dev)
+        self.parity ^= 1
+        self.slot ^= 1
+
+    @property
+    def rec(self):
+        """The current recurrent state."""
+        return self.rec_slots[self.slot]
+
+    def step(self, h, out=None, pos=None, verify: bool = False):
         """One decode step over ``h [M, hidden]`` bf16 (M ≤ 16 tokens): returns the layer output; advances the state.
-        ``pos`` is accepted for a uniform layer interface (the recurrence needs no position)."""
+        ``pos`` is accepted for a uniform layer interface (the recurrence needs no position). ``verify``: a
+        speculative verify pass — the outputs for every row, the state left for :meth:`commit`."""
         proj, o, h1, act, h2 = self.buffers(h.shape[0])
         out = h2 if out is None else out
         kernels.gemv(self.w_in.packed, h, norm_w=self.norm_w, eps=self.eps, out=proj)
+        rec = self.rec_slots[self.slot]
         # the gated norm rides on the output projection at M <= 2 (gemv_row); at M >= 3 its GEMV kernel keeps the
         # activations in registers and the norm stays a small kernel of its own. z must be a 16-byte aligned view.
         defer = h.shape[0] <= 2 and proj.stride(0) % 8 == 0
         cin, cout = self.conv_state[self.parity], self.conv_state[1 - self.parity]
-        kernels.gdn_step(proj, cin, cout, self.rec_state, self.rec_state, conv_w=self.conv_w, neg_exp_a=self.neg_exp_a,
+        if verify:                              # the verify pass writes the other slots; commit() settles them
+            rec_out = self._second_slot()
+        else:
+            rec_out = rec
+        kernels.gdn_step(proj, cin, cout, rec, rec_out, conv_w=self.conv_w, neg_exp_a=self.neg_exp_a,
                          dt_bias=self.dt_bias, norm_w=self.gdn_norm_w, k_heads=self.hk, v_heads=self.hv, dk=self.dk,
                          dv=self.dv, conv_width=self.conv, eps=self.eps, out=o, defer_norm=defer)
-        self.parity ^= 1
+        if verify:
+            self._verify_proj = proj
+        else:
+            self.parity ^= 1
         # the gated RMSNorm (gdn_norm) is applied by the output projection while it stages o; z = proj[:, :hv·dv]
         kernels.gemv(self.w_out.packed, o, epilogue="residual", residual=h, out=h1,
                      gated_norm=(self.gdn_norm_w, proj[:, : self.hv * self.dv], self.eps) if defer else None)
@@ -159,7 +191,7 @@ class GdnDecoderLayer:
                 "conv_w": self.conv_w.float().cpu().numpy(), "a_log": self.a_log.cpu().numpy(),
                 "dt_bias": self.dt_bias.cpu().numpy(), "gdn_norm_w": self.gdn_norm_w.cpu().numpy(),
                 "conv_state": self.conv_state[self.parity].float().cpu().numpy(),
-                "rec_state": self.rec_state.cpu().numpy()}
+                "rec_state": self.rec.cpu().numpy()}
 
 
 class AttnDecoderLayer:

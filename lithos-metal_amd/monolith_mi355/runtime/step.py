@@ -237,7 +237,8 @@ class StepProgram:
             self.capture()
         st = self.state
         launches = -(-max_steps // self.steps_per_graph)
-        cap = token_capacity if token_capacity is not None else launches * self.steps_per_graph + 16
+        per_step = getattr(self, "t", 1)                     # tokens a step can emit
+        cap = token_capacity if token_capacity is not None else launches * self.steps_per_graph * per_step + 16
         tokens = np.zeros(max(cap, 1), np.int32)
         d = hip.MiRunnerDesc(graph_exec=self.graph.exec, stream=self.graph.stream, state=hip.ptr(st.buf),
                              ring=st.ring.addr, ring_capacity=st.ring_capacity, host_ctl=st.ctl.addr,
@@ -248,3 +249,63 @@ class StepProgram:
         return StepReport(stats.launches * self.steps_per_graph, stats.launches, stats.batches, stats.gpu_ms,
                           stats.wall_ms, stats.host_busy_ms, bool(stats.done), int(stats.error),
                           tokens[: d.n_tokens].tolist(), stats.launch_ms, stats.wait_ms)
+
+
+class SpecProgram(StepProgram):
+    """The speculative decode round on a static ``1 + gamma``-row step (the reference's DSpark program,
+    ``compiler/emit.py:1392-1470`` with ``speculative=True``, minus the drafter): ``embed(pending_tokens) → layers at
+    M = 1 + gamma (Gated DeltaNet layers verify into their second state slot, attention appends every row) → lm_head
+    → argmax per row → accept_scan (the matching prefix + bonus token to the ring) → gdn_commit per GDN layer (replay
+    of the committed rows) → draft source → verify_select (the next step's rows)``. Every count the round needs
+    (verify length, committed rows, position) stays on the device, so the step replays as a graph. Rows past the
+    step's ``t_this_step`` are computed and discarded; their cache entries are overwritten by later steps.
+
+    The drafter itself is outside this build: ``draft_table`` (int32 ``[ctx, ≥ gamma]``) stands in for it — row p
+    holds the drafts proposed after a token at position p — read by ``embed`` at the step state's position."""
+
+    def __init__(self, model, state: StepState, *, gamma: int, draft_table, eos: Sequence[int] = (), ctx_cap: int = 0,
+                 steps_per_graph: int = 2, stream=None):
+        torch = _torch()
+        if not 1 <= gamma <= 15:
+            raise ValueError("gamma must be in 1..15")
+        super().__init__(model, state, eos=eos, ctx_cap=ctx_cap, steps_per_graph=steps_per_graph, stream=stream)
+        self.gamma, self.t = gamma, gamma + 1
+        dev = state.buf.device
+        vocab, hidden = model.embed_table.shape
+        self.h0 = torch.empty(self.t, hidden, dtype=torch.bfloat16, device=dev)
+        self.logits = torch.empty(self.t, vocab, dtype=torch.bfloat16, device=dev)
+        w = -(-gamma // 4) * 4                               # drafts per table row, padded to 16 bytes
+        if draft_table.dtype != torch.int32 or draft_table.dim() != 2 or draft_table.shape[1] < gamma:
+            raise ValueError("draft_table must be int32 [ctx, >= gamma]")
+        tbl = torch.zeros(draft_table.shape[0], w, dtype=torch.int32, device=dev)
+        tbl[:, :gamma] = draft_table[:, :gamma]
+        self.draft_rows = tbl.view(torch.bfloat16)           # [ctx, 2w] 16-bit words: embed copies them verbatim
+        self.draft_buf = torch.zeros(1, 2 * w, dtype=torch.bfloat16, device=dev)
+        self.drafts = self.draft_buf.view(torch.int32).view(-1)
+        self.conf = torch.ones(gamma, dtype=torch.float32, device=dev)
+        self.log = torch.zeros(64, dtype=torch.int32, device=dev)
+
+    def enqueue_step(self):
+        torch = _torch()
+        m, st, s, t = self.model, self.state, self.stream, self.t
+        kernels.embed(m.embed_table, st.view("pending_tokens", t), t=t, out=self.h0, stream=s)
+        h = self.h0
+        pos = st.view("position")
+        with torch.cuda.stream(s):
+            for layer in m.layers:
+                h = layer.step(h, pos=pos, verify=True) if getattr(layer, "ping_pong", False) else layer.step(h, pos=pos)
+        kernels.gemv(m.lm_head, h, norm_w=m.norm_w, eps=m.eps, out=self.logits, stream=s)
+        kernels.argmax(self.logits, out=self.ids, stream=s)
+        kernels.accept_scan(st.buf, self.ids, st.ring.addr, st.ring_capacity, eos=self.eos, log=self.log,
+                            ctx_cap=self.ctx_cap, host_ctl=st.ctl.addr, stream=s)
+        with torch.cuda.stream(s):
+            for layer in m.layers:
+                if getattr(layer, "ping_pong", False):
+                    layer.commit(st.view("checkpoint_index"))
+        kernels.embed(self.draft_rows, st.view("position"), t=1, out=self.draft_buf, stream=s)
+        kernels.verify_select(st.buf, self.drafts, self.conf, gamma=self.gamma, threshold=float(self.gamma),
+                              t_max=t, mode=2, ctx_cap=self.ctx_cap, stream=s)
+
+    def acceptance(self) -> List[int]:
+        """The accept scan's per-step log entries ``(committed << 16) | (L << 8) | accepted`` of the last 64 steps."""
+        return self.log.cpu().tolist()

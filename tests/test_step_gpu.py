@@ -458,3 +458,41 @@ def test_decoder_program_sampling_matches_host_loop(torch_gpu):
     first = prog.step_eager(2)
     rep = prog.run(steps - 2, launches_per_batch=2, in_flight=2)
     assert first + rep.tokens == host
+
+
+# ---- the speculative round: graph replay of verify → accept → commit → select ------------------------------------
+
+def _spec_run(torch, table, steps, *, eager_steps=2, ctx_cap=240):
+    from monolith_mi355.runtime.step import SpecProgram, StepState
+    model = _decoder(torch, 31)
+    st = StepState(ring_capacity=512)
+    prog = SpecProgram(model, st, gamma=7, draft_table=table, ctx_cap=ctx_cap, steps_per_graph=2)
+    st.start(position=40, token=9)
+    first = prog.step_eager(eager_steps)
+    rep = prog.run(steps - eager_steps, launches_per_batch=2, in_flight=2)
+    return first + rep.tokens, st.read(), prog
+
+
+def test_spec_program_accepted_drafts_change_nothing_but_the_step_count(torch_gpu):
+    """Run A: random drafts (all but never accepted) — one token per step. Run B: the drafts are A's own tokens —
+    up to eight per step. Every row of the verify pass computes exactly what a one-token step computes at that
+    position (GEMV, recurrence, cache appends and attention are per-row), so B's tokens are A's, in far fewer
+    steps; the committed state (position, ring) follows the tokens."""
+    torch = torch_gpu
+    _say("spec program")
+    rng = np.random.default_rng(5)
+    ctx = 256
+    rand = torch.from_numpy(rng.integers(0, 4096, size=(ctx, 7), dtype=np.int32)).cuda()
+    a, st_a, _ = _spec_run(torch, rand, 40)
+    assert len(a) >= 40 and st_a["error"] == 0
+    seq = [9] + a                                            # the token at position 40 + i
+    perfect = np.zeros((ctx, 7), np.int32)
+    for p in range(40, ctx):
+        for j in range(7):
+            i = p - 40 + 1 + j
+            perfect[p, j] = seq[i] if i < len(seq) else 0
+    b, st_b, prog = _spec_run(torch, torch.from_numpy(perfect).cuda(), 8)
+    assert len(b) >= 40 and b[:40] == a[:40], (a, b)
+    assert st_b["step"] == 8 and st_b["position"] == 40 + len(b) and st_b["ring_head"] == len(b)
+    log = [((e >> 16), (e >> 8) & 0xFF, e & 0xFF) for e in prog.acceptance()[:8]]
+    assert log[0] == (1, 0, 0) and all(x == (8, 7, 7) for x in log[1:5]), log   # whole blocks accepted
