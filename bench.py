@@ -10,7 +10,7 @@ M = 8, the gated-GQA layer (24 q / 4 KV heads of 128, int8 KV cache at a 32K con
 and the MLP alone; the FP8 E4M3 GEMV (the 27B checkpoint's format for its mixer projections) at the
 GDN in_proj shape with its fused norm, M = 1 and 8; and the GPU-resident token loop (embedding, a GDN and an
 attention layer, the BF16 LM head over a 248320-token vocabulary, argmax and advance, replayed as a graph by the
-native pump; wall time per token).
+native pump; wall time per token), and the speculative round on the same model (eight rows verified per step).
 
 One step = one layer forward over one token batch. Weights, states and KV caches are resident in HBM before the
 timed region; the step rotates over ``--layers`` distinct layer instances (≥ 2 GB in all), so the 256 MB MALL
@@ -178,6 +178,30 @@ def main():
             loop_info = {"tokens": len(rep.tokens), "gpu_ms_per_token": round(rep.gpu_ms / rep.steps_submitted, 5),
                          "host_busy_fraction": round(rep.host_busy_ms / rep.wall_ms, 4)}
             del prog, model, layers
+            # the speculative round (gamma = 7: eight rows verified per step) on the same two layers + LM head,
+            # drafts from a table the accept scan rejects (random ids): the round's time; every row is computed
+            # whatever is accepted, so tokens per second scale with the accepted drafts per step
+            from monolith_mi355.runtime.step import SpecProgram
+            layers = [GdnDecoderLayer(seed=72, device=dev), AttnDecoderLayer(seed=73, ctx=CTX, device=dev)]
+            layers[1].fill_cache(CTX - 1024, gen)
+            model = DecoderModel(layers, vocab=248320, hidden=5120, device=dev)
+            st = StepState(ring_capacity=8192, device=dev)
+            table = torch.randint(0, 248320, (CTX, 7), generator=gen, device=dev, dtype=torch.int32)
+            prog = SpecProgram(model, st, gamma=7, draft_table=table, ctx_cap=CTX - 16, steps_per_graph=2)
+            start = CTX - 1024
+            st.start(position=start, token=11)
+            prog.step_eager(2)
+            st.start(position=start, token=11)
+            prog.run(16, launches_per_batch=8, in_flight=2)
+            st.start(position=start, token=11)
+            rep = prog.run(128, launches_per_batch=8, in_flight=2)
+            spec_ms = rep.wall_ms / rep.steps_submitted
+            spec_info = {"ms_per_round": round(spec_ms, 5), "rows_per_round": 8,
+                         "tokens_per_s_at_0_accepted": round(1e3 / spec_ms, 1),
+                         "tokens_per_s_if_all_7_accepted": round(8e3 / spec_ms, 1),
+                         "workload": "embed + GDN layer + attention layer (32K) + BF16 lm_head 248320 at M = 8 + "
+                                     "argmax + accept_scan + gdn_commit + draft table + verify_select, graph replay"}
+            del prog, model, layers
 
     def rate(key):
         ms, b = out[key]
@@ -228,6 +252,7 @@ def main():
         "mlp_m8": entry("mlp_m8", 8),
         "fp8_in_proj_m1": entry("fp8_m1", 1),
         "fp8_in_proj_m8": entry("fp8_m8", 8),
+        "spec_round_2layers_ctx32k": spec_info,
         "token_loop_2layers_ctx32k": dict(entry("loop", 1), **loop_info,
                                           workload="embed + GDN layer + attention layer (32K) + BF16 lm_head 248320 "
                                                    "+ argmax + advance, graph replay through the native pump"),

@@ -310,7 +310,7 @@ __global__ __launch_bounds__(64) void advance_step(mi_advance_desc d) {
   if (threadIdx.x != 0) return;
   mi_step_state* st = d.state;
   if (st->done) return;
-  const uint32_t t = st->t_this_step;
+  const uint32_t t = min(max(st->t_this_step, 1u), (uint32_t)MI_STEP_T_MAX);   // a state the host left inconsistent
   if (st->prefill_left > 0) {                       // a prompt chunk: no token leaves the step
     st->position += t;
     st->step += 1;
@@ -318,7 +318,7 @@ __global__ __launch_bounds__(64) void advance_step(mi_advance_desc d) {
     publish_ctl(d.host_ctl, st);
     return;
   }
-  const int32_t tok = d.tokens[t > 0 ? t - 1 : 0];
+  const int32_t tok = d.tokens[t - 1];
   const uint32_t head = st->ring_head;
   if (head - st->ring_tail >= d.ring_cap) {         // the host has not drained: overflow
     st->error = 1;
@@ -419,7 +419,9 @@ __global__ __launch_bounds__(64) void accept_scan_step(mi_accept_scan_desc d) {
   if (threadIdx.x != 0) return;
   mi_step_state* st = d.state;
   if (st->done) return;
-  const uint32_t t = st->t_this_step;
+  // the step's rows and verify length as the state holds them, kept inside the token rows whatever the host left
+  // there (t in 1..16, L <= t - 1), so no row index falls outside the step
+  const uint32_t t = min(max(st->t_this_step, 1u), (uint32_t)MI_STEP_T_MAX);
   if (st->prefill_left > 0) {                       // a prompt chunk: nothing to verify; its rows are injected next
     if (d.log_cap) d.log[st->step % d.log_cap] = (t << 16) | 0xFFFFu;
     st->position += t;
@@ -431,7 +433,7 @@ __global__ __launch_bounds__(64) void accept_scan_step(mi_accept_scan_desc d) {
     publish_ctl(d.host_ctl, st);
     return;
   }
-  const uint32_t L = st->verify_len;
+  const uint32_t L = min(st->verify_len, t - 1);
   const uint32_t base = t - 1 - L;                  // the anchor's row
   uint32_t acc = 0;
   while (acc < L && d.tokens[base + acc] == st->pending_tokens[base + acc + 1]) ++acc;

@@ -114,11 +114,14 @@ class StepState:
         torch.cuda.synchronize(self.buf.device)
 
     def start(self, *, position: int, token: int, stop_at: int = 0, prefill_left: int = 0):
-        """Begin a sequence: the step at ``position`` embeds ``token``; the ring and the stop flags restart."""
+        """Begin a sequence: the step at ``position`` embeds ``token``; the ring, the stop flags and every
+        speculative field (verify length, drafts, acceptance, injection counts) restart; the RNG words are kept."""
         self.ring.array[:] = 0
         self.ctl.array[:] = 0
         self.write(step=0, position=position, kv_len=position, t_this_step=1, pending_tokens=[token], anchor=token,
-                   done=0, error=0, ring_head=0, ring_tail=0, stop_at=stop_at, prefill_left=prefill_left)
+                   gamma=0, draft_tokens=[], confidence=[], verify_len=0, accepted=0, checkpoint_index=0,
+                   drafter_ctx_len=0, done=0, error=0, ring_head=0, ring_tail=0, prefill_left=prefill_left,
+                   n_inject=0, stop_at=stop_at, n_chain=0)
 
     def drain(self, tokens: List[int]) -> int:
         """Take ring slots in sequence order (the host pump does this natively; here for eager loops)."""

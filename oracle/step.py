@@ -67,7 +67,7 @@ def advance(st: Dict[str, object], tokens: Sequence[int], ring: np.ndarray, *, e
     full (error 1), make it the pending token, move position / step, stop at ``stop_at``, an EOS id or ``ctx_cap``."""
     if st["done"]:
         return
-    t = st["t_this_step"]
+    t = min(max(st["t_this_step"], 1), 16)          # this build's guard: rows stay inside the step's 16
     if st["prefill_left"] > 0:
         st["position"] += t
         st["step"] += 1
@@ -161,7 +161,7 @@ def accept_scan(st: Dict[str, object], tokens: Sequence[int], ring: np.ndarray, 
     """``spec_ops.metal:148-195``: commit the matching prefix of the drafts and the bonus token, advance the state."""
     if st["done"]:
         return
-    t = st["t_this_step"]
+    t = min(max(st["t_this_step"], 1), 16)          # this build's guard: rows stay inside the step's 16
     cap = ring.shape[0]
     log_cap = 0 if log is None else log.shape[0]
     if st["prefill_left"] > 0:
@@ -174,7 +174,7 @@ def accept_scan(st: Dict[str, object], tokens: Sequence[int], ring: np.ndarray, 
         if ctx_cap and st["position"] >= ctx_cap:
             st["error"], st["done"] = 2, 1
         return
-    L = st["verify_len"]
+    L = min(st["verify_len"], t - 1)                # this build's guard (the reference kernel trusts the state)
     base = t - 1 - L
     acc = 0
     while acc < L and int(tokens[base + acc]) == st["pending_tokens"][base + acc + 1]:

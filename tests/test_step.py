@@ -270,3 +270,13 @@ def test_sample_oracle_follows_the_warped_softmax():
     p = O.warped_probabilities(lf, temperature=0.9)
     sigma = np.sqrt(p * (1 - p) / n)
     assert np.all(np.abs(counts / n - p)[:16] <= 4 * sigma[:16] + 1e-9) and counts[16:].sum() == 0
+
+
+def test_accept_scan_oracle_guards_an_inconsistent_state():
+    """A verify length longer than the step (a state the host left stale) is read as the step allows: t = 1 means
+    the anchor row alone, whatever verify_len says (this build's guard; the kernel then never indexes outside the
+    step's rows)."""
+    st = O.new_state(t_this_step=1, verify_len=7, position=10, pending_tokens=[3, 4, 5])
+    ring = np.zeros(8, np.uint64)
+    O.accept_scan(st, [42] + [0] * 15, ring)
+    assert st["ring_head"] == 1 and int(ring[0]) & 0xFFFFFFFF == 42 and st["position"] == 11 and st["accepted"] == 0

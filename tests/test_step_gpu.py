@@ -496,3 +496,26 @@ def test_spec_program_accepted_drafts_change_nothing_but_the_step_count(torch_gp
     assert st_b["step"] == 8 and st_b["position"] == 40 + len(b) and st_b["ring_head"] == len(b)
     log = [((e >> 16), (e >> 8) & 0xFF, e & 0xFF) for e in prog.acceptance()[:8]]
     assert log[0] == (1, 0, 0) and all(x == (8, 7, 7) for x in log[1:5]), log   # whole blocks accepted
+
+
+def test_start_resets_the_speculative_fields_and_the_scan_guards_a_stale_state(torch_gpu):
+    """Regression: a program restarted with StepState.start after speculative steps kept verify_len, and the accept
+    scan then indexed rows below the step. start() clears every speculative field; the scan also keeps L <= t - 1."""
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    from monolith_mi355.runtime.step import StepState
+    st = StepState(ring_capacity=8)
+    st.write(t_this_step=8, verify_len=7, accepted=5, checkpoint_index=6, n_inject=6, gamma=7,
+             draft_tokens=[1] * 15, confidence=[0.5] * 15, drafter_ctx_len=3, n_chain=1)
+    st.start(position=10, token=3)
+    g = st.read()
+    for k in ("verify_len", "accepted", "checkpoint_index", "n_inject", "gamma", "drafter_ctx_len", "n_chain"):
+        assert g[k] == 0, k
+    assert g["draft_tokens"] == [0] * 15 and g["confidence"] == [0.0] * 15 and g["t_this_step"] == 1
+    st.write(verify_len=7)                                   # stale, as before the fix
+    ids = torch.full((16,), 42, dtype=torch.int32, device="cuda")
+    kernels.accept_scan(st.buf, ids, st.ring.addr, 8, host_ctl=st.ctl.addr)
+    torch.cuda.synchronize()
+    g = st.read()
+    assert g["ring_head"] == 1 and g["position"] == 11 and g["accepted"] == 0
+    assert int(st.ring.array[0]) & 0xFFFFFFFF == 42
