@@ -8,7 +8,8 @@ and the NVFP4 gated MLP of BASELINE configs[1] (gate|up 2×17408×5120 with silu
 residual). ``value`` is that layer's algorithmic HBM bytes ÷ its step time at M = 1. Beside it: the same layer at
 M = 8, the gated-GQA layer (24 q / 4 KV heads of 128, int8 KV cache at a 32K context; configs[2]) at M = 1 and 8,
 and the MLP alone; the FP8 E4M3 GEMV (the 27B checkpoint's format for its mixer projections) at the
-GDN in_proj shape with its fused norm, M = 1 and 8; and the GPU-resident token loop (embedding, a GDN and an
+GDN in_proj shape with its fused norm, M = 1 and 8; the hybrid MoE layer's feed-forward (configs[4]: router, top-8 of
+256 NVFP4 experts, shared expert, combine), M = 1 and 8; and the GPU-resident token loop (embedding, a GDN and an
 attention layer, the BF16 LM head over a 248320-token vocabulary, argmax and advance, replayed as a graph by the
 native pump; wall time per token), and the speculative round on the same model (eight rows verified per step).
 
@@ -45,7 +46,7 @@ def parse():
     p.add_argument("--layers", type=int, default=10, help="distinct layer instances the steps rotate over")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--only", choices=["gdn", "attn", "mlp", "gateup", "fp8", "loop", "copy"], default=None,
+    p.add_argument("--only", choices=["gdn", "attn", "mlp", "gateup", "fp8", "moe", "loop", "copy"], default=None,
                    help="time one workload only (profiling runs; copy = a 256 MiB device copy, the counter reference)")
     return p.parse_args()
 
@@ -156,6 +157,19 @@ def main():
                 out[f"attn_m{m}"] = (ms, attn[0].bytes_per_step(m, pos))
             del attn
 
+        if args.only in (None, "moe"):
+            # the hybrid MoE layer's feed-forward: hidden 2048, 256 NVFP4 experts of 512, top-8 +
+            # shared expert; two instances rotate (each ≈ 0.45 GB of experts); bytes count the experts chosen
+            from monolith_mi355.layers import MoeBlock
+            blocks = [MoeBlock(seed=80 + i, device=dev) for i in range(2)]
+            for m in (1, 8):
+                x = torch.randn(m, 2048, generator=gen, device=dev).to(torch.bfloat16)
+                ms = timed_graph(lambda i: blocks[i % 2](x), args.steps, args.warmup, stream)
+                distinct = [len(set(b.buffers(m)[1][0].flatten().tolist())) for b in blocks]
+                nbytes = sum(b.bytes_per_step(m, d) for b, d in zip(blocks, distinct)) // len(blocks)
+                out[f"moe_m{m}"] = (ms, nbytes)
+                moe_experts = distinct
+            del blocks
         if args.only in (None, "loop"):
             # the GPU-resident token loop: embed → GDN layer → attention layer (32K context) → final norm + BF16
             # lm_head (248320×5120) → argmax → advance, replayed as a graph of 2 steps by the native pump
@@ -252,6 +266,9 @@ def main():
         "mlp_m8": entry("mlp_m8", 8),
         "fp8_in_proj_m1": entry("fp8_m1", 1),
         "fp8_in_proj_m8": entry("fp8_m8", 8),
+        "moe_block_m1": dict(entry("moe_m1", 1), workload="MoE feed-forward: router + top-8 of 256 NVFP4 experts "
+                             "(hidden 2048, intermediate 512) + shared expert + combine"),
+        "moe_block_m8": entry("moe_m8", 8),
         "spec_round_2layers_ctx32k": spec_info,
         "token_loop_2layers_ctx32k": dict(entry("loop", 1), **loop_info,
                                           workload="embed + GDN layer + attention layer (32K) + BF16 lm_head 248320 "

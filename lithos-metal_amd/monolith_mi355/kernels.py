@@ -282,17 +282,26 @@ def gqa_decode(proj, cache: KVCache, pos, *, heads: int, rope_cos, rope_sin, gat
 GROUP_REC = 18
 
 
-def moe_route(logits, top_k: int, *, renorm: bool = True, groups: bool = True, stream=None):
+def moe_route(logits, top_k: int, *, renorm: bool = True, groups: bool = True, out=None, stream=None):
     """``moe_route`` (``ops/moe.py``): ``logits [T, E]`` bf16 → ``(ids [T, k] int32, weights [T, k] float32,
-    groups [max_groups, 18] int32 or None)``; ``max_groups = min(E, T·k)``. The groups feed ``moe_gemv``."""
+    groups [max_groups, 18] int32 or None)``; ``max_groups = min(E, T·k)``. The groups feed ``moe_gemv``. ``out``:
+    preallocated ``(ids, weights, groups)`` (a captured step allocates nothing)."""
     torch = _torch()
     _bf16_2d(logits, "moe_route logits", aligned=False)
     t, e = logits.shape
     dev = logits.device
-    ids = torch.empty((t, top_k), dtype=torch.int32, device=dev)
-    w = torch.empty((t, top_k), dtype=torch.float32, device=dev)
     max_groups = min(e, t * top_k)
-    g = torch.empty((max_groups, GROUP_REC), dtype=torch.int32, device=dev) if groups else None
+    if out is not None:
+        ids, w, g = out
+        if (ids.dtype != torch.int32 or ids.numel() < t * top_k or w.dtype != torch.float32 or w.numel() < t * top_k
+                or (groups and (g is None or g.dtype != torch.int32 or g.shape[0] < max_groups
+                                or g.shape[1] != GROUP_REC))):
+            raise ValueError("moe_route: out must be (int32 [T, k], float32 [T, k], int32 [max_groups, 18])")
+        g = g if groups else None
+    else:
+        ids = torch.empty((t, top_k), dtype=torch.int32, device=dev)
+        w = torch.empty((t, top_k), dtype=torch.float32, device=dev)
+        g = torch.empty((max_groups, GROUP_REC), dtype=torch.int32, device=dev) if groups else None
     d = hip.MiMoeRouteDesc(t=t, n_experts=e, top_k=top_k, renorm=int(renorm), logits=hip.ptr(logits),
                            ld_logits=logits.stride(0), ids=hip.ptr(ids), weights=hip.ptr(w), groups=hip.ptr(g),
                            max_groups=max_groups if groups else 0)

@@ -268,6 +268,78 @@ class AttnDecoderLayer:
                 "v_codes": c.v_codes_token_major().cpu().numpy(), "v_scales": c.v_scales.cpu().numpy()}
 
 
+class MoeBlock:
+    """The hybrid MoE layer's feed-forward (``nn/moe.py``; BASELINE configs[4], 35B-A3B-like): RMSNorm fused into the
+    router GEMV (BF16) and the expert GEMVs, softmax top-k routing (renormalized) with the expert groups, the grouped
+    gate|up GEMV (silu·mul, rounded as the reference's expert MLP) and down GEMV over the chosen experts only, one
+    shared expert with its σ-gate, and the weighted combine plus residual. NVFP4 experts stored back to back."""
+
+    def __init__(self, *, hidden=2048, experts=256, top_k=8, inter=512, shared_inter=512, eps=1e-6, device="cuda",
+                 seed=0):
+        torch = _torch()
+        gen = torch.Generator(device=device)
+        gen.manual_seed(seed)
+        self.hidden, self.experts, self.top_k, self.inter, self.eps = hidden, experts, top_k, inter, eps
+        self.norm_w = 1.0 + torch.randn(hidden, generator=gen, device=device) * 0.1
+        self.router_w = (torch.randn(experts, hidden, generator=gen, device=device) * 0.02).to(torch.bfloat16)
+        self.router = kernels.PackedWeight("bf16", experts, hidden, 1, DV.pack_bf16(self.router_w), None)
+
+        def stack(mats):
+            return kernels.PackedWeight("nvfp4", mats[0].packed.n, mats[0].packed.k, len(mats),
+                                        torch.cat([m.packed.data for m in mats]),
+                                        torch.cat([m.packed.row_scale for m in mats]))
+        self.gate_up_q = [nvfp4_matrix(2 * inter, hidden, gen, device, gate_up=True) for _ in range(experts)]
+        self.down_q = [nvfp4_matrix(hidden, inter, gen, device) for _ in range(experts)]
+        self.gate_up, self.down = stack(self.gate_up_q), stack(self.down_q)
+        self.shared_gate_up = nvfp4_matrix(2 * shared_inter, hidden, gen, device, gate_up=True)
+        self.shared_down = nvfp4_matrix(hidden, shared_inter, gen, device)
+        self.shared_gate_w = (torch.randn(1, hidden, generator=gen, device=device) * 0.02).to(torch.bfloat16)
+        self.shared_gate = kernels.PackedWeight("bf16", 1, hidden, 1, DV.pack_bf16(self.shared_gate_w), None)
+        self.shared_inter = shared_inter
+        self._bufs: Dict[int, tuple] = {}
+
+    def buffers(self, m: int):
+        torch = _torch()
+        if m not in self._bufs:
+            dev, k, g = self.norm_w.device, self.top_k, min(self.experts, m * self.top_k)
+            bf = torch.bfloat16
+            self._bufs[m] = (torch.empty(m, self.experts, dtype=bf, device=dev),
+                             (torch.empty(m, k, dtype=torch.int32, device=dev),
+                              torch.empty(m, k, dtype=torch.float32, device=dev),
+                              torch.empty(g, kernels.GROUP_REC, dtype=torch.int32, device=dev)),
+                             torch.empty(m * k, self.inter, dtype=bf, device=dev),
+                             torch.empty(m * k, self.hidden, dtype=bf, device=dev),
+                             torch.empty(m, self.shared_inter, dtype=bf, device=dev),
+                             torch.empty(m, self.hidden, dtype=bf, device=dev),
+                             torch.empty(m, 1, dtype=bf, device=dev),
+                             torch.empty(m, self.hidden, dtype=bf, device=dev))
+        return self._bufs[m]
+
+    def __call__(self, h, out=None):
+        """``h [M, hidden]`` bf16 → the block's output with the residual added (M ≤ 16)."""
+        m = h.shape[0]
+        logits, route, act, hk, s_act, s_out, s_gate, y = self.buffers(m)
+        out = y if out is None else out
+        kernels.gemv(self.router, h, norm_w=self.norm_w, eps=self.eps, out=logits)
+        _, wts, groups = kernels.moe_route(logits, self.top_k, renorm=True, out=route)
+        kernels.moe_gemv(self.gate_up, h, groups, tokens=m, top_k=self.top_k, x_per_slot=False,
+                         epilogue="silu_mul_rounded", norm_w=self.norm_w, eps=self.eps, out=act)
+        kernels.moe_gemv(self.down, act, groups, tokens=m, top_k=self.top_k, x_per_slot=True, out=hk)
+        kernels.gemv(self.shared_gate_up.packed, h, epilogue="silu_mul", norm_w=self.norm_w, eps=self.eps, out=s_act)
+        kernels.gemv(self.shared_down.packed, s_act, out=s_out)
+        kernels.gemv(self.shared_gate, h, norm_w=self.norm_w, eps=self.eps, out=s_gate)
+        return kernels.moe_combine(hk, wts, top_k=self.top_k, shared=s_out, shared_gate=s_gate, residual=h, out=out)
+
+    def bytes_per_step(self, m: int, distinct_experts: int) -> int:
+        """Algorithmic HBM bytes of one step with ``distinct_experts`` experts chosen over the M tokens."""
+        k = self.top_k
+        expert = _gemv_bytes(2 * self.inter, self.hidden, 0) + _gemv_bytes(self.hidden, self.inter, 0)
+        return (self.experts * self.hidden * 2 + m * self.hidden * 2 + self.hidden * 4      # router, x, norm w
+                + distinct_experts * expert + m * k * (self.inter * 2 * 2 + self.hidden * 2 * 2)
+                + _gemv_bytes(2 * self.shared_inter, self.hidden, m, n_out=self.shared_inter)
+                + _gemv_bytes(self.hidden, self.shared_inter, m) + self.hidden * 2 + m * self.hidden * 4)
+
+
 class DecoderModel:
     """Embedding, decoder layers, final RMSNorm and LM head (``nn/decoder.py``, ``models/*``): what a step program
     runs once per token. ``lm_head`` is BF16 (the reference's unquantized head), its RMSNorm fused on load."""

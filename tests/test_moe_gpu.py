@@ -208,3 +208,42 @@ def test_moe_rejects_bad_descriptors():
     for kw in (dict(hidden=2044), dict(ldh=2047), dict(h=8), dict(shared=256, ld_shared=2048), dict(out=0)):
         assert lib.mi_moe_combine(C.byref(hip.MiMoeCombineDesc(**{**cb, **kw})), None) == 1, kw
         assert hip.last_error().startswith("mi_moe_combine")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("t", [1, 8])
+def test_moe_block_layer(torch_gpu, t):
+    """layers.MoeBlock (the bench's MoE workload) against the oracle's SparseMoE forward, with its own weights
+    dequantized bit-exactly on the device (gate|up rows un-interleaved): route ids equal, output within the bar."""
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    from monolith_mi355.layers import MoeBlock
+    blk = MoeBlock(experts=32, seed=3)
+    rng = np.random.default_rng(40 + t)
+    h = rbf(rng.standard_normal((t, 2048)))
+    hd = to_dev_bf16(torch, h)
+    y = from_dev_bf16(blk(hd))
+    logits = from_dev_bf16(blk.buffers(t)[0])
+    ids = blk.buffers(t)[1][0].cpu().numpy()
+
+    def dense(w, expert=0, gate_up=False):
+        d = kernels.dequant(w, expert=expert).cpu().numpy()
+        if gate_up:
+            n, k = d.shape
+            d = d.reshape(n // 16, 2, 8, k)
+            d = np.concatenate([d[:, 0].reshape(-1, k), d[:, 1].reshape(-1, k)])
+        return d
+
+    w_gu = np.stack([dense(blk.gate_up, e, True) for e in range(32)])
+    w_dn = np.stack([dense(blk.down, e) for e in range(32)])
+    s_gu, s_dn = dense(blk.shared_gate_up.packed, 0, True), dense(blk.shared_down.packed)
+    wn = (blk.norm_w.cpu().numpy() - 1.0).astype(np.float32)
+    xn = ON.rms_norm(h, wn, 1e-6)
+    from oracle.fp import bf16_to_f32
+    rw = bf16_to_f32(blk.router_w.view(torch.int16).cpu().numpy().astype(np.uint16))
+    gw = bf16_to_f32(blk.shared_gate_w.view(torch.int16).cpu().numpy().astype(np.uint16))
+    assert check_against_oracle(logits, ON.linear(xn, rw)).ok_rounded()
+    ref, ref_ids, _ = ON.moe_forward(xn, h, logits, 8, w_gu, w_dn, renorm=True, shared=(s_gu, s_dn, gw))
+    assert np.array_equal(ids, ref_ids)
+    chk = check_against_oracle(y, ref)
+    assert chk.ok_rounded(), chk
