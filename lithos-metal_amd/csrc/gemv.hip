@@ -1221,9 +1221,10 @@ __global__ __launch_bounds__(512) void gemv_tk(Args a) {
     uint16_t* dst = xs + (size_t)j * ld;
     const int nv = cols / 8;
     float sq = 0.0f;
+    const bool whole = kw == a.chunks;          // the split covers the row: its sum of squares comes with the staging
     for (int v = lane; v < nv; v += 64) {
       const uint4 q = *reinterpret_cast<const uint4*>(src + v * 8);
-      if (a.norm_w) {
+      if (a.norm_w && whole) {
         const uint32_t qq[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -1233,8 +1234,20 @@ __global__ __launch_bounds__(512) void gemv_tk(Args a) {
       }
       *reinterpret_cast<uint4*>(dst + v * 8) = q;
     }
+    if (a.norm_w && !whole) {                   // K split: the whole row's sum of squares, in the same order
+      const uint16_t* row = a.x + xrow_of(j) * a.ldx;
+      for (int v = lane; v < a.chunks * KC / 8; v += 64) {
+        const uint4 q = *reinterpret_cast<const uint4*>(row + v * 8);
+        const uint32_t qq[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float lo = bf16_bits_to_f32(qq[i] & 0xFFFFu), hi = bf16_bits_to_f32(qq[i] >> 16);
+          sq = fmaf(lo, lo, fmaf(hi, hi, sq));
+        }
+      }
+    }
     float rr = 1.0f;
-    if (a.norm_w) rr = 1.0f / sqrtf(wave_sum(sq) / (float)a.k + a.eps);   // one split covers the row here
+    if (a.norm_w) rr = 1.0f / sqrtf(wave_sum(sq) / (float)a.k + a.eps);
     float mx = 0.0f;
     if (a.norm_w || a.gnorm_w || MF || FMT == FMT_INT4) {
       wave_lds_sync();
@@ -1721,7 +1734,7 @@ Plan plan_row(const mi_gemv_desc* d, int fmt, int chunks, int rows, int n_tiles,
     sscanf(env, "%d,%d,%d", &force_kw, &force_ks, &force_rt);
   for (int ks : {1, 3, 2, 4}) {
     if (force_ks && ks != force_ks) continue;
-    if (ks > 1 && (d->norm_w || d->groups)) break;
+    if (ks > 1 && d->groups) break;
     int kc = (chunks + ks - 1) / ks;
     if (fmt == FMT_NVFP4 && ks > 1) kc = (kc + 7) / 8 * 8;      // splits on scale-group boundaries
     if (ks > 1 && (ks - 1) * kc >= chunks) continue;
@@ -1789,7 +1802,7 @@ Plan plan_tk(const mi_gemv_desc* d, int fmt, int chunks, int n_tiles, int groups
   double best_cost = 1e30;
   for (int ks = 1; ks <= 16; ++ks) {
     if (force[0] && ks != force[0]) continue;
-    if (ks > 1 && (d->norm_w || d->groups)) break;
+    if (ks > 1 && d->groups) break;
     int kc = (chunks + ks - 1) / ks;
     if (fmt == FMT_NVFP4 && ks > 1) kc = (kc + 7) / 8 * 8;   // splits on scale-group boundaries
     if (ks > 1 && (ks - 1) * kc >= chunks) continue;    // no empty split

@@ -33,6 +33,7 @@ __device__ __forceinline__ float wave_min(float v) { return -wave_max(-v); }
 
 __global__ __launch_bounds__(64 * MAX_T) void moe_route(RouteArgs a) {
   __shared__ int sel[MAX_T * MAX_K];
+  __shared__ int fresh[64 * MAX_T];
   const int lane = threadIdx.x & 63, t = threadIdx.x >> 6;
   const int E = a.n_experts, k = a.top_k;
   if (t < a.t) {                                    // wave-uniform
@@ -84,37 +85,37 @@ __global__ __launch_bounds__(64 * MAX_T) void moe_route(RouteArgs a) {
   }
   if (!a.groups) return;                            // workgroup-uniform
   __syncthreads();
-  // groups: record g = the g-th distinct expert in pair order; pairs of a record ascending
+  // groups: record g = the g-th distinct expert in pair order; pairs of a record ascending. One thread per pair
+  // (P = t·k <= 64·t = blockDim): first use, rank and count by one pass over the pairs, then the record index as the
+  // number of first uses before this expert's first use.
   const int P = a.t * k;
-  for (int p = threadIdx.x; p < P; p += blockDim.x) {
-    const int e = sel[p];
-    int first = p, rank = 0, count = 0;
+  const int p = threadIdx.x;
+  int e = -1, first = p, rank = 0, count = 0;
+  if (p < P) {
+    e = sel[p];
     for (int q = 0; q < P; ++q) {
       if (sel[q] != e) continue;
       if (q < first) first = q;
       if (q < p) ++rank;
       ++count;
     }
-    int g = 0;                                      // distinct experts first used before `first`
-    for (int q = 0; q < first; ++q) {
-      bool seen = false;
-      for (int r = 0; r < q; ++r) seen |= sel[r] == sel[q];
-      g += !seen;
-    }
+  }
+  fresh[p] = p < P && first == p;
+  __syncthreads();
+  int distinct = 0, g = 0;
+  for (int q = 0; q < P; ++q) {
+    distinct += fresh[q];
+    g += q < first ? fresh[q] : 0;
+  }
+  if (p < P) {
     int32_t* rec = a.groups + (long long)g * GROUP_REC;
     rec[2 + rank] = p;
     if (rank == 0) { rec[0] = e; rec[1] = count; }
   }
   // the records past the distinct experts: empty
-  int distinct = 0;
-  for (int q = 0; q < P; ++q) {
-    bool seen = false;
-    for (int r = 0; r < q; ++r) seen |= sel[r] == sel[q];
-    distinct += !seen;
-  }
-  for (int g = distinct + (int)threadIdx.x; g < a.max_groups; g += blockDim.x) {
-    a.groups[(long long)g * GROUP_REC] = -1;
-    a.groups[(long long)g * GROUP_REC + 1] = 0;
+  for (int r = distinct + p; r < a.max_groups; r += blockDim.x) {
+    a.groups[(long long)r * GROUP_REC] = -1;
+    a.groups[(long long)r * GROUP_REC + 1] = 0;
   }
 }
 
