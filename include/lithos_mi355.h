@@ -74,6 +74,29 @@ int mi_graph_end(void* stream, void** graph_exec);       /* finish capture, inst
 int mi_graph_launch(void* graph_exec, void* stream);     /* replay (Icb executeCommandsInBuffer) */
 int mi_graph_destroy(void* graph_exec);
 
+/* ---- run-time kernels (metal_core.h:50-66 Library(source, macros) / Pipeline(function); native.mm:42-58
+ *      Dispatch; metal_core.mm:95-127). Source compiles with hiprtc for gfx950 into a code object (no GPU needed);
+ *      macros are n (name, value) pairs → -Dname=value (an empty value → -Dname). A compile error returns
+ *      MI_E_INVALID with the compiler log's tail in mi_last_error. Library and kernel handles are opaque; a kernel
+ *      lives as long as its library. mi_launch passes the kernel's parameters as one packed block laid out as the
+ *      kernel's parameter list (the HIP kernarg segment), at most 4096 bytes. ------------------------------------ */
+typedef struct mi_kernel_attrs {
+  int32_t max_threads_per_block, static_lds_bytes, registers, scratch_bytes, wave_size;
+} mi_kernel_attrs;
+int mi_library_compile(const char* source, const char* const* macros, int32_t n_macros, int32_t fast_math,
+                       void** code, size_t* code_bytes);   /* code: malloc'd, release with mi_code_free */
+int mi_code_free(void* code);
+int mi_library_load(const void* code, size_t code_bytes, void** library);    /* on the current device */
+int mi_library_release(void* library);
+int mi_kernel_get(void* library, const char* name, void** kernel);          /* "no kernel named …" if absent */
+int mi_kernel_info(void* kernel, mi_kernel_attrs* out);
+int mi_launch(void* kernel, const void* args, size_t args_bytes, const uint32_t grid[3], const uint32_t block[3],
+              uint32_t lds_bytes, void* stream);                            /* grid in workgroups */
+
+/* ---- a file window in device memory (metal_core.mm:70-90 Buffer(path, offset, nbytes): page-aligned offset and
+ *      length, as there). Read through a 64 MiB pinned staging buffer; release with mi_free. */
+int mi_buf_from_file(const char* path, uint64_t offset, size_t bytes, void** ptr);
+
 /* ---- weight packs ----------------------------------------------------------------------------------------------
  * The T16 pack: 16-row tiles × 128-column chunks (32 for BF16), one 1152-byte unit per (tile, chunk) holding the
  * 64 lanes' 16-byte code words followed by the tile's block scales — the gfx950 counterpart of the reference's

@@ -45,7 +45,7 @@ def build(verbose: bool = False) -> Path:
     if failed:
         raise RuntimeError("hipcc failed:\n" + "\n\n".join(f"{s}:\n{m}" for s, m in failed))
     tmp = OUT.with_suffix(".so.tmp")
-    subprocess.run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)], check=True)
+    subprocess.run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-lhiprtc", "-o", str(tmp)], check=True)
     os.replace(tmp, OUT)
     return OUT
 

@@ -132,6 +132,11 @@ class MiRunnerStats(C.Structure):
 
 # name -> (restype, argtypes); every int-returning entry point is error-checked
 _VP, _I32, _SZ, _F = C.c_void_p, C.c_int32, C.c_size_t, C.c_float
+class MiKernelAttrs(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("max_threads_per_block", "static_lds_bytes", "registers", "scratch_bytes",
+                                         "wave_size")]
+
+
 SIGNATURES = {
     "mi_version": (C.c_char_p, []),
     "mi_last_error": (C.c_int, [C.c_char_p, _SZ]),
@@ -177,6 +182,14 @@ SIGNATURES = {
     "mi_runner_run": (C.c_int, [C.POINTER(MiRunnerDesc), C.POINTER(MiRunnerStats)]),
     "mi_host_alloc": (_VP, [_SZ]),
     "mi_host_free": (C.c_int, [_VP]),
+    "mi_library_compile": (C.c_int, [C.c_char_p, C.POINTER(C.c_char_p), _I32, _I32, C.POINTER(_VP), C.POINTER(_SZ)]),
+    "mi_code_free": (C.c_int, [_VP]),
+    "mi_library_load": (C.c_int, [_VP, _SZ, C.POINTER(_VP)]),
+    "mi_library_release": (C.c_int, [_VP]),
+    "mi_kernel_get": (C.c_int, [_VP, C.c_char_p, C.POINTER(_VP)]),
+    "mi_kernel_info": (C.c_int, [_VP, C.POINTER(MiKernelAttrs)]),
+    "mi_launch": (C.c_int, [_VP, _VP, _SZ, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32), C.c_uint32, _VP]),
+    "mi_buf_from_file": (C.c_int, [C.c_char_p, C.c_uint64, _SZ, C.POINTER(_VP)]),
 }
 
 
@@ -196,6 +209,12 @@ def load(path: Optional[os.PathLike] = None) -> C.CDLL:
     if not p.exists():
         raise MiError(f"{p} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
                       f"or `python lithos-metal_amd/build.py`")
+    # torch first, so that this library binds to the HIP runtime torch loads and the two share devices and
+    # streams: with hiprtc used before torch initialised the GPU, this library's calls saw no device
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = C.CDLL(str(p))
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)
