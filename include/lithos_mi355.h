@@ -403,6 +403,12 @@ typedef struct mi_runner_desc {
   uint64_t max_tokens;
   int32_t* tokens;            /* host */
   uint64_t tokens_capacity, n_tokens;
+  /* optional, for a step state held in pinned host memory in a program's own layout (Engine programs): the runner
+   * stores the tail into state_ring_tail (instead of copying it into state->ring_tail) and reads done / error from
+   * state_done / state_error (instead of host_ctl[1] / [2]); state may then be NULL. host_ctl[0] keeps the tail. */
+  uint32_t* state_ring_tail;
+  const uint32_t* state_done;
+  const uint32_t* state_error;
 } mi_runner_desc;
 typedef struct mi_runner_stats {
   uint64_t launches, batches, tokens;

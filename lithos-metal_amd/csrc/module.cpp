@@ -107,8 +107,10 @@ int mi_kernel_get(void* library, const char* name, void** kernel) {
   MI_REQUIRE(library && name && kernel, "mi_kernel_get: null argument");
   hipFunction_t f;
   const hipError_t e = hipModuleGetFunction(&f, static_cast<hipModule_t>(library), name);
-  if (e == hipErrorNotFound || e == hipErrorInvalidSymbol)
+  if (e == hipErrorNotFound || e == hipErrorInvalidSymbol) {
+    (void)hipGetLastError();   // the lookup's error is reported here, not to the next HIP caller
     return mi_set_error(MI_E_INVALID, "no kernel named %s", name);
+  }
   MI_TRY_HIP(e, "hipModuleGetFunction");
   *kernel = f;
   return MI_OK;

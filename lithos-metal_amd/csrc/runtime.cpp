@@ -22,6 +22,7 @@ int mi_set_error(int code, const char* fmt, ...) {
 
 int mi_check_hip(hipError_t e, const char* what) {
   if (e == hipSuccess) return MI_OK;
+  (void)hipGetLastError();     // reported here: clear the thread's sticky error so the next caller's check is its own
   return mi_set_error(MI_E_HIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
 }
 

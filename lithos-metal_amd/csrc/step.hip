@@ -506,8 +506,9 @@ bool drain_ring(mi_runner_desc* d) {
 extern "C" {
 
 int mi_runner_run(mi_runner_desc* d, mi_runner_stats* st) {
-  MI_REQUIRE(d && st && d->graph_exec && d->state && d->ring && d->host_ctl && (d->tokens || !d->tokens_capacity),
-             "mi_runner_run: null pointer");
+  MI_REQUIRE(d && st && d->graph_exec && (d->state || d->state_ring_tail) && d->ring && d->host_ctl &&
+             (d->tokens || !d->tokens_capacity), "mi_runner_run: null pointer");
+  MI_REQUIRE(!d->state_done == !d->state_error, "mi_runner_run: state_done and state_error go together");
   MI_REQUIRE(d->ring_capacity > 0 && d->launches_per_batch > 0 && d->in_flight > 0,
              "mi_runner_run: ring_capacity, launches_per_batch and in_flight must be >= 1");
   MI_REQUIRE(d->n_tokens <= d->tokens_capacity, "mi_runner_run: n_tokens exceeds tokens_capacity");
@@ -543,8 +544,8 @@ int mi_runner_run(mi_runner_desc* d, mi_runner_stats* st) {
     if (e == hipSuccess && hipEventElapsedTime(&ms, b.a, b.b) == hipSuccess) st->gpu_ms += ms;
     st->batches++;
     full = drain_ring(d) || full;
-    st->done = __atomic_load_n(&d->host_ctl[1], __ATOMIC_ACQUIRE);
-    st->error = __atomic_load_n(&d->host_ctl[2], __ATOMIC_RELAXED);
+    st->done = __atomic_load_n(d->state_done ? d->state_done : &d->host_ctl[1], __ATOMIC_ACQUIRE);
+    st->error = __atomic_load_n(d->state_error ? d->state_error : &d->host_ctl[2], __ATOMIC_RELAXED);
   };
   while (st->launches < d->max_launches && !st->done && !full && err == hipSuccess &&
          (d->max_tokens == 0 || d->n_tokens - first < d->max_tokens)) {
@@ -552,7 +553,10 @@ int mi_runner_run(mi_runner_desc* d, mi_runner_stats* st) {
     const uint32_t n = (uint32_t)std::min<uint64_t>(d->launches_per_batch, d->max_launches - st->launches);
     Batch& b = pool[next];
     // the tail the GPU checks for overflow: the host's value when the copy runs (it only grows)
-    err = hipMemcpyAsync(&d->state->ring_tail, &d->host_ctl[0], sizeof(uint32_t), hipMemcpyHostToDevice, s);
+    if (d->state_ring_tail)       // a host-resident state: a newer tail than the copy would give is as correct
+      __atomic_store_n(d->state_ring_tail, __atomic_load_n(&d->host_ctl[0], __ATOMIC_RELAXED), __ATOMIC_RELEASE);
+    else
+      err = hipMemcpyAsync(&d->state->ring_tail, &d->host_ctl[0], sizeof(uint32_t), hipMemcpyHostToDevice, s);
     if (err == hipSuccess) err = hipEventRecord(b.a, s);
     for (uint32_t i = 0; i < n && err == hipSuccess; ++i) err = hipGraphLaunch(exec, s);
     if (err == hipSuccess) err = hipEventRecord(b.b, s);

@@ -121,7 +121,8 @@ class MiRunnerDesc(C.Structure):
     _fields_ = [("graph_exec", C.c_void_p), ("stream", C.c_void_p), ("state", C.c_void_p), ("ring", C.c_void_p),
                 ("ring_capacity", C.c_uint32), ("host_ctl", C.c_void_p), ("max_launches", C.c_uint32),
                 ("launches_per_batch", C.c_uint32), ("in_flight", C.c_uint32), ("max_tokens", C.c_uint64),
-                ("tokens", C.c_void_p), ("tokens_capacity", C.c_uint64), ("n_tokens", C.c_uint64)]
+                ("tokens", C.c_void_p), ("tokens_capacity", C.c_uint64), ("n_tokens", C.c_uint64),
+                ("state_ring_tail", C.c_void_p), ("state_done", C.c_void_p), ("state_error", C.c_void_p)]
 
 
 class MiRunnerStats(C.Structure):

@@ -124,6 +124,52 @@ class Buffer:
             pass
 
 
+class HostResidentBuffer(Buffer):
+    """A buffer in pinned, device-accessible host memory (``mi_host_alloc``): what a program's step state and
+    token ring live in when the host pump reads them without a copy. ``gpu_address`` is valid on the device."""
+
+    def __init__(self, device: Device, nbytes: int):
+        self.device, self._n = device, int(nbytes)
+        addr = hip.load().mi_host_alloc(max(self._n, 1))
+        if not addr:
+            raise hip.MiError(f"mi_host_alloc({nbytes}) failed: {hip.last_error()}")
+        self._addr = int(addr)
+        C.memset(self._addr, 0, max(self._n, 1))
+        self._p = C.c_void_p()            # nothing for Buffer.__del__ to free
+
+    @property
+    def gpu_address(self) -> int:
+        return self._addr
+
+    def word(self, offset: int) -> int:
+        """Host address of the 4-byte word at ``offset``."""
+        if offset < 0 or offset + 4 > self._n:
+            raise IndexError("HostResidentBuffer.word out of range")
+        return self._addr + offset
+
+    def read(self, offset: int = 0, nbytes: int = 0) -> bytes:
+        if offset < 0 or nbytes < 0 or offset + nbytes > self._n:
+            raise IndexError("Buffer.read out of range")
+        return C.string_at(self._addr + offset, nbytes)
+
+    def write(self, data, offset: int = 0) -> None:
+        data = bytes(data)
+        if offset < 0 or offset + len(data) > self._n:
+            raise IndexError("Buffer.write out of range")
+        C.memmove(self._addr + offset, data, len(data))
+
+    def fill(self, value: int) -> None:
+        C.memset(self._addr, int(value) & 0xFF, self._n)
+
+    def __del__(self):
+        try:
+            if getattr(self, "_addr", 0) and hip._lib is not None:
+                hip._lib.mi_host_free(C.c_void_p(self._addr))
+                self._addr = 0
+        except Exception:
+            pass
+
+
 def compile_source(source: str, macros: Optional[Dict[str, str]] = None, fast_math: bool = False) -> bytes:
     """HIP C++ → a gfx950 code object (bytes). Needs no GPU."""
     macros = macros or {}
