@@ -297,6 +297,10 @@ class MoeBlock:
         self.shared_gate = kernels.PackedWeight("bf16", 1, hidden, 1, DV.pack_bf16(self.shared_gate_w), None)
         self.shared_inter = shared_inter
         self._bufs: Dict[int, tuple] = {}
+        # the shared expert runs on a second stream beside the router → experts chain (default priority), with its
+        # own zeroed split-K workspace so the two branches never share partials or fold counters
+        self.side = torch.cuda.Stream(device=device)
+        self.side_ws = torch.zeros(8 << 20, dtype=torch.uint8, device=device)
 
     def buffers(self, m: int):
         torch = _torch()
@@ -320,14 +324,31 @@ class MoeBlock:
         m = h.shape[0]
         logits, route, act, hk, s_act, s_out, s_gate, y = self.buffers(m)
         out = y if out is None else out
+        torch = _torch()
+
+        def shared(ws=None):
+            kernels.gemv(self.shared_gate_up.packed, h, epilogue="silu_mul", norm_w=self.norm_w, eps=self.eps,
+                         out=s_act, workspace=ws)
+            kernels.gemv(self.shared_down.packed, s_act, out=s_out, workspace=ws)
+            kernels.gemv(self.shared_gate, h, norm_w=self.norm_w, eps=self.eps, out=s_gate, workspace=ws)
+
+        # M >= 3: the shared expert and its gate run beside the router → experts chain (M = 8: 104 → 82 µs); at
+        # M <= 2 its kernels are short and the fork / join costs more than it hides (34 → 39 µs), so one stream
+        main = torch.cuda.current_stream(h.device)
+        concurrent = m > 2
+        if concurrent:
+            self.side.wait_stream(main)
+            with torch.cuda.stream(self.side):
+                shared(self.side_ws)
+        else:
+            shared()
         kernels.gemv(self.router, h, norm_w=self.norm_w, eps=self.eps, out=logits)
         _, wts, groups = kernels.moe_route(logits, self.top_k, renorm=True, out=route)
         kernels.moe_gemv(self.gate_up, h, groups, tokens=m, top_k=self.top_k, x_per_slot=False,
                          epilogue="silu_mul_rounded", norm_w=self.norm_w, eps=self.eps, out=act)
         kernels.moe_gemv(self.down, act, groups, tokens=m, top_k=self.top_k, x_per_slot=True, out=hk)
-        kernels.gemv(self.shared_gate_up.packed, h, epilogue="silu_mul", norm_w=self.norm_w, eps=self.eps, out=s_act)
-        kernels.gemv(self.shared_down.packed, s_act, out=s_out)
-        kernels.gemv(self.shared_gate, h, norm_w=self.norm_w, eps=self.eps, out=s_gate)
+        if concurrent:
+            main.wait_stream(self.side)
         return kernels.moe_combine(hk, wts, top_k=self.top_k, shared=s_out, shared_gate=s_gate, residual=h, out=out)
 
     def bytes_per_step(self, m: int, distinct_experts: int) -> int:
