@@ -295,6 +295,9 @@ class MoeBlock:
         self.shared_down = nvfp4_matrix(hidden, shared_inter, gen, device)
         self.shared_gate_w = (torch.randn(1, hidden, generator=gen, device=device) * 0.02).to(torch.bfloat16)
         self.shared_gate = kernels.PackedWeight("bf16", 1, hidden, 1, DV.pack_bf16(self.shared_gate_w), None)
+        # the router and the shared expert's gate read the same normed h: one BF16 GEMV of experts + 1 rows
+        self.router_gate = kernels.PackedWeight("bf16", experts + 1, hidden, 1,
+                                                DV.pack_bf16(torch.cat([self.router_w, self.shared_gate_w])), None)
         self.shared_inter = shared_inter
         self._bufs: Dict[int, tuple] = {}
         # the shared expert runs on a second stream beside the router → experts chain (default priority), with its
@@ -307,7 +310,7 @@ class MoeBlock:
         if m not in self._bufs:
             dev, k, g = self.norm_w.device, self.top_k, min(self.experts, m * self.top_k)
             bf = torch.bfloat16
-            self._bufs[m] = (torch.empty(m, self.experts, dtype=bf, device=dev),
+            self._bufs[m] = (torch.empty(m, (self.experts + 1 + 7) // 8 * 8, dtype=bf, device=dev),
                              (torch.empty(m, k, dtype=torch.int32, device=dev),
                               torch.empty(m, k, dtype=torch.float32, device=dev),
                               torch.empty(g, kernels.GROUP_REC, dtype=torch.int32, device=dev)),
@@ -330,9 +333,8 @@ class MoeBlock:
             kernels.gemv(self.shared_gate_up.packed, h, epilogue="silu_mul", norm_w=self.norm_w, eps=self.eps,
                          out=s_act, workspace=ws)
             kernels.gemv(self.shared_down.packed, s_act, out=s_out, workspace=ws)
-            kernels.gemv(self.shared_gate, h, norm_w=self.norm_w, eps=self.eps, out=s_gate, workspace=ws)
 
-        # M >= 3: the shared expert and its gate run beside the router → experts chain (M = 8: 104 → 82 µs); at
+        # M >= 3: the shared expert runs beside the router → experts chain (M = 8: 104 → 82 µs); at
         # M <= 2 its kernels are short and the fork / join costs more than it hides (34 → 39 µs), so one stream
         main = torch.cuda.current_stream(h.device)
         concurrent = m > 2
@@ -342,14 +344,16 @@ class MoeBlock:
                 shared(self.side_ws)
         else:
             shared()
-        kernels.gemv(self.router, h, norm_w=self.norm_w, eps=self.eps, out=logits)
-        _, wts, groups = kernels.moe_route(logits, self.top_k, renorm=True, out=route)
+        e = self.experts
+        kernels.gemv(self.router_gate, h, norm_w=self.norm_w, eps=self.eps, out=logits[:, :e + 1])
+        _, wts, groups = kernels.moe_route(logits[:, :e], self.top_k, renorm=True, out=route)
         kernels.moe_gemv(self.gate_up, h, groups, tokens=m, top_k=self.top_k, x_per_slot=False,
                          epilogue="silu_mul_rounded", norm_w=self.norm_w, eps=self.eps, out=act)
         kernels.moe_gemv(self.down, act, groups, tokens=m, top_k=self.top_k, x_per_slot=True, out=hk)
         if concurrent:
             main.wait_stream(self.side)
-        return kernels.moe_combine(hk, wts, top_k=self.top_k, shared=s_out, shared_gate=s_gate, residual=h, out=out)
+        return kernels.moe_combine(hk, wts, top_k=self.top_k, shared=s_out, shared_gate=logits[:, e:e + 1], residual=h,
+                                   out=out)
 
     def bytes_per_step(self, m: int, distinct_experts: int) -> int:
         """Algorithmic HBM bytes of one step with ``distinct_experts`` experts chosen over the M tokens."""

@@ -223,7 +223,8 @@ def test_moe_block_layer(torch_gpu, t):
     h = rbf(rng.standard_normal((t, 2048)))
     hd = to_dev_bf16(torch, h)
     y = from_dev_bf16(blk(hd))
-    logits = from_dev_bf16(blk.buffers(t)[0])
+    both = from_dev_bf16(blk.buffers(t)[0])           # router logits | the shared gate's logit, one GEMV
+    logits, gate = both[:, :32], both[:, 32:33]
     ids = blk.buffers(t)[1][0].cpu().numpy()
 
     def dense(w, expert=0, gate_up=False):
@@ -243,6 +244,7 @@ def test_moe_block_layer(torch_gpu, t):
     rw = bf16_to_f32(blk.router_w.view(torch.int16).cpu().numpy().astype(np.uint16))
     gw = bf16_to_f32(blk.shared_gate_w.view(torch.int16).cpu().numpy().astype(np.uint16))
     assert check_against_oracle(logits, ON.linear(xn, rw)).ok_rounded()
+    assert check_against_oracle(gate, ON.linear(xn, gw)).ok_rounded()
     ref, ref_ids, _ = ON.moe_forward(xn, h, logits, 8, w_gu, w_dn, renorm=True, shared=(s_gu, s_dn, gw))
     assert np.array_equal(ids, ref_ids)
     chk = check_against_oracle(y, ref)
