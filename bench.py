@@ -46,7 +46,7 @@ def parse():
     p.add_argument("--layers", type=int, default=10, help="distinct layer instances the steps rotate over")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--only", choices=["gdn", "attn", "mlp", "gateup", "fp8", "moe", "loop", "copy"], default=None,
+    p.add_argument("--only", choices=["gdn", "attn", "mlp", "gateup", "fp8", "int4", "moe", "loop", "copy"], default=None,
                    help="time one workload only (profiling runs; copy = a 256 MiB device copy, the counter reference)")
     return p.parse_args()
 
@@ -146,6 +146,26 @@ def main():
                                  stream)
                 out[f"fp8_m{m}"] = (ms, nb + m * k8 * 2 + m * n8 * 2)
             del mats
+        if args.only in (None, "int4"):
+            # affine 4-bit (MLX rule, group 64, BF16 scale + bias): configs[0] (4096², M = 1) and the 27B gate|up
+            # shape with silu·mul (M = 1 and 8). Packed bytes filled with one finite pattern (codes 4/2/12/3,
+            # scale = bias = bf16 0.0103): the stream and the arithmetic are the real ones, the values are not
+            lib = hip.load()
+            for tag, n4, k4, ms_ in (("int4_4096", 4096, 4096, (1,)), ("int4_gateup", 34816, 5120, (1, 8))):
+                nbytes = lib.mi_pack_bytes(hip.MI_FMT["int4_affine"], n4, k4)
+                mats = [kernels.PackedWeight("int4_affine", n4, k4, 1,
+                                             torch.full((nbytes // 2,), 0x3C24, dtype=torch.int16, device=dev)
+                                             .view(torch.uint8), None)
+                        for _ in range(n if n4 * k4 > 1 << 26 else 1)]
+                epi = "silu_mul" if tag == "int4_gateup" else None
+                n_out = n4 // 2 if epi else n4
+                for m in ms_:
+                    x = torch.randn(m, k4, generator=gen, device=dev).to(torch.bfloat16)
+                    y4 = torch.empty(m, n_out, dtype=torch.bfloat16, device=dev)
+                    ms = timed_graph(lambda i: kernels.gemv(mats[i % len(mats)], x, epilogue=epi, out=y4),
+                                     args.steps, args.warmup, stream)
+                    out[f"{tag}_m{m}"] = (ms, n4 * k4 * 9 // 16 + m * k4 * 2 + m * n_out * 2)
+                del mats
         if args.only in (None, "attn"):
             attn = [AttnDecoderLayer(seed=40 + i, ctx=CTX, device=dev) for i in range(n)]
             for layer in attn:
@@ -266,6 +286,9 @@ def main():
         "mlp_m8": entry("mlp_m8", 8),
         "fp8_in_proj_m1": entry("fp8_m1", 1),
         "fp8_in_proj_m8": entry("fp8_m8", 8),
+        "int4_gemv_4096_m1": dict(entry("int4_4096_m1", 1), workload="configs[0]: affine 4-bit GEMV 4096x4096, M=1"),
+        "int4_gateup_m1": dict(entry("int4_gateup_m1", 1), workload="affine 4-bit gate|up 34816x5120 + silu_mul"),
+        "int4_gateup_m8": entry("int4_gateup_m8", 8),
         "moe_block_m1": dict(entry("moe_m1", 1), workload="MoE feed-forward: router + top-8 of 256 NVFP4 experts "
                              "(hidden 2048, intermediate 512) + shared expert + combine"),
         "moe_block_m8": entry("moe_m8", 8),
