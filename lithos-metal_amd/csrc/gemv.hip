@@ -1818,6 +1818,9 @@ Plan plan_tk(const mi_gemv_desc* d, int fmt, int chunks, int n_tiles, int groups
           if (force[3] && D != force[3]) continue;
           // NVFP4 on whole scale groups streams with D = 8 (the piece ring); otherwise any depth
           if (fmt == FMT_NVFP4 && chunks % 8 == 0 && kc % 8 == 0 && D != 8) continue;
+          // INT4 on the matrix path: a deeper ring costs more in occupancy than it adds in flight (27B gate|up at
+          // M = 8: D = 4 32.5 µs, D = 8 35.0 µs, the D = 12 plan the model preferred 52.7 µs)
+          if (fmt == FMT_INT4 && mf && D != 4) continue;
           const double wgs = (double)((n_tiles + tb - 1) / tb) * ks * groups;
           const int per_cu_lds = std::max(1, (int)(kMaxLds / lds));
           const int per_cu = std::min(per_cu_lds, 32 / S);
