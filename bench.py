@@ -77,7 +77,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU (each box here has one MI355X); --gpus {args.gpus} is not "
-              f"supported — the multi-GPU sharding is described in DESIGN.md", file=sys.stderr)
+              f"supported — the multi-GPU sharding is design-only in this build", file=sys.stderr)
         sys.exit(2)
     import torch
     from monolith_mi355 import kernels
