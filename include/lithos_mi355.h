@@ -180,6 +180,9 @@ typedef struct mi_gdn_desc {
                                 replay the committed tokens from the step's input state (rec_in != rec_out) into the
                                 output slot; no read-out (y may be NULL) */
   const int32_t* t_dev;      /* device-resident token count 0..t (the accept scan's committed count), or NULL = t */
+  const uint32_t* done;      /* a step program's mi_step_state.done, or NULL: once it is set the step takes no token —
+                                conv_out and rec_out receive conv_in and rec_in unchanged (so a graph's fixed ping-pong
+                                stays in phase) and y is not written (gdn_mixer.metal:281,330 return at done) */
 } mi_gdn_desc;
 int mi_gdn_step(const mi_gdn_desc* d, void* stream);
 
@@ -210,6 +213,8 @@ typedef struct mi_gqa_desc {
   size_t workspace_bytes;
   const int32_t* pos_dev;    /* device-resident position (a step program's mi_step_state.position) or NULL = pos;
                                 the key ranges are then planned for ctx_max - t and the kernels read the position */
+  const uint32_t* done;      /* a step program's mi_step_state.done, or NULL: once it is set nothing is appended to
+                                the cache and y is not written (gqa_decode.metal:53,239 return at done) */
 } mi_gqa_desc;
 size_t mi_gqa_workspace_bytes(const mi_gqa_desc* d);
 int mi_gqa_decode(const mi_gqa_desc* d, void* stream);

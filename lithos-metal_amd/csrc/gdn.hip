@@ -40,7 +40,15 @@ struct GdnArgs {
   float eps;
   int commit;               // the speculative commit pass: state only, no read-out
   const int32_t* t_dev;     // device-resident token count (<= t), or null
+  const uint32_t* done;     // the step state's stop flag, or null: when set the step takes no token
 };
+
+// tokens this launch takes: the device count (commit pass) or t, and none once the program has stopped — with
+// T = 0 the kernel copies conv_in → conv_out and rec_in → rec_out unchanged and writes no read-out
+__device__ __forceinline__ int tokens_now(const GdnArgs& a) {
+  if (a.done && *a.done) return 0;
+  return a.t_dev ? min(max(*a.t_dev, 0), a.t) : a.t;
+}
 
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + __expf(-x)); }
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
@@ -54,7 +62,7 @@ __global__ __launch_bounds__(64 * (WAVES + CONV_WAVES)) void gdn_step(GdnArgs a)
   __shared__ float beta_s[TMAX], eg_s[TMAX];
   const int h = blockIdx.x, sl = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int T = a.t_dev ? min(max(*a.t_dev, 0), a.t) : a.t;
+  const int T = tokens_now(a);
   const int rep = a.hv / a.hk;
   const int kh = h / rep;
   const int key_dim = a.hk * DK;
@@ -178,7 +186,7 @@ __global__ __launch_bounds__(64 * (WAVES + CONV_WAVES)) void gdn_step(GdnArgs a)
 // (head, token)
 __global__ __launch_bounds__(64) void gdn_gated_norm(GdnArgs a) {
   const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
-  if (a.t_dev && t >= *a.t_dev) return;
+  if (t >= tokens_now(a)) return;
   uint16_t* y = a.y + (long long)t * a.ldy + h * DV;
   const float v0 = bf16_bits_to_f32(y[lane]), v1 = bf16_bits_to_f32(y[lane + 64]);
   const float r = 1.0f / sqrtf(wave_sum(v0 * v0 + v1 * v1) / (float)DV + a.eps);
@@ -211,7 +219,7 @@ extern "C" int mi_gdn_step(const mi_gdn_desc* d, void* stream) {
   a.conv_w = d->conv_w; a.neg_exp_a = d->neg_exp_a; a.dt_bias = d->dt_bias; a.norm_w = d->norm_w;
   a.conv_in = d->conv_in; a.conv_out = d->conv_out; a.rec_in = d->rec_in; a.rec_out = d->rec_out;
   a.y = d->y; a.ldy = d->ld_y; a.eps = d->eps;
-  a.commit = d->commit; a.t_dev = d->t_dev;
+  a.commit = d->commit; a.t_dev = d->t_dev; a.done = d->done;
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(gdn_step, dim3(d->v_heads, NSLICE), dim3(64 * (WAVES + CONV_WAVES)), 0, s, a);
   MI_TRY_HIP(hipGetLastError(), "gdn_step launch");

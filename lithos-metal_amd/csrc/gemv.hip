@@ -96,6 +96,13 @@ struct Args {
 };
 
 // ---- weight decode ---------------------------------------------------------------------------------------------
+// The mantissa factor ±1.mmm of a decoded E4M3 block scale (FP32 bits u; every nonzero E4M3 value, subnormals
+// included, is an FP32 normal), or ±0 for a zero scale: the power-of-two part is then 0.0, which the scaled FP4
+// conversions read as 2^-127 — BF16 keeps that, so the block must be zeroed by its factor
+__device__ __forceinline__ float nv_mant(uint32_t u) {
+  return __uint_as_float((u & 0x7F800000u) ? ((u & 0x807FFFFFu) | 0x3F800000u) : (u & 0x80000000u));
+}
+
 // E4M3 block-scale byte pair → (power-of-two parts, signed mantissa factors as F16)
 struct ScalePair {
   float e0, e1;
@@ -108,8 +115,8 @@ __device__ __forceinline__ ScalePair nvfp4_scales(uint32_t two_bytes) {
   ScalePair s;
   s.e0 = __uint_as_float(u0 & 0x7F800000u);
   s.e1 = __uint_as_float(u1 & 0x7F800000u);
-  s.m0 = (f16_t)__uint_as_float((u0 & 0x807FFFFFu) | 0x3F800000u);   // ±1.mmm, exact in F16
-  s.m1 = (f16_t)__uint_as_float((u1 & 0x807FFFFFu) | 0x3F800000u);
+  s.m0 = (f16_t)nv_mant(u0);   // ±1.mmm, exact in F16
+  s.m1 = (f16_t)nv_mant(u1);
   return s;
 }
 
@@ -452,8 +459,8 @@ __global__ __launch_bounds__(KW == 16 ? 640 : 1024) void gemv_row(Args a) {
                                : __builtin_amdgcn_cvt_pk_f32_fp8((int)word, false);
       const uint32_t u0 = __float_as_uint(f.x), u1 = __float_as_uint(f.y);
       const float e[2] = {__uint_as_float(u0 & 0x7F800000u), __uint_as_float(u1 & 0x7F800000u)};
-      const float mant[2] = {__uint_as_float((u0 & 0x807FFFFFu) | 0x3F800000u),
-                             __uint_as_float((u1 & 0x807FFFFFu) | 0x3F800000u)};
+      const float mant[2] = {nv_mant(u0),
+                             nv_mant(u1)};
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
         float part[MT];
@@ -814,8 +821,8 @@ void gemv_rowp(Args a) {
                                  : __builtin_amdgcn_cvt_pk_f32_fp8((int)word, false);
         const uint32_t u0 = __float_as_uint(f.x), u1 = __float_as_uint(f.y);
         const float e[2] = {__uint_as_float(u0 & 0x7F800000u), __uint_as_float(u1 & 0x7F800000u)};
-        const float mant[2] = {__uint_as_float((u0 & 0x807FFFFFu) | 0x3F800000u),
-                               __uint_as_float((u1 & 0x807FFFFFu) | 0x3F800000u)};
+        const float mant[2] = {nv_mant(u0),
+                               nv_mant(u1)};
   #pragma unroll
         for (int b = 0; b < 2; ++b) {
           float part[MT];
@@ -1098,8 +1105,8 @@ __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
                                  : __builtin_amdgcn_cvt_pk_f32_fp8((int)word, false);
         const uint32_t b0 = __float_as_uint(f.x), b1 = __float_as_uint(f.y);
         const float e0 = __uint_as_float(b0 & 0x7F800000u), e1 = __uint_as_float(b1 & 0x7F800000u);
-        const f16_t m0 = (f16_t)__uint_as_float((b0 & 0x807FFFFFu) | 0x3F800000u);
-        const f16_t m1 = (f16_t)__uint_as_float((b1 & 0x807FFFFFu) | 0x3F800000u);
+        const f16_t m0 = (f16_t)nv_mant(b0);
+        const f16_t m1 = (f16_t)nv_mant(b1);
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
           const f16x8 bv = nvfp4_decode8(dw[s], s < 2 ? e0 : e1, s < 2 ? m0 : m1);
@@ -1412,8 +1419,8 @@ __global__ __launch_bounds__(512) void gemv_tk(Args a) {
       const f32x2 f = __builtin_amdgcn_cvt_pk_f32_fp8((int)two, false);
       const uint32_t u0 = __float_as_uint(f.x), u1 = __float_as_uint(f.y);
       const float e[2] = {__uint_as_float(u0 & 0x7F800000u), __uint_as_float(u1 & 0x7F800000u)};
-      const float mant[2] = {__uint_as_float((u0 & 0x807FFFFFu) | 0x3F800000u),
-                             __uint_as_float((u1 & 0x807FFFFFu) | 0x3F800000u)};
+      const float mant[2] = {nv_mant(u0),
+                             nv_mant(u1)};
       const uint32_t dw[4] = {u.q.x, u.q.y, u.q.z, u.q.w};
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
@@ -2001,28 +2008,6 @@ constexpr int kFoldTiles = 16384;
 constexpr size_t kFoldCounterBytes = kFoldTiles * sizeof(uint32_t);
 size_t fold_counter_bytes(int) { return kFoldCounterBytes; }
 
-// the library's FP32 partials buffer for split-K plans (per device, grown on demand; a caller that cannot allocate
-// passes its own through mi_gemv_desc.workspace)
-std::mutex g_ws_mu;
-std::vector<std::pair<void*, size_t>> g_ws;
-
-int partials_workspace(size_t bytes, void** out) {
-  int dev = 0;
-  MI_TRY_HIP(hipGetDevice(&dev), "hipGetDevice");
-  std::lock_guard<std::mutex> lk(g_ws_mu);
-  if ((int)g_ws.size() <= dev) g_ws.resize(dev + 1, {nullptr, 0});
-  auto& w = g_ws[dev];
-  if (w.second < bytes) {
-    if (w.first) MI_TRY_HIP(hipFree(w.first), "hipFree(gemv partials)");
-    w = {nullptr, 0};
-    MI_TRY_HIP(hipMalloc(&w.first, bytes), "hipMalloc(gemv partials)");
-    MI_TRY_HIP(hipMemset(w.first, 0, bytes), "hipMemset(gemv partials)");   // the arrival counters start at zero
-    w.second = bytes;
-  }
-  *out = w.first;
-  return MI_OK;
-}
-
 }  // namespace
 
 extern "C" {
@@ -2093,7 +2078,7 @@ int mi_gemv(const mi_gemv_desc* d, void* stream) {
     void* ws = d->workspace;
     if (ws) {
       MI_REQUIRE(d->workspace_bytes >= need, "mi_gemv: workspace %zu B < %zu B", d->workspace_bytes, need);
-    } else if (int rc = partials_workspace(need, &ws)) {
+    } else if (int rc = mi_library_scratch(MI_SCRATCH_GEMV, need, static_cast<hipStream_t>(stream), &ws)) {
       return rc;
     }
     a.part = reinterpret_cast<float*>(static_cast<char*>(ws) + cb);

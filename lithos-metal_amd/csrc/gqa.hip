@@ -44,7 +44,10 @@ struct GqaArgs {
   float* part_o; float* part_ml;                // [kv][group][rows][D], [kv][group][rows][2]
   uint16_t* y; int ldy;
   const int32_t* pos_dev;                       // device-resident position (a step program's StepState), or null
+  const uint32_t* done;                         // the step state's stop flag, or null: set = append nothing
 };
+
+__device__ __forceinline__ bool stopped(const GqaArgs& a) { return a.done && *a.done; }
 
 // the cache position of the step's first new token: the descriptor's, or the one a step program keeps on the device
 __device__ __forceinline__ int cur_pos(const GqaArgs& a) { return a.pos_dev ? *a.pos_dev : a.pos; }
@@ -138,6 +141,7 @@ __device__ __forceinline__ int vblock_pos(int k) { return (k >> 5) * 32 + ((k & 
 __global__ __launch_bounds__(64) void gqa_prep(GqaArgs a) {
   __shared__ float tmp[D];
   const int lane = threadIdx.x, x = blockIdx.x, t = blockIdx.y;
+  if (stopped(a)) return;
   const int q_cols = a.gate ? 2 * D : D;
   const uint16_t* row = a.proj + (long long)t * a.ldp;
   if (x < a.heads) {
@@ -199,6 +203,7 @@ __global__ __launch_bounds__(64 * NW, RT == 1 ? 2 : 1) void gqa_decode(GqaArgs a
   __shared__ float mls[NW][RT * 16][2];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int j = blockIdx.y, g = blockIdx.x;
+  if (stopped(a)) return;                               // workgroup-uniform
   const int pos = cur_pos(a);
   const int n_keys = min(pos + a.t, a.ctx);
   const int kb = g * a.group_len;
@@ -395,6 +400,7 @@ constexpr int MW = 8;
 __global__ __launch_bounds__(64 * MW) void gqa_merge(GqaArgs a) {
   __shared__ float red[MW][D + 1];
   const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (stopped(a)) return;
   const int j = h / a.rep;
   const int row = t * a.rep + (h - j * a.rep);
   const long long b0 = (long long)j * a.n_groups * a.rows + row;      // partial g at b0 + g·rows
@@ -457,25 +463,6 @@ Layout layout(int kv, int n_groups, int rows) {
   return l;
 }
 
-std::mutex g_mu;
-std::vector<std::pair<void*, size_t>> g_ws;
-
-int workspace(size_t bytes, void** out) {
-  int dev = 0;
-  MI_TRY_HIP(hipGetDevice(&dev), "hipGetDevice");
-  std::lock_guard<std::mutex> lk(g_mu);
-  if ((int)g_ws.size() <= dev) g_ws.resize(dev + 1, {nullptr, 0});
-  auto& w = g_ws[dev];
-  if (w.second < bytes) {
-    if (w.first) MI_TRY_HIP(hipFree(w.first), "hipFree(gqa workspace)");
-    w = {nullptr, 0};
-    MI_TRY_HIP(hipMalloc(&w.first, bytes), "hipMalloc(gqa workspace)");
-    w.second = bytes;
-  }
-  *out = w.first;
-  return MI_OK;
-}
-
 }  // namespace
 
 // the position the key ranges are planned for: the descriptor's, or — with a device position — the largest one the
@@ -509,6 +496,7 @@ extern "C" int mi_gqa_decode(const mi_gqa_desc* d, void* stream) {
   a.gate = d->gate; a.qk_norm = d->qk_norm; a.rep = rep; a.rows = rows;
   const Plan pl = plan(plan_pos(d), d->kv_heads, rows);
   a.pos_dev = d->pos_dev;
+  a.done = d->done;
   a.n_groups = pl.n_groups;
   a.group_len = pl.group_len;
   a.proj = d->proj; a.ldp = d->ld_proj; a.cosb = d->rope_cos; a.sinb = d->rope_sin;
@@ -519,7 +507,7 @@ extern "C" int mi_gqa_decode(const mi_gqa_desc* d, void* stream) {
   void* ws = d->workspace;
   if (ws) {
     MI_REQUIRE(d->workspace_bytes >= need, "mi_gqa_decode: workspace %zu B < %zu B", d->workspace_bytes, need);
-  } else if (int rc = workspace(need, &ws)) {
+  } else if (int rc = mi_library_scratch(MI_SCRATCH_GQA, need, static_cast<hipStream_t>(stream), &ws)) {
     return rc;
   }
   const Layout L = layout(d->kv_heads, a.n_groups, rows);

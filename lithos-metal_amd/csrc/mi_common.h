@@ -19,6 +19,14 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 int mi_set_error(int code, const char* fmt, ...);          // records the message, returns code
 int mi_check_hip(hipError_t e, const char* what);         // 0 on success, else MI_E_HIP with the HIP message
 
+// The library's own scratch buffers (split-K partials and fold counters, attention partials, argmax counters) for
+// callers that pass none: one per (kind, device, stream), so calls on different streams never share one. A buffer is
+// zeroed when allocated (kernels that keep counters leave them at zero). It grows on demand but is never freed
+// before the process ends — a graph captured earlier keeps the address it recorded — and it refuses to grow while
+// the stream is being captured (the caller runs one eager call of the shape first, or passes its own workspace).
+enum MiScratchKind { MI_SCRATCH_GEMV = 0, MI_SCRATCH_GQA = 1, MI_SCRATCH_ARGMAX = 2 };
+int mi_library_scratch(int kind, size_t bytes, hipStream_t stream, void** out);
+
 #define MI_TRY_HIP(expr, what)                          \
   do {                                                  \
     int _rc = mi_check_hip((expr), (what));             \

@@ -3,7 +3,8 @@
 //
 // Semantics: softmax in FP32 over the BF16 logits, k rounds of argmax over the probabilities with ties to the lowest
 // expert index, the chosen probabilities optionally renormalized by their sum (taken in pick order), weights rounded
-// to BF16 and stored as FP32. Combine: Σ_j w_j·h_j (fused multiply-adds in slot order) (+ bf16(σ(gate))·shared)
+// to BF16 and stored as FP32. A round that finds no finite probability (a row of NaN logits) gives expert id -1 with
+// weight 0, and that pair joins no expert group, so no expert GEMV ever reads past the expert table. Combine: Σ_j w_j·h_j (fused multiply-adds in slot order) (+ bf16(σ(gate))·shared)
 // (+ residual) in FP32, one BF16 rounding.
 //
 // MI355X design:
@@ -66,7 +67,12 @@ __global__ __launch_bounds__(64 * MAX_T) void moe_route(RouteArgs a) {
       for (int i = 0; i < MAX_PER_LANE; ++i)
         if (v[i] > best) { best = v[i]; bi = lane + 64 * i; }        // strictly greater: the lane's lowest index
       const float gmax = wave_max(best);
-      const int e = (int)wave_min(best == gmax ? (float)bi : (float)(1 << 20));
+      int e = (int)wave_min(best == gmax ? (float)bi : (float)(1 << 20));
+      if (e >= E) {                     // no finite probability left (NaN logits): no expert, weight 0
+        ce[r] = -1;
+        cw[r] = 0.0f;
+        continue;
+      }
 #pragma unroll
       for (int i = 0; i < MAX_PER_LANE; ++i)
         if (lane + 64 * i == e) v[i] = -1.0f;
@@ -75,7 +81,7 @@ __global__ __launch_bounds__(64 * MAX_T) void moe_route(RouteArgs a) {
       wsum += gmax;
     }
     for (int r = 0; r < k; ++r) {
-      const float w = a.renorm ? cw[r] / wsum : cw[r];
+      const float w = a.renorm && wsum > 0.0f ? cw[r] / wsum : cw[r];
       if (lane == 0) {
         a.ids[t * k + r] = ce[r];
         a.weights[t * k + r] = round_bf16(w);
@@ -91,7 +97,7 @@ __global__ __launch_bounds__(64 * MAX_T) void moe_route(RouteArgs a) {
   const int P = a.t * k;
   const int p = threadIdx.x;
   int e = -1, first = p, rank = 0, count = 0;
-  if (p < P) {
+  if (p < P && sel[p] >= 0) {          // a pair without an expert (id -1) joins no group
     e = sel[p];
     for (int q = 0; q < P; ++q) {
       if (sel[q] != e) continue;
@@ -100,14 +106,14 @@ __global__ __launch_bounds__(64 * MAX_T) void moe_route(RouteArgs a) {
       ++count;
     }
   }
-  fresh[p] = p < P && first == p;
+  fresh[p] = e >= 0 && first == p;
   __syncthreads();
   int distinct = 0, g = 0;
   for (int q = 0; q < P; ++q) {
     distinct += fresh[q];
     g += q < first ? fresh[q] : 0;
   }
-  if (p < P) {
+  if (e >= 0) {
     int32_t* rec = a.groups + (long long)g * GROUP_REC;
     rec[2 + rank] = p;
     if (rank == 0) { rec[0] = e; rec[1] = count; }

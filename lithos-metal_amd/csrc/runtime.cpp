@@ -5,6 +5,10 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <map>
+#include <mutex>
+#include <tuple>
+#include <vector>
 
 #include "mi_common.h"
 
@@ -24,6 +28,41 @@ int mi_check_hip(hipError_t e, const char* what) {
   if (e == hipSuccess) return MI_OK;
   (void)hipGetLastError();     // reported here: clear the thread's sticky error so the next caller's check is its own
   return mi_set_error(MI_E_HIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+namespace {
+struct Scratch { void* ptr; size_t bytes; };
+std::mutex g_scratch_mu;
+std::map<std::tuple<int, int, hipStream_t>, Scratch> g_scratch;
+std::vector<void*> g_retired;   // outgrown buffers: kept until the process ends (captured graphs may point at them)
+}  // namespace
+
+int mi_library_scratch(int kind, size_t bytes, hipStream_t stream, void** out) {
+  int dev = 0;
+  MI_TRY_HIP(hipGetDevice(&dev), "hipGetDevice");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  Scratch& w = g_scratch[std::make_tuple(kind, dev, stream)];
+  if (w.bytes < bytes) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    MI_TRY_HIP(hipStreamIsCapturing(stream, &cs), "hipStreamIsCapturing");
+    if (cs != hipStreamCaptureStatusNone)
+      return mi_set_error(MI_E_INVALID, "library scratch (kind %d) must grow from %zu to %zu bytes during a graph "
+                          "capture: run one eager call of this shape on the stream first, or pass a workspace",
+                          kind, w.bytes, bytes);
+    const size_t grow = bytes < (64u << 10) ? (64u << 10) : bytes;
+    void* p = nullptr;
+    MI_TRY_HIP(hipMalloc(&p, grow), "hipMalloc(library scratch)");
+    // zeroed on the stream that will use it, so the clear is ordered before that stream's kernels (a plain
+    // hipMemset runs on the null stream, which a non-blocking stream does not wait for)
+    if (int rc = mi_check_hip(hipMemsetAsync(p, 0, grow, stream), "hipMemsetAsync(library scratch)")) {
+      (void)hipFree(p);
+      return rc;
+    }
+    if (w.ptr) g_retired.push_back(w.ptr);
+    w = {p, grow};
+  }
+  *out = w.ptr;
+  return MI_OK;
 }
 
 extern "C" {

@@ -345,29 +345,6 @@ __global__ void fill_neg_inf(float* p, int n) {
   if ((int)threadIdx.x < n) p[threadIdx.x] = -INFINITY;
 }
 
-// the library's argmax workspace (per device, grown on demand, zeroed when allocated: the kernels keep its counters
-// at zero); calls sharing it must be ordered on one stream
-std::mutex g_am_mu;
-std::vector<std::pair<void*, size_t>> g_am;
-
-int argmax_workspace(size_t bytes, void** out) {
-  int dev = 0;
-  MI_TRY_HIP(hipGetDevice(&dev), "hipGetDevice");
-  std::lock_guard<std::mutex> lk(g_am_mu);
-  if ((int)g_am.size() <= dev) g_am.resize(dev + 1, {nullptr, 0});
-  auto& w = g_am[dev];
-  if (w.second < bytes) {
-    const size_t grow = bytes < 64 * 1024 ? 64 * 1024 : bytes;
-    if (w.first) MI_TRY_HIP(hipFree(w.first), "hipFree(argmax workspace)");
-    w = {nullptr, 0};
-    MI_TRY_HIP(hipMalloc(&w.first, grow), "hipMalloc(argmax workspace)");
-    MI_TRY_HIP(hipMemset(w.first, 0, grow), "hipMemset(argmax workspace)");
-    w.second = grow;
-  }
-  *out = w.first;
-  return MI_OK;
-}
-
 __global__ __launch_bounds__(64) void verify_select_step(mi_verify_select_desc d) {
   if (threadIdx.x != 0) return;
   mi_step_state* st = d.state;
@@ -601,7 +578,7 @@ int mi_argmax(const mi_argmax_desc* d, void* stream) {
   void* ws = d->workspace;
   if (ws) {
     MI_REQUIRE(d->workspace_bytes >= need, "mi_argmax: workspace %zu B < %zu B", d->workspace_bytes, need);
-  } else if (int rc = argmax_workspace(need, &ws)) {
+  } else if (int rc = mi_library_scratch(MI_SCRATCH_ARGMAX, need, static_cast<hipStream_t>(stream), &ws)) {
     return rc;
   }
   auto* counters = static_cast<uint32_t*>(ws);
@@ -638,7 +615,7 @@ int mi_sample(const mi_sample_desc* d, void* stream) {
   void* ws = d->workspace;
   if (ws) {
     MI_REQUIRE(d->workspace_bytes >= need, "mi_sample: workspace %zu B < %zu B", d->workspace_bytes, need);
-  } else if (int rc = argmax_workspace(need, &ws)) {
+  } else if (int rc = mi_library_scratch(MI_SCRATCH_ARGMAX, need, static_cast<hipStream_t>(stream), &ws)) {
     return rc;
   }
   char* wb = static_cast<char*>(ws);

@@ -23,6 +23,12 @@ def _torch():
     return torch
 
 
+def _check_flag(flag, name):
+    torch = _torch()
+    if flag is not None and (flag.dtype != torch.int32 or flag.numel() != 1 or flag.device.type != "cuda"):
+        raise ValueError(f"{name}: done must be a one-element int32 device tensor (the step state's flag)")
+
+
 @dataclass
 class PackedWeight:
     """A T16 pack resident in HBM: ``data`` uint8 ``[experts·nbytes]``, NVFP4 / FP8 ``row_scale`` float32
@@ -129,7 +135,7 @@ def dequant(w: PackedWeight, expert: int = 0, stream=None):
 
 def gdn_step(proj, conv_in, conv_out, rec_in, rec_out, *, conv_w, neg_exp_a, dt_bias, norm_w, k_heads, v_heads,
              dk=128, dv=128, conv_width=4, eps=1e-6, ab=None, offsets=None, out=None, stream=None,
-             defer_norm: bool = False, commit: bool = False, t_dev=None):
+             defer_norm: bool = False, commit: bool = False, t_dev=None, done=None):
     """``gdn_mixer`` + ``gdn_norm`` (``ops/gdn.py:1-24``) for ``proj [T, N1]`` bf16 in part order
     ``z | q | k | v | a | b`` (``nn/gdn.py:48-52``) unless ``offsets`` (z, q, k, v, a, b) says otherwise.
     Conv state ``[conv_dim, W-1]`` bf16 is read from ``conv_in`` and written to ``conv_out`` (distinct); the FP32
@@ -137,7 +143,9 @@ def gdn_step(proj, conv_in, conv_out, rec_in, rec_out, *, conv_w, neg_exp_a, dt_
     Returns ``[T, hv·dv]`` bf16: the gated-norm output, or with ``defer_norm`` the BF16 read-out ``o`` for a
     consumer that applies the norm itself (``gemv(..., gated_norm=...)``). ``commit`` is ``gdn_commit``
     (``ops/gdn.py:13-17``): the speculative commit pass re-runs the first ``t_dev`` (device int32, ≤ T; None = all)
-    tokens from the step's input state into ``rec_out`` / ``conv_out`` and returns None (no read-out)."""
+    tokens from the step's input state into ``rec_out`` / ``conv_out`` and returns None (no read-out). ``done``: a
+    step program's stop flag (one-element device int32 view of the step state): once set, the step takes no token —
+    the states pass through unchanged (``gdn_mixer.metal:281,330`` return at done)."""
     torch = _torch()
     _bf16_2d(proj, "gdn proj", aligned=False)
     t = proj.shape[0]
@@ -161,6 +169,7 @@ def gdn_step(proj, conv_in, conv_out, rec_in, rec_out, *, conv_w, neg_exp_a, dt_
         raise ValueError("gdn_step: the commit pass needs distinct rec_in / rec_out (two state slots)")
     if t_dev is not None and (t_dev.dtype != torch.int32 or t_dev.numel() != 1):
         raise ValueError("gdn_step: t_dev must be a one-element int32 device tensor")
+    _check_flag(done, "gdn_step")
     if out is None and not commit:
         out = torch.empty((t, vd), dtype=torch.bfloat16, device=proj.device)
     d = hip.MiGdnDesc(t=t, k_heads=k_heads, v_heads=v_heads, dk=dk, dv=dv, conv_width=conv_width, proj=hip.ptr(proj),
@@ -169,7 +178,7 @@ def gdn_step(proj, conv_in, conv_out, rec_in, rec_out, *, conv_w, neg_exp_a, dt_
                       neg_exp_a=hip.ptr(neg_exp_a), dt_bias=hip.ptr(dt_bias), norm_w=hip.ptr(norm_w),
                       conv_in=hip.ptr(conv_in), conv_out=hip.ptr(conv_out), rec_in=hip.ptr(rec_in),
                       rec_out=hip.ptr(rec_out), y=hip.ptr(out), ld_y=out.stride(0) if out is not None else 0, eps=eps,
-                      defer_norm=int(defer_norm), commit=int(commit), t_dev=hip.ptr(t_dev))
+                      defer_norm=int(defer_norm), commit=int(commit), t_dev=hip.ptr(t_dev), done=hip.ptr(done))
     hip.call("mi_gdn_step", C.byref(d), hip.stream_handle(stream))
     return out
 
@@ -232,13 +241,14 @@ class KVCache:
 
 def gqa_decode(proj, cache: KVCache, pos, *, heads: int, rope_cos, rope_sin, gate: bool = True,
                q_norm=None, k_norm=None, eps: float = 1e-6, scaling: Optional[float] = None, out=None, stream=None,
-               workspace=None):
+               workspace=None, done=None):
     """``gqa_decode`` + ``gqa_merge`` (``ops/attention.py``; ``GQAAttention.mix``, ``nn/attention.py:215-243``) for
     ``proj [T, N1]`` bf16 (``q|gate`` per head, then ``k``, ``v``): q/k norm (``q_norm``/``k_norm`` = the (1 + w)
     float32 weights, both or neither), partial RoPE from the BF16 tables ``[ctx_max, rotary_dim]``, the new k/v
     quantized into ``cache`` at ``pos..pos+T``, attention over the cache, × σ(gate). Returns ``[T, heads·D]`` bf16.
     ``pos`` is an int, or a one-element int32 device tensor the kernels read (a step program's StepState position:
-    the same launch serves every step of a replayed graph)."""
+    the same launch serves every step of a replayed graph). ``done``: a step program's stop flag (one-element device
+    int32): once set, nothing is appended to the cache and ``out`` is not written."""
     torch = _torch()
     _bf16_2d(proj, "gqa proj", aligned=False)
     t = proj.shape[0]
@@ -264,6 +274,7 @@ def gqa_decode(proj, cache: KVCache, pos, *, heads: int, rope_cos, rope_sin, gat
         if pos.dtype != torch.int32 or pos.numel() != 1 or pos.device.type != "cuda":
             raise ValueError("gqa_decode: pos must be an int or a one-element int32 device tensor")
         pos_dev, pos = pos, 0
+    _check_flag(done, "gqa_decode")
     desc = hip.MiGqaDesc(t=t, heads=heads, kv_heads=kv, head_dim=d, rotary_dim=rope_cos.shape[1], pos=pos,
                          ctx_max=cache.ctx_max, gate=int(gate), qk_norm=int(q_norm is not None), proj=hip.ptr(proj),
                          ld_proj=proj.stride(0), rope_cos=hip.ptr(rope_cos), rope_sin=hip.ptr(rope_sin),
@@ -273,7 +284,7 @@ def gqa_decode(proj, cache: KVCache, pos, *, heads: int, rope_cos, rope_sin, gat
                          v_scales=hip.ptr(cache.v_scales), y=hip.ptr(out), ld_y=out.stride(0),
                          workspace=hip.ptr(workspace),
                          workspace_bytes=0 if workspace is None else workspace.numel() * workspace.element_size(),
-                         pos_dev=hip.ptr(pos_dev))
+                         pos_dev=hip.ptr(pos_dev), done=hip.ptr(done))
     hip.call("mi_gqa_decode", C.byref(desc), hip.stream_handle(stream))
     return out
 

@@ -123,19 +123,26 @@ class GdnDecoderLayer:
 
     ping_pong = True          # the conv state alternates between two buffers: a captured program holds step pairs
 
+    def defers_norm(self, m: int) -> bool:
+        """Whether a step of ``m`` tokens leaves the gated RMSNorm to the output projection (``o`` then holds the
+        BF16 read-out): at M <= 2 (gemv_row stages its input where the norm fits); at M >= 3 its GEMV kernel keeps
+        the activations in registers and the norm stays a small kernel of its own. z must be a 16-byte aligned view
+        of the projection."""
+        return m <= 2 and self.n_proj % 8 == 0
+
     def _second_slot(self):
         if self.rec_slots[1 - self.slot] is None:
             self.rec_slots[1 - self.slot] = self.rec_slots[self.slot].clone()
         return self.rec_slots[1 - self.slot]
 
-    def commit(self, t_dev):
+    def commit(self, t_dev, done=None):
         """``gdn_commit`` after a verify pass (``step(..., verify=True)``): replay the first ``t_dev`` (device int32:
         the accept scan's committed rows) tokens of that pass from its input state into the other slots, which
         become the layer's state."""
         kernels.gdn_step(self._verify_proj, self.conv_state[self.parity], self.conv_state[1 - self.parity],
                          self.rec_slots[self.slot], self._second_slot(), conv_w=self.conv_w, neg_exp_a=self.neg_exp_a,
                          dt_bias=self.dt_bias, norm_w=self.gdn_norm_w, k_heads=self.hk, v_heads=self.hv, dk=self.dk,
-                         dv=self.dv, conv_width=self.conv, eps=self.eps, commit=True, t_dev=t_dev)
+                         dv=self.dv, conv_width=self.conv, eps=self.eps, commit=True, t_dev=t_dev, done=done)
         self.parity ^= 1
         self.slot ^= 1
 
@@ -144,17 +151,16 @@ class GdnDecoderLayer:
         """The current recurrent state."""
         return self.rec_slots[self.slot]
 
-    def step(self, h, out=None, pos=None, verify: bool = False):
+    def step(self, h, out=None, pos=None, verify: bool = False, done=None):
         """One decode step over ``h [M, hidden]`` bf16 (M ≤ 16 tokens): returns the layer output; advances the state.
         ``pos`` is accepted for a uniform layer interface (the recurrence needs no position). ``verify``: a
-        speculative verify pass — the outputs for every row, the state left for :meth:`commit`."""
+        speculative verify pass — the outputs for every row, the state left for :meth:`commit`. ``done``: a step
+        program's stop flag; once set the state passes through unchanged."""
         proj, o, h1, act, h2 = self.buffers(h.shape[0])
         out = h2 if out is None else out
         kernels.gemv(self.w_in.packed, h, norm_w=self.norm_w, eps=self.eps, out=proj)
         rec = self.rec_slots[self.slot]
-        # the gated norm rides on the output projection at M <= 2 (gemv_row); at M >= 3 its GEMV kernel keeps the
-        # activations in registers and the norm stays a small kernel of its own. z must be a 16-byte aligned view.
-        defer = h.shape[0] <= 2 and proj.stride(0) % 8 == 0
+        defer = self.defers_norm(h.shape[0])
         cin, cout = self.conv_state[self.parity], self.conv_state[1 - self.parity]
         if verify:                              # the verify pass writes the other slots; commit() settles them
             rec_out = self._second_slot()
@@ -162,7 +168,7 @@ class GdnDecoderLayer:
             rec_out = rec
         kernels.gdn_step(proj, cin, cout, rec, rec_out, conv_w=self.conv_w, neg_exp_a=self.neg_exp_a,
                          dt_bias=self.dt_bias, norm_w=self.gdn_norm_w, k_heads=self.hk, v_heads=self.hv, dk=self.dk,
-                         dv=self.dv, conv_width=self.conv, eps=self.eps, out=o, defer_norm=defer)
+                         dv=self.dv, conv_width=self.conv, eps=self.eps, out=o, defer_norm=defer, done=done)
         if verify:
             self._verify_proj = proj
         else:
@@ -235,14 +241,15 @@ class AttnDecoderLayer:
                              torch.empty(m, self.hidden, dtype=torch.bfloat16, device=dev))
         return self._bufs[m]
 
-    def step(self, h, pos: int, out=None):
+    def step(self, h, pos: int, out=None, done=None):
         """One decode step over ``h [M, hidden]`` at positions ``pos..pos+M-1``; the new k/v enter the cache. ``pos``
-        is an int or a one-element device int32 tensor (the step state's position in a captured program)."""
+        is an int or a one-element device int32 tensor (the step state's position in a captured program); ``done``
+        the program's stop flag (once set, nothing enters the cache)."""
         proj, o, h1, act, h2 = self.buffers(h.shape[0])
         out = h2 if out is None else out
         kernels.gemv(self.w_qkv.packed, h, norm_w=self.norm_w, eps=self.eps, out=proj)
         kernels.gqa_decode(proj, self.cache, pos, heads=self.heads, rope_cos=self.cos, rope_sin=self.sin, gate=True,
-                           q_norm=self.q_norm, k_norm=self.k_norm, eps=self.eps, out=o)
+                           q_norm=self.q_norm, k_norm=self.k_norm, eps=self.eps, out=o, done=done)
         kernels.gemv(self.w_o.packed, o, epilogue="residual", residual=h, out=h1)
         return self.mlp(h1, act=act, out=out)
 

@@ -45,7 +45,7 @@ class MiGdnDesc(C.Structure):
                 ("neg_exp_a", C.c_void_p), ("dt_bias", C.c_void_p), ("norm_w", C.c_void_p), ("conv_in", C.c_void_p),
                 ("conv_out", C.c_void_p), ("rec_in", C.c_void_p), ("rec_out", C.c_void_p), ("y", C.c_void_p),
                 ("ld_y", C.c_int32), ("eps", C.c_float), ("defer_norm", C.c_int32), ("commit", C.c_int32),
-                ("t_dev", C.c_void_p)]
+                ("t_dev", C.c_void_p), ("done", C.c_void_p)]
 
 
 class MiGqaDesc(C.Structure):
@@ -55,7 +55,8 @@ class MiGqaDesc(C.Structure):
                 ("rope_sin", C.c_void_p), ("q_norm", C.c_void_p), ("k_norm", C.c_void_p), ("eps", C.c_float),
                 ("scaling", C.c_float), ("k_codes", C.c_void_p), ("k_scales", C.c_void_p), ("v_codes", C.c_void_p),
                 ("v_scales", C.c_void_p), ("y", C.c_void_p), ("ld_y", C.c_int32), ("workspace", C.c_void_p),
-                ("workspace_bytes", C.c_size_t), ("pos_dev", C.c_void_p)]
+                ("workspace_bytes", C.c_size_t), ("pos_dev", C.c_void_p),
+                ("done", C.c_void_p)]
 
 
 class MiMoeRouteDesc(C.Structure):

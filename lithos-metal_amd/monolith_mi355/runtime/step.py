@@ -202,7 +202,7 @@ class StepProgram:
         torch = _torch()
         with torch.cuda.stream(s):
             for layer in m.layers:
-                h = layer.step(h, pos=pos)
+                h = layer.step(h, pos=pos, done=st.view("done"))
         kernels.gemv(m.lm_head, h, norm_w=m.norm_w, eps=m.eps, out=self.logits, stream=s)
         if self.sampling:
             kernels.sample(self.logits, state=st.buf, out=self.ids, stream=s, **self.sampling)
@@ -296,7 +296,10 @@ class SpecProgram(StepProgram):
         pos = st.view("position")
         with torch.cuda.stream(s):
             for layer in m.layers:
-                h = layer.step(h, pos=pos, verify=True) if getattr(layer, "ping_pong", False) else layer.step(h, pos=pos)
+                if getattr(layer, "ping_pong", False):
+                    h = layer.step(h, pos=pos, verify=True, done=st.view("done"))
+                else:
+                    h = layer.step(h, pos=pos, done=st.view("done"))
         kernels.gemv(m.lm_head, h, norm_w=m.norm_w, eps=m.eps, out=self.logits, stream=s)
         kernels.argmax(self.logits, out=self.ids, stream=s)
         kernels.accept_scan(st.buf, self.ids, st.ring.addr, st.ring_capacity, eos=self.eos, log=self.log,
@@ -304,7 +307,7 @@ class SpecProgram(StepProgram):
         with torch.cuda.stream(s):
             for layer in m.layers:
                 if getattr(layer, "ping_pong", False):
-                    layer.commit(st.view("checkpoint_index"))
+                    layer.commit(st.view("checkpoint_index"), done=st.view("done"))
         kernels.embed(self.draft_rows, st.view("position"), t=1, out=self.draft_buf, stream=s)
         kernels.verify_select(st.buf, self.drafts, self.conf, gamma=self.gamma, threshold=float(self.gamma),
                               t_max=t, mode=2, ctx_cap=self.ctx_cap, stream=s)

@@ -35,6 +35,13 @@ class OracleCheck:
     max_ulp_elementwise: int
     max_rel_err: float
     max_ulp_at_scale: float = 0.0
+    tol_violations: int = 0          # elements outside |y − ref| ≤ 1e-3 + 1e-2·|ref|
+    n: int = 0
+
+    @property
+    def within(self) -> bool:
+        """Every element within the stated tolerance (``within_tolerance``)."""
+        return self.tol_violations == 0
 
     def ok(self) -> bool:
         return self.max_ulp_at_rms <= 2.0 and self.max_rel_err < 1e-4
@@ -52,10 +59,18 @@ def check_against_oracle(y, y_ref) -> OracleCheck:
     mags = np.maximum(np.abs(y_ref), rms)
     ulps = 2.0 ** (np.floor(np.log2(np.maximum(mags, 1e-30))) - 7)
     return OracleCheck(float(err.max() / bf16_ulp_of(rms)), int(bf16_ulp_diff(y, y_ref).max()),
-                       float(err.max() / denom), float((err / ulps).max()))
+                       float(err.max() / denom), float((err / ulps).max()),
+                       int(np.count_nonzero(~(err <= 1e-3 + 1e-2 * np.abs(y_ref)))), int(err.size))
+
+
+def tolerance_violations(y, y_ref, rtol: float = 1e-2, atol: float = 1e-3) -> int:
+    """How many elements miss ``|y − ref| ≤ atol + rtol·|ref|`` (NaN counts as a miss)."""
+    y = np.asarray(y, dtype=np.float64)
+    y_ref = np.asarray(y_ref, dtype=np.float64)
+    return int(np.count_nonzero(~(np.abs(y - y_ref) <= atol + rtol * np.abs(y_ref))))
 
 
 def within_tolerance(y, y_ref, rtol: float = 1e-2, atol: float = 1e-3) -> bool:
-    y = np.asarray(y, dtype=np.float64)
-    y_ref = np.asarray(y_ref, dtype=np.float64)
-    return bool(np.all(np.abs(y - y_ref) <= atol + rtol * np.abs(y_ref)))
+    """The north-star bar for BF16 outputs with FP32 accumulation: every element within 1e-2 relative / 1e-3
+    absolute of the oracle."""
+    return tolerance_violations(y, y_ref, rtol, atol) == 0

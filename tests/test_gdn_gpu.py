@@ -37,7 +37,7 @@ def _check(got, ref, conv_got, conv_ref, rec_got, rec_ref):
     err = float(np.abs(rec_got - rec_ref).max())
     assert err <= 8 * 2.0 ** -23 * scale, (err, scale)
     chk = check_against_oracle(got, ref)
-    assert chk.ok_rounded(), chk
+    assert chk.ok_rounded() and chk.within, chk
 
 
 @pytest.mark.parametrize("hk,hv", [(16, 48), (4, 4), (2, 6)])

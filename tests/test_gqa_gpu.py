@@ -54,12 +54,22 @@ def _download(cache):
             cache.v_codes_token_major().cpu().numpy().transpose(1, 0, 2), cache.v_scales.cpu().numpy().T)
 
 
-def _check_out(y, ref):
+def _check_out(y, ref, n_keys):
     assert np.isfinite(y).all()
     g, r = y.astype(np.float64).ravel(), ref.astype(np.float64).ravel()
     cos = float(g @ r / (np.linalg.norm(g) * np.linalg.norm(r) + 1e-30))
     scale = float(np.abs(r).max())
     assert cos > 0.99999 and np.abs(g - r).max() <= 2 * bf16_ulp_of(scale), (cos, np.abs(g - r).max(), scale)
+    # element-wise 1e-2 / 1e-3: exact at the BASELINE contexts; a short context's output can be a cancelling sum
+    # of a few keys, where P rounded before normalisation (online softmax) differs from the oracle's P rounded after
+    # by more than the bar on a few elements: at most 0.5 % of them (the fraction is printed)
+    err = np.abs(g - r)
+    over = ~(err <= 1e-3 + 1e-2 * np.abs(r))
+    bad = int(over.sum())
+    worst = float((err / (1e-3 + 1e-2 * np.abs(r))).max())
+    print(f"  element-wise 1e-2/1e-3 ({n_keys} keys): {bad} of {g.size} outside, worst {worst:.2f}× the bound",
+          flush=True)
+    assert bad == 0 if n_keys >= 256 else bad <= 0.005 * g.size, (bad, g.size, worst)
 
 
 def _check_cache(got, want, pos, t, exact):
@@ -94,7 +104,7 @@ def _run(torch, rng, ctx, pos, t, rot=64, gate=True, qk_norm=False, steps=1, dev
                                q_norm=qn, k_norm=kn, eps=EPS)
         torch.cuda.synchronize()
         _check_cache(_download(cache), (kc, ks, vc, vs), pos, t, exact=not qk_norm)
-        _check_out(from_dev_bf16(y), ref)
+        _check_out(from_dev_bf16(y), ref, pos + t)
         pos += t
 
 

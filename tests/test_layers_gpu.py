@@ -1,10 +1,15 @@
 """Whole decode layers (``h += mixer(norm1(h)); h += mlp(norm2(h))``, ``nn/decoder.py:14-26``) built from the HIP
 kernels against the same layer composed from the oracle's functions on the exactly dequantized weights: the Gated
 DeltaNet layer and the gated-GQA layer over the int8 KV cache, at the 27B geometry (hidden 5120) and a small one,
-M = 1 and 8, two consecutive steps (state carried). Bar: the reference's composite layer bar
-(``tests/kernels/test_gqa_decode.py:347``: cosine > 0.9999, max |error| ≤ 1e-2 of the output's largest magnitude) —
-each GEMV's BF16 rounding can flip against the oracle's and the flip propagates — on the output and on the GDN
-recurrent state."""
+M = 1 and 8, two consecutive steps (state carried).
+
+Bars: every stage of the layer (the norm-fused projection, the mixer, the output projection with its residual, the
+gate|up and down GEMVs) against the oracle fed the device's own input to that stage, element-wise within 1e-2
+relative / 1e-3 absolute — the attention core within its kernel test's bar; and the whole
+layer end to end from the oracle's own chain with the reference's composite layer bar
+(``tests/kernels/test_gqa_decode.py:347``: cosine > 0.9999, max |error| ≤ 1e-2 of the output's largest magnitude),
+on the output and on the GDN recurrent state: end to end, each GEMV's BF16 rounding can flip against the oracle's and
+the flip propagates, so that fraction is printed, not asserted element-wise."""
 
 import numpy as np
 import pytest
@@ -13,6 +18,7 @@ from helpers import from_dev_bf16, to_dev_bf16
 from oracle import formats as OF
 from oracle import nn as ON
 from oracle.fp import rbf
+from oracle.gates import check_against_oracle, tolerance_violations
 
 pytestmark = pytest.mark.gpu
 EPS = 1e-6
@@ -31,17 +37,39 @@ def _deq_gate_up(q):
     return out
 
 
-def _bar(got, ref):
+def _bar(got, ref, what):
+    """The end-to-end layer bar: cosine and max error norm-wise (the reference's layer bar); the element-wise
+    fraction outside 1e-2 / 1e-3 is printed — each GEMV's BF16 rounding can flip against the oracle's, and a flip
+    moves every later stage by up to an ULP, so element-wise exactness is asserted per stage (``_stage``)."""
     g, r = got.astype(np.float64).ravel(), ref.astype(np.float64).ravel()
     cos = float(g @ r / (np.linalg.norm(g) * np.linalg.norm(r) + 1e-30))
     err, scale = float(np.abs(g - r).max()), float(np.abs(r).max())
-    assert cos > 0.9999 and err <= 1e-2 * scale, (cos, err, scale)
+    assert cos > 0.9999 and err <= 1e-2 * scale, (what, cos, err, scale)
+    print(f"  {what} end to end: {tolerance_violations(g, r)} of {g.size} outside 1e-2/1e-3 (cos {cos:.7f})",
+          flush=True)
+
+
+def _stage(got, ref, what):
+    """One stage of the layer given the device's own input to it: the north-star bar element-wise (every element
+    within 1e-3 + 1e-2·|ref|) and the reference's ``ok_rounded``."""
+    chk = check_against_oracle(got, ref)
+    print(f"  {what}: {chk.tol_violations} of {chk.n} outside 1e-2/1e-3", flush=True)
+    assert chk.within and chk.ok_rounded(), (what, chk)
 
 
 def _mlp(h1, ex):
     x2 = ON.rms_norm(h1, ex["norm2"], EPS, one_plus=False)
     act = ON.linear(x2, _deq_gate_up(ex["gate_up"]), epilogue="silu_mul")
     return ON.linear(act, _deq(ex["down"]), epilogue="residual", residual=h1)
+
+
+def _mlp_stages(layer, m, h1_dev, ex):
+    """The MLP's two GEMVs, each against the oracle fed the device's own input."""
+    _, _, _, act, h2 = layer.buffers(m)
+    act_d, h2_d = from_dev_bf16(act), from_dev_bf16(h2)
+    x2 = ON.rms_norm(h1_dev, ex["norm2"], EPS, one_plus=False)
+    _stage(act_d, ON.linear(x2, _deq_gate_up(ex["gate_up"]), epilogue="silu_mul"), "gate|up silu·mul")
+    _stage(h2_d, ON.linear(act_d, _deq(ex["down"]), epilogue="residual", residual=h1_dev), "down + residual")
 
 
 @pytest.mark.parametrize("geom", ["small", "27b"])
@@ -54,18 +82,33 @@ def test_gdn_decoder_layer(torch_gpu, geom, m):
     ex = layer.export()
     conv, rec = ex["conv_state"], ex["rec_state"]
     w_in, w_out = _deq(ex["w_in"]), _deq(ex["w_out"])
+    hv = layer.hv
+    gdn_kw = dict(conv_w=ex["conv_w"], a_log=ex["a_log"], dt_bias=ex["dt_bias"], norm_w=ex["gdn_norm_w"],
+                  k_heads=layer.hk, v_heads=hv, dk=128, dv=128, eps=EPS)
     rng = np.random.default_rng(m)
     for step in range(2):
         print(f"gdn layer {geom} m={m} step {step}", flush=True)
+        dev_state = layer.export()                      # the device's state before this step
         h = rbf(rng.standard_normal((m, layer.hidden)))
         got = from_dev_bf16(layer.step(to_dev_bf16(torch, h)))
+        # stage by stage, each fed the device's own input
+        proj_d, o_dev, h1_dev = (from_dev_bf16(b) for b in layer.buffers(m)[:3])
+        xn = ON.rms_norm(h, ex["norm1"], EPS, one_plus=False)
+        _stage(proj_d, ON.linear(xn, w_in), "in_proj (norm fused)")
+        y_ref, _, _ = ON.gdn_mix(proj_d, dev_state["conv_state"], dev_state["rec_state"], **gdn_kw)
+        if layer.defers_norm(m):                        # o holds the read-out; the norm rides on out_proj
+            o_dev = ON.gated_rms_norm(o_dev.reshape(m * hv, 128), proj_d[:, : hv * 128].reshape(m * hv, 128),
+                                      ex["gdn_norm_w"], EPS).reshape(m, hv * 128)
+        _stage(o_dev, y_ref, "gdn mixer (gated norm)")
+        _stage(h1_dev, ON.linear(o_dev, w_out, epilogue="residual", residual=h), "out_proj + residual")
+        _mlp_stages(layer, m, h1_dev, ex)
+        # end to end from the oracle's own chain
         xn = ON.rms_norm(h, ex["norm1"], EPS, one_plus=False)
         proj = ON.linear(xn, w_in)
-        o, conv, rec = ON.gdn_mix(proj, conv, rec, conv_w=ex["conv_w"], a_log=ex["a_log"], dt_bias=ex["dt_bias"],
-                                  norm_w=ex["gdn_norm_w"], k_heads=layer.hk, v_heads=layer.hv, dk=128, dv=128, eps=EPS)
+        o, conv, rec = ON.gdn_mix(proj, conv, rec, **gdn_kw)
         h1 = ON.linear(o, w_out, epilogue="residual", residual=h)
-        _bar(got, _mlp(h1, ex))
-        _bar(layer.rec_state.cpu().numpy(), rec)
+        _bar(got, _mlp(h1, ex), "layer output")
+        _bar(layer.rec_state.cpu().numpy(), rec, "recurrent state")
 
 
 @pytest.mark.parametrize("geom,ctx,pos", [("small", 1024, 300), ("27b", 4096, 4000)])
@@ -88,10 +131,20 @@ def test_attention_decoder_layer(torch_gpu, geom, ctx, pos, m):
     for step in range(2):
         print(f"attn layer {geom} m={m} step {step} pos={pos}", flush=True)
         h = rbf(rng.standard_normal((m, layer.hidden)))
+        dev = layer.export()                            # the device's cache before this step
         got = from_dev_bf16(layer.step(to_dev_bf16(torch, h), pos))
+        proj_d, o_dev, h1_dev = (from_dev_bf16(b) for b in layer.buffers(m)[:3])
         xn = ON.rms_norm(h, ex["norm1"], EPS, one_plus=False)
+        _stage(proj_d, ON.linear(xn, w_qkv), "qkv proj (norm fused)")
+        o_ref = ON.gqa_mix(proj_d, dev["k_codes"].transpose(1, 0, 2).copy(), dev["k_scales"].T.copy(),
+                           dev["v_codes"].transpose(1, 0, 2).copy(), dev["v_scales"].T.copy(), pos, **cfg)
+        bad = tolerance_violations(o_dev, o_ref)        # attention's own bar is the kernel test's (test_gqa_gpu)
+        print(f"  attention core: {bad} of {o_dev.size} outside 1e-2/1e-3", flush=True)
+        assert bad <= 0.005 * o_dev.size, bad
+        _stage(h1_dev, ON.linear(o_dev, w_o, epilogue="residual", residual=h), "o_proj + residual")
+        _mlp_stages(layer, m, h1_dev, ex)
         proj = ON.linear(xn, w_qkv)
         o = ON.gqa_mix(proj, kc, ks, vc, vs, pos, **cfg)
         h1 = ON.linear(o, w_o, epilogue="residual", residual=h)
-        _bar(got, _mlp(h1, ex))
+        _bar(got, _mlp(h1, ex), "layer output")
         pos += m

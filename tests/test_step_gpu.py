@@ -519,3 +519,42 @@ def test_start_resets_the_speculative_fields_and_the_scan_guards_a_stale_state(t
     g = st.read()
     assert g["ring_head"] == 1 and g["position"] == 11 and g["accepted"] == 0
     assert int(st.ring.array[0]) & 0xFFFFFFFF == 42
+
+
+def test_decoder_program_stop_inside_a_graph_leaves_the_state_of_the_emitted_steps(torch_gpu):
+    """stop_at = 5 with four steps per graph: the stop falls on the first step of the second launch's pair, so the
+    steps queued after it in the same graph still run. They must take no token: the Gated DeltaNet recurrent and conv
+    state and the attention KV cache equal those of a host loop over exactly the five emitted steps (bit for bit),
+    and nothing is appended at the sixth position."""
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    from monolith_mi355.runtime.step import StepProgram, StepState
+    _say("decoder program: stop inside a graph")
+    emitted = 5
+    a = _decoder(torch, 13)
+    tok, pos, host = 7, 40, []
+    for _ in range(emitted):
+        h = kernels.embed(a.embed_table, torch.tensor([tok], dtype=torch.int32, device="cuda"))
+        for layer in a.layers:
+            h = layer.step(h, pos=pos)
+        logits = kernels.gemv(a.lm_head, h, norm_w=a.norm_w, eps=a.eps)
+        tok = int(O.argmax(from_dev_bf16(logits))[0])
+        host.append(tok)
+        pos += 1
+    b = _decoder(torch, 13)
+    st = StepState(ring_capacity=64)
+    prog = StepProgram(b, st, ctx_cap=256, steps_per_graph=4)
+    st.start(position=40, token=7, stop_at=emitted)
+    first = prog.step_eager(2)                     # steps 1, 2 eagerly; then graphs of steps 3-6 and 7-10
+    rep = prog.run(8, launches_per_batch=1, in_flight=1)
+    torch.cuda.synchronize()
+    assert first + rep.tokens == host and rep.done
+    g = st.read()
+    assert g["step"] == emitted and g["position"] == 40 + emitted and g["done"] == 1
+    ga, gb = a.layers[0], b.layers[0]
+    assert torch.equal(ga.rec, gb.rec), "GDN recurrent state moved after the stop"
+    assert torch.equal(ga.conv_state[ga.parity], gb.conv_state[gb.parity]), "GDN conv state moved after the stop"
+    ca, cb = a.layers[1].cache, b.layers[1].cache
+    for name in ("k_codes", "v_codes", "k_scales", "v_scales"):
+        assert torch.equal(getattr(ca, name), getattr(cb, name)), f"KV cache {name} differs after the stop"
+    assert int(cb.k_scales[:, 40 + emitted].abs().sum()) == 0
