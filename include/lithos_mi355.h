@@ -141,6 +141,13 @@ typedef struct mi_gemv_desc {
 } mi_gemv_desc;
 size_t mi_gemv_workspace_bytes(const mi_gemv_desc* d);   /* 0 when the plan needs none */
 int mi_gemv(const mi_gemv_desc* d, void* stream);
+/* mi_gemv that allocates nothing — no counterpart in the reference: for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same descriptor, plans and
+ * kernels as mi_gemv, with workspace = NULL: split-K plans use one fixed device-resident array per GPU
+ * (mi_gemv_noalloc_scratch_bytes(), 8 MiB), and a shape needing more returns MI_E_INVALID. Every call on a GPU shares
+ * that GPU's array: calls that overlap in time on one GPU (several streams, or host threads) race. */
+int mi_gemv_noalloc(const mi_gemv_desc* d, void* stream);
+size_t mi_gemv_noalloc_scratch_bytes(void);
 /* the launch plan mi_gemv would use (host only; the tiles per workgroup of a fused-norm M = 1 plan follow the
  * current device's occupancy): out = [kernel (1: gemv_row, the M <= 2 kernel whose waves split a tile's K; 2:
  * gemv_tk, the tile-streaming kernel), waves per workgroup, chunks per wave (row) or chunks per K split (tk),

@@ -2039,10 +2039,16 @@ int mi_gemv_plan(const mi_gemv_desc* d, int32_t out[7]) {
   return MI_OK;
 }
 
-int mi_gemv(const mi_gemv_desc* d, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// The body of mi_gemv and mi_gemv_noalloc. fixed_ws: the split-K buffer to use (the no-allocation entry point's
+// device-resident array), or null: the caller's workspace, else the library's scratch.
+int gemv_impl(const mi_gemv_desc* d, void* stream, void* fixed_ws, size_t fixed_bytes, const char* name) {
   if (int rc = check_desc(d)) return rc;
   const Plan p = make_plan(d);
-  MI_REQUIRE(p.kernel, "mi_gemv: no launch plan fits (k=%d, m=%d)", d->k, d->m);
+  MI_REQUIRE(p.kernel, "%s: no launch plan fits (k=%d, m=%d)", name, d->k, d->m);
   Args a{};
   a.w = static_cast<const uint8_t*>(d->w);
   a.row_scale = d->row_scale;
@@ -2075,9 +2081,12 @@ int mi_gemv(const mi_gemv_desc* d, void* stream) {
   if (p.ks > 1) {
     const size_t cb = fold_counter_bytes(d->n);
     const size_t need = cb + (size_t)p.ks * d->m * ((d->n + 15) / 16) * 16 * sizeof(float);
-    void* ws = d->workspace;
-    if (ws) {
-      MI_REQUIRE(d->workspace_bytes >= need, "mi_gemv: workspace %zu B < %zu B", d->workspace_bytes, need);
+    void* ws = fixed_ws ? fixed_ws : d->workspace;
+    if (fixed_ws) {
+      MI_REQUIRE(need <= fixed_bytes, "%s: this shape needs %zu B of split-K scratch, more than the %zu B the "
+                 "no-allocation entry point holds (use mi_gemv with a workspace)", name, need, fixed_bytes);
+    } else if (ws) {
+      MI_REQUIRE(d->workspace_bytes >= need, "%s: workspace %zu B < %zu B", name, d->workspace_bytes, need);
     } else if (int rc = mi_library_scratch(MI_SCRATCH_GEMV, need, static_cast<hipStream_t>(stream), &ws)) {
       return rc;
     }
@@ -2095,6 +2104,54 @@ int mi_gemv(const mi_gemv_desc* d, void* stream) {
   MI_TRY_HIP(hipGetLastError(), "gemv launch");
   return MI_OK;
 }
+
+// ---- the no-allocation entry point's scratch: one device-resident array per GPU, found once per device with
+// hipGetSymbolAddress (the array's host-side name is not a device address) ------------------------------------------
+constexpr size_t kNoAllocScratchBytes = 8u << 20;   // fold counters (64 KiB) + split-K partials
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+__global__ void clear_words(uint32_t* p, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+std::mutex g_noalloc_mu;
+std::vector<void*> g_noalloc_ptr;     // per device: the address of that device's copy of `scratch`, or null
+
+// the current device's scratch address; on a device's first call its fold counters are cleared by a small fill
+// kernel on the caller's stream (ordered before this call's kernels; captured with them if the caller captures)
+int noalloc_scratch(hipStream_t s, void** out) {
+  int dev = 0;
+  MI_TRY_HIP(hipGetDevice(&dev), "hipGetDevice");
+  std::lock_guard<std::mutex> lk(g_noalloc_mu);
+  if ((int)g_noalloc_ptr.size() <= dev) g_noalloc_ptr.resize(dev + 1, nullptr);
+  if (!g_noalloc_ptr[dev]) {
+    void* ptr = nullptr;
+    MI_TRY_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    hipLaunchKernelGGL(clear_words, dim3(16), dim3(256), 0, s, static_cast<uint32_t*>(ptr),
+                       (int)(kFoldCounterBytes / sizeof(uint32_t)));
+    MI_TRY_HIP(hipGetLastError(), "clear_words launch");
+    g_noalloc_ptr[dev] = ptr;
+  }
+  *out = g_noalloc_ptr[dev];
+  return MI_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mi_gemv(const mi_gemv_desc* d, void* stream) { return gemv_impl(d, stream, nullptr, 0, "mi_gemv"); }
+
+int mi_gemv_noalloc(const mi_gemv_desc* d, void* stream) {
+  MI_REQUIRE(d, "mi_gemv_noalloc: null descriptor");
+  MI_REQUIRE(!d->workspace, "mi_gemv_noalloc: takes no workspace (its split-K scratch is the library's fixed "
+             "device array); pass workspace = NULL");
+  void* ws = nullptr;
+  if (int rc = noalloc_scratch(static_cast<hipStream_t>(stream), &ws)) return rc;
+  return gemv_impl(d, stream, ws, kNoAllocScratchBytes, "mi_gemv_noalloc");
+}
+
+size_t mi_gemv_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
 
 int mi_dequant(int32_t format, const void* w, const float* row_scale, int32_t n, int32_t k, float* out, void* stream) {
   MI_REQUIRE(w && out, "mi_dequant: null pointer");

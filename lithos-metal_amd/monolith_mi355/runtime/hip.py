@@ -166,6 +166,8 @@ SIGNATURES = {
     "mi_pack_bytes": (_SZ, [_I32, _I32, _I32]),
     "mi_gemv_workspace_bytes": (_SZ, [C.POINTER(MiGemvDesc)]),
     "mi_gemv": (C.c_int, [C.POINTER(MiGemvDesc), _VP]),
+    "mi_gemv_noalloc": (C.c_int, [C.POINTER(MiGemvDesc), _VP]),
+    "mi_gemv_noalloc_scratch_bytes": (_SZ, []),
     "mi_gemv_plan": (C.c_int, [C.POINTER(MiGemvDesc), C.POINTER(_I32)]),
     "mi_dequant": (C.c_int, [_I32, _VP, _VP, _I32, _I32, _VP, _VP]),
     "mi_gdn_step": (C.c_int, [C.POINTER(MiGdnDesc), _VP]),
