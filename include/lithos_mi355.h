@@ -154,6 +154,20 @@ size_t mi_gemv_noalloc_scratch_bytes(void);
  * tiles per workgroup, K splits, LDS bytes, workgroups] */
 int mi_gemv_plan(const mi_gemv_desc* d, int32_t out[7]);
 
+/* A chain of dependent one-token NVFP4 GEMVs in ONE persistent launch — a decode layer's projection tail
+ * (out_proj → gate|up → down, or the MLP's gate|up → down): the counterpart of the reference's region / MLP fusion
+ * into a megakernel with bounded worker synchronization (compiler/region_fusion.py:25-58, compiler/mlp_fusion.py:103-130,
+ * runtime/engine.py:100-105). Phase i is phases[i] with mi_gemv's semantics (m = 1, dense, BF16 output, fused input
+ * RMSNorm or gated head norm, residual / silu·mul epilogues; K up to 6144 with a fused norm, longer K split in order)
+ * and starts only after phase i-1 has finished, so it may read any earlier phase's output (as x or residual).
+ * workspace: mi_gemv_chain_workspace_bytes, zeroed once before its first use (its counters return to zero after every
+ * launch); NULL = the library's own. mi_gemv_chain_error reads the control block's error flag (1: a wait ran past its
+ * bound because the grid could not run together; the results are then wrong). */
+#define MI_CHAIN_MAX_PHASES 4
+size_t mi_gemv_chain_workspace_bytes(const mi_gemv_desc* phases, int32_t n_phases);
+int mi_gemv_chain(const mi_gemv_desc* phases, int32_t n_phases, void* workspace, size_t workspace_bytes, void* stream);
+int mi_gemv_chain_error(const void* workspace, void* stream, uint32_t* out);
+
 /* exact dequantization of a T16 pack to FP32 [n, k] through the kernels' own decode (the bit-exact check of
  * Format.dequantize, formats/base.py:52-81 / nvfp4.py:139-144 / int4_affine.py:85-91) */
 int mi_dequant(int32_t format, const void* w, const float* row_scale, int32_t n, int32_t k, float* out, void* stream);

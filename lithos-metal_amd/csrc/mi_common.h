@@ -24,7 +24,7 @@ int mi_check_hip(hipError_t e, const char* what);         // 0 on success, else 
 // zeroed when allocated (kernels that keep counters leave them at zero). It grows on demand but is never freed
 // before the process ends — a graph captured earlier keeps the address it recorded — and it refuses to grow while
 // the stream is being captured (the caller runs one eager call of the shape first, or passes its own workspace).
-enum MiScratchKind { MI_SCRATCH_GEMV = 0, MI_SCRATCH_GQA = 1, MI_SCRATCH_ARGMAX = 2 };
+enum MiScratchKind { MI_SCRATCH_GEMV = 0, MI_SCRATCH_GQA = 1, MI_SCRATCH_ARGMAX = 2, MI_SCRATCH_CHAIN = 3 };
 int mi_library_scratch(int kind, size_t bytes, hipStream_t stream, void** out);
 
 #define MI_TRY_HIP(expr, what)                          \

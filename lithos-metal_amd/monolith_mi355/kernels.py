@@ -83,6 +83,15 @@ def gemv(w: PackedWeight, x, *, epilogue=None, residual=None, norm_w=None, eps: 
     float32 weight of a fused input RMSNorm; ``out_f32`` writes the unrounded FP32 result (``lm_head``).
     ``gated_norm = (w [128] float32, z [M, K] bf16 view, eps)`` applies the Gated DeltaNet output norm
     (``gdn_norm``, ``nn/gdn.py:86-93``) to x per 128-column head while staging it."""
+    d, out = _gemv_desc(w, x, epilogue=epilogue, residual=residual, norm_w=norm_w, eps=eps, out=out,
+                        workspace=workspace, out_f32=out_f32, gated_norm=gated_norm)
+    hip.call("mi_gemv", C.byref(d), hip.stream_handle(stream))
+    return out
+
+
+def _gemv_desc(w: PackedWeight, x, *, epilogue=None, residual=None, norm_w=None, eps: float = 1e-6, out=None,
+               workspace=None, out_f32: bool = False, gated_norm=None):
+    """The checked ``mi_gemv_desc`` of one GEMV (and its output tensor, allocated when not given)."""
     torch = _torch()
     _bf16_2d(x, "gemv x")
     m, k = x.shape
@@ -118,8 +127,29 @@ def gemv(w: PackedWeight, x, *, epilogue=None, residual=None, norm_w=None, eps: 
                        workspace=hip.ptr(workspace), workspace_bytes=0 if workspace is None else workspace.numel(),
                        out_f32=int(out_f32), gnorm_w=hip.ptr(gw), gnorm_z=hip.ptr(gz),
                        ld_gnorm_z=gz.stride(0) if gz is not None else 0, gnorm_eps=geps)
-    hip.call("mi_gemv", C.byref(d), hip.stream_handle(stream))
-    return out
+    return d, out
+
+
+def gemv_chain(phases, *, workspace=None, stream=None):
+    """A chain of dependent one-token NVFP4 GEMVs in one persistent launch (``mi_gemv_chain``): ``phases`` is a list
+    of ``(w, x, kwargs)`` with :func:`gemv`'s keyword arguments (``epilogue``, ``residual``, ``norm_w``, ``eps``,
+    ``out``, ``gated_norm``); phase i runs after phase i-1 has finished, so its ``x`` or ``residual`` may be an
+    earlier phase's ``out``. The fused counterpart of the reference's MLP / region megakernels
+    (``compiler/mlp_fusion.py:103-130``). Returns the outputs."""
+    if not 1 <= len(phases) <= 4:
+        raise ValueError("gemv_chain: 1..4 phases")
+    descs, outs = [], []
+    for w, x, kw in phases:
+        if w.format != "nvfp4" or x.shape[0] != 1:
+            raise ValueError("gemv_chain: NVFP4 weights and one token")
+        d, o = _gemv_desc(w, x, **kw)
+        descs.append(d)
+        outs.append(o)
+    arr = (hip.MiGemvDesc * len(descs))(*descs)
+    ws = 0 if workspace is None else hip.ptr(workspace)
+    nb = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    hip.call("mi_gemv_chain", arr, len(descs), ws, nb, hip.stream_handle(stream))
+    return outs
 
 
 def dequant(w: PackedWeight, expert: int = 0, stream=None):

@@ -1,7 +1,8 @@
 """Decode layers composed from the HIP kernels: ``h += mixer(norm1(h)); h += mlp(norm2(h))`` (``nn/decoder.py:14-26``)
 with a Gated DeltaNet (``nn/gdn.py:21-120``) or gated GQA (``nn/attention.py:27-155``) mixer and the gated MLP
 (``nn/mlp.py:14-30``), every projection an NVFP4 GEMV with its RMSNorm fused on load and its residual add fused in
-the epilogue. A step is 5 launches for the GDN layer and 7 for the attention layer; nothing allocates inside
+the epilogue. A step is 5 launches for the GDN layer and 7 for the attention layer (with MI_LAYER_CHAIN=1 the
+one-token projection tail is one persistent GEMV chain launch instead of three); nothing allocates inside
 ``step`` when ``out`` buffers are given, so a step can be captured into a HIP graph.
 
 Weights are synthetic (N(0, 0.02) quantized on the GPU with the reference NVFP4 rule) — there is no network for
@@ -11,6 +12,7 @@ state, attention KV cache), so several instances are several layers of one model
 
 from __future__ import annotations
 
+import os
 from dataclasses import dataclass
 from typing import Dict, Optional
 
@@ -23,6 +25,12 @@ from .formats import device as DV
 def _torch():
     import torch
     return torch
+
+
+# MI_LAYER_CHAIN=1: at one token, a layer's projection tail (output projection → gate|up → down) runs as one
+# persistent GEMV chain launch (kernels.gemv_chain) instead of one launch per GEMV. Off by default: at the 27B shapes
+# the chain measured slower (MLP 46–48 µs against 38–41 µs for the two launches)
+CHAIN_TAIL = os.environ.get("MI_LAYER_CHAIN", "0") == "1"
 
 
 @dataclass
@@ -72,7 +80,19 @@ class GatedMLP:
         self.gate_up = nvfp4_matrix(2 * inter, hidden, gen, device, gate_up=True)
         self.down = nvfp4_matrix(hidden, inter, gen, device)
 
+    def phases(self, h, act, out):
+        """The MLP as GEMV-chain phases: gate|up (norm fused, silu·mul) → down (+ residual h)."""
+        return [(self.gate_up.packed, h, dict(epilogue="silu_mul", norm_w=self.norm_w, eps=self.eps, out=act)),
+                (self.down.packed, act, dict(epilogue="residual", residual=h, out=out))]
+
     def __call__(self, h, act=None, out=None):
+        if CHAIN_TAIL and h.shape[0] == 1:
+            torch = _torch()
+            if act is None:
+                act = torch.empty(1, self.inter, dtype=torch.bfloat16, device=h.device)
+            if out is None:
+                out = torch.empty_like(h)
+            return kernels.gemv_chain(self.phases(h, act, out))[1]
         act = kernels.gemv(self.gate_up.packed, h, epilogue="silu_mul", norm_w=self.norm_w, eps=self.eps, out=act)
         return kernels.gemv(self.down.packed, act, epilogue="residual", residual=h, out=out)
 
@@ -174,8 +194,12 @@ class GdnDecoderLayer:
         else:
             self.parity ^= 1
         # the gated RMSNorm (gdn_norm) is applied by the output projection while it stages o; z = proj[:, :hv·dv]
-        kernels.gemv(self.w_out.packed, o, epilogue="residual", residual=h, out=h1,
-                     gated_norm=(self.gdn_norm_w, proj[:, : self.hv * self.dv], self.eps) if defer else None)
+        gated = (self.gdn_norm_w, proj[:, : self.hv * self.dv], self.eps) if defer else None
+        if CHAIN_TAIL and h.shape[0] == 1:
+            kernels.gemv_chain([(self.w_out.packed, o, dict(epilogue="residual", residual=h, out=h1, gated_norm=gated))]
+                               + self.mlp.phases(h1, act, out))
+            return out
+        kernels.gemv(self.w_out.packed, o, epilogue="residual", residual=h, out=h1, gated_norm=gated)
         return self.mlp(h1, act=act, out=out)
 
     def mixer_bytes(self, m: int) -> int:
@@ -250,6 +274,10 @@ class AttnDecoderLayer:
         kernels.gemv(self.w_qkv.packed, h, norm_w=self.norm_w, eps=self.eps, out=proj)
         kernels.gqa_decode(proj, self.cache, pos, heads=self.heads, rope_cos=self.cos, rope_sin=self.sin, gate=True,
                            q_norm=self.q_norm, k_norm=self.k_norm, eps=self.eps, out=o, done=done)
+        if CHAIN_TAIL and h.shape[0] == 1:
+            kernels.gemv_chain([(self.w_o.packed, o, dict(epilogue="residual", residual=h, out=h1))]
+                               + self.mlp.phases(h1, act, out))
+            return out
         kernels.gemv(self.w_o.packed, o, epilogue="residual", residual=h, out=h1)
         return self.mlp(h1, act=act, out=out)
 

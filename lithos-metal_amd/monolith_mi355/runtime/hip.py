@@ -167,6 +167,9 @@ SIGNATURES = {
     "mi_gemv_workspace_bytes": (_SZ, [C.POINTER(MiGemvDesc)]),
     "mi_gemv": (C.c_int, [C.POINTER(MiGemvDesc), _VP]),
     "mi_gemv_noalloc": (C.c_int, [C.POINTER(MiGemvDesc), _VP]),
+    "mi_gemv_chain_workspace_bytes": (_SZ, [C.POINTER(MiGemvDesc), _I32]),
+    "mi_gemv_chain": (C.c_int, [C.POINTER(MiGemvDesc), _I32, _VP, _SZ, _VP]),
+    "mi_gemv_chain_error": (C.c_int, [_VP, _VP, C.POINTER(C.c_uint32)]),
     "mi_gemv_noalloc_scratch_bytes": (_SZ, []),
     "mi_gemv_plan": (C.c_int, [C.POINTER(MiGemvDesc), C.POINTER(_I32)]),
     "mi_dequant": (C.c_int, [_I32, _VP, _VP, _I32, _I32, _VP, _VP]),
