@@ -172,6 +172,25 @@ int mi_gemv_chain_error(const void* workspace, void* stream, uint32_t* out);
  * Format.dequantize, formats/base.py:52-81 / nvfp4.py:139-144 / int4_affine.py:85-91) */
 int mi_dequant(int32_t format, const void* w, const float* row_scale, int32_t n, int32_t k, float* out, void* stream);
 
+/* ---- RMSNorm as standalone ops (ops/norm.py:11-12: rmsnorm_stat, norm_apply; kernels/common/rmsnorm_stat.metal:18-40,
+ *      norm_apply.metal:24-51) — for a norm that does not feed a GEMV directly (mi_gemv fuses it on load) ----------
+ * rmsnorm_stat: stat[i] = Σ_k h[i][k]² (FP32). norm_apply: x[i] = bf16(h[i]·rsqrt(s/k + eps)·w), s = Σ of the
+ * stat_parts partial sums stat[i][·], or — with stat = NULL — computed in the same launch; w is the (1 + w) weight.
+ * h and x: BF16 rows, 16-byte aligned, strides multiples of 8, k a multiple of 8. */
+typedef struct mi_norm_desc {
+  int32_t t, k;
+  const uint16_t* h;
+  int32_t ldh;
+  float* stat;               /* rmsnorm_stat: output [t]; norm_apply: input [t][stat_parts] or NULL */
+  int32_t stat_parts;
+  const float* w;            /* norm_apply: (1 + w) [k] FP32 */
+  uint16_t* x;               /* norm_apply: output [t][ldx] */
+  int32_t ldx;
+  float eps;
+} mi_norm_desc;
+int mi_rmsnorm_stat(const mi_norm_desc* d, void* stream);
+int mi_norm_apply(const mi_norm_desc* d, void* stream);
+
 /* ---- Gated DeltaNet decode step (ops/gdn.py `gdn_mixer` + `gdn_norm`; nn/gdn.py:64-93;
  *      kernels/common/gdn_mixer.metal:272-589; GdnParams kernels.py:686-720) ------------------------------------
  * proj holds the in-projection output of T tokens: z | q | k | v | a | b at the given column offsets (a|b may sit
@@ -204,6 +223,10 @@ typedef struct mi_gdn_desc {
   const uint32_t* done;      /* a step program's mi_step_state.done, or NULL: once it is set the step takes no token —
                                 conv_out and rec_out receive conv_in and rec_in unchanged (so a graph's fixed ping-pong
                                 stays in phase) and y is not written (gdn_mixer.metal:281,330 return at done) */
+  const uint32_t* step;      /* a step program's mi_step_state.step, or NULL. Set: the conv state is two slots
+                                [2][conv_dim][W-1] at conv_in (conv_out = NULL), chosen by the step's parity — read
+                                slot step & 1, write the other (gdn_mixer.metal:25-37's SLOTS = 2); the commit pass
+                                runs after the accept scan advanced step, so it reads slot (step + 1) & 1 */
 } mi_gdn_desc;
 int mi_gdn_step(const mi_gdn_desc* d, void* stream);
 

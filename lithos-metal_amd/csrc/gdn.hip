@@ -41,7 +41,23 @@ struct GdnArgs {
   int commit;               // the speculative commit pass: state only, no read-out
   const int32_t* t_dev;     // device-resident token count (<= t), or null
   const uint32_t* done;     // the step state's stop flag, or null: when set the step takes no token
+  const uint32_t* step;     // the step state's step counter, or null: conv_in is then two slots chosen by parity
+  long long conv_slot;      // elements per conv-state slot
 };
+
+// the conv state this launch reads and writes: the given buffers, or the two slots by the step's parity (the
+// commit pass runs after the accept scan advanced the step: it reads the slot the verify pass read)
+__device__ __forceinline__ void conv_slots(const GdnArgs& a, const uint16_t*& cin, uint16_t*& cout) {
+  if (!a.step) {
+    cin = a.conv_in;
+    cout = a.conv_out;
+    return;
+  }
+  const uint32_t rd = (*a.step + (a.commit ? 1u : 0u)) & 1u;
+  uint16_t* base = const_cast<uint16_t*>(a.conv_in);
+  cin = base + rd * a.conv_slot;
+  cout = base + (rd ^ 1u) * a.conv_slot;
+}
 
 // tokens this launch takes: the device count (commit pass) or t, and none once the program has stopped — with
 // T = 0 the kernel copies conv_in → conv_out and rec_in → rec_out unchanged and writes no read-out
@@ -63,6 +79,9 @@ __global__ __launch_bounds__(64 * (WAVES + CONV_WAVES)) void gdn_step(GdnArgs a)
   const int h = blockIdx.x, sl = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int T = tokens_now(a);
+  const uint16_t* conv_in;
+  uint16_t* conv_out;
+  conv_slots(a, conv_in, conv_out);
   const int rep = a.hv / a.hk;
   const int kh = h / rep;
   const int key_dim = a.hk * DK;
@@ -97,7 +116,7 @@ __global__ __launch_bounds__(64 * (WAVES + CONV_WAVES)) void gdn_step(GdnArgs a)
 #pragma unroll
     for (int j = 0; j < CW; ++j) w[j] = bf(a.conv_w, (long long)ch * CW + j);
 #pragma unroll
-    for (int j = 0; j < CW - 1; ++j) xs[j] = bf(a.conv_in, (long long)ch * (CW - 1) + j);
+    for (int j = 0; j < CW - 1; ++j) xs[j] = bf(conv_in, (long long)ch * (CW - 1) + j);
 #pragma unroll
     for (int t = 0; t < TMAX; ++t) xs[CW - 1 + t] = t < T ? bf(a.proj, (long long)t * a.ldp + src_off) : 0.0f;
 #pragma unroll
@@ -114,7 +133,7 @@ __global__ __launch_bounds__(64 * (WAVES + CONV_WAVES)) void gdn_step(GdnArgs a)
         float v = xs[j];
 #pragma unroll
         for (int t = 1; t <= TMAX; ++t) v = (t == T) ? xs[t + j] : v;
-        a.conv_out[(long long)ch * (CW - 1) + j] = f32_to_bf16_bits(v);
+        conv_out[(long long)ch * (CW - 1) + j] = f32_to_bf16_bits(v);
       }
     }
   }
@@ -207,9 +226,11 @@ extern "C" int mi_gdn_step(const mi_gdn_desc* d, void* stream) {
   MI_REQUIRE(d->t >= 1 && d->t <= TMAX, "mi_gdn_step: t=%d must be in 1..%d", d->t, TMAX);
   MI_REQUIRE(d->dk == DK && d->dv == DV && d->conv_width == CW, "mi_gdn_step: built for dk=dv=%d, conv width %d", DK, CW);
   MI_REQUIRE(d->k_heads > 0 && d->v_heads > 0 && d->v_heads % d->k_heads == 0, "mi_gdn_step: v_heads must be a multiple of k_heads");
-  MI_REQUIRE(d->proj && d->conv_w && d->neg_exp_a && d->dt_bias && d->norm_w && d->conv_in && d->conv_out && d->rec_in &&
-             d->rec_out && (d->y || d->commit), "mi_gdn_step: null pointer");
-  MI_REQUIRE(d->conv_in != d->conv_out, "mi_gdn_step: conv_in and conv_out must be distinct buffers (shared key heads)");
+  MI_REQUIRE(d->proj && d->conv_w && d->neg_exp_a && d->dt_bias && d->norm_w && d->conv_in && (d->conv_out || d->step) &&
+             d->rec_in && d->rec_out && (d->y || d->commit), "mi_gdn_step: null pointer");
+  MI_REQUIRE(d->step ? !d->conv_out : d->conv_in != d->conv_out,
+             "mi_gdn_step: conv_in and conv_out must be distinct buffers (shared key heads); with step, conv_in holds "
+             "both slots and conv_out is NULL");
   MI_REQUIRE(!d->commit || d->rec_in != d->rec_out, "mi_gdn_step: the commit pass replays from the step's input state: "
              "rec_in and rec_out must be distinct");
   GdnArgs a{};
@@ -220,6 +241,8 @@ extern "C" int mi_gdn_step(const mi_gdn_desc* d, void* stream) {
   a.conv_in = d->conv_in; a.conv_out = d->conv_out; a.rec_in = d->rec_in; a.rec_out = d->rec_out;
   a.y = d->y; a.ldy = d->ld_y; a.eps = d->eps;
   a.commit = d->commit; a.t_dev = d->t_dev; a.done = d->done;
+  a.step = d->step;
+  a.conv_slot = (long long)(2 * d->k_heads * d->dk + d->v_heads * d->dv) * (d->conv_width - 1);
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(gdn_step, dim3(d->v_heads, NSLICE), dim3(64 * (WAVES + CONV_WAVES)), 0, s, a);
   MI_TRY_HIP(hipGetLastError(), "gdn_step launch");

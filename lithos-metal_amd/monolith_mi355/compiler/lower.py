@@ -1,0 +1,127 @@
+"""Lower the decode layers built from this package (``layers.py``) to the op graph, bound to their live device memory:
+the reference's layer ``lower`` methods (``nn/linear.py:63-191``, ``nn/gdn.py``, ``nn/attention.py``, ``nn/mlp.py``,
+``nn/decoder.py``) for one token per step.
+
+Weights, norms and states are the layers' own tensors (the program binds them by storage); activations between ops
+are values the program allocates. Layer by layer the ops are the ones ``layers.py`` launches eagerly:
+
+* Gated DeltaNet layer: ``gemv`` in_proj (norm fused) → ``gdn_mixer`` (conv state in two slots by the step's parity,
+  the recurrent state in place; the gated norm deferred to the next GEMV where ``defers_norm``) → ``gemv`` out_proj
+  (+ residual) → the MLP;
+* attention layer: ``gemv`` q|gate|k|v (norm fused) → ``gqa_decode`` at the step state's position → ``gemv`` o_proj
+  (+ residual) → the MLP;
+* MLP: ``gemv`` gate|up (norm fused, silu·mul) → ``gemv`` down (+ residual);
+* the token loop: ``embed`` of the pending token → the layers → ``lm_head`` (final norm fused, BF16 logits) →
+  ``argmax`` → ``advance``.
+"""
+
+from __future__ import annotations
+
+from typing import List
+
+from .ir import Graph, Value, Weight
+
+
+def _dt(t) -> str:
+    import torch
+    return {torch.bfloat16: "bf16", torch.float32: "f32", torch.float16: "f16", torch.int8: "i8", torch.uint8: "u8",
+            torch.int32: "i32"}[t.dtype]
+
+
+def bound(name: str, t, role: str) -> Value:
+    """A value held by the tensor ``t``."""
+    return Value(name, tuple(t.shape), _dt(t), role=role, tensor=t)
+
+
+def weight(name: str, pw) -> Weight:
+    """A packed weight (``kernels.PackedWeight``) as a graph value."""
+    rs = bound(f"{name}.row_scale", pw.row_scale, "weights") if pw.row_scale is not None else None
+    return Weight(name, (pw.nbytes,), "u8", role="weights", tensor=pw.data, format=pw.format, n=pw.n, k=pw.k,
+                  experts=pw.experts, row_scale=rs)
+
+
+def act(name: str, *shape: int, dtype: str = "bf16") -> Value:
+    return Value(name, tuple(shape), dtype)
+
+
+def lower_mlp(g: Graph, mlp, h: Value, prefix: str) -> Value:
+    inter = mlp.inter
+    a = act(f"{prefix}.act", g.t, inter)
+    out = act(f"{prefix}.out", g.t, h.shape[1])
+    g.add("gemv", [h, weight(f"{prefix}.gate_up", mlp.gate_up.packed)], [a], epilogue="silu_mul",
+          norm_w=bound(f"{prefix}.norm", mlp.norm_w, "weights"), eps=mlp.eps, name=f"{prefix}.gate_up")
+    g.add("gemv", [a, weight(f"{prefix}.down", mlp.down.packed)], [out], epilogue="residual", residual=h,
+          name=f"{prefix}.down")
+    return out
+
+
+def lower_gdn_layer(g: Graph, layer, h: Value, prefix: str) -> Value:
+    hidden = layer.hidden
+    proj = act(f"{prefix}.proj", g.t, layer.n_proj)
+    o = act(f"{prefix}.o", g.t, layer.hv * layer.dv)
+    h1 = act(f"{prefix}.h1", g.t, hidden)
+    g.add("gemv", [h, weight(f"{prefix}.in_proj", layer.w_in.packed)], [proj],
+          norm_w=bound(f"{prefix}.norm1", layer.norm_w, "weights"), eps=layer.eps, name=f"{prefix}.in_proj")
+    defer = layer.defers_norm(g.t)
+    norm_w = bound(f"{prefix}.gdn_norm", layer.gdn_norm_w, "weights")
+    g.add("gdn_mixer", [proj, bound(f"{prefix}.conv", layer.conv_state, "state"),
+                        bound(f"{prefix}.rec", layer.rec_state, "state")], [o],
+          k_heads=layer.hk, v_heads=layer.hv, dk=layer.dk, dv=layer.dv, conv_width=layer.conv, eps=layer.eps,
+          defer_norm=defer, conv_w=bound(f"{prefix}.conv_w", layer.conv_w, "weights"),
+          neg_exp_a=bound(f"{prefix}.neg_exp_a", layer.neg_exp_a, "weights"),
+          dt_bias=bound(f"{prefix}.dt_bias", layer.dt_bias, "weights"), norm_w=norm_w, name=f"{prefix}.gdn")
+    gated = None
+    if defer:                                      # z = proj[:, :hv·dv], a view with the projection's row stride
+        z = Value(f"{prefix}.z", (g.t, layer.hv * layer.dv), "bf16", ld=layer.n_proj, base=proj)
+        gated = (norm_w, z, layer.eps)
+    g.add("gemv", [o, weight(f"{prefix}.out_proj", layer.w_out.packed)], [h1], epilogue="residual", residual=h,
+          gated_norm=gated, name=f"{prefix}.out_proj")
+    return lower_mlp(g, layer.mlp, h1, f"{prefix}.mlp")
+
+
+def lower_attn_layer(g: Graph, layer, h: Value, prefix: str) -> Value:
+    c = layer.cache
+    proj = act(f"{prefix}.proj", g.t, layer.n_proj)
+    o = act(f"{prefix}.o", g.t, layer.heads * layer.d)
+    h1 = act(f"{prefix}.h1", g.t, layer.hidden)
+    g.add("gemv", [h, weight(f"{prefix}.qkv", layer.w_qkv.packed)], [proj],
+          norm_w=bound(f"{prefix}.norm1", layer.norm_w, "weights"), eps=layer.eps, name=f"{prefix}.qkv")
+    g.add("gqa_decode", [proj, bound(f"{prefix}.k_codes", c.k_codes, "state"),
+                         bound(f"{prefix}.k_scales", c.k_scales, "state"),
+                         bound(f"{prefix}.v_codes", c.v_codes, "state"),
+                         bound(f"{prefix}.v_scales", c.v_scales, "state"),
+                         bound(f"{prefix}.cos", layer.cos, "weights"), bound(f"{prefix}.sin", layer.sin, "weights"),
+                         bound(f"{prefix}.q_norm", layer.q_norm, "weights"),
+                         bound(f"{prefix}.k_norm", layer.k_norm, "weights")], [o],
+          heads=layer.heads, kv_heads=layer.kv, head_dim=layer.d, ctx_max=c.ctx_max, gate=True, eps=layer.eps,
+          name=f"{prefix}.gqa")
+    g.add("gemv", [o, weight(f"{prefix}.o_proj", layer.w_o.packed)], [h1], epilogue="residual", residual=h,
+          name=f"{prefix}.o_proj")
+    return lower_mlp(g, layer.mlp, h1, f"{prefix}.mlp")
+
+
+def lower_layer(g: Graph, layer, h: Value, prefix: str) -> Value:
+    if getattr(layer, "ping_pong", False):
+        return lower_gdn_layer(g, layer, h, prefix)
+    return lower_attn_layer(g, layer, h, prefix)
+
+
+def lower_decoder(model) -> Graph:
+    """The one-token step of a ``layers.DecoderModel``: embed → layers → final norm + lm_head → argmax → advance."""
+    g = Graph(t=1)
+    vocab, hidden = model.embed_table.shape
+    h = act("h0", 1, hidden)
+    g.add("embed", [bound("embed_table", model.embed_table, "weights")], [h])
+    for i, layer in enumerate(model.layers):
+        h = lower_layer(g, layer, h, f"layers.{i}")
+    logits = act("logits", 1, vocab)
+    ids = act("ids", 16, dtype="i32")
+    g.add("lm_head", [h, weight("lm_head", model.lm_head)], [logits], norm_w=bound("norm", model.norm_w, "weights"),
+          eps=model.eps, bf16=True)
+    g.add("argmax", [logits], [ids])
+    g.add("advance", [ids], [])
+    return g
+
+
+def layer_values(g: Graph) -> List[Value]:
+    return g.values()

@@ -23,10 +23,10 @@ def _torch():
     return torch
 
 
-def _check_flag(flag, name):
+def _check_flag(flag, name, what="done"):
     torch = _torch()
     if flag is not None and (flag.dtype != torch.int32 or flag.numel() != 1 or flag.device.type != "cuda"):
-        raise ValueError(f"{name}: done must be a one-element int32 device tensor (the step state's flag)")
+        raise ValueError(f"{name}: {what} must be a one-element int32 device tensor (a step-state field)")
 
 
 @dataclass
@@ -152,6 +152,43 @@ def gemv_chain(phases, *, workspace=None, stream=None):
     return outs
 
 
+def rmsnorm_stat(h, *, out=None, stream=None):
+    """``rmsnorm_stat`` (``ops/norm.py:11``): ``stat[i] = Σ_k h[i, k]²`` (float32) over BF16 rows."""
+    torch = _torch()
+    _bf16_2d(h, "rmsnorm_stat h")
+    t, k = h.shape
+    if out is None:
+        out = torch.empty(t, dtype=torch.float32, device=h.device)
+    if out.dtype != torch.float32 or out.numel() < t:
+        raise ValueError("rmsnorm_stat: out must be float32 [t]")
+    d = hip.MiNormDesc(t=t, k=k, h=hip.ptr(h), ldh=h.stride(0), stat=hip.ptr(out), stat_parts=1)
+    hip.call("mi_rmsnorm_stat", C.byref(d), hip.stream_handle(stream))
+    return out
+
+
+def norm_apply(h, w, *, stat=None, eps: float = 1e-6, out=None, stream=None):
+    """``norm_apply`` (``ops/norm.py:12``): ``x = bf16(h·rsqrt(s / K + eps)·w)`` with ``w`` the (1 + w) float32
+    weight and ``s`` the row's Σh² — the sum of ``stat [t, parts]``'s partials, or computed here when ``stat`` is
+    None."""
+    torch = _torch()
+    _bf16_2d(h, "norm_apply h")
+    t, k = h.shape
+    if w.dtype != torch.float32 or w.numel() != k or not w.is_contiguous():
+        raise ValueError("norm_apply: w must be a contiguous float32 [K]")
+    parts = 1
+    if stat is not None:
+        if stat.dtype != torch.float32 or stat.shape[0] < t or not stat.is_contiguous():
+            raise ValueError("norm_apply: stat must be a contiguous float32 [t] or [t, parts]")
+        parts = 1 if stat.dim() == 1 else stat.shape[1]
+    if out is None:
+        out = torch.empty(t, k, dtype=torch.bfloat16, device=h.device)
+    _bf16_2d(out, "norm_apply out")
+    d = hip.MiNormDesc(t=t, k=k, h=hip.ptr(h), ldh=h.stride(0), stat=hip.ptr(stat), stat_parts=parts, w=hip.ptr(w),
+                       x=hip.ptr(out), ldx=out.stride(0), eps=eps)
+    hip.call("mi_norm_apply", C.byref(d), hip.stream_handle(stream))
+    return out
+
+
 def dequant(w: PackedWeight, expert: int = 0, stream=None):
     """The packed matrix decoded to float32 ``[N, K]`` by the kernels' own decode (exactness check)."""
     torch = _torch()
@@ -165,7 +202,7 @@ def dequant(w: PackedWeight, expert: int = 0, stream=None):
 
 def gdn_step(proj, conv_in, conv_out, rec_in, rec_out, *, conv_w, neg_exp_a, dt_bias, norm_w, k_heads, v_heads,
              dk=128, dv=128, conv_width=4, eps=1e-6, ab=None, offsets=None, out=None, stream=None,
-             defer_norm: bool = False, commit: bool = False, t_dev=None, done=None):
+             defer_norm: bool = False, commit: bool = False, t_dev=None, done=None, step=None):
     """``gdn_mixer`` + ``gdn_norm`` (``ops/gdn.py:1-24``) for ``proj [T, N1]`` bf16 in part order
     ``z | q | k | v | a | b`` (``nn/gdn.py:48-52``) unless ``offsets`` (z, q, k, v, a, b) says otherwise.
     Conv state ``[conv_dim, W-1]`` bf16 is read from ``conv_in`` and written to ``conv_out`` (distinct); the FP32
@@ -175,7 +212,10 @@ def gdn_step(proj, conv_in, conv_out, rec_in, rec_out, *, conv_w, neg_exp_a, dt_
     (``ops/gdn.py:13-17``): the speculative commit pass re-runs the first ``t_dev`` (device int32, ≤ T; None = all)
     tokens from the step's input state into ``rec_out`` / ``conv_out`` and returns None (no read-out). ``done``: a
     step program's stop flag (one-element device int32 view of the step state): once set, the step takes no token —
-    the states pass through unchanged (``gdn_mixer.metal:281,330`` return at done)."""
+    the states pass through unchanged (``gdn_mixer.metal:281,330`` return at done). ``step``: a step program's step
+    counter (one-element device int32): ``conv_in`` is then both conv-state slots ``[2, conv_dim, W-1]`` and
+    ``conv_out`` is None — the step reads slot ``step & 1`` and writes the other (the reference's two slots by step
+    parity), so one captured step serves every step of a replay."""
     torch = _torch()
     _bf16_2d(proj, "gdn proj", aligned=False)
     t = proj.shape[0]
@@ -184,8 +224,12 @@ def gdn_step(proj, conv_in, conv_out, rec_in, rec_out, *, conv_w, neg_exp_a, dt_
     if offsets is None:
         offsets = (0, vd, vd + kd, vd + 2 * kd, vd + conv_dim, vd + conv_dim + v_heads)
     z_off, q_off, k_off, v_off, a_off, b_off = offsets
-    for name, tns, shape, dt in (("conv_in", conv_in, (conv_dim, conv_width - 1), torch.bfloat16),
-                                 ("conv_out", conv_out, (conv_dim, conv_width - 1), torch.bfloat16),
+    if step is not None and conv_out is not None:
+        raise ValueError("gdn_step: with step, conv_in holds both slots and conv_out is None")
+    conv_shapes = ((("conv_in", conv_in, (2, conv_dim, conv_width - 1), torch.bfloat16),) if step is not None else
+                   (("conv_in", conv_in, (conv_dim, conv_width - 1), torch.bfloat16),
+                    ("conv_out", conv_out, (conv_dim, conv_width - 1), torch.bfloat16)))
+    for name, tns, shape, dt in conv_shapes + (
                                  ("rec_in", rec_in, (v_heads, dk, dv), torch.float32),
                                  ("rec_out", rec_out, (v_heads, dk, dv), torch.float32),
                                  ("conv_w", conv_w, (conv_dim, conv_width), torch.bfloat16),
@@ -200,15 +244,18 @@ def gdn_step(proj, conv_in, conv_out, rec_in, rec_out, *, conv_w, neg_exp_a, dt_
     if t_dev is not None and (t_dev.dtype != torch.int32 or t_dev.numel() != 1):
         raise ValueError("gdn_step: t_dev must be a one-element int32 device tensor")
     _check_flag(done, "gdn_step")
+    _check_flag(step, "gdn_step", "step")
     if out is None and not commit:
         out = torch.empty((t, vd), dtype=torch.bfloat16, device=proj.device)
     d = hip.MiGdnDesc(t=t, k_heads=k_heads, v_heads=v_heads, dk=dk, dv=dv, conv_width=conv_width, proj=hip.ptr(proj),
                       ld_proj=proj.stride(0), z_off=z_off, q_off=q_off, k_off=k_off, v_off=v_off, ab=hip.ptr(ab),
                       ld_ab=ab.stride(0) if ab is not None else 0, a_off=a_off, b_off=b_off, conv_w=hip.ptr(conv_w),
                       neg_exp_a=hip.ptr(neg_exp_a), dt_bias=hip.ptr(dt_bias), norm_w=hip.ptr(norm_w),
-                      conv_in=hip.ptr(conv_in), conv_out=hip.ptr(conv_out), rec_in=hip.ptr(rec_in),
+                      conv_in=hip.ptr(conv_in), conv_out=hip.ptr(conv_out) if conv_out is not None else 0,
+                      rec_in=hip.ptr(rec_in),
                       rec_out=hip.ptr(rec_out), y=hip.ptr(out), ld_y=out.stride(0) if out is not None else 0, eps=eps,
-                      defer_norm=int(defer_norm), commit=int(commit), t_dev=hip.ptr(t_dev), done=hip.ptr(done))
+                      defer_norm=int(defer_norm), commit=int(commit), t_dev=hip.ptr(t_dev), done=hip.ptr(done),
+                      step=hip.ptr(step))
     hip.call("mi_gdn_step", C.byref(d), hip.stream_handle(stream))
     return out
 

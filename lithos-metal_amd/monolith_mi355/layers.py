@@ -122,8 +122,9 @@ class GdnDecoderLayer:
         self.dt_bias = torch.randn(v_heads, generator=gen, device=device).to(torch.bfloat16).float()
         self.gdn_norm_w = (1.0 + torch.randn(dv, generator=gen, device=device) * 0.2).to(torch.bfloat16).float()
         self.mlp = GatedMLP(hidden, inter, gen, device, eps)
-        self.conv_state = [(torch.randn(self.conv_dim, conv - 1, generator=gen, device=device) * 0.5).to(torch.bfloat16),
-                           torch.zeros(self.conv_dim, conv - 1, dtype=torch.bfloat16, device=device)]
+        # both conv-state slots in one tensor [2, conv_dim, W-1]: a step reads one and writes the other
+        self.conv_state = torch.zeros(2, self.conv_dim, conv - 1, dtype=torch.bfloat16, device=device)
+        self.conv_state[0] = (torch.randn(self.conv_dim, conv - 1, generator=gen, device=device) * 0.5).to(torch.bfloat16)
         self.rec_state = torch.randn(v_heads, dk, dv, generator=gen, device=device) * 0.1
         self.rec_slots = [self.rec_state, None]    # the second recurrent-state slot of a speculative verify pass
         self.slot = 0

@@ -15,8 +15,9 @@ def _op(name, klass, domain, kernel=None, **consts):
 
 GEMV = _op("gemv", OpClass.MAP, "rows", "mi_gemv")
 LM_HEAD = _op("lm_head", OpClass.MAP, "rows", "mi_gemv", out_f32=1)
-RMSNORM_STAT = _op("rmsnorm_stat", OpClass.REDUCE, "span", "mi_gemv", fused_into="gemv")
-NORM_APPLY = _op("norm_apply", OpClass.MAP, "span", "mi_gemv", fused_into="gemv")
+# standalone kernels; a norm that feeds a GEMV is fused into its load instead (mi_gemv_desc.norm_w)
+RMSNORM_STAT = _op("rmsnorm_stat", OpClass.REDUCE, "span", "mi_rmsnorm_stat")
+NORM_APPLY = _op("norm_apply", OpClass.MAP, "span", "mi_norm_apply")
 GQA_DECODE = _op("gqa_decode", OpClass.MAP, "heads", "mi_gqa_decode")
 GQA_MERGE = _op("gqa_merge", OpClass.MAP, "heads", "mi_gqa_decode", fused_into="gqa_decode")
 GDN_MIXER = _op("gdn_mixer", OpClass.MAP, "heads", "mi_gdn_step")

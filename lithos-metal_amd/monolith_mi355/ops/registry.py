@@ -30,15 +30,15 @@ T = TypeVar("T")
 
 
 class Registry(Generic[T]):
-    """Name → item, registered once (``monolith/registry.py``)."""
+    """A name table whose entries cannot be replaced by a different object (``monolith/registry.py``)."""
 
     def __init__(self, what: str) -> None:
         self.what = what
         self._items: Dict[str, T] = {}
 
     def register(self, name: str, item: T) -> T:
-        if name in self._items and self._items[name] is not item:
-            raise ValueError(f"{self.what} {name!r} is already registered")
+        if self._items.get(name, item) is not item:
+            raise ValueError(f"{name!r}: another {self.what} holds this name")
         self._items[name] = item
         return item
 
@@ -62,7 +62,8 @@ class Registry(Generic[T]):
 
 @dataclass(frozen=True)
 class KernelBinding:
-    """Which entry point implements an op on a profile, with its fixed parameters and workgroups per CU."""
+    """The implementation of an op on one profile: the libmi355 entry point, the descriptor fields it fixes, and
+    how many of its workgroups the planner expects per CU."""
 
     kernel: str
     function_constants: Mapping[str, Any] = field(default_factory=dict)
@@ -71,7 +72,7 @@ class KernelBinding:
 
 @dataclass(frozen=True)
 class CostModel:
-    """Per-block cost the planner reasons with (bytes streamed, ALU work, ALU-bound flag)."""
+    """What one block of the op's domain costs: bytes it streams, arithmetic it does, which of the two bounds it."""
 
     bytes_per_block: int = 0
     flops_per_block: int = 0
@@ -80,7 +81,8 @@ class CostModel:
 
 @dataclass
 class OpDef:
-    """An op kind: its class, the kind of block domain it partitions over, its cost, and its kernel bindings."""
+    """One op kind of the IR: how its blocks combine (``klass``), what its domain is split into, its cost, and the
+    per-profile implementations (``"*"`` binds every profile)."""
 
     name: str
     klass: OpClass
@@ -92,8 +94,9 @@ class OpDef:
         return self.kernels.get(profile_key) or self.kernels.get(WILDCARD)
 
     def bind(self, profile_key: str, binding: KernelBinding) -> "OpDef":
-        if profile_key in self.kernels and self.kernels[profile_key] != binding:
-            raise ValueError(f"op {self.name}: profile {profile_key!r} already bound to {self.kernels[profile_key]}")
+        held = self.kernels.get(profile_key)
+        if held is not None and held != binding:
+            raise ValueError(f"{self.name} on {profile_key}: bound to {held.kernel} already, not to {binding.kernel}")
         self.kernels[profile_key] = binding
         return self
 

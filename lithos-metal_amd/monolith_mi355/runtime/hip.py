@@ -45,7 +45,7 @@ class MiGdnDesc(C.Structure):
                 ("neg_exp_a", C.c_void_p), ("dt_bias", C.c_void_p), ("norm_w", C.c_void_p), ("conv_in", C.c_void_p),
                 ("conv_out", C.c_void_p), ("rec_in", C.c_void_p), ("rec_out", C.c_void_p), ("y", C.c_void_p),
                 ("ld_y", C.c_int32), ("eps", C.c_float), ("defer_norm", C.c_int32), ("commit", C.c_int32),
-                ("t_dev", C.c_void_p), ("done", C.c_void_p)]
+                ("t_dev", C.c_void_p), ("done", C.c_void_p), ("step", C.c_void_p)]
 
 
 class MiGqaDesc(C.Structure):
@@ -57,6 +57,12 @@ class MiGqaDesc(C.Structure):
                 ("v_scales", C.c_void_p), ("y", C.c_void_p), ("ld_y", C.c_int32), ("workspace", C.c_void_p),
                 ("workspace_bytes", C.c_size_t), ("pos_dev", C.c_void_p),
                 ("done", C.c_void_p)]
+
+
+class MiNormDesc(C.Structure):
+    _fields_ = [("t", C.c_int32), ("k", C.c_int32), ("h", C.c_void_p), ("ldh", C.c_int32), ("stat", C.c_void_p),
+                ("stat_parts", C.c_int32), ("w", C.c_void_p), ("x", C.c_void_p), ("ldx", C.c_int32),
+                ("eps", C.c_float)]
 
 
 class MiMoeRouteDesc(C.Structure):
@@ -174,6 +180,8 @@ SIGNATURES = {
     "mi_gemv_plan": (C.c_int, [C.POINTER(MiGemvDesc), C.POINTER(_I32)]),
     "mi_dequant": (C.c_int, [_I32, _VP, _VP, _I32, _I32, _VP, _VP]),
     "mi_gdn_step": (C.c_int, [C.POINTER(MiGdnDesc), _VP]),
+    "mi_rmsnorm_stat": (C.c_int, [C.POINTER(MiNormDesc), _VP]),
+    "mi_norm_apply": (C.c_int, [C.POINTER(MiNormDesc), _VP]),
     "mi_gqa_workspace_bytes": (_SZ, [C.POINTER(MiGqaDesc)]),
     "mi_gqa_decode": (C.c_int, [C.POINTER(MiGqaDesc), _VP]),
     "mi_moe_route": (C.c_int, [C.POINTER(MiMoeRouteDesc), _VP]),

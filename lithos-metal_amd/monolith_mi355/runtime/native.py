@@ -88,6 +88,15 @@ class Buffer:
         hip.call("mi_buf_from_file", os.fsencode(path), int(offset), int(nbytes), C.byref(b._p))
         return b
 
+    @classmethod
+    def view(cls, device: Device, address: int, nbytes: int, owner=None) -> "Buffer":
+        """Device memory this object does not own — a window of an allocation made elsewhere (a torch tensor's
+        storage, another buffer); ``owner`` is kept alive as long as the view."""
+        b = cls.__new__(cls)
+        b.device, b._n, b._p = device, int(nbytes), C.c_void_p(int(address))
+        b._owner, b._borrowed = owner, True
+        return b
+
     @property
     def nbytes(self) -> int:
         return self._n
@@ -117,6 +126,8 @@ class Buffer:
 
     def __del__(self):
         try:
+            if getattr(self, "_borrowed", False):
+                return
             if getattr(self, "_p", None) and self._p.value and hip._lib is not None:
                 hip._lib.mi_free(self._p)
                 self._p = C.c_void_p()

@@ -12,7 +12,7 @@ from __future__ import annotations
 
 import json
 import struct
-from dataclasses import dataclass, field
+from dataclasses import dataclass, field, fields
 from pathlib import Path
 from typing import Dict, List, Mapping, Optional, Sequence, Tuple
 
@@ -84,8 +84,8 @@ class StepStateLayout:
 
 @dataclass
 class KernelSpec:
-    source: str                          # HIP C++ (extern "C" __global__ kernels)
-    function: str
+    source: str                          # HIP C++ (extern "C" __global__ kernels); "" for a library kernel
+    function: str                        # kernel name, or "lib:<entry point>" — a typed entry point of libmi355
     macros: Dict[str, str] = field(default_factory=dict)
     language_version: int = 0            # carried for the format; HIP sources compile as C++17
 
@@ -111,6 +111,48 @@ class OpSpec:
     meta: Dict[str, object] = field(default_factory=dict)
 
 
+# ---- program.json v1 --------------------------------------------------------------------------------------------------
+# Each spec class serializes field by field; a codec entry renames a field in the file and/or converts its value
+# (name in the file, to_json, from_json). Fields without an entry are written as they are. The key names and value
+# forms are the v1 format's, so files written by either side load on the other.
+def _hex_in(v):
+    return bytes.fromhex(v) if v else None
+
+
+def _tuples(v):
+    return [tuple(x) for x in v]
+
+
+_CODECS = {
+    KernelSpec: {"macros": ("macros", dict, dict), "language_version": ("language_version", int, int)},
+    BufferSpec: {"init": ("init_hex", lambda b: b.hex() if b is not None else None, _hex_in),
+                 "file_offset": ("file_offset", int, int)},
+    OpSpec: {"bindings": ("bindings", _tuples, _tuples), "grid": ("grid", tuple, tuple),
+             "threadgroup": ("threadgroup", tuple, tuple), "threadgroup_memory": ("threadgroup_memory", _tuples, _tuples),
+             "meta": ("meta", dict, dict)},
+}
+
+
+def _encode(spec) -> dict:
+    codec = _CODECS.get(type(spec), {})
+    out = {}
+    for f in fields(spec):
+        key, to_json, _ = codec.get(f.name, (f.name, None, None))
+        v = getattr(spec, f.name)
+        out[key] = to_json(v) if to_json is not None else v
+    return out
+
+
+def _decode(cls, d: Mapping[str, object]):
+    codec = _CODECS.get(cls, {})
+    kw = {}
+    for f in fields(cls):
+        key, _, from_json = codec.get(f.name, (f.name, None, None))
+        if key in d:
+            kw[f.name] = from_json(d[key]) if from_json is not None else d[key]
+    return cls(**kw)
+
+
 @dataclass
 class Program:
     kernels: Dict[str, KernelSpec]
@@ -124,40 +166,34 @@ class Program:
     backend_id: str = "common"
     config_digest: str = ""
 
+    _SCALARS = ("step_state", "ring", "ring_capacity", "context_capacity", "backend_id", "config_digest")
+
+    def to_dict(self) -> dict:
+        d = {"version": 1}
+        d.update({k: getattr(self, k) for k in self._SCALARS})
+        d["layout"] = {"t_max": self.layout.t_max, "gamma_max": self.layout.gamma_max}
+        d["kernels"] = {name: _encode(k) for name, k in self.kernels.items()}
+        d["buffers"] = {name: _encode(b) for name, b in self.buffers.items()}
+        d["ops"] = [_encode(o) for o in self.ops]
+        return d
+
     def to_json(self) -> str:
-        d = {"version": 1, "step_state": self.step_state, "ring": self.ring, "ring_capacity": self.ring_capacity,
-             "context_capacity": self.context_capacity, "backend_id": self.backend_id,
-             "config_digest": self.config_digest,
-             "layout": {"t_max": self.layout.t_max, "gamma_max": self.layout.gamma_max},
-             "kernels": {k: {"function": v.function, "macros": v.macros, "source": v.source,
-                             "language_version": v.language_version} for k, v in self.kernels.items()},
-             "buffers": {k: {"nbytes": v.nbytes, "role": v.role,
-                             "init_hex": v.init.hex() if v.init is not None else None,
-                             "file": v.file, "file_offset": v.file_offset} for k, v in self.buffers.items()},
-             "ops": [{"kernel": o.kernel, "bindings": o.bindings, "grid": o.grid, "threadgroup": o.threadgroup,
-                      "barrier_before": o.barrier_before, "threadgroup_memory": o.threadgroup_memory,
-                      "name": o.name, "meta": o.meta} for o in self.ops]}
-        return json.dumps(d, indent=1)
+        return json.dumps(self.to_dict(), indent=1)
+
+    @classmethod
+    def from_dict(cls, d: Mapping[str, object]) -> "Program":
+        if d.get("version") != 1:
+            raise ValueError(f"program.json version {d.get('version')!r}: this runtime reads version 1")
+        lay = d["layout"]
+        extra = {k: d[k] for k in cls._SCALARS if k in d}
+        return cls(kernels={n: _decode(KernelSpec, v) for n, v in d["kernels"].items()},
+                   buffers={n: _decode(BufferSpec, v) for n, v in d["buffers"].items()},
+                   ops=[_decode(OpSpec, o) for o in d["ops"]],
+                   layout=StepStateLayout(int(lay["t_max"]), int(lay["gamma_max"])), **extra)
 
     @classmethod
     def from_json(cls, text: str) -> "Program":
-        d = json.loads(text)
-        if d.get("version") != 1:
-            raise ValueError("unsupported program version")
-        return cls(
-            kernels={k: KernelSpec(v["source"], v["function"], dict(v.get("macros", {})),
-                                   int(v.get("language_version", 0))) for k, v in d["kernels"].items()},
-            buffers={k: BufferSpec(v["nbytes"], bytes.fromhex(v["init_hex"]) if v.get("init_hex") else None,
-                                   v.get("role", "arena"), v.get("file"), int(v.get("file_offset", 0)))
-                     for k, v in d["buffers"].items()},
-            ops=[OpSpec(o["kernel"], [tuple(b) for b in o["bindings"]], tuple(o["grid"]), tuple(o["threadgroup"]),
-                        o.get("barrier_before", o.get("barrier_after", True)),
-                        [tuple(t) for t in o.get("threadgroup_memory", [])], o.get("name", ""),
-                        dict(o.get("meta", {}))) for o in d["ops"]],
-            step_state=d["step_state"], ring=d["ring"], ring_capacity=d["ring_capacity"],
-            context_capacity=int(d.get("context_capacity", 0)),
-            layout=StepStateLayout(d["layout"]["t_max"], d["layout"]["gamma_max"]),
-            backend_id=d.get("backend_id", "common"), config_digest=d.get("config_digest", ""))
+        return cls.from_dict(json.loads(text))
 
     def save(self, path) -> None:
         Path(path).write_text(self.to_json())

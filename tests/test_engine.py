@@ -179,33 +179,6 @@ def test_profile_gives_per_op_gpu_times(torch_gpu):
     assert len(runs) == 3 and all(len(r) == 2 for r in runs)
     for (s0, e0), (s1, e1) in runs:
         assert 0 <= s0 <= e0 <= s1 + 1e-3 and s1 <= e1 and e1 - s0 < 5.0 and e0 > s0
-    import json
-    import tempfile
-
-    from monolith_mi355.runtime.trace import format_budget, op_timings, write_chrome_trace
-    t = op_timings(eng.program, runs)
-    assert [x.name for x in t] == ["map", "advance"] and all(x.ms_min > 0 for x in t)
-    assert "total" in format_budget(t, 8000.0)
-    with tempfile.NamedTemporaryFile(suffix=".json") as f:
-        write_chrome_trace(f.name, eng.program, runs)
-        ev = json.load(open(f.name))["traceEvents"]
-        assert len(ev) == 6 and ev[0]["ph"] == "X" and ev[0]["name"] == "map"
-
-
-def test_op_timings_fold_per_t_variants():
-    """Predicated per-T variants of one op count once: durations add, bytes once; the budget sorts by time."""
-    from monolith_mi355.runtime.trace import budget, format_budget, op_timings
-    p = _program(5)
-    v = OpSpec("toy", [], (1, 1, 1), (64, 1, 1), name="gemv:q", meta={"t_range": [1, 1], "kind": "gemv", "bytes": 2000})
-    w = OpSpec("toy", [], (1, 1, 1), (64, 1, 1), name="gemv:q", meta={"t_range": [2, 8], "kind": "gemv", "bytes": 2000})
-    p.ops = [v, w, p.ops[1]]
-    runs = [[(0.0, 0.010), (0.010, 0.011), (0.011, 0.020)], [(0.0, 0.004), (0.004, 0.005), (0.005, 0.010)]]
-    t = op_timings(p, runs)
-    assert [x.name for x in t] == ["gemv:q", "advance"]
-    assert abs(t[0].ms_min - 0.005) < 1e-12 and abs(t[0].ms_median - 0.011) < 1e-12 and t[0].bytes == 2000
-    assert abs(t[0].gbps - 2000 / (0.005 * 1e6)) < 1e-9 and t[1].gbps is None
-    assert [r[0] for r in budget(t)] == ["gemv", "advance"]
-    assert "bandwidth bound" in format_budget(t, 1000.0)
 
 
 @pytest.mark.gpu

@@ -182,3 +182,34 @@ def test_gdn_commit_needs_two_slots(torch_gpu):
     c0, c1 = torch.zeros(conv_dim, 3, dtype=torch.bfloat16, device="cuda"), torch.zeros(conv_dim, 3, dtype=torch.bfloat16, device="cuda")
     with pytest.raises(ValueError):
         kernels.gdn_step(proj, c0, c1, rec, rec, k_heads=hk, v_heads=hv, commit=True, **dp)
+
+
+def test_gdn_conv_slots_by_step_parity(torch_gpu):
+    """With the step counter (``step``): one call shape serves every step — the conv window is read from slot
+    ``step & 1`` of ``[2, conv_dim, 3]`` and written to the other. Three steps with the counter advanced on the device
+    equal the same steps with the slots named explicitly, bit for bit (outputs, both slots, recurrent state)."""
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    hk, hv, t = 4, 8, 1
+    rng = np.random.default_rng(77)
+    p = _params(rng, hk, hv)
+    dp = _dev_params(torch, p)
+    conv_dim = 2 * hk * 128 + hv * 128
+    n1 = hv * 128 + conv_dim + 2 * hv
+    conv = rbf(rng.standard_normal((conv_dim, 3)) * 0.5)
+    rec = (rng.standard_normal((hv, 128, 128)) * 0.1).astype(np.float32)
+    slots = torch.zeros(2, conv_dim, 3, dtype=torch.bfloat16, device="cuda")
+    slots[0] = to_dev_bf16(torch, conv)
+    explicit = slots.clone()
+    rec_a, rec_b = torch.from_numpy(rec).cuda(), torch.from_numpy(rec).cuda()
+    step = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for s in range(3):
+        pd = to_dev_bf16(torch, rbf(rng.standard_normal((t, n1))))
+        ya = kernels.gdn_step(pd, slots, None, rec_a, rec_a, k_heads=hk, v_heads=hv, eps=EPS, step=step, **dp)
+        yb = kernels.gdn_step(pd, explicit[s & 1], explicit[(s + 1) & 1], rec_b, rec_b, k_heads=hk, v_heads=hv,
+                              eps=EPS, **dp)
+        step += 1
+        torch.cuda.synchronize()
+        assert torch.equal(ya, yb) and torch.equal(slots, explicit) and torch.equal(rec_a, rec_b), s
+    with pytest.raises(ValueError, match="conv_out is None"):
+        kernels.gdn_step(pd, slots, explicit[0], rec_a, rec_a, k_heads=hk, v_heads=hv, eps=EPS, step=step, **dp)

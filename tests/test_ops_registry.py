@@ -46,57 +46,3 @@ def test_coverage_reports_missing():
     with pytest.raises(CoverageError) as e:
         check_coverage(["gemv", name, "no_such_op"])
     assert f"{name} (no binding)" in str(e.value) and "no_such_op (unknown op)" in str(e.value)
-
-
-def test_run_refuses_fused_and_unbound_ops():
-    from monolith_mi355.ops import CoverageError, run
-    with pytest.raises(CoverageError):
-        run("norm_apply")
-    with pytest.raises(CoverageError):
-        run(_unbound())
-
-
-@pytest.mark.gpu
-def test_run_gemv_matches_kernel_call(torch_gpu):
-    import numpy as np
-    from helpers import spec_of, to_dev_bf16
-    from oracle import formats as OF
-    from monolith_mi355 import kernels
-    from monolith_mi355.ops import run
-    rng = np.random.default_rng(5)
-    m = OF.nvfp4_random(64, 512, rng)
-    w = kernels.upload(spec_of(m))
-    x = to_dev_bf16(torch_gpu, rng.standard_normal((1, 512)))
-    a = run("gemv", x, w).view(torch_gpu.int16)
-    b = kernels.gemv(w, x).view(torch_gpu.int16)
-    assert torch_gpu.equal(a, b)
-
-
-@pytest.mark.gpu
-def test_run_gdn_commit_matches_kernel_call(torch_gpu):
-    """``gdn_commit`` through the op registry: the same state as the kernel's commit pass."""
-    import numpy as np
-    import torch
-    from monolith_mi355 import kernels
-    from monolith_mi355.ops import run
-    hk, hv = 2, 4
-    conv_dim = 2 * hk * 128 + hv * 128
-    g = torch.Generator(device="cuda").manual_seed(3)
-    proj = (torch.randn(4, hv * 128 + conv_dim + 2 * hv, generator=g, device="cuda")).to(torch.bfloat16)
-    prm = dict(conv_w=(torch.randn(conv_dim, 4, generator=g, device="cuda") * 0.3).to(torch.bfloat16),
-               neg_exp_a=-torch.ones(hv, device="cuda"), dt_bias=torch.zeros(hv, device="cuda"),
-               norm_w=torch.ones(128, device="cuda"), k_heads=hk, v_heads=hv)
-    conv_a = (torch.randn(conv_dim, 3, generator=g, device="cuda")).to(torch.bfloat16)
-    rec_a = torch.randn(hv, 128, 128, generator=g, device="cuda") * 0.1
-    n = torch.tensor([2], dtype=torch.int32, device="cuda")
-    outs = []
-    for via_run in (False, True):
-        conv_b = torch.zeros_like(conv_a)
-        rec_b = torch.zeros_like(rec_a)
-        if via_run:
-            run("gdn_commit", proj, conv_a, conv_b, rec_a, rec_b, committed=n, **prm)
-        else:
-            kernels.gdn_step(proj, conv_a, conv_b, rec_a, rec_b, commit=True, t_dev=n, **prm)
-        torch.cuda.synchronize()
-        outs.append((conv_b.cpu(), rec_b.cpu()))
-    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
