@@ -19,8 +19,14 @@ cannot serve them — like consecutive layers of one model. The timed steps are 
 not in the number), bracketed by HIP events on the stream they run on. Synthetic data: weights N(0, 0.02) quantized
 with the reference NVFP4 rule on the GPU, activations N(0, 1) BF16, GDN state N(0, 0.1), KV codes uniform int8.
 
+Per-config lines beside the layer: configs[0] (INT4 4096², M = 1, rotated over ≥ 2 GiB of copies), each
+configs[1] GEMV alone (gate|up, down; M = 1 and 8), the configs[2] attention core alone at 4K / 16K / 32K (M = 1
+and 8, ≥ 2 GiB of KV caches rotated) and the configs[3] Gated DeltaNet step alone (M = 1 and 8, ≥ 2 GiB of states
+rotated).
+
 Prints ONE JSON line. ``roofline`` is for the dominant kernel (the gate|up GEMV, 34816×5120 NVFP4 at M = 1) timed
-alone the same way; ``cpu_baseline`` times the C/OpenMP restatement of the reference's CPU oracle GEMV on the host.
+alone the same way; ``cpu_baseline`` times the reference's CPU path for the same layer on the host (numpy and the
+C/OpenMP restatement of its oracle GEMV, M = 1 and 8) and configs[0] on one core.
 """
 
 from __future__ import annotations
@@ -44,9 +50,9 @@ def parse():
     p.add_argument("--steps", type=int, default=100)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--layers", type=int, default=10, help="distinct layer instances the steps rotate over")
-    p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--cpu-seconds", type=float, default=20.0)
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--only", choices=["gdn", "attn", "mlp", "gateup", "fp8", "int4", "moe", "loop", "copy"], default=None,
+    p.add_argument("--only", choices=["gdn", "attn", "mlp", "gateup", "gemv", "fp8", "int4", "gqa", "gdnstep", "moe", "loop", "copy"], default=None,
                    help="time one workload only (profiling runs; copy = a 256 MiB device copy, the counter reference)")
     return p.parse_args()
 
@@ -125,6 +131,19 @@ def main():
             ms = timed_graph(lambda i: kernels.gemv(gdn[i % n].mlp.gate_up.packed, x, epilogue="silu_mul", out=act),
                              args.steps, args.warmup, stream)
             out["gateup_m1"] = (ms, 34816 * 5120 * 9 // 16 + 5120 * 2 + 17408 * 2)
+        if args.only in (None, "gemv"):
+            # each MLP GEMV alone — gate|up (silu·mul) and down (+ residual) at M = 1 and 8
+            for m in (1, 8):
+                x, xa = xin(m), torch.randn(m, 17408, generator=gen, device=dev).to(torch.bfloat16)
+                act = torch.empty(m, 17408, dtype=torch.bfloat16, device=dev)
+                y = torch.empty(m, 5120, dtype=torch.bfloat16, device=dev)
+                if m > 1:
+                    ms = timed_graph(lambda i: kernels.gemv(gdn[i % n].mlp.gate_up.packed, x, epilogue="silu_mul",
+                                                            out=act), args.steps, args.warmup, stream)
+                    out[f"gateup_m{m}"] = (ms, 34816 * 5120 * 9 // 16 + m * 5120 * 2 + m * 17408 * 2)
+                ms = timed_graph(lambda i: kernels.gemv(gdn[i % n].mlp.down.packed, xa, epilogue="residual", residual=x,
+                                                        out=y), args.steps, args.warmup, stream)
+                out[f"down_m{m}"] = (ms, 5120 * 17408 * 9 // 16 + m * 17408 * 2 + 2 * m * 5120 * 2)
         del gdn
         torch.cuda.empty_cache()
         if args.only in (None, "fp8"):
@@ -147,25 +166,90 @@ def main():
                 out[f"fp8_m{m}"] = (ms, nb + m * k8 * 2 + m * n8 * 2)
             del mats
         if args.only in (None, "int4"):
-            # affine 4-bit (MLX rule, group 64, BF16 scale + bias): configs[0] (4096², M = 1) and the 27B gate|up
-            # shape with silu·mul (M = 1 and 8). Packed bytes filled with one finite pattern (codes 4/2/12/3,
-            # scale = bias = bf16 0.0103): the stream and the arithmetic are the real ones, the values are not
-            lib = hip.load()
-            for tag, n4, k4, ms_ in (("int4_4096", 4096, 4096, (1,)), ("int4_gateup", 34816, 5120, (1, 8))):
-                nbytes = lib.mi_pack_bytes(hip.MI_FMT["int4_affine"], n4, k4)
-                mats = [kernels.PackedWeight("int4_affine", n4, k4, 1,
-                                             torch.full((nbytes // 2,), 0x3C24, dtype=torch.int16, device=dev)
-                                             .view(torch.uint8), None)
-                        for _ in range(n if n4 * k4 > 1 << 26 else 1)]
-                epi = "silu_mul" if tag == "int4_gateup" else None
-                n_out = n4 // 2 if epi else n4
-                for m in ms_:
-                    x = torch.randn(m, k4, generator=gen, device=dev).to(torch.bfloat16)
-                    y4 = torch.empty(m, n_out, dtype=torch.bfloat16, device=dev)
-                    ms = timed_graph(lambda i: kernels.gemv(mats[i % len(mats)], x, epilogue=epi, out=y4),
-                                     args.steps, args.warmup, stream)
-                    out[f"{tag}_m{m}"] = (ms, n4 * k4 * 9 // 16 + m * k4 * 2 + m * n_out * 2)
-                del mats
+            # affine 4-bit (MLX rule, group 64, BF16 scale + bias), weights N(0, 0.02) quantized by the product's
+            # quantizer: configs[0] (4096², M = 1) rotated over ≥ 2 GiB of distinct device copies (one per launch of
+            # the timed graph, so the 256 MB MALL holds none of them), and the 27B gate|up shape with silu·mul
+            # (M = 1 and 8; 512 quantized rows repeated down the matrix, ten device copies)
+            from monolith_mi355.formats import DequantSpec, INT4Affine
+            import numpy as np
+            rng = np.random.default_rng(1)
+
+            def int4_matrix(n4, k4, block=512):
+                q = INT4Affine().quantize(rng.standard_normal((min(block, n4), k4)).astype(np.float32) * 0.02)
+                reps = -(-n4 // q.tensors["weight"].shape[0])
+                t = {k_: np.tile(v, (reps, 1))[:n4].copy() for k_, v in q.tensors.items()}
+                return kernels.upload(DequantSpec("int4_affine", (n4, k4), t, dict(q.params)), device=dev)
+
+            c1 = int4_matrix(4096, 4096, block=4096)
+            c1_copies = -(-(2 << 30) // c1.nbytes)
+            mats = [c1] + [kernels.PackedWeight("int4_affine", 4096, 4096, 1, c1.data.clone(), None)
+                           for _ in range(c1_copies - 1)]
+            x = torch.randn(1, 4096, generator=gen, device=dev).to(torch.bfloat16)
+            y4 = torch.empty(1, 4096, dtype=torch.bfloat16, device=dev)
+            ms = timed_graph(lambda i: kernels.gemv(mats[i % len(mats)], x, out=y4), max(args.steps, len(mats)),
+                             args.warmup, stream)
+            out["int4_4096_m1"] = (ms, 4096 * 4096 * 9 // 16 + 4096 * 2 + 4096 * 2)
+            c1_info = {"copies_rotated": len(mats), "bytes_rotated": len(mats) * c1.nbytes}
+            del mats, c1
+            gu = int4_matrix(34816, 5120)
+            mats = [gu] + [kernels.PackedWeight("int4_affine", 34816, 5120, 1, gu.data.clone(), None)
+                           for _ in range(n - 1)]
+            for m in (1, 8):
+                x = torch.randn(m, 5120, generator=gen, device=dev).to(torch.bfloat16)
+                y4 = torch.empty(m, 17408, dtype=torch.bfloat16, device=dev)
+                ms = timed_graph(lambda i: kernels.gemv(mats[i % len(mats)], x, epilogue="silu_mul", out=y4),
+                                 args.steps, args.warmup, stream)
+                out[f"int4_gateup_m{m}"] = (ms, 34816 * 5120 * 9 // 16 + m * 5120 * 2 + m * 17408 * 2)
+            del mats, gu
+        if args.only in (None, "gqa"):
+            # the attention core alone (q/k norm, RoPE, int8 append, attention, gate) at 4K / 16K / 32K,
+            # M = 1 and 8, rotated over ≥ 2 GiB of distinct KV caches (one per launch of the timed graph)
+            from monolith_mi355.kernels import KVCache
+            cos, sin = kernels.rope_tables(1e6, 64, CTX, device=dev)
+            qn = 1.0 + torch.randn(128, generator=gen, device=dev) * 0.1
+            kn = 1.0 + torch.randn(128, generator=gen, device=dev) * 0.1
+            for ctx in (4096, 16384, 32768):
+                per = ctx * 4 * (2 * 128 + 4)
+                caches = [KVCache(4, ctx, 128, device=dev) for _ in range(-(-(2 << 30) // per))]
+                for c in caches:
+                    c.k_codes.random_(-127, 128, generator=gen)
+                    c.v_codes.random_(-127, 128, generator=gen)
+                    c.k_scales.fill_(3.0 / 127)
+                    c.v_scales.fill_(3.0 / 127)
+                for m in (1, 8):
+                    pos = ctx - 16
+                    proj = torch.randn(m, 7168, generator=gen, device=dev).to(torch.bfloat16)
+                    o = torch.empty(m, 3072, dtype=torch.bfloat16, device=dev)
+                    ms = timed_graph(lambda i: kernels.gqa_decode(proj, caches[i % len(caches)], pos, heads=24,
+                                                                  rope_cos=cos, rope_sin=sin, q_norm=qn, k_norm=kn,
+                                                                  out=o), len(caches), args.warmup, stream)
+                    nkv = pos + m
+                    out[f"gqa_{ctx // 1024}k_m{m}"] = (ms, nkv * 4 * (2 * 128 + 4) + m * 7168 * 2 + m * 3072 * 2
+                                                       + m * 4 * (2 * 128 + 4))
+                del caches
+                torch.cuda.empty_cache()
+        if args.only in (None, "gdnstep"):
+            # the Gated DeltaNet step alone (conv, gates, delta rule, gated norm; output bf16) at M = 1
+            # and 8, rotated over ≥ 2 GiB of distinct recurrent states (one per launch of the timed graph)
+            hk, hv, d = 16, 48, 128
+            conv_dim, n1 = 2 * hk * d + hv * d, hv * d + 2 * hk * d + hv * d + 2 * hv
+            per = hv * d * d * 4
+            count = -(-(2 << 30) // per)
+            recs = torch.randn(count, hv, d, d, generator=gen, device=dev) * 0.1
+            convs = (torch.randn(count, 2, conv_dim, 3, generator=gen, device=dev) * 0.5).to(torch.bfloat16)
+            prm = dict(conv_w=(torch.randn(conv_dim, 4, generator=gen, device=dev) * 0.3).to(torch.bfloat16),
+                       neg_exp_a=-torch.ones(hv, device=dev), dt_bias=torch.zeros(hv, device=dev),
+                       norm_w=1.0 + torch.randn(d, generator=gen, device=dev) * 0.2)
+            for m in (1, 8):
+                proj = torch.randn(m, n1, generator=gen, device=dev).to(torch.bfloat16)
+                y = torch.empty(m, hv * d, dtype=torch.bfloat16, device=dev)
+                ms = timed_graph(lambda i: kernels.gdn_step(proj, convs[i % count, 0], convs[i % count, 1],
+                                                            recs[i % count], recs[i % count], k_heads=hk, v_heads=hv,
+                                                            out=y, **prm), count, args.warmup, stream)
+                out[f"gdnstep_m{m}"] = (ms, 2 * per + 2 * conv_dim * 3 * 2 + conv_dim * 4 * 2 + 3 * hv * 4 + d * 4
+                                        + m * n1 * 2 + m * hv * d * 2)
+            del recs, convs
+            torch.cuda.empty_cache()
         if args.only in (None, "attn"):
             attn = [AttnDecoderLayer(seed=40 + i, ctx=CTX, device=dev) for i in range(n)]
             for layer in attn:
@@ -250,7 +334,8 @@ def main():
     prof = ROOT / "profiles" / "gemv_nvfp4_gateup_m1_traffic.json"
     if prof.exists():
         traffic = json.loads(prof.read_text()).get("hbm_bytes_per_launch")
-    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds, b1_bytes=out["gdn_m1"][1],
+                                                  b8_bytes=out["gdn_m8"][1])
 
     def entry(key, m):
         ms, b, gbs = rate(key)
@@ -286,7 +371,19 @@ def main():
         "mlp_m8": entry("mlp_m8", 8),
         "fp8_in_proj_m1": entry("fp8_m1", 1),
         "fp8_in_proj_m8": entry("fp8_m8", 8),
-        "int4_gemv_4096_m1": dict(entry("int4_4096_m1", 1), workload="configs[0]: affine 4-bit GEMV 4096x4096, M=1"),
+        "int4_gemv_4096_m1": dict(entry("int4_4096_m1", 1), **c1_info,
+                                  workload="configs[0]: affine 4-bit GEMV 4096x4096, M=1, N(0,0.02) weights quantized "
+                                           "(MLX rule), rotated over distinct device copies"),
+        "gemv_gateup_m1": dict(entry("gateup_m1", 1), workload="configs[1]: NVFP4 gate|up 34816x5120 + silu_mul"),
+        "gemv_gateup_m8": entry("gateup_m8", 8),
+        "gemv_down_m1": dict(entry("down_m1", 1), workload="configs[1]: NVFP4 down 5120x17408 + residual"),
+        "gemv_down_m8": entry("down_m8", 8),
+        "gqa_core": {f"ctx{c}k_m{m}": entry(f"gqa_{c}k_m{m}", m) for c in (4, 16, 32) for m in (1, 8)},
+        "gqa_core_workload": "configs[2]: gqa_prep + gqa_decode + gqa_merge alone (24 q / 4 KV heads x 128, int8 KV, "
+                             "q/k norm, RoPE 64 of 128, gate), position ctx-16, rotated over >= 2 GiB of KV caches",
+        "gdn_step_m1": dict(entry("gdnstep_m1", 1), workload="configs[3]: Gated DeltaNet step alone (hk16/hv48 x128, "
+                            "conv 4, gated norm, bf16 out), rotated over >= 2 GiB of recurrent states"),
+        "gdn_step_m8": entry("gdnstep_m8", 8),
         "int4_gateup_m1": dict(entry("int4_gateup_m1", 1), workload="affine 4-bit gate|up 34816x5120 + silu_mul"),
         "int4_gateup_m8": entry("int4_gateup_m8", 8),
         "moe_block_m1": dict(entry("moe_m1", 1), workload="MoE feed-forward: router + top-8 of 256 NVFP4 experts "
@@ -305,29 +402,32 @@ def main():
     print(json.dumps(line))
 
 
-def cpu_baseline(seconds: float):
-    """The C/OpenMP restatement of the reference's oracle GEMV (dequantize to FP32, multiply) on this host's cores,
-    over the layer's down projection [5120×17408] at M = 1, repeated for about ``seconds``."""
-    import numpy as np
+def cpu_baseline(seconds: float, b1_bytes: int, b8_bytes: int):
+    """The reference's CPU path for the same decode layer on this host (``oracle/baseline.py``): numpy (dequantize to
+    float32 + BLAS matmul, the oracle's mixer) and the C/OpenMP restatement of the oracle GEMV (packed weights
+    streamed once, rows over all cores) with the same mixer, the 27B GDN layer at M = 1 and 8; and configs[0] (INT4
+    4096², M = 1) on one core. ``value``: the C/OpenMP layer at M = 1, in the GPU line's unit (the layer's
+    algorithmic bytes ÷ its step time)."""
     sys.path.insert(0, str(ROOT))
-    from oracle import cpu as OC
-    hidden, inter = 5120, 17408
-    rng = np.random.default_rng(0)
-    m = {"weight": rng.integers(0, 256, size=(hidden, inter // 2), dtype=np.uint8),
-         "weight_scale": rng.integers(0x20, 0x48, size=(hidden, inter // 16), dtype=np.uint8),
-         "weight_scale_2": 0.02 / (6 * 448) * 64}
-    x = rng.standard_normal((1, inter)).astype(np.float32)
-    nt = OC.threads()
-    OC.nvfp4_gemv(m, x, nt)
-    reps, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        OC.nvfp4_gemv(m, x, nt)
-        reps += 1
-    dt = (time.perf_counter() - t0) / reps
-    w_bytes = hidden * inter * 9 // 16
-    return {"value": round(w_bytes / dt / 1e9, 2), "unit": "GB/s", "cores": nt, "kind": "port",
-            "sample": f"{reps} runs of the layer's NVFP4 down GEMV [5120x17408] at M=1 ({seconds:.0f} s), "
-                      f"{dt * 1e3:.2f} ms each, GB/s of its weight bytes"}
+    from oracle import baseline as OB
+    r = OB.run(seconds)
+
+    def gbs(key, nbytes):
+        return round(nbytes / r[key]["s_per_step"] / 1e9, 3)
+    legs = {k: dict(v, s_per_step=round(v["s_per_step"], 5)) for k, v in r.items()}
+    for m, b in ((1, b1_bytes), (8, b8_bytes)):
+        legs[f"numpy_m{m}"]["GB/s"] = gbs(f"numpy_m{m}", b)
+        legs[f"c_openmp_m{m}"]["GB/s"] = gbs(f"c_openmp_m{m}", b)
+        for leg in ("numpy", "c_openmp"):
+            legs[f"{leg}_m{m}"]["tokens_per_s"] = round(m / r[f"{leg}_m{m}"]["s_per_step"], 3)
+    legs["c1_int4_4096_m1_1thread"]["GB/s"] = gbs("c1_int4_4096_m1_1thread", 4096 * 4096 * 9 // 16 + 4 * 4096)
+    return {"value": legs["c_openmp_m1"]["GB/s"], "unit": "GB/s", "cores": r["c_openmp_m1"]["threads"],
+            "kind": "port",
+            "sample": f"one 27B GDN decode layer (weights N(0,0.02) NVFP4-quantized), about {seconds:.0f} s of CPU "
+                      f"time in all: C/OpenMP GEMVs + numpy mixer at M=1 and 8 ({r['c_openmp_m1']['reps']} and "
+                      f"{r['c_openmp_m8']['reps']} steps), the numpy oracle path (dequantize + matmul) one step each, "
+                      f"INT4 4096x4096 M=1 on 1 core",
+            "legs": legs}
 
 
 if __name__ == "__main__":

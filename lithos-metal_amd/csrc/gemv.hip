@@ -23,8 +23,10 @@
 //    exact F16 by v_cvt_scalef32_pk_f16_fp4 and a packed multiply by the mantissa factor). A workgroup stages one K
 //    split of the activations once and streams many tiles against it, so the activations are re-read per workgroup,
 //    not per tile; long K is split across workgroups with FP32 partials added in order by gemv_tk_reduce.
-// There is no cross-workgroup reduction inside a kernel: on gfx950 the agent-scope fences it needs (an L2 write-
-// back + invalidate per workgroup) cost more than the GEMV.
+// Cross-workgroup reduction: gemv_row with split K folds its splits in the kernel (the last split of a tile to
+// arrive adds them in split order) through device-scope atomic read-modify-writes only, with no release / acquire
+// fence — on gfx950 such a fence writes back / invalidates the whole L2 per workgroup and costs more than the GEMV.
+// gemv_tk and gemv_rowm leave their split partials to the ordered gemv_tk_reduce launch.
 #include "mi_common.h"
 #include "t16.h"
 

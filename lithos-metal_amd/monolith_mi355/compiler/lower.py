@@ -10,7 +10,8 @@ are values the program allocates. Layer by layer the ops are the ones ``layers.p
   (+ residual) → the MLP;
 * attention layer: ``gemv`` q|gate|k|v (norm fused) → ``gqa_decode`` at the step state's position → ``gemv`` o_proj
   (+ residual) → the MLP;
-* MLP: ``gemv`` gate|up (norm fused, silu·mul) → ``gemv`` down (+ residual);
+* MLP: ``gemv`` gate|up (norm fused, silu·mul) → ``gemv`` down (+ residual); a MoE block (``lower_moe``) in its place:
+  the shared expert, the router, ``moe_route``, the grouped ``moe_gemv`` pair and ``moe_combine``;
 * the token loop: ``embed`` of the pending token → the layers → ``lm_head`` (final norm fused, BF16 logits) →
   ``argmax`` → ``advance``.
 """
@@ -44,7 +45,46 @@ def act(name: str, *shape: int, dtype: str = "bf16") -> Value:
     return Value(name, tuple(shape), dtype)
 
 
+def lower_moe(g: Graph, moe, h: Value, prefix: str) -> Value:
+    """A ``layers.MoeBlock`` (``nn/moe.py``): the shared expert (norm fused, silu·mul → down), the router and the
+    shared expert's σ-gate as one BF16 GEMV of E + 1 rows into a row padded to 8, the top-k route with its expert
+    groups, the grouped gate|up and down GEMVs, the weighted combine with the gated shared expert and the residual.
+    One stream: the ops run in this order (the eager block forks the shared expert only at M > 2)."""
+    m, e, k = g.t, moe.experts, moe.top_k
+    pad = (e + 1 + 7) // 8 * 8
+    norm = bound(f"{prefix}.norm", moe.norm_w, "weights")
+    s_act = act(f"{prefix}.shared_act", m, moe.shared_inter)
+    s_out = act(f"{prefix}.shared_out", m, moe.hidden)
+    g.add("gemv", [h, weight(f"{prefix}.shared_gate_up", moe.shared_gate_up.packed)], [s_act], epilogue="silu_mul",
+          norm_w=norm, eps=moe.eps, name=f"{prefix}.shared_gate_up")
+    g.add("gemv", [s_act, weight(f"{prefix}.shared_down", moe.shared_down.packed)], [s_out],
+          name=f"{prefix}.shared_down")
+    logits = act(f"{prefix}.router_logits", m, pad)
+    router_out = Value(f"{prefix}.router_gate", (m, e + 1), "bf16", ld=pad, base=logits)
+    route_in = Value(f"{prefix}.route_logits", (m, e), "bf16", ld=pad, base=logits)
+    gate = Value(f"{prefix}.shared_gate", (m, 1), "bf16", ld=pad, offset=2 * e, base=logits)
+    g.add("gemv", [h, weight(f"{prefix}.router", moe.router_gate)], [router_out], norm_w=norm, eps=moe.eps,
+          name=f"{prefix}.router")
+    ids = act(f"{prefix}.ids", m, k, dtype="i32")
+    wts = act(f"{prefix}.weights", m, k, dtype="f32")
+    from ..kernels import GROUP_REC
+    groups = act(f"{prefix}.groups", min(e, m * k), GROUP_REC, dtype="i32")
+    g.add("moe_route", [route_in], [ids, wts, groups], top_k=k, renorm=True, name=f"{prefix}.route")
+    a = act(f"{prefix}.expert_act", m * k, moe.inter)
+    hk = act(f"{prefix}.expert_out", m * k, moe.hidden)
+    g.add("moe_gemv", [h, weight(f"{prefix}.gate_up", moe.gate_up), groups], [a], tokens=m, top_k=k,
+          x_per_slot=False, epilogue="silu_mul_rounded", norm_w=norm, eps=moe.eps, name=f"{prefix}.experts_gate_up")
+    g.add("moe_gemv", [a, weight(f"{prefix}.down", moe.down), groups], [hk], tokens=m, top_k=k, x_per_slot=True,
+          name=f"{prefix}.experts_down")
+    out = act(f"{prefix}.out", m, moe.hidden)
+    g.add("moe_combine", [hk, wts], [out], top_k=k, shared=s_out, shared_gate=gate, residual=h,
+          name=f"{prefix}.combine")
+    return out
+
+
 def lower_mlp(g: Graph, mlp, h: Value, prefix: str) -> Value:
+    if hasattr(mlp, "experts"):
+        return lower_moe(g, mlp, h, prefix)
     inter = mlp.inter
     a = act(f"{prefix}.act", g.t, inter)
     out = act(f"{prefix}.out", g.t, h.shape[1])

@@ -358,8 +358,9 @@ class MoeBlock:
                              torch.empty(m, self.hidden, dtype=bf, device=dev))
         return self._bufs[m]
 
-    def __call__(self, h, out=None):
-        """``h [M, hidden]`` bf16 → the block's output with the residual added (M ≤ 16)."""
+    def __call__(self, h, act=None, out=None):
+        """``h [M, hidden]`` bf16 → the block's output with the residual added (M ≤ 16). ``act`` is accepted so the
+        block can stand in for a decoder layer's dense MLP (it keeps its own intermediates)."""
         m = h.shape[0]
         logits, route, act, hk, s_act, s_out, s_gate, y = self.buffers(m)
         out = y if out is None else out

@@ -28,22 +28,6 @@ def rope_head_perm(head_dim: int, rotary_dim: int) -> np.ndarray:
     return perm.astype(np.int64)
 
 
-def head_dim_perm(n_heads: int, head_dim: int, rotary_dim: int, *, stride=None, offset: int = 0) -> np.ndarray:
-    """``rope_head_perm`` applied to every head of a matrix whose head ``h`` starts at row ``h·stride + offset``."""
-    stride = stride or head_dim
-    rows = np.arange(n_heads * stride)
-    base = rope_head_perm(head_dim, rotary_dim)
-    for h in range(n_heads):
-        lo = h * stride + offset
-        rows[lo: lo + head_dim] = lo + base
-    return rows
-
-
-def compose(outer: np.ndarray, inner: np.ndarray) -> np.ndarray:
-    """Apply ``inner`` first, then ``outer`` (both ``perm[new] = old``)."""
-    return np.asarray(inner)[np.asarray(outer)]
-
-
 def bf16_round_f32(w: np.ndarray, *, dtype_in: str = "BF16") -> np.ndarray:
     """The BF16 value a BF16 reference model holds, as float32 (F32 inputs rounded to BF16 first)."""
     if dtype_in == "BF16":

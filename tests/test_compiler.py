@@ -120,3 +120,37 @@ def test_emitted_program_equals_step_program(torch_gpu):
     # the re-encoded (op by op) run continues the same sequence
     rep2 = eng.run(4, steps_per_cb=2, in_flight=1, reencode=True)
     assert len(rep2.tokens) == 4 and eng.state()["step"] == steps + 4
+
+
+@pytest.mark.gpu
+def test_emitted_moe_program_equals_step_program(torch_gpu):
+    """A hybrid MoE decoder (the GDN layer's MLP replaced by a 64-expert top-8 block with a shared expert): the
+    emitted program (router, route, grouped expert GEMVs, combine) against the hand-built StepProgram, bit for bit."""
+    torch = torch_gpu
+    from monolith_mi355.compiler import Profile, compile_program
+    from monolith_mi355.layers import MoeBlock
+    from monolith_mi355.runtime.engine import Engine, bound_buffers
+    from monolith_mi355.runtime.step import StepProgram, StepState
+
+    def model(seed):
+        m = _decoder(torch, seed, "cuda")
+        m.layers[0].mlp = MoeBlock(hidden=1024, experts=64, top_k=8, inter=512, shared_inter=512, device="cuda",
+                                   seed=seed + 5)
+        return m
+    steps = 8
+    a = model(31)
+    st = StepState(ring_capacity=64)
+    prog = StepProgram(a, st, ctx_cap=256, steps_per_graph=2)
+    st.start(position=40, token=3)
+    tok_a = prog.step_eager(2) + prog.run(steps - 2, launches_per_batch=1, in_flight=2).tokens
+    b = model(31)
+    p = compile_program(b, Profile(ring_capacity=64, ctx_cap=256))
+    names = [o.name for o in p.ops]
+    assert "layers.0.mlp.route" in names and "layers.0.mlp.combine" in names
+    eng = Engine(p, buffers=bound_buffers(p))
+    eng.buffers[p.step_state].write(p.layout.pack(dict(position=40, kv_len=40, t_this_step=1, pending_tokens=[3],
+                                                       anchor=3)), 0)
+    rep = eng.run(steps, steps_per_cb=2, in_flight=2)
+    torch.cuda.synchronize()
+    assert rep.tokens == tok_a, (rep.tokens, tok_a)
+    assert torch.equal(a.layers[0].rec_state, b.layers[0].rec_state)
