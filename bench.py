@@ -112,7 +112,7 @@ def main():
         return
 
     with torch.cuda.stream(stream):
-        gdn = [GdnDecoderLayer(seed=10 + i, device=dev) for i in range(n)] if args.only in (None, "gdn", "mlp", "gateup") else []
+        gdn = [GdnDecoderLayer(seed=10 + i, device=dev) for i in range(n)] if args.only in (None, "gdn", "mlp", "gateup", "gemv") else []
         for m in (1, 8):
             if args.only not in (None, "gdn"):
                 break

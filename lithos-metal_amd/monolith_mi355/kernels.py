@@ -325,7 +325,8 @@ def gqa_decode(proj, cache: KVCache, pos, *, heads: int, rope_cos, rope_sin, gat
     quantized into ``cache`` at ``pos..pos+T``, attention over the cache, × σ(gate). Returns ``[T, heads·D]`` bf16.
     ``pos`` is an int, or a one-element int32 device tensor the kernels read (a step program's StepState position:
     the same launch serves every step of a replayed graph). ``done``: a step program's stop flag (one-element device
-    int32): once set, nothing is appended to the cache and ``out`` is not written."""
+    int32): once set, nothing is appended to the cache and ``out`` is not written. ``workspace``: a uint8 tensor of
+    ``mi_gqa_workspace_bytes`` for the key-range partials, or None for the library's own."""
     torch = _torch()
     _bf16_2d(proj, "gqa proj", aligned=False)
     t = proj.shape[0]
