@@ -334,6 +334,10 @@ def main():
     prof = ROOT / "profiles" / "gemv_nvfp4_gateup_m1_traffic.json"
     if prof.exists():
         traffic = json.loads(prof.read_text()).get("hbm_bytes_per_launch")
+    counters = None                                    # per-kernel HBM traffic ratios and MFMA busy fractions
+    cprof = ROOT / "profiles" / "kernel_counters.json"
+    if cprof.exists():
+        counters = json.loads(cprof.read_text())
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds, b1_bytes=out["gdn_m1"][1],
                                                   b8_bytes=out["gdn_m8"][1])
 
@@ -398,6 +402,7 @@ def main():
                      "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes": k_bytes, "avg_launch_us": round(k_ms * 1e3, 3)},
         "cpu_baseline": cpu,
+        "counters": counters,
     }
     print(json.dumps(line))
 
