@@ -230,14 +230,16 @@ typedef struct mi_gdn_desc {
 } mi_gdn_desc;
 int mi_gdn_step(const mi_gdn_desc* d, void* stream);
 
-/* ---- GQA decode attention over an int8 KV cache (ops/attention.py `gqa_decode` + `gqa_merge`;
+/* ---- GQA decode attention over an int8 or BF16 KV cache (ops/attention.py `gqa_decode` + `gqa_merge`;
  *      nn/attention.py:215-243; kernels/common/gqa_decode.metal:32-302; GqaParams kernels.py:604-611) ----------
  * proj [T][heads·(gate ? 2 : 1)·D + 2·kv·D] BF16 in checkpoint column order (q|gate per head, then k, v). The new
- * tokens are normed (qk_norm), roped (cos/sin [ctx_max][rotary_dim] BF16, cat(freqs, freqs)), quantized and
- * appended at pos..pos+T. Cache (this backend's layout): k_codes [kv][ctx_max][D] int8, v_codes
- * [kv][ctx_max/64][D][64] int8 (transposed inside 64-key blocks), k_scales / v_scales [kv][ctx_max] f16 bits
- * (scale = f16(absmax/127) per token and KV head); ctx_max a multiple of 64.
- * y [T][heads·D] BF16 (× bf16(σ(gate)) when gate). D = 128, T <= 16, heads/kv·T <= 64 rows per KV head. */
+ * tokens are normed (qk_norm), roped (cos/sin [ctx_max][rotary_dim] BF16, cat(freqs, freqs)) and appended at
+ * pos..pos+T. Cache (this backend's layout): k_codes [kv][ctx_max][D], v_codes [kv][ctx_max/64][D][64] (transposed
+ * inside 64-key blocks), both int8 codes with k_scales / v_scales [kv][ctx_max] f16 bits (scale = f16(absmax/127)
+ * per token and KV head) when kv_dtype = MI_KV_INT8, or BF16 values (the reference's cache, nn/attention.py:87-89;
+ * the scale pointers unused) when kv_dtype = MI_KV_BF16; ctx_max a multiple of 64.
+ * y [T][heads·D] BF16 (× bf16(σ(gate)) when gate). D = 128 or 256, T <= 16, heads/kv·T <= 64 rows per KV head. */
+enum { MI_KV_INT8 = 0, MI_KV_BF16 = 1 };
 typedef struct mi_gqa_desc {
   int32_t t, heads, kv_heads, head_dim, rotary_dim, pos, ctx_max, gate, qk_norm;
   const uint16_t* proj;
@@ -247,9 +249,9 @@ typedef struct mi_gqa_desc {
   const float* q_norm;       /* (1 + w) [D], or NULL */
   const float* k_norm;
   float eps, scaling;
-  int8_t* k_codes;
+  void* k_codes;             /* int8 codes or BF16 values, per kv_dtype */
   uint16_t* k_scales;
-  int8_t* v_codes;
+  void* v_codes;
   uint16_t* v_scales;
   uint16_t* y;
   int32_t ld_y;
@@ -259,6 +261,7 @@ typedef struct mi_gqa_desc {
                                 the key ranges are then planned for ctx_max - t and the kernels read the position */
   const uint32_t* done;      /* a step program's mi_step_state.done, or NULL: once it is set nothing is appended to
                                 the cache and y is not written (gqa_decode.metal:53,239 return at done) */
+  int32_t kv_dtype;          /* MI_KV_INT8 (0) or MI_KV_BF16 (1) */
 } mi_gqa_desc;
 size_t mi_gqa_workspace_bytes(const mi_gqa_desc* d);
 int mi_gqa_decode(const mi_gqa_desc* d, void* stream);

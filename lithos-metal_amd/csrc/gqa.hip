@@ -1,46 +1,52 @@
-// GQA decode attention over an int8 KV cache, T new tokens (ops/attention.py `gqa_decode` + `gqa_merge`;
+// GQA decode attention over an int8 or BF16 KV cache, T new tokens (ops/attention.py `gqa_decode` + `gqa_merge`;
 // nn/attention.py:215-243; nn/oracle.py:112-134; kernels/common/gqa_decode.metal:32-302).
 //
 // Semantics: q|gate per head, k, v from the projection; optional q/k RMSNorm(1 + w); partial RoPE (rotate_half on
 // the first rotary_dim dims, BF16 arithmetic, BF16 tables); the fresh k/v are quantized into the cache
 // (per token and KV head: scale = f16(absmax / 127), code = rint(x / scale)); scores bf16(bf16(q·k)·D^-½) over the
 // dequantized cache, causal inside the step; softmax in FP32 with P rounded to BF16; P·V in FP32 → BF16;
-// × bf16(σ(gate)).
+// × bf16(σ(gate)). With the BF16 cache (the reference's own, nn/attention.py:87-89) the fresh k/v are stored as they
+// are and the scores use them directly. Head dims 128 and 256 (the reference's 27B attention layer is 24/4/256).
 //
 // MI355X design, three launches:
-//  * Cache layout (this backend's): K codes [kv][ctx][D] int8; V codes [kv][ctx/64][D][64] int8 — transposed inside
-//    blocks of 64 keys, so a P·V B tile is 8 consecutive keys of one dim and a 64-key chunk is 8 KB contiguous, like
-//    K's; scales [kv][ctx] f16. Every chunk is two contiguous 8 KB streams read with 16- and 8-byte loads.
-//  * gqa_prep: one wave per (head or KV head, token), all in parallel: q rows normed, roped and prescaled by a power
-//    of two into F16 (the MFMA A operand, in the workspace); k/v quantized and appended to the cache.
+//  * Cache layout (this backend's): K [kv][ctx][D]; V [kv][ctx/64][D][64] — transposed inside blocks of 64 keys, so a
+//    P·V B tile is 8 consecutive keys of one dim and a chunk of keys is contiguous, like K's; int8 codes with f16
+//    scales [kv][ctx], or BF16 values. Every chunk is two contiguous streams read with 16- and 8-byte loads. A
+//    chunk is 64 keys (int8, D = 128) or 32 (BF16, or D = 256), sized so a wave holds one in registers and the next
+//    in flight.
+//  * gqa_prep: one wave per (head or KV head, token), all in parallel: q rows normed, roped and (int8 cache)
+//    prescaled by a power of two into F16 — the MFMA B operand, in the workspace; k/v quantized (or stored as BF16)
+//    and appended to the cache.
 //  * gqa_decode: a workgroup of 4 waves per (KV head, key range); each wave streams its share of the range in
-//    64-key chunks with the next chunk's codes prefetched into registers. The rep·T query rows of the KV head are A
+//    chunks with the next chunk's K side prefetched into registers. The rep·T query rows of the KV head are A
 //    tiles of v_mfma_f32_16x16x32_f16; int8 codes become exact F16 with an XOR / byte-permute / packed subtract;
 //    QKᵀ and P·V run on MFMA, the softmax online; the V scale folds into P (with a per-chunk power of two so it
-//    stays in F16 range). The 4 waves fold their (O, m, l) in LDS; the workgroup writes one partial.
+//    stays in F16 range). The BF16 cache feeds v_mfma_f32_16x16x32_bf16 as it is (q, P and the cache are all
+//    BF16-valued: the products are exact). The 4 waves fold their (O, m, l) in LDS; the workgroup writes one partial.
 //  * gqa_merge: one wave per (head, token) folds the partials in key order and applies the gate — deterministic.
 #include "mi_common.h"
 
 #include <algorithm>
+#include <type_traits>
 #include <cstdlib>
 #include <mutex>
 #include <vector>
 
 namespace {
 
-constexpr int D = 128;
-constexpr int CHUNK = 64;       // keys per inner step
+constexpr int BLOCK = 64;       // keys per V block (the V codes are transposed inside it)
 constexpr int TMAX = 16;
+constexpr int DMAX = 256;
 
 struct GqaArgs {
-  int t, heads, kv, rot, pos, ctx, gate, qk_norm, rep, rows;
+  int t, heads, kv, d, rot, pos, ctx, gate, qk_norm, rep, rows;
   int n_groups, group_len;                      // decode workgroups per KV head, keys per workgroup
   const uint16_t* proj; int ldp;
   const uint16_t* cosb; const uint16_t* sinb;   // [ctx][rot] BF16
   const float* q_norm; const float* k_norm;     // (1 + w), [D]
   float eps, scaling;
-  int8_t* kc; uint16_t* ks; int8_t* vc; uint16_t* vs;
-  f16_t* qf; float* qsc;                        // [kv][64][D] prescaled F16 query rows, [kv][64] their 2^p
+  void* kc; uint16_t* ks; void* vc; uint16_t* vs;   // int8 codes + f16 scales, or BF16 values (no scales)
+  uint16_t* qf; float* qsc;                     // [kv][64][D] query rows (F16 prescaled, or BF16), [kv][64] 2^p
   float* part_o; float* part_ml;                // [kv][group][rows][D], [kv][group][rows][2]
   uint16_t* y; int ldy;
   const int32_t* pos_dev;                       // device-resident position (a step program's StepState), or null
@@ -68,58 +74,75 @@ __device__ __forceinline__ f16x8 i8x8_to_f16(uint32_t lo, uint32_t hi) {
   return f16x8{x.x, x.y, y.x, y.y, z.x, z.y, w.x, w.y};
 }
 
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
+
 // q/k head vector of token t after the optional (1+w) RMSNorm and partial RoPE, into dst[D] (BF16 values as f32).
-// The whole wave cooperates: lane l handles dims l and l + 64.
+// The whole wave cooperates: lane l handles dims l + 64·u.
+template <int DH>
 __device__ void prep_vec(const GqaArgs& a, const uint16_t* src, const float* nw, int t, float* dst, int lane) {
-  float x0 = bfv(src, lane), x1 = bfv(src, lane + 64);
+  constexpr int U = DH / 64;
+  float x[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) x[u] = bfv(src, lane + 64 * u);
   if (a.qk_norm) {
-    const float ms = wave_sum(x0 * x0 + x1 * x1) / (float)D;
-    const float r = 1.0f / sqrtf(ms + a.eps);
-    x0 = round_bf16((x0 * r) * nw[lane]);
-    x1 = round_bf16((x1 * r) * nw[lane + 64]);
+    float ss = 0.0f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) ss += x[u] * x[u];
+    const float r = 1.0f / sqrtf(wave_sum(ss) / (float)DH + a.eps);
+#pragma unroll
+    for (int u = 0; u < U; ++u) x[u] = round_bf16((x[u] * r) * nw[lane + 64 * u]);
   }
-  dst[lane] = x0;
-  dst[lane + 64] = x1;
+#pragma unroll
+  for (int u = 0; u < U; ++u) dst[lane + 64 * u] = x[u];
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   __builtin_amdgcn_wave_barrier();
   const int half = a.rot / 2;
   const int p = min(cur_pos(a) + t, a.ctx - 1);     // a device position past the cache (a stopped program's queued
                                                    // steps) must not read past the RoPE tables
-  float o[2];
+  float o[U];
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
+  for (int u = 0; u < U; ++u) {
     const int i = lane + 64 * u;
-    const float xi = dst[i];
     if (i < a.rot) {
       const float c = bfv(a.cosb, (long long)p * a.rot + i), s = bfv(a.sinb, (long long)p * a.rot + i);
       const float rot = i < half ? -dst[i + half] : dst[i - half];
-      o[u] = round_bf16(round_bf16(xi * c) + round_bf16(rot * s));
+      o[u] = round_bf16(round_bf16(x[u] * c) + round_bf16(rot * s));
     } else {
-      o[u] = xi;
+      o[u] = x[u];
     }
   }
   __builtin_amdgcn_wave_barrier();
-  dst[lane] = o[0];
-  dst[lane + 64] = o[1];
+#pragma unroll
+  for (int u = 0; u < U; ++u) dst[lane + 64 * u] = o[u];
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   __builtin_amdgcn_wave_barrier();
 }
 
-// quantize a BF16-valued vector src[D] (LDS) into int8 codes + f16 scale (wave cooperative); returns nothing,
-// writes codes to (dst_codes + stride · i) and the scale to *dst_scale
-__device__ void quant_store(const float* src, int8_t* codes, long long stride, uint16_t* scale_out, int lane) {
-  const float x0 = src[lane], x1 = src[lane + 64];
-  const float amax = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
-  const f16_t sh = (f16_t)(amax / 127.0f);
-  const float sc = (float)sh;
-  float c0 = 0.0f, c1 = 0.0f;
-  if (sc > 0.0f) {
-    c0 = fminf(fmaxf(rintf(x0 / sc), -127.0f), 127.0f);
-    c1 = fminf(fmaxf(rintf(x1 / sc), -127.0f), 127.0f);
+// store a BF16-valued vector src[D] (LDS) as one cache row (wave cooperative): int8 codes at codes + stride·i and the
+// f16 scale at *scale_out, or BF16 values at values + stride·i
+template <int DH, bool BF>
+__device__ void store_row(const float* src, void* dst, long long stride, uint16_t* scale_out, int lane) {
+  constexpr int U = DH / 64;
+  float x[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) x[u] = src[lane + 64 * u];
+  if constexpr (BF) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) static_cast<uint16_t*>(dst)[stride * (lane + 64 * u)] = f32_to_bf16_bits(x[u]);
+  } else {
+    float m = 0.0f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) m = fmaxf(m, fabsf(x[u]));
+    const float amax = wave_max(m);
+    const f16_t sh = (f16_t)(amax / 127.0f);
+    const float sc = (float)sh;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float c = sc > 0.0f ? fminf(fmaxf(rintf(x[u] / sc), -127.0f), 127.0f) : 0.0f;
+      static_cast<int8_t*>(dst)[stride * (lane + 64 * u)] = (int8_t)(int)c;
+    }
+    if (lane == 0) *scale_out = __builtin_bit_cast(uint16_t, sh);
   }
-  codes[stride * lane] = (int8_t)(int)c0;
-  codes[stride * (lane + 64)] = (int8_t)(int)c1;
-  if (lane == 0) *scale_out = __builtin_bit_cast(uint16_t, sh);
 }
 
 constexpr int MAXROWS = 64;     // query rows per KV head (rep·T)
@@ -138,68 +161,127 @@ __device__ __forceinline__ int prescale_exp(float mx) {   // 2^-p·mx in [2^14, 
 // the B operand of k-block ks its 8 values are tiles 2·ks, 2·ks + 1 — and those 8 keys sit together.
 __device__ __forceinline__ int vblock_pos(int k) { return (k >> 5) * 32 + ((k & 15) >> 2) * 8 + ((k >> 4) & 1) * 4 + (k & 3); }
 
+template <int DH, bool BF>
 __global__ __launch_bounds__(64) void gqa_prep(GqaArgs a) {
-  __shared__ float tmp[D];
+  constexpr int U = DH / 64;
+  __shared__ float tmp[DH];
   const int lane = threadIdx.x, x = blockIdx.x, t = blockIdx.y;
   if (stopped(a)) return;
-  const int q_cols = a.gate ? 2 * D : D;
+  const int q_cols = a.gate ? 2 * DH : DH;
   const uint16_t* row = a.proj + (long long)t * a.ldp;
   if (x < a.heads) {
     const int j = x / a.rep, qrow = t * a.rep + (x - j * a.rep);
-    prep_vec(a, row + x * q_cols, a.q_norm, t, tmp, lane);
-    const float x0 = tmp[lane], x1 = tmp[lane + 64];
-    const int p = prescale_exp(wave_max(fmaxf(fabsf(x0), fabsf(x1))));
-    const float inv = pow2f(-p);
-    f16_t* dst = a.qf + ((long long)j * MAXROWS + qrow) * D;
-    dst[lane] = (f16_t)(x0 * inv);
-    dst[lane + 64] = (f16_t)(x1 * inv);
-    if (lane == 0) a.qsc[j * MAXROWS + qrow] = pow2f(p);
+    prep_vec<DH>(a, row + x * q_cols, a.q_norm, t, tmp, lane);
+    uint16_t* dst = a.qf + ((long long)j * MAXROWS + qrow) * DH;
+    if constexpr (BF) {                           // BF16 rows as they are (the BF16 MFMA takes them exactly)
+#pragma unroll
+      for (int u = 0; u < U; ++u) dst[lane + 64 * u] = f32_to_bf16_bits(tmp[lane + 64 * u]);
+      if (lane == 0) a.qsc[j * MAXROWS + qrow] = 1.0f;
+    } else {                                      // F16 prescaled by a power of two (exact above 2^-14 of the max)
+      float m = 0.0f;
+#pragma unroll
+      for (int u = 0; u < U; ++u) m = fmaxf(m, fabsf(tmp[lane + 64 * u]));
+      const int p = prescale_exp(wave_max(m));
+      const float inv = pow2f(-p);
+#pragma unroll
+      for (int u = 0; u < U; ++u) dst[lane + 64 * u] = __builtin_bit_cast(uint16_t, (f16_t)(tmp[lane + 64 * u] * inv));
+      if (lane == 0) a.qsc[j * MAXROWS + qrow] = pow2f(p);
+    }
   } else {
     const int j = x - a.heads, p = cur_pos(a) + t;
     if (p >= a.ctx) return;                       // past the cache (a device position the host cannot check)
-    prep_vec(a, row + a.heads * q_cols + j * D, a.k_norm, t, tmp, lane);
-    quant_store(tmp, a.kc + ((long long)j * a.ctx + p) * D, 1, a.ks + (long long)j * a.ctx + p, lane);
+    constexpr int ES = BF ? 2 : 1;                // bytes per cache element
+    char* kc = static_cast<char*>(a.kc);
+    char* vc = static_cast<char*>(a.vc);
+    prep_vec<DH>(a, row + a.heads * q_cols + j * DH, a.k_norm, t, tmp, lane);
+    store_row<DH, BF>(tmp, kc + ((long long)j * a.ctx + p) * DH * ES, 1, a.ks ? a.ks + (long long)j * a.ctx + p : nullptr,
+                      lane);
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
-    const uint16_t* v = row + a.heads * q_cols + a.kv * D + j * D;
-    tmp[lane] = bfv(v, lane);
-    tmp[lane + 64] = bfv(v, lane + 64);
+    const uint16_t* v = row + a.heads * q_cols + a.kv * DH + j * DH;
+#pragma unroll
+    for (int u = 0; u < U; ++u) tmp[lane + 64 * u] = bfv(v, lane + 64 * u);
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
-    quant_store(tmp, a.vc + ((long long)j * a.ctx + (p & ~(CHUNK - 1))) * D + vblock_pos(p & (CHUNK - 1)), CHUNK,
-                a.vs + (long long)j * a.ctx + p, lane);
+    store_row<DH, BF>(tmp, vc + (((long long)j * a.ctx + (p & ~(BLOCK - 1))) * DH + vblock_pos(p & (BLOCK - 1))) * ES,
+                      BLOCK, a.vs ? a.vs + (long long)j * a.ctx + p : nullptr, lane);
   }
 }
 
-// a chunk's K side as this lane holds it: codes of key 16·kt + m16, dims 32·kg + [0, 32); scales of keys
-// 16·kt + 4·kg + [0, 4)
-struct KChunk {
-  uint4 k[4][2];
-  uint2 ksc[4], vsc[4];
+// The geometry of one decode instantiation: head dim DH, cache element type (BF: BF16, else int8 codes + scales).
+template <int DH, bool BF>
+struct Geo {
+  static constexpr int CH = (!BF && DH == 128) ? 64 : 32;   // keys per chunk
+  static constexpr int KT = CH / 16;                          // score tiles per chunk
+  static constexpr int KS = CH / 32;                          // P·V k-blocks per chunk
+  static constexpr int NS = DH / 32;                          // QKᵀ k-blocks per score tile
+  static constexpr int NC = DH / 16;                          // O column tiles
+  static constexpr int KW = BF ? NS : NS / 2;                 // 16-byte K loads per key and lane
+  static constexpr int VW = BF ? 4 : 2;                       // dwords of V per (k-block, column tile) and lane
 };
 
-__device__ __forceinline__ void load_k(const int8_t* kbase, const uint16_t* ksb, const uint16_t* vsb, int k0, int m16,
-                                       int kg, KChunk& c) {
+// a chunk as this lane holds it: K of key k0 + 16·kt + m16, dims (DH/4)·kg + [0, DH/4); the scales of keys
+// k0 + 16·kt + 4·kg + [0, 4) (int8); V of dim 16·ct + m16, keys (block order) 32·ks + 8·kg + [0, 8)
+template <int DH, bool BF>
+struct Chunk {
+  using G = Geo<DH, BF>;
+  uint4 k[G::KT][G::KW];
+  uint2 ksc[BF ? 1 : G::KT], vsc[BF ? 1 : G::KT];
+  uint32_t v[G::KS][G::NC][G::VW];
+};
+
+template <int DH, bool BF>
+__device__ __forceinline__ void load_k(const GqaArgs& a, int j, int k0, int m16, int kg, Chunk<DH, BF>& c) {
+  using G = Geo<DH, BF>;
+  constexpr int ES = BF ? 2 : 1;
+  const char* kb = static_cast<const char*>(a.kc) + (long long)j * a.ctx * DH * ES;
 #pragma unroll
-  for (int kt = 0; kt < 4; ++kt) {
-    const int8_t* kp = kbase + (long long)(k0 + kt * 16 + m16) * D + 32 * kg;
-    c.k[kt][0] = *reinterpret_cast<const uint4*>(kp);
-    c.k[kt][1] = *reinterpret_cast<const uint4*>(kp + 16);
-    c.ksc[kt] = *reinterpret_cast<const uint2*>(ksb + k0 + kt * 16 + 4 * kg);
-    c.vsc[kt] = *reinterpret_cast<const uint2*>(vsb + k0 + kt * 16 + 4 * kg);
+  for (int kt = 0; kt < G::KT; ++kt) {
+    const char* kp = kb + ((long long)(k0 + kt * 16 + m16) * DH + (DH / 4) * kg) * ES;
+#pragma unroll
+    for (int w = 0; w < G::KW; ++w) c.k[kt][w] = *reinterpret_cast<const uint4*>(kp + 16 * w);
+    if constexpr (!BF) {
+      c.ksc[kt] = *reinterpret_cast<const uint2*>(a.ks + (long long)j * a.ctx + k0 + kt * 16 + 4 * kg);
+      c.vsc[kt] = *reinterpret_cast<const uint2*>(a.vs + (long long)j * a.ctx + k0 + kt * 16 + 4 * kg);
+    }
   }
+}
+
+template <int DH, bool BF>
+__device__ __forceinline__ void load_v(const GqaArgs& a, int j, int k0, int m16, int kg, Chunk<DH, BF>& c) {
+  using G = Geo<DH, BF>;
+  constexpr int ES = BF ? 2 : 1;
+  // the chunk's keys in their V block: block k0 / 64, positions (k0 % 64) + [0, CH)
+  const char* vp = static_cast<const char*>(a.vc) +
+                   (((long long)j * a.ctx + (k0 & ~(BLOCK - 1))) * DH + (k0 & (BLOCK - 1)) + 8 * kg) * ES;
+#pragma unroll
+  for (int ks = 0; ks < G::KS; ++ks)
+#pragma unroll
+    for (int ct = 0; ct < G::NC; ++ct) {
+      const char* q = vp + ((long long)(ct * 16 + m16) * BLOCK + ks * 32) * ES;
+      if constexpr (BF) {
+        const uint4 u = *reinterpret_cast<const uint4*>(q);
+        c.v[ks][ct][0] = u.x; c.v[ks][ct][1] = u.y; c.v[ks][ct][2] = u.z; c.v[ks][ct][3] = u.w;
+      } else {
+        const uint2 u = *reinterpret_cast<const uint2*>(q);
+        c.v[ks][ct][0] = u.x; c.v[ks][ct][1] = u.y;
+      }
+    }
 }
 
 __device__ __forceinline__ float f16_lo(uint32_t u) { return (float)__builtin_bit_cast(f16_t, (uint16_t)(u & 0xFFFF)); }
 __device__ __forceinline__ float f16_hi(uint32_t u) { return (float)__builtin_bit_cast(f16_t, (uint16_t)(u >> 16)); }
 
 // The decode workgroup: NW waves over one key range of KV head j. Everything is computed transposed so that a
-// lane owns one query row (row = 16·rt + m16): Sᵀ = K·Qᵀ (A = K codes as F16, B = the prescaled F16 query rows),
-// softmax over the lane's 16 keys plus the lanes l ^ 16, l ^ 32, l ^ 48 of the same row, and Oᵀ += Vᵀ·Pᵀ with
-// Pᵀ straight from the score registers (no LDS round trip) — every per-row quantity is lane-local.
-template <int RT>
-__global__ __launch_bounds__(64 * NW, RT == 1 ? 2 : 1) void gqa_decode(GqaArgs a) {   // RT = 1: 2 waves / SIMD
-  __shared__ __attribute__((aligned(16))) float red[RT * 16][D + 4];   // the workgroup's O, row-major
+// lane owns one query row (row = 16·rt + m16): Sᵀ = K·Qᵀ (A = the K tile, B = the query rows), softmax over the
+// lane's keys plus the lanes l ^ 16, l ^ 32, l ^ 48 of the same row, and Oᵀ += Vᵀ·Pᵀ with Pᵀ straight from the score
+// registers (no LDS round trip) — every per-row quantity is lane-local.
+template <int RT, int DH, bool BF>
+__global__ __launch_bounds__(64 * NW, (RT == 1 && DH == 128) ? 2 : 1) void gqa_decode(GqaArgs a) {
+  using G = Geo<DH, BF>;
+  using OpT = typename std::conditional<BF, bf16x8, f16x8>::type;
+  constexpr int CH = G::CH;
+  __shared__ __attribute__((aligned(16))) float red[RT * 16][DH + 4];   // the workgroup's O, row-major
   __shared__ float mls[NW][RT * 16][2];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int j = blockIdx.y, g = blockIdx.x;
@@ -210,102 +292,106 @@ __global__ __launch_bounds__(64 * NW, RT == 1 ? 2 : 1) void gqa_decode(GqaArgs a
   // the last group also takes the new tokens; with a device position the groups cover the planned bound and the
   // ones past the position are empty (their partials fold in with weight 0)
   const int ke = g == a.n_groups - 1 ? n_keys : min(kb + a.group_len, n_keys);
-  const int nch = max(0, (ke - kb + CHUNK - 1) / CHUNK);
-  const int k_begin = kb + (w * nch / NW) * CHUNK;
-  const int k_end = min(ke, kb + ((w + 1) * nch / NW) * CHUNK);
+  const int nch = max(0, (ke - kb + CH - 1) / CH);
+  const int k_begin = kb + (w * nch / NW) * CH;
+  const int k_end = min(ke, kb + ((w + 1) * nch / NW) * CH);
   const int m16 = lane & 15, kg = lane >> 4;
 
-  const int8_t* kbase = a.kc + (long long)j * a.ctx * D;
-  const int8_t* vbase = a.vc + (long long)j * a.ctx * D;
-  const uint16_t* ksb = a.ks + (long long)j * a.ctx;
-  const uint16_t* vsb = a.vs + (long long)j * a.ctx;
-  KChunk cur, nxt;
-  if (k_begin < k_end) load_k(kbase, ksb, vsb, k_begin, m16, kg, cur);   // chunks lie inside the cache: ctx % 64 == 0
+  Chunk<DH, BF> cur, nxt;
+  if (k_begin < k_end) load_k<DH, BF>(a, j, k_begin, m16, kg, cur);   // chunks lie inside the cache: ctx % 64 == 0
 
-  // the query rows as B tiles (k-permuted: lane holds dims 32·kg + 8·s + i of row 16·rt + m16), zero past rows
-  f16x8 qb[RT][4];
-  float rsc[RT];                                        // the lane's row: 2^p of its prescale
+  // the query rows as B tiles (k-permuted: lane holds dims (DH/4)·kg + 8·s + i of row 16·rt + m16), zero past rows
+  OpT qb[RT][G::NS];
+  float rsc[RT];                                        // the lane's row: 2^p of its prescale (int8 cache)
   int qlim[RT];                                         // the lane's row: last key it may see (causal)
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     const int row = rt * 16 + m16;
     const bool ok = row < a.rows;
-    const f16_t* src = a.qf + ((long long)j * MAXROWS + (ok ? row : 0)) * D + 32 * kg;
+    const uint16_t* src = a.qf + ((long long)j * MAXROWS + (ok ? row : 0)) * DH + (DH / 4) * kg;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const f16x8 v = *reinterpret_cast<const f16x8*>(src + 8 * s);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) qb[rt][s][i] = ok ? v[i] : (f16_t)0.0f;
+    for (int s = 0; s < G::NS; ++s) {
+      const uint4 u = *reinterpret_cast<const uint4*>(src + 8 * s);
+      qb[rt][s] = __builtin_bit_cast(OpT, ok ? u : uint4{0u, 0u, 0u, 0u});
     }
     rsc[rt] = ok ? a.qsc[j * MAXROWS + row] : 1.0f;
     qlim[rt] = ok ? pos + row / a.rep : n_keys;         // rows past `rows` hold q = 0: finite, never written
   }
 
-  f32x4 o[RT][8];                                       // o[rt][ct][i] = O[row 16·rt + m16][dim 16·ct + 4·kg + i]
-  float m_run[RT], l_run[RT];                           // l_run: this lane's share (its 16 keys per chunk)
+  f32x4 o[RT][G::NC];                                   // o[rt][ct][i] = O[row 16·rt + m16][dim 16·ct + 4·kg + i]
+  float m_run[RT], l_run[RT];                           // l_run: this lane's share (its keys per chunk)
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
 #pragma unroll
-    for (int ct = 0; ct < 8; ++ct) o[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int ct = 0; ct < G::NC; ++ct) o[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
     m_run[rt] = -INFINITY;
     l_run[rt] = 0.0f;
   }
-  int pv_cur = 0;                                       // O is held in units of 2^pv_cur
+  int pv_cur = 0;                                       // O is held in units of 2^pv_cur (int8 cache)
 
-  for (int k0 = k_begin; k0 < k_end; k0 += CHUNK) {
-    // this chunk's V codes, then the next chunk's K side (the last iteration reloads its own, in bounds)
-    uint2 vr[2][8];
-    const int8_t* vp = vbase + (long long)k0 * D + 8 * kg;
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-      for (int ct = 0; ct < 8; ++ct) vr[ks][ct] = *reinterpret_cast<const uint2*>(vp + (ct * 16 + m16) * CHUNK + ks * 32);
-    load_k(kbase, ksb, vsb, k0 + CHUNK < k_end ? k0 + CHUNK : k0, m16, kg, nxt);
+  for (int k0 = k_begin; k0 < k_end; k0 += CH) {
+    // this chunk's V, then the next chunk's K side (the last iteration reloads its own, in bounds)
+    load_v<DH, BF>(a, j, k0, m16, kg, cur);
+    load_k<DH, BF>(a, j, k0 + CH < k_end ? k0 + CH : k0, m16, kg, nxt);
 
-    const bool full = k0 + CHUNK <= k_end && k0 + CHUNK - 1 <= pos;     // every key valid and visible to every row
-    float ksc[4][4], vsc[4][4];
-    float vmax = 0.0f;
+    const bool full = k0 + CH <= k_end && k0 + CH - 1 <= pos;     // every key valid and visible to every row
+    float ksc[G::KT][4], vsc[G::KT][4];
+    int pv = pv_cur;
+    float resc = 1.0f;
+    if constexpr (!BF) {
+      float vmax = 0.0f;
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      const uint2 kq = cur.ksc[kt], vq = cur.vsc[kt];
-      ksc[kt][0] = f16_lo(kq.x); ksc[kt][1] = f16_hi(kq.x); ksc[kt][2] = f16_lo(kq.y); ksc[kt][3] = f16_hi(kq.y);
-      vsc[kt][0] = f16_lo(vq.x); vsc[kt][1] = f16_hi(vq.x); vsc[kt][2] = f16_lo(vq.y); vsc[kt][3] = f16_hi(vq.y);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (!full && k0 + kt * 16 + 4 * kg + i >= k_end) vsc[kt][i] = 0.0f;
-        vmax = fmaxf(vmax, vsc[kt][i]);
-      }
-    }
-    vmax = max_xor32(max_xor16(vmax));
-    // the chunk's V-scale prescale 2^-pv keeps P'' = p·v_scale·2^-pv in F16 range
-    const int pv = vmax == 0.0f ? pv_cur : prescale_exp(vmax);
-    const float pv_inv = pow2f(-pv), resc = pow2f(pv_cur - pv);
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) vsc[kt][i] *= pv_inv;
-
-    f16x8 kb4[4][4];
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      kb4[kt][0] = i8x8_to_f16(cur.k[kt][0].x, cur.k[kt][0].y);
-      kb4[kt][1] = i8x8_to_f16(cur.k[kt][0].z, cur.k[kt][0].w);
-      kb4[kt][2] = i8x8_to_f16(cur.k[kt][1].x, cur.k[kt][1].y);
-      kb4[kt][3] = i8x8_to_f16(cur.k[kt][1].z, cur.k[kt][1].w);
-    }
-    f16x8 pb[RT][2];                                    // Pᵀ B tiles: element i of k-block ks = key tile 2·ks + i/4
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      float sc[4][4];
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb4[kt][s], qb[rt][s], acc, 0, 0, 0);
+      for (int kt = 0; kt < G::KT; ++kt) {
+        const uint2 kq = cur.ksc[kt], vq = cur.vsc[kt];
+        ksc[kt][0] = f16_lo(kq.x); ksc[kt][1] = f16_hi(kq.x); ksc[kt][2] = f16_lo(kq.y); ksc[kt][3] = f16_hi(kq.y);
+        vsc[kt][0] = f16_lo(vq.x); vsc[kt][1] = f16_hi(vq.x); vsc[kt][2] = f16_lo(vq.y); vsc[kt][3] = f16_hi(vq.y);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          float v = round_bf16(round_bf16(acc[i] * (rsc[rt] * ksc[kt][i])) * a.scaling);
+          if (!full && k0 + kt * 16 + 4 * kg + i >= k_end) vsc[kt][i] = 0.0f;
+          vmax = fmaxf(vmax, vsc[kt][i]);
+        }
+      }
+      vmax = max_xor32(max_xor16(vmax));
+      // the chunk's V-scale prescale 2^-pv keeps P'' = p·v_scale·2^-pv in F16 range
+      pv = vmax == 0.0f ? pv_cur : prescale_exp(vmax);
+      const float pv_inv = pow2f(-pv);
+      resc = pow2f(pv_cur - pv);
+#pragma unroll
+      for (int kt = 0; kt < G::KT; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vsc[kt][i] *= pv_inv;
+    }
+
+    OpT ka[G::KT][G::NS];                               // the K tiles as MFMA A operands
+#pragma unroll
+    for (int kt = 0; kt < G::KT; ++kt)
+#pragma unroll
+      for (int s = 0; s < G::NS; ++s) {
+        if constexpr (BF) {
+          ka[kt][s] = as_bf16x8(cur.k[kt][s]);
+        } else {
+          const uint4 u = cur.k[kt][s / 2];
+          ka[kt][s] = (s & 1) ? i8x8_to_f16(u.z, u.w) : i8x8_to_f16(u.x, u.y);
+        }
+      }
+    OpT pb[RT][G::KS];                                  // Pᵀ B tiles: element i of k-block ks = key tile 2·ks + i/4
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      float sc[G::KT][4];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < G::KT; ++kt) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < G::NS; ++s) {
+          if constexpr (BF) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[kt][s], qb[rt][s], acc, 0, 0, 0);
+          else acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[kt][s], qb[rt][s], acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float v;
+          if constexpr (BF) v = round_bf16(round_bf16(acc[i]) * a.scaling);
+          else v = round_bf16(round_bf16(acc[i] * (rsc[rt] * ksc[kt][i])) * a.scaling);
           if (!full) {
             const int key = k0 + kt * 16 + 4 * kg + i;
             v = (key < k_end && key <= qlim[rt]) ? v : -INFINITY;
@@ -319,32 +405,49 @@ __global__ __launch_bounds__(64 * NW, RT == 1 ? 2 : 1) void gqa_decode(GqaArgs a
       const float alpha = m_run[rt] == -INFINITY ? 0.0f : __expf(m_run[rt] - mnew);
       float psum = 0.0f;
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+      for (int kt = 0; kt < G::KT; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float p = sc[kt][i] == -INFINITY ? 0.0f : __expf(sc[kt][i] - mnew);
           psum += p;
-          pb[rt][kt >> 1][(kt & 1) * 4 + i] = (f16_t)(round_bf16(p) * vsc[kt][i]);
+          if constexpr (BF) pb[rt][kt >> 1][(kt & 1) * 4 + i] = (__bf16)p;
+          else pb[rt][kt >> 1][(kt & 1) * 4 + i] = (f16_t)(round_bf16(p) * vsc[kt][i]);
         }
       l_run[rt] = l_run[rt] * alpha + psum;
       m_run[rt] = mnew;
       const float f = alpha * resc;
 #pragma unroll
-      for (int ct = 0; ct < 8; ++ct)
+      for (int ct = 0; ct < G::NC; ++ct)
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[rt][ct][i] *= f;
     }
     pv_cur = pv;
     // Oᵀ += Vᵀ·Pᵀ
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+    for (int ks = 0; ks < G::KS; ++ks)
 #pragma unroll
-      for (int ct = 0; ct < 8; ++ct) {
-        const f16x8 va = i8x8_to_f16(vr[ks][ct].x, vr[ks][ct].y);
+      for (int ct = 0; ct < G::NC; ++ct) {
+        if constexpr (BF) {
+          const bf16x8 va = as_bf16x8(uint4{cur.v[ks][ct][0], cur.v[ks][ct][1], cur.v[ks][ct][2], cur.v[ks][ct][3]});
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) o[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[rt][ks], o[rt][ct], 0, 0, 0);
+          for (int rt = 0; rt < RT; ++rt)
+            o[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[rt][ks], o[rt][ct], 0, 0, 0);
+        } else {
+          const f16x8 va = i8x8_to_f16(cur.v[ks][ct][0], cur.v[ks][ct][1]);
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt)
+            o[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[rt][ks], o[rt][ct], 0, 0, 0);
+        }
       }
-    cur = nxt;
+#pragma unroll
+    for (int kt = 0; kt < G::KT; ++kt) {
+#pragma unroll
+      for (int ww = 0; ww < G::KW; ++ww) cur.k[kt][ww] = nxt.k[kt][ww];
+      if constexpr (!BF) {
+        cur.ksc[kt] = nxt.ksc[kt];
+        cur.vsc[kt] = nxt.vsc[kt];
+      }
+    }
   }
 
   // ---- fold the workgroup's waves: common max, O summed in LDS in wave order, one partial per workgroup ---------
@@ -366,7 +469,7 @@ __global__ __launch_bounds__(64 * NW, RT == 1 ? 2 : 1) void gqa_decode(GqaArgs a
     for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, mls[ww][row][0]);
     const float f = m_run[rt] == -INFINITY ? 0.0f : __expf(m_run[rt] - M) * unscale;
 #pragma unroll
-    for (int ct = 0; ct < 8; ++ct)
+    for (int ct = 0; ct < G::NC; ++ct)
 #pragma unroll
       for (int i = 0; i < 4; ++i) o[rt][ct][i] *= f;
   }
@@ -375,7 +478,7 @@ __global__ __launch_bounds__(64 * NW, RT == 1 ? 2 : 1) void gqa_decode(GqaArgs a
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-        for (int ct = 0; ct < 8; ++ct) {
+        for (int ct = 0; ct < G::NC; ++ct) {
           f32x4* dst = reinterpret_cast<f32x4*>(&red[rt * 16 + m16][ct * 16 + 4 * kg]);
           *dst = ww == 0 ? o[rt][ct] : *dst + o[rt][ct];
         }
@@ -383,7 +486,7 @@ __global__ __launch_bounds__(64 * NW, RT == 1 ? 2 : 1) void gqa_decode(GqaArgs a
     __syncthreads();
   }
   const long long base = ((long long)j * a.n_groups + g) * a.rows;
-  for (int idx = threadIdx.x; idx < a.rows * D; idx += 64 * NW) a.part_o[base * D + idx] = red[idx / D][idx % D];
+  for (int idx = threadIdx.x; idx < a.rows * DH; idx += 64 * NW) a.part_o[base * DH + idx] = red[idx / DH][idx % DH];
   for (int row = threadIdx.x; row < a.rows; row += 64 * NW) {
     float M = -INFINITY, L = 0.0f;
     for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, mls[ww][row][0]);
@@ -397,8 +500,10 @@ __global__ __launch_bounds__(64 * NW, RT == 1 ? 2 : 1) void gqa_decode(GqaArgs a
 // one workgroup of MW waves per (query head, token): wave w folds partials w, w + MW, … (all its loads in flight
 // at once), then wave 0 adds the MW sums in wave order — deterministic; normalize, BF16, × bf16(σ(gate))
 constexpr int MW = 8;
+template <int DH>
 __global__ __launch_bounds__(64 * MW) void gqa_merge(GqaArgs a) {
-  __shared__ float red[MW][D + 1];
+  constexpr int U = DH / 64;
+  __shared__ float red[MW][DH + 1];
   const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   if (stopped(a)) return;
   const int j = h / a.rep;
@@ -407,37 +512,46 @@ __global__ __launch_bounds__(64 * MW) void gqa_merge(GqaArgs a) {
   float M = -INFINITY;
   for (int g = lane; g < a.n_groups; g += 64) M = fmaxf(M, a.part_ml[(b0 + (long long)g * a.rows) * 2]);
   M = wave_max(M);
-  float l = 0.0f, o0 = 0.0f, o1 = 0.0f;
+  float l = 0.0f, o[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) o[u] = 0.0f;
 #pragma unroll 8
   for (int g = w; g < a.n_groups; g += MW) {
     const long long b = b0 + (long long)g * a.rows;
     const float m = a.part_ml[b * 2], lg = a.part_ml[b * 2 + 1];
-    const float x0 = a.part_o[b * D + lane], x1 = a.part_o[b * D + lane + 64];
     const float wgt = m == -INFINITY ? 0.0f : __expf(m - M);
     l += wgt * lg;
-    o0 += wgt * x0;
-    o1 += wgt * x1;
+#pragma unroll
+    for (int u = 0; u < U; ++u) o[u] += wgt * a.part_o[b * DH + lane + 64 * u];
   }
-  red[w][lane] = o0;
-  red[w][lane + 64] = o1;
-  if (lane == 0) red[w][D] = l;
+#pragma unroll
+  for (int u = 0; u < U; ++u) red[w][lane + 64 * u] = o[u];
+  if (lane == 0) red[w][DH] = l;
   __syncthreads();
   if (w != 0) return;
-  o0 = red[0][lane]; o1 = red[0][lane + 64]; l = red[0][D];
 #pragma unroll
-  for (int ww = 1; ww < MW; ++ww) { o0 += red[ww][lane]; o1 += red[ww][lane + 64]; l += red[ww][D]; }
-  float y0 = round_bf16(o0 / l), y1 = round_bf16(o1 / l);
-  if (a.gate) {
-    const uint16_t* gp = a.proj + (long long)t * a.ldp + h * 2 * D + D;
-    y0 = round_bf16(y0 * round_bf16(1.0f / (1.0f + __expf(-bfv(gp, lane)))));
-    y1 = round_bf16(y1 * round_bf16(1.0f / (1.0f + __expf(-bfv(gp, lane + 64)))));
+  for (int u = 0; u < U; ++u) o[u] = red[0][lane + 64 * u];
+  l = red[0][DH];
+#pragma unroll
+  for (int ww = 1; ww < MW; ++ww) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) o[u] += red[ww][lane + 64 * u];
+    l += red[ww][DH];
   }
-  a.y[(long long)t * a.ldy + h * D + lane] = f32_to_bf16_bits(y0);
-  a.y[(long long)t * a.ldy + h * D + lane + 64] = f32_to_bf16_bits(y1);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    float y = round_bf16(o[u] / l);
+    if (a.gate) {
+      const uint16_t* gp = a.proj + (long long)t * a.ldp + h * 2 * DH + DH;
+      y = round_bf16(y * round_bf16(1.0f / (1.0f + __expf(-bfv(gp, lane + 64 * u)))));
+    }
+    a.y[(long long)t * a.ldy + h * DH + lane + 64 * u] = f32_to_bf16_bits(y);
+  }
 }
 
-// Key ranges: a workgroup covers NW·cw chunks of the pos cached keys (the last one also the t new tokens), cw chosen
-// for about 1024 waves over the cache — one workgroup per CU, each wave streaming its chunks with one in flight.
+// Key ranges: a workgroup covers NW·cw blocks of 64 of the pos cached keys (the last one also the t new tokens), cw
+// chosen for about 1024 waves over the cache — one workgroup per CU, each wave streaming its chunks with one in
+// flight.
 struct Plan { int n_groups, group_len; };
 Plan plan(int pos, int kv, int rows) {
   (void)rows;
@@ -445,22 +559,38 @@ Plan plan(int pos, int kv, int rows) {
     const char* e = getenv("MI_GQA_WAVES");
     return e ? std::max(64LL, atoll(e)) : 1024LL;
   }();
-  const int cw = (int)std::max<long long>(1, ((long long)pos * kv + waves_target * CHUNK - 1) / (waves_target * CHUNK));
-  const int len = NW * cw * CHUNK;
+  const int cw = (int)std::max<long long>(1, ((long long)pos * kv + waves_target * BLOCK - 1) / (waves_target * BLOCK));
+  const int len = NW * cw * BLOCK;
   return {std::max(1, (pos + len - 1) / len), len};
 }
 
 size_t align256(size_t b) { return (b + 255) / 256 * 256; }
 
 struct Layout { size_t qf, qsc, part_o, part_ml, total; };
-Layout layout(int kv, int n_groups, int rows) {
+Layout layout(int kv, int n_groups, int rows, int d) {
   Layout l{};
   l.qf = 0;
-  l.qsc = align256((size_t)kv * MAXROWS * D * sizeof(f16_t));
+  l.qsc = align256((size_t)kv * MAXROWS * d * sizeof(uint16_t));
   l.part_o = l.qsc + align256((size_t)kv * MAXROWS * sizeof(float));
-  l.part_ml = l.part_o + align256((size_t)kv * n_groups * rows * D * sizeof(float));
+  l.part_ml = l.part_o + align256((size_t)kv * n_groups * rows * d * sizeof(float));
   l.total = l.part_ml + align256((size_t)kv * n_groups * rows * 2 * sizeof(float));
   return l;
+}
+
+template <int DH, bool BF>
+int launch(const GqaArgs& a, int rows, hipStream_t s) {
+  hipLaunchKernelGGL((gqa_prep<DH, BF>), dim3(a.heads + a.kv, a.t), dim3(64), 0, s, a);
+  MI_TRY_HIP(hipGetLastError(), "gqa_prep launch");
+  const dim3 grid(a.n_groups, a.kv), block(64 * NW);
+  const int rt = (rows + 15) / 16;
+  if (rt == 1) hipLaunchKernelGGL((gqa_decode<1, DH, BF>), grid, block, 0, s, a);
+  else if (rt == 2) hipLaunchKernelGGL((gqa_decode<2, DH, BF>), grid, block, 0, s, a);
+  else if (rt == 3) hipLaunchKernelGGL((gqa_decode<3, DH, BF>), grid, block, 0, s, a);
+  else hipLaunchKernelGGL((gqa_decode<4, DH, BF>), grid, block, 0, s, a);
+  MI_TRY_HIP(hipGetLastError(), "gqa_decode launch");
+  hipLaunchKernelGGL((gqa_merge<DH>), dim3(a.heads, a.t), dim3(64 * MW), 0, s, a);
+  MI_TRY_HIP(hipGetLastError(), "gqa_merge launch");
+  return MI_OK;
 }
 
 }  // namespace
@@ -470,30 +600,35 @@ Layout layout(int kv, int n_groups, int rows) {
 int plan_pos(const mi_gqa_desc* d) { return d->pos_dev ? std::max(0, d->ctx_max - d->t) : d->pos; }
 
 extern "C" size_t mi_gqa_workspace_bytes(const mi_gqa_desc* d) {
-  if (!d || d->t < 1 || d->kv_heads < 1 || d->heads % d->kv_heads) return 0;
+  if (!d || d->t < 1 || d->kv_heads < 1 || d->heads % d->kv_heads || d->head_dim < 1 || d->head_dim > DMAX) return 0;
   const int rows = d->heads / d->kv_heads * d->t;
-  return layout(d->kv_heads, plan(plan_pos(d), d->kv_heads, rows).n_groups, rows).total;
+  return layout(d->kv_heads, plan(plan_pos(d), d->kv_heads, rows).n_groups, rows, d->head_dim).total;
 }
 
 extern "C" int mi_gqa_decode(const mi_gqa_desc* d, void* stream) {
   MI_REQUIRE(d, "mi_gqa_decode: null descriptor");
-  MI_REQUIRE(d->head_dim == D, "mi_gqa_decode: built for head_dim %d", D);
+  MI_REQUIRE(d->head_dim == 128 || d->head_dim == 256, "mi_gqa_decode: head_dim %d (built for 128 and 256)",
+             d->head_dim);
+  MI_REQUIRE(d->kv_dtype == MI_KV_INT8 || d->kv_dtype == MI_KV_BF16, "mi_gqa_decode: kv_dtype %d", d->kv_dtype);
+  const bool bf = d->kv_dtype == MI_KV_BF16;
   MI_REQUIRE(d->t >= 1 && d->t <= TMAX, "mi_gqa_decode: t=%d must be in 1..%d", d->t, TMAX);
   MI_REQUIRE(d->kv_heads > 0 && d->heads % d->kv_heads == 0, "mi_gqa_decode: heads must be a multiple of kv_heads");
   const int rep = d->heads / d->kv_heads;
   const int rows = rep * d->t;
   MI_REQUIRE(rows <= 64, "mi_gqa_decode: rep·t = %d query rows per KV head exceeds 64", rows);
-  MI_REQUIRE(d->rotary_dim >= 0 && d->rotary_dim <= D && d->rotary_dim % 2 == 0, "mi_gqa_decode: bad rotary_dim");
+  MI_REQUIRE(d->rotary_dim >= 0 && d->rotary_dim <= d->head_dim && d->rotary_dim % 2 == 0,
+             "mi_gqa_decode: bad rotary_dim");
   MI_REQUIRE(d->pos_dev || (d->pos >= 0 && d->pos + d->t <= d->ctx_max), "mi_gqa_decode: pos + t exceeds the cache (%d)",
              d->ctx_max);
-  MI_REQUIRE(d->ctx_max % CHUNK == 0, "mi_gqa_decode: ctx_max must be a multiple of %d", CHUNK);
-  MI_REQUIRE(d->proj && d->k_codes && d->k_scales && d->v_codes && d->v_scales && d->y, "mi_gqa_decode: null pointer");
+  MI_REQUIRE(d->ctx_max % BLOCK == 0, "mi_gqa_decode: ctx_max must be a multiple of %d", BLOCK);
+  MI_REQUIRE(d->proj && d->k_codes && d->v_codes && d->y, "mi_gqa_decode: null pointer");
+  MI_REQUIRE(bf || (d->k_scales && d->v_scales), "mi_gqa_decode: the int8 cache needs k_scales and v_scales");
   MI_REQUIRE(d->rotary_dim == 0 || (d->rope_cos && d->rope_sin), "mi_gqa_decode: RoPE tables missing");
   MI_REQUIRE(!d->qk_norm || (d->q_norm && d->k_norm), "mi_gqa_decode: qk_norm needs q_norm and k_norm");
-  MI_REQUIRE(((uintptr_t)d->k_codes & 15) == 0 && ((uintptr_t)d->v_codes & 7) == 0, "mi_gqa_decode: cache alignment");
+  MI_REQUIRE(((uintptr_t)d->k_codes & 15) == 0 && ((uintptr_t)d->v_codes & 15) == 0, "mi_gqa_decode: cache alignment");
   GqaArgs a{};
-  a.t = d->t; a.heads = d->heads; a.kv = d->kv_heads; a.rot = d->rotary_dim; a.pos = d->pos; a.ctx = d->ctx_max;
-  a.gate = d->gate; a.qk_norm = d->qk_norm; a.rep = rep; a.rows = rows;
+  a.t = d->t; a.heads = d->heads; a.kv = d->kv_heads; a.d = d->head_dim; a.rot = d->rotary_dim; a.pos = d->pos;
+  a.ctx = d->ctx_max; a.gate = d->gate; a.qk_norm = d->qk_norm; a.rep = rep; a.rows = rows;
   const Plan pl = plan(plan_pos(d), d->kv_heads, rows);
   a.pos_dev = d->pos_dev;
   a.done = d->done;
@@ -501,7 +636,9 @@ extern "C" int mi_gqa_decode(const mi_gqa_desc* d, void* stream) {
   a.group_len = pl.group_len;
   a.proj = d->proj; a.ldp = d->ld_proj; a.cosb = d->rope_cos; a.sinb = d->rope_sin;
   a.q_norm = d->q_norm; a.k_norm = d->k_norm; a.eps = d->eps; a.scaling = d->scaling;
-  a.kc = d->k_codes; a.ks = d->k_scales; a.vc = d->v_codes; a.vs = d->v_scales;
+  a.kc = d->k_codes; a.vc = d->v_codes;
+  a.ks = bf ? nullptr : d->k_scales;
+  a.vs = bf ? nullptr : d->v_scales;
   a.y = d->y; a.ldy = d->ld_y;
   const size_t need = mi_gqa_workspace_bytes(d);
   void* ws = d->workspace;
@@ -510,23 +647,13 @@ extern "C" int mi_gqa_decode(const mi_gqa_desc* d, void* stream) {
   } else if (int rc = mi_library_scratch(MI_SCRATCH_GQA, need, static_cast<hipStream_t>(stream), &ws)) {
     return rc;
   }
-  const Layout L = layout(d->kv_heads, a.n_groups, rows);
+  const Layout L = layout(d->kv_heads, a.n_groups, rows, d->head_dim);
   char* wb = static_cast<char*>(ws);
-  a.qf = reinterpret_cast<f16_t*>(wb + L.qf);
+  a.qf = reinterpret_cast<uint16_t*>(wb + L.qf);
   a.qsc = reinterpret_cast<float*>(wb + L.qsc);
   a.part_o = reinterpret_cast<float*>(wb + L.part_o);
   a.part_ml = reinterpret_cast<float*>(wb + L.part_ml);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(gqa_prep, dim3(d->heads + d->kv_heads, d->t), dim3(64), 0, s, a);
-  MI_TRY_HIP(hipGetLastError(), "gqa_prep launch");
-  const dim3 grid(a.n_groups, d->kv_heads), block(64 * NW);
-  const int rt = (rows + 15) / 16;
-  if (rt == 1) hipLaunchKernelGGL(gqa_decode<1>, grid, block, 0, s, a);
-  else if (rt == 2) hipLaunchKernelGGL(gqa_decode<2>, grid, block, 0, s, a);
-  else if (rt == 3) hipLaunchKernelGGL(gqa_decode<3>, grid, block, 0, s, a);
-  else hipLaunchKernelGGL(gqa_decode<4>, grid, block, 0, s, a);
-  MI_TRY_HIP(hipGetLastError(), "gqa_decode launch");
-  hipLaunchKernelGGL(gqa_merge, dim3(d->heads, d->t), dim3(64 * MW), 0, s, a);
-  MI_TRY_HIP(hipGetLastError(), "gqa_merge launch");
-  return MI_OK;
+  if (d->head_dim == 128) return bf ? launch<128, true>(a, rows, s) : launch<128, false>(a, rows, s);
+  return bf ? launch<256, true>(a, rows, s) : launch<256, false>(a, rows, s);
 }

@@ -164,7 +164,8 @@ def gqa_decode(ctx: EmitContext, op: Op):
     scalars = dict(t=proj.shape[0], heads=a["heads"], kv_heads=a["kv_heads"], head_dim=d, rotary_dim=cos.shape[1],
                    pos=0, ctx_max=a["ctx_max"], gate=int(a.get("gate", True)), qk_norm=int(qn is not None),
                    ld_proj=proj.row_stride, eps=float(a.get("eps", 1e-6)),
-                   scaling=float(a.get("scaling", d ** -0.5)), ld_y=y.row_stride)
+                   scaling=float(a.get("scaling", d ** -0.5)), ld_y=y.row_stride,
+                   kv_dtype=int(a.get("kv_dtype", hip.MI_KV_INT8)))
     ptrs = dict(proj=proj, rope_cos=cos, rope_sin=sin, q_norm=qn, k_norm=kn, k_codes=kc, k_scales=ks, v_codes=vc,
                 v_scales=vs, y=y, pos_dev=_state(ctx, "position"), done=_state(ctx, "done"))
     probe = _probe(hip.MiGqaDesc, scalars, [f for f, v in ptrs.items() if v is not None])

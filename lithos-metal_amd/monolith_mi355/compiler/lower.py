@@ -126,14 +126,16 @@ def lower_attn_layer(g: Graph, layer, h: Value, prefix: str) -> Value:
     h1 = act(f"{prefix}.h1", g.t, layer.hidden)
     g.add("gemv", [h, weight(f"{prefix}.qkv", layer.w_qkv.packed)], [proj],
           norm_w=bound(f"{prefix}.norm1", layer.norm_w, "weights"), eps=layer.eps, name=f"{prefix}.qkv")
+    scales = c.k_scales is not None
     g.add("gqa_decode", [proj, bound(f"{prefix}.k_codes", c.k_codes, "state"),
-                         bound(f"{prefix}.k_scales", c.k_scales, "state"),
+                         bound(f"{prefix}.k_scales", c.k_scales, "state") if scales else None,
                          bound(f"{prefix}.v_codes", c.v_codes, "state"),
-                         bound(f"{prefix}.v_scales", c.v_scales, "state"),
+                         bound(f"{prefix}.v_scales", c.v_scales, "state") if scales else None,
                          bound(f"{prefix}.cos", layer.cos, "weights"), bound(f"{prefix}.sin", layer.sin, "weights"),
                          bound(f"{prefix}.q_norm", layer.q_norm, "weights"),
                          bound(f"{prefix}.k_norm", layer.k_norm, "weights")], [o],
           heads=layer.heads, kv_heads=layer.kv, head_dim=layer.d, ctx_max=c.ctx_max, gate=True, eps=layer.eps,
+          kv_dtype=c.kv_dtype,
           name=f"{prefix}.gqa")
     g.add("gemv", [o, weight(f"{prefix}.o_proj", layer.w_o.packed)], [h1], epilogue="residual", residual=h,
           name=f"{prefix}.o_proj")

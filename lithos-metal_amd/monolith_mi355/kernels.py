@@ -277,26 +277,35 @@ def torch_index(a, device):
 
 
 class KVCache:
-    """One attention layer's int8 KV cache in this backend's layout (the reference keeps BF16 ``[ctx_max, Hkv, D]``,
-    ``nn/attention.py:207-209``): ``k_codes [kv, ctx_max, D]`` int8, ``v_codes [kv, ctx_max/64, D, 64]`` int8
-    (transposed inside blocks of 64 keys — key k of a block at position ``V_POS[k]``, the order in which the
-    kernel's score tiles hold the keys — so each 64-key block is 8 KB contiguous), ``k_scales`` / ``v_scales [kv, ctx_max]`` float16 — ``scale = f16(absmax / 127)`` per token
-    and KV head. 288 GB of HBM holds a 262 144-token context for all 16
-    attention layers of the 27B model at 4 KV heads × 128 dims many times over."""
+    """One attention layer's KV cache in this backend's layout: ``k_codes [kv, ctx_max, D]`` and ``v_codes
+    [kv, ctx_max/64, D, 64]`` (transposed inside blocks of 64 keys — key k of a block at position ``V_POS[k]``, the
+    order in which the kernel's score tiles hold the keys — so each block of keys is contiguous). ``dtype="int8"``:
+    int8 codes with ``k_scales`` / ``v_scales [kv, ctx_max]`` float16, ``scale = f16(absmax / 127)`` per token and
+    KV head; ``dtype="bf16"``: the reference's BF16 values (``nn/attention.py:87-89``, ``[ctx_max, Hkv, D]`` there)
+    and no scales. 288 GB of HBM holds a 262 144-token int8 context for all 16 attention layers of the 27B model at
+    4 KV heads × 128 dims many times over."""
 
     BLOCK = 64
     V_POS = np.array([(k >> 5) * 32 + ((k & 15) >> 2) * 8 + ((k >> 4) & 1) * 4 + (k & 3) for k in range(64)])
 
-    def __init__(self, kv_heads: int, ctx_max: int, head_dim: int = 128, device="cuda"):
+    def __init__(self, kv_heads: int, ctx_max: int, head_dim: int = 128, device="cuda", dtype: str = "int8"):
         torch = _torch()
         if ctx_max % self.BLOCK:
             raise ValueError(f"KVCache: ctx_max must be a multiple of {self.BLOCK}")
-        self.kv_heads, self.ctx_max, self.head_dim = kv_heads, ctx_max, head_dim
-        self.k_codes = torch.zeros((kv_heads, ctx_max, head_dim), dtype=torch.int8, device=device)
-        self.v_codes = torch.zeros((kv_heads, ctx_max // self.BLOCK, head_dim, self.BLOCK), dtype=torch.int8,
-                                   device=device)
-        self.k_scales = torch.zeros((kv_heads, ctx_max), dtype=torch.float16, device=device)
-        self.v_scales = torch.zeros((kv_heads, ctx_max), dtype=torch.float16, device=device)
+        if dtype not in ("int8", "bf16"):
+            raise ValueError("KVCache: dtype is 'int8' or 'bf16'")
+        self.kv_heads, self.ctx_max, self.head_dim, self.dtype = kv_heads, ctx_max, head_dim, dtype
+        el = torch.int8 if dtype == "int8" else torch.bfloat16
+        self.k_codes = torch.zeros((kv_heads, ctx_max, head_dim), dtype=el, device=device)
+        self.v_codes = torch.zeros((kv_heads, ctx_max // self.BLOCK, head_dim, self.BLOCK), dtype=el, device=device)
+        self.k_scales = self.v_scales = None
+        if dtype == "int8":
+            self.k_scales = torch.zeros((kv_heads, ctx_max), dtype=torch.float16, device=device)
+            self.v_scales = torch.zeros((kv_heads, ctx_max), dtype=torch.float16, device=device)
+
+    @property
+    def kv_dtype(self) -> int:
+        return hip.MI_KV_BF16 if self.dtype == "bf16" else hip.MI_KV_INT8
 
     def v_codes_token_major(self):
         """``v_codes`` as ``[kv, ctx_max, D]`` (a copy)."""
@@ -306,14 +315,19 @@ class KVCache:
         return self.v_codes.index_select(3, idx).permute(0, 1, 3, 2).reshape(kv, nb * b, d)
 
     def set_v_token_major(self, codes):
-        """Store ``codes [kv, ctx_max, D]`` int8 into the blocked ``v_codes``."""
+        """Store ``codes [kv, ctx_max, D]`` (int8 codes or BF16 values) into the blocked ``v_codes``."""
         kv, nb, d, b = self.v_codes.shape
         blocks = codes.reshape(kv, nb, b, d).permute(0, 1, 3, 2)           # [kv, nb, D, key]
         self.v_codes[..., torch_index(self.V_POS, self.v_codes.device)] = blocks
 
     @property
     def nbytes(self) -> int:
-        return sum(int(t.numel() * t.element_size()) for t in (self.k_codes, self.v_codes, self.k_scales, self.v_scales))
+        return sum(int(t.numel() * t.element_size()) for t in (self.k_codes, self.v_codes, self.k_scales, self.v_scales)
+                   if t is not None)
+
+    def bytes_per_key(self) -> int:
+        """HBM bytes one cached key costs a step (its K and V rows and scales, every KV head)."""
+        return self.kv_heads * (4 * self.head_dim if self.dtype == "bf16" else 2 * self.head_dim + 4)
 
 
 def gqa_decode(proj, cache: KVCache, pos, *, heads: int, rope_cos, rope_sin, gate: bool = True,
@@ -322,7 +336,8 @@ def gqa_decode(proj, cache: KVCache, pos, *, heads: int, rope_cos, rope_sin, gat
     """``gqa_decode`` + ``gqa_merge`` (``ops/attention.py``; ``GQAAttention.mix``, ``nn/attention.py:215-243``) for
     ``proj [T, N1]`` bf16 (``q|gate`` per head, then ``k``, ``v``): q/k norm (``q_norm``/``k_norm`` = the (1 + w)
     float32 weights, both or neither), partial RoPE from the BF16 tables ``[ctx_max, rotary_dim]``, the new k/v
-    quantized into ``cache`` at ``pos..pos+T``, attention over the cache, × σ(gate). Returns ``[T, heads·D]`` bf16.
+    appended to ``cache`` (int8: quantized; bf16: as they are) at ``pos..pos+T``, attention over the cache,
+    × σ(gate). Head dim 128 or 256. Returns ``[T, heads·D]`` bf16.
     ``pos`` is an int, or a one-element int32 device tensor the kernels read (a step program's StepState position:
     the same launch serves every step of a replayed graph). ``done``: a step program's stop flag (one-element device
     int32): once set, nothing is appended to the cache and ``out`` is not written. ``workspace``: a uint8 tensor of
@@ -359,7 +374,7 @@ def gqa_decode(proj, cache: KVCache, pos, *, heads: int, rope_cos, rope_sin, gat
                          q_norm=hip.ptr(q_norm), k_norm=hip.ptr(k_norm), eps=eps,
                          scaling=d ** -0.5 if scaling is None else scaling, k_codes=hip.ptr(cache.k_codes),
                          k_scales=hip.ptr(cache.k_scales), v_codes=hip.ptr(cache.v_codes),
-                         v_scales=hip.ptr(cache.v_scales), y=hip.ptr(out), ld_y=out.stride(0),
+                         v_scales=hip.ptr(cache.v_scales), y=hip.ptr(out), ld_y=out.stride(0), kv_dtype=cache.kv_dtype,
                          workspace=hip.ptr(workspace),
                          workspace_bytes=0 if workspace is None else workspace.numel() * workspace.element_size(),
                          pos_dev=hip.ptr(pos_dev), done=hip.ptr(done))

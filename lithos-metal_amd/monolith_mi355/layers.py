@@ -227,10 +227,11 @@ class GdnDecoderLayer:
 
 class AttnDecoderLayer:
     """Gated GQA layer (hidden 5120, 24 query / 4 KV heads of 128, partial RoPE 64 at θ = 1e6, q/k norm, output
-    gate, int8 KV cache of ``ctx`` tokens, MLP 17408). Projection rows q|gate per head, then k, v."""
+    gate, KV cache of ``ctx`` tokens — int8, or the reference's BF16 with ``kv_dtype="bf16"`` — MLP 17408; head dim
+    128 or 256). Projection rows q|gate per head, then k, v."""
 
     def __init__(self, *, hidden=5120, heads=24, kv_heads=4, head_dim=128, rotary_dim=64, theta=1e6, ctx=32768,
-                 inter=17408, eps=1e-6, device="cuda", seed=0):
+                 inter=17408, eps=1e-6, device="cuda", seed=0, kv_dtype="int8"):
         torch = _torch()
         gen = torch.Generator(device=device)
         gen.manual_seed(seed)
@@ -242,14 +243,22 @@ class AttnDecoderLayer:
         self.q_norm = (1.0 + torch.randn(head_dim, generator=gen, device=device) * 0.1).to(torch.bfloat16).float()
         self.k_norm = (1.0 + torch.randn(head_dim, generator=gen, device=device) * 0.1).to(torch.bfloat16).float()
         self.cos, self.sin = kernels.rope_tables(theta, rotary_dim, ctx, device=device)
-        self.cache = kernels.KVCache(kv_heads, ctx, head_dim, device=device)
+        self.cache = kernels.KVCache(kv_heads, ctx, head_dim, device=device, dtype=kv_dtype)
         self.mlp = GatedMLP(hidden, inter, gen, device, eps)
         self._bufs: Dict[int, tuple] = {}
 
     def fill_cache(self, n: int, gen=None):
-        """Random int8 codes and f16 scales (N(0, 1) K/V quantized per token) in the first ``n`` positions."""
+        """The first ``n`` positions: random int8 codes and f16 scales (N(0, 1) K/V quantized per token), or BF16
+        N(0, 1) values."""
         torch = _torch()
         c = self.cache
+        if c.dtype == "bf16":
+            c.k_codes[:, :n] = torch.randn(c.k_codes[:, :n].shape, generator=gen, device=c.k_codes.device).to(
+                torch.bfloat16)
+            nb = -(-n // 64)
+            c.v_codes[:, :nb] = torch.randn(c.v_codes[:, :nb].shape, generator=gen, device=c.v_codes.device).to(
+                torch.bfloat16)
+            return
         c.k_codes[:, :n].random_(-127, 128, generator=gen)
         c.v_codes[:, : -(-n // 64)].random_(-127, 128, generator=gen)
         c.k_scales[:, :n] = 3.0 / 127
@@ -283,9 +292,8 @@ class AttnDecoderLayer:
         return self.mlp(h1, act=act, out=out)
 
     def mixer_bytes(self, m: int, pos: int) -> int:
-        n = pos + m
-        return (n * self.kv * (2 * self.d + 4) + m * self.n_proj * 2 + m * self.heads * self.d * 2
-                + m * self.kv * (2 * self.d + 4))
+        per_key = self.cache.bytes_per_key()
+        return (pos + m) * per_key + m * self.n_proj * 2 + m * self.heads * self.d * 2 + m * per_key
 
     def bytes_per_step(self, m: int, pos: int) -> int:
         return (_gemv_bytes(self.n_proj, self.hidden, m) + self.hidden * 4 + self.mixer_bytes(m, pos)

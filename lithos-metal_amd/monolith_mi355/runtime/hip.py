@@ -48,6 +48,9 @@ class MiGdnDesc(C.Structure):
                 ("t_dev", C.c_void_p), ("done", C.c_void_p), ("step", C.c_void_p)]
 
 
+MI_KV_INT8, MI_KV_BF16 = 0, 1
+
+
 class MiGqaDesc(C.Structure):
     _fields_ = [("t", C.c_int32), ("heads", C.c_int32), ("kv_heads", C.c_int32), ("head_dim", C.c_int32),
                 ("rotary_dim", C.c_int32), ("pos", C.c_int32), ("ctx_max", C.c_int32), ("gate", C.c_int32),
@@ -56,7 +59,7 @@ class MiGqaDesc(C.Structure):
                 ("scaling", C.c_float), ("k_codes", C.c_void_p), ("k_scales", C.c_void_p), ("v_codes", C.c_void_p),
                 ("v_scales", C.c_void_p), ("y", C.c_void_p), ("ld_y", C.c_int32), ("workspace", C.c_void_p),
                 ("workspace_bytes", C.c_size_t), ("pos_dev", C.c_void_p),
-                ("done", C.c_void_p)]
+                ("done", C.c_void_p), ("kv_dtype", C.c_int32)]
 
 
 class MiNormDesc(C.Structure):

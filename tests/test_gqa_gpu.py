@@ -206,3 +206,88 @@ def test_gqa_rejects_bad_descriptors():
         assert lib.mi_gqa_decode(C.byref(d), None) == 1, kw
         assert hip.last_error().startswith("mi_gqa_decode")
     assert lib.mi_gqa_workspace_bytes(C.byref(hip.MiGqaDesc(**base))) > 0
+
+
+# ---- head dim 256 and the reference's BF16 cache ---------------------------------------------------------------------
+def _run_geometry(torch, rng, ctx, pos, t, d, kv_dtype, qk_norm=True, steps=2, device_pos=False, rot=64):
+    """One attention layer's cache of head dim ``d`` (int8 or BF16) against ``ON.gqa_mix`` / ``ON.gqa_mix_bf16``
+    (the reference's layer over its BF16 cache): new rows exact (BF16: the k/v values themselves; with q/k norm a
+    BF16 rounding may flip on ≤ 0.1 % of them, by one step), the rest of the cache untouched, output bars as above."""
+    from monolith_mi355 import kernels
+    cfg = dict(heads=H, kv_heads=KV, head_dim=d, rotary_dim=rot, theta=1e6, eps=EPS, gate=True, qk_norm=qk_norm,
+               q_norm=rbf(rng.standard_normal(d) * 0.1), k_norm=rbf(rng.standard_normal(d) * 0.1))
+    cos, sin = kernels.rope_tables(1e6, rot, ctx)
+    cfg["tables"] = (from_dev_bf16(cos), from_dev_bf16(sin))
+    cache = kernels.KVCache(KV, ctx, d, dtype=kv_dtype)
+    if kv_dtype == "bf16":
+        kf = np.zeros((ctx, KV, d), np.float32)
+        vf = np.zeros((ctx, KV, d), np.float32)
+        kf[:pos] = rbf(rng.standard_normal((pos, KV, d)))
+        vf[:pos] = rbf(rng.standard_normal((pos, KV, d)))
+        cache.k_codes.copy_(to_dev_bf16(torch, kf.transpose(1, 0, 2).copy()))
+        cache.set_v_token_major(to_dev_bf16(torch, vf.transpose(1, 0, 2).copy()))
+    else:
+        kc = np.zeros((ctx, KV, d), np.int8)
+        vc = np.zeros((ctx, KV, d), np.int8)
+        ks = np.zeros((ctx, KV), np.float16)
+        vs = np.zeros((ctx, KV), np.float16)
+        if pos:
+            kc[:pos], ks[:pos] = ON.kv_quantize(rbf(rng.standard_normal((pos, KV, d))))
+            vc[:pos], vs[:pos] = ON.kv_quantize(rbf(rng.standard_normal((pos, KV, d))))
+        _upload(torch, cache, kc, ks, vc, vs)
+    qn = torch.from_numpy((1 + cfg["q_norm"]).astype(np.float32)).cuda() if qk_norm else None
+    kn = torch.from_numpy((1 + cfg["k_norm"]).astype(np.float32)).cuda() if qk_norm else None
+    n1 = H * 2 * d + 2 * KV * d
+    for _ in range(steps):
+        proj = rbf(rng.standard_normal((t, n1)))
+        if kv_dtype == "bf16":
+            ref = ON.gqa_mix_bf16(proj, kf, vf, pos, **cfg)
+        else:
+            ref = ON.gqa_mix(proj, kc, ks, vc, vs, pos, **cfg)
+        p_arg = torch.tensor([pos], dtype=torch.int32, device="cuda") if device_pos else pos
+        y = kernels.gqa_decode(to_dev_bf16(torch, proj), cache, p_arg, heads=H, rope_cos=cos, rope_sin=sin,
+                               q_norm=qn, k_norm=kn, eps=EPS)
+        torch.cuda.synchronize()
+        if kv_dtype == "bf16":
+            gk = from_dev_bf16(cache.k_codes).transpose(1, 0, 2)
+            gv = from_dev_bf16(cache.v_codes_token_major()).transpose(1, 0, 2)
+            for name, g, w in (("k", gk, kf), ("v", gv, vf)):
+                assert np.array_equal(g[:pos], w[:pos]) and np.array_equal(g[pos + t:], w[pos + t:]), name
+                gn, wn = g[pos: pos + t], w[pos: pos + t]
+                if name == "v" or not qk_norm:
+                    assert np.array_equal(gn, wn), name
+                else:
+                    assert np.mean(gn == wn) >= 0.999 and np.all(np.abs(gn - wn) <= 2 ** -7 * np.abs(wn)), name
+        else:
+            _check_cache(_download(cache), (kc, ks, vc, vs), pos, t, exact=not qk_norm)
+        _check_out(from_dev_bf16(y), ref, pos + t)
+        pos += t
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("d,kv_dtype", [(128, "bf16"), (256, "bf16"), (256, "int8")])
+@pytest.mark.parametrize("ctx,pos,t", [(1024, 300, 1), (1024, 290, 8), (4096, 4000, 1), (4096, 3990, 8)])
+def test_gqa_decode_head_dim_and_bf16_cache(torch_gpu, d, kv_dtype, ctx, pos, t):
+    print(f"gqa d={d} cache={kv_dtype} ctx={ctx} pos={pos} t={t}", flush=True)
+    _run_geometry(torch_gpu, np.random.default_rng(d + ctx + pos + t), ctx, pos, t, d, kv_dtype)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("d,kv_dtype", [(128, "bf16"), (256, "int8")])
+def test_gqa_decode_head_dim_and_bf16_cache_device_position(torch_gpu, d, kv_dtype):
+    print(f"gqa d={d} cache={kv_dtype} device position", flush=True)
+    _run_geometry(torch_gpu, np.random.default_rng(d + 5), 2048, 1500, 3, d, kv_dtype, qk_norm=False,
+                  device_pos=True, rot=128)
+
+
+def test_gqa_rejects_bad_kv_dtype():
+    import ctypes as C
+    from monolith_mi355.runtime import hip
+    lib = hip.load()
+    base = dict(t=1, heads=24, kv_heads=4, head_dim=256, rotary_dim=64, pos=10, ctx_max=1024, gate=1, proj=256,
+                ld_proj=14336, rope_cos=256, rope_sin=256, k_codes=256, v_codes=256, y=256, ld_y=6144, eps=1e-6,
+                scaling=0.0625, kv_dtype=2)
+    assert lib.mi_gqa_decode(C.byref(hip.MiGqaDesc(**base)), None) == 1 and "kv_dtype" in hip.last_error()
+    d = hip.MiGqaDesc(**{**base, "kv_dtype": 0})           # the int8 cache needs its scales
+    assert lib.mi_gqa_decode(C.byref(d), None) == 1 and "scales" in hip.last_error()
+    assert lib.mi_gqa_workspace_bytes(C.byref(hip.MiGqaDesc(**{**base, "kv_dtype": 1}))) > 0
