@@ -853,7 +853,7 @@ void gemv_rowp(Args a) {
   }
 }
 
-// ---- gemv_rowm: 3 <= M <= 16, NVFP4 and FP8 --------------------------------------------------------------------
+// ---- gemv_rowm: 3 <= M <= 16, NVFP4, FP8 and INT4 ---------------------------------------------------------------
 // The gemv_row wave layout on the matrix cores, over several tiles per workgroup. Workgroup = S waves over tiles
 // blockIdx.x + j·G (j < ntl) and K split blockIdx.z; wave w owns a 512-column slice (4 NVFP4 / 8 FP8 chunks) of
 // every one of them. The
@@ -861,13 +861,17 @@ void gemv_rowp(Args a) {
 // v_mfma_f32_16x16x32_f16 (token = A row; each token power-of-two scaled into F16 range over the wave's slice;
 // normalized first when the input norm is fused); the weights are the B operand, decoded exactly to F16. Each wave
 // issues tile j + 1 as soon as tile j is consumed (the operands leave no VGPRs for a second tile in flight). A
-// tile's K slices meet in LDS after the last tile, in the gemv_row order.
+// tile's K slices meet in LDS after the last tile, in the gemv_row order. INT4: the codes decode to exact F16
+// integers, the activations take the codes' column order (int4_perm8) and each 64-column group's dot product is
+// scaled and offset by its (scale, bias) pair with the token's Σx over the group (held per lane for the launch).
 // LDS: nw[K] (fused norm) | stat[S][16] | red[rt][S][16 tokens][16 rows].
 template <int FMT>
 __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
-  constexpr int KC = chunk_cols(FMT), KW = 512 / KC;   // a wave's slice is 512 columns: 4 NVFP4 / 8 FP8 chunks
+  constexpr int KC = chunk_cols(FMT), KW = 512 / KC;   // a wave's slice is 512 columns: 4 NVFP4 / INT4, 8 FP8 chunks
   constexpr int SPC = KC / 32;                  // MFMA steps per chunk: the lane's KC/4 columns, 8 per step
-  static_assert(FMT == FMT_NVFP4 || FMT == FMT_FP8, "gemv_rowm: NVFP4 or FP8");
+  static_assert(FMT == FMT_NVFP4 || FMT == FMT_FP8 || FMT == FMT_INT4, "gemv_rowm: NVFP4, FP8 or INT4");
+  constexpr bool I4 = FMT == FMT_INT4;
+  constexpr int UB = I4 ? UNIT_Q : 1024;        // bytes from one chunk's codes to the next
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -885,10 +889,12 @@ __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
   auto tile_of = [&](int j) { return (int)blockIdx.x + j * G; };
   float* nws = reinterpret_cast<float*>(smem);                                  // [K] when the norm is fused
   float* stat = nws + (a.norm_w ? a.k : 0);                                    // [S][16]
-  float* red = stat + S * 16;                                                  // [rt][S][16][16]
+  float* sxl = stat + S * 16;                                                  // INT4: [S][KW][2][16]
+  float* red = sxl + (I4 ? S * KW * 2 * 16 : 0);                               // [rt][S][16][16]
 
   // ---- the first tile's weights, then the activations ------------------------------------------------------------
-  const long long c0_off = FMT == FMT_NVFP4 ? nv_code_off(c0) : (long long)c0 * UNIT_B;
+  const long long c0_off = FMT == FMT_NVFP4 ? nv_code_off(c0) : (long long)c0 * unit_bytes(FMT);
+  uint2 sb0[I4 ? KW : 1];                       // INT4: the (scale, bias) pairs of row m_row's two groups per chunk
   auto issue = [&](uint4 (&u)[KW], uint4& sv, int j) {
     const uint8_t* tbase = wmat + (long long)tile_of(j) * a.tile_stride;
     if constexpr (FMT == FMT_NVFP4) {
@@ -904,21 +910,26 @@ __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
       sv = uint4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
-    for (int cc = 0; cc < KW; ++cc)             // units of 1 KiB codes
-      if (cc < kw) u[cc] = *reinterpret_cast<const uint4*>(tbase + c0_off + cc * 1024 + 16 * lane);
+    for (int cc = 0; cc < KW; ++cc)             // 1 KiB of codes per chunk
+      if (cc < kw) {
+        u[cc] = *reinterpret_cast<const uint4*>(tbase + c0_off + cc * UB + 16 * lane);
+        if constexpr (I4) sb0[cc] = *reinterpret_cast<const uint2*>(tbase + c0_off + cc * UB + 1024 + 8 * (lane & 15));
+      }
   };
   uint4 u0[KW], s0;
   issue(u0, s0, 0);
 
-  // x[token m_row][c0·KC + cc·KC + (KC/4)·g + 8s + (0..7)]: the A operand of step s of chunk cc
+  // x[token m_row][c0·KC + cc·KC + col(g, s) + (0..7)]: the A operand of step s of chunk cc, col(g, s) =
+  // (KC/4)·g + 8s (NVFP4 / FP8) or 32s + 8g (INT4: the codes' column order in a unit)
   const bool real = m_row < cnt;
+  auto xcol = [&](int s) { return I4 ? 32 * s + 8 * g : (KC / 4) * g + 8 * s; };
   uint4 xa[KW][SPC];
-  const uint16_t* xrow = a.x + (long long)(real ? m_row : 0) * a.ldx + c0 * KC + (KC / 4) * g;
+  const uint16_t* xrow = a.x + (long long)(real ? m_row : 0) * a.ldx + c0 * KC;
 #pragma unroll
   for (int cc = 0; cc < KW; ++cc)
 #pragma unroll
     for (int s = 0; s < SPC; ++s)
-      xa[cc][s] = cc < kw ? *reinterpret_cast<const uint4*>(xrow + cc * KC + 8 * s) : uint4{0u, 0u, 0u, 0u};
+      xa[cc][s] = cc < kw ? *reinterpret_cast<const uint4*>(xrow + cc * KC + xcol(s)) : uint4{0u, 0u, 0u, 0u};
   if (!real) {                                // padding token rows: zero operands (their loads read row 0)
 #pragma unroll
     for (int cc = 0; cc < KW; ++cc)
@@ -951,7 +962,7 @@ __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
 #pragma unroll
       for (int s = 0; s < SPC; ++s) {
         if (cc >= kw) break;
-        const float* wv = nws + (c0 + cc) * KC + (KC / 4) * g + 8 * s;
+        const float* wv = nws + (c0 + cc) * KC + xcol(s);
         const float4 w0 = *reinterpret_cast<const float4*>(wv), w1 = *reinterpret_cast<const float4*>(wv + 4);
         const float ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
         uint32_t* vv = reinterpret_cast<uint32_t*>(&xa[cc][s]);
@@ -985,10 +996,22 @@ __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
 #pragma unroll
     for (int s = 0; s < SPC; ++s) {
       uint32_t* vv = reinterpret_cast<uint32_t*>(&xa[cc][s]);
+      if constexpr (I4) {                     // element e of the operand = column int4_perm8(e)
+        uint16_t hv[8];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const f16x2 h = {(f16_t)(bf16_bits_to_f32(vv[q] & 0xFFFFu) * inv), (f16_t)(bf16_bits_to_f32(vv[q] >> 16) * inv)};
-        vv[q] = __builtin_bit_cast(uint32_t, h);
+        for (int q = 0; q < 4; ++q) { hv[2 * q] = vv[q] & 0xFFFFu; hv[2 * q + 1] = vv[q] >> 16; }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f16x2 h = {(f16_t)(bf16_bits_to_f32(hv[int4_perm8(2 * q)]) * inv),
+                           (f16_t)(bf16_bits_to_f32(hv[int4_perm8(2 * q + 1)]) * inv)};
+          vv[q] = __builtin_bit_cast(uint32_t, h);
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f16x2 h = {(f16_t)(bf16_bits_to_f32(vv[q] & 0xFFFFu) * inv), (f16_t)(bf16_bits_to_f32(vv[q] >> 16) * inv)};
+          vv[q] = __builtin_bit_cast(uint32_t, h);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);      // one operand at a time: no FP32 copies of the whole slice
     }
@@ -996,9 +1019,29 @@ __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
   float ps[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) ps[i] = __shfl(psc, 4 * g + i, 64);
+  // INT4: Σx (prescaled F16) per 64-column group — steps {0, 1} and {2, 3} of each chunk — per token (the sum over
+  // its four k-group lanes), kept in the wave's LDS rows: tile_mma reads those of its output tokens 4g + i
+  float* sxw = sxl + wave * KW * 2 * 16;
+  if constexpr (I4) {
+#pragma unroll
+    for (int cc = 0; cc < KW; ++cc)
+#pragma unroll
+      for (int gp = 0; gp < 2; ++gp) {
+        float sx = 0.0f;
+#pragma unroll
+        for (int s = 2 * gp; s < 2 * gp + 2; ++s) {
+          const f16x8 h = __builtin_bit_cast(f16x8, xa[cc][s]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) sx += (float)h[e];
+        }
+        sx = add_xor32(add_xor16(cc < kw ? sx : 0.0f));
+        if (g == 0) sxw[(cc * 2 + gp) * 16 + m_row] = sx;
+      }
+    wave_lds_sync();
+  }
 
   // ---- tile by tile: 16 MFMAs over the slice, the partial (tokens × rows) into LDS ----------------------------------
-  auto tile_mma = [&](const uint4 (&u)[KW], const uint4 sv, int jt) {
+  auto tile_mma = [&](const uint4 (&u)[KW], const uint4 sv, const uint2 (&sbs)[I4 ? KW : 1], int jt) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int cc = 0; cc < KW; ++cc) {
@@ -1017,6 +1060,22 @@ __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
           const f16x8 bv = nvfp4_decode8(dw[s], s < 2 ? e0 : e1, s < 2 ? m0 : m1);
           acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, xa[cc][s]), bv, acc, 0, 0, 0);
         }
+      } else if constexpr (I4) {                // the two 64-column groups, each scaled and offset on its own
+        f32x4 da = {0.f, 0.f, 0.f, 0.f}, db = {0.f, 0.f, 0.f, 0.f};
+        da = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, xa[cc][0]), int4_decode8(dw[0]), da, 0, 0, 0);
+        da = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, xa[cc][1]), int4_decode8(dw[1]), da, 0, 0, 0);
+        db = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, xa[cc][2]), int4_decode8(dw[2]), db, 0, 0, 0);
+        db = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, xa[cc][3]), int4_decode8(dw[3]), db, 0, 0, 0);
+        const uint2 sb = sbs[cc];
+        const float sca = bf16_bits_to_f32(sb.x & 0xFFFFu), bia = bf16_bits_to_f32(sb.x >> 16);
+        const float scb = bf16_bits_to_f32(sb.y & 0xFFFFu), bib = bf16_bits_to_f32(sb.y >> 16);
+        const f32x4 sxa = *reinterpret_cast<const f32x4*>(sxw + (cc * 2) * 16 + 4 * g);
+        const f32x4 sxb = *reinterpret_cast<const f32x4*>(sxw + (cc * 2 + 1) * 16 + 4 * g);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[i] = fmaf(sca, da[i], fmaf(bia, sxa[i], acc[i]));
+          acc[i] = fmaf(scb, db[i], fmaf(bib, sxb[i], acc[i]));
+        }
       } else {                                  // FP8: the lane's 16 codes, 8 per step
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
@@ -1031,7 +1090,7 @@ __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
     for (int i = 0; i < 4; ++i) rp[(4 * g + i) * 16 + m_row] = active ? acc[i] * ps[i] : 0.0f;
   };
   for (int j = 0; j < ntl; ++j) {
-    tile_mma(u0, s0, j);
+    tile_mma(u0, s0, sb0, j);
     if (j + 1 < ntl) issue(u0, s0, j + 1);
   }
 
@@ -1760,7 +1819,7 @@ Plan plan_tk(const mi_gemv_desc* d, int fmt, int chunks, int n_tiles, int groups
   return best;
 }
 
-// gemv_rowm (3 <= M <= 16, NVFP4 / FP8): waves of 512 columns over K splits of at most 12 waves; as many
+// gemv_rowm (3 <= M <= 16, NVFP4 / FP8 / INT4): waves of 512 columns over K splits of at most 12 waves; as many
 // workgroups as are resident at once, each over rt tiles
 template <int FMT> __global__ void gemv_rowm(Args a);
 int rowm_blocks_per_cu(int fmt, int threads, size_t lds) {
@@ -1776,8 +1835,9 @@ int rowm_blocks_per_cu(int fmt, int threads, size_t lds) {
     if (it != cache.end()) return it->second;
   }
   int n = 0;
-  const void* kern = fmt == FMT_FP8 ? reinterpret_cast<const void*>(gemv_rowm<FMT_FP8>)
-                                    : reinterpret_cast<const void*>(gemv_rowm<FMT_NVFP4>);
+  const void* kern = fmt == FMT_FP8    ? reinterpret_cast<const void*>(gemv_rowm<FMT_FP8>)
+                     : fmt == FMT_INT4 ? reinterpret_cast<const void*>(gemv_rowm<FMT_INT4>)
+                                       : reinterpret_cast<const void*>(gemv_rowm<FMT_NVFP4>);
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, threads, lds) !=
           hipSuccess || n <= 0) {
     (void)hipGetLastError();
@@ -1790,7 +1850,8 @@ int rowm_blocks_per_cu(int fmt, int threads, size_t lds) {
 
 Plan plan_rowm(const mi_gemv_desc* d, int chunks, int n_tiles) {
   Plan best{};
-  if ((d->format != FMT_NVFP4 && d->format != FMT_FP8) || d->groups || d->gnorm_w || d->m < 3 || d->m > 16 ||
+  if ((d->format != FMT_NVFP4 && d->format != FMT_FP8 && d->format != FMT_INT4) || d->groups || d->gnorm_w ||
+      d->m < 3 || d->m > 16 ||
       (d->format == FMT_NVFP4 && chunks % 4))     // NVFP4 slices start on half scale groups
     return best;
   const int kw = 512 / chunk_cols(d->format);    // chunks per wave (512 columns)
@@ -1803,7 +1864,8 @@ Plan plan_rowm(const mi_gemv_desc* d, int chunks, int n_tiles) {
   if (ks > 1) kc = (kc + 7) / 8 * 8;             // splits on scale-group boundaries (whole waves for FP8)
   if (kc > 12 * kw || (ks > 1 && (ks - 1) * kc >= chunks)) return best;
   const int S = (kc + kw - 1) / kw;
-  const size_t fixed = (d->norm_w ? (size_t)d->k * 4 : 0) + (size_t)S * 16 * 4;
+  const size_t fixed = (d->norm_w ? (size_t)d->k * 4 : 0) + (size_t)S * 16 * 4 +
+                       (d->format == FMT_INT4 ? (size_t)S * (512 / chunk_cols(FMT_INT4)) * 2 * 16 * 4 : 0);
   const size_t per_tile = (size_t)S * 16 * 16 * 4;
   const int per_cu = rowm_blocks_per_cu(d->format, 64 * S, fixed + 4 * per_tile);
   const long long slots = std::max<long long>(1, (long long)cu_count() * std::max(per_cu, 1) / ks);
@@ -1824,12 +1886,16 @@ Plan make_plan(const mi_gemv_desc* d) {
   const int n_tiles = (d->n + 15) / 16;
   const int groups = d->groups ? d->max_groups : 1;
   const int rows = d->groups ? std::min(16, d->m) : d->m;   // a group holds at most one pair per token
-  const char* fk = getenv("MI_GEMV_KERNEL");                 // "row" / "tk" pins the kernel (tuning sweeps)
-  if (rows <= 2 && !(fk && fk[0] == 't')) {
+  const char* fk = getenv("MI_GEMV_KERNEL");                 // "row" / "tk" / "rowm" pins the kernel (sweeps)
+  const bool pin_tk = fk && fk[0] == 't', pin_rowm = fk && strcmp(fk, "rowm") == 0;
+  if (rows <= 2 && !pin_tk) {
     const Plan p = plan_row(d, fmt, chunks, rows, n_tiles, groups);
     if (p.kernel) return p;
   }
-  if (rows > 2 && !(fk && fk[0] == 't')) {
+  // INT4 at M >= 3 runs on gemv_tk unless gemv_rowm is pinned: measured on the 27B gate|up shape at M = 8,
+  // gemv_rowm takes 37.4 µs against gemv_tk's 35.5 (its per-group scale / bias work is VALU time the NVFP4 decode
+  // does not have), although gemv_tk moves 11 MB of split partials more
+  if (rows > 2 && !pin_tk && (fmt != FMT_INT4 || pin_rowm)) {
     const Plan p = plan_rowm(d, chunks, n_tiles);
     if (p.kernel) return p;
   }
@@ -1871,7 +1937,7 @@ void launch_row_k(const Args& a, const Plan& p, dim3 g, hipStream_t s) {
 
 template <int FMT>
 void launch(const Args& a, const Plan& p, int groups, hipStream_t s) {
-  if constexpr (FMT == FMT_NVFP4 || FMT == FMT_FP8) {
+  if constexpr (FMT == FMT_NVFP4 || FMT == FMT_FP8 || FMT == FMT_INT4) {
     if (p.kernel == 3) {
       allow_lds(gemv_rowm<FMT>);
       hipLaunchKernelGGL(gemv_rowm<FMT>, dim3(p.G, 1, p.ks), dim3(64 * p.S), p.lds_bytes, s, a);

@@ -243,17 +243,19 @@ def test_gemv_gated_head_norm(torch_gpu, fmt, mtok, plan, rng, monkeypatch):
     assert chk.ok_rounded() and chk.within, (fmt, mtok, plan, chk)
 
 
-@pytest.mark.parametrize("fmt", ["nvfp4", "fp8_e4m3"])
+@pytest.mark.parametrize("fmt", ["nvfp4", "fp8_e4m3", "int4_affine"])
 @pytest.mark.parametrize("mtok", [3, 8, 16])
 @pytest.mark.parametrize("n,k,plan", [(1040, 2048, None), (1040, 2048, "1,3"), (336, 6144, "2,1"),
                                       (336, 6144, "3,2"), (5120, 17408, None)])
 @pytest.mark.parametrize("epi", [None, "residual", "silu_mul"])
 def test_gemv_rowm_plans(torch_gpu, fmt, mtok, n, k, plan, epi, rng, monkeypatch):
-    """The M >= 3 NVFP4 kernel (K slices per wave on the matrix cores, several tiles per workgroup) over forced
-    K splits and tiles per workgroup, against the oracle."""
+    """The M >= 3 kernel (K slices per wave on the matrix cores, several tiles per workgroup; NVFP4, FP8, INT4) over
+    forced K splits and tiles per workgroup, against the oracle."""
     from monolith_mi355 import kernels
     if plan:
         monkeypatch.setenv("MI_GEMV_ROWM", plan)
+    if fmt == "int4_affine":                       # INT4 takes gemv_rowm only when it is pinned
+        monkeypatch.setenv("MI_GEMV_KERNEL", "rowm")
     m = _matrix(fmt, n, k, rng)
     x = rbf(rng.standard_normal((mtok, k)))
     res = rbf(rng.standard_normal((mtok, n)))

@@ -58,10 +58,12 @@ def test_one_hot_columns_are_the_dequantized_weights(torch_gpu, fmt, plan, monke
     mtok, env = PLANS[plan]
     if fmt == "fp8_e4m3" and plan.startswith("tk"):
         pytest.skip("gemv_tk has no FP8 path: FP8 runs on gemv_row / gemv_rowm")
-    if fmt in ("int4_affine", "bf16") and plan.startswith("rowm"):
-        pytest.skip("gemv_rowm takes NVFP4 and FP8; INT4 / BF16 at M >= 3 run on gemv_tk")
+    if fmt == "bf16" and plan.startswith("rowm"):
+        pytest.skip("gemv_rowm takes NVFP4, FP8 and INT4; BF16 at M >= 3 runs on gemv_tk")
     for key, val in env.items():
         monkeypatch.setenv(key, val)
+    if fmt == "int4_affine" and plan.startswith("rowm"):      # INT4 takes gemv_rowm only when it is pinned
+        monkeypatch.setenv("MI_GEMV_KERNEL", "rowm")
     n = 40
     k = 3072 if "split" in plan else 1024
     rng = np.random.default_rng(abs(hash((fmt, plan))) % 2 ** 32)
