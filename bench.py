@@ -269,7 +269,7 @@ def main():
             for m in (1, 8):
                 x = torch.randn(m, 2048, generator=gen, device=dev).to(torch.bfloat16)
                 ms = timed_graph(lambda i: blocks[i % 2](x), args.steps, args.warmup, stream)
-                distinct = [len(set(b.buffers(m)[1][0].flatten().tolist())) for b in blocks]
+                distinct = [len(set(b.buffers(m)[1][0][:, :b.top_k].flatten().tolist())) for b in blocks]
                 nbytes = sum(b.bytes_per_step(m, d) for b, d in zip(blocks, distinct)) // len(blocks)
                 out[f"moe_m{m}"] = (ms, nbytes)
                 moe_experts = distinct

@@ -138,6 +138,11 @@ typedef struct mi_gemv_desc {
   const uint16_t* gnorm_z;   /* z [m][ld_gnorm_z] BF16, same rows as x */
   int32_t ld_gnorm_z;
   float gnorm_eps;
+  /* grouped mode: the MoE shared expert stacked after the routed experts (its index, >= 1; 0 = none) runs in the
+   * same launch as a group of its own with its own epilogue — the shared expert's gate|up is one BF16 rounding of
+   * silu(gate)·up where the routed experts round gate and up first (nn/moe.py:327-337 against nn/mlp.py:25-26) */
+  int32_t shared_expert;
+  int32_t shared_epilogue;   /* MI_EPI_* for the shared expert's group */
 } mi_gemv_desc;
 size_t mi_gemv_workspace_bytes(const mi_gemv_desc* d);   /* 0 when the plan needs none */
 int mi_gemv(const mi_gemv_desc* d, void* stream);
@@ -272,7 +277,10 @@ int mi_gqa_decode(const mi_gqa_desc* d, void* stream);
  * top-k with ties to the lowest expert index, renormalized over the k when renorm. With `groups` non-NULL the same
  * launch writes the expert groups of the grouped GEMV (mi_gemv_desc.groups): max_groups records of 18 int32 —
  * expert, count, then the count pair ids p = t·top_k + slot ascending — one per distinct expert in order of first
- * use, the rest expert = -1, count = 0. t <= 16, n_experts <= 512, top_k <= 16. */
+ * use, the rest expert = -1, count = 0. t <= 16, n_experts <= 512, top_k <= 16.
+ * shared_expert > 0: the shared expert joins every token as slot top_k — id shared_expert, weight
+ * bf16(σ(logits[t][shared_gate_col])) (the shared gate's logit, a row of the router GEMV) — so ids / weights are
+ * [t][top_k + 1], pairs p = t·(top_k + 1) + slot, and the shared expert is one more group (max_groups one more). */
 typedef struct mi_moe_route_desc {
   int32_t t, n_experts, top_k, renorm;
   const uint16_t* logits;
@@ -281,6 +289,8 @@ typedef struct mi_moe_route_desc {
   float* weights;
   int32_t* groups;
   int32_t max_groups;
+  int32_t shared_expert;     /* 0 = none */
+  int32_t shared_gate_col;
 } mi_moe_route_desc;
 int mi_moe_route(const mi_moe_route_desc* d, void* stream);
 

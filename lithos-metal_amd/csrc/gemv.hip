@@ -69,6 +69,7 @@ struct Args {
   float gnorm_eps;
   int row_ld;               // gemv_row: LDS row stride of a wave's staged slice (elements)
   int row_wave_lds;         // gemv_row: LDS bytes per wave
+  int shared_expert, shared_epilogue;   // grouped: the shared expert's group takes its own epilogue (0 = none)
 };
 
 // ---- weight decode ---------------------------------------------------------------------------------------------
@@ -133,15 +134,20 @@ __device__ __forceinline__ void store_out(const Args& a, long long idx, float v)
 
 // one output value: row tile·16 + m_row of token t, already scaled by its row scale; `up` is the value of the row
 // 8 below it (the up half of a silu·mul tile), fetched by the caller with a shuffle every lane executes
-__device__ __forceinline__ void emit(const Args& a, const int32_t* pairs, int cnt, int tile, bool tile_ok, int m_row,
-                                     int t, float v, float up) {
+// the epilogue of a workgroup's matrix: the descriptor's, or the shared expert's for its group
+__device__ __forceinline__ int epilogue_of(const Args& a, int expert) {
+  return a.shared_expert > 0 && expert == a.shared_expert ? a.shared_epilogue : a.epilogue;
+}
+
+__device__ __forceinline__ void emit(const Args& a, int epi, const int32_t* pairs, int cnt, int tile, bool tile_ok,
+                                     int m_row, int t, float v, float up) {
   if (!tile_ok || t >= cnt) return;
   const int yr = pairs ? pairs[t] : t;
-  if (a.epilogue == MI_EPI_SILU_MUL || a.epilogue == MI_EPI_SILU_MUL_ROUNDED) {
+  if (epi == MI_EPI_SILU_MUL || epi == MI_EPI_SILU_MUL_ROUNDED) {
     const int col = tile * 8 + m_row;
     if (m_row >= 8 || col >= a.n / 2) return;
     float o;
-    if (a.epilogue == MI_EPI_SILU_MUL_ROUNDED) {
+    if (epi == MI_EPI_SILU_MUL_ROUNDED) {
       const float gb = round_bf16(v), ub = round_bf16(up);
       o = silu_f(gb) * ub;
     } else {
@@ -152,7 +158,7 @@ __device__ __forceinline__ void emit(const Args& a, const int32_t* pairs, int cn
     const int row = tile * 16 + m_row;
     if (row >= a.n) return;
     float o = v;
-    if (a.epilogue == MI_EPI_RESIDUAL) o += bf16_bits_to_f32(a.res[(long long)t * a.ldr + row]);
+    if (epi == MI_EPI_RESIDUAL) o += bf16_bits_to_f32(a.res[(long long)t * a.ldr + row]);
     store_out(a, (long long)yr * a.ldy + row, o);
   }
 }
@@ -509,7 +515,7 @@ __global__ __launch_bounds__(KW == 16 ? 640 : 1024) void gemv_row(Args a) {
     float v = vt[t];
     v *= rs;
     const float up = __shfl_down(v, 8, 16);
-    if (g == 0) emit(a, pairs, cnt, tile, true, m_row, t, v, up);
+    if (g == 0) emit(a, epilogue_of(a, expert), pairs, cnt, tile, true, m_row, t, v, up);
   }
 }
 
@@ -849,7 +855,7 @@ void gemv_rowp(Args a) {
     }
     v *= a.row_scale != nullptr ? a.row_scale[(long long)expert * a.n_tiles * 16 + row] : 1.0f;
     const float up = __shfl_down(v, 8, 16);
-    if (ok) emit(a, pairs, cnt, tile, true, r, t, v, up);
+    if (ok) emit(a, epilogue_of(a, expert), pairs, cnt, tile, true, r, t, v, up);
   }
 }
 
@@ -1107,7 +1113,7 @@ __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
     }
     v *= a.row_scale != nullptr ? a.row_scale[row] : 1.0f;
     const float up = __shfl_down(v, 8, 16);
-    if (g == 0) emit(a, nullptr, cnt, tile, true, m_row, t, v, up);
+    if (g == 0) emit(a, a.epilogue, nullptr, cnt, tile, true, m_row, t, v, up);
   }
 }
 
@@ -1467,7 +1473,7 @@ __global__ __launch_bounds__(512) void gemv_tk(Args a) {
         if (a.ks == 1) {
           const float vs = v * rs;
           const float up = __shfl_down(vs, 8, 16);
-          emit(a, pairs, cnt, tile, true, m_row, t, vs, up);
+          emit(a, epilogue_of(a, expert), pairs, cnt, tile, true, m_row, t, vs, up);
         } else if (t < cnt) {
           a.part[((long long)split * a.m + t) * n_pad + row] = v;
         }
@@ -1480,7 +1486,7 @@ __global__ __launch_bounds__(512) void gemv_tk(Args a) {
         if (a.ks == 1) {
           const float vs = v * rs;
           const float up = __shfl_down(vs, 8, 16);
-          if (g == 0) emit(a, pairs, cnt, tile, true, m_row, t, vs, up);
+          if (g == 0) emit(a, epilogue_of(a, expert), pairs, cnt, tile, true, m_row, t, vs, up);
         } else if (g == 0 && t < cnt) {
           a.part[((long long)split * a.m + t) * n_pad + row] = v;
         }
@@ -1626,6 +1632,12 @@ int check_desc(const mi_gemv_desc* d) {
   MI_REQUIRE(!silu || d->n % 16 == 0, "mi_gemv: silu_mul needs n %% 16 == 0 (8 gate + 8 up rows per tile)");
   MI_REQUIRE(d->ldy >= (silu ? d->n / 2 : d->n), "mi_gemv: ldy too small");
   MI_REQUIRE(!d->groups || (d->max_groups > 0 && d->top_k > 0), "mi_gemv: grouped mode needs max_groups and top_k");
+  {
+    const auto silu = [](int e) { return e == MI_EPI_SILU_MUL || e == MI_EPI_SILU_MUL_ROUNDED; };
+    MI_REQUIRE(!d->groups || d->shared_expert <= 0 || (silu(d->shared_epilogue) == silu(d->epilogue) &&
+                                                       d->shared_epilogue != MI_EPI_RESIDUAL),
+               "mi_gemv: the shared expert's epilogue must give the routed experts' output width (no residual)");
+  }
   MI_REQUIRE(((uintptr_t)d->x & 15) == 0 && d->ldx % 8 == 0, "mi_gemv: x must be 16-byte aligned with ldx %% 8 == 0");
   MI_REQUIRE(((uintptr_t)d->w & 15) == 0, "mi_gemv: weight pack must be 16-byte aligned");
   MI_REQUIRE(!d->norm_w || ((uintptr_t)d->norm_w & 15) == 0, "mi_gemv: norm_w must be 16-byte aligned");
@@ -2040,6 +2052,8 @@ int gemv_impl(const mi_gemv_desc* d, void* stream, void* fixed_ws, size_t fixed_
   a.tile_stride = tile_bytes(d->format, a.chunks);
   a.expert_stride = (long long)a.n_tiles * a.tile_stride;
   a.epilogue = d->epilogue;
+  a.shared_expert = d->groups ? d->shared_expert : 0;
+  a.shared_epilogue = d->shared_epilogue;
   a.top_k = d->top_k;
   a.x_per_slot = d->x_per_slot;
   a.out_f32 = d->out_f32;

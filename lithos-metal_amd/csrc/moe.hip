@@ -15,6 +15,8 @@
 //  * moe_combine: one workgroup per token, 8 columns per lane with 16-byte loads.
 #include "mi_common.h"
 
+#include <algorithm>
+
 namespace {
 
 constexpr int MAX_PER_LANE = 8;      // E <= 512
@@ -28,15 +30,17 @@ struct RouteArgs {
   int32_t* ids;
   float* weights;
   int32_t* groups;
+  int shared_expert, shared_gate_col;           // shared_expert > 0: slot top_k of every token (the shared expert)
 };
 
 __device__ __forceinline__ float wave_min(float v) { return -wave_max(-v); }
 
 __global__ __launch_bounds__(64 * MAX_T) void moe_route(RouteArgs a) {
-  __shared__ int sel[MAX_T * MAX_K];
+  __shared__ int sel[MAX_T * (MAX_K + 1)];
   __shared__ int fresh[64 * MAX_T];
   const int lane = threadIdx.x & 63, t = threadIdx.x >> 6;
   const int E = a.n_experts, k = a.top_k;
+  const int ks = k + (a.shared_expert > 0 ? 1 : 0);   // slots per token (the shared expert last)
   if (t < a.t) {                                    // wave-uniform
     float v[MAX_PER_LANE];
     float m = -INFINITY;
@@ -83,10 +87,18 @@ __global__ __launch_bounds__(64 * MAX_T) void moe_route(RouteArgs a) {
     for (int r = 0; r < k; ++r) {
       const float w = a.renorm && wsum > 0.0f ? cw[r] / wsum : cw[r];
       if (lane == 0) {
-        a.ids[t * k + r] = ce[r];
-        a.weights[t * k + r] = round_bf16(w);
+        a.ids[t * ks + r] = ce[r];
+        a.weights[t * ks + r] = round_bf16(w);
       }
-      sel[t * k + r] = ce[r];
+      sel[t * ks + r] = ce[r];
+    }
+    if (a.shared_expert > 0) {                      // the shared expert: weight bf16(σ(its gate's logit))
+      if (lane == 0) {
+        const float g = bf16_bits_to_f32(a.logits[(long long)t * a.ld_logits + a.shared_gate_col]);
+        a.ids[t * ks + k] = a.shared_expert;
+        a.weights[t * ks + k] = round_bf16(1.0f / (1.0f + expf(-g)));
+      }
+      sel[t * ks + k] = a.shared_expert;
     }
   }
   if (!a.groups) return;                            // workgroup-uniform
@@ -94,7 +106,7 @@ __global__ __launch_bounds__(64 * MAX_T) void moe_route(RouteArgs a) {
   // groups: record g = the g-th distinct expert in pair order; pairs of a record ascending. One thread per pair
   // (P = t·k <= 64·t = blockDim): first use, rank and count by one pass over the pairs, then the record index as the
   // number of first uses before this expert's first use.
-  const int P = a.t * k;
+  const int P = a.t * ks;
   const int p = threadIdx.x;
   int e = -1, first = p, rank = 0, count = 0;
   if (p < P && sel[p] >= 0) {          // a pair without an expert (id -1) joins no group
@@ -187,10 +199,14 @@ extern "C" int mi_moe_route(const mi_moe_route_desc* d, void* stream) {
   MI_REQUIRE(d->top_k >= 1 && d->top_k <= MAX_K && d->top_k <= d->n_experts, "mi_moe_route: top_k=%d out of range",
              d->top_k);
   MI_REQUIRE(d->logits && d->ids && d->weights && d->ld_logits >= d->n_experts, "mi_moe_route: bad logits / outputs");
-  MI_REQUIRE(!d->groups || d->max_groups >= d->t * d->top_k || d->max_groups >= d->n_experts,
+  const int sh = d->shared_expert > 0 ? 1 : 0;
+  MI_REQUIRE(!sh || (d->shared_expert >= d->n_experts && d->shared_gate_col >= 0 && d->shared_gate_col < d->ld_logits),
+             "mi_moe_route: the shared expert's index must follow the routed experts and its gate column lie in the "
+             "logits row");
+  MI_REQUIRE(!d->groups || d->max_groups >= std::min(d->t * d->top_k, d->n_experts) + sh,
              "mi_moe_route: max_groups=%d cannot hold every distinct expert", d->max_groups);
   RouteArgs a{d->t, d->n_experts, d->top_k, d->renorm, d->ld_logits, d->max_groups, d->logits, d->ids, d->weights,
-              d->groups};
+              d->groups, d->shared_expert, d->shared_gate_col};
   hipLaunchKernelGGL(moe_route, dim3(1), dim3(64 * d->t), 0, static_cast<hipStream_t>(stream), a);
   MI_TRY_HIP(hipGetLastError(), "moe_route launch");
   return MI_OK;

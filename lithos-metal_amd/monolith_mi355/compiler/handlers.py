@@ -72,7 +72,9 @@ def _gemv_common(ctx: EmitContext, op: Op, *, out_f32: bool = False, grouped: bo
         ptrs.update(gnorm_w=gw, gnorm_z=gz)
     if grouped:
         groups = op.inputs[2]
-        scalars.update(max_groups=groups.shape[0], top_k=a["top_k"], x_per_slot=int(a.get("x_per_slot", False)))
+        scalars.update(max_groups=groups.shape[0], top_k=a["top_k"], x_per_slot=int(a.get("x_per_slot", False)),
+                       shared_expert=int(a.get("shared_expert", 0)),
+                       shared_epilogue=EPILOGUE[a.get("shared_epilogue")])
         ptrs["groups"] = groups
     probe = _probe(hip.MiGemvDesc, scalars, [f for f, v in ptrs.items() if v is not None])
     need = int(hip.load().mi_gemv_workspace_bytes(C.byref(probe)))
@@ -183,7 +185,8 @@ def moe_route(ctx: EmitContext, op: Op):
     a = op.attrs
     scalars = dict(t=logits.shape[0], n_experts=a.get("n_experts", logits.shape[1]), top_k=a["top_k"],
                    renorm=int(a.get("renorm", True)), ld_logits=logits.row_stride,
-                   max_groups=groups.shape[0] if groups is not None else 0)
+                   max_groups=groups.shape[0] if groups is not None else 0,
+                   shared_expert=int(a.get("shared_expert", 0)), shared_gate_col=int(a.get("shared_gate_col", 0)))
     return lib_op(ctx, "mi_moe_route", hip.MiMoeRouteDesc, scalars,
                   dict(logits=logits, ids=ids, weights=weights, groups=groups), a.get("name", "moe_route"),
                   writes=("ids", "weights", "groups"))

@@ -46,39 +46,52 @@ def act(name: str, *shape: int, dtype: str = "bf16") -> Value:
 
 
 def lower_moe(g: Graph, moe, h: Value, prefix: str) -> Value:
-    """A ``layers.MoeBlock`` (``nn/moe.py``): the shared expert (norm fused, silu·mul → down), the router and the
-    shared expert's σ-gate as one BF16 GEMV of E + 1 rows into a row padded to 8, the top-k route with its expert
-    groups, the grouped gate|up and down GEMVs, the weighted combine with the gated shared expert and the residual.
-    One stream: the ops run in this order (the eager block forks the shared expert only at M > 2)."""
+    """A ``layers.MoeBlock`` (``nn/moe.py``): the router and the shared expert's σ-gate as one BF16 GEMV of E + 1 rows
+    into a row padded to 8, the top-k route with its expert groups, the grouped gate|up and down GEMVs, the weighted
+    combine with the residual. With the shared expert stacked after the routed ones (``fused_shared``) it is slot k
+    of every token inside the grouped launches (its own silu·mul epilogue) and of the combine; otherwise it runs as
+    two dense GEMVs first and the combine adds it with its gate. One stream: the ops run in this order."""
     m, e, k = g.t, moe.experts, moe.top_k
     pad = (e + 1 + 7) // 8 * 8
     norm = bound(f"{prefix}.norm", moe.norm_w, "weights")
-    s_act = act(f"{prefix}.shared_act", m, moe.shared_inter)
-    s_out = act(f"{prefix}.shared_out", m, moe.hidden)
-    g.add("gemv", [h, weight(f"{prefix}.shared_gate_up", moe.shared_gate_up.packed)], [s_act], epilogue="silu_mul",
-          norm_w=norm, eps=moe.eps, name=f"{prefix}.shared_gate_up")
-    g.add("gemv", [s_act, weight(f"{prefix}.shared_down", moe.shared_down.packed)], [s_out],
-          name=f"{prefix}.shared_down")
+    fused = getattr(moe, "fused_shared", False)
+    s_out = None
+    if not fused:
+        s_act = act(f"{prefix}.shared_act", m, moe.shared_inter)
+        s_out = act(f"{prefix}.shared_out", m, moe.hidden)
+        g.add("gemv", [h, weight(f"{prefix}.shared_gate_up", moe.shared_gate_up.packed)], [s_act],
+              epilogue="silu_mul", norm_w=norm, eps=moe.eps, name=f"{prefix}.shared_gate_up")
+        g.add("gemv", [s_act, weight(f"{prefix}.shared_down", moe.shared_down.packed)], [s_out],
+              name=f"{prefix}.shared_down")
     logits = act(f"{prefix}.router_logits", m, pad)
     router_out = Value(f"{prefix}.router_gate", (m, e + 1), "bf16", ld=pad, base=logits)
     route_in = Value(f"{prefix}.route_logits", (m, e), "bf16", ld=pad, base=logits)
     gate = Value(f"{prefix}.shared_gate", (m, 1), "bf16", ld=pad, offset=2 * e, base=logits)
     g.add("gemv", [h, weight(f"{prefix}.router", moe.router_gate)], [router_out], norm_w=norm, eps=moe.eps,
           name=f"{prefix}.router")
-    ids = act(f"{prefix}.ids", m, k, dtype="i32")
-    wts = act(f"{prefix}.weights", m, k, dtype="f32")
+    ks = k + (1 if fused else 0)                     # slots per token
+    ids = act(f"{prefix}.ids", m, ks, dtype="i32")
+    wts = act(f"{prefix}.weights", m, ks, dtype="f32")
     from ..kernels import GROUP_REC
-    groups = act(f"{prefix}.groups", min(e, m * k), GROUP_REC, dtype="i32")
-    g.add("moe_route", [route_in], [ids, wts, groups], top_k=k, renorm=True, name=f"{prefix}.route")
-    a = act(f"{prefix}.expert_act", m * k, moe.inter)
-    hk = act(f"{prefix}.expert_out", m * k, moe.hidden)
-    g.add("moe_gemv", [h, weight(f"{prefix}.gate_up", moe.gate_up), groups], [a], tokens=m, top_k=k,
-          x_per_slot=False, epilogue="silu_mul_rounded", norm_w=norm, eps=moe.eps, name=f"{prefix}.experts_gate_up")
-    g.add("moe_gemv", [a, weight(f"{prefix}.down", moe.down), groups], [hk], tokens=m, top_k=k, x_per_slot=True,
-          name=f"{prefix}.experts_down")
+    groups = act(f"{prefix}.groups", min(e, m * k) + (1 if fused else 0), GROUP_REC, dtype="i32")
+    shared = dict(shared_expert=e) if fused else {}
+    g.add("moe_route", [route_in], [ids, wts, groups], top_k=k, renorm=True, name=f"{prefix}.route",
+          **(dict(shared_expert=e, shared_gate_col=e) if fused else {}))
+    a = act(f"{prefix}.expert_act", m * ks, moe.inter)
+    hk = act(f"{prefix}.expert_out", m * ks, moe.hidden)
+    gu = moe.gate_up_s if fused else moe.gate_up
+    dn = moe.down_s if fused else moe.down
+    g.add("moe_gemv", [h, weight(f"{prefix}.gate_up", gu), groups], [a], tokens=m, top_k=ks, x_per_slot=False,
+          epilogue="silu_mul_rounded", norm_w=norm, eps=moe.eps, name=f"{prefix}.experts_gate_up",
+          **(dict(shared, shared_epilogue="silu_mul") if fused else {}))
+    g.add("moe_gemv", [a, weight(f"{prefix}.down", dn), groups], [hk], tokens=m, top_k=ks, x_per_slot=True,
+          name=f"{prefix}.experts_down", **shared)
     out = act(f"{prefix}.out", m, moe.hidden)
-    g.add("moe_combine", [hk, wts], [out], top_k=k, shared=s_out, shared_gate=gate, residual=h,
-          name=f"{prefix}.combine")
+    if fused:
+        g.add("moe_combine", [hk, wts], [out], top_k=ks, residual=h, name=f"{prefix}.combine")
+    else:
+        g.add("moe_combine", [hk, wts], [out], top_k=k, shared=s_out, shared_gate=gate, residual=h,
+              name=f"{prefix}.combine")
     return out
 
 

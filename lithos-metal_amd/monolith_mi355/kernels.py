@@ -386,38 +386,48 @@ def gqa_decode(proj, cache: KVCache, pos, *, heads: int, rope_cos, rope_sin, gat
 GROUP_REC = 18
 
 
-def moe_route(logits, top_k: int, *, renorm: bool = True, groups: bool = True, out=None, stream=None):
+def moe_route(logits, top_k: int, *, renorm: bool = True, groups: bool = True, out=None, stream=None,
+              shared_expert: int = 0, shared_gate=None):
     """``moe_route`` (``ops/moe.py``): ``logits [T, E]`` bf16 → ``(ids [T, k] int32, weights [T, k] float32,
     groups [max_groups, 18] int32 or None)``; ``max_groups = min(E, T·k)``. The groups feed ``moe_gemv``. ``out``:
-    preallocated ``(ids, weights, groups)`` (a captured step allocates nothing)."""
+    preallocated ``(ids, weights, groups)`` (a captured step allocates nothing). ``shared_expert`` > 0 (its index in
+    the stacked experts, after the routed ones) with ``shared_gate`` = the column of ``logits``' rows that holds the
+    shared gate's logit (the logits tensor a view of a wider router output): every token gets slot k = the shared
+    expert with weight bf16(σ(gate)), so ids / weights are ``[T, k + 1]`` and there is one group more."""
     torch = _torch()
     _bf16_2d(logits, "moe_route logits", aligned=False)
     t, e = logits.shape
     dev = logits.device
-    max_groups = min(e, t * top_k)
+    sh = 1 if shared_expert > 0 else 0
+    if sh and (shared_gate is None or shared_expert < e or not 0 <= shared_gate < logits.stride(0)):
+        raise ValueError("moe_route: the shared expert follows the routed ones and its gate column lies in the row")
+    ks = top_k + sh
+    max_groups = min(e, t * top_k) + sh
     if out is not None:
         ids, w, g = out
-        if (ids.dtype != torch.int32 or ids.numel() < t * top_k or w.dtype != torch.float32 or w.numel() < t * top_k
+        if (ids.dtype != torch.int32 or ids.numel() < t * ks or w.dtype != torch.float32 or w.numel() < t * ks
                 or (groups and (g is None or g.dtype != torch.int32 or g.shape[0] < max_groups
                                 or g.shape[1] != GROUP_REC))):
             raise ValueError("moe_route: out must be (int32 [T, k], float32 [T, k], int32 [max_groups, 18])")
         g = g if groups else None
     else:
-        ids = torch.empty((t, top_k), dtype=torch.int32, device=dev)
-        w = torch.empty((t, top_k), dtype=torch.float32, device=dev)
+        ids = torch.empty((t, ks), dtype=torch.int32, device=dev)
+        w = torch.empty((t, ks), dtype=torch.float32, device=dev)
         g = torch.empty((max_groups, GROUP_REC), dtype=torch.int32, device=dev) if groups else None
     d = hip.MiMoeRouteDesc(t=t, n_experts=e, top_k=top_k, renorm=int(renorm), logits=hip.ptr(logits),
                            ld_logits=logits.stride(0), ids=hip.ptr(ids), weights=hip.ptr(w), groups=hip.ptr(g),
-                           max_groups=max_groups if groups else 0)
+                           max_groups=max_groups if groups else 0, shared_expert=shared_expert,
+                           shared_gate_col=shared_gate if sh else 0)
     hip.call("mi_moe_route", C.byref(d), hip.stream_handle(stream))
     return ids, w, g
 
 
 def moe_gemv(w: PackedWeight, x, groups, *, tokens: int, top_k: int, x_per_slot: bool, epilogue=None, norm_w=None,
-             eps: float = 1e-6, out=None, stream=None):
+             eps: float = 1e-6, out=None, stream=None, shared_expert: int = 0, shared_epilogue=None):
     """``moe_gemv`` (``ops/moe.py``; the grouped mode of ``gemv``): for every group record (expert e, its pairs
     p = t·k + j), ``out[p] = x_row · W_eᵀ`` with ``x_row = x[p]`` (``x_per_slot``) or ``x[p // k]``; ``w`` holds the
-    experts back to back. ``out [T·k, n_out]`` bf16."""
+    experts back to back. ``out [T·k, n_out]`` bf16. ``shared_expert`` > 0: that expert's group (the shared expert
+    stacked after the routed ones) takes ``shared_epilogue``."""
     torch = _torch()
     _bf16_2d(x, "moe_gemv x")
     if x.shape[1] != w.k:
@@ -438,7 +448,8 @@ def moe_gemv(w: PackedWeight, x, groups, *, tokens: int, top_k: int, x_per_slot:
                        row_scale=hip.ptr(w.row_scale), x=hip.ptr(x), ldx=x.stride(0), y=hip.ptr(out),
                        ldy=out.stride(0), epilogue=hip.MI_EPI[epilogue], residual=0, ldr=0, norm_w=hip.ptr(norm_w),
                        eps=eps, groups=hip.ptr(groups), max_groups=groups.shape[0], top_k=top_k,
-                       x_per_slot=int(x_per_slot), workspace=0, workspace_bytes=0, out_f32=0)
+                       x_per_slot=int(x_per_slot), workspace=0, workspace_bytes=0, out_f32=0,
+                       shared_expert=shared_expert, shared_epilogue=hip.MI_EPI[shared_epilogue])
     hip.call("mi_gemv", C.byref(d), hip.stream_handle(stream))
     return out
 

@@ -334,7 +334,6 @@ class MoeBlock:
                                         torch.cat([m.packed.row_scale for m in mats]))
         self.gate_up_q = [nvfp4_matrix(2 * inter, hidden, gen, device, gate_up=True) for _ in range(experts)]
         self.down_q = [nvfp4_matrix(hidden, inter, gen, device) for _ in range(experts)]
-        self.gate_up, self.down = stack(self.gate_up_q), stack(self.down_q)
         self.shared_gate_up = nvfp4_matrix(2 * shared_inter, hidden, gen, device, gate_up=True)
         self.shared_down = nvfp4_matrix(hidden, shared_inter, gen, device)
         self.shared_gate_w = (torch.randn(1, hidden, generator=gen, device=device) * 0.02).to(torch.bfloat16)
@@ -343,6 +342,21 @@ class MoeBlock:
         self.router_gate = kernels.PackedWeight("bf16", experts + 1, hidden, 1,
                                                 DV.pack_bf16(torch.cat([self.router_w, self.shared_gate_w])), None)
         self.shared_inter = shared_inter
+        # the shared expert stacked after the routed ones (when it has their shape): it then runs inside the grouped
+        # expert launches as slot k of every token, weight bf16(σ(gate)) from the router's row E — two launches
+        # fewer and no second stream; the combine takes it as one more slot
+        self.fused_shared = shared_inter == inter
+
+        def routed(st):                                  # the first E experts of a stack, as views
+            nb = st.data.numel() // st.experts
+            return kernels.PackedWeight(st.format, st.n, st.k, experts, st.data[: experts * nb],
+                                        st.row_scale[: experts * (st.row_scale.numel() // st.experts)])
+        if self.fused_shared:
+            self.gate_up_s = stack(self.gate_up_q + [self.shared_gate_up])
+            self.down_s = stack(self.down_q + [self.shared_down])
+            self.gate_up, self.down = routed(self.gate_up_s), routed(self.down_s)
+        else:
+            self.gate_up, self.down = stack(self.gate_up_q), stack(self.down_q)
         self._bufs: Dict[int, tuple] = {}
         # the shared expert runs on a second stream beside the router → experts chain (default priority), with its
         # own zeroed split-K workspace so the two branches never share partials or fold counters
@@ -352,7 +366,8 @@ class MoeBlock:
     def buffers(self, m: int):
         torch = _torch()
         if m not in self._bufs:
-            dev, k, g = self.norm_w.device, self.top_k, min(self.experts, m * self.top_k)
+            sh = 1 if self.fused_shared else 0
+            dev, k, g = self.norm_w.device, self.top_k + sh, min(self.experts, m * self.top_k) + sh
             bf = torch.bfloat16
             self._bufs[m] = (torch.empty(m, (self.experts + 1 + 7) // 8 * 8, dtype=bf, device=dev),
                              (torch.empty(m, k, dtype=torch.int32, device=dev),
@@ -373,6 +388,16 @@ class MoeBlock:
         logits, route, act, hk, s_act, s_out, s_gate, y = self.buffers(m)
         out = y if out is None else out
         torch = _torch()
+        e, k = self.experts, self.top_k
+        if self.fused_shared:
+            kernels.gemv(self.router_gate, h, norm_w=self.norm_w, eps=self.eps, out=logits[:, :e + 1])
+            _, wts, groups = kernels.moe_route(logits[:, :e], k, renorm=True, out=route, shared_expert=e,
+                                               shared_gate=e)
+            kernels.moe_gemv(self.gate_up_s, h, groups, tokens=m, top_k=k + 1, x_per_slot=False,
+                             epilogue="silu_mul_rounded", norm_w=self.norm_w, eps=self.eps, out=act,
+                             shared_expert=e, shared_epilogue="silu_mul")
+            kernels.moe_gemv(self.down_s, act, groups, tokens=m, top_k=k + 1, x_per_slot=True, out=hk)
+            return kernels.moe_combine(hk, wts, top_k=k + 1, residual=h, out=out)
 
         def shared(ws=None):
             kernels.gemv(self.shared_gate_up.packed, h, epilogue="silu_mul", norm_w=self.norm_w, eps=self.eps,

@@ -34,7 +34,8 @@ class MiGemvDesc(C.Structure):
                 ("ldr", C.c_int32), ("norm_w", C.c_void_p), ("eps", C.c_float), ("groups", C.c_void_p),
                 ("max_groups", C.c_int32), ("top_k", C.c_int32), ("x_per_slot", C.c_int32),
                 ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t), ("out_f32", C.c_int32),
-                ("gnorm_w", C.c_void_p), ("gnorm_z", C.c_void_p), ("ld_gnorm_z", C.c_int32), ("gnorm_eps", C.c_float)]
+                ("gnorm_w", C.c_void_p), ("gnorm_z", C.c_void_p), ("ld_gnorm_z", C.c_int32), ("gnorm_eps", C.c_float),
+                ("shared_expert", C.c_int32), ("shared_epilogue", C.c_int32)]
 
 
 class MiGdnDesc(C.Structure):
@@ -71,7 +72,8 @@ class MiNormDesc(C.Structure):
 class MiMoeRouteDesc(C.Structure):
     _fields_ = [("t", C.c_int32), ("n_experts", C.c_int32), ("top_k", C.c_int32), ("renorm", C.c_int32),
                 ("logits", C.c_void_p), ("ld_logits", C.c_int32), ("ids", C.c_void_p), ("weights", C.c_void_p),
-                ("groups", C.c_void_p), ("max_groups", C.c_int32)]
+                ("groups", C.c_void_p), ("max_groups", C.c_int32), ("shared_expert", C.c_int32),
+                ("shared_gate_col", C.c_int32)]
 
 
 class MiMoeCombineDesc(C.Structure):

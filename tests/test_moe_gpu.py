@@ -194,6 +194,33 @@ def test_sparse_moe_block_baseline_geometry(torch_gpu, t):
     assert chk.ok_rounded() and chk.within, chk
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("t", [1, 5, 16])
+def test_moe_route_with_the_shared_expert_slot(torch_gpu, t):
+    """``shared_expert``: the routed slots exactly as without it; slot k = the shared expert (index E) with weight
+    bf16(σ(logit of the gate column)); the groups hold every pair once, one record for the shared expert with the t
+    pairs p = tok·(k + 1) + k, and the routed experts' records in the same first-use order as without it."""
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    rng = np.random.default_rng(t)
+    e, k = 64, 8
+    lg = rbf(rng.standard_normal((t, 72)))               # E logits, then the shared gate's column, padding
+    dev = to_dev_bf16(torch, lg)
+    ids, w, groups = kernels.moe_route(dev[:, :e], k, renorm=True, shared_expert=e, shared_gate=e)
+    ids, w, groups = ids.cpu().numpy(), w.cpu().numpy(), groups.cpu().numpy()
+    ref_ids, ref_w = ON.moe_route(lg[:, :e], k, True)
+    assert np.array_equal(ids[:, :k], ref_ids) and np.array_equal(w[:, :k], ref_w)
+    assert (ids[:, k] == e).all() and np.array_equal(w[:, k], rbf(ON.sigmoid(lg[:, e])))
+    recs = groups[groups[:, 1] > 0]
+    sh = recs[recs[:, 0] == e]
+    assert len(sh) == 1 and list(sh[0, 2: 2 + t]) == [tok * (k + 1) + k for tok in range(t)]
+    pairs = sorted(int(p) for r in recs for p in r[2: 2 + r[1]])
+    assert pairs == list(range(t * (k + 1)))
+    # the routed experts' records: the same experts, in the same first-use order, as without the shared slot
+    plain = kernels.moe_route(dev[:, :e], k, renorm=True)[2].cpu().numpy()
+    assert list(recs[recs[:, 0] != e, 0]) == list(plain[plain[:, 1] > 0, 0])
+
+
 def test_moe_rejects_bad_descriptors():
     import ctypes as C
     from monolith_mi355.runtime import hip
@@ -201,7 +228,8 @@ def test_moe_rejects_bad_descriptors():
     base = dict(t=2, n_experts=256, top_k=8, renorm=1, logits=256, ld_logits=256, ids=256, weights=256, groups=0,
                 max_groups=0)
     for kw in (dict(t=0), dict(t=17), dict(n_experts=513), dict(top_k=17), dict(top_k=0), dict(ld_logits=100),
-               dict(groups=256, max_groups=10), dict(logits=0)):
+               dict(groups=256, max_groups=10), dict(logits=0), dict(shared_expert=100, shared_gate_col=256),
+               dict(shared_expert=200, shared_gate_col=0)):
         assert lib.mi_moe_route(C.byref(hip.MiMoeRouteDesc(**{**base, **kw})), None) == 1, kw
         assert hip.last_error().startswith("mi_moe_route")
     cb = dict(t=2, hidden=2048, top_k=8, h=256, ldh=2048, weights=256, out=256, ldo=2048)
@@ -243,7 +271,12 @@ def test_moe_block_layer(torch_gpu, t, n_exp):
     y = from_dev_bf16(blk(hd))
     both = from_dev_bf16(blk.buffers(t)[0])           # router logits | the shared gate's logit, one GEMV
     logits, gate = both[:, :n_exp], both[:, n_exp:n_exp + 1]
-    ids = blk.buffers(t)[1][0].cpu().numpy()
+    ids_all = blk.buffers(t)[1][0].cpu().numpy()
+    ids = ids_all[:, :8]
+    if blk.fused_shared:                               # the shared expert: slot 8 of every token, weight bf16(σ(gate))
+        assert (ids_all[:, 8] == n_exp).all()
+        w_all = blk.buffers(t)[1][1].cpu().numpy()
+        assert np.array_equal(w_all[:, 8], rbf(ON.sigmoid(gate[:, 0])))
 
     def dense(w, expert=0, gate_up=False):
         d = kernels.dequant(w, expert=expert).cpu().numpy()
