@@ -122,7 +122,8 @@ typedef struct mi_gemv_desc {
   int32_t ldr;
   const float* norm_w;       /* fused input RMSNorm: x = bf16(h·rsqrt(mean h²+eps)·norm_w), norm_w = (1+w) [k]; NULL = off */
   float eps;
-  const int32_t* groups;     /* grouped (MoE) mode: [max_groups][18] = expert, count, 16 pair ids (mi_moe_group) */
+  const int32_t* groups;     /* grouped (MoE) mode: [max_groups][18] = expert, count, 16 pair ids (mi_moe_route);
+                                written instead of read when route_logits is set */
   int32_t max_groups;
   int32_t top_k;             /* pair p = token·top_k + slot */
   int32_t x_per_slot;        /* grouped: x row = p (1) or p / top_k (0); y row = p */
@@ -143,6 +144,16 @@ typedef struct mi_gemv_desc {
    * silu(gate)·up where the routed experts round gate and up first (nn/moe.py:327-337 against nn/mlp.py:25-26) */
   int32_t shared_expert;
   int32_t shared_epilogue;   /* MI_EPI_* for the shared expert's group */
+  /* grouped mode at one token (m = 1): the launch routes for itself — the top-k of route_logits (the token's router
+   * row: route_experts BF16 logits, the shared gate's logit at route_gate_col), exactly mi_moe_route's — group g is
+   * slot g (the shared expert last, when shared_expert > 0; top_k = max_groups = route_top_k (+1)), and its first
+   * workgroup writes the route for the launches after it: route_ids / route_weights [top_k] and the group records
+   * in `groups` (record g = slot g). NULL = the groups are read from `groups`. No counterpart in the reference: it
+   * removes the route launch between the router and the expert GEMVs. */
+  const uint16_t* route_logits;
+  int32_t route_experts, route_top_k, route_renorm, route_gate_col;
+  int32_t* route_ids;
+  float* route_weights;
 } mi_gemv_desc;
 size_t mi_gemv_workspace_bytes(const mi_gemv_desc* d);   /* 0 when the plan needs none */
 int mi_gemv(const mi_gemv_desc* d, void* stream);

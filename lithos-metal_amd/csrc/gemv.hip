@@ -28,6 +28,7 @@
 // fence — on gfx950 such a fence writes back / invalidates the whole L2 per workgroup and costs more than the GEMV.
 // gemv_tk and gemv_rowm leave their split partials to the ordered gemv_tk_reduce launch.
 #include "mi_common.h"
+#include "route.h"
 #include "t16.h"
 
 #include <algorithm>
@@ -70,6 +71,14 @@ struct Args {
   int row_ld;               // gemv_row: LDS row stride of a wave's staged slice (elements)
   int row_wave_lds;         // gemv_row: LDS bytes per wave
   int shared_expert, shared_epilogue;   // grouped: the shared expert's group takes its own epilogue (0 = none)
+  // grouped, one token: the launch routes for itself (group g = slot g of the token's top-k, the shared expert
+  // last) from the router's logits row, and its first workgroup writes the route (ids, weights, groups) for the
+  // launches after it
+  const uint16_t* route_logits;
+  int route_e, route_k, route_renorm, route_gate_col, route_n;   // route_n: group records to write
+  int32_t* route_ids;
+  float* route_weights;
+  int32_t* route_groups;
 };
 
 // ---- weight decode ---------------------------------------------------------------------------------------------
@@ -205,7 +214,42 @@ __global__ __launch_bounds__(KW == 16 ? 640 : 1024) void gemv_row(Args a) {
   const int tile = blockIdx.x;
   int expert = 0, cnt = a.m;
   const int32_t* pairs = nullptr;
-  if (a.groups) {
+  __shared__ int route_sel[ROUTE_MAX_K + 2];    // routing for itself: the slots' experts, then this group's pair
+  if (a.route_logits) {                         // workgroup-uniform: one token, group g = slot g
+    if (wave == 0) {
+      int ce[ROUTE_MAX_K];
+      float cw[ROUTE_MAX_K];
+      route_topk(a.route_logits, a.route_e, a.route_k, a.route_renorm, lane, ce, cw);
+      const int k = a.route_k, ks = k + (a.shared_expert > 0 ? 1 : 0);
+      if (lane == 0) {
+        for (int r = 0; r < k; ++r) route_sel[r] = ce[r];
+        if (ks > k) route_sel[k] = a.shared_expert;
+        route_sel[ROUTE_MAX_K + 1] = blockIdx.y;
+        if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0) {   // the route for the launches after this one
+          for (int r = 0; r < k; ++r) {
+            a.route_ids[r] = ce[r];
+            a.route_weights[r] = cw[r];
+          }
+          if (ks > k) {
+            a.route_ids[k] = a.shared_expert;
+            a.route_weights[k] = route_shared_weight(bf16_bits_to_f32(a.route_logits[a.route_gate_col]));
+          }
+          for (int r = 0; r < a.route_n; ++r) {                          // record r = slot r (pair r)
+            int32_t* rec = a.route_groups + r * GROUP_REC;
+            const int e = r < ks ? (r < k ? ce[r] : a.shared_expert) : -1;
+            rec[0] = e;
+            rec[1] = e >= 0 ? 1 : 0;
+            rec[2] = r;
+          }
+        }
+      }
+    }
+    __syncthreads();
+    expert = route_sel[blockIdx.y];
+    cnt = 1;
+    pairs = &route_sel[ROUTE_MAX_K + 1];
+    if (expert < 0) return;                   // a slot without an expert (NaN logits): the workgroup leaves
+  } else if (a.groups) {
     const int32_t* g = a.groups + blockIdx.y * GROUP_REC;
     expert = g[0];
     cnt = g[1];
@@ -1638,6 +1682,15 @@ int check_desc(const mi_gemv_desc* d) {
                                                        d->shared_epilogue != MI_EPI_RESIDUAL),
                "mi_gemv: the shared expert's epilogue must give the routed experts' output width (no residual)");
   }
+  if (d->route_logits) {
+    const int ks = d->route_top_k + (d->shared_expert > 0 ? 1 : 0);
+    MI_REQUIRE(d->groups && d->m == 1 && d->route_experts >= 1 && d->route_experts <= 64 * ROUTE_MAX_PER_LANE &&
+                   d->route_top_k >= 1 && d->route_top_k <= ROUTE_MAX_K && d->route_top_k <= d->route_experts &&
+                   d->top_k == ks && d->max_groups == ks && d->route_ids && d->route_weights &&
+                   (d->shared_expert <= 0 || (d->shared_expert >= d->route_experts && d->route_gate_col >= 0)),
+               "mi_gemv: routing in the launch needs one token, groups = slots = route_top_k (+1 with the shared "
+               "expert), 1..512 experts, top_k <= 16 and the route outputs");
+  }
   MI_REQUIRE(((uintptr_t)d->x & 15) == 0 && d->ldx % 8 == 0, "mi_gemv: x must be 16-byte aligned with ldx %% 8 == 0");
   MI_REQUIRE(((uintptr_t)d->w & 15) == 0, "mi_gemv: weight pack must be 16-byte aligned");
   MI_REQUIRE(!d->norm_w || ((uintptr_t)d->norm_w & 15) == 0, "mi_gemv: norm_w must be 16-byte aligned");
@@ -2032,6 +2085,7 @@ int gemv_impl(const mi_gemv_desc* d, void* stream, void* fixed_ws, size_t fixed_
   if (int rc = check_desc(d)) return rc;
   const Plan p = make_plan(d);
   MI_REQUIRE(p.kernel, "%s: no launch plan fits (k=%d, m=%d)", name, d->k, d->m);
+  MI_REQUIRE(!d->route_logits || (p.kernel == 1 && p.ks == 1), "%s: routing in the launch runs on gemv_row", name);
   Args a{};
   a.w = static_cast<const uint8_t*>(d->w);
   a.row_scale = d->row_scale;
@@ -2054,6 +2108,15 @@ int gemv_impl(const mi_gemv_desc* d, void* stream, void* fixed_ws, size_t fixed_
   a.epilogue = d->epilogue;
   a.shared_expert = d->groups ? d->shared_expert : 0;
   a.shared_epilogue = d->shared_epilogue;
+  a.route_logits = d->route_logits;
+  a.route_e = d->route_experts;
+  a.route_k = d->route_top_k;
+  a.route_renorm = d->route_renorm;
+  a.route_gate_col = d->route_gate_col;
+  a.route_n = d->max_groups;
+  a.route_ids = d->route_ids;
+  a.route_weights = d->route_weights;
+  a.route_groups = const_cast<int32_t*>(d->groups);
   a.top_k = d->top_k;
   a.x_per_slot = d->x_per_slot;
   a.out_f32 = d->out_f32;

@@ -14,13 +14,14 @@
 //    p = t·k + j, ascending) — so the expert GEMVs stream exactly the chosen experts, each once per step.
 //  * moe_combine: one workgroup per token, 8 columns per lane with 16-byte loads.
 #include "mi_common.h"
+#include "route.h"
 
 #include <algorithm>
 
 namespace {
 
-constexpr int MAX_PER_LANE = 8;      // E <= 512
-constexpr int MAX_K = 16;
+constexpr int MAX_PER_LANE = ROUTE_MAX_PER_LANE;   // E <= 512
+constexpr int MAX_K = ROUTE_MAX_K;
 constexpr int MAX_T = 16;
 constexpr int GROUP_REC = 18;        // expert, count, 16 pair ids (the grouped GEMV's record)
 
@@ -33,8 +34,6 @@ struct RouteArgs {
   int shared_expert, shared_gate_col;           // shared_expert > 0: slot top_k of every token (the shared expert)
 };
 
-__device__ __forceinline__ float wave_min(float v) { return -wave_max(-v); }
-
 __global__ __launch_bounds__(64 * MAX_T) void moe_route(RouteArgs a) {
   __shared__ int sel[MAX_T * (MAX_K + 1)];
   __shared__ int fresh[64 * MAX_T];
@@ -42,61 +41,21 @@ __global__ __launch_bounds__(64 * MAX_T) void moe_route(RouteArgs a) {
   const int E = a.n_experts, k = a.top_k;
   const int ks = k + (a.shared_expert > 0 ? 1 : 0);   // slots per token (the shared expert last)
   if (t < a.t) {                                    // wave-uniform
-    float v[MAX_PER_LANE];
-    float m = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < MAX_PER_LANE; ++i) {
-      const int e = lane + 64 * i;
-      v[i] = e < E ? bf16_bits_to_f32(a.logits[(long long)t * a.ld_logits + e]) : -INFINITY;
-      m = fmaxf(m, v[i]);
-    }
-    m = wave_max(m);
-    float s = 0.0f;
-#pragma unroll
-    for (int i = 0; i < MAX_PER_LANE; ++i) {
-      const int e = lane + 64 * i;
-      v[i] = e < E ? expf(v[i] - m) : 0.0f;
-      s += v[i];
-    }
-    s = wave_sum(s);
-#pragma unroll
-    for (int i = 0; i < MAX_PER_LANE; ++i) v[i] = lane + 64 * i < E ? v[i] / s : -1.0f;   // -1: absent or taken
-    float cw[MAX_K];
     int ce[MAX_K];
-    float wsum = 0.0f;
+    float cw[MAX_K];
+    route_topk(a.logits + (long long)t * a.ld_logits, E, k, a.renorm, lane, ce, cw);
     for (int r = 0; r < k; ++r) {
-      float best = -1.0f;
-      int bi = 1 << 20;
-#pragma unroll
-      for (int i = 0; i < MAX_PER_LANE; ++i)
-        if (v[i] > best) { best = v[i]; bi = lane + 64 * i; }        // strictly greater: the lane's lowest index
-      const float gmax = wave_max(best);
-      int e = (int)wave_min(best == gmax ? (float)bi : (float)(1 << 20));
-      if (e >= E) {                     // no finite probability left (NaN logits): no expert, weight 0
-        ce[r] = -1;
-        cw[r] = 0.0f;
-        continue;
-      }
-#pragma unroll
-      for (int i = 0; i < MAX_PER_LANE; ++i)
-        if (lane + 64 * i == e) v[i] = -1.0f;
-      ce[r] = e;
-      cw[r] = gmax;
-      wsum += gmax;
-    }
-    for (int r = 0; r < k; ++r) {
-      const float w = a.renorm && wsum > 0.0f ? cw[r] / wsum : cw[r];
       if (lane == 0) {
         a.ids[t * ks + r] = ce[r];
-        a.weights[t * ks + r] = round_bf16(w);
+        a.weights[t * ks + r] = cw[r];
       }
       sel[t * ks + r] = ce[r];
     }
     if (a.shared_expert > 0) {                      // the shared expert: weight bf16(σ(its gate's logit))
       if (lane == 0) {
-        const float g = bf16_bits_to_f32(a.logits[(long long)t * a.ld_logits + a.shared_gate_col]);
         a.ids[t * ks + k] = a.shared_expert;
-        a.weights[t * ks + k] = round_bf16(1.0f / (1.0f + expf(-g)));
+        a.weights[t * ks + k] =
+            route_shared_weight(bf16_bits_to_f32(a.logits[(long long)t * a.ld_logits + a.shared_gate_col]));
       }
       sel[t * ks + k] = a.shared_expert;
     }

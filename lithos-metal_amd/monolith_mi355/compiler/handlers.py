@@ -76,6 +76,11 @@ def _gemv_common(ctx: EmitContext, op: Op, *, out_f32: bool = False, grouped: bo
                        shared_expert=int(a.get("shared_expert", 0)),
                        shared_epilogue=EPILOGUE[a.get("shared_epilogue")])
         ptrs["groups"] = groups
+        route = a.get("route")
+        if route is not None:                       # one token: the launch routes for itself
+            scalars.update(route_experts=route["logits"].shape[1], route_top_k=route["top_k"],
+                           route_renorm=int(route.get("renorm", True)), route_gate_col=route.get("gate_col", 0))
+            ptrs.update(route_logits=route["logits"], route_ids=route["ids"], route_weights=route["weights"])
     probe = _probe(hip.MiGemvDesc, scalars, [f for f, v in ptrs.items() if v is not None])
     need = int(hip.load().mi_gemv_workspace_bytes(C.byref(probe)))
     if need:
@@ -100,7 +105,8 @@ def lm_head(ctx: EmitContext, op: Op):
 def moe_gemv(ctx: EmitContext, op: Op):
     """``moe_gemv`` (``ops/moe.py``): the grouped GEMV over the experts the route chose."""
     scalars, ptrs = _gemv_common(ctx, op, grouped=True)
-    return lib_op(ctx, "mi_gemv", hip.MiGemvDesc, scalars, ptrs, op.attrs.get("name", "moe_gemv"), writes=("y",))
+    writes = ("y", "groups", "route_ids", "route_weights") if op.attrs.get("route") is not None else ("y",)
+    return lib_op(ctx, "mi_gemv", hip.MiGemvDesc, scalars, ptrs, op.attrs.get("name", "moe_gemv"), writes=writes)
 
 
 def rmsnorm_stat(ctx: EmitContext, op: Op):

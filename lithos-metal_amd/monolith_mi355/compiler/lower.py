@@ -49,8 +49,9 @@ def lower_moe(g: Graph, moe, h: Value, prefix: str) -> Value:
     """A ``layers.MoeBlock`` (``nn/moe.py``): the router and the shared expert's σ-gate as one BF16 GEMV of E + 1 rows
     into a row padded to 8, the top-k route with its expert groups, the grouped gate|up and down GEMVs, the weighted
     combine with the residual. With the shared expert stacked after the routed ones (``fused_shared``) it is slot k
-    of every token inside the grouped launches (its own silu·mul epilogue) and of the combine; otherwise it runs as
-    two dense GEMVs first and the combine adds it with its gate. One stream: the ops run in this order."""
+    of every token inside the grouped launches (its own silu·mul epilogue) and of the combine, and at one token the
+    gate|up launch routes for itself (no route op); otherwise the shared expert runs as two dense GEMVs first and
+    the combine adds it with its gate. One stream: the ops run in this order."""
     m, e, k = g.t, moe.experts, moe.top_k
     pad = (e + 1 + 7) // 8 * 8
     norm = bound(f"{prefix}.norm", moe.norm_w, "weights")
@@ -75,15 +76,19 @@ def lower_moe(g: Graph, moe, h: Value, prefix: str) -> Value:
     from ..kernels import GROUP_REC
     groups = act(f"{prefix}.groups", min(e, m * k) + (1 if fused else 0), GROUP_REC, dtype="i32")
     shared = dict(shared_expert=e) if fused else {}
-    g.add("moe_route", [route_in], [ids, wts, groups], top_k=k, renorm=True, name=f"{prefix}.route",
-          **(dict(shared_expert=e, shared_gate_col=e) if fused else {}))
+    inline = fused and m == 1                        # one token: the gate|up launch routes for itself
+    if not inline:
+        g.add("moe_route", [route_in], [ids, wts, groups], top_k=k, renorm=True, name=f"{prefix}.route",
+              **(dict(shared_expert=e, shared_gate_col=e) if fused else {}))
     a = act(f"{prefix}.expert_act", m * ks, moe.inter)
     hk = act(f"{prefix}.expert_out", m * ks, moe.hidden)
     gu = moe.gate_up_s if fused else moe.gate_up
     dn = moe.down_s if fused else moe.down
+    extra = dict(shared, shared_epilogue="silu_mul") if fused else {}
+    if inline:
+        extra["route"] = dict(logits=route_in, ids=ids, weights=wts, top_k=k, renorm=True, gate_col=e)
     g.add("moe_gemv", [h, weight(f"{prefix}.gate_up", gu), groups], [a], tokens=m, top_k=ks, x_per_slot=False,
-          epilogue="silu_mul_rounded", norm_w=norm, eps=moe.eps, name=f"{prefix}.experts_gate_up",
-          **(dict(shared, shared_epilogue="silu_mul") if fused else {}))
+          epilogue="silu_mul_rounded", norm_w=norm, eps=moe.eps, name=f"{prefix}.experts_gate_up", **extra)
     g.add("moe_gemv", [a, weight(f"{prefix}.down", dn), groups], [hk], tokens=m, top_k=ks, x_per_slot=True,
           name=f"{prefix}.experts_down", **shared)
     out = act(f"{prefix}.out", m, moe.hidden)

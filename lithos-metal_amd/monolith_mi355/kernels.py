@@ -423,11 +423,14 @@ def moe_route(logits, top_k: int, *, renorm: bool = True, groups: bool = True, o
 
 
 def moe_gemv(w: PackedWeight, x, groups, *, tokens: int, top_k: int, x_per_slot: bool, epilogue=None, norm_w=None,
-             eps: float = 1e-6, out=None, stream=None, shared_expert: int = 0, shared_epilogue=None):
+             eps: float = 1e-6, out=None, stream=None, shared_expert: int = 0, shared_epilogue=None, route=None):
     """``moe_gemv`` (``ops/moe.py``; the grouped mode of ``gemv``): for every group record (expert e, its pairs
     p = t·k + j), ``out[p] = x_row · W_eᵀ`` with ``x_row = x[p]`` (``x_per_slot``) or ``x[p // k]``; ``w`` holds the
     experts back to back. ``out [T·k, n_out]`` bf16. ``shared_expert`` > 0: that expert's group (the shared expert
-    stacked after the routed ones) takes ``shared_epilogue``."""
+    stacked after the routed ones) takes ``shared_epilogue``. ``route`` (one token): ``dict(logits=…, ids=…,
+    weights=…, top_k=k, renorm=True, gate_col=…)`` — the launch routes for itself from the token's router row
+    (exactly ``moe_route``'s ids and weights), group g = slot g, and writes ids / weights and the group records into
+    ``groups`` for the launches after it; ``top_k`` is then k (+1 with ``shared_expert``)."""
     torch = _torch()
     _bf16_2d(x, "moe_gemv x")
     if x.shape[1] != w.k:
@@ -450,6 +453,14 @@ def moe_gemv(w: PackedWeight, x, groups, *, tokens: int, top_k: int, x_per_slot:
                        eps=eps, groups=hip.ptr(groups), max_groups=groups.shape[0], top_k=top_k,
                        x_per_slot=int(x_per_slot), workspace=0, workspace_bytes=0, out_f32=0,
                        shared_expert=shared_expert, shared_epilogue=hip.MI_EPI[shared_epilogue])
+    if route is not None:
+        lg = route["logits"]
+        if lg.dtype != torch.bfloat16 or lg.dim() != 2 or lg.shape[0] != 1 or tokens != 1:
+            raise ValueError("moe_gemv: routing in the launch takes one token's bf16 logits row [1, E]")
+        d.route_logits, d.route_experts = hip.ptr(lg), lg.shape[1]
+        d.route_top_k, d.route_renorm = route["top_k"], int(route.get("renorm", True))
+        d.route_gate_col = route.get("gate_col", 0)
+        d.route_ids, d.route_weights = hip.ptr(route["ids"]), hip.ptr(route["weights"])
     hip.call("mi_gemv", C.byref(d), hip.stream_handle(stream))
     return out
 

@@ -391,11 +391,15 @@ class MoeBlock:
         e, k = self.experts, self.top_k
         if self.fused_shared:
             kernels.gemv(self.router_gate, h, norm_w=self.norm_w, eps=self.eps, out=logits[:, :e + 1])
-            _, wts, groups = kernels.moe_route(logits[:, :e], k, renorm=True, out=route, shared_expert=e,
-                                               shared_gate=e)
+            ids, wts, groups = route
+            if m == 1:                  # one token: the expert gate|up launch routes for itself (one launch fewer)
+                inline = dict(logits=logits[:, :e], ids=ids, weights=wts, top_k=k, renorm=True, gate_col=e)
+            else:
+                kernels.moe_route(logits[:, :e], k, renorm=True, out=route, shared_expert=e, shared_gate=e)
+                inline = None
             kernels.moe_gemv(self.gate_up_s, h, groups, tokens=m, top_k=k + 1, x_per_slot=False,
                              epilogue="silu_mul_rounded", norm_w=self.norm_w, eps=self.eps, out=act,
-                             shared_expert=e, shared_epilogue="silu_mul")
+                             shared_expert=e, shared_epilogue="silu_mul", route=inline)
             kernels.moe_gemv(self.down_s, act, groups, tokens=m, top_k=k + 1, x_per_slot=True, out=hk)
             return kernels.moe_combine(hk, wts, top_k=k + 1, residual=h, out=out)
 

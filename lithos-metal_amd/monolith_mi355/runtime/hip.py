@@ -35,7 +35,9 @@ class MiGemvDesc(C.Structure):
                 ("max_groups", C.c_int32), ("top_k", C.c_int32), ("x_per_slot", C.c_int32),
                 ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t), ("out_f32", C.c_int32),
                 ("gnorm_w", C.c_void_p), ("gnorm_z", C.c_void_p), ("ld_gnorm_z", C.c_int32), ("gnorm_eps", C.c_float),
-                ("shared_expert", C.c_int32), ("shared_epilogue", C.c_int32)]
+                ("shared_expert", C.c_int32), ("shared_epilogue", C.c_int32), ("route_logits", C.c_void_p),
+                ("route_experts", C.c_int32), ("route_top_k", C.c_int32), ("route_renorm", C.c_int32),
+                ("route_gate_col", C.c_int32), ("route_ids", C.c_void_p), ("route_weights", C.c_void_p)]
 
 
 class MiGdnDesc(C.Structure):

@@ -146,7 +146,9 @@ def test_emitted_moe_program_equals_step_program(torch_gpu):
     b = model(31)
     p = compile_program(b, Profile(ring_capacity=64, ctx_cap=256))
     names = [o.name for o in p.ops]
-    assert "layers.0.mlp.route" in names and "layers.0.mlp.combine" in names
+    # one token: the expert gate|up launch routes for itself (no route op); the combine takes the shared slot
+    assert "layers.0.mlp.route" not in names and "layers.0.mlp.combine" in names
+    assert "layers.0.mlp.experts_gate_up" in names
     eng = Engine(p, buffers=bound_buffers(p))
     eng.buffers[p.step_state].write(p.layout.pack(dict(position=40, kv_len=40, t_this_step=1, pending_tokens=[3],
                                                        anchor=3)), 0)

@@ -221,6 +221,45 @@ def test_moe_route_with_the_shared_expert_slot(torch_gpu, t):
     assert list(recs[recs[:, 0] != e, 0]) == list(plain[plain[:, 1] > 0, 0])
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("nan_row", [False, True])
+def test_moe_gemv_routes_for_itself_at_one_token(torch_gpu, nan_row):
+    """At one token the expert gate|up launch routes for itself (``route=``): the same ids and weights as
+    ``moe_route`` bit for bit, the group records slot by slot (one pair each), and the same activations as the
+    launch fed ``moe_route``'s groups; a NaN logits row routes nowhere (experts -1, weight 0, no group computes)."""
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    from monolith_mi355.layers import MoeBlock
+    blk = MoeBlock(experts=64, seed=7)
+    e, k = 64, 8
+    rng = np.random.default_rng(3)
+    h = to_dev_bf16(torch, rbf(rng.standard_normal((1, 2048))))
+    lg = rbf(rng.standard_normal((1, 72)))
+    if nan_row:
+        lg[0, :e] = np.nan
+    logits = to_dev_bf16(torch, lg)
+    ids_a, w_a, g_a = kernels.moe_route(logits[:, :e], k, renorm=True, shared_expert=e, shared_gate=e)
+    act_a = kernels.moe_gemv(blk.gate_up_s, h, g_a, tokens=1, top_k=k + 1, x_per_slot=False,
+                             epilogue="silu_mul_rounded", norm_w=blk.norm_w, shared_expert=e,
+                             shared_epilogue="silu_mul")
+    ids_b = torch.full((1, k + 1), -7, dtype=torch.int32, device="cuda")
+    w_b = torch.zeros(1, k + 1, dtype=torch.float32, device="cuda")
+    g_b = torch.full((k + 1, kernels.GROUP_REC), -7, dtype=torch.int32, device="cuda")
+    act_b = torch.zeros_like(act_a)
+    kernels.moe_gemv(blk.gate_up_s, h, g_b, tokens=1, top_k=k + 1, x_per_slot=False, epilogue="silu_mul_rounded",
+                     norm_w=blk.norm_w, shared_expert=e, shared_epilogue="silu_mul", out=act_b,
+                     route=dict(logits=logits[:, :e], ids=ids_b, weights=w_b, top_k=k, renorm=True, gate_col=e))
+    torch.cuda.synchronize()
+    assert torch.equal(ids_a, ids_b) and torch.equal(w_a.view(torch.int32), w_b.view(torch.int32))
+    gb = g_b.cpu().numpy()
+    ib = ids_b.cpu().numpy()[0]
+    assert list(gb[:, 0]) == list(ib) and list(gb[:, 1]) == [int(x >= 0) for x in ib] and list(gb[:, 2]) == list(range(k + 1))
+    rows = [r for r in range(k + 1) if ib[r] >= 0]                   # slots with an expert were computed
+    assert torch.equal(act_a[rows], act_b[rows])
+    if nan_row:
+        assert (ib[:k] == -1).all() and ib[k] == e and len(rows) == 1
+
+
 def test_moe_rejects_bad_descriptors():
     import ctypes as C
     from monolith_mi355.runtime import hip
