@@ -228,6 +228,26 @@ def main():
                                                        + m * 4 * (2 * 128 + 4))
                 del caches
                 torch.cuda.empty_cache()
+            # the reference's own attention geometry (24 / 4 heads of 256, BF16 cache: nn/attention.py:87-89) at 32K
+            cos2, sin2 = kernels.rope_tables(1e6, 64, CTX, device=dev)
+            qn2 = 1.0 + torch.randn(256, generator=gen, device=dev) * 0.1
+            kn2 = 1.0 + torch.randn(256, generator=gen, device=dev) * 0.1
+            per = CTX * 4 * 4 * 256
+            caches = [KVCache(4, CTX, 256, device=dev, dtype="bf16") for _ in range(-(-(2 << 30) // per))]
+            for c in caches:
+                c.k_codes.normal_(generator=gen)
+                c.v_codes.normal_(generator=gen)
+            for m in (1, 8):
+                pos = CTX - 16
+                proj = torch.randn(m, 24 * 512 + 8 * 256, generator=gen, device=dev).to(torch.bfloat16)
+                o = torch.empty(m, 24 * 256, dtype=torch.bfloat16, device=dev)
+                ms = timed_graph(lambda i: kernels.gqa_decode(proj, caches[i % len(caches)], pos, heads=24,
+                                                              rope_cos=cos2, rope_sin=sin2, q_norm=qn2, k_norm=kn2,
+                                                              out=o), len(caches), args.warmup, stream)
+                out[f"gqa_ref_m{m}"] = (ms, (pos + m) * 4 * 4 * 256 + m * proj.shape[1] * 2 + m * 6144 * 2
+                                        + m * 4 * 4 * 256)
+            del caches
+            torch.cuda.empty_cache()
         if args.only in (None, "gdnstep"):
             # the Gated DeltaNet step alone (conv, gates, delta rule, gated norm; output bf16) at M = 1
             # and 8, rotated over ≥ 2 GiB of distinct recurrent states (one per launch of the timed graph)
@@ -385,6 +405,9 @@ def main():
         "gqa_core": {f"ctx{c}k_m{m}": entry(f"gqa_{c}k_m{m}", m) for c in (4, 16, 32) for m in (1, 8)},
         "gqa_core_workload": "configs[2]: gqa_prep + gqa_decode + gqa_merge alone (24 q / 4 KV heads x 128, int8 KV, "
                              "q/k norm, RoPE 64 of 128, gate), position ctx-16, rotated over >= 2 GiB of KV caches",
+        "gqa_core_reference_geometry": {f"ctx32k_m{m}": entry(f"gqa_ref_m{m}", m) for m in (1, 8)},
+        "gqa_core_reference_geometry_workload": "the reference's attention (24 q / 4 KV heads x 256, BF16 KV cache, "
+                                                "q/k norm, RoPE 64, gate) at 32K, rotated over >= 2 GiB of caches",
         "gdn_step_m1": dict(entry("gdnstep_m1", 1), workload="configs[3]: Gated DeltaNet step alone (hk16/hv48 x128, "
                             "conv 4, gated norm, bf16 out), rotated over >= 2 GiB of recurrent states"),
         "gdn_step_m8": entry("gdnstep_m8", 8),

@@ -300,13 +300,16 @@ __global__ __launch_bounds__(64 * NW, (RT == 1 && DH == 128) ? 2 : 1) void gqa_d
   Chunk<DH, BF> cur, nxt;
   if (k_begin < k_end) load_k<DH, BF>(a, j, k_begin, m16, kg, cur);   // chunks lie inside the cache: ctx % 64 == 0
 
-  // the query rows as B tiles (k-permuted: lane holds dims (DH/4)·kg + 8·s + i of row 16·rt + m16), zero past rows
+  // the query rows as B tiles (k-permuted: lane holds dims (DH/4)·kg + 8·s + i of row r0 + 16·rt + m16), zero past
+  // rows; r0: the first of this workgroup's row tiles (blockIdx.z > 0 when the row tiles are split over workgroups)
+  const int r0 = blockIdx.z * RT * 16;
+  const int nrows = min(RT * 16, a.rows - r0);
   OpT qb[RT][G::NS];
   float rsc[RT];                                        // the lane's row: 2^p of its prescale (int8 cache)
   int qlim[RT];                                         // the lane's row: last key it may see (causal)
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
-    const int row = rt * 16 + m16;
+    const int row = r0 + rt * 16 + m16;
     const bool ok = row < a.rows;
     const uint16_t* src = a.qf + ((long long)j * MAXROWS + (ok ? row : 0)) * DH + (DH / 4) * kg;
 #pragma unroll
@@ -485,9 +488,9 @@ __global__ __launch_bounds__(64 * NW, (RT == 1 && DH == 128) ? 2 : 1) void gqa_d
     }
     __syncthreads();
   }
-  const long long base = ((long long)j * a.n_groups + g) * a.rows;
-  for (int idx = threadIdx.x; idx < a.rows * DH; idx += 64 * NW) a.part_o[base * DH + idx] = red[idx / DH][idx % DH];
-  for (int row = threadIdx.x; row < a.rows; row += 64 * NW) {
+  const long long base = ((long long)j * a.n_groups + g) * a.rows + r0;
+  for (int idx = threadIdx.x; idx < nrows * DH; idx += 64 * NW) a.part_o[base * DH + idx] = red[idx / DH][idx % DH];
+  for (int row = threadIdx.x; row < nrows; row += 64 * NW) {
     float M = -INFINITY, L = 0.0f;
     for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, mls[ww][row][0]);
     for (int ww = 0; ww < NW; ++ww)
@@ -583,10 +586,14 @@ int launch(const GqaArgs& a, int rows, hipStream_t s) {
   MI_TRY_HIP(hipGetLastError(), "gqa_prep launch");
   const dim3 grid(a.n_groups, a.kv), block(64 * NW);
   const int rt = (rows + 15) / 16;
-  if (rt == 1) hipLaunchKernelGGL((gqa_decode<1, DH, BF>), grid, block, 0, s, a);
-  else if (rt == 2) hipLaunchKernelGGL((gqa_decode<2, DH, BF>), grid, block, 0, s, a);
-  else if (rt == 3) hipLaunchKernelGGL((gqa_decode<3, DH, BF>), grid, block, 0, s, a);
-  else hipLaunchKernelGGL((gqa_decode<4, DH, BF>), grid, block, 0, s, a);
+  if constexpr (DH == 256) {     // one row tile per workgroup (grid z): more tiles' accumulators would spill
+    hipLaunchKernelGGL((gqa_decode<1, DH, BF>), dim3(a.n_groups, a.kv, rt), block, 0, s, a);
+  } else {
+    if (rt == 1) hipLaunchKernelGGL((gqa_decode<1, DH, BF>), grid, block, 0, s, a);
+    else if (rt == 2) hipLaunchKernelGGL((gqa_decode<2, DH, BF>), grid, block, 0, s, a);
+    else if (rt == 3) hipLaunchKernelGGL((gqa_decode<3, DH, BF>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((gqa_decode<4, DH, BF>), grid, block, 0, s, a);
+  }
   MI_TRY_HIP(hipGetLastError(), "gqa_decode launch");
   hipLaunchKernelGGL((gqa_merge<DH>), dim3(a.heads, a.t), dim3(64 * MW), 0, s, a);
   MI_TRY_HIP(hipGetLastError(), "gqa_merge launch");
