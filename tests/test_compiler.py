@@ -120,6 +120,30 @@ def test_emitted_program_equals_step_program(torch_gpu):
     # the re-encoded (op by op) run continues the same sequence
     rep2 = eng.run(4, steps_per_cb=2, in_flight=1, reencode=True)
     assert len(rep2.tokens) == 4 and eng.state()["step"] == steps + 4
+    # per-op timings of the emitted step (library calls profiled like run-time kernels)
+    times = eng.profile(1)[0]
+    assert len(times) == len(p.ops) and all(e >= s0 for s0, e in times)
+
+
+@pytest.mark.gpu
+def test_emitted_program_survives_json(torch_gpu):
+    """program.json round trip: the reloaded program, given the same bound buffers (its names are stable), emits
+    the same tokens as the original on a twin model."""
+    torch = torch_gpu
+    from monolith_mi355.compiler import Profile, compile_program
+    from monolith_mi355.runtime.engine import Engine, bound_buffers
+    from monolith_mi355.runtime.program import Program
+    runs = []
+    for reload in (False, True):
+        m = _decoder(torch, 41, "cuda")
+        p = compile_program(m, Profile(ring_capacity=64, ctx_cap=256))
+        q = Program.from_json(p.to_json()) if reload else p
+        eng = Engine(q, buffers=bound_buffers(p))
+        eng.buffers[q.step_state].write(q.layout.pack(dict(position=40, kv_len=40, t_this_step=1,
+                                                           pending_tokens=[5], anchor=5)), 0)
+        runs.append(eng.run(6, steps_per_cb=2, in_flight=2).tokens)
+        torch.cuda.synchronize()
+    assert runs[0] == runs[1] and len(runs[0]) == 6
 
 
 @pytest.mark.gpu
