@@ -910,7 +910,7 @@ void gemv_rowp(Args a) {
 // wave's activations for those chunks stay in VGPRs for the whole launch as the F16 A operands of
 // v_mfma_f32_16x16x32_f16 (token = A row; each token power-of-two scaled into F16 range over the wave's slice;
 // normalized first when the input norm is fused); the weights are the B operand, decoded exactly to F16. Each wave
-// issues tile j + 1 as soon as tile j is consumed (the operands leave no VGPRs for a second tile in flight). A
+// keeps two tiles in flight (NVFP4 / FP8; one for INT4) and issues the next as soon as one is consumed. A
 // tile's K slices meet in LDS after the last tile, in the gemv_row order. INT4: the codes decode to exact F16
 // integers, the activations take the codes' column order (int4_perm8) and each 64-column group's dot product is
 // scaled and offset by its (scale, bias) pair with the token's Σx over the group (held per lane for the launch).
@@ -944,30 +944,37 @@ __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
 
   // ---- the first tile's weights, then the activations ------------------------------------------------------------
   const long long c0_off = FMT == FMT_NVFP4 ? nv_code_off(c0) : (long long)c0 * unit_bytes(FMT);
-  uint2 sb0[I4 ? KW : 1];                       // INT4: the (scale, bias) pairs of row m_row's two groups per chunk
-  auto issue = [&](uint4 (&u)[KW], uint4& sv, int j) {
+  // NVFP4 / FP8 keep two tiles in flight per wave (the 12-wave workgroup leaves 168 VGPRs a lane); INT4's Σx
+  // terms leave room for one
+  constexpr int DEPTH = I4 ? 1 : 2;
+  uint2 sb0[I4 ? KW : 1], sb1[I4 ? KW : 1];     // INT4: the (scale, bias) pairs of row m_row's two groups per chunk
+  auto issue = [&](uint4 (&u)[KW], uint4& sv, uint2 (&sb)[I4 ? KW : 1], int j) {
     const uint8_t* tbase = wmat + (long long)tile_of(j) * a.tile_stride;
+    // every load unconditional (a chunk past the wave's kw re-reads chunk 0 and is never used), so the loads of
+    // the tiles in flight stay in issue order and a tile waits for its own loads only
     if constexpr (FMT == FMT_NVFP4) {
       const int gi = c0 >> 3;
       const uint8_t* p = tbase + nv_scale_off(gi, a.chunks);
-      if (nv_piece(nv_group_chunks(gi, a.chunks)) == 16) {
-        sv = *reinterpret_cast<const uint4*>(p + 16 * lane);
-      } else {
-        const uint2 t = *reinterpret_cast<const uint2*>(p + 8 * lane);
-        sv = uint4{t.x, t.y, 0u, 0u};
-      }
+      // 16 scale bytes a lane in a group of 8 chunks, else 8 (a group of at most 4 chunks starts a slice, so its
+      // lanes use sv.x / sv.y only and t1 repeats t0)
+      const bool wide = nv_piece(nv_group_chunks(gi, a.chunks)) == 16;
+      const uint2 t0 = *reinterpret_cast<const uint2*>(p + (wide ? 16 : 8) * lane);
+      const uint2 t1 = *reinterpret_cast<const uint2*>(p + (wide ? 16 * lane + 8 : 8 * lane));
+      sv = uint4{t0.x, t0.y, t1.x, t1.y};
     } else {
       sv = uint4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
-    for (int cc = 0; cc < KW; ++cc)             // 1 KiB of codes per chunk
-      if (cc < kw) {
-        u[cc] = *reinterpret_cast<const uint4*>(tbase + c0_off + cc * UB + 16 * lane);
-        if constexpr (I4) sb0[cc] = *reinterpret_cast<const uint2*>(tbase + c0_off + cc * UB + 1024 + 8 * (lane & 15));
-      }
+    for (int cc = 0; cc < KW; ++cc) {           // 1 KiB of codes per chunk
+      const long long off = c0_off + (cc < kw ? cc : 0) * UB;
+      u[cc] = *reinterpret_cast<const uint4*>(tbase + off + 16 * lane);
+      if constexpr (I4) sb[cc] = *reinterpret_cast<const uint2*>(tbase + off + 1024 + 8 * (lane & 15));
+    }
+    __builtin_amdgcn_sched_barrier(0);          // the tile's loads stay where they are in the issue order
   };
-  uint4 u0[KW], s0;
-  issue(u0, s0, 0);
+  uint4 u0[KW], s0, u1[KW], s1;
+  issue(u0, s0, sb0, 0);
+  if (DEPTH > 1) issue(u1, s1, sb1, min(1, ntl - 1));
 
   // x[token m_row][c0·KC + cc·KC + col(g, s) + (0..7)]: the A operand of step s of chunk cc, col(g, s) =
   // (KC/4)·g + 8s (NVFP4 / FP8) or 32s + 8g (INT4: the codes' column order in a unit)
@@ -1139,9 +1146,23 @@ __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) rp[(4 * g + i) * 16 + m_row] = active ? acc[i] * ps[i] : 0.0f;
   };
-  for (int j = 0; j < ntl; ++j) {
-    tile_mma(u0, s0, sb0, j);
-    if (j + 1 < ntl) issue(u0, s0, j + 1);
+  if constexpr (DEPTH == 1) {
+    for (int j = 0; j < ntl; ++j) {
+      tile_mma(u0, s0, sb0, j);
+      if (j + 1 < ntl) issue(u0, s0, sb0, j + 1);
+    }
+  } else {
+    // tiles j and j + 1 in flight: consume one, issue j + 2 into its place. Every issue happens (past the last
+    // tile it re-reads the last tile, from L2, unused), so each tile's loads are older than exactly one tile's
+    // and its wait leaves the other tile in flight
+    int j = 0;
+    for (; j + 1 < ntl; j += 2) {
+      tile_mma(u0, s0, sb0, j);
+      issue(u0, s0, sb0, min(j + 2, ntl - 1));
+      tile_mma(u1, s1, sb1, j + 1);
+      issue(u1, s1, sb1, min(j + 3, ntl - 1));
+    }
+    if (j < ntl) tile_mma(u0, s0, sb0, j);
   }
 
   // ---- per (tile, token): the K slices in the gemv_row order, then the epilogue --------------------------------
