@@ -45,20 +45,6 @@ struct GdnArgs {
   long long conv_slot;      // elements per conv-state slot
 };
 
-// the conv state this launch reads and writes: the given buffers, or the two slots by the step's parity (the
-// commit pass runs after the accept scan advanced the step: it reads the slot the verify pass read)
-__device__ __forceinline__ void conv_slots(const GdnArgs& a, const uint16_t*& cin, uint16_t*& cout) {
-  if (!a.step) {
-    cin = a.conv_in;
-    cout = a.conv_out;
-    return;
-  }
-  const uint32_t rd = (*a.step + (a.commit ? 1u : 0u)) & 1u;
-  uint16_t* base = const_cast<uint16_t*>(a.conv_in);
-  cin = base + rd * a.conv_slot;
-  cout = base + (rd ^ 1u) * a.conv_slot;
-}
-
 // tokens this launch takes: the device count (commit pass) or t, and none once the program has stopped — with
 // T = 0 the kernel copies conv_in → conv_out and rec_in → rec_out unchanged and writes no read-out
 __device__ __forceinline__ int tokens_now(const GdnArgs& a) {
@@ -71,6 +57,8 @@ __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)
 __device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : log1pf(__expf(x)); }
 __device__ __forceinline__ float bf(const uint16_t* p, long long i) { return bf16_bits_to_f32(p[i]); }
 
+// TT: a bound on the tokens (>= a.t), so the conv waves' loads are a fixed, unconditional set
+template <int TT>
 __global__ __launch_bounds__(64 * (WAVES + CONV_WAVES)) void gdn_step(GdnArgs a) {
   __shared__ float qs[TMAX][DK];   // conv → silu → L2-norm (q also /√dk)
   __shared__ float ks[TMAX][DK];
@@ -78,10 +66,10 @@ __global__ __launch_bounds__(64 * (WAVES + CONV_WAVES)) void gdn_step(GdnArgs a)
   __shared__ float beta_s[TMAX], eg_s[TMAX];
   const int h = blockIdx.x, sl = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the device words first (the oldest loads, so waiting for them waits for nothing else): the token count and
+  // the step counter that picks the conv slots
   const int T = tokens_now(a);
-  const uint16_t* conv_in;
-  uint16_t* conv_out;
-  conv_slots(a, conv_in, conv_out);
+  const uint32_t rd = a.step ? ((*a.step + (a.commit ? 1u : 0u)) & 1u) : 0u;
   const int rep = a.hv / a.hk;
   const int kh = h / rep;
   const int key_dim = a.hk * DK;
@@ -96,54 +84,77 @@ __global__ __launch_bounds__(64 * (WAVES + CONV_WAVES)) void gdn_step(GdnArgs a)
     const float* sin = a.rec_in + (long long)h * DK * DV;
 #pragma unroll
     for (int i = 0; i < 32; ++i) s[i] = sin[(long long)(32 * rg + i) * DV + col];
-  }
-
-  // ---- causal conv1d + SiLU over the head's q, k (key head kh) and this slice's v channels ---------------------
-  const bool kw_writer = (h % rep) == 0 && sl == 0;   // the workgroup that writes its key head's q/k conv state
-  for (int cidx = tid - 64 * WAVES; cidx >= 0 && cidx < 2 * DK + SLICE; cidx += 64 * CONV_WAVES) {
-    int ch;           // channel index in the conv input order q | k | v
-    int src_off;      // column of that channel in proj
-    float* dst;
-    int ld;           // LDS row stride of dst
-    bool writer;      // which workgroup writes this channel's new conv state
-    if (cidx < DK) { ch = kh * DK + cidx; src_off = a.q_off + kh * DK + cidx; dst = &qs[0][cidx]; ld = DK; writer = kw_writer; }
-    else if (cidx < 2 * DK) { const int i = cidx - DK; ch = key_dim + kh * DK + i; src_off = a.k_off + kh * DK + i; dst = &ks[0][i]; ld = DK; writer = kw_writer; }
-    else {
-      const int i = cidx - 2 * DK, hc = sl * SLICE + i;
-      ch = 2 * key_dim + h * DV + hc; src_off = a.v_off + h * DV + hc; dst = &vs[0][i]; ld = SLICE; writer = true;
-    }
-    float w[CW], xs[CW - 1 + TMAX];
+  } else {
+    // ---- causal conv1d + SiLU over the head's q, k (key head kh) and this slice's v channels: CPT channels per
+    // thread. Every load is issued before any is used and none is conditional (a channel index past the last
+    // re-reads the last, rows past a.t - 1 re-read that row, and both conv slots are read when the step picks
+    // one), so the whole section waits for one round of memory latency
+    constexpr int NCH = 2 * DK + SLICE, CPT = (NCH + 64 * CONV_WAVES - 1) / (64 * CONV_WAVES);
+    const int ct = tid - 64 * WAVES;
+    const int tl = a.t - 1;
+    const bool kw_writer = (h % rep) == 0 && sl == 0;   // the workgroup that writes its key head's q/k conv state
+    const uint16_t* slot1 = a.step ? a.conv_in + a.conv_slot : a.conv_in;
+    int chs[CPT], offs[CPT];
+    uint2 wv[CPT];
+    uint16_t cs[2][CPT][CW - 1], xp[CPT][TT];
 #pragma unroll
-    for (int j = 0; j < CW; ++j) w[j] = bf(a.conv_w, (long long)ch * CW + j);
-#pragma unroll
-    for (int j = 0; j < CW - 1; ++j) xs[j] = bf(conv_in, (long long)ch * (CW - 1) + j);
-#pragma unroll
-    for (int t = 0; t < TMAX; ++t) xs[CW - 1 + t] = t < T ? bf(a.proj, (long long)t * a.ldp + src_off) : 0.0f;
-#pragma unroll
-    for (int t = 0; t < TMAX; ++t) {
-      if (t >= T) break;
-      float y = 0.0f;
-#pragma unroll
-      for (int j = 0; j < CW; ++j) y = __fadd_rn(y, __fmul_rn(w[j], xs[j + t]));   // the oracle's y += w·x
-      dst[t * ld] = round_bf16(silu_f(round_bf16(y)));
-    }
-    if (writer) {                 // the last CW-1 inputs of [state | x]
+    for (int k = 0; k < CPT; ++k) {
+      const int cidx = min(ct + 64 * CONV_WAVES * k, NCH - 1);
+      const int i = cidx < DK ? cidx : cidx < 2 * DK ? cidx - DK : cidx - 2 * DK;
+      chs[k] = cidx < DK ? kh * DK + i : cidx < 2 * DK ? key_dim + kh * DK + i : 2 * key_dim + h * DV + sl * SLICE + i;
+      offs[k] = cidx < DK ? a.q_off + kh * DK + i : cidx < 2 * DK ? a.k_off + kh * DK + i : a.v_off + h * DV + sl * SLICE + i;
+      wv[k] = *reinterpret_cast<const uint2*>(a.conv_w + (long long)chs[k] * CW);   // CW = 4 BF16 taps, 8 bytes
 #pragma unroll
       for (int j = 0; j < CW - 1; ++j) {
-        float v = xs[j];
+        cs[0][k][j] = a.conv_in[(long long)chs[k] * (CW - 1) + j];
+        cs[1][k][j] = slot1[(long long)chs[k] * (CW - 1) + j];
+      }
 #pragma unroll
-        for (int t = 1; t <= TMAX; ++t) v = (t == T) ? xs[t + j] : v;
-        conv_out[(long long)ch * (CW - 1) + j] = f32_to_bf16_bits(v);
+      for (int t = 0; t < TT; ++t) xp[k][t] = a.proj[(long long)min(t, tl) * a.ldp + offs[k]];
+    }
+    // gates per token: β = bf16(σ(b)), e^g with g = −exp(A_log)·softplus(a + dt_bias)
+    const int tg = min(ct, tl);
+    const uint16_t bq = a.ab[(long long)tg * a.ldab + a.b_off + h], aq = a.ab[(long long)tg * a.ldab + a.a_off + h];
+    const float nea = a.neg_exp_a[h], dtb = a.dt_bias[h];
+
+    uint16_t* conv_out = a.step ? const_cast<uint16_t*>(a.conv_in) + (rd ^ 1u) * a.conv_slot : a.conv_out;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int cidx = ct + 64 * CONV_WAVES * k;
+      if (cidx >= NCH) break;
+      const int i = cidx < DK ? cidx : cidx < 2 * DK ? cidx - DK : cidx - 2 * DK;
+      float* dst = cidx < DK ? &qs[0][i] : cidx < 2 * DK ? &ks[0][i] : &vs[0][i];
+      const int ld = cidx < 2 * DK ? DK : SLICE;
+      const bool writer = cidx < 2 * DK ? kw_writer : true;   // which workgroup writes this channel's conv state
+      const float w[CW] = {bf16_bits_to_f32(wv[k].x & 0xFFFFu), bf16_bits_to_f32(wv[k].x >> 16),
+                           bf16_bits_to_f32(wv[k].y & 0xFFFFu), bf16_bits_to_f32(wv[k].y >> 16)};
+      float xs[CW - 1 + TT];
+#pragma unroll
+      for (int j = 0; j < CW - 1; ++j) xs[j] = bf16_bits_to_f32(rd ? cs[1][k][j] : cs[0][k][j]);
+#pragma unroll
+      for (int t = 0; t < TT; ++t) xs[CW - 1 + t] = t < T ? bf16_bits_to_f32(xp[k][t]) : 0.0f;
+#pragma unroll
+      for (int t = 0; t < TT; ++t) {
+        if (t >= T) break;
+        float y = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CW; ++j) y = __fadd_rn(y, __fmul_rn(w[j], xs[j + t]));   // the oracle's y += w·x
+        dst[t * ld] = round_bf16(silu_f(round_bf16(y)));
+      }
+      if (writer) {                 // the last CW-1 inputs of [state | x]
+#pragma unroll
+        for (int j = 0; j < CW - 1; ++j) {
+          float v = xs[j];
+#pragma unroll
+          for (int t = 1; t <= TT; ++t) v = (t == T) ? xs[t + j] : v;
+          conv_out[(long long)chs[k] * (CW - 1) + j] = f32_to_bf16_bits(v);
+        }
       }
     }
-  }
-  // gates per token: β = bf16(σ(b)), e^g with g = −exp(A_log)·softplus(a + dt_bias)
-  if (tid >= 64 * WAVES && tid - 64 * WAVES < T) {
-    const int t = tid - 64 * WAVES;
-    const float bv = bf(a.ab, (long long)t * a.ldab + a.b_off + h);
-    const float av = bf(a.ab, (long long)t * a.ldab + a.a_off + h);
-    beta_s[t] = round_bf16(sigmoid_f(bv));
-    eg_s[t] = expf(a.neg_exp_a[h] * softplus_f(av + a.dt_bias[h]));
+    if (ct < T) {
+      beta_s[ct] = round_bf16(sigmoid_f(bf16_bits_to_f32(bq)));
+      eg_s[ct] = expf(nea * softplus_f(bf16_bits_to_f32(aq) + dtb));
+    }
   }
   __syncthreads();
 
@@ -244,7 +255,12 @@ extern "C" int mi_gdn_step(const mi_gdn_desc* d, void* stream) {
   a.step = d->step;
   a.conv_slot = (long long)(2 * d->k_heads * d->dk + d->v_heads * d->dv) * (d->conv_width - 1);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(gdn_step, dim3(d->v_heads, NSLICE), dim3(64 * (WAVES + CONV_WAVES)), 0, s, a);
+  const dim3 grid(d->v_heads, NSLICE), block(64 * (WAVES + CONV_WAVES));
+  if (d->t == 1) hipLaunchKernelGGL(gdn_step<1>, grid, block, 0, s, a);
+  else if (d->t <= 2) hipLaunchKernelGGL(gdn_step<2>, grid, block, 0, s, a);
+  else if (d->t <= 4) hipLaunchKernelGGL(gdn_step<4>, grid, block, 0, s, a);
+  else if (d->t <= 8) hipLaunchKernelGGL(gdn_step<8>, grid, block, 0, s, a);
+  else hipLaunchKernelGGL(gdn_step<TMAX>, grid, block, 0, s, a);
   MI_TRY_HIP(hipGetLastError(), "gdn_step launch");
   if (!d->defer_norm && !d->commit) {
     hipLaunchKernelGGL(gdn_gated_norm, dim3(d->v_heads, d->t), dim3(64), 0, s, a);
