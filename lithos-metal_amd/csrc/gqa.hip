@@ -158,8 +158,10 @@ __device__ __forceinline__ int prescale_exp(float mx) {   // 2^-p·mx in [2^14, 
 
 // Position of key k (0..63) inside its V block: the P·V MFMA sums over keys in any order, so the order is the one
 // in which the score tile already holds them — lane (kg, m16) holds keys 16·kt + 4·kg + i of score tile kt, and as
-// the B operand of k-block ks its 8 values are tiles 2·ks, 2·ks + 1 — and those 8 keys sit together.
-__device__ __forceinline__ int vblock_pos(int k) { return (k >> 5) * 32 + ((k & 15) >> 2) * 8 + ((k >> 4) & 1) * 4 + (k & 3); }
+// the B operand of k-block ks (keys 32·ks + …) its 8 values are tiles 2·ks, 2·ks + 1 — and those 8 keys sit
+// together, with lane group kg's two k-blocks side by side (16 positions from 16·kg): one 16-byte load per lane
+// and dim for a 64-key int8 chunk.
+__device__ __forceinline__ int vblock_pos(int k) { return ((k & 15) >> 2) * 16 + (k >> 5) * 8 + ((k >> 4) & 1) * 4 + (k & 3); }
 
 template <int DH, bool BF>
 __global__ __launch_bounds__(64) void gqa_prep(GqaArgs a) {
@@ -251,14 +253,23 @@ template <int DH, bool BF>
 __device__ __forceinline__ void load_v(const GqaArgs& a, int j, int k0, int m16, int kg, Chunk<DH, BF>& c) {
   using G = Geo<DH, BF>;
   constexpr int ES = BF ? 2 : 1;
-  // the chunk's keys in their V block: block k0 / 64, positions (k0 % 64) + [0, CH)
+  // the chunk's keys in their V block (block k0 / 64): lane group kg's 8 keys of k-block ks of a chunk starting at
+  // key 32·h of the block sit at positions 16·kg + 8·(h + ks)
   const char* vp = static_cast<const char*>(a.vc) +
-                   (((long long)j * a.ctx + (k0 & ~(BLOCK - 1))) * DH + (k0 & (BLOCK - 1)) + 8 * kg) * ES;
+                   (((long long)j * a.ctx + (k0 & ~(BLOCK - 1))) * DH + 16 * kg + 8 * ((k0 & (BLOCK - 1)) >> 5)) * ES;
+  if constexpr (!BF && G::KS == 2) {            // both k-blocks in one 16-byte load
+#pragma unroll
+    for (int ct = 0; ct < G::NC; ++ct) {
+      const uint4 u = *reinterpret_cast<const uint4*>(vp + (long long)(ct * 16 + m16) * BLOCK);
+      c.v[0][ct][0] = u.x; c.v[0][ct][1] = u.y; c.v[1][ct][0] = u.z; c.v[1][ct][1] = u.w;
+    }
+    return;
+  }
 #pragma unroll
   for (int ks = 0; ks < G::KS; ++ks)
 #pragma unroll
     for (int ct = 0; ct < G::NC; ++ct) {
-      const char* q = vp + ((long long)(ct * 16 + m16) * BLOCK + ks * 32) * ES;
+      const char* q = vp + ((long long)(ct * 16 + m16) * BLOCK + ks * 8) * ES;
       if constexpr (BF) {
         const uint4 u = *reinterpret_cast<const uint4*>(q);
         c.v[ks][ct][0] = u.x; c.v[ks][ct][1] = u.y; c.v[ks][ct][2] = u.z; c.v[ks][ct][3] = u.w;
@@ -277,13 +288,14 @@ __device__ __forceinline__ float f16_hi(uint32_t u) { return (float)__builtin_bi
 // lane's keys plus the lanes l ^ 16, l ^ 32, l ^ 48 of the same row, and Oᵀ += Vᵀ·Pᵀ with Pᵀ straight from the score
 // registers (no LDS round trip) — every per-row quantity is lane-local.
 template <int RT, int DH, bool BF>
-__global__ __launch_bounds__(64 * NW, (RT == 1 && DH == 128) ? 2 : 1) void gqa_decode(GqaArgs a) {
+__global__ __launch_bounds__(64 * NW, 1) void gqa_decode(GqaArgs a) {
   using G = Geo<DH, BF>;
   using OpT = typename std::conditional<BF, bf16x8, f16x8>::type;
   constexpr int CH = G::CH;
   __shared__ __attribute__((aligned(16))) float red[RT * 16][DH + 4];   // the workgroup's O, row-major
   __shared__ float mls[NW][RT * 16][2];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: the key range is a scalar loop
   const int j = blockIdx.y, g = blockIdx.x;
   if (stopped(a)) return;                               // workgroup-uniform
   const int pos = cur_pos(a);
@@ -296,9 +308,6 @@ __global__ __launch_bounds__(64 * NW, (RT == 1 && DH == 128) ? 2 : 1) void gqa_d
   const int k_begin = kb + (w * nch / NW) * CH;
   const int k_end = min(ke, kb + ((w + 1) * nch / NW) * CH);
   const int m16 = lane & 15, kg = lane >> 4;
-
-  Chunk<DH, BF> cur, nxt;
-  if (k_begin < k_end) load_k<DH, BF>(a, j, k_begin, m16, kg, cur);   // chunks lie inside the cache: ctx % 64 == 0
 
   // the query rows as B tiles (k-permuted: lane holds dims (DH/4)·kg + 8·s + i of row r0 + 16·rt + m16), zero past
   // rows; r0: the first of this workgroup's row tiles (blockIdx.z > 0 when the row tiles are split over workgroups)
@@ -321,6 +330,25 @@ __global__ __launch_bounds__(64 * NW, (RT == 1 && DH == 128) ? 2 : 1) void gqa_d
     qlim[rt] = ok ? pos + row / a.rep : n_keys;         // rows past `rows` hold q = 0: finite, never written
   }
 
+  // Where the registers allow (VA), two chunks in flight: buffer A holds chunks k_begin, k_begin + 2·CH, …, B the
+  // ones between, each chunk's K and V loaded one chunk ahead; otherwise each chunk is loaded as it starts.
+  // Every load is issued whether or not its chunk exists (a chunk past the wave's range re-reads the last one in
+  // range, or the range's start when it is empty — chunks lie inside the cache: ctx % 64 == 0), after the query
+  // rows, so the in-order memory counter lets a chunk's wait leave the other chunk's loads outstanding.
+  constexpr bool VA = DH == 128 && (RT <= 2 || (RT == 3 && BF));   // two chunks: at most 48 loads in flight
+  Chunk<DH, BF> ca, cb;
+  const int k_last = k_begin < k_end ? k_begin + ((k_end - 1 - k_begin) / CH) * CH : min(k_begin, a.ctx - CH);
+  auto load_chunk = [&](Chunk<DH, BF>& c, int k0) {
+    const int kk = min(k0, k_last);
+    load_k<DH, BF>(a, j, kk, m16, kg, c);
+    load_v<DH, BF>(a, j, kk, m16, kg, c);
+    __builtin_amdgcn_sched_barrier(0);                // the loads stay here, ahead of the chunk's math
+  };
+  if constexpr (VA) {
+    load_chunk(ca, k_begin);
+    load_chunk(cb, k_begin + CH);
+  }
+
   f32x4 o[RT][G::NC];                                   // o[rt][ct][i] = O[row 16·rt + m16][dim 16·ct + 4·kg + i]
   float m_run[RT], l_run[RT];                           // l_run: this lane's share (its keys per chunk)
 #pragma unroll
@@ -332,11 +360,12 @@ __global__ __launch_bounds__(64 * NW, (RT == 1 && DH == 128) ? 2 : 1) void gqa_d
   }
   int pv_cur = 0;                                       // O is held in units of 2^pv_cur (int8 cache)
 
-  for (int k0 = k_begin; k0 < k_end; k0 += CH) {
-    // this chunk's V, then the next chunk's K side (the last iteration reloads its own, in bounds)
-    load_v<DH, BF>(a, j, k0, m16, kg, cur);
-    load_k<DH, BF>(a, j, k0 + CH < k_end ? k0 + CH : k0, m16, kg, nxt);
-
+  auto process = [&](Chunk<DH, BF>& cur, int k0) {
+    if constexpr (!VA) {                              // no registers for a second chunk: load this one now
+      load_k<DH, BF>(a, j, min(k0, k_last), m16, kg, cur);
+      load_v<DH, BF>(a, j, min(k0, k_last), m16, kg, cur);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     const bool full = k0 + CH <= k_end && k0 + CH - 1 <= pos;     // every key valid and visible to every row
     float ksc[G::KT][4], vsc[G::KT][4];
     int pv = pv_cur;
@@ -442,13 +471,33 @@ __global__ __launch_bounds__(64 * NW, (RT == 1 && DH == 128) ? 2 : 1) void gqa_d
             o[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[rt][ks], o[rt][ct], 0, 0, 0);
         }
       }
-#pragma unroll
-    for (int kt = 0; kt < G::KT; ++kt) {
-#pragma unroll
-      for (int ww = 0; ww < G::KW; ++ww) cur.k[kt][ww] = nxt.k[kt][ww];
-      if constexpr (!BF) {
-        cur.ksc[kt] = nxt.ksc[kt];
-        cur.vsc[kt] = nxt.vsc[kt];
+  };
+  // head dim 128, one row tile: the first two chunks straight-line (all of a wave's range up to 32K keys, where the
+  // compiler's waits are exact; in the loop the waits of the chunk at its head drain both buffers), the rest in the
+  // loop. Larger geometries do not have the registers for the extra copies of the chunk code.
+  constexpr bool SL = RT == 1 && DH == 128;
+  if constexpr (!VA) {
+    for (int k0 = k_begin; k0 < k_end; k0 += CH) process(ca, k0);
+  } else if (!SL) {
+    for (int k0 = k_begin; k0 < k_end; k0 += 2 * CH) {
+      process(ca, k0);
+      load_chunk(ca, k0 + 2 * CH);
+      if (k0 + CH >= k_end) break;
+      process(cb, k0 + CH);
+      load_chunk(cb, k0 + 3 * CH);
+    }
+  } else if (k_begin < k_end) {
+    process(ca, k_begin);
+    load_chunk(ca, k_begin + 2 * CH);
+    if (k_begin + CH < k_end) {
+      process(cb, k_begin + CH);
+      load_chunk(cb, k_begin + 3 * CH);
+      for (int k0 = k_begin + 2 * CH; k0 < k_end; k0 += 2 * CH) {
+        process(ca, k0);
+        load_chunk(ca, k0 + 2 * CH);
+        if (k0 + CH >= k_end) break;
+        process(cb, k0 + CH);
+        load_chunk(cb, k0 + 3 * CH);
       }
     }
   }

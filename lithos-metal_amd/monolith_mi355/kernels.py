@@ -286,7 +286,7 @@ class KVCache:
     4 KV heads × 128 dims many times over."""
 
     BLOCK = 64
-    V_POS = np.array([(k >> 5) * 32 + ((k & 15) >> 2) * 8 + ((k >> 4) & 1) * 4 + (k & 3) for k in range(64)])
+    V_POS = np.array([((k & 15) >> 2) * 16 + (k >> 5) * 8 + ((k >> 4) & 1) * 4 + (k & 3) for k in range(64)])
 
     def __init__(self, kv_heads: int, ctx_max: int, head_dim: int = 128, device="cuda", dtype: str = "int8"):
         torch = _torch()
