@@ -76,37 +76,60 @@ __device__ __forceinline__ f16x8 i8x8_to_f16(uint32_t lo, uint32_t hi) {
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
 
-// q/k head vector of token t after the optional (1+w) RMSNorm and partial RoPE, into dst[D] (BF16 values as f32).
-// The whole wave cooperates: lane l handles dims l + 64·u.
+// A q/k head vector's inputs, every one loaded before any is used (lane l: dims l + 64·u): the BF16 values, the
+// norm weights, the RoPE cos / sin at the token's position (index clamped into the table past the rotary dims).
 template <int DH>
-__device__ void prep_vec(const GqaArgs& a, const uint16_t* src, const float* nw, int t, float* dst, int lane) {
+struct HeadIn {
+  float x[DH / 64], w[DH / 64], c[DH / 64], s[DH / 64];
+};
+
+__device__ float kZeros[DMAX];     // read in place of an absent table (norm weights, RoPE): the values go unused
+
+template <int DH>
+__device__ __forceinline__ void load_head(const GqaArgs& a, const uint16_t* src, const float* nw, int p, int lane,
+                                          HeadIn<DH>& in) {
+  // every load unconditional (a loaded value that meets a branch is waited for there): absent tables read zeros
+  const float* wp = a.qk_norm ? nw : kZeros;
+  const uint16_t* cp = a.rot > 0 ? a.cosb + (long long)p * a.rot : reinterpret_cast<const uint16_t*>(kZeros);
+  const uint16_t* sp = a.rot > 0 ? a.sinb + (long long)p * a.rot : reinterpret_cast<const uint16_t*>(kZeros);
+#pragma unroll
+  for (int u = 0; u < DH / 64; ++u) {
+    const int i = lane + 64 * u, ic = max(min(i, a.rot - 1), 0);
+    in.x[u] = bfv(src, i);
+    in.w[u] = wp[i];
+    in.c[u] = bfv(cp, ic);
+    in.s[u] = bfv(sp, ic);
+  }
+}
+
+// the vector after the optional (1+w) RMSNorm and partial RoPE, into dst[D] (BF16 values as f32); the whole wave
+// cooperates
+template <int DH>
+__device__ void prep_vec(const GqaArgs& a, const HeadIn<DH>& in, float* dst, int lane) {
   constexpr int U = DH / 64;
   float x[U];
 #pragma unroll
-  for (int u = 0; u < U; ++u) x[u] = bfv(src, lane + 64 * u);
+  for (int u = 0; u < U; ++u) x[u] = in.x[u];
   if (a.qk_norm) {
     float ss = 0.0f;
 #pragma unroll
     for (int u = 0; u < U; ++u) ss += x[u] * x[u];
     const float r = 1.0f / sqrtf(wave_sum(ss) / (float)DH + a.eps);
 #pragma unroll
-    for (int u = 0; u < U; ++u) x[u] = round_bf16((x[u] * r) * nw[lane + 64 * u]);
+    for (int u = 0; u < U; ++u) x[u] = round_bf16((x[u] * r) * in.w[u]);
   }
 #pragma unroll
   for (int u = 0; u < U; ++u) dst[lane + 64 * u] = x[u];
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   __builtin_amdgcn_wave_barrier();
   const int half = a.rot / 2;
-  const int p = min(cur_pos(a) + t, a.ctx - 1);     // a device position past the cache (a stopped program's queued
-                                                   // steps) must not read past the RoPE tables
   float o[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int i = lane + 64 * u;
     if (i < a.rot) {
-      const float c = bfv(a.cosb, (long long)p * a.rot + i), s = bfv(a.sinb, (long long)p * a.rot + i);
       const float rot = i < half ? -dst[i + half] : dst[i - half];
-      o[u] = round_bf16(round_bf16(x[u] * c) + round_bf16(rot * s));
+      o[u] = round_bf16(round_bf16(x[u] * in.c[u]) + round_bf16(rot * in.s[u]));
     } else {
       o[u] = x[u];
     }
@@ -171,9 +194,15 @@ __global__ __launch_bounds__(64) void gqa_prep(GqaArgs a) {
   if (stopped(a)) return;
   const int q_cols = a.gate ? 2 * DH : DH;
   const uint16_t* row = a.proj + (long long)t * a.ldp;
+  const int pos = cur_pos(a);
+  // a device position past the cache (a stopped program's queued steps) must not read past the RoPE tables
+  const int pr = min(pos + t, a.ctx - 1);
+  HeadIn<DH> in;
   if (x < a.heads) {
+    load_head<DH>(a, row + x * q_cols, a.q_norm, pr, lane, in);
+    __builtin_amdgcn_sched_barrier(0);
     const int j = x / a.rep, qrow = t * a.rep + (x - j * a.rep);
-    prep_vec<DH>(a, row + x * q_cols, a.q_norm, t, tmp, lane);
+    prep_vec<DH>(a, in, tmp, lane);
     uint16_t* dst = a.qf + ((long long)j * MAXROWS + qrow) * DH;
     if constexpr (BF) {                           // BF16 rows as they are (the BF16 MFMA takes them exactly)
 #pragma unroll
@@ -190,19 +219,25 @@ __global__ __launch_bounds__(64) void gqa_prep(GqaArgs a) {
       if (lane == 0) a.qsc[j * MAXROWS + qrow] = pow2f(p);
     }
   } else {
-    const int j = x - a.heads, p = cur_pos(a) + t;
+    const int j = x - a.heads, p = pos + t;
     if (p >= a.ctx) return;                       // past the cache (a device position the host cannot check)
+    // the key's inputs and the value row, all loaded before any is used
+    load_head<DH>(a, row + a.heads * q_cols + j * DH, a.k_norm, pr, lane, in);
+    const uint16_t* v = row + a.heads * q_cols + a.kv * DH + j * DH;
+    float vv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) vv[u] = bfv(v, lane + 64 * u);
+    __builtin_amdgcn_sched_barrier(0);
     constexpr int ES = BF ? 2 : 1;                // bytes per cache element
     char* kc = static_cast<char*>(a.kc);
     char* vc = static_cast<char*>(a.vc);
-    prep_vec<DH>(a, row + a.heads * q_cols + j * DH, a.k_norm, t, tmp, lane);
+    prep_vec<DH>(a, in, tmp, lane);
     store_row<DH, BF>(tmp, kc + ((long long)j * a.ctx + p) * DH * ES, 1, a.ks ? a.ks + (long long)j * a.ctx + p : nullptr,
                       lane);
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
-    const uint16_t* v = row + a.heads * q_cols + a.kv * DH + j * DH;
 #pragma unroll
-    for (int u = 0; u < U; ++u) tmp[lane + 64 * u] = bfv(v, lane + 64 * u);
+    for (int u = 0; u < U; ++u) tmp[lane + 64 * u] = vv[u];
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
     store_row<DH, BF>(tmp, vc + (((long long)j * a.ctx + (p & ~(BLOCK - 1))) * DH + vblock_pos(p & (BLOCK - 1))) * ES,
@@ -555,26 +590,64 @@ constexpr int MW = 8;
 template <int DH>
 __global__ __launch_bounds__(64 * MW) void gqa_merge(GqaArgs a) {
   constexpr int U = DH / 64;
+  constexpr int GB = 8;                                     // partials a wave holds at once (the one-pass form)
   __shared__ float red[MW][DH + 1];
-  const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __shared__ float mxs[MW];
+  const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (stopped(a)) return;
   const int j = h / a.rep;
   const int row = t * a.rep + (h - j * a.rep);
   const long long b0 = (long long)j * a.n_groups * a.rows + row;      // partial g at b0 + g·rows
-  float M = -INFINITY;
-  for (int g = lane; g < a.n_groups; g += 64) M = fmaxf(M, a.part_ml[(b0 + (long long)g * a.rows) * 2]);
-  M = wave_max(M);
-  float l = 0.0f, o[U];
+  // the gate first (an independent load; without a gate the row's first values are read and unused)
+  const uint16_t* gp = a.proj + (long long)t * a.ldp + (a.gate ? h * 2 * DH + DH : 0);
+  float gv[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) gv[u] = bfv(gp, lane + 64 * u);
+  float M = -INFINITY, l = 0.0f, o[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) o[u] = 0.0f;
-#pragma unroll 8
-  for (int g = w; g < a.n_groups; g += MW) {
-    const long long b = b0 + (long long)g * a.rows;
-    const float m = a.part_ml[b * 2], lg = a.part_ml[b * 2 + 1];
-    const float wgt = m == -INFINITY ? 0.0f : __expf(m - M);
-    l += wgt * lg;
+  if (a.n_groups <= MW * GB) {
+    // one pass: every partial of the wave (groups w, w + MW, …; past the last, the last again with weight 0) in
+    // flight at once, then the common max and the weighted sums in group order
+    float pm[GB], pl[GB], po[GB][U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) o[u] += wgt * a.part_o[b * DH + lane + 64 * u];
+    for (int i = 0; i < GB; ++i) {
+      const long long b = b0 + (long long)min(w + MW * i, a.n_groups - 1) * a.rows;
+      pm[i] = a.part_ml[b * 2];
+      pl[i] = a.part_ml[b * 2 + 1];
+#pragma unroll
+      for (int u = 0; u < U; ++u) po[i][u] = a.part_o[b * DH + lane + 64 * u];
+    }
+    __builtin_amdgcn_sched_barrier(0);                        // all of them issued before the first wait
+    float mw = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < GB; ++i)
+      if (w + MW * i < a.n_groups) mw = fmaxf(mw, pm[i]);
+    if (lane == 0) mxs[w] = mw;
+    __syncthreads();
+#pragma unroll
+    for (int ww = 0; ww < MW; ++ww) M = fmaxf(M, mxs[ww]);
+#pragma unroll
+    for (int i = 0; i < GB; ++i) {
+      if (w + MW * i >= a.n_groups) break;
+      const float wgt = pm[i] == -INFINITY ? 0.0f : __expf(pm[i] - M);
+      l += wgt * pl[i];
+#pragma unroll
+      for (int u = 0; u < U; ++u) o[u] += wgt * po[i][u];
+    }
+  } else {
+    for (int g = lane; g < a.n_groups; g += 64) M = fmaxf(M, a.part_ml[(b0 + (long long)g * a.rows) * 2]);
+    M = wave_max(M);
+#pragma unroll 8
+    for (int g = w; g < a.n_groups; g += MW) {
+      const long long b = b0 + (long long)g * a.rows;
+      const float m = a.part_ml[b * 2], lg = a.part_ml[b * 2 + 1];
+      const float wgt = m == -INFINITY ? 0.0f : __expf(m - M);
+      l += wgt * lg;
+#pragma unroll
+      for (int u = 0; u < U; ++u) o[u] += wgt * a.part_o[b * DH + lane + 64 * u];
+    }
   }
 #pragma unroll
   for (int u = 0; u < U; ++u) red[w][lane + 64 * u] = o[u];
@@ -593,10 +666,7 @@ __global__ __launch_bounds__(64 * MW) void gqa_merge(GqaArgs a) {
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     float y = round_bf16(o[u] / l);
-    if (a.gate) {
-      const uint16_t* gp = a.proj + (long long)t * a.ldp + h * 2 * DH + DH;
-      y = round_bf16(y * round_bf16(1.0f / (1.0f + __expf(-bfv(gp, lane + 64 * u)))));
-    }
+    if (a.gate) y = round_bf16(y * round_bf16(1.0f / (1.0f + __expf(-gv[u]))));
     a.y[(long long)t * a.ldy + h * DH + lane + 64 * u] = f32_to_bf16_bits(y);
   }
 }
