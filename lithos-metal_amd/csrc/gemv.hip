@@ -626,7 +626,7 @@ void gemv_rowp(Args a) {
   // chunk cc of the slice at a compile-time offset from chunk c0 (NVFP4: KW = 4 slices lie in one group of 8,
   // longer ones start on a group); chunks past a short slice are not loaded (their arithmetic is skipped)
   const long long c0_off = FMT == FMT_NVFP4 ? nv_code_off(c0) : (long long)c0 * unit_bytes(FMT);
-  auto issue = [&](Units<FMT> (&u)[KW], uint4 (&sv)[NG], int j) {
+  auto issue_scales = [&](uint4 (&sv)[NG], int j) {
     const uint8_t* tbase = wmat + (long long)tile_of(j) * a.tile_stride;
     if constexpr (FMT == FMT_NVFP4) {
 #pragma unroll
@@ -634,37 +634,35 @@ void gemv_rowp(Args a) {
         const int gi = min((c0 >> 3) + q, (a.chunks - 1) >> 3);
         const int gsz = nv_group_chunks(gi, a.chunks);
         const uint8_t* p = tbase + nv_scale_off(gi, a.chunks);
-        if (nv_piece(gsz) == 16) {
-          sv[q] = *reinterpret_cast<const uint4*>(p + 16 * lane);
-        } else {
-          const uint2 t = *reinterpret_cast<const uint2*>(p + 8 * lane);
-          sv[q] = uint4{t.x, t.y, 0u, 0u};
-        }
+        // a group of 8 chunks holds 16 scale bytes a lane, a shorter one 8 (then t1 repeats t0: such a group is
+        // one slice, starting on the group, whose chunks use sv.x / sv.y only); both loads unconditional, so no
+        // value waits for them at a branch
+        const bool wide = nv_piece(gsz) == 16;
+        const uint2 t0 = *reinterpret_cast<const uint2*>(p + (wide ? 16 : 8) * lane);
+        const uint2 t1 = *reinterpret_cast<const uint2*>(p + (wide ? 16 * lane + 8 : 8 * lane));
+        sv[q] = uint4{t0.x, t0.y, t1.x, t1.y};
       }
     }
-    const uint8_t* cb = tbase + c0_off;
-    auto one = [&](int cc) {
-      if constexpr (FMT == FMT_NVFP4) {
-        const int off = KW <= 4 ? cc * 1024 : (cc >> 3) * 9216 + (cc & 7) * 1024;
-        u[cc].q = *reinterpret_cast<const uint4*>(cb + off + 16 * lane);
-      } else {
-        const uint8_t* p = cb + cc * unit_bytes(FMT);
-        u[cc].q = *reinterpret_cast<const uint4*>(p + 16 * lane);
-        if constexpr (FMT == FMT_INT4) u[cc].sb = *reinterpret_cast<const uint2*>(p + 1024 + 8 * (lane & 15));
-      }
-    };
-    if (kwl == KW) {                          // the common case: straight-line loads
-#pragma unroll
-      for (int cc = 0; cc < KW; ++cc) one(cc);
+  };
+  // chunk cc of tile j into u[cc] (cc a compile-time index; a chunk past a short slice re-reads the slice's last
+  // one, never used: every load unconditional)
+  auto issue_chunk = [&](Units<FMT> (&u)[KW], int cc, int j) {
+    const int sc = min(cc, kwl - 1);
+    const uint8_t* cb = wmat + (long long)tile_of(j) * a.tile_stride + c0_off;
+    if constexpr (FMT == FMT_NVFP4) {
+      const int off = KW <= 4 ? sc * 1024 : (sc >> 3) * 9216 + (sc & 7) * 1024;
+      u[cc].q = *reinterpret_cast<const uint4*>(cb + off + 16 * lane);
     } else {
-#pragma unroll
-      for (int cc = 0; cc < KW; ++cc)
-        if (cc < kwl) one(cc);
+      const uint8_t* p = cb + sc * unit_bytes(FMT);
+      u[cc].q = *reinterpret_cast<const uint4*>(p + 16 * lane);
+      if constexpr (FMT == FMT_INT4) u[cc].sb = *reinterpret_cast<const uint2*>(p + 1024 + 8 * (lane & 15));
     }
   };
   Units<FMT> u0[KW];
-  uint4 s0[NG];
-  issue(u0, s0, 0);
+  uint4 s0[NG], s1[NG];
+  issue_scales(s0, 0);
+#pragma unroll
+  for (int cc = 0; cc < KW; ++cc) issue_chunk(u0, cc, 0);
 
   // ---- stage the slice (normalized when the norm is fused: Σh² over the row from every wave's slice) ----------
   uint8_t* wl = smem + (size_t)wave * a.row_wave_lds;
@@ -756,7 +754,9 @@ void gemv_rowp(Args a) {
 
   // ---- the slice's dot products, tile by tile --------------------------------------------------------------------
   const int g = lane >> 4, m_row = lane & 15;
-  auto tile_dot = [&](const Units<FMT> (&uu)[KW], const uint4 (&ss)[NG], int jt) {
+  // tile jt from uu / ss; as soon as chunk cc is consumed, chunk cc of tile jn (the next, or jt itself at the last)
+  // streams into its registers — a whole tile in flight with no second buffer
+  auto tile_dot = [&](Units<FMT> (&uu)[KW], const uint4 (&ss)[NG], int jt, int jn) {
     float acc[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
@@ -862,13 +862,10 @@ void gemv_rowp(Args a) {
           }
       }
     };
-    if (kw == KW) {
 #pragma unroll
-      for (int cc = 0; cc < KW; ++cc) slice_chunk(cc);
-    } else {
-#pragma unroll
-      for (int cc = 0; cc < KW; ++cc)
-        if (cc < kw) slice_chunk(cc);
+    for (int cc = 0; cc < KW; ++cc) {
+      if (cc < kw) slice_chunk(cc);
+      issue_chunk(uu, cc, jn);
     }
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
@@ -876,10 +873,15 @@ void gemv_rowp(Args a) {
       if (g == 0) red[((jt * S + wave) * MT + t) * 16 + m_row] = v;
     }
   };
-  for (int j = 0; j < ntl; ++j) {
-    tile_dot(u0, s0, j);
-    if (j + 1 < ntl) issue(u0, s0, j + 1);
+  // tiles in pairs, the scale pieces alternating between s0 and s1 (each loaded before the next tile's chunks)
+  int j = 0;
+  for (; j + 1 < ntl; j += 2) {
+    issue_scales(s1, j + 1);
+    tile_dot(u0, s0, j, j + 1);
+    issue_scales(s0, min(j + 2, ntl - 1));
+    tile_dot(u0, s1, j + 1, min(j + 2, ntl - 1));
   }
+  if (j < ntl) tile_dot(u0, s0, j, j);
 
   // ---- per tile: the K slices in wave order, then the epilogue (16-lane groups hold one tile's rows) -----------
   __syncthreads();
