@@ -41,6 +41,8 @@ __global__ __launch_bounds__(64 * MAX_T) void moe_route(RouteArgs a) {
   const int E = a.n_experts, k = a.top_k;
   const int ks = k + (a.shared_expert > 0 ? 1 : 0);   // slots per token (the shared expert last)
   if (t < a.t) {                                    // wave-uniform
+    // the shared expert's gate logit first: its load is then in flight with the router row's
+    const uint16_t gq = a.logits[(long long)t * a.ld_logits + max(a.shared_gate_col, 0)];
     int ce[MAX_K];
     float cw[MAX_K];
     route_topk(a.logits + (long long)t * a.ld_logits, E, k, a.renorm, lane, ce, cw);
@@ -54,8 +56,7 @@ __global__ __launch_bounds__(64 * MAX_T) void moe_route(RouteArgs a) {
     if (a.shared_expert > 0) {                      // the shared expert: weight bf16(σ(its gate's logit))
       if (lane == 0) {
         a.ids[t * ks + k] = a.shared_expert;
-        a.weights[t * ks + k] =
-            route_shared_weight(bf16_bits_to_f32(a.logits[(long long)t * a.ld_logits + a.shared_gate_col]));
+        a.weights[t * ks + k] = route_shared_weight(bf16_bits_to_f32(gq));
       }
       sel[t * ks + k] = a.shared_expert;
     }

@@ -14,11 +14,16 @@ constexpr int ROUTE_MAX_K = 16;
 __device__ __forceinline__ void route_topk(const uint16_t* logits, int E, int k, int renorm, int lane, int* ce,
                                            float* cw) {
   float v[ROUTE_MAX_PER_LANE];
+  uint16_t raw[ROUTE_MAX_PER_LANE];
+  // every load unconditional (an index past the experts re-reads the last logit, then masked), so they are all in
+  // flight at once: a load whose value meets a branch is waited for there, one round trip each
+#pragma unroll
+  for (int i = 0; i < ROUTE_MAX_PER_LANE; ++i) raw[i] = logits[min(lane + 64 * i, E - 1)];
   float m = -INFINITY;
 #pragma unroll
   for (int i = 0; i < ROUTE_MAX_PER_LANE; ++i) {
     const int e = lane + 64 * i;
-    v[i] = e < E ? bf16_bits_to_f32(logits[e]) : -INFINITY;
+    v[i] = e < E ? bf16_bits_to_f32(raw[i]) : -INFINITY;
     m = fmaxf(m, v[i]);
   }
   m = wave_max(m);
