@@ -148,10 +148,18 @@ __device__ __forceinline__ int epilogue_of(const Args& a, int expert) {
   return a.shared_expert > 0 && expert == a.shared_expert ? a.shared_epilogue : a.epilogue;
 }
 
+__device__ __forceinline__ void emit_row(const Args& a, int epi, int yr, int cnt, int tile, bool tile_ok, int m_row,
+                                         int t, float v, float up);
 __device__ __forceinline__ void emit(const Args& a, int epi, const int32_t* pairs, int cnt, int tile, bool tile_ok,
                                      int m_row, int t, float v, float up) {
   if (!tile_ok || t >= cnt) return;
-  const int yr = pairs ? pairs[t] : t;
+  emit_row(a, epi, pairs ? pairs[t] : t, cnt, tile, tile_ok, m_row, t, v, up);
+}
+
+// the same with token t's output row yr given
+__device__ __forceinline__ void emit_row(const Args& a, int epi, int yr, int cnt, int tile, bool tile_ok, int m_row,
+                                         int t, float v, float up) {
+  if (!tile_ok || t >= cnt) return;
   if (epi == MI_EPI_SILU_MUL || epi == MI_EPI_SILU_MUL_ROUNDED) {
     const int col = tile * 8 + m_row;
     if (m_row >= 8 || col >= a.n / 2) return;
@@ -1260,6 +1268,14 @@ __global__ __launch_bounds__(512) void gemv_tk(Args a) {
 
   // ---- stage the split's activations: wave j stages token rows j, j + S, … -------------------------------------
   if (threadIdx.x < 16) reinterpret_cast<uint32_t*>(const_cast<uint8_t*>(zero))[threadIdx.x] = 0u;
+  // the epilogue's inputs staged once, behind the ring's first units: the row scales of the workgroup's tiles and
+  // the group's pair ids — a global load inside the stream would wait for every unit of the ring issued before it
+  float* rs_s = reinterpret_cast<float*>(const_cast<uint8_t*>(zero) + 64);   // [tb·16]
+  int* pairs_s = reinterpret_cast<int*>(rs_s + a.tb * 16);                   // [16]
+  const int n_pad = a.n_tiles * 16;
+  for (int i = threadIdx.x; i < ntl * 16; i += blockDim.x)
+    rs_s[i] = a.row_scale != nullptr ? a.row_scale[(long long)expert * n_pad + tile0 * 16 + i] : 1.0f;
+  if (pairs && (int)threadIdx.x < cnt) pairs_s[threadIdx.x] = pairs[threadIdx.x];
   for (int j = wave; j < xrows; j += S) {
     const uint16_t* src = a.x + xrow_of(j) * a.ldx + kb * KC;
     uint16_t* dst = xs + (size_t)j * ld;
@@ -1528,10 +1544,9 @@ __global__ __launch_bounds__(512) void gemv_tk(Args a) {
   };
 
   // a finished tile: scale, then the epilogue (one split) or the FP32 partial (several)
-  const int n_pad = a.n_tiles * 16;
   auto finish = [&](int tile) {
     const int row = tile * 16 + m_row;
-    const float rs = a.row_scale != nullptr ? a.row_scale[(long long)expert * n_pad + row] : 1.0f;
+    const float rs = rs_s[(tile - tile0) * 16 + m_row];
     if constexpr (MF) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -1540,7 +1555,7 @@ __global__ __launch_bounds__(512) void gemv_tk(Args a) {
         if (a.ks == 1) {
           const float vs = v * rs;
           const float up = __shfl_down(vs, 8, 16);
-          emit(a, epilogue_of(a, expert), pairs, cnt, tile, true, m_row, t, vs, up);
+          if (t < cnt) emit_row(a, epilogue_of(a, expert), pairs ? pairs_s[t] : t, cnt, tile, true, m_row, t, vs, up);
         } else if (t < cnt) {
           a.part[((long long)split * a.m + t) * n_pad + row] = v;
         }
@@ -1553,7 +1568,8 @@ __global__ __launch_bounds__(512) void gemv_tk(Args a) {
         if (a.ks == 1) {
           const float vs = v * rs;
           const float up = __shfl_down(vs, 8, 16);
-          if (g == 0) emit(a, epilogue_of(a, expert), pairs, cnt, tile, true, m_row, t, vs, up);
+          if (g == 0 && t < cnt)
+            emit_row(a, epilogue_of(a, expert), pairs ? pairs_s[t] : t, cnt, tile, true, m_row, t, vs, up);
         } else if (g == 0 && t < cnt) {
           a.part[((long long)split * a.m + t) * n_pad + row] = v;
         }
@@ -1880,8 +1896,9 @@ Plan plan_tk(const mi_gemv_desc* d, int fmt, int chunks, int n_tiles, int groups
           // INT4 on the matrix path: a deeper ring costs more in occupancy than it adds in flight (27B gate|up at
           // M = 8: D = 4 32.5 µs, D = 8 35.0 µs, the D = 12 plan the model preferred 52.7 µs)
           if (fmt == FMT_INT4 && mf && D != 4) continue;
+          const int lds_t = lds + tb * 16 * 4 + 64;   // + the staged row scales and pair ids
           const double wgs = (double)((n_tiles + tb - 1) / tb) * ks * groups;
-          const int per_cu_lds = std::max(1, (int)(kMaxLds / lds));
+          const int per_cu_lds = std::max(1, (int)(kMaxLds / lds_t));
           const int per_cu = std::min(per_cu_lds, 32 / S);
           const double resident_waves = std::min(wgs, 256.0 * per_cu) * S / 256.0;
           const double inflight = resident_waves * D * ub;
@@ -1898,7 +1915,7 @@ Plan plan_tk(const mi_gemv_desc* d, int fmt, int chunks, int n_tiles, int groups
           if (cost < best_cost) {
             best_cost = cost;
             best.kernel = 2; best.S = S; best.kw = kc; best.tb = tb; best.ks = ks; best.depth = D;
-            best.lds_rows = lrows; best.lds_bytes = lds;
+            best.lds_rows = lrows; best.lds_bytes = lds_t;
           }
         }
       }
