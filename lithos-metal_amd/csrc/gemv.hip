@@ -182,6 +182,17 @@ __device__ __forceinline__ void emit_row(const Args& a, int epi, int yr, int cnt
 
 
 // ---- one chunk of one tile in registers ---------------------------------------------------------------------
+// 16 bytes of streamed weights: read once per launch, so loaded non-temporally (they need not stay in the caches)
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_stream(const uint8_t* p) {
+#ifdef MI_WEIGHTS_TEMPORAL
+  return *reinterpret_cast<const uint4*>(p);
+#else
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return uint4{v.x, v.y, v.z, v.w};
+#endif
+}
+
 template <int FMT>
 struct Units {
   uint4 q;                   // lane l: 16 bytes of codes (NVFP4 / INT4) or 8 BF16 values
@@ -193,7 +204,7 @@ struct Units {
 template <int FMT, bool SCALE>
 __device__ __forceinline__ void load_chunk(Units<FMT>& u, const uint8_t* tb, int c, int chunks, int lane) {
   if constexpr (FMT == FMT_NVFP4) {
-    u.q = *reinterpret_cast<const uint4*>(tb + nv_code_off(c) + 16 * lane);
+    u.q = ld_stream(tb + nv_code_off(c) + 16 * lane);
     if constexpr (SCALE) {
       const int gi = c >> 3;
       u.s = *reinterpret_cast<const uint16_t*>(tb + nv_scale_off(gi, chunks) + nv_piece(nv_group_chunks(gi, chunks)) * lane +
@@ -201,7 +212,7 @@ __device__ __forceinline__ void load_chunk(Units<FMT>& u, const uint8_t* tb, int
     }
   } else {
     const uint8_t* p = tb + (long long)c * unit_bytes(FMT);
-    u.q = *reinterpret_cast<const uint4*>(p + 16 * lane);
+    u.q = ld_stream(p + 16 * lane);
     if constexpr (FMT == FMT_INT4) u.sb = *reinterpret_cast<const uint2*>(p + 1024 + 8 * (lane & 15));
   }
 }
@@ -659,10 +670,10 @@ void gemv_rowp(Args a) {
     const uint8_t* cb = wmat + (long long)tile_of(j) * a.tile_stride + c0_off;
     if constexpr (FMT == FMT_NVFP4) {
       const int off = KW <= 4 ? sc * 1024 : (sc >> 3) * 9216 + (sc & 7) * 1024;
-      u[cc].q = *reinterpret_cast<const uint4*>(cb + off + 16 * lane);
+      u[cc].q = ld_stream(cb + off + 16 * lane);
     } else {
       const uint8_t* p = cb + sc * unit_bytes(FMT);
-      u[cc].q = *reinterpret_cast<const uint4*>(p + 16 * lane);
+      u[cc].q = ld_stream(p + 16 * lane);
       if constexpr (FMT == FMT_INT4) u[cc].sb = *reinterpret_cast<const uint2*>(p + 1024 + 8 * (lane & 15));
     }
   };
@@ -977,7 +988,7 @@ __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
 #pragma unroll
     for (int cc = 0; cc < KW; ++cc) {           // 1 KiB of codes per chunk
       const long long off = c0_off + (cc < kw ? cc : 0) * UB;
-      u[cc] = *reinterpret_cast<const uint4*>(tbase + off + 16 * lane);
+      u[cc] = ld_stream(tbase + off + 16 * lane);
       if constexpr (I4) sb[cc] = *reinterpret_cast<const uint2*>(tbase + off + 1024 + 8 * (lane & 15));
     }
     __builtin_amdgcn_sched_barrier(0);          // the tile's loads stay where they are in the issue order
