@@ -1708,6 +1708,7 @@ struct Plan {
   int rt = 1, G = 0;       // gemv_row: tiles per workgroup (at most), workgroups along the tiles
   int lds_rows = 1, row_ld = 0, row_wave_lds = 0;
   size_t lds_bytes = 0;
+  bool prenorm = false;    // the input norm as its own norm_apply launch into the workspace, then the plain GEMV
 };
 
 int check_desc(const mi_gemv_desc* d) {
@@ -1996,7 +1997,48 @@ Plan plan_rowm(const mi_gemv_desc* d, int chunks, int n_tiles) {
   return best;
 }
 
+Plan make_plan_fused(const mi_gemv_desc* d);
+
+// split-K workspace: a fixed region of per-tile arrival counters (the same for every shape, so partials of one call
+// never land on the counters of another), then the FP32 partials [ks][m][n_tiles·16], then (prenorm) the
+// normalized input rows [m][k] BF16
+constexpr int kFoldTiles = 16384;
+constexpr size_t kFoldCounterBytes = kFoldTiles * sizeof(uint32_t);
+size_t fold_counter_bytes(int) { return kFoldCounterBytes; }
+
+// At M >= 3 the input RMSNorm runs as its own norm_apply launch (one workgroup per token) into the workspace, and the
+// GEMV reads the normalized rows: inside gemv_rowm / gemv_tk every workgroup would normalize the whole [M, K] input
+// again (per element: two multiplies and a BF16 rounding, on operand lanes of which half are padding rows at M = 8)
+// behind a workgroup barrier. Measured on the 27B shapes at M = 8, bit-identical: gate|up 33.0 → 30.5 µs, in_proj
+// 24.7 → 22.0 µs (the extra launch ≈ 2.9 µs). At M <= 2 gemv_row's fused norm costs less than a launch.
+bool wants_prenorm(const mi_gemv_desc* d) {
+  static const bool off = getenv("MI_GEMV_PRENORM") && getenv("MI_GEMV_PRENORM")[0] == '0';   // A/B comparisons
+  const int rows = d->groups ? std::min(16, d->m) : d->m;
+  return !off && d->norm_w && rows > 2 && !(d->groups && d->x_per_slot) && !d->route_logits && d->k % 8 == 0;
+}
+
 Plan make_plan(const mi_gemv_desc* d) {
+  if (!wants_prenorm(d)) return make_plan_fused(d);
+  mi_gemv_desc plain = *d;
+  plain.norm_w = nullptr;
+  Plan p = make_plan_fused(&plain);
+  p.prenorm = p.kernel != 0;
+  return p;
+}
+
+// the normalized rows' place in the workspace (after the split-K counters and partials), and the bytes in all
+size_t split_bytes(const mi_gemv_desc* d, const Plan& p) {
+  return p.ks > 1 ? fold_counter_bytes(d->n) + (size_t)p.ks * d->m * ((d->n + 15) / 16) * 16 * sizeof(float) : 0;
+}
+// (past the counters also without a split: a workspace is shared between calls, and the counters must stay zero)
+size_t prenorm_offset(const mi_gemv_desc* d, const Plan& p) {
+  return (std::max(split_bytes(d, p), fold_counter_bytes(d->n)) + 255) / 256 * 256;
+}
+size_t workspace_need(const mi_gemv_desc* d, const Plan& p) {
+  return p.prenorm ? prenorm_offset(d, p) + (size_t)d->m * d->k * sizeof(uint16_t) : split_bytes(d, p);
+}
+
+Plan make_plan_fused(const mi_gemv_desc* d) {
   const int fmt = d->format;
   const int chunks = d->k / chunk_cols(fmt);
   const int n_tiles = (d->n + 15) / 16;
@@ -2089,12 +2131,6 @@ void launch(const Args& a, const Plan& p, int groups, hipStream_t s) {
   }
 }
 
-// split-K workspace: a fixed region of per-tile arrival counters (the same for every shape, so partials of one call
-// never land on the counters of another), then the FP32 partials [ks][m][n_tiles·16]
-constexpr int kFoldTiles = 16384;
-constexpr size_t kFoldCounterBytes = kFoldTiles * sizeof(uint32_t);
-size_t fold_counter_bytes(int) { return kFoldCounterBytes; }
-
 }  // namespace
 
 extern "C" {
@@ -2109,8 +2145,7 @@ size_t mi_pack_bytes(int32_t format, int32_t n, int32_t k) {
 
 size_t mi_gemv_workspace_bytes(const mi_gemv_desc* d) {
   if (check_desc(d) != MI_OK) return 0;
-  const Plan p = make_plan(d);
-  return p.ks > 1 ? fold_counter_bytes(d->n) + (size_t)p.ks * d->m * ((d->n + 15) / 16) * 16 * sizeof(float) : 0;
+  return workspace_need(d, make_plan(d));
 }
 
 int mi_gemv_plan(const mi_gemv_desc* d, int32_t out[7]) {
@@ -2177,18 +2212,31 @@ int gemv_impl(const mi_gemv_desc* d, void* stream, void* fixed_ws, size_t fixed_
   a.kc = p.kernel == 1 ? p.tb : p.kw;     // chunks per K split
   a.row_ld = p.row_ld;
   a.row_wave_lds = p.row_wave_lds;
-  if (p.ks > 1) {
-    const size_t cb = fold_counter_bytes(d->n);
-    const size_t need = cb + (size_t)p.ks * d->m * ((d->n + 15) / 16) * 16 * sizeof(float);
-    void* ws = fixed_ws ? fixed_ws : d->workspace;
+  const size_t need = workspace_need(d, p);
+  void* ws = nullptr;
+  if (need) {
+    ws = fixed_ws ? fixed_ws : d->workspace;
     if (fixed_ws) {
-      MI_REQUIRE(need <= fixed_bytes, "%s: this shape needs %zu B of split-K scratch, more than the %zu B the "
+      MI_REQUIRE(need <= fixed_bytes, "%s: this shape needs %zu B of scratch, more than the %zu B the "
                  "no-allocation entry point holds (use mi_gemv with a workspace)", name, need, fixed_bytes);
     } else if (ws) {
       MI_REQUIRE(d->workspace_bytes >= need, "%s: workspace %zu B < %zu B", name, d->workspace_bytes, need);
     } else if (int rc = mi_library_scratch(MI_SCRATCH_GEMV, need, static_cast<hipStream_t>(stream), &ws)) {
       return rc;
     }
+  }
+  if (p.prenorm) {                              // x → bf16(RMSNorm(x)·w) rows in the workspace; the GEMV reads them
+    uint16_t* xn = reinterpret_cast<uint16_t*>(static_cast<char*>(ws) + prenorm_offset(d, p));
+    mi_norm_desc nd{};
+    nd.t = d->m; nd.k = d->k; nd.h = d->x; nd.ldh = d->ldx; nd.stat = nullptr; nd.stat_parts = 1;
+    nd.w = d->norm_w; nd.x = xn; nd.ldx = d->k; nd.eps = d->eps;
+    if (int rc = mi_norm_apply(&nd, stream)) return rc;
+    a.x = xn;
+    a.ldx = d->k;
+    a.norm_w = nullptr;
+  }
+  if (p.ks > 1) {
+    const size_t cb = fold_counter_bytes(d->n);
     a.part = reinterpret_cast<float*>(static_cast<char*>(ws) + cb);
     // gemv_row folds its splits in the kernel (MI_GEMV_FOLD=0: the separate reduction launch, for comparisons)
     static const bool fold = !(getenv("MI_GEMV_FOLD") && getenv("MI_GEMV_FOLD")[0] == '0');

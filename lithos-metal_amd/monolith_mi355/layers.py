@@ -358,6 +358,7 @@ class MoeBlock:
         else:
             self.gate_up, self.down = stack(self.gate_up_q), stack(self.down_q)
         self._bufs: Dict[int, tuple] = {}
+        self._xn: Dict[int, object] = {}
         # the shared expert runs on a second stream beside the router → experts chain (default priority), with its
         # own zeroed split-K workspace so the two branches never share partials or fold counters
         self.side = torch.cuda.Stream(device=device)
@@ -381,6 +382,11 @@ class MoeBlock:
                              torch.empty(m, self.hidden, dtype=bf, device=dev))
         return self._bufs[m]
 
+    def _normed(self, m: int):
+        if m not in self._xn:
+            self._xn[m] = _torch().empty(m, self.hidden, dtype=_torch().bfloat16, device=self.norm_w.device)
+        return self._xn[m]
+
     def __call__(self, h, act=None, out=None):
         """``h [M, hidden]`` bf16 → the block's output with the residual added (M ≤ 16). ``act`` is accepted so the
         block can stand in for a decoder layer's dense MLP (it keeps its own intermediates)."""
@@ -390,15 +396,20 @@ class MoeBlock:
         torch = _torch()
         e, k = self.experts, self.top_k
         if self.fused_shared:
-            kernels.gemv(self.router_gate, h, norm_w=self.norm_w, eps=self.eps, out=logits[:, :e + 1])
+            # M >= 3: the input norm once, for the router and the experts (inside each GEMV every workgroup would
+            # normalize the whole [M, K] input again); M <= 2: fused into both GEMVs' loads
+            x, nw = h, self.norm_w
+            if m > 2:
+                x, nw = kernels.norm_apply(h, self.norm_w, eps=self.eps, out=self._normed(m)), None
+            kernels.gemv(self.router_gate, x, norm_w=nw, eps=self.eps, out=logits[:, :e + 1])
             ids, wts, groups = route
             if m == 1:                  # one token: the expert gate|up launch routes for itself (one launch fewer)
                 inline = dict(logits=logits[:, :e], ids=ids, weights=wts, top_k=k, renorm=True, gate_col=e)
             else:
                 kernels.moe_route(logits[:, :e], k, renorm=True, out=route, shared_expert=e, shared_gate=e)
                 inline = None
-            kernels.moe_gemv(self.gate_up_s, h, groups, tokens=m, top_k=k + 1, x_per_slot=False,
-                             epilogue="silu_mul_rounded", norm_w=self.norm_w, eps=self.eps, out=act,
+            kernels.moe_gemv(self.gate_up_s, x, groups, tokens=m, top_k=k + 1, x_per_slot=False,
+                             epilogue="silu_mul_rounded", norm_w=nw, eps=self.eps, out=act,
                              shared_expert=e, shared_epilogue="silu_mul", route=inline)
             kernels.moe_gemv(self.down_s, act, groups, tokens=m, top_k=k + 1, x_per_slot=True, out=hk)
             return kernels.moe_combine(hk, wts, top_k=k + 1, residual=h, out=out)
