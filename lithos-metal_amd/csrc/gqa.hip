@@ -17,8 +17,9 @@
 //  * gqa_prep: one wave per (head or KV head, token), all in parallel: q rows normed, roped and (int8 cache)
 //    prescaled by a power of two into F16 — the MFMA B operand, in the workspace; k/v quantized (or stored as BF16)
 //    and appended to the cache.
-//  * gqa_decode: a workgroup of 4 waves per (KV head, key range); each wave streams its share of the range in
-//    chunks with the next chunk's K side prefetched into registers. The rep·T query rows of the KV head are A
+//  * gqa_decode: a workgroup of 4 waves per (KV head, key range) — 8 at head dim 128 with one row tile on a long
+//    cache (one chunk per wave, two waves per SIMD); each wave streams its share of the range in chunks with the next
+//    chunk's K side prefetched into registers (4 waves). The rep·T query rows of the KV head are A
 //    tiles of v_mfma_f32_16x16x32_f16; int8 codes become exact F16 with an XOR / byte-permute / packed subtract;
 //    QKᵀ and P·V run on MFMA, the softmax online; the V scale folds into P (with a per-chunk power of two so it
 //    stays in F16 range). The BF16 cache feeds v_mfma_f32_16x16x32_bf16 as it is (q, P and the cache are all
@@ -169,7 +170,7 @@ __device__ void store_row(const float* src, void* dst, long long stride, uint16_
 }
 
 constexpr int MAXROWS = 64;     // query rows per KV head (rep·T)
-constexpr int NW = 4;           // waves per decode workgroup
+constexpr int kNW = 4;          // waves per decode workgroup (head dim 256; 128: gqa_waves())
 
 __device__ __forceinline__ float pow2f(int e) { return __uint_as_float((uint32_t)(127 + e) << 23); }
 
@@ -322,7 +323,7 @@ __device__ __forceinline__ float f16_hi(uint32_t u) { return (float)__builtin_bi
 // lane owns one query row (row = 16·rt + m16): Sᵀ = K·Qᵀ (A = the K tile, B = the query rows), softmax over the
 // lane's keys plus the lanes l ^ 16, l ^ 32, l ^ 48 of the same row, and Oᵀ += Vᵀ·Pᵀ with Pᵀ straight from the score
 // registers (no LDS round trip) — every per-row quantity is lane-local.
-template <int RT, int DH, bool BF>
+template <int RT, int DH, bool BF, int NW>
 __global__ __launch_bounds__(64 * NW, 1) void gqa_decode(GqaArgs a) {
   using G = Geo<DH, BF>;
   using OpT = typename std::conditional<BF, bf16x8, f16x8>::type;
@@ -370,7 +371,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gqa_decode(GqaArgs a) {
   // Every load is issued whether or not its chunk exists (a chunk past the wave's range re-reads the last one in
   // range, or the range's start when it is empty — chunks lie inside the cache: ctx % 64 == 0), after the query
   // rows, so the in-order memory counter lets a chunk's wait leave the other chunk's loads outstanding.
-  constexpr bool VA = DH == 128 && (RT <= 2 || (RT == 3 && BF));   // two chunks: at most 48 loads in flight
+  constexpr bool VA = NW == 4 && DH == 128 && (RT <= 2 || (RT == 3 && BF));   // two chunks: at most 48 loads in flight
   Chunk<DH, BF> ca, cb;
   const int k_last = k_begin < k_end ? k_begin + ((k_end - 1 - k_begin) / CH) * CH : min(k_begin, a.ctx - CH);
   auto load_chunk = [&](Chunk<DH, BF>& c, int k0) {
@@ -675,14 +676,21 @@ __global__ __launch_bounds__(64 * MW) void gqa_merge(GqaArgs a) {
 // chosen for about 1024 waves over the cache — one workgroup per CU, each wave streaming its chunks with one in
 // flight.
 struct Plan { int n_groups, group_len; };
-Plan plan(int pos, int kv, int rows) {
+// Waves per decode workgroup: 8 at head dim 128 with one row tile when the 4-wave plan would give each wave two or
+// more chunks (32K: one chunk each, two waves per SIMD, the same key ranges and partials): 32K M = 1 22.5 → 20.0 µs.
+// Where 4 waves hold one chunk each (4K, 16K), 8 would only halve the workgroups (4K 16.4 → 17.2 µs). More row tiles
+// spill at two waves per SIMD. MI_GQA_NW=4 pins 4 (comparisons).
+int gqa_waves(int d, int rows, int pos, int kv) {
+  const char* e = getenv("MI_GQA_NW");
+  if (d != 128 || rows > 16 || (e && atoi(e) == 4)) return kNW;
+  return (long long)pos * kv > 256LL * kNW * BLOCK ? 8 : kNW;     // the 4-wave plan: two chunks or more per wave
+}
+Plan plan(int pos, int kv, int rows, int nw) {
   (void)rows;
-  static const long long waves_target = [] {            // MI_GQA_WAVES: tuning override
-    const char* e = getenv("MI_GQA_WAVES");
-    return e ? std::max(64LL, atoll(e)) : 1024LL;
-  }();
+  const char* e = getenv("MI_GQA_WAVES");             // MI_GQA_WAVES: tuning override
+  const long long waves_target = e ? std::max(64LL, atoll(e)) : 256LL * nw;
   const int cw = (int)std::max<long long>(1, ((long long)pos * kv + waves_target * BLOCK - 1) / (waves_target * BLOCK));
-  const int len = NW * cw * BLOCK;
+  const int len = nw * cw * BLOCK;
   return {std::max(1, (pos + len - 1) / len), len};
 }
 
@@ -700,18 +708,20 @@ Layout layout(int kv, int n_groups, int rows, int d) {
 }
 
 template <int DH, bool BF>
-int launch(const GqaArgs& a, int rows, hipStream_t s) {
+int launch(const GqaArgs& a, int rows, int nw, hipStream_t s) {
   hipLaunchKernelGGL((gqa_prep<DH, BF>), dim3(a.heads + a.kv, a.t), dim3(64), 0, s, a);
   MI_TRY_HIP(hipGetLastError(), "gqa_prep launch");
-  const dim3 grid(a.n_groups, a.kv), block(64 * NW);
+  const dim3 grid(a.n_groups, a.kv), block(64 * nw);
   const int rt = (rows + 15) / 16;
   if constexpr (DH == 256) {     // one row tile per workgroup (grid z): more tiles' accumulators would spill
-    hipLaunchKernelGGL((gqa_decode<1, DH, BF>), dim3(a.n_groups, a.kv, rt), block, 0, s, a);
+    hipLaunchKernelGGL((gqa_decode<1, DH, BF, kNW>), dim3(a.n_groups, a.kv, rt), block, 0, s, a);
+  } else if (nw == 8) {          // one row tile (gqa_waves): more tiles' accumulators would spill at 2 waves / SIMD
+    hipLaunchKernelGGL((gqa_decode<1, DH, BF, 8>), grid, block, 0, s, a);
   } else {
-    if (rt == 1) hipLaunchKernelGGL((gqa_decode<1, DH, BF>), grid, block, 0, s, a);
-    else if (rt == 2) hipLaunchKernelGGL((gqa_decode<2, DH, BF>), grid, block, 0, s, a);
-    else if (rt == 3) hipLaunchKernelGGL((gqa_decode<3, DH, BF>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((gqa_decode<4, DH, BF>), grid, block, 0, s, a);
+    if (rt == 1) hipLaunchKernelGGL((gqa_decode<1, DH, BF, kNW>), grid, block, 0, s, a);
+    else if (rt == 2) hipLaunchKernelGGL((gqa_decode<2, DH, BF, kNW>), grid, block, 0, s, a);
+    else if (rt == 3) hipLaunchKernelGGL((gqa_decode<3, DH, BF, kNW>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((gqa_decode<4, DH, BF, kNW>), grid, block, 0, s, a);
   }
   MI_TRY_HIP(hipGetLastError(), "gqa_decode launch");
   hipLaunchKernelGGL((gqa_merge<DH>), dim3(a.heads, a.t), dim3(64 * MW), 0, s, a);
@@ -728,7 +738,7 @@ int plan_pos(const mi_gqa_desc* d) { return d->pos_dev ? std::max(0, d->ctx_max 
 extern "C" size_t mi_gqa_workspace_bytes(const mi_gqa_desc* d) {
   if (!d || d->t < 1 || d->kv_heads < 1 || d->heads % d->kv_heads || d->head_dim < 1 || d->head_dim > DMAX) return 0;
   const int rows = d->heads / d->kv_heads * d->t;
-  return layout(d->kv_heads, plan(plan_pos(d), d->kv_heads, rows).n_groups, rows, d->head_dim).total;
+  return layout(d->kv_heads, plan(plan_pos(d), d->kv_heads, rows, gqa_waves(d->head_dim, rows, plan_pos(d), d->kv_heads)).n_groups, rows, d->head_dim).total;
 }
 
 extern "C" int mi_gqa_decode(const mi_gqa_desc* d, void* stream) {
@@ -755,7 +765,8 @@ extern "C" int mi_gqa_decode(const mi_gqa_desc* d, void* stream) {
   GqaArgs a{};
   a.t = d->t; a.heads = d->heads; a.kv = d->kv_heads; a.d = d->head_dim; a.rot = d->rotary_dim; a.pos = d->pos;
   a.ctx = d->ctx_max; a.gate = d->gate; a.qk_norm = d->qk_norm; a.rep = rep; a.rows = rows;
-  const Plan pl = plan(plan_pos(d), d->kv_heads, rows);
+  const int nw = gqa_waves(d->head_dim, rows, plan_pos(d), d->kv_heads);
+  const Plan pl = plan(plan_pos(d), d->kv_heads, rows, nw);
   a.pos_dev = d->pos_dev;
   a.done = d->done;
   a.n_groups = pl.n_groups;
@@ -780,6 +791,6 @@ extern "C" int mi_gqa_decode(const mi_gqa_desc* d, void* stream) {
   a.part_o = reinterpret_cast<float*>(wb + L.part_o);
   a.part_ml = reinterpret_cast<float*>(wb + L.part_ml);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (d->head_dim == 128) return bf ? launch<128, true>(a, rows, s) : launch<128, false>(a, rows, s);
-  return bf ? launch<256, true>(a, rows, s) : launch<256, false>(a, rows, s);
+  if (d->head_dim == 128) return bf ? launch<128, true>(a, rows, nw, s) : launch<128, false>(a, rows, nw, s);
+  return bf ? launch<256, true>(a, rows, nw, s) : launch<256, false>(a, rows, nw, s);
 }
