@@ -1813,10 +1813,10 @@ int row_blocks_per_cu(int fmt, int kw, int threads, size_t lds) {
 // more loads in flight). One K split, except long K over few tiles (N = 5120, K = 17408: 320 workgroups leave a
 // quarter of the CUs a second round) where three splits with FP32 partials measured ~10 % faster; a fused norm or
 // a grouped (MoE) launch always takes one split.
-Plan plan_row(const mi_gemv_desc* d, int fmt, int chunks, int rows, int n_tiles, int groups) {
+Plan plan_row(const mi_gemv_desc* d, int fmt, int chunks, int rows, int n_tiles, int groups, int kw_pref = 0) {
   Plan best{};
   double best_cost = 1e30;
-  int force_ks = 0, force_kw = 0, force_rt = 0;
+  int force_ks = 0, force_kw = kw_pref, force_rt = 0;
   if (const char* env = getenv("MI_GEMV_ROW"))                                   // tuning sweeps
     sscanf(env, "%d,%d,%d", &force_kw, &force_ks, &force_rt);
   for (int ks : {1, 3, 2, 4}) {
@@ -2048,6 +2048,18 @@ Plan make_plan_fused(const mi_gemv_desc* d) {
   const bool pin_tk = fk && fk[0] == 't', pin_rowm = fk && strcmp(fk, "rowm") == 0;
   if (rows <= 2 && !pin_tk) {
     const Plan p = plan_row(d, fmt, chunks, rows, n_tiles, groups);
+    // A fused-norm tile per workgroup whose 4-chunk waves leave a second, partial round of workgroups (too few
+    // tiles per slot for gemv_rowp): 8 chunks per wave halves the waves per tile, so every tile is resident in one
+    // round. 27B in_proj (1030 tiles): 14.7–15.2 → 14.2–14.4 µs; gate|up (gemv_rowp) and the shapes without the
+    // norm measured best as planned.
+    if (p.kernel == 1 && p.rt == 1 && p.ks == 1 && p.kw == 4 && rows == 1 && d->norm_w && !d->groups &&
+        fmt == FMT_NVFP4 && chunks % 8 == 0 && !getenv("MI_GEMV_ROW")) {
+      const long long slots = (long long)cu_count() * std::max(row_blocks_per_cu(fmt, 4, 64 * p.S, p.lds_bytes), 1);
+      if (n_tiles > slots) {
+        const Plan p8 = plan_row(d, fmt, chunks, rows, n_tiles, groups, 8);
+        if (p8.kernel) return p8;
+      }
+    }
     if (p.kernel) return p;
   }
   // INT4 at M >= 3 runs on gemv_tk unless gemv_rowm is pinned: measured on the 27B gate|up shape at M = 8,
