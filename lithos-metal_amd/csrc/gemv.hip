@@ -1977,6 +1977,13 @@ Plan plan_rowm(const mi_gemv_desc* d, int chunks, int n_tiles) {
   int force_ks = 0, force_rt = 0;
   if (const char* env = getenv("MI_GEMV_ROWM")) sscanf(env, "%d,%d", &force_ks, &force_rt);   // tuning sweeps
   if (force_ks) ks = force_ks;
+  // one split whose tiles' waves fill under three quarters of the chip's wave slots (12 per CU at this kernel's
+  // VGPR budget): three K splits, so the tiles spread over every CU (27B attention o_proj at M = 8, 320 tiles of 6
+  // waves: 14.0 → 11.6 µs with the reduction launch; out_proj's 12 waves per tile measured best unsplit)
+  if (!force_ks && ks == 1 && !d->norm_w && (long long)n_tiles * ((chunks + kw - 1) / kw) * 4 < 3LL * cu_count() * 12) {
+    const int kc3 = ((chunks + 2) / 3 + 7) / 8 * 8;
+    if (2 * kc3 < chunks) ks = 3;                // three non-empty splits on scale-group boundaries
+  }
   int kc = (chunks + ks - 1) / ks;
   if (ks > 1) kc = (kc + 7) / 8 * 8;             // splits on scale-group boundaries (whole waves for FP8)
   if (kc > 12 * kw || (ks > 1 && (ks - 1) * kc >= chunks)) return best;
