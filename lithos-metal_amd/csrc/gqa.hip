@@ -42,6 +42,7 @@ constexpr int DMAX = 256;
 struct GqaArgs {
   int t, heads, kv, d, rot, pos, ctx, gate, qk_norm, rep, rows;
   int n_groups, group_len;                      // decode workgroups per KV head, keys per workgroup
+  int xcd_tiles;                                // > 1: row tiles over workgroups in the XCD-grouped 1-D grid
   const uint16_t* proj; int ldp;
   const uint16_t* cosb; const uint16_t* sinb;   // [ctx][rot] BF16
   const float* q_norm; const float* k_norm;     // (1 + w), [D]
@@ -332,7 +333,19 @@ __global__ __launch_bounds__(64 * NW, 1) void gqa_decode(GqaArgs a) {
   __shared__ float mls[NW][RT * 16][2];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: the key range is a scalar loop
-  const int j = blockIdx.y, g = blockIdx.x;
+  // the workgroup's (key range g, KV head j, row-tile group zt): from the grid, or — row tiles spread over
+  // workgroups (a.xcd_tiles = their number) — from a 1-D grid in which the tiles of one key range take dispatch
+  // slots 8 apart: consecutive workgroups go to the 8 XCDs in turn, so the range's tiles run together on one XCD
+  // and all but the first read the range from that XCD's L2
+  int g = blockIdx.x, j = blockIdx.y, zt = blockIdx.z;
+  if (a.xcd_tiles > 1) {
+    const int id = blockIdx.x, slot = id >> 3;
+    zt = slot % a.xcd_tiles;
+    const int r = (slot / a.xcd_tiles) * 8 + (id & 7);           // key range × KV head
+    if (r >= a.n_groups * a.kv) return;                          // grid padding: workgroup-uniform
+    g = r % a.n_groups;
+    j = r / a.n_groups;
+  }
   if (stopped(a)) return;                               // workgroup-uniform
   const int pos = cur_pos(a);
   const int n_keys = min(pos + a.t, a.ctx);
@@ -347,7 +360,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gqa_decode(GqaArgs a) {
 
   // the query rows as B tiles (k-permuted: lane holds dims (DH/4)·kg + 8·s + i of row r0 + 16·rt + m16), zero past
   // rows; r0: the first of this workgroup's row tiles (blockIdx.z > 0 when the row tiles are split over workgroups)
-  const int r0 = blockIdx.z * RT * 16;
+  const int r0 = zt * RT * 16;
   const int nrows = min(RT * 16, a.rows - r0);
   OpT qb[RT][G::NS];
   float rsc[RT];                                        // the lane's row: 2^p of its prescale (int8 cache)
@@ -713,8 +726,15 @@ int launch(const GqaArgs& a, int rows, int nw, hipStream_t s) {
   MI_TRY_HIP(hipGetLastError(), "gqa_prep launch");
   const dim3 grid(a.n_groups, a.kv), block(64 * nw);
   const int rt = (rows + 15) / 16;
-  if constexpr (DH == 256) {     // one row tile per workgroup (grid z): more tiles' accumulators would spill
-    hipLaunchKernelGGL((gqa_decode<1, DH, BF, kNW>), dim3(a.n_groups, a.kv, rt), block, 0, s, a);
+  if constexpr (DH == 256) {     // one row tile per workgroup: more tiles' accumulators would spill
+    if (rt > 1) {                // a key range's row tiles on one XCD (gqa_decode's 1-D grid)
+      GqaArgs b = a;
+      b.xcd_tiles = rt;
+      const int slots = (a.n_groups * a.kv + 7) / 8 * rt;
+      hipLaunchKernelGGL((gqa_decode<1, DH, BF, kNW>), dim3(slots * 8), block, 0, s, b);
+    } else {
+      hipLaunchKernelGGL((gqa_decode<1, DH, BF, kNW>), dim3(a.n_groups, a.kv, 1), block, 0, s, a);
+    }
   } else if (nw == 8) {          // one row tile (gqa_waves): more tiles' accumulators would spill at 2 waves / SIMD
     hipLaunchKernelGGL((gqa_decode<1, DH, BF, 8>), grid, block, 0, s, a);
   } else {
