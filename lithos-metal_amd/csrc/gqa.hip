@@ -329,7 +329,11 @@ __global__ __launch_bounds__(64 * NW, 1) void gqa_decode(GqaArgs a) {
   using G = Geo<DH, BF>;
   using OpT = typename std::conditional<BF, bf16x8, f16x8>::type;
   constexpr int CH = G::CH;
-  __shared__ __attribute__((aligned(16))) float red[RT * 16][DH + 4];   // the workgroup's O, row-major
+  // one row tile at head dim 128: the waves' O meet in a pairwise tree through per-wave slabs (wave w > 0 owns slab
+  // w - 1); otherwise they are summed into red one wave after another
+  constexpr bool TREE = RT == 1 && DH == 128;
+  __shared__ __attribute__((aligned(16))) float red[TREE ? 1 : RT * 16][DH + 4];   // the workgroup's O, row-major
+  __shared__ __attribute__((aligned(16))) float slab[TREE ? NW - 1 : 1][16][DH + 4];
   __shared__ float mls[NW][RT * 16][2];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: the key range is a scalar loop
@@ -551,7 +555,8 @@ __global__ __launch_bounds__(64 * NW, 1) void gqa_decode(GqaArgs a) {
     }
   }
 
-  // ---- fold the workgroup's waves: common max, O summed in LDS in wave order, one partial per workgroup ---------
+  // ---- fold the workgroup's waves: common max, O summed in LDS (a pairwise tree, or in wave order), one partial per
+  // workgroup ----------------------------------------------------------------------------------------------------
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     const float l = quad16_sum(l_run[rt]);
@@ -574,20 +579,43 @@ __global__ __launch_bounds__(64 * NW, 1) void gqa_decode(GqaArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) o[rt][ct][i] *= f;
   }
-  for (int ww = 0; ww < NW; ++ww) {
-    if (w == ww) {
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-        for (int ct = 0; ct < G::NC; ++ct) {
-          f32x4* dst = reinterpret_cast<f32x4*>(&red[rt * 16 + m16][ct * 16 + 4 * kg]);
-          *dst = ww == 0 ? o[rt][ct] : *dst + o[rt][ct];
-        }
-    }
-    __syncthreads();
-  }
   const long long base = ((long long)j * a.n_groups + g) * a.rows + r0;
-  for (int idx = threadIdx.x; idx < nrows * DH; idx += 64 * NW) a.part_o[base * DH + idx] = red[idx / DH][idx % DH];
+  if constexpr (TREE) {
+    // step `half`: waves [half, 2·half) publish their O, waves [0, half) add it (wave r takes wave r + half); the
+    // slabs a step writes were not read in the step before, so one barrier per step. A fixed order: deterministic.
+    for (int half = NW / 2; half >= 1; half >>= 1) {
+      if (w >= half && w < 2 * half) {
+#pragma unroll
+        for (int ct = 0; ct < G::NC; ++ct)
+          *reinterpret_cast<f32x4*>(&slab[w - 1][m16][ct * 16 + 4 * kg]) = o[0][ct];
+      }
+      __syncthreads();
+      if (w < half) {
+#pragma unroll
+        for (int ct = 0; ct < G::NC; ++ct)
+          o[0][ct] += *reinterpret_cast<const f32x4*>(&slab[w + half - 1][m16][ct * 16 + 4 * kg]);
+      }
+    }
+    if (w == 0 && m16 < nrows) {                        // wave 0 holds the workgroup's O: straight to its partial
+#pragma unroll
+      for (int ct = 0; ct < G::NC; ++ct)
+        *reinterpret_cast<f32x4*>(a.part_o + (base + m16) * DH + ct * 16 + 4 * kg) = o[0][ct];
+    }
+  } else {
+    for (int ww = 0; ww < NW; ++ww) {
+      if (w == ww) {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+          for (int ct = 0; ct < G::NC; ++ct) {
+            f32x4* dst = reinterpret_cast<f32x4*>(&red[rt * 16 + m16][ct * 16 + 4 * kg]);
+            *dst = ww == 0 ? o[rt][ct] : *dst + o[rt][ct];
+          }
+      }
+      __syncthreads();
+    }
+    for (int idx = threadIdx.x; idx < nrows * DH; idx += 64 * NW) a.part_o[base * DH + idx] = red[idx / DH][idx % DH];
+  }
   for (int row = threadIdx.x; row < nrows; row += 64 * NW) {
     float M = -INFINITY, L = 0.0f;
     for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, mls[ww][row][0]);
