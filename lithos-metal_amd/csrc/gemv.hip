@@ -275,10 +275,15 @@ __global__ __launch_bounds__(KW == 16 ? 640 : 1024) void gemv_row(Args a) {
     pairs = g + 2;
     if (cnt <= 0 || expert < 0) return;       // the whole workgroup leaves together
   }
-  if (cnt > MT) cnt = MT;
+  // a grouped launch (one K split) takes a group's pairs MT at a time, pass blockIdx.z: a group of fewer pairs
+  // leaves its passes past them at once
+  const int pass = a.groups && !a.route_logits ? (int)blockIdx.z : 0;
+  if (pass * MT >= cnt) return;                 // workgroup-uniform
+  if (pairs) pairs += pass * MT;
+  cnt = min(MT, cnt - pass * MT);
   const long long xr0 = pairs ? (a.x_per_slot ? pairs[0] : pairs[0] / a.top_k) : 0;
   const long long xr1 = MT > 1 ? (pairs ? (a.x_per_slot ? pairs[cnt - 1] : pairs[cnt - 1] / a.top_k) : cnt - 1) : 0;
-  const int split = blockIdx.z;                  // K split (a.ks of a.kc chunks each; FP32 partials when > 1)
+  const int split = a.groups ? 0 : (int)blockIdx.z;   // K split (a.ks of a.kc chunks each; FP32 partials when > 1)
   const int c0_raw = split * a.kc + wave * KW;
   const int kw = min(KW, min(a.chunks, (split + 1) * a.kc) - c0_raw);   // <= 0: a wave past a short last split
   const int c0 = kw > 0 ? c0_raw : 0;           // such a wave reads chunk 0 (in bounds) and adds nothing
@@ -1709,6 +1714,7 @@ struct Plan {
   int lds_rows = 1, row_ld = 0, row_wave_lds = 0;
   size_t lds_bytes = 0;
   bool prenorm = false;    // the input norm as its own norm_apply launch into the workspace, then the plain GEMV
+  int passes = 1;          // gemv_row, grouped: pair passes of MT (grid z)
 };
 
 int check_desc(const mi_gemv_desc* d) {
@@ -2069,6 +2075,16 @@ Plan make_plan_fused(const mi_gemv_desc* d) {
     }
     if (p.kernel) return p;
   }
+  // Grouped (MoE) NVFP4 launches at M >= 3: routing spreads the tokens over the experts, so a group holds one or
+  // two pairs (the shared expert's group all of them): gemv_row takes them two per workgroup (grid z: the passes)
+  // instead of gemv_tk padding every group to 16 MFMA rows
+  if (rows > 2 && d->groups && fmt == FMT_NVFP4 && !pin_tk && !pin_rowm && !getenv("MI_MOE_TK")) {
+    Plan p = plan_row(d, fmt, chunks, 2, n_tiles, groups);
+    if (p.kernel && p.ks == 1) {
+      p.passes = (rows + 1) / 2;
+      return p;
+    }
+  }
   // INT4 at M >= 3 runs on gemv_tk unless gemv_rowm is pinned: measured on the 27B gate|up shape at M = 8,
   // gemv_rowm takes 37.4 µs against gemv_tk's 35.5 (its per-group scale / bias work is VALU time the NVFP4 decode
   // does not have), although gemv_tk moves 11 MB of split partials more
@@ -2127,7 +2143,7 @@ void launch(const Args& a, const Plan& p, int groups, hipStream_t s) {
     }
   }
   if (p.kernel == 1) {
-    const dim3 g(p.G, groups, p.ks);
+    const dim3 g(p.G, groups, a.groups ? p.passes : p.ks);
     if (p.lds_rows == 2) launch_row_k<FMT, 2>(a, p, g, s);
     else launch_row_k<FMT, 1>(a, p, g, s);
     if (p.ks > 1 && !a.fold_cnt) {
@@ -2176,7 +2192,7 @@ int mi_gemv_plan(const mi_gemv_desc* d, int32_t out[7]) {
   const int groups = d->groups ? d->max_groups : 1;
   out[0] = p.kernel; out[1] = p.S; out[2] = p.kw;
   out[3] = p.kernel == 1 ? p.rt : p.tb; out[4] = p.ks; out[5] = (int32_t)p.lds_bytes;
-  out[6] = (p.kernel != 2 ? p.G * p.ks : (n_tiles + p.tb - 1) / p.tb * p.ks) * groups;
+  out[6] = (p.kernel != 2 ? p.G * (d->groups && p.kernel == 1 ? p.passes : p.ks) : (n_tiles + p.tb - 1) / p.tb * p.ks) * groups;
   return MI_OK;
 }
 
