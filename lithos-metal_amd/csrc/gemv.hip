@@ -79,6 +79,7 @@ struct Args {
   int32_t* route_ids;
   float* route_weights;
   int32_t* route_groups;
+  int passes;               // gemv_row, dense M > 2: tokens taken MT per workgroup along grid z (0 / 1: none)
 };
 
 // ---- weight decode ---------------------------------------------------------------------------------------------
@@ -175,7 +176,7 @@ __device__ __forceinline__ void emit_row(const Args& a, int epi, int yr, int cnt
     const int row = tile * 16 + m_row;
     if (row >= a.n) return;
     float o = v;
-    if (epi == MI_EPI_RESIDUAL) o += bf16_bits_to_f32(a.res[(long long)t * a.ldr + row]);
+    if (epi == MI_EPI_RESIDUAL) o += bf16_bits_to_f32(a.res[(long long)yr * a.ldr + row]);   // dense: yr = token
     store_out(a, (long long)yr * a.ldy + row, o);
   }
 }
@@ -275,15 +276,17 @@ __global__ __launch_bounds__(KW == 16 ? 640 : 1024) void gemv_row(Args a) {
     pairs = g + 2;
     if (cnt <= 0 || expert < 0) return;       // the whole workgroup leaves together
   }
-  // a grouped launch (one K split) takes a group's pairs MT at a time, pass blockIdx.z: a group of fewer pairs
-  // leaves its passes past them at once
-  const int pass = a.groups && !a.route_logits ? (int)blockIdx.z : 0;
+  // more than MT tokens (a grouped launch's pairs, or a.passes > 1 dense tokens) are taken MT per workgroup, pass
+  // blockIdx.z (one K split); a pass past the tokens leaves at once
+  const bool zpass = (a.groups && !a.route_logits) || a.passes > 1;
+  const int pass = zpass ? (int)blockIdx.z : 0;
   if (pass * MT >= cnt) return;                 // workgroup-uniform
   if (pairs) pairs += pass * MT;
   cnt = min(MT, cnt - pass * MT);
-  const long long xr0 = pairs ? (a.x_per_slot ? pairs[0] : pairs[0] / a.top_k) : 0;
-  const long long xr1 = MT > 1 ? (pairs ? (a.x_per_slot ? pairs[cnt - 1] : pairs[cnt - 1] / a.top_k) : cnt - 1) : 0;
-  const int split = a.groups ? 0 : (int)blockIdx.z;   // K split (a.ks of a.kc chunks each; FP32 partials when > 1)
+  const int t0 = pairs ? 0 : pass * MT;         // dense: the pass's first token
+  const long long xr0 = pairs ? (a.x_per_slot ? pairs[0] : pairs[0] / a.top_k) : t0;
+  const long long xr1 = MT > 1 ? (pairs ? (a.x_per_slot ? pairs[cnt - 1] : pairs[cnt - 1] / a.top_k) : t0 + cnt - 1) : 0;
+  const int split = zpass ? 0 : (int)blockIdx.z;   // K split (a.ks of a.kc chunks each; FP32 partials when > 1)
   const int c0_raw = split * a.kc + wave * KW;
   const int kw = min(KW, min(a.chunks, (split + 1) * a.kc) - c0_raw);   // <= 0: a wave past a short last split
   const int c0 = kw > 0 ? c0_raw : 0;           // such a wave reads chunk 0 (in bounds) and adds nothing
@@ -583,7 +586,7 @@ __global__ __launch_bounds__(KW == 16 ? 640 : 1024) void gemv_row(Args a) {
     float v = vt[t];
     v *= rs;
     const float up = __shfl_down(v, 8, 16);
-    if (g == 0) emit(a, epilogue_of(a, expert), pairs, cnt, tile, true, m_row, t, v, up);
+    if (g == 0 && t < cnt) emit_row(a, epilogue_of(a, expert), pairs ? pairs[t] : t0 + t, cnt, tile, true, m_row, t, v, up);
   }
 }
 
@@ -1714,7 +1717,7 @@ struct Plan {
   int lds_rows = 1, row_ld = 0, row_wave_lds = 0;
   size_t lds_bytes = 0;
   bool prenorm = false;    // the input norm as its own norm_apply launch into the workspace, then the plain GEMV
-  int passes = 1;          // gemv_row, grouped: pair passes of MT (grid z)
+  int passes = 1;          // gemv_row over more than two tokens or pairs: workgroups of two along grid z
 };
 
 int check_desc(const mi_gemv_desc* d) {
@@ -2077,10 +2080,12 @@ Plan make_plan_fused(const mi_gemv_desc* d) {
   }
   // Grouped (MoE) NVFP4 launches at M >= 3: routing spreads the tokens over the experts, so a group holds one or
   // two pairs (the shared expert's group all of them): gemv_row takes them two per workgroup (grid z: the passes)
-  // instead of gemv_tk padding every group to 16 MFMA rows
-  if (rows > 2 && d->groups && fmt == FMT_NVFP4 && !pin_tk && !pin_rowm && !getenv("MI_MOE_TK")) {
+  // instead of gemv_tk padding every group to 16 MFMA rows. A small BF16 matrix (the MoE router, 1 MB) the same
+  // way, two tokens per workgroup: its passes re-read it from the caches, and no split-K reduction launch follows.
+  const bool small_bf16 = fmt == FMT_BF16 && !d->groups && (size_t)d->n * d->k * 2 <= (8u << 20);
+  if (rows > 2 && ((d->groups && fmt == FMT_NVFP4) || small_bf16) && !pin_tk && !pin_rowm && !getenv("MI_MOE_TK")) {
     Plan p = plan_row(d, fmt, chunks, 2, n_tiles, groups);
-    if (p.kernel && p.ks == 1) {
+    if (p.kernel && p.ks == 1 && p.rt == 1) {
       p.passes = (rows + 1) / 2;
       return p;
     }
@@ -2143,7 +2148,7 @@ void launch(const Args& a, const Plan& p, int groups, hipStream_t s) {
     }
   }
   if (p.kernel == 1) {
-    const dim3 g(p.G, groups, a.groups ? p.passes : p.ks);
+    const dim3 g(p.G, groups, p.passes > 1 ? p.passes : p.ks);
     if (p.lds_rows == 2) launch_row_k<FMT, 2>(a, p, g, s);
     else launch_row_k<FMT, 1>(a, p, g, s);
     if (p.ks > 1 && !a.fold_cnt) {
@@ -2192,7 +2197,7 @@ int mi_gemv_plan(const mi_gemv_desc* d, int32_t out[7]) {
   const int groups = d->groups ? d->max_groups : 1;
   out[0] = p.kernel; out[1] = p.S; out[2] = p.kw;
   out[3] = p.kernel == 1 ? p.rt : p.tb; out[4] = p.ks; out[5] = (int32_t)p.lds_bytes;
-  out[6] = (p.kernel != 2 ? p.G * (d->groups && p.kernel == 1 ? p.passes : p.ks) : (n_tiles + p.tb - 1) / p.tb * p.ks) * groups;
+  out[6] = (p.kernel != 2 ? p.G * (p.passes > 1 ? p.passes : p.ks) : (n_tiles + p.tb - 1) / p.tb * p.ks) * groups;
   return MI_OK;
 }
 
@@ -2247,6 +2252,7 @@ int gemv_impl(const mi_gemv_desc* d, void* stream, void* fixed_ws, size_t fixed_
   a.kc = p.kernel == 1 ? p.tb : p.kw;     // chunks per K split
   a.row_ld = p.row_ld;
   a.row_wave_lds = p.row_wave_lds;
+  a.passes = d->groups ? 0 : p.passes;
   const size_t need = workspace_need(d, p);
   void* ws = nullptr;
   if (need) {
