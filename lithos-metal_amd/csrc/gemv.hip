@@ -2082,8 +2082,11 @@ Plan make_plan_fused(const mi_gemv_desc* d) {
   // two pairs (the shared expert's group all of them): gemv_row takes them two per workgroup (grid z: the passes)
   // instead of gemv_tk padding every group to 16 MFMA rows. A small BF16 matrix (the MoE router, 1 MB) the same
   // way, two tokens per workgroup: its passes re-read it from the caches, and no split-K reduction launch follows.
-  const bool small_bf16 = fmt == FMT_BF16 && !d->groups && (size_t)d->n * d->k * 2 <= (8u << 20);
-  if (rows > 2 && ((d->groups && fmt == FMT_NVFP4) || small_bf16) && !pin_tk && !pin_rowm && !getenv("MI_MOE_TK")) {
+  // (NVFP4 stays on gemv_rowm: the attention o_proj, 8.8 MB, measured 11.8 → 10.5–10.8 µs alone but no faster in
+  // the layer; out_proj, 17.7 MB, and q|k|v, 20 MB, are slower with passes)
+  const bool small = !d->groups && !d->gnorm_w && fmt == FMT_BF16 && (size_t)d->n * d->k * 2 <= (8u << 20);
+  if (rows > 2 && ((d->groups && fmt == FMT_NVFP4) || small) && !pin_tk && !pin_rowm &&
+      !(getenv("MI_GEMV_PASSES") && getenv("MI_GEMV_PASSES")[0] == '0')) {       // =0: the earlier plans (A/B)
     Plan p = plan_row(d, fmt, chunks, 2, n_tiles, groups);
     if (p.kernel && p.ks == 1 && p.rt == 1) {
       p.passes = (rows + 1) / 2;
