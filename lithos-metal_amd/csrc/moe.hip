@@ -36,7 +36,6 @@ struct RouteArgs {
 
 __global__ __launch_bounds__(64 * MAX_T) void moe_route(RouteArgs a) {
   __shared__ int sel[MAX_T * (MAX_K + 1)];
-  __shared__ int fresh[64 * MAX_T];
   const int lane = threadIdx.x & 63, t = threadIdx.x >> 6;
   const int E = a.n_experts, k = a.top_k;
   const int ks = k + (a.shared_expert > 0 ? 1 : 0);   // slots per token (the shared expert last)
@@ -62,28 +61,48 @@ __global__ __launch_bounds__(64 * MAX_T) void moe_route(RouteArgs a) {
     }
   }
   if (!a.groups) return;                            // workgroup-uniform
-  __syncthreads();
-  // groups: record g = the g-th distinct expert in pair order; pairs of a record ascending. One thread per pair
-  // (P = t·k <= 64·t = blockDim): first use, rank and count by one pass over the pairs, then the record index as the
-  // number of first uses before this expert's first use.
+  // groups: record g = the g-th distinct expert in pair order; pairs of a record ascending. Per chosen expert, LDS
+  // holds its lowest pair and its pairs as a bit mask (order-independent atomic min / or); a pair's rank is the
+  // popcount of its expert's bits below it, the count all of them, and the record index the popcount of the
+  // first-use bits below the expert's first use — no pass over the pairs.
+  constexpr int PW = (MAX_T * (MAX_K + 1) + 31) / 32;     // words of a pair mask
+  __shared__ int first_use[64 * MAX_PER_LANE];
+  __shared__ uint32_t pmask[64 * MAX_PER_LANE][PW];
+  __shared__ uint32_t fresh[PW];
   const int P = a.t * ks;
   const int p = threadIdx.x;
-  int e = -1, first = p, rank = 0, count = 0;
-  if (p < P && sel[p] >= 0) {          // a pair without an expert (id -1) joins no group
-    e = sel[p];
-    for (int q = 0; q < P; ++q) {
-      if (sel[q] != e) continue;
-      if (q < first) first = q;
-      if (q < p) ++rank;
-      ++count;
+  __syncthreads();                                  // every wave's slots are in sel
+  const int e = p < P ? sel[p] : -1;                // a pair without an expert (id -1) joins no group
+  if (e >= 0) {                                     // clear the chosen experts' entries (idempotent)
+    first_use[e] = P;
+#pragma unroll
+    for (int w = 0; w < PW; ++w) pmask[e][w] = 0u;
+  }
+  if (p < PW) fresh[p] = 0u;
+  __syncthreads();
+  if (e >= 0) {
+    atomicMin(&first_use[e], p);
+    atomicOr(&pmask[e][p >> 5], 1u << (p & 31));
+  }
+  __syncthreads();
+  int first = p, rank = 0, count = 0;
+  if (e >= 0) {
+    first = first_use[e];
+    if (first == p) atomicOr(&fresh[p >> 5], 1u << (p & 31));
+#pragma unroll
+    for (int w = 0; w < PW; ++w) {
+      const uint32_t m = pmask[e][w];
+      count += __popc(m);
+      rank += w < (p >> 5) ? __popc(m) : w == (p >> 5) ? __popc(m & ((1u << (p & 31)) - 1u)) : 0;
     }
   }
-  fresh[p] = e >= 0 && first == p;
   __syncthreads();
   int distinct = 0, g = 0;
-  for (int q = 0; q < P; ++q) {
-    distinct += fresh[q];
-    g += q < first ? fresh[q] : 0;
+#pragma unroll
+  for (int w = 0; w < PW; ++w) {
+    const uint32_t m = fresh[w];
+    distinct += __popc(m);
+    g += w < (first >> 5) ? __popc(m) : w == (first >> 5) ? __popc(m & ((1u << (first & 31)) - 1u)) : 0;
   }
   if (e >= 0) {
     int32_t* rec = a.groups + (long long)g * GROUP_REC;
