@@ -154,6 +154,8 @@ typedef struct mi_gemv_desc {
   int32_t route_experts, route_top_k, route_renorm, route_gate_col;
   int32_t* route_ids;
   float* route_weights;
+  /* grouped mode: at most this many pairs per record (mi_moe_route's pairs_per_record); 0 = up to 16 */
+  int32_t group_max_pairs;
 } mi_gemv_desc;
 size_t mi_gemv_workspace_bytes(const mi_gemv_desc* d);   /* 0 when the plan needs none */
 int mi_gemv(const mi_gemv_desc* d, void* stream);
@@ -302,6 +304,10 @@ typedef struct mi_moe_route_desc {
   int32_t max_groups;
   int32_t shared_expert;     /* 0 = none */
   int32_t shared_gate_col;
+  /* 1..16: an expert's pairs go into consecutive records of at most this many (max_groups >= t·slots), so a grouped
+   * GEMV that takes two pairs per workgroup needs one pass per record; 0 = one record per expert (up to 16 pairs).
+   * No counterpart in the reference (its groups are per expert). */
+  int32_t pairs_per_record;
 } mi_moe_route_desc;
 int mi_moe_route(const mi_moe_route_desc* d, void* stream);
 

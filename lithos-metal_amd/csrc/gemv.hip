@@ -2094,7 +2094,8 @@ Plan make_plan_fused(const mi_gemv_desc* d) {
       !(getenv("MI_GEMV_PASSES") && getenv("MI_GEMV_PASSES")[0] == '0')) {       // =0: the earlier plans (A/B)
     Plan p = plan_row(d, fmt, chunks, 2, n_tiles, groups);
     if (p.kernel && p.ks == 1 && p.rt == 1) {
-      p.passes = (rows + 1) / 2;
+      // records of at most two pairs (mi_moe_route's pairs_per_record): one pass; else the passes along z
+      p.passes = d->groups && d->group_max_pairs > 0 && d->group_max_pairs <= 2 ? 1 : (rows + 1) / 2;
       return p;
     }
   }

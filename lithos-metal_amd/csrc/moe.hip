@@ -32,6 +32,7 @@ struct RouteArgs {
   float* weights;
   int32_t* groups;
   int shared_expert, shared_gate_col;           // shared_expert > 0: slot top_k of every token (the shared expert)
+  int pairs_per_record;                         // 1..16: an expert's pairs in records of at most this many; 0: 16
 };
 
 __global__ __launch_bounds__(64 * MAX_T) void moe_route(RouteArgs a) {
@@ -61,14 +62,17 @@ __global__ __launch_bounds__(64 * MAX_T) void moe_route(RouteArgs a) {
     }
   }
   if (!a.groups) return;                            // workgroup-uniform
-  // groups: record g = the g-th distinct expert in pair order; pairs of a record ascending. Per chosen expert, LDS
-  // holds its lowest pair and its pairs as a bit mask (order-independent atomic min / or); a pair's rank is the
-  // popcount of its expert's bits below it, the count all of them, and the record index the popcount of the
-  // first-use bits below the expert's first use — no pass over the pairs.
+  // groups: an expert's pairs, ascending, in records of at most PR pairs; the records of one expert consecutive, the
+  // experts in order of first use. Per chosen expert, LDS holds its lowest pair and its pairs as a bit mask
+  // (order-independent atomic min / or): a pair's rank is the popcount of its expert's bits below it, the count all
+  // of them. The expert's first record is the scan, over the pairs in order, of the records each expert's first
+  // pair opens (a wave scan, then the waves' totals) — no pass over the pairs.
   constexpr int PW = (MAX_T * (MAX_K + 1) + 31) / 32;     // words of a pair mask
   __shared__ int first_use[64 * MAX_PER_LANE];
   __shared__ uint32_t pmask[64 * MAX_PER_LANE][PW];
-  __shared__ uint32_t fresh[PW];
+  __shared__ int pre[64 * MAX_T];                   // the records opened before each pair
+  __shared__ int wtot[MAX_T];
+  const int PR = a.pairs_per_record > 0 ? a.pairs_per_record : GROUP_REC - 2;
   const int P = a.t * ks;
   const int p = threadIdx.x;
   __syncthreads();                                  // every wave's slots are in sel
@@ -78,7 +82,6 @@ __global__ __launch_bounds__(64 * MAX_T) void moe_route(RouteArgs a) {
 #pragma unroll
     for (int w = 0; w < PW; ++w) pmask[e][w] = 0u;
   }
-  if (p < PW) fresh[p] = 0u;
   __syncthreads();
   if (e >= 0) {
     atomicMin(&first_use[e], p);
@@ -88,7 +91,6 @@ __global__ __launch_bounds__(64 * MAX_T) void moe_route(RouteArgs a) {
   int first = p, rank = 0, count = 0;
   if (e >= 0) {
     first = first_use[e];
-    if (first == p) atomicOr(&fresh[p >> 5], 1u << (p & 31));
 #pragma unroll
     for (int w = 0; w < PW; ++w) {
       const uint32_t m = pmask[e][w];
@@ -96,21 +98,30 @@ __global__ __launch_bounds__(64 * MAX_T) void moe_route(RouteArgs a) {
       rank += w < (p >> 5) ? __popc(m) : w == (p >> 5) ? __popc(m & ((1u << (p & 31)) - 1u)) : 0;
     }
   }
-  __syncthreads();
-  int distinct = 0, g = 0;
+  const int opened = e >= 0 && first == p ? (count + PR - 1) / PR : 0;   // records an expert's first pair opens
+  int inc = opened;                                 // inclusive scan over the wave's pairs
 #pragma unroll
-  for (int w = 0; w < PW; ++w) {
-    const uint32_t m = fresh[w];
-    distinct += __popc(m);
-    g += w < (first >> 5) ? __popc(m) : w == (first >> 5) ? __popc(m & ((1u << (first & 31)) - 1u)) : 0;
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(inc, off, 64);
+    inc += lane >= off ? y : 0;
   }
+  if (lane == 63) wtot[t] = inc;
+  __syncthreads();
+  int before = 0, total = 0;
+  for (int w = 0; w < a.t; ++w) {
+    before += w < t ? wtot[w] : 0;
+    total += wtot[w];
+  }
+  pre[p] = before + inc - opened;
+  __syncthreads();
   if (e >= 0) {
-    int32_t* rec = a.groups + (long long)g * GROUP_REC;
-    rec[2 + rank] = p;
-    if (rank == 0) { rec[0] = e; rec[1] = count; }
+    const int q = rank / PR;
+    int32_t* rec = a.groups + (long long)(pre[first] + q) * GROUP_REC;
+    rec[2 + rank - q * PR] = p;
+    if (rank == q * PR) { rec[0] = e; rec[1] = min(PR, count - q * PR); }
   }
-  // the records past the distinct experts: empty
-  for (int r = distinct + p; r < a.max_groups; r += blockDim.x) {
+  // the records past the last one: empty
+  for (int r = total + p; r < a.max_groups; r += blockDim.x) {
     a.groups[(long long)r * GROUP_REC] = -1;
     a.groups[(long long)r * GROUP_REC + 1] = 0;
   }
@@ -182,10 +193,14 @@ extern "C" int mi_moe_route(const mi_moe_route_desc* d, void* stream) {
   MI_REQUIRE(!sh || (d->shared_expert >= d->n_experts && d->shared_gate_col >= 0 && d->shared_gate_col < d->ld_logits),
              "mi_moe_route: the shared expert's index must follow the routed experts and its gate column lie in the "
              "logits row");
-  MI_REQUIRE(!d->groups || d->max_groups >= std::min(d->t * d->top_k, d->n_experts) + sh,
-             "mi_moe_route: max_groups=%d cannot hold every distinct expert", d->max_groups);
+  MI_REQUIRE(d->pairs_per_record >= 0 && d->pairs_per_record <= GROUP_REC - 2,
+             "mi_moe_route: pairs_per_record=%d must be in 0..%d", d->pairs_per_record, GROUP_REC - 2);
+  MI_REQUIRE(!d->groups || d->max_groups >= (d->pairs_per_record > 0 ? d->t * (d->top_k + sh)
+                                                                     : std::min(d->t * d->top_k, d->n_experts) + sh),
+             "mi_moe_route: max_groups=%d cannot hold every record (t·slots with pairs_per_record, else the distinct "
+             "experts)", d->max_groups);
   RouteArgs a{d->t, d->n_experts, d->top_k, d->renorm, d->ld_logits, d->max_groups, d->logits, d->ids, d->weights,
-              d->groups, d->shared_expert, d->shared_gate_col};
+              d->groups, d->shared_expert, d->shared_gate_col, d->pairs_per_record};
   hipLaunchKernelGGL(moe_route, dim3(1), dim3(64 * d->t), 0, static_cast<hipStream_t>(stream), a);
   MI_TRY_HIP(hipGetLastError(), "moe_route launch");
   return MI_OK;

@@ -387,13 +387,15 @@ GROUP_REC = 18
 
 
 def moe_route(logits, top_k: int, *, renorm: bool = True, groups: bool = True, out=None, stream=None,
-              shared_expert: int = 0, shared_gate=None):
+              shared_expert: int = 0, shared_gate=None, pairs_per_record: int = 0):
     """``moe_route`` (``ops/moe.py``): ``logits [T, E]`` bf16 → ``(ids [T, k] int32, weights [T, k] float32,
     groups [max_groups, 18] int32 or None)``; ``max_groups = min(E, T·k)``. The groups feed ``moe_gemv``. ``out``:
     preallocated ``(ids, weights, groups)`` (a captured step allocates nothing). ``shared_expert`` > 0 (its index in
     the stacked experts, after the routed ones) with ``shared_gate`` = the column of ``logits``' rows that holds the
     shared gate's logit (the logits tensor a view of a wider router output): every token gets slot k = the shared
-    expert with weight bf16(σ(gate)), so ids / weights are ``[T, k + 1]`` and there is one group more."""
+    expert with weight bf16(σ(gate)), so ids / weights are ``[T, k + 1]`` and there is one group more.
+    ``pairs_per_record`` (1..16): an expert's pairs go into consecutive records of at most that many (``max_groups``
+    is then ``T·slots``), for a grouped GEMV that takes two pairs per workgroup (``moe_gemv(group_max_pairs=2)``)."""
     torch = _torch()
     _bf16_2d(logits, "moe_route logits", aligned=False)
     t, e = logits.shape
@@ -402,7 +404,9 @@ def moe_route(logits, top_k: int, *, renorm: bool = True, groups: bool = True, o
     if sh and (shared_gate is None or shared_expert < e or not 0 <= shared_gate < logits.stride(0)):
         raise ValueError("moe_route: the shared expert follows the routed ones and its gate column lies in the row")
     ks = top_k + sh
-    max_groups = min(e, t * top_k) + sh
+    if not 0 <= pairs_per_record <= GROUP_REC - 2:
+        raise ValueError("moe_route: pairs_per_record in 0..16")
+    max_groups = t * ks if pairs_per_record else min(e, t * top_k) + sh
     if out is not None:
         ids, w, g = out
         if (ids.dtype != torch.int32 or ids.numel() < t * ks or w.dtype != torch.float32 or w.numel() < t * ks
@@ -417,20 +421,22 @@ def moe_route(logits, top_k: int, *, renorm: bool = True, groups: bool = True, o
     d = hip.MiMoeRouteDesc(t=t, n_experts=e, top_k=top_k, renorm=int(renorm), logits=hip.ptr(logits),
                            ld_logits=logits.stride(0), ids=hip.ptr(ids), weights=hip.ptr(w), groups=hip.ptr(g),
                            max_groups=max_groups if groups else 0, shared_expert=shared_expert,
-                           shared_gate_col=shared_gate if sh else 0)
+                           shared_gate_col=shared_gate if sh else 0, pairs_per_record=pairs_per_record)
     hip.call("mi_moe_route", C.byref(d), hip.stream_handle(stream))
     return ids, w, g
 
 
 def moe_gemv(w: PackedWeight, x, groups, *, tokens: int, top_k: int, x_per_slot: bool, epilogue=None, norm_w=None,
-             eps: float = 1e-6, out=None, stream=None, shared_expert: int = 0, shared_epilogue=None, route=None):
+             eps: float = 1e-6, out=None, stream=None, shared_expert: int = 0, shared_epilogue=None, route=None,
+             group_max_pairs: int = 0):
     """``moe_gemv`` (``ops/moe.py``; the grouped mode of ``gemv``): for every group record (expert e, its pairs
     p = t·k + j), ``out[p] = x_row · W_eᵀ`` with ``x_row = x[p]`` (``x_per_slot``) or ``x[p // k]``; ``w`` holds the
     experts back to back. ``out [T·k, n_out]`` bf16. ``shared_expert`` > 0: that expert's group (the shared expert
     stacked after the routed ones) takes ``shared_epilogue``. ``route`` (one token): ``dict(logits=…, ids=…,
     weights=…, top_k=k, renorm=True, gate_col=…)`` — the launch routes for itself from the token's router row
     (exactly ``moe_route``'s ids and weights), group g = slot g, and writes ids / weights and the group records into
-    ``groups`` for the launches after it; ``top_k`` is then k (+1 with ``shared_expert``)."""
+    ``groups`` for the launches after it; ``top_k`` is then k (+1 with ``shared_expert``). ``group_max_pairs``: the
+    records hold at most that many pairs (``moe_route(pairs_per_record=…)``; 0 = up to 16)."""
     torch = _torch()
     _bf16_2d(x, "moe_gemv x")
     if x.shape[1] != w.k:
@@ -452,7 +458,8 @@ def moe_gemv(w: PackedWeight, x, groups, *, tokens: int, top_k: int, x_per_slot:
                        ldy=out.stride(0), epilogue=hip.MI_EPI[epilogue], residual=0, ldr=0, norm_w=hip.ptr(norm_w),
                        eps=eps, groups=hip.ptr(groups), max_groups=groups.shape[0], top_k=top_k,
                        x_per_slot=int(x_per_slot), workspace=0, workspace_bytes=0, out_f32=0,
-                       shared_expert=shared_expert, shared_epilogue=hip.MI_EPI[shared_epilogue])
+                       shared_expert=shared_expert, shared_epilogue=hip.MI_EPI[shared_epilogue],
+                       group_max_pairs=group_max_pairs)
     if route is not None:
         lg = route["logits"]
         if lg.dtype != torch.bfloat16 or lg.dim() != 2 or lg.shape[0] != 1 or tokens != 1:

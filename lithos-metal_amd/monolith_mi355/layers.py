@@ -368,7 +368,9 @@ class MoeBlock:
         torch = _torch()
         if m not in self._bufs:
             sh = 1 if self.fused_shared else 0
-            dev, k, g = self.norm_w.device, self.top_k + sh, min(self.experts, m * self.top_k) + sh
+            # at M >= 3 the route splits an expert's pairs into records of two (one pass of the grouped GEMV each)
+            dev, k = self.norm_w.device, self.top_k + sh
+            g = m * k if m > 2 else min(self.experts, m * self.top_k) + sh
             bf = torch.bfloat16
             self._bufs[m] = (torch.empty(m, (self.experts + 1 + 7) // 8 * 8, dtype=bf, device=dev),
                              (torch.empty(m, k, dtype=torch.int32, device=dev),
@@ -406,12 +408,15 @@ class MoeBlock:
             if m == 1:                  # one token: the expert gate|up launch routes for itself (one launch fewer)
                 inline = dict(logits=logits[:, :e], ids=ids, weights=wts, top_k=k, renorm=True, gate_col=e)
             else:
-                kernels.moe_route(logits[:, :e], k, renorm=True, out=route, shared_expert=e, shared_gate=e)
+                kernels.moe_route(logits[:, :e], k, renorm=True, out=route, shared_expert=e, shared_gate=e,
+                                  pairs_per_record=2 if m > 2 else 0)
                 inline = None
+            ppr = 2 if m > 2 else 0
             kernels.moe_gemv(self.gate_up_s, x, groups, tokens=m, top_k=k + 1, x_per_slot=False,
                              epilogue="silu_mul_rounded", norm_w=nw, eps=self.eps, out=act,
-                             shared_expert=e, shared_epilogue="silu_mul", route=inline)
-            kernels.moe_gemv(self.down_s, act, groups, tokens=m, top_k=k + 1, x_per_slot=True, out=hk)
+                             shared_expert=e, shared_epilogue="silu_mul", route=inline, group_max_pairs=ppr)
+            kernels.moe_gemv(self.down_s, act, groups, tokens=m, top_k=k + 1, x_per_slot=True, out=hk,
+                             group_max_pairs=ppr)
             return kernels.moe_combine(hk, wts, top_k=k + 1, residual=h, out=out)
 
         def shared(ws=None):

@@ -37,7 +37,8 @@ class MiGemvDesc(C.Structure):
                 ("gnorm_w", C.c_void_p), ("gnorm_z", C.c_void_p), ("ld_gnorm_z", C.c_int32), ("gnorm_eps", C.c_float),
                 ("shared_expert", C.c_int32), ("shared_epilogue", C.c_int32), ("route_logits", C.c_void_p),
                 ("route_experts", C.c_int32), ("route_top_k", C.c_int32), ("route_renorm", C.c_int32),
-                ("route_gate_col", C.c_int32), ("route_ids", C.c_void_p), ("route_weights", C.c_void_p)]
+                ("route_gate_col", C.c_int32), ("route_ids", C.c_void_p), ("route_weights", C.c_void_p),
+                ("group_max_pairs", C.c_int32)]
 
 
 class MiGdnDesc(C.Structure):
@@ -75,7 +76,7 @@ class MiMoeRouteDesc(C.Structure):
     _fields_ = [("t", C.c_int32), ("n_experts", C.c_int32), ("top_k", C.c_int32), ("renorm", C.c_int32),
                 ("logits", C.c_void_p), ("ld_logits", C.c_int32), ("ids", C.c_void_p), ("weights", C.c_void_p),
                 ("groups", C.c_void_p), ("max_groups", C.c_int32), ("shared_expert", C.c_int32),
-                ("shared_gate_col", C.c_int32)]
+                ("shared_gate_col", C.c_int32), ("pairs_per_record", C.c_int32)]
 
 
 class MiMoeCombineDesc(C.Structure):

@@ -366,3 +366,49 @@ def test_moe_route_nan_row_routes_nowhere(torch_gpu):
     pairs = sorted(int(p) for r in recs for p in r[2: 2 + r[1]])
     assert pairs == [p for p in range(24) if p // 8 != 1]
     assert ((recs[:, 0] >= 0) & (recs[:, 0] < 256)).all()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("t", [3, 8, 16])
+def test_moe_route_records_of_two_pairs(torch_gpu, t):
+    """``moe_route(pairs_per_record=2)``: every pair in exactly one record; a record holds one expert's pairs,
+    ascending, at most two; an expert's records consecutive and the experts in order of first use (the unsplit
+    records, cut in twos); the grouped gate|up and down GEMVs over them (``group_max_pairs=2``, one pass per
+    record) give the same outputs bit for bit as over the unsplit records. Tied logits force big groups."""
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    from monolith_mi355.layers import MoeBlock
+    blk = MoeBlock(experts=64, seed=13)
+    e, k = 64, 8
+    rng = np.random.default_rng(21 + t)
+    lg = rbf(rng.standard_normal((t, 72)))
+    lg[: t // 2, :e] = lg[0, :e]                    # half the tokens route identically: groups of t / 2 pairs
+    logits = to_dev_bf16(torch, lg)
+    ids, w, g1 = kernels.moe_route(logits[:, :e], k, renorm=True, shared_expert=e, shared_gate=e)
+    ids2, w2, g2 = kernels.moe_route(logits[:, :e], k, renorm=True, shared_expert=e, shared_gate=e,
+                                     pairs_per_record=2)
+    torch.cuda.synchronize()
+    assert torch.equal(ids, ids2) and torch.equal(w.view(torch.int32), w2.view(torch.int32))
+    a, b = g1.cpu().numpy(), g2.cpu().numpy()
+    assert b.shape[0] == t * (k + 1)
+    cut = []                                         # the unsplit records cut into twos, in order
+    for rec in a:
+        if rec[1] <= 0:
+            continue
+        pairs = list(rec[2: 2 + rec[1]])
+        cut += [(int(rec[0]), pairs[i: i + 2]) for i in range(0, len(pairs), 2)]
+    got = [(int(r[0]), list(r[2: 2 + r[1]])) for r in b if r[1] > 0]
+    assert got == cut
+    assert all(r[0] == -1 and r[1] == 0 for r in b[len(got):])
+    h = to_dev_bf16(torch, rbf(rng.standard_normal((t, 2048))))
+    kw = dict(tokens=t, top_k=k + 1, shared_expert=e, shared_epilogue="silu_mul")
+    act1 = kernels.moe_gemv(blk.gate_up_s, h, g1, x_per_slot=False, epilogue="silu_mul_rounded", norm_w=blk.norm_w,
+                            **kw)
+    act2 = kernels.moe_gemv(blk.gate_up_s, h, g2, x_per_slot=False, epilogue="silu_mul_rounded", norm_w=blk.norm_w,
+                            group_max_pairs=2, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(act1.view(torch.int16), act2.view(torch.int16))
+    y1 = kernels.moe_gemv(blk.down_s, act1, g1, tokens=t, top_k=k + 1, x_per_slot=True)
+    y2 = kernels.moe_gemv(blk.down_s, act1, g2, tokens=t, top_k=k + 1, x_per_slot=True, group_max_pairs=2)
+    torch.cuda.synchronize()
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
