@@ -82,3 +82,42 @@ def test_gemv_rejects_bad_descriptors_before_launch():
     for kw in bad:
         assert lib.mi_gemv(C.byref(_desc(hip, **kw)), None) == 1, kw      # MI_E_INVALID, nothing enqueued
         assert hip.last_error().startswith("mi_gemv")
+
+
+def test_ctypes_descriptors_match_the_header_layout(tmp_path):
+    """Every ctypes mirror of a header struct has the C layout: each field's offset and the struct's size, from a
+    small program compiled against ``include/lithos_mi355.h`` (a descriptor shorter than the C struct would let the
+    library read past it)."""
+    import shutil
+    import subprocess
+    from monolith_mi355.runtime import hip
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    classes = [v for k, v in vars(hip).items()
+               if isinstance(v, type) and issubclass(v, C.Structure) and k.startswith("Mi")]
+    assert len(classes) >= 15
+
+    def c_name(cls):
+        return "mi" + re.sub(r"([A-Z])", lambda m: "_" + m.group(1).lower(), cls.__name__[2:])
+
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{ROOT / "include" / "lithos_mi355.h"}"',
+             "int main(void) {"]
+    for cls in classes:
+        n = c_name(cls)
+        lines.append(f'  printf("{cls.__name__} size %zu\\n", sizeof({n}));')
+        for f, _ in cls._fields_:
+            lines.append(f'  printf("{cls.__name__} {f} %zu\\n", offsetof({n}, {f}));')
+    lines.append("  return 0;\n}")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run([cc, "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True, capture_output=True)
+    want = {}
+    for line in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.splitlines():
+        cls_name, field, value = line.split()
+        want[(cls_name, field)] = int(value)
+    for cls in classes:
+        assert C.sizeof(cls) == want[(cls.__name__, "size")], (cls.__name__, C.sizeof(cls))
+        for f, _ in cls._fields_:
+            assert getattr(cls, f).offset == want[(cls.__name__, f)], (cls.__name__, f)
