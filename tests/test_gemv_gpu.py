@@ -79,7 +79,7 @@ def _run(torch, m, x, **kw):
 
 
 @pytest.mark.parametrize("fmt", ["nvfp4", "int4_affine", "bf16", "fp8_e4m3"])
-@pytest.mark.parametrize("mtok", [1, 2, 8, 16])
+@pytest.mark.parametrize("mtok", [1, 2, 3, 8, 16])
 @pytest.mark.parametrize("n,k", [(48, 256), (77, 1024), (1040, 2048)])
 def test_gemv_matches_oracle(torch_gpu, fmt, mtok, n, k, rng):
     m = _matrix(fmt, n, k, rng)
