@@ -5,10 +5,12 @@
 //
 // MI355X design: the state columns of a head are independent through the whole step (the Σ over dk stays inside a
 // column), so a workgroup takes one value head's 32-column slice (grid hv × 4: 192 workgroups, enough to spread the
-// 6 MB state stream over the chip), two state waves of 16 columns each plus two waves that compute the conv while
-// the state streams in. Lane (c = l%16, rg = l/16) of a state wave holds
-// S[32·rg .. 32·rg+32][col] in 32 VGPRs for all T tokens; the Σ over dk is 32 FMAs in-lane plus a 4-lane shuffle
-// reduction, so the sequential token loop never touches memory or a barrier. Each workgroup computes the conv,
+// 6 MB state stream over the chip), state waves of SC columns each plus two waves that compute the conv while
+// the state streams in. Lane (c = l%SC, rg = l/SC) of a state wave holds the R = 128·SC/64 rows
+// S[R·rg .. R·rg+R][col] in R VGPRs for all T tokens; the Σ over dk is R FMAs in-lane plus a shuffle reduction over
+// the 64/SC lanes of the column, so the sequential token loop never touches memory or a barrier. One token takes
+// SC = 16 (two state waves, 32 rows per lane); several take SC = 8 (four state waves, 16 rows per lane), halving
+// each wave's serial work per token. Each workgroup computes the conv,
 // SiLU and L2 norms of its key head's q/k (256 channels, repeated per slice: cheap) and of its own 32 v channels.
 // Conv state is read from one buffer and written to another (several value heads read the same key head's
 // channels: the reference solves the same race with two slots by step parity, gdn_mixer.metal:25-37); the
@@ -20,9 +22,11 @@
 namespace {
 
 constexpr int DK = 128, DV = 128, CW = 4, TMAX = 16;
-constexpr int WAVES = 2, COLS = 16;            // per workgroup: 2 state waves of 16 columns …
-constexpr int CONV_WAVES = 2;                  // … and 2 waves that compute the conv while the state streams in
-constexpr int SLICE = WAVES * COLS, NSLICE = DV / SLICE;
+constexpr int SLICE = 32, NSLICE = DV / SLICE; // a workgroup: one value head's 32-column slice, in state waves of
+constexpr int CONV_WAVES = 2;                  // SC columns each, and 2 waves that compute the conv meanwhile
+
+// v(l) + v(l ^ 8) inside a row of 16 lanes (DPP row rotate by 8), the same value in both lanes
+__device__ __forceinline__ float add_xor8(float v) { return v + dpp_f<0x128>(v); }
 
 struct GdnArgs {
   int t, hk, hv;
@@ -58,8 +62,11 @@ __device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : lo
 __device__ __forceinline__ float bf(const uint16_t* p, long long i) { return bf16_bits_to_f32(p[i]); }
 
 // TT: a bound on the tokens (>= a.t), so the conv waves' loads are a fixed, unconditional set
-template <int TT>
-__global__ __launch_bounds__(64 * (WAVES + CONV_WAVES)) void gdn_step(GdnArgs a) {
+// SC: columns per state wave — 16 (two state waves, 32 rows of the column per lane) or 8 (four state waves, 16 rows
+// per lane: half the serial work per token, for launches of several tokens)
+template <int TT, int SC>
+__global__ __launch_bounds__(64 * (SLICE / SC + CONV_WAVES)) void gdn_step(GdnArgs a) {
+  constexpr int WAVES = SLICE / SC, RG = 64 / SC, R = DK / RG;
   __shared__ float qs[TMAX][DK];   // conv → silu → L2-norm (q also /√dk)
   __shared__ float ks[TMAX][DK];
   __shared__ float vs[TMAX][SLICE];
@@ -76,14 +83,14 @@ __global__ __launch_bounds__(64 * (WAVES + CONV_WAVES)) void gdn_step(GdnArgs a)
 
   // ---- waves 0..WAVES-1 load the state slice; the CONV_WAVES after them compute the conv meanwhile (the vector
   // memory counter is per wave, so the conv's loads do not queue behind the state's) ------------------------------
-  const int c = lane & 15, rg = lane >> 4;
-  const int col = sl * SLICE + wave * COLS + c;   // column in the head
-  const int lcol = wave * COLS + c;               // column in the slice
-  float s[32];
+  const int c = lane % SC, rg = lane / SC;
+  const int col = sl * SLICE + wave * SC + c;     // column in the head
+  const int lcol = wave * SC + c;                 // column in the slice
+  float s[R];
   if (wave < WAVES) {
     const float* sin = a.rec_in + (long long)h * DK * DV;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) s[i] = sin[(long long)(32 * rg + i) * DV + col];
+    for (int i = 0; i < R; ++i) s[i] = sin[(long long)(R * rg + i) * DV + col];
   } else {
     // ---- causal conv1d + SiLU over the head's q, k (key head kh) and this slice's v channels: CPT channels per
     // thread. Every load is issued before any is used and none is conditional (a channel index past the last
@@ -158,7 +165,7 @@ __global__ __launch_bounds__(64 * (WAVES + CONV_WAVES)) void gdn_step(GdnArgs a)
   }
   __syncthreads();
 
-  // ---- L2 norms: wave w takes tokens w, w + 4, … -----------------------------------------------------------------
+  // ---- L2 norms: wave w takes tokens w, w + (waves), …--------------------------------------------------------
   for (int t = wave; t < T; t += WAVES + CONV_WAVES) {
     const float q0 = qs[t][lane], q1 = qs[t][lane + 64];
     const float k0 = ks[t][lane], k1 = ks[t][lane + 64];
@@ -172,31 +179,45 @@ __global__ __launch_bounds__(64 * (WAVES + CONV_WAVES)) void gdn_step(GdnArgs a)
   __syncthreads();
   if (wave >= WAVES) return;
 
-  // ---- the recurrence, token by token, state in registers --------------------------------------------------------
-  for (int t = 0; t < T; ++t) {
-    const float e = eg_s[t];
-    const float4* k4 = reinterpret_cast<const float4*>(&ks[t][32 * rg]);
-    const float4* q4 = reinterpret_cast<const float4*>(&qs[t][32 * rg]);
-    float kk[32], qq[32];
+  // ---- the recurrence, token by token, state in registers. The token loop is unrolled over the bound TT and the
+  // next token's k and q are read from LDS while this token computes, so the chain from one token to the next holds
+  // no LDS latency; v, β and e^g of every token are read before the loop ------------------------------------------
+  float vv[TT], bv[TT], ev[TT];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+  for (int t = 0; t < TT; ++t) { vv[t] = vs[t][lcol]; bv[t] = beta_s[t]; ev[t] = eg_s[t]; }
+  float kk[R], qq[R];
+  auto stage = [&](int t, float* kd, float* qd) {
+    const float4* k4 = reinterpret_cast<const float4*>(&ks[t][R * rg]);
+    const float4* q4 = reinterpret_cast<const float4*>(&qs[t][R * rg]);
+#pragma unroll
+    for (int i = 0; i < R / 4; ++i) {
       const float4 kv = k4[i], qv = q4[i];
-      kk[4 * i] = kv.x; kk[4 * i + 1] = kv.y; kk[4 * i + 2] = kv.z; kk[4 * i + 3] = kv.w;
-      qq[4 * i] = qv.x; qq[4 * i + 1] = qv.y; qq[4 * i + 2] = qv.z; qq[4 * i + 3] = qv.w;
+      kd[4 * i] = kv.x; kd[4 * i + 1] = kv.y; kd[4 * i + 2] = kv.z; kd[4 * i + 3] = kv.w;
+      qd[4 * i] = qv.x; qd[4 * i + 1] = qv.y; qd[4 * i + 2] = qv.z; qd[4 * i + 3] = qv.w;
     }
+  };
+  stage(0, kk, qq);
+#pragma unroll
+  for (int t = 0; t < TT; ++t) {
+    if (t >= T) break;
+    float kn[R], qn[R];
+    if (t + 1 < TT) stage(t + 1, kn, qn);   // rows past T hold stale values and are never used
+    const float e = ev[t];
     float m0 = 0.f, m1 = 0.f, m2 = 0.f, m3 = 0.f;
 #pragma unroll
-    for (int i = 0; i < 32; i += 4) {
+    for (int i = 0; i < R; i += 4) {
       s[i] = __fmul_rn(s[i], e); s[i + 1] = __fmul_rn(s[i + 1], e);
       s[i + 2] = __fmul_rn(s[i + 2], e); s[i + 3] = __fmul_rn(s[i + 3], e);
       m0 = fmaf(s[i], kk[i], m0); m1 = fmaf(s[i + 1], kk[i + 1], m1);
       m2 = fmaf(s[i + 2], kk[i + 2], m2); m3 = fmaf(s[i + 3], kk[i + 3], m3);
     }
-    const float kv_mem = quad16_sum((m0 + m1) + (m2 + m3));
-    const float delta = (vs[t][lcol] - kv_mem) * beta_s[t];
+    float kv_part = (m0 + m1) + (m2 + m3);
+    if (SC == 8) kv_part = add_xor8(kv_part);
+    const float kv_mem = quad16_sum(kv_part);
+    const float delta = (vv[t] - kv_mem) * bv[t];
     float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
 #pragma unroll
-    for (int i = 0; i < 32; i += 4) {
+    for (int i = 0; i < R; i += 4) {
       s[i] = __fadd_rn(s[i], __fmul_rn(kk[i], delta));
       s[i + 1] = __fadd_rn(s[i + 1], __fmul_rn(kk[i + 1], delta));
       s[i + 2] = __fadd_rn(s[i + 2], __fmul_rn(kk[i + 2], delta));
@@ -204,12 +225,18 @@ __global__ __launch_bounds__(64 * (WAVES + CONV_WAVES)) void gdn_step(GdnArgs a)
       o0 = fmaf(s[i], qq[i], o0); o1 = fmaf(s[i + 1], qq[i + 1], o1);
       o2 = fmaf(s[i + 2], qq[i + 2], o2); o3 = fmaf(s[i + 3], qq[i + 3], o3);
     }
-    const float o = quad16_sum((o0 + o1) + (o2 + o3));
+    float o_part = (o0 + o1) + (o2 + o3);
+    if (SC == 8) o_part = add_xor8(o_part);
+    const float o = quad16_sum(o_part);
     if (rg == 0 && !a.commit) a.y[(long long)t * a.ldy + h * DV + col] = f32_to_bf16_bits(o);   // the BF16 read-out
+    if (t + 1 < TT) {
+#pragma unroll
+      for (int i = 0; i < R; ++i) { kk[i] = kn[i]; qq[i] = qn[i]; }
+    }
   }
   float* sout = a.rec_out + (long long)h * DK * DV;
 #pragma unroll
-  for (int i = 0; i < 32; ++i) sout[(long long)(32 * rg + i) * DV + col] = s[i];
+  for (int i = 0; i < R; ++i) sout[(long long)(R * rg + i) * DV + col] = s[i];
 }
 
 // gated RMSNorm over each head's dv read-outs, in place: y = bf16(bf16(bf16(w)·bf16(o·r))·silu(z)); one wave per
@@ -255,12 +282,18 @@ extern "C" int mi_gdn_step(const mi_gdn_desc* d, void* stream) {
   a.step = d->step;
   a.conv_slot = (long long)(2 * d->k_heads * d->dk + d->v_heads * d->dv) * (d->conv_width - 1);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(d->v_heads, NSLICE), block(64 * (WAVES + CONV_WAVES));
-  if (d->t == 1) hipLaunchKernelGGL(gdn_step<1>, grid, block, 0, s, a);
-  else if (d->t <= 2) hipLaunchKernelGGL(gdn_step<2>, grid, block, 0, s, a);
-  else if (d->t <= 4) hipLaunchKernelGGL(gdn_step<4>, grid, block, 0, s, a);
-  else if (d->t <= 8) hipLaunchKernelGGL(gdn_step<8>, grid, block, 0, s, a);
-  else hipLaunchKernelGGL(gdn_step<TMAX>, grid, block, 0, s, a);
+  // several tokens: four state waves of 8 columns (MI_GDN_SC=16 keeps two of 16)
+  static const bool narrow_ok = [] { const char* e = getenv("MI_GDN_SC"); return !(e && atoi(e) == 16); }();
+  const dim3 grid(d->v_heads, NSLICE), b16(64 * (SLICE / 16 + CONV_WAVES)), b8(64 * (SLICE / 8 + CONV_WAVES));
+  if (d->t == 1) hipLaunchKernelGGL((gdn_step<1, 16>), grid, b16, 0, s, a);
+  else if (d->t <= 2) hipLaunchKernelGGL((gdn_step<2, 16>), grid, b16, 0, s, a);
+  else if (!narrow_ok) {
+    if (d->t <= 4) hipLaunchKernelGGL((gdn_step<4, 16>), grid, b16, 0, s, a);
+    else if (d->t <= 8) hipLaunchKernelGGL((gdn_step<8, 16>), grid, b16, 0, s, a);
+    else hipLaunchKernelGGL((gdn_step<TMAX, 16>), grid, b16, 0, s, a);
+  } else if (d->t <= 4) hipLaunchKernelGGL((gdn_step<4, 8>), grid, b8, 0, s, a);
+  else if (d->t <= 8) hipLaunchKernelGGL((gdn_step<8, 8>), grid, b8, 0, s, a);
+  else hipLaunchKernelGGL((gdn_step<TMAX, 8>), grid, b8, 0, s, a);
   MI_TRY_HIP(hipGetLastError(), "gdn_step launch");
   if (!d->defer_norm && !d->commit) {
     hipLaunchKernelGGL(gdn_gated_norm, dim3(d->v_heads, d->t), dim3(64), 0, s, a);

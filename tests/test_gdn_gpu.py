@@ -41,7 +41,7 @@ def _check(got, ref, conv_got, conv_ref, rec_got, rec_ref):
 
 
 @pytest.mark.parametrize("hk,hv", [(16, 48), (4, 4), (2, 6)])
-@pytest.mark.parametrize("t", [1, 4, 8])
+@pytest.mark.parametrize("t", [1, 3, 4, 8, 16])
 def test_gdn_step_matches_oracle(torch_gpu, hk, hv, t):
     torch = torch_gpu
     from monolith_mi355 import kernels
