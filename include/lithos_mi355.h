@@ -156,6 +156,9 @@ typedef struct mi_gemv_desc {
   float* route_weights;
   /* grouped mode: at most this many pairs per record (mi_moe_route's pairs_per_record); 0 = up to 16 */
   int32_t group_max_pairs;
+  /* with route_logits: the logits row's width in elements (route_experts <= route_ld; the shared gate's column
+   * route_gate_col < route_ld), so the launch never reads past the row */
+  int32_t route_ld;
 } mi_gemv_desc;
 size_t mi_gemv_workspace_bytes(const mi_gemv_desc* d);   /* 0 when the plan needs none */
 int mi_gemv(const mi_gemv_desc* d, void* stream);
@@ -180,7 +183,8 @@ int mi_gemv_plan(const mi_gemv_desc* d, int32_t out[7]);
  * and starts only after phase i-1 has finished, so it may read any earlier phase's output (as x or residual).
  * workspace: mi_gemv_chain_workspace_bytes, zeroed once before its first use (its counters return to zero after every
  * launch); NULL = the library's own. mi_gemv_chain_error reads the control block's error flag (1: a wait ran past its
- * bound because the grid could not run together; the results are then wrong). */
+ * bound because the grid could not run together; the results are then wrong) and clears it, so each read reports the
+ * launches since the previous read. */
 #define MI_CHAIN_MAX_PHASES 4
 size_t mi_gemv_chain_workspace_bytes(const mi_gemv_desc* phases, int32_t n_phases);
 int mi_gemv_chain(const mi_gemv_desc* phases, int32_t n_phases, void* workspace, size_t workspace_bytes, void* stream);

@@ -496,6 +496,10 @@ extern "C" int mi_gemv_chain_error(const void* workspace, void* stream, uint32_t
   if (!ws && mi_library_scratch(MI_SCRATCH_CHAIN, kCtlBytes, static_cast<hipStream_t>(stream), &ws)) return MI_E_HIP;
   MI_TRY_HIP(hipMemcpyAsync(out, static_cast<char*>(ws) + 4 * (MAX_PHASES + 1), 4, hipMemcpyDeviceToHost,
                             static_cast<hipStream_t>(stream)), "hipMemcpyAsync(chain error)");
+  // reading the flag clears it (the launches re-arm only their phase counters), so a later read reports later
+  // launches only; this call synchronizes its stream, so it is never part of a captured graph
+  MI_TRY_HIP(hipMemsetAsync(static_cast<char*>(ws) + 4 * (MAX_PHASES + 1), 0, 4, static_cast<hipStream_t>(stream)),
+             "hipMemsetAsync(chain error)");
   MI_TRY_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)), "hipStreamSynchronize");
   return MI_OK;
 }

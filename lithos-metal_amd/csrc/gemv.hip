@@ -1747,9 +1747,13 @@ int check_desc(const mi_gemv_desc* d) {
     MI_REQUIRE(d->groups && d->m == 1 && d->route_experts >= 1 && d->route_experts <= 64 * ROUTE_MAX_PER_LANE &&
                    d->route_top_k >= 1 && d->route_top_k <= ROUTE_MAX_K && d->route_top_k <= d->route_experts &&
                    d->top_k == ks && d->max_groups == ks && d->route_ids && d->route_weights &&
-                   (d->shared_expert <= 0 || (d->shared_expert >= d->route_experts && d->route_gate_col >= 0)),
+                   d->route_ld >= d->route_experts &&
+                   (d->shared_expert <= 0 || (d->shared_expert >= d->route_experts &&
+                                              d->shared_expert <= 64 * ROUTE_MAX_PER_LANE && d->route_gate_col >= 0 &&
+                                              d->route_gate_col < d->route_ld)),
                "mi_gemv: routing in the launch needs one token, groups = slots = route_top_k (+1 with the shared "
-               "expert), 1..512 experts, top_k <= 16 and the route outputs");
+               "expert, index <= 512, its gate column inside the route_ld-wide logits row), 1..512 experts, "
+               "top_k <= 16 and the route outputs");
   }
   MI_REQUIRE(((uintptr_t)d->x & 15) == 0 && d->ldx % 8 == 0, "mi_gemv: x must be 16-byte aligned with ldx %% 8 == 0");
   MI_REQUIRE(((uintptr_t)d->w & 15) == 0, "mi_gemv: weight pack must be 16-byte aligned");

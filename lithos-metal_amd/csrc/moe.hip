@@ -68,8 +68,9 @@ __global__ __launch_bounds__(64 * MAX_T) void moe_route(RouteArgs a) {
   // of them. The expert's first record is the scan, over the pairs in order, of the records each expert's first
   // pair opens (a wave scan, then the waves' totals) — no pass over the pairs.
   constexpr int PW = (MAX_T * (MAX_K + 1) + 31) / 32;     // words of a pair mask
-  __shared__ int first_use[64 * MAX_PER_LANE];
-  __shared__ uint32_t pmask[64 * MAX_PER_LANE][PW];
+  // indexed by expert id: the routed experts (< 512) and the shared expert (<= 512, checked on the host)
+  __shared__ int first_use[64 * MAX_PER_LANE + 1];
+  __shared__ uint32_t pmask[64 * MAX_PER_LANE + 1][PW];
   __shared__ int pre[64 * MAX_T];                   // the records opened before each pair
   __shared__ int wtot[MAX_T];
   const int PR = a.pairs_per_record > 0 ? a.pairs_per_record : GROUP_REC - 2;
@@ -190,9 +191,10 @@ extern "C" int mi_moe_route(const mi_moe_route_desc* d, void* stream) {
              d->top_k);
   MI_REQUIRE(d->logits && d->ids && d->weights && d->ld_logits >= d->n_experts, "mi_moe_route: bad logits / outputs");
   const int sh = d->shared_expert > 0 ? 1 : 0;
-  MI_REQUIRE(!sh || (d->shared_expert >= d->n_experts && d->shared_gate_col >= 0 && d->shared_gate_col < d->ld_logits),
-             "mi_moe_route: the shared expert's index must follow the routed experts and its gate column lie in the "
-             "logits row");
+  MI_REQUIRE(!sh || (d->shared_expert >= d->n_experts && d->shared_expert <= 64 * MAX_PER_LANE &&
+                     d->shared_gate_col >= 0 && d->shared_gate_col < d->ld_logits),
+             "mi_moe_route: the shared expert's index must follow the routed experts (at most %d) and its gate column "
+             "lie in the logits row", 64 * MAX_PER_LANE);
   MI_REQUIRE(d->pairs_per_record >= 0 && d->pairs_per_record <= GROUP_REC - 2,
              "mi_moe_route: pairs_per_record=%d must be in 0..%d", d->pairs_per_record, GROUP_REC - 2);
   MI_REQUIRE(!d->groups || d->max_groups >= (d->pairs_per_record > 0 ? d->t * (d->top_k + sh)

@@ -79,7 +79,8 @@ def _gemv_common(ctx: EmitContext, op: Op, *, out_f32: bool = False, grouped: bo
         route = a.get("route")
         if route is not None:                       # one token: the launch routes for itself
             scalars.update(route_experts=route["logits"].shape[1], route_top_k=route["top_k"],
-                           route_renorm=int(route.get("renorm", True)), route_gate_col=route.get("gate_col", 0))
+                           route_renorm=int(route.get("renorm", True)), route_gate_col=route.get("gate_col", 0),
+                           route_ld=route["logits"].row_stride)
             ptrs.update(route_logits=route["logits"], route_ids=route["ids"], route_weights=route["weights"])
     probe = _probe(hip.MiGemvDesc, scalars, [f for f, v in ptrs.items() if v is not None])
     need = int(hip.load().mi_gemv_workspace_bytes(C.byref(probe)))

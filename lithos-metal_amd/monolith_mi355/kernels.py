@@ -401,7 +401,7 @@ def moe_route(logits, top_k: int, *, renorm: bool = True, groups: bool = True, o
     t, e = logits.shape
     dev = logits.device
     sh = 1 if shared_expert > 0 else 0
-    if sh and (shared_gate is None or shared_expert < e or not 0 <= shared_gate < logits.stride(0)):
+    if sh and (shared_gate is None or not e <= shared_expert <= 512 or not 0 <= shared_gate < logits.stride(0)):
         raise ValueError("moe_route: the shared expert follows the routed ones and its gate column lies in the row")
     ks = top_k + sh
     if not 0 <= pairs_per_record <= GROUP_REC - 2:
@@ -466,7 +466,7 @@ def moe_gemv(w: PackedWeight, x, groups, *, tokens: int, top_k: int, x_per_slot:
             raise ValueError("moe_gemv: routing in the launch takes one token's bf16 logits row [1, E]")
         d.route_logits, d.route_experts = hip.ptr(lg), lg.shape[1]
         d.route_top_k, d.route_renorm = route["top_k"], int(route.get("renorm", True))
-        d.route_gate_col = route.get("gate_col", 0)
+        d.route_gate_col, d.route_ld = route.get("gate_col", 0), lg.stride(0)
         d.route_ids, d.route_weights = hip.ptr(route["ids"]), hip.ptr(route["weights"])
     hip.call("mi_gemv", C.byref(d), hip.stream_handle(stream))
     return out

@@ -38,7 +38,7 @@ class MiGemvDesc(C.Structure):
                 ("shared_expert", C.c_int32), ("shared_epilogue", C.c_int32), ("route_logits", C.c_void_p),
                 ("route_experts", C.c_int32), ("route_top_k", C.c_int32), ("route_renorm", C.c_int32),
                 ("route_gate_col", C.c_int32), ("route_ids", C.c_void_p), ("route_weights", C.c_void_p),
-                ("group_max_pairs", C.c_int32)]
+                ("group_max_pairs", C.c_int32), ("route_ld", C.c_int32)]
 
 
 class MiGdnDesc(C.Structure):

@@ -8,8 +8,13 @@ gate|up and down GEMVs) against the oracle fed the device's own input to that st
 relative / 1e-3 absolute — the attention core within its kernel test's bar; and the whole
 layer end to end from the oracle's own chain with the reference's composite layer bar
 (``tests/kernels/test_gqa_decode.py:347``: cosine > 0.9999, max |error| ≤ 1e-2 of the output's largest magnitude),
-on the output and on the GDN recurrent state: end to end, each GEMV's BF16 rounding can flip against the oracle's and
-the flip propagates, so that fraction is printed, not asserted element-wise."""
+on the output and on the GDN recurrent state. End to end, each GEMV's BF16 rounding can flip against the oracle's and
+the flip propagates (the stage bars show each kernel is within tolerance of the oracle on its own input), so the
+element-wise fraction outside 1e-2 / 1e-3 is bounded by a per-case ceiling about 1.5x the worst measured on MI355X
+(``E2E_CEILING``) rather than asserted at zero: the layers are deterministic, so a regression in any stage shows
+up as a fraction above it. Measured worst (of two steps, both M): GDN small 0.01 %, GDN 27B 5.4 %, attention small
+0.9 %, attention 27B 13.4 % (its output sums an MLP of K = 17408 over an attention output of ~1/sqrt(4000) scale,
+so its ULP flips move the most elements past 1e-2 of a small reference value); the recurrent state 0."""
 
 import numpy as np
 import pytest
@@ -22,6 +27,9 @@ from oracle.gates import check_against_oracle, tolerance_violations
 
 pytestmark = pytest.mark.gpu
 EPS = 1e-6
+# end-to-end element-wise ceiling per (mixer, geometry): about 1.5x the worst fraction measured on MI355X
+E2E_CEILING = {("gdn", "small"): 0.005, ("gdn", "27b"): 0.08, ("attn", "small"): 0.015, ("attn", "27b"): 0.20,
+               ("state", "small"): 0.0, ("state", "27b"): 0.0}
 
 
 def _deq(q):
@@ -37,16 +45,17 @@ def _deq_gate_up(q):
     return out
 
 
-def _bar(got, ref, what):
-    """The end-to-end layer bar: cosine and max error norm-wise (the reference's layer bar); the element-wise
-    fraction outside 1e-2 / 1e-3 is printed — each GEMV's BF16 rounding can flip against the oracle's, and a flip
-    moves every later stage by up to an ULP, so element-wise exactness is asserted per stage (``_stage``)."""
+def _bar(got, ref, what, ceiling):
+    """The end-to-end layer bar: cosine and max error norm-wise (the reference's layer bar), and the element-wise
+    fraction outside 1e-2 / 1e-3 at most ``ceiling`` — each GEMV's BF16 rounding can flip against the oracle's, and
+    a flip moves every later stage by up to an ULP, so element-wise exactness is asserted per stage (``_stage``)."""
     g, r = got.astype(np.float64).ravel(), ref.astype(np.float64).ravel()
     cos = float(g @ r / (np.linalg.norm(g) * np.linalg.norm(r) + 1e-30))
     err, scale = float(np.abs(g - r).max()), float(np.abs(r).max())
     assert cos > 0.9999 and err <= 1e-2 * scale, (what, cos, err, scale)
-    print(f"  {what} end to end: {tolerance_violations(g, r)} of {g.size} outside 1e-2/1e-3 (cos {cos:.7f})",
-          flush=True)
+    bad = tolerance_violations(g, r)
+    print(f"  {what} end to end: {bad} of {g.size} outside 1e-2/1e-3 (cos {cos:.7f})", flush=True)
+    assert bad <= ceiling * g.size, (what, bad, g.size, ceiling)
 
 
 def _stage(got, ref, what):
@@ -107,8 +116,8 @@ def test_gdn_decoder_layer(torch_gpu, geom, m):
         proj = ON.linear(xn, w_in)
         o, conv, rec = ON.gdn_mix(proj, conv, rec, **gdn_kw)
         h1 = ON.linear(o, w_out, epilogue="residual", residual=h)
-        _bar(got, _mlp(h1, ex), "layer output")
-        _bar(layer.rec_state.cpu().numpy(), rec, "recurrent state")
+        _bar(got, _mlp(h1, ex), "layer output", E2E_CEILING[("gdn", geom)])
+        _bar(layer.rec_state.cpu().numpy(), rec, "recurrent state", E2E_CEILING[("state", geom)])
 
 
 @pytest.mark.parametrize("geom,ctx,pos", [("small", 1024, 300), ("27b", 4096, 4000)])
@@ -138,13 +147,15 @@ def test_attention_decoder_layer(torch_gpu, geom, ctx, pos, m):
         _stage(proj_d, ON.linear(xn, w_qkv), "qkv proj (norm fused)")
         o_ref = ON.gqa_mix(proj_d, dev["k_codes"].transpose(1, 0, 2).copy(), dev["k_scales"].T.copy(),
                            dev["v_codes"].transpose(1, 0, 2).copy(), dev["v_scales"].T.copy(), pos, **cfg)
-        bad = tolerance_violations(o_dev, o_ref)        # attention's own bar is the kernel test's (test_gqa_gpu)
+        # the kernel test's bar: none outside at a long cache (4K), at most 0.5 % over a few hundred keys (an output
+        # formed by a few cancelling keys carries P's rounding before normalisation against the oracle's after)
+        bad = tolerance_violations(o_dev, o_ref)
         print(f"  attention core: {bad} of {o_dev.size} outside 1e-2/1e-3", flush=True)
-        assert bad <= 0.005 * o_dev.size, bad
+        assert bad <= (0 if geom == "27b" else 0.005 * o_dev.size), bad     # 27b: 4000+ keys
         _stage(h1_dev, ON.linear(o_dev, w_o, epilogue="residual", residual=h), "o_proj + residual")
         _mlp_stages(layer, m, h1_dev, ex)
         proj = ON.linear(xn, w_qkv)
         o = ON.gqa_mix(proj, kc, ks, vc, vs, pos, **cfg)
         h1 = ON.linear(o, w_o, epilogue="residual", residual=h)
-        _bar(got, _mlp(h1, ex), "layer output")
+        _bar(got, _mlp(h1, ex), "layer output", E2E_CEILING[("attn", geom)])
         pos += m

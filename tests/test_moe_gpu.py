@@ -76,6 +76,36 @@ def test_moe_route_tied_logits_and_underflow(torch_gpu):
     assert list(ids.cpu().numpy()[1, :4]) == [2, 9, 0, 1]
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("t", [1, 8, 16])
+def test_moe_route_512_experts_with_the_shared_expert_last(torch_gpu, t):
+    """The largest expert table (512) with the shared expert at index 512: ids and weights match the oracle, the
+    shared slot carries bf16(σ(gate logit)), and the groups cover every pair once — the grouping's per-expert LDS
+    tables hold index 512 (one past the routed experts)."""
+    from monolith_mi355 import kernels
+    torch = torch_gpu
+    rng = np.random.default_rng(512 + t)
+    e, k = 512, 8
+    logits = rbf(rng.standard_normal((t, e + 1)) * 2)        # column 512: the shared expert's gate logit
+    for ppr in (0, 2):
+        ids, w, groups = kernels.moe_route(to_dev_bf16(torch, logits)[:, :e], k, renorm=True, shared_expert=e,
+                                           shared_gate=e, pairs_per_record=ppr)
+        ref_ids, ref_w = ON.moe_route(logits[:, :e], k, True)
+        got_ids, got_w = ids.cpu().numpy(), w.cpu().numpy()
+        assert np.array_equal(got_ids[:, :k], ref_ids)
+        assert np.all(got_ids[:, k] == e)
+        assert np.allclose(got_w[:, :k], ref_w, rtol=0, atol=2 ** -8 * ref_w.max())
+        sg = 1.0 / (1.0 + np.exp(-logits[:, e].astype(np.float64)))
+        assert np.array_equal(got_w[:, k], rbf(got_w[:, k])) and np.all(np.abs(got_w[:, k] - sg) <= 2 ** -8)
+        g = groups.cpu().numpy()
+        seen = sorted(int(p) for rec in g if rec[1] > 0 for p in rec[2: 2 + rec[1]])
+        assert seen == list(range(t * (k + 1)))
+        for rec in g:
+            for p in rec[2: 2 + rec[1]]:
+                assert got_ids[p // (k + 1), p % (k + 1)] == rec[0]
+        assert sum(int(rec[1]) for rec in g if rec[0] == e) == t
+
+
 def _experts(rng, n_exp, inter, hidden):
     """Per expert: gate|up slab (chunk-interleaved by 8, per-row tensor scales) and down, plus their exact
     dequantized float32 matrices ([gate; up] un-interleaved)."""
@@ -297,7 +327,8 @@ class _LazyExperts:
 def test_moe_block_layer(torch_gpu, t, n_exp):
     """layers.MoeBlock (the bench's MoE workload; 256 experts is C5) against the oracle's SparseMoE forward, with its
     own weights dequantized bit-exactly on the device (gate|up rows un-interleaved): route ids equal — from the
-    device's router logits and, where those equal the oracle's router GEMV bit for bit, from the oracle's — output
+    device's router logits, where those equal the oracle's router GEMV bit for bit from the oracle's, and on every
+    row from the oracle's router logits routed by the device — output
     within the bars (``ok_rounded`` and 1e-2 relative / 1e-3 absolute element-wise)."""
     torch = torch_gpu
     from monolith_mi355 import kernels
@@ -344,6 +375,9 @@ def test_moe_block_layer(torch_gpu, t, n_exp):
     oracle_ids, _ = ON.moe_route(rbf(ref_logits), 8, True)
     assert np.array_equal(ids[same], oracle_ids[same])         # end to end from the oracle's own router GEMV
     print(f"  router rows bit-identical to the oracle's: {int(same.sum())} of {t}", flush=True)
+    # every row, whatever the GEMV's last-ulp agreement: the oracle's own router logits routed by the device
+    dev_ids, _, _ = kernels.moe_route(to_dev_bf16(torch, rbf(ref_logits)), 8, renorm=True)
+    assert np.array_equal(dev_ids.cpu().numpy(), oracle_ids)
     chk = check_against_oracle(y, ref)
     assert chk.ok_rounded() and chk.within, chk
 
