@@ -239,8 +239,8 @@ typedef struct mi_gdn_desc {
   int32_t defer_norm;        /* 1: y gets the BF16 read-out o and the gated RMSNorm is left to the consumer (the
                                 output projection's mi_gemv, gnorm_* fields); 0: y is the normed, gated output */
   int32_t commit;            /* 1: the speculative commit pass (ops/gdn.py `gdn_commit`, gdn_mixer.metal:331-347):
-                                replay the committed tokens from the step's input state (rec_in != rec_out) into the
-                                output slot; no read-out (y may be NULL) */
+                                replay the committed tokens from the step's input state rec_in into rec_out (the same
+                                slot, in place, or another); no read-out (y may be NULL) */
   const int32_t* t_dev;      /* device-resident token count 0..t (the accept scan's committed count), or NULL = t */
   const uint32_t* done;      /* a step program's mi_step_state.done, or NULL: once it is set the step takes no token —
                                 conv_out and rec_out receive conv_in and rec_in unchanged (so a graph's fixed ping-pong
@@ -284,6 +284,11 @@ typedef struct mi_gqa_desc {
   const uint32_t* done;      /* a step program's mi_step_state.done, or NULL: once it is set nothing is appended to
                                 the cache and y is not written (gqa_decode.metal:53,239 return at done) */
   int32_t kv_dtype;          /* MI_KV_INT8 (0) or MI_KV_BF16 (1) */
+  /* the reference's packed projection (nn/attention.py:52-64, 133-155): proj holds q | k | v (q heads·D columns)
+   * and the gate rows come from their own buffer [T][ld_gate] (the sibling GEMV's output); NULL = the checkpoint
+   * order above. The RoPE head-dim permutation of that layout is rotary_dim = head_dim with the permuted tables. */
+  const uint16_t* gate_src;
+  int32_t ld_gate;
 } mi_gqa_desc;
 size_t mi_gqa_workspace_bytes(const mi_gqa_desc* d);
 int mi_gqa_decode(const mi_gqa_desc* d, void* stream);
@@ -375,6 +380,8 @@ typedef struct mi_embed_desc {
   const uint16_t* table;
   uint16_t* out;
   int32_t ldo;
+  int32_t t16;                /* 1: table is a BF16 T16 weight slab (the pack's embedding, nn/embedding.py:31-37's
+                                 `packed`): a row is gathered from its tile's 32-column chunks; 0: row-major */
 } mi_embed_desc;
 int mi_embed(const mi_embed_desc* d, void* stream);
 

@@ -269,8 +269,8 @@ extern "C" int mi_gdn_step(const mi_gdn_desc* d, void* stream) {
   MI_REQUIRE(d->step ? !d->conv_out : d->conv_in != d->conv_out,
              "mi_gdn_step: conv_in and conv_out must be distinct buffers (shared key heads); with step, conv_in holds "
              "both slots and conv_out is NULL");
-  MI_REQUIRE(!d->commit || d->rec_in != d->rec_out, "mi_gdn_step: the commit pass replays from the step's input state: "
-             "rec_in and rec_out must be distinct");
+  // rec_in and rec_out may alias, in the commit pass too: each workgroup holds its state columns in registers from
+  // the first load to the last store, and no other workgroup reads them
   GdnArgs a{};
   a.t = d->t; a.hk = d->k_heads; a.hv = d->v_heads;
   a.proj = d->proj; a.ldp = d->ld_proj; a.z_off = d->z_off; a.q_off = d->q_off; a.k_off = d->k_off; a.v_off = d->v_off;

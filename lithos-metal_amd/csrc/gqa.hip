@@ -44,6 +44,7 @@ struct GqaArgs {
   int n_groups, group_len;                      // decode workgroups per KV head, keys per workgroup
   int xcd_tiles;                                // > 1: row tiles over workgroups in the XCD-grouped 1-D grid
   const uint16_t* proj; int ldp;
+  const uint16_t* gsrc; int ldg;                // the gate rows in their own buffer (proj then holds q|k|v), or null
   const uint16_t* cosb; const uint16_t* sinb;   // [ctx][rot] BF16
   const float* q_norm; const float* k_norm;     // (1 + w), [D]
   float eps, scaling;
@@ -194,7 +195,7 @@ __global__ __launch_bounds__(64) void gqa_prep(GqaArgs a) {
   __shared__ float tmp[DH];
   const int lane = threadIdx.x, x = blockIdx.x, t = blockIdx.y;
   if (stopped(a)) return;
-  const int q_cols = a.gate ? 2 * DH : DH;
+  const int q_cols = a.gate && !a.gsrc ? 2 * DH : DH;
   const uint16_t* row = a.proj + (long long)t * a.ldp;
   const int pos = cur_pos(a);
   // a device position past the cache (a stopped program's queued steps) must not read past the RoPE tables
@@ -642,7 +643,8 @@ __global__ __launch_bounds__(64 * MW) void gqa_merge(GqaArgs a) {
   const int row = t * a.rep + (h - j * a.rep);
   const long long b0 = (long long)j * a.n_groups * a.rows + row;      // partial g at b0 + g·rows
   // the gate first (an independent load; without a gate the row's first values are read and unused)
-  const uint16_t* gp = a.proj + (long long)t * a.ldp + (a.gate ? h * 2 * DH + DH : 0);
+  const uint16_t* gp = a.gsrc ? a.gsrc + (long long)t * a.ldg + h * DH
+                              : a.proj + (long long)t * a.ldp + (a.gate ? h * 2 * DH + DH : 0);
   float gv[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) gv[u] = bfv(gp, lane + 64 * u);
@@ -810,6 +812,8 @@ extern "C" int mi_gqa_decode(const mi_gqa_desc* d, void* stream) {
   MI_REQUIRE(d->rotary_dim == 0 || (d->rope_cos && d->rope_sin), "mi_gqa_decode: RoPE tables missing");
   MI_REQUIRE(!d->qk_norm || (d->q_norm && d->k_norm), "mi_gqa_decode: qk_norm needs q_norm and k_norm");
   MI_REQUIRE(((uintptr_t)d->k_codes & 15) == 0 && ((uintptr_t)d->v_codes & 15) == 0, "mi_gqa_decode: cache alignment");
+  MI_REQUIRE(!d->gate_src || (d->gate && d->ld_gate >= d->heads * d->head_dim),
+             "mi_gqa_decode: gate_src needs gate = 1 and ld_gate >= heads·head_dim");
   GqaArgs a{};
   a.t = d->t; a.heads = d->heads; a.kv = d->kv_heads; a.d = d->head_dim; a.rot = d->rotary_dim; a.pos = d->pos;
   a.ctx = d->ctx_max; a.gate = d->gate; a.qk_norm = d->qk_norm; a.rep = rep; a.rows = rows;
@@ -819,7 +823,7 @@ extern "C" int mi_gqa_decode(const mi_gqa_desc* d, void* stream) {
   a.done = d->done;
   a.n_groups = pl.n_groups;
   a.group_len = pl.group_len;
-  a.proj = d->proj; a.ldp = d->ld_proj; a.cosb = d->rope_cos; a.sinb = d->rope_sin;
+  a.proj = d->proj; a.ldp = d->ld_proj; a.gsrc = d->gate_src; a.ldg = d->ld_gate; a.cosb = d->rope_cos; a.sinb = d->rope_sin;
   a.q_norm = d->q_norm; a.k_norm = d->k_norm; a.eps = d->eps; a.scaling = d->scaling;
   a.kc = d->k_codes; a.vc = d->v_codes;
   a.ks = bf ? nullptr : d->k_scales;

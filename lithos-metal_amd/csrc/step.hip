@@ -24,7 +24,11 @@ __global__ __launch_bounds__(EMBED_THREADS) void embed_rows(mi_embed_desc d) {
   if (col >= d.hidden) return;
   const int tok = d.tokens[i];
   const long long row = (tok >= 0 && tok < d.vocab) ? tok : 0;
-  const uint4 v = *reinterpret_cast<const uint4*>(d.table + row * d.hidden + col);
+  // T16 BF16 slab: tile = 16 rows × (hidden / 32) chunks of 512 elements; inside a chunk, column group q (8 columns)
+  // of row r sits at q·128 + r·8
+  const long long at = d.t16 ? ((row >> 4) * (d.hidden >> 5) + (col >> 5)) * 512 + ((col >> 3) & 3) * 128 + (row & 15) * 8
+                             : row * d.hidden + col;
+  const uint4 v = *reinterpret_cast<const uint4*>(d.table + at);
   *reinterpret_cast<uint4*>(d.out + (long long)i * d.ldo + col) = v;
 }
 
@@ -558,6 +562,7 @@ int mi_embed(const mi_embed_desc* d, void* stream) {
   MI_REQUIRE(d->t >= 1 && d->t <= 16 && d->vocab > 0 && d->hidden > 0 && d->hidden % 8 == 0 && d->ldo >= d->hidden &&
              d->ldo % 8 == 0, "mi_embed: bad shape");
   MI_REQUIRE(((uintptr_t)d->table & 15) == 0 && ((uintptr_t)d->out & 15) == 0, "mi_embed: table / out alignment");
+  MI_REQUIRE(!d->t16 || d->hidden % 32 == 0, "mi_embed: a T16 table needs hidden %% 32 == 0");
   const dim3 grid((d->hidden / 8 + EMBED_THREADS - 1) / EMBED_THREADS, d->t);
   hipLaunchKernelGGL(embed_rows, grid, dim3(EMBED_THREADS), 0, static_cast<hipStream_t>(stream), *d);
   MI_TRY_HIP(hipGetLastError(), "embed launch");

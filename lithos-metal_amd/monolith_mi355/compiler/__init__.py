@@ -1,13 +1,15 @@
-"""The compiler side of the operator API for gfx950: an op graph (``ir``), the backend with its extension points and
-the handler context (``context``), one handler per op kind on the library's entry points (``handlers``), lowering of
-this package's decode layers (``lower``) and emission into the ``program.json`` format (``emit``)."""
+"""The compiler side of the operator API for gfx950: ``emit_program`` / ``compile_program`` take a step graph in the
+reference's op contract (``monolith_mi355.core``; built by ``monolith_mi355.nn`` or by the reference's own modules)
+and a pack, run the backend's fusion passes (``plan``) and emit a ``program.json`` program of library calls through
+one handler per op kind (``handlers``); ``lower`` bridges the hand-built ``layers.DecoderModel`` into those terms."""
 
 from .context import EmitContext, Gfx950Backend, Profile, current_backend, dispatch, get_backend, register_backend, using_backend
-from .emit import compile_program, emit_program, shared_emit
+from .emit import compile_program, emit_program, lower_round, shared_emit
 from .handlers import HANDLERS
-from .ir import Graph, Op, Value, Weight
-from .lower import lower_decoder, lower_layer
+from .lower import compile_decoder, describe, load_states, state_images, write_pack
+from .plan import PASSES, Plan, run_passes
 
 __all__ = ["EmitContext", "Gfx950Backend", "Profile", "current_backend", "dispatch", "get_backend",
-           "register_backend", "using_backend", "compile_program", "emit_program", "shared_emit", "HANDLERS", "Graph",
-           "Op", "Value", "Weight", "lower_decoder", "lower_layer"]
+           "register_backend", "using_backend", "compile_program", "emit_program", "lower_round", "shared_emit",
+           "HANDLERS", "compile_decoder", "describe", "load_states", "state_images", "write_pack", "PASSES", "Plan",
+           "run_passes"]

@@ -28,20 +28,27 @@ from inspect import signature
 from typing import Any, Dict, List, Optional, Sequence, Tuple
 
 from ..runtime.program import BufferSpec, KernelSpec, OpSpec, Program, StepStateLayout
-from .ir import Value
 
 STATE_LAYOUT = (16, 15)                     # mi_step_state: StepStateLayout(t_max=16, gamma_max=15)
 
 
 @dataclass
 class Profile:
-    """What a compile targets: the backend, the token ring, the stop rules."""
+    """What a compile targets (the reference's ``ChipConfig`` as far as emission reads it): the backend, the op
+    registry's binding key, the token ring, the stop rules, and the KV cache the attention ops keep (``"bf16"``,
+    the reference's, or ``"int8"`` with per-token scales in state buffers of their own)."""
 
     backend: str = "gfx950"
     ring_capacity: int = 4096
     ctx_cap: int = 0                        # positions a sequence may occupy (0: unbounded)
     eos: Tuple[int, ...] = ()
+    kv_cache: str = "bf16"
+    name: str = "MI355X"
     extra: Dict[str, Any] = field(default_factory=dict)
+
+    @property
+    def key(self) -> str:
+        return "gfx950"
 
     @property
     def fingerprint(self) -> str:
@@ -121,19 +128,31 @@ def dispatch(entry: str):
     return wrap
 
 
-class EmitContext:
-    """The program under construction and where each value lives in it."""
+WINDOW_BYTES = 2 << 30          # a file window of the pack is at most 2 GiB (``compiler/emit.py:38``)
 
-    def __init__(self, profile: Profile, t: int = 1) -> None:
-        self.profile, self.t = profile, t
-        self.layout = StepStateLayout(*STATE_LAYOUT)
-        self.program = Program(kernels={}, buffers={}, ops=[], ring_capacity=profile.ring_capacity,
-                               layout=self.layout, context_capacity=profile.ctx_cap)
+
+class EmitContext:
+    """The program under construction (``compiler/emit.py:97-205``'s ``_Ctx``): where each value of the plan lives —
+    pack windows for weights and constants, the step state for inputs named after its fields, program buffers for
+    states (role ``state``) and activations (role ``arena``); aliases and row views as offsets into their base."""
+
+    def __init__(self, profile: Profile, plan, packs: Sequence[Any] = (), *, layout: Optional[StepStateLayout] = None,
+                 ring_capacity: Optional[int] = None, ctx_cap: Optional[int] = None) -> None:
+        self.profile, self.plan, self.t = profile, plan, plan.t
+        self.layout = layout or StepStateLayout(*STATE_LAYOUT)
+        if (self.layout.t_max, self.layout.gamma_max) != STATE_LAYOUT:
+            raise ValueError(f"the gfx950 step state is StepStateLayout{STATE_LAYOUT} (mi_step_state)")
+        ring = profile.ring_capacity if ring_capacity is None else ring_capacity
+        self.program = Program(kernels={}, buffers={}, ops=[], ring_capacity=ring, layout=self.layout,
+                               context_capacity=profile.ctx_cap if ctx_cap is None else ctx_cap)
         self.program.buffers[self.program.step_state] = BufferSpec(self.layout.size, None, "step_state")
-        self.program.buffers[self.program.ring] = BufferSpec(8 * profile.ring_capacity, None, "ring")
-        self.bound: Dict[str, Any] = {}      # buffer name -> the tensor whose storage it is (handed to Engine)
-        self._by_storage: Dict[int, str] = {}
-        self._by_value: Dict[int, str] = {}
+        self.program.buffers[self.program.ring] = BufferSpec(8 * ring, None, "ring")
+        self.packs = list(packs)
+        self.slabs: Dict[str, dict] = {}
+        self.aux: Dict[str, dict] = {}
+        self.windows: Dict[str, Tuple[str, int]] = {}       # slab / aux name -> (buffer, offset)
+        self.row_scales: Dict[str, Tuple[str, int]] = {}
+        self._map_packs()
         self._shared: Dict[str, str] = {}
         self.counter = 0
 
@@ -141,33 +160,90 @@ class EmitContext:
         self.counter += 1
         return f"{stem}.{self.counter}"
 
+    # ---- the pack ----------------------------------------------------------------------------------------------
+    def _map_packs(self) -> None:
+        """Each pack's slabs, row-scale tables and aux entries grouped into page-aligned file windows of at most
+        2 GiB, in file order (``compiler/emit.py:220-256``)."""
+        n_win = 0
+        for pk in self.packs:
+            man = pk.manifest
+            path = str(pk.dir / man["pack"])
+            align, file_bytes = int(man.get("alignment", 4096)), int(man["nbytes"])
+            entries = []
+            for s in man["slabs"]:
+                if s["name"] in self.slabs:
+                    raise ValueError(f"emit: two packs hold a slab named {s['name']!r}")
+                self.slabs[s["name"]] = s
+                entries.append((s["offset"], s["nbytes"], "slab", s["name"]))
+                if s.get("row_scales_offset") is not None:
+                    entries.append((s["row_scales_offset"], 4 * s["row_scales_len"], "rs", s["name"]))
+            for a in man["aux"]:
+                if a["name"] in self.aux:
+                    raise ValueError(f"emit: two packs hold an entry named {a['name']!r}")
+                self.aux[a["name"]] = a
+                entries.append((a["offset"], a["nbytes"], "aux", a["name"]))
+            entries.sort()
+            windows, start, end, members = [], None, 0, []
+            for off, nb, kind, name in entries:
+                if start is None or off + nb - start > WINDOW_BYTES:
+                    if start is not None:
+                        windows.append((start, end, members))
+                    start, end, members = off - off % align, off + nb, []
+                end = max(end, off + nb)
+                members.append((off, kind, name))
+            if start is not None:
+                windows.append((start, end, members))
+            for start, end, members in windows:
+                bname = f"pack.{n_win}"
+                n_win += 1
+                end = min(-(-end // align) * align, file_bytes)
+                self.program.buffers[bname] = BufferSpec(end - start, None, "weights", path, start)
+                for off, kind, name in members:
+                    (self.row_scales if kind == "rs" else self.windows)[name] = (bname, off - start)
+
+    def slab(self, name: str) -> dict:
+        try:
+            return self.slabs[name]
+        except KeyError:
+            raise KeyError(f"emit: no pack holds the slab {name!r}") from None
+
     # ---- where values live -------------------------------------------------------------------------------------
-    def buf(self, v: Optional[Value]) -> Optional[Tuple[str, int]]:
-        """``(buffer name, byte offset)`` of a value: its step-state field, the storage of its bound tensor, or a
-        buffer the program allocates."""
-        if v is None:
-            return None
-        if v.base is not None:
-            name, off = self.buf(v.base)
-            return name, off + v.offset
-        if v.role == "step_state":
-            return self.program.step_state, self.layout.offset(v.field) + v.offset
-        if v.tensor is not None:
-            st = v.tensor.untyped_storage()
-            base = st.data_ptr()
-            name = self._by_storage.get(base)
-            if name is None:
-                name = self._name(f"{v.role}.{v.name}")
-                self._by_storage[base] = name
-                self.program.buffers[name] = BufferSpec(st.nbytes(), None, v.role)
-                self.bound[name] = v.tensor
-            return name, v.tensor.data_ptr() - base + v.offset
-        name = self._by_value.get(id(v))
-        if name is None:
-            name = self._name(f"{v.role}.{v.name}")
-            self._by_value[id(v)] = name
-            self.program.buffers[name] = BufferSpec(max(v.nbytes, 16), None, v.role)
-        return name, v.offset
+    def buf(self, v) -> Optional[Tuple[str, int]]:
+        """``(buffer name, byte offset)`` of a plan value (or an explicit ``(buffer, offset)`` pair)."""
+        if v is None or isinstance(v, tuple):
+            return v
+        p = self.plan
+        if v.name in p.alias:
+            root, col = p.root(v)
+            bname, off = self.buf(p.values[root])
+            return bname, off + col * _itemsize(p.values[root])
+        if getattr(v, "view_of", None) is not None:
+            base_name, row = v.view_of
+            base = p.values[base_name]
+            bname, off = self.buf(base)
+            return bname, off + row * p.width(base) * _itemsize(base)
+        if v.is_weight or v.is_const:
+            if v.name not in self.windows:
+                raise KeyError(f"emit: the pack has no entry for {v.name!r}")
+            return self.windows[v.name]
+        if v.is_input:
+            fld = "pending_tokens" if v.name == "tokens" else v.name
+            if fld in self.layout.offsets:
+                return self.program.step_state, self.layout.offset(fld)
+        nbytes = max(_itemsize(v) * _numel(p.shape(v)), 16)
+        role = "state" if v.is_state else "arena"
+        spec = self.program.buffers.get(v.name)
+        if spec is None:
+            self.program.buffers[v.name] = BufferSpec(nbytes, None, role)
+        elif spec.nbytes < nbytes:
+            spec.nbytes = nbytes
+        return v.name, 0
+
+    def ld(self, v) -> int:
+        return self.plan.ld(v)
+
+    def field(self, name: str) -> Tuple[str, int]:
+        return self.program.step_state, self.layout.offset(name)
 
     def params(self, name: str, data: bytes) -> str:
         bname = self._name(f"params.{name}")
@@ -210,3 +286,18 @@ class EmitContext:
         op = OpSpec(kernel, [tuple(b) for b in bindings], tuple(grid), tuple(tg), True, [], name, dict(meta))
         self.program.ops.append(op)
         return op
+
+
+_ITEM = {"bf16": 2, "f16": 2, "f32": 4, "i32": 4, "u32": 4, "i64": 8, "u8": 1, "bool": 1, "i8": 1}
+
+
+def _itemsize(v) -> int:
+    it = getattr(v.dtype, "itemsize", None)
+    return int(it) if it is not None else _ITEM[str(v.dtype)]
+
+
+def _numel(shape) -> int:
+    n = 1
+    for d in shape:
+        n *= int(d)
+    return n

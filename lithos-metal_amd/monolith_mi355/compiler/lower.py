@@ -1,187 +1,167 @@
-"""Lower the decode layers built from this package (``layers.py``) to the op graph, bound to their live device memory:
-the reference's layer ``lower`` methods (``nn/linear.py:63-191``, ``nn/gdn.py``, ``nn/attention.py``, ``nn/mlp.py``,
-``nn/decoder.py``) for one token per step.
+"""A ``layers.DecoderModel`` (the hand-built decode layers) in the reference's terms: the module tree that lowers to
+the same step graph (``nn.HybridDecoder``), the pack of its weights under the names that tree's ops reference
+(``Packer.add_packed``: the device bytes as they are, so the program streams the same bits), and the images of its
+states in the program's state buffers. ``compile_decoder`` chains them with ``compile_program``.
 
-Weights, norms and states are the layers' own tensors (the program binds them by storage); activations between ops
-are values the program allocates. Layer by layer the ops are the ones ``layers.py`` launches eagerly:
-
-* Gated DeltaNet layer: ``gemv`` in_proj (norm fused) → ``gdn_mixer`` (conv state in two slots by the step's parity,
-  the recurrent state in place; the gated norm deferred to the next GEMV where ``defers_norm``) → ``gemv`` out_proj
-  (+ residual) → the MLP;
-* attention layer: ``gemv`` q|gate|k|v (norm fused) → ``gqa_decode`` at the step state's position → ``gemv`` o_proj
-  (+ residual) → the MLP;
-* MLP: ``gemv`` gate|up (norm fused, silu·mul) → ``gemv`` down (+ residual); a MoE block (``lower_moe``) in its place:
-  the shared expert, the router, ``moe_route``, the grouped ``moe_gemv`` pair and ``moe_combine``;
-* the token loop: ``embed`` of the pending token → the layers → ``lm_head`` (final norm fused, BF16 logits) →
-  ``argmax`` → ``advance``.
+Pack order is part of the plan: a MoE block's router and shared-expert gate, its routed experts' gate|up and the
+shared expert's, and their downs, are written back to back, which lets the emitter stack each pair into one launch
+(``plan.merge_adjacent_slabs``, ``plan.fuse_shared_expert``) — the launches the hand-built block makes.
 """
 
 from __future__ import annotations
 
-from typing import List
+from pathlib import Path
+from typing import Dict, List, Tuple
 
-from .ir import Graph, Value, Weight
+import numpy as np
+
+from .. import nn as NN
 
 
-def _dt(t) -> str:
+def _np(t) -> np.ndarray:
+    return t.detach().contiguous().cpu().numpy()
+
+
+def _bits(t) -> np.ndarray:
+    """A BF16 tensor's bit patterns."""
     import torch
-    return {torch.bfloat16: "bf16", torch.float32: "f32", torch.float16: "f16", torch.int8: "i8", torch.uint8: "u8",
-            torch.int32: "i32"}[t.dtype]
+    return _np(t.contiguous().view(torch.int16)).view(np.uint16)
 
 
-def bound(name: str, t, role: str) -> Value:
-    """A value held by the tensor ``t``."""
-    return Value(name, tuple(t.shape), _dt(t), role=role, tensor=t)
-
-
-def weight(name: str, pw) -> Weight:
-    """A packed weight (``kernels.PackedWeight``) as a graph value."""
-    rs = bound(f"{name}.row_scale", pw.row_scale, "weights") if pw.row_scale is not None else None
-    return Weight(name, (pw.nbytes,), "u8", role="weights", tensor=pw.data, format=pw.format, n=pw.n, k=pw.k,
-                  experts=pw.experts, row_scale=rs)
-
-
-def act(name: str, *shape: int, dtype: str = "bf16") -> Value:
-    return Value(name, tuple(shape), dtype)
-
-
-def lower_moe(g: Graph, moe, h: Value, prefix: str) -> Value:
-    """A ``layers.MoeBlock`` (``nn/moe.py``): the router and the shared expert's σ-gate as one BF16 GEMV of E + 1 rows
-    into a row padded to 8, the top-k route with its expert groups, the grouped gate|up and down GEMVs, the weighted
-    combine with the residual. With the shared expert stacked after the routed ones (``fused_shared``) it is slot k
-    of every token inside the grouped launches (its own silu·mul epilogue) and of the combine, and at one token the
-    gate|up launch routes for itself (no route op); otherwise the shared expert runs as two dense GEMVs first and
-    the combine adds it with its gate. One stream: the ops run in this order."""
-    m, e, k = g.t, moe.experts, moe.top_k
-    pad = (e + 1 + 7) // 8 * 8
-    norm = bound(f"{prefix}.norm", moe.norm_w, "weights")
-    fused = getattr(moe, "fused_shared", False)
-    s_out = None
-    if not fused:
-        s_act = act(f"{prefix}.shared_act", m, moe.shared_inter)
-        s_out = act(f"{prefix}.shared_out", m, moe.hidden)
-        g.add("gemv", [h, weight(f"{prefix}.shared_gate_up", moe.shared_gate_up.packed)], [s_act],
-              epilogue="silu_mul", norm_w=norm, eps=moe.eps, name=f"{prefix}.shared_gate_up")
-        g.add("gemv", [s_act, weight(f"{prefix}.shared_down", moe.shared_down.packed)], [s_out],
-              name=f"{prefix}.shared_down")
-    logits = act(f"{prefix}.router_logits", m, pad)
-    router_out = Value(f"{prefix}.router_gate", (m, e + 1), "bf16", ld=pad, base=logits)
-    route_in = Value(f"{prefix}.route_logits", (m, e), "bf16", ld=pad, base=logits)
-    gate = Value(f"{prefix}.shared_gate", (m, 1), "bf16", ld=pad, offset=2 * e, base=logits)
-    g.add("gemv", [h, weight(f"{prefix}.router", moe.router_gate)], [router_out], norm_w=norm, eps=moe.eps,
-          name=f"{prefix}.router")
-    ks = k + (1 if fused else 0)                     # slots per token
-    ids = act(f"{prefix}.ids", m, ks, dtype="i32")
-    wts = act(f"{prefix}.weights", m, ks, dtype="f32")
-    from ..kernels import GROUP_REC
-    groups = act(f"{prefix}.groups", min(e, m * k) + (1 if fused else 0), GROUP_REC, dtype="i32")
-    shared = dict(shared_expert=e) if fused else {}
-    inline = fused and m == 1                        # one token: the gate|up launch routes for itself
-    if not inline:
-        g.add("moe_route", [route_in], [ids, wts, groups], top_k=k, renorm=True, name=f"{prefix}.route",
-              **(dict(shared_expert=e, shared_gate_col=e) if fused else {}))
-    a = act(f"{prefix}.expert_act", m * ks, moe.inter)
-    hk = act(f"{prefix}.expert_out", m * ks, moe.hidden)
-    gu = moe.gate_up_s if fused else moe.gate_up
-    dn = moe.down_s if fused else moe.down
-    extra = dict(shared, shared_epilogue="silu_mul") if fused else {}
-    if inline:
-        extra["route"] = dict(logits=route_in, ids=ids, weights=wts, top_k=k, renorm=True, gate_col=e)
-    g.add("moe_gemv", [h, weight(f"{prefix}.gate_up", gu), groups], [a], tokens=m, top_k=ks, x_per_slot=False,
-          epilogue="silu_mul_rounded", norm_w=norm, eps=moe.eps, name=f"{prefix}.experts_gate_up", **extra)
-    g.add("moe_gemv", [a, weight(f"{prefix}.down", dn), groups], [hk], tokens=m, top_k=ks, x_per_slot=True,
-          name=f"{prefix}.experts_down", **shared)
-    out = act(f"{prefix}.out", m, moe.hidden)
-    if fused:
-        g.add("moe_combine", [hk, wts], [out], top_k=ks, residual=h, name=f"{prefix}.combine")
-    else:
-        g.add("moe_combine", [hk, wts], [out], top_k=k, shared=s_out, shared_gate=gate, residual=h,
-              name=f"{prefix}.combine")
-    return out
-
-
-def lower_mlp(g: Graph, mlp, h: Value, prefix: str) -> Value:
-    if hasattr(mlp, "experts"):
-        return lower_moe(g, mlp, h, prefix)
-    inter = mlp.inter
-    a = act(f"{prefix}.act", g.t, inter)
-    out = act(f"{prefix}.out", g.t, h.shape[1])
-    g.add("gemv", [h, weight(f"{prefix}.gate_up", mlp.gate_up.packed)], [a], epilogue="silu_mul",
-          norm_w=bound(f"{prefix}.norm", mlp.norm_w, "weights"), eps=mlp.eps, name=f"{prefix}.gate_up")
-    g.add("gemv", [a, weight(f"{prefix}.down", mlp.down.packed)], [out], epilogue="residual", residual=h,
-          name=f"{prefix}.down")
-    return out
-
-
-def lower_gdn_layer(g: Graph, layer, h: Value, prefix: str) -> Value:
-    hidden = layer.hidden
-    proj = act(f"{prefix}.proj", g.t, layer.n_proj)
-    o = act(f"{prefix}.o", g.t, layer.hv * layer.dv)
-    h1 = act(f"{prefix}.h1", g.t, hidden)
-    g.add("gemv", [h, weight(f"{prefix}.in_proj", layer.w_in.packed)], [proj],
-          norm_w=bound(f"{prefix}.norm1", layer.norm_w, "weights"), eps=layer.eps, name=f"{prefix}.in_proj")
-    defer = layer.defers_norm(g.t)
-    norm_w = bound(f"{prefix}.gdn_norm", layer.gdn_norm_w, "weights")
-    g.add("gdn_mixer", [proj, bound(f"{prefix}.conv", layer.conv_state, "state"),
-                        bound(f"{prefix}.rec", layer.rec_state, "state")], [o],
-          k_heads=layer.hk, v_heads=layer.hv, dk=layer.dk, dv=layer.dv, conv_width=layer.conv, eps=layer.eps,
-          defer_norm=defer, conv_w=bound(f"{prefix}.conv_w", layer.conv_w, "weights"),
-          neg_exp_a=bound(f"{prefix}.neg_exp_a", layer.neg_exp_a, "weights"),
-          dt_bias=bound(f"{prefix}.dt_bias", layer.dt_bias, "weights"), norm_w=norm_w, name=f"{prefix}.gdn")
-    gated = None
-    if defer:                                      # z = proj[:, :hv·dv], a view with the projection's row stride
-        z = Value(f"{prefix}.z", (g.t, layer.hv * layer.dv), "bf16", ld=layer.n_proj, base=proj)
-        gated = (norm_w, z, layer.eps)
-    g.add("gemv", [o, weight(f"{prefix}.out_proj", layer.w_out.packed)], [h1], epilogue="residual", residual=h,
-          gated_norm=gated, name=f"{prefix}.out_proj")
-    return lower_mlp(g, layer.mlp, h1, f"{prefix}.mlp")
-
-
-def lower_attn_layer(g: Graph, layer, h: Value, prefix: str) -> Value:
-    c = layer.cache
-    proj = act(f"{prefix}.proj", g.t, layer.n_proj)
-    o = act(f"{prefix}.o", g.t, layer.heads * layer.d)
-    h1 = act(f"{prefix}.h1", g.t, layer.hidden)
-    g.add("gemv", [h, weight(f"{prefix}.qkv", layer.w_qkv.packed)], [proj],
-          norm_w=bound(f"{prefix}.norm1", layer.norm_w, "weights"), eps=layer.eps, name=f"{prefix}.qkv")
-    scales = c.k_scales is not None
-    g.add("gqa_decode", [proj, bound(f"{prefix}.k_codes", c.k_codes, "state"),
-                         bound(f"{prefix}.k_scales", c.k_scales, "state") if scales else None,
-                         bound(f"{prefix}.v_codes", c.v_codes, "state"),
-                         bound(f"{prefix}.v_scales", c.v_scales, "state") if scales else None,
-                         bound(f"{prefix}.cos", layer.cos, "weights"), bound(f"{prefix}.sin", layer.sin, "weights"),
-                         bound(f"{prefix}.q_norm", layer.q_norm, "weights"),
-                         bound(f"{prefix}.k_norm", layer.k_norm, "weights")], [o],
-          heads=layer.heads, kv_heads=layer.kv, head_dim=layer.d, ctx_max=c.ctx_max, gate=True, eps=layer.eps,
-          kv_dtype=c.kv_dtype,
-          name=f"{prefix}.gqa")
-    g.add("gemv", [o, weight(f"{prefix}.o_proj", layer.w_o.packed)], [h1], epilogue="residual", residual=h,
-          name=f"{prefix}.o_proj")
-    return lower_mlp(g, layer.mlp, h1, f"{prefix}.mlp")
-
-
-def lower_layer(g: Graph, layer, h: Value, prefix: str) -> Value:
-    if getattr(layer, "ping_pong", False):
-        return lower_gdn_layer(g, layer, h, prefix)
-    return lower_attn_layer(g, layer, h, prefix)
-
-
-def lower_decoder(model) -> Graph:
-    """The one-token step of a ``layers.DecoderModel``: embed → layers → final norm + lm_head → argmax → advance."""
-    g = Graph(t=1)
-    vocab, hidden = model.embed_table.shape
-    h = act("h0", 1, hidden)
-    g.add("embed", [bound("embed_table", model.embed_table, "weights")], [h])
+def describe(model) -> NN.HybridDecoder:
+    """The module tree of ``model``'s geometry (layer kinds, heads, MoE blocks)."""
+    kinds, gdn, attn, moe, moe_layers, inter = [], None, None, None, [], None
     for i, layer in enumerate(model.layers):
-        h = lower_layer(g, layer, h, f"layers.{i}")
-    logits = act("logits", 1, vocab)
-    ids = act("ids", 16, dtype="i32")
-    g.add("lm_head", [h, weight("lm_head", model.lm_head)], [logits], norm_w=bound("norm", model.norm_w, "weights"),
-          eps=model.eps, bf16=True)
-    g.add("argmax", [logits], [ids])
-    g.add("advance", [ids], [])
-    return g
+        if getattr(layer, "ping_pong", False):
+            kinds.append("gdn")
+            gdn = dict(k_heads=layer.hk, v_heads=layer.hv, dk=layer.dk, dv=layer.dv, conv_width=layer.conv)
+        else:
+            if getattr(layer, "layout", "checkpoint") != "packed":
+                raise ValueError(f"layer {i}: the reference's graph reads the packed attention layout "
+                                 "(AttnDecoderLayer(layout='packed'))")
+            kinds.append("attention")
+            attn = dict(heads=layer.heads, kv_heads=layer.kv, head_dim=layer.d, rotary_dim=layer.rotary_dim,
+                        theta=layer.theta, gate=True)
+            ctx = layer.cache.ctx_max
+        mlp = layer.mlp
+        if hasattr(mlp, "experts"):
+            moe_layers.append(i)
+            moe = dict(experts=mlp.experts, top_k=mlp.top_k, inter=mlp.inter, shared_inter=mlp.shared_inter)
+        else:
+            inter = mlp.inter
+    ctxs = {l.cache.ctx_max for l in model.layers if not getattr(l, "ping_pong", False)}
+    if len(ctxs) > 1:
+        raise ValueError("the attention layers must share one context capacity (one RoPE table)")
+    return NN.HybridDecoder(vocab=model.vocab, hidden=model.hidden, layer_types=kinds, inter=inter or 1,
+                            eps=model.eps, gdn=gdn, attention=attn, moe=moe, moe_layers=moe_layers,
+                            max_context=ctxs.pop() if ctxs else 4096)
 
 
-def layer_values(g: Graph) -> List[Value]:
-    return g.values()
+def _slab(name: str, pw, *, n=None, experts=None) -> dict:
+    return dict(name=name, format=pw.format, n=pw.n if n is None else n, k=pw.k,
+                experts=pw.experts if experts is None else experts, data=_np(pw.data),
+                row_scale=None if pw.row_scale is None else _np(pw.row_scale))
+
+
+def write_pack(model, out_dir, spec: NN.HybridDecoder = None, tables=None):
+    """Write ``model``'s weights as a gfx950 pack under ``spec``'s slab and constant names, plus ``tables``
+    (``{name: (array, safetensors dtype)}``, e.g. a speculative program's ``draft_table``); returns the
+    ``PackFile``."""
+    from ..formats import device as DV
+    from ..kernels import PackedWeight
+    from ..packs import Packer, PackFile
+    spec = spec or describe(model)
+    out = Path(out_dir)
+    pk = Packer(None, out)                           # no checkpoint: every slab arrives packed
+
+    def f32(name, t):
+        pk.add_table(name, _np(t).astype(np.float32), "F32")
+
+    emb = PackedWeight("bf16", model.vocab, model.hidden, 1, DV.pack_bf16(model.embed_table), None)
+    pk.add_packed([_slab(spec.embed_tokens.slab_name, emb)])
+    for blk, layer in zip(spec.blocks, model.layers):
+        f32(f"{blk.input_norm.prefix}weight", layer.norm_w)
+        mx = blk.mixer
+        if isinstance(mx, NN.GatedDeltaNet):
+            pk.add_packed([_slab(mx.in_proj.slab_groups()[0].name, layer.w_in.packed)])
+            pk.add_packed([_slab(mx.out_proj.slab_groups()[0].name, layer.w_out.packed)])
+            pk.add_table(f"{mx.prefix}conv_w", _bits(layer.conv_w), "BF16")
+            f32(f"{mx.prefix}a_log", layer.neg_exp_a)
+            f32(f"{mx.prefix}dt_bias", layer.dt_bias)
+            f32(f"{mx.prefix}norm_w", layer.gdn_norm_w)
+        else:
+            pk.add_packed([_slab(mx.qkv.slab_groups()[0].name, layer.w_qkv.packed)])
+            pk.add_packed([_slab(mx.o_proj.slab_groups()[0].name, layer.w_o.packed)])
+            f32(f"{mx.prefix}q_norm", layer.q_norm)
+            f32(f"{mx.prefix}k_norm", layer.k_norm)
+        mlp, m = blk.mlp, layer.mlp
+        f32(f"{blk.post_norm.prefix}weight", m.norm_w)
+        if isinstance(mlp, NN.SparseMoE):
+            e = m.experts
+            router = PackedWeight("bf16", e, m.hidden, 1, DV.pack_bf16(m.router_w), None)
+            pk.add_packed([_slab(mlp.router.slab_groups()[0].name, router),
+                           _slab(mlp.shared_gate.slab_groups()[0].name, m.shared_gate)])
+            gu_name, dn_name = mlp.gate_up.slab.slab_groups()[0].name, mlp.down.slab.slab_groups()[0].name
+            pk.add_packed([_slab(gu_name, m.gate_up), _slab(mlp.shared_gate_up.slab_groups()[0].name,
+                                                              m.shared_gate_up.packed)])
+            pk.add_packed([_slab(dn_name, m.down), _slab(mlp.shared_down.slab_groups()[0].name,
+                                                         m.shared_down.packed)])
+        else:
+            pk.add_packed([_slab(mlp.gate_up.slab_groups()[0].name, m.gate_up.packed)])
+            pk.add_packed([_slab(mlp.down.slab_groups()[0].name, m.down.packed)])
+    attn = [l for l in model.layers if not getattr(l, "ping_pong", False)]
+    if attn:
+        pk.add_table("rope_cos", _bits(attn[0].cos), "BF16")
+        pk.add_table("rope_sin", _bits(attn[0].sin), "BF16")
+    f32(f"{spec.norm.prefix}weight", model.norm_w)
+    pk.add_packed([_slab(spec.lm_head.slab_name, model.lm_head)])
+    for name, (arr, dtype) in (tables or {}).items():
+        pk.add_table(name, np.asarray(arr), dtype)
+    pk.write({"model": "decoder", "layers": [type(l).__name__ for l in model.layers]})
+    return PackFile(out)
+
+
+def state_images(model, spec: NN.HybridDecoder = None) -> Dict[str, bytes]:
+    """The bytes to load into the program's state buffers so it continues from ``model``'s states: the GDN conv
+    state with the current slot first (the program's step 0 reads slot 0), the recurrent state in slot 0, and the
+    KV caches in the backend's layout (int8 codes with their scales in ``<cache>.scales``, or BF16 values)."""
+    import torch
+    spec = spec or describe(model)
+    out: Dict[str, bytes] = {}
+    for blk, layer in zip(spec.blocks, model.layers):
+        mx = blk.mixer
+        if isinstance(mx, NN.GatedDeltaNet):
+            cs = layer.conv_state
+            cur, other = cs[layer.parity], cs[1 - layer.parity]
+            out[f"{mx.prefix}conv_state"] = _np(torch.stack([cur, other]).contiguous().view(torch.int16)).tobytes()
+            rec = layer.rec
+            out[f"{mx.prefix}rec_state"] = _np(torch.stack([rec, torch.zeros_like(rec)])).tobytes()
+        else:
+            c = layer.cache
+            out[f"{mx.prefix}k_cache"] = _np(c.k_codes.contiguous().view(torch.uint8)).tobytes()
+            out[f"{mx.prefix}v_cache"] = _np(c.v_codes.contiguous().view(torch.uint8)).tobytes()
+            if c.k_scales is not None:
+                out[f"{mx.prefix}k_cache.scales"] = _np(c.k_scales.contiguous().view(torch.uint8)).tobytes()
+                out[f"{mx.prefix}v_cache.scales"] = _np(c.v_scales.contiguous().view(torch.uint8)).tobytes()
+    return out
+
+
+def compile_decoder(model, out_dir, profile, *, tables=None, **options) -> Tuple[object, object, Dict[str, bytes]]:
+    """``(program, pack, state images)`` of ``model``'s step: its pack written to ``out_dir`` (with ``tables``), its
+    module tree lowered to the reference-contract graph and emitted from that pack (``options`` go to
+    ``compile_program``: ``t``, ``gamma`` …)."""
+    from .emit import compile_program
+    spec = describe(model)
+    pack = write_pack(model, out_dir, spec, tables)
+    return compile_program(spec, pack, profile, **options), pack, state_images(model, spec)
+
+
+def load_states(engine, images: Dict[str, bytes]) -> None:
+    """Write state images into an Engine's buffers (every name must be a state buffer of its program)."""
+    for name, data in images.items():
+        spec = engine.program.buffers.get(name)
+        if spec is None or spec.role != "state":
+            raise KeyError(f"{name}: not a state buffer of the program")
+        if len(data) > spec.nbytes:
+            raise ValueError(f"{name}: {len(data)} bytes for a {spec.nbytes}-byte state")
+        engine.buffers[name].write(data, 0)

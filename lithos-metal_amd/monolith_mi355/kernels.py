@@ -332,7 +332,7 @@ class KVCache:
 
 def gqa_decode(proj, cache: KVCache, pos, *, heads: int, rope_cos, rope_sin, gate: bool = True,
                q_norm=None, k_norm=None, eps: float = 1e-6, scaling: Optional[float] = None, out=None, stream=None,
-               workspace=None, done=None):
+               workspace=None, done=None, gate_src=None):
     """``gqa_decode`` + ``gqa_merge`` (``ops/attention.py``; ``GQAAttention.mix``, ``nn/attention.py:215-243``) for
     ``proj [T, N1]`` bf16 (``q|gate`` per head, then ``k``, ``v``): q/k norm (``q_norm``/``k_norm`` = the (1 + w)
     float32 weights, both or neither), partial RoPE from the BF16 tables ``[ctx_max, rotary_dim]``, the new k/v
@@ -341,12 +341,18 @@ def gqa_decode(proj, cache: KVCache, pos, *, heads: int, rope_cos, rope_sin, gat
     ``pos`` is an int, or a one-element int32 device tensor the kernels read (a step program's StepState position:
     the same launch serves every step of a replayed graph). ``done``: a step program's stop flag (one-element device
     int32): once set, nothing is appended to the cache and ``out`` is not written. ``workspace``: a uint8 tensor of
-    ``mi_gqa_workspace_bytes`` for the key-range partials, or None for the library's own."""
+    ``mi_gqa_workspace_bytes`` for the key-range partials, or None for the library's own. ``gate_src``: the
+    reference's packed layout (``nn/attention.py:52-64``) — ``proj`` holds ``q | k | v`` and the gate rows are this
+    ``[T, heads·D]`` bf16 view; with the RoPE head-dim permutation the tables are ``[ctx_max, D]``."""
     torch = _torch()
     _bf16_2d(proj, "gqa proj", aligned=False)
     t = proj.shape[0]
     d, kv = cache.head_dim, cache.kv_heads
-    q_cols = heads * (2 if gate else 1) * d
+    if gate_src is not None:
+        _bf16_2d(gate_src, "gqa gate", aligned=False)
+        if not gate or gate_src.shape[0] < t or gate_src.shape[1] < heads * d:
+            raise ValueError("gqa_decode: gate_src must be [T, heads·D] bf16 and needs gate=True")
+    q_cols = heads * (2 if gate and gate_src is None else 1) * d
     if proj.shape[1] < q_cols + 2 * kv * d:
         raise ValueError(f"gqa_decode: proj has {proj.shape[1]} columns, needs {q_cols + 2 * kv * d}")
     if (q_norm is None) != (k_norm is None):
@@ -377,7 +383,8 @@ def gqa_decode(proj, cache: KVCache, pos, *, heads: int, rope_cos, rope_sin, gat
                          v_scales=hip.ptr(cache.v_scales), y=hip.ptr(out), ld_y=out.stride(0), kv_dtype=cache.kv_dtype,
                          workspace=hip.ptr(workspace),
                          workspace_bytes=0 if workspace is None else workspace.numel() * workspace.element_size(),
-                         pos_dev=hip.ptr(pos_dev), done=hip.ptr(done))
+                         pos_dev=hip.ptr(pos_dev), done=hip.ptr(done), gate_src=hip.ptr(gate_src),
+                         ld_gate=0 if gate_src is None else gate_src.stride(0))
     hip.call("mi_gqa_decode", C.byref(desc), hip.stream_handle(stream))
     return out
 
@@ -503,21 +510,29 @@ def moe_combine(h, weights, *, top_k: int, shared=None, shared_gate=None, residu
 
 def embed(table, tokens, *, t: Optional[int] = None, out=None, stream=None):
     """``embed`` (``ops/embed.py:1-7``): ``out[i] = table[tokens[i]]`` for ``i < t`` over a BF16 ``table
-    [vocab, hidden]``; ``tokens`` is a device int32 vector (a view of the step state's ``pending_tokens`` in a step
-    program); an id outside ``[0, vocab)`` reads row 0."""
+    [vocab, hidden]`` — or a BF16 ``PackedWeight`` (the pack's embedding slab, gathered from its T16 tiles);
+    ``tokens`` is a device int32 vector (a view of the step state's ``pending_tokens`` in a step program); an id
+    outside ``[0, vocab)`` reads row 0."""
     torch = _torch()
-    _bf16_2d(table, "embed table")
-    vocab, hidden = table.shape
+    t16 = isinstance(table, PackedWeight)
+    if t16:
+        if table.format != "bf16" or table.experts != 1:
+            raise ValueError("embed: a packed table must be one BF16 slab")
+        vocab, hidden, src = table.n, table.k, table.data
+    else:
+        _bf16_2d(table, "embed table")
+        vocab, hidden = table.shape
+        src = table
     t = tokens.numel() if t is None else t
     if tokens.dtype != torch.int32 or tokens.numel() < t or not 1 <= t <= 16:
         raise ValueError("embed: tokens must be a device int32 vector of 1..16 ids")
     if out is None:
-        out = torch.empty((t, hidden), dtype=torch.bfloat16, device=table.device)
+        out = torch.empty((t, hidden), dtype=torch.bfloat16, device=src.device)
     _bf16_2d(out, "embed out")
     if out.shape[0] < t or out.shape[1] != hidden:
         raise ValueError("embed: out must be [t, hidden]")
-    d = hip.MiEmbedDesc(t=t, vocab=vocab, hidden=hidden, tokens=hip.ptr(tokens), table=hip.ptr(table),
-                        out=hip.ptr(out), ldo=out.stride(0))
+    d = hip.MiEmbedDesc(t=t, vocab=vocab, hidden=hidden, tokens=hip.ptr(tokens), table=hip.ptr(src),
+                        out=hip.ptr(out), ldo=out.stride(0), t16=int(t16))
     hip.call("mi_embed", C.byref(d), hip.stream_handle(stream))
     return out
 

@@ -231,11 +231,17 @@ class AttnDecoderLayer:
     128 or 256). Projection rows q|gate per head, then k, v."""
 
     def __init__(self, *, hidden=5120, heads=24, kv_heads=4, head_dim=128, rotary_dim=64, theta=1e6, ctx=32768,
-                 inter=17408, eps=1e-6, device="cuda", seed=0, kv_dtype="int8"):
+                 inter=17408, eps=1e-6, device="cuda", seed=0, kv_dtype="int8", layout="checkpoint"):
+        """``layout="packed"``: the projection rows in the reference's pack order ``[q | k | v | gate]`` with the
+        RoPE head-dim permutation on q and k (``nn/attention.py:52-64``), the permuted full-width RoPE tables and
+        norm weights — the same weights and the same attention, laid out as a compiled program holds them."""
         torch = _torch()
         gen = torch.Generator(device=device)
         gen.manual_seed(seed)
+        if layout not in ("checkpoint", "packed"):
+            raise ValueError(f"AttnDecoderLayer: layout {layout!r}")
         self.hidden, self.heads, self.kv, self.d, self.eps = hidden, heads, kv_heads, head_dim, eps
+        self.layout, self.rotary_dim, self.theta = layout, rotary_dim, theta
         self.n_proj = heads * 2 * head_dim + 2 * kv_heads * head_dim
         self.norm_w = 1.0 + torch.randn(hidden, generator=gen, device=device) * 0.1
         self.w_qkv = nvfp4_matrix(self.n_proj, hidden, gen, device)
@@ -243,6 +249,24 @@ class AttnDecoderLayer:
         self.q_norm = (1.0 + torch.randn(head_dim, generator=gen, device=device) * 0.1).to(torch.bfloat16).float()
         self.k_norm = (1.0 + torch.randn(head_dim, generator=gen, device=device) * 0.1).to(torch.bfloat16).float()
         self.cos, self.sin = kernels.rope_tables(theta, rotary_dim, ctx, device=device)
+        if layout == "packed":
+            from . import nn as NN
+            from .formats.fp import f32_to_bf16
+            spec = NN.GQAAttention(hidden, heads, kv_heads, head_dim, rotary_dim, theta, eps, prefix="", max_context=ctx)
+            self.row_perm = spec.row_perm()
+            self.core_rows = spec.core_rows
+            perm = torch.as_tensor(self.row_perm, device=device)
+            m = self.w_qkv
+            codes, scales, rs = m.codes[perm], m.scales[perm], m.row_scale[perm]
+            n_pad = -(-self.n_proj // 16) * 16
+            rs_pad = torch.cat([rs, rs.new_ones(n_pad - self.n_proj)]) if n_pad != self.n_proj else rs
+            self.w_qkv = QuantizedMatrix(codes, scales, rs, kernels.PackedWeight(
+                "nvfp4", self.n_proj, hidden, 1, DV.pack_nvfp4(codes, scales), rs_pad.contiguous()))
+            hp = torch.as_tensor(NN.rope_head_perm(head_dim, rotary_dim), device=device)
+            self.q_norm, self.k_norm = self.q_norm[hp].contiguous(), self.k_norm[hp].contiguous()
+            cos, sin = NN.rope_tables_permuted(theta, head_dim, rotary_dim, ctx)
+            self.cos = torch.from_numpy(f32_to_bf16(cos).astype(np.int16)).view(torch.bfloat16).to(device)
+            self.sin = torch.from_numpy(f32_to_bf16(sin).astype(np.int16)).view(torch.bfloat16).to(device)
         self.cache = kernels.KVCache(kv_heads, ctx, head_dim, device=device, dtype=kv_dtype)
         self.mlp = GatedMLP(hidden, inter, gen, device, eps)
         self._bufs: Dict[int, tuple] = {}
@@ -282,8 +306,9 @@ class AttnDecoderLayer:
         proj, o, h1, act, h2 = self.buffers(h.shape[0])
         out = h2 if out is None else out
         kernels.gemv(self.w_qkv.packed, h, norm_w=self.norm_w, eps=self.eps, out=proj)
+        gate_src = proj[:, self.core_rows:] if self.layout == "packed" else None
         kernels.gqa_decode(proj, self.cache, pos, heads=self.heads, rope_cos=self.cos, rope_sin=self.sin, gate=True,
-                           q_norm=self.q_norm, k_norm=self.k_norm, eps=self.eps, out=o, done=done)
+                           q_norm=self.q_norm, k_norm=self.k_norm, eps=self.eps, out=o, done=done, gate_src=gate_src)
         if CHAIN_TAIL and h.shape[0] == 1:
             kernels.gemv_chain([(self.w_o.packed, o, dict(epilogue="residual", residual=h, out=h1))]
                                + self.mlp.phases(h1, act, out))
@@ -361,8 +386,9 @@ class MoeBlock:
         self._xn: Dict[int, object] = {}
         # the shared expert runs on a second stream beside the router → experts chain (default priority), with its
         # own zeroed split-K workspace so the two branches never share partials or fold counters
-        self.side = torch.cuda.Stream(device=device)
-        self.side_ws = torch.zeros(8 << 20, dtype=torch.uint8, device=device)
+        on_gpu = torch.device(device).type == "cuda"
+        self.side = torch.cuda.Stream(device=device) if on_gpu else None
+        self.side_ws = torch.zeros(8 << 20 if on_gpu else 16, dtype=torch.uint8, device=device)
 
     def buffers(self, m: int):
         torch = _torch()

@@ -57,10 +57,13 @@ def _unit_scale(spec: DequantSpec) -> DequantSpec:
 
 class Packer:
     def __init__(self, checkpoint, out_dir) -> None:
-        self.ckpt = Checkpoint(checkpoint)
-        self.dtypes = {n: self.ckpt.info(n).dtype for n in self.ckpt.names()}
-        self.shapes = {n: self.ckpt.info(n).shape for n in self.ckpt.names()}
-        self.groups = group_tensors(self.ckpt.names(), self.dtypes)
+        """``checkpoint``: a safetensors file / directory, or None for a pack written only from already packed slabs
+        and computed tables (``add_packed``, ``add_table``)."""
+        self.ckpt = Checkpoint(checkpoint) if checkpoint is not None else None
+        names = self.ckpt.names() if self.ckpt is not None else []
+        self.dtypes = {n: self.ckpt.info(n).dtype for n in names}
+        self.shapes = {n: self.ckpt.info(n).shape for n in names}
+        self.groups = group_tensors(names, self.dtypes)
         self.out = Path(out_dir)
         self.out.mkdir(parents=True, exist_ok=True)
         self._fh = open(self.out / "weights.pack", "wb")
@@ -136,6 +139,37 @@ class Packer:
                                "tensor_scale": sc} for s, r, sc in zip(segments, rows, scales)]}
         self._slabs.append(entry)
         return entry
+
+    def add_packed(self, slabs: Sequence[Dict[str, Any]]) -> List[Dict[str, Any]]:
+        """Slabs already in the T16 layout (a model's device weights, a re-pack): each ``dict(name, format, n, k,
+        data, row_scale=None, experts=1)`` with ``data`` the pack bytes of ``experts`` matrices of ``n`` rows and
+        ``row_scale`` their per-row table (padded to whole tiles per expert). The slabs of one call are written back
+        to back — their code bytes contiguous, then their row-scale tables contiguous — so an emitter may stream two
+        adjacent slabs of one format and K as one stacked matrix (a router and the shared expert's gate, the routed
+        experts and the shared expert)."""
+        self._align()
+        entries = []
+        for sl in slabs:
+            fmt, n, k, experts = sl["format"], int(sl["n"]), int(sl["k"]), int(sl.get("experts", 1))
+            if fmt not in FORMATS:
+                raise ValueError(f"slab {sl['name']}: unknown format {fmt!r}")
+            data = np.ascontiguousarray(np.asarray(sl["data"]).view(np.uint8).reshape(-1))
+            if data.size != experts * T16.pack_bytes(fmt, n, k):
+                raise ValueError(f"slab {sl['name']}: {data.size} bytes for {experts} × T16 {fmt} [{n}, {k}] "
+                                 f"({T16.pack_bytes(fmt, n, k)} each)")
+            entries.append({"name": sl["name"], "format": fmt, "n": n, "k": k, "experts": experts,
+                            "offset": self._put(data.tobytes()), "nbytes": int(data.size), "row_scales_offset": None,
+                            "row_scales_len": None, "row_perm": bool(sl.get("row_perm", False)), "segments": [],
+                            "_rs": sl.get("row_scale")})
+        for e in entries:
+            rs = e.pop("_rs")
+            if rs is not None:
+                rs = np.ascontiguousarray(np.asarray(rs, np.float32).reshape(-1))
+                if rs.size != e["experts"] * -(-e["n"] // 16) * 16:
+                    raise ValueError(f"slab {e['name']}: row-scale table of {rs.size}, expected whole tiles per expert")
+                e["row_scales_offset"], e["row_scales_len"] = self._put(rs.tobytes()), int(rs.size)
+        self._slabs.extend(entries)
+        return entries
 
     def add_aux(self, name: str, source: str, *, transform: Optional[str] = None, perm=None) -> Dict[str, Any]:
         info = self.ckpt.info(source)

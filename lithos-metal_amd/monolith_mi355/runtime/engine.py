@@ -66,7 +66,8 @@ class StepReport:
 DESCRIPTORS = {"mi_gemv": hip.MiGemvDesc, "mi_gdn_step": hip.MiGdnDesc, "mi_gqa_decode": hip.MiGqaDesc,
                "mi_moe_route": hip.MiMoeRouteDesc, "mi_moe_combine": hip.MiMoeCombineDesc, "mi_embed": hip.MiEmbedDesc,
                "mi_argmax": hip.MiArgmaxDesc, "mi_advance": hip.MiAdvanceDesc, "mi_rmsnorm_stat": hip.MiNormDesc,
-               "mi_norm_apply": hip.MiNormDesc}
+               "mi_norm_apply": hip.MiNormDesc, "mi_accept_scan": hip.MiAcceptScanDesc,
+               "mi_verify_select": hip.MiVerifySelectDesc}
 LIB_PREFIX = "lib:"
 
 

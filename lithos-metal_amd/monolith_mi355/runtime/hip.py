@@ -63,7 +63,7 @@ class MiGqaDesc(C.Structure):
                 ("scaling", C.c_float), ("k_codes", C.c_void_p), ("k_scales", C.c_void_p), ("v_codes", C.c_void_p),
                 ("v_scales", C.c_void_p), ("y", C.c_void_p), ("ld_y", C.c_int32), ("workspace", C.c_void_p),
                 ("workspace_bytes", C.c_size_t), ("pos_dev", C.c_void_p),
-                ("done", C.c_void_p), ("kv_dtype", C.c_int32)]
+                ("done", C.c_void_p), ("kv_dtype", C.c_int32), ("gate_src", C.c_void_p), ("ld_gate", C.c_int32)]
 
 
 class MiNormDesc(C.Structure):
@@ -100,7 +100,7 @@ class MiStepState(C.Structure):
 
 class MiEmbedDesc(C.Structure):
     _fields_ = [("t", C.c_int32), ("vocab", C.c_int32), ("hidden", C.c_int32), ("tokens", C.c_void_p),
-                ("table", C.c_void_p), ("out", C.c_void_p), ("ldo", C.c_int32)]
+                ("table", C.c_void_p), ("out", C.c_void_p), ("ldo", C.c_int32), ("t16", C.c_int32)]
 
 
 class MiArgmaxDesc(C.Structure):

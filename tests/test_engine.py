@@ -1,7 +1,17 @@
-"""The program format and the Engine, after the reference's toy-program gate (``tests/runtime/test_toy_program.py``):
-a two-op self-advancing program replayed from one capture for 1,000 steps with tokens drained from the ring,
-replay ≡ re-encode, early exit after ``done``, ring wrap and overflow, the JSON round trip, the pipeline cache,
-per-op profiles and file-backed weights. The kernels are the toy's, written in HIP."""
+"""``program.json`` and ``Engine`` on a program small enough to predict exactly on the host.
+
+The program ("mixer"): a map op stirs an integer vector with the step counter (``x[i] = 5·x[i] + step + i``, mod
+2^32), then a one-thread op reads two of its words, emits their digest as the step's token into the ring (tagged with
+its 1-based sequence number), advances the step state and sets ``done`` after ``stop`` steps; both ops return at once
+once ``done`` is set, and the emit op turns a full ring (the host's tail not keeping up) into ``error = 1``. Integer
+arithmetic makes every step's token and the final vector exact, so the checks are equalities.
+
+Acceptance criteria (the reference's runtime gate, ``tests/runtime/test_toy_program.py``, in this file's own
+harness): 1,000 steps replayed from one capture with every token drained in order; graph replay and op-by-op
+re-encoding agree bit for bit; submission stops early once ``done`` is set; the ring wraps; an overrun is an error,
+never a corrupted token; the JSON round trip; compiled kernels reused across engines; per-op GPU times; weights read
+from a file window.
+"""
 
 import os
 import struct
@@ -13,201 +23,208 @@ from monolith_mi355.runtime import hip
 from monolith_mi355.runtime.program import BufferSpec, KernelSpec, OpSpec, Program, StepStateLayout
 
 LAYOUT = StepStateLayout(t_max=8, gamma_max=7)
-H = 4096
+N = 4096
+MASK = np.uint64(0xFFFFFFFF)
 
-SRC = LAYOUT.to_hip() + r"""
-struct Params { unsigned n_stop, ring_cap, width, pad; };
-// op A (map): every element of h advances with the step; returns at once when the program is done
-extern "C" __global__ void toy_map(float* h, const StepState* st, const Params* p) {
+MIXER = LAYOUT.to_hip() + r"""
+struct Knobs { unsigned stop, ring_slots, n, unused; };
+extern "C" __global__ void mixer_stir(unsigned* x, const StepState* st, const Knobs* k) {
   if (st->done) return;
   const unsigned i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < p->width) h[i] = h[i] * 0.5f + float(st->step + 1);
+  if (i < k->n) x[i] = x[i] * 5u + st->step + i;
 }
-// op B (serial, one thread): consume h[0], emit a token, advance the state, stop at n_stop
-extern "C" __global__ void toy_serial(const float* h, StepState* st, const Params* p, unsigned long long* ring) {
+extern "C" __global__ void mixer_emit(const unsigned* x, StepState* st, const Knobs* k, unsigned long long* ring) {
   if (threadIdx.x != 0 || blockIdx.x != 0 || st->done) return;
-  const unsigned s = st->step + 1, head = st->ring_head;
-  if (head - st->ring_tail >= p->ring_cap) { st->error = 1; st->done = 1; return; }
-  const int token = int(s * 7u) + (h[0] > 0.0f ? 0 : 1000000);
-  ring[head % p->ring_cap] = ((unsigned long long)(head + 1u) << 32) | (unsigned)token;
+  const unsigned head = st->ring_head;
+  if (head - st->ring_tail >= k->ring_slots) { st->error = 1u; st->done = 1u; return; }
+  const unsigned token = (x[0] ^ (x[k->n - 1] >> 7)) & 0xFFFFFu;
+  ring[head % k->ring_slots] = ((unsigned long long)(head + 1u) << 32) | token;
   st->ring_head = head + 1u;
-  st->step = s;
-  st->position = st->position + 1;
-  if (s >= p->n_stop) st->done = 1;
+  st->step += 1u;
+  st->position += 1u;
+  if (st->step >= k->stop) st->done = 1u;
 }
 """
 
 
-def _program(n_stop: int, ring_cap: int = 256) -> Program:
-    params = struct.pack("<IIII", n_stop, ring_cap, H, 0)
+def mixer(stop: int, ring_slots: int = 256) -> Program:
+    """The two-op program, its vector starting at ``x[i] = 2654435761·i`` (mod 2^32)."""
+    x0 = (np.arange(N, dtype=np.uint64) * np.uint64(2654435761) & MASK).astype(np.uint32)
     return Program(
-        kernels={"toy": KernelSpec(SRC, "toy_map"), "toy_serial": KernelSpec(SRC, "toy_serial")},
-        buffers={"h": BufferSpec(H * 4, np.ones(H, np.float32).tobytes(), "arena"),
+        kernels={"stir": KernelSpec(MIXER, "mixer_stir"), "emit": KernelSpec(MIXER, "mixer_emit")},
+        buffers={"x": BufferSpec(N * 4, x0.tobytes(), "arena"),
                  "step_state": BufferSpec(LAYOUT.size, LAYOUT.pack({}), "step_state"),
-                 "params": BufferSpec(16, params, "params"),
-                 "ring": BufferSpec(ring_cap * 8, None, "ring")},
-        ops=[OpSpec("toy", [(0, "h", 0), (1, "step_state", 0), (2, "params", 0)], (H // 384 + 1, 1, 1), (384, 1, 1),
-                    True, name="map"),
-             OpSpec("toy_serial", [(0, "h", 0), (1, "step_state", 0), (2, "params", 0), (3, "ring", 0)], (1, 1, 1),
-                    (64, 1, 1), True, name="advance")],
-        ring_capacity=ring_cap, layout=LAYOUT)
+                 "knobs": BufferSpec(16, struct.pack("<IIII", stop, ring_slots, N, 0), "params"),
+                 "ring": BufferSpec(ring_slots * 8, None, "ring")},
+        ops=[OpSpec("stir", [(0, "x", 0), (1, "step_state", 0), (2, "knobs", 0)], (N // 256, 1, 1), (256, 1, 1),
+                    True, name="stir"),
+             OpSpec("emit", [(0, "x", 0), (1, "step_state", 0), (2, "knobs", 0), (3, "ring", 0)], (1, 1, 1),
+                    (64, 1, 1), True, name="emit")],
+        ring_capacity=ring_slots, layout=LAYOUT)
 
 
-def _expected_h(steps: int) -> float:
-    h = 1.0
+def predicted(steps: int):
+    """(tokens, final vector) of ``steps`` steps, computed on the host in uint64 and reduced mod 2^32."""
+    i = np.arange(N, dtype=np.uint64)
+    x = (i * np.uint64(2654435761)) & MASK
+    tokens = []
     for s in range(steps):
-        h = h * 0.5 + (s + 1)
-    return h
+        x = (x * np.uint64(5) + np.uint64(s) + i) & MASK
+        tokens.append(int((x[0] ^ (x[N - 1] >> np.uint64(7))) & np.uint64(0xFFFFF)))
+    return tokens, x.astype(np.uint32)
 
 
 # ---- CPU -------------------------------------------------------------------------------------------------------
-def test_layout_matches_the_c_abi_state():
-    """mi_step_state is the layout at t_max = 16, gamma_max = 15: same offsets, same size."""
+def test_c_abi_state_is_the_layout_at_16_and_15():
+    import ctypes
     lay = StepStateLayout(16, 15)
-    assert lay.size == C_sizeof_state()
+    assert lay.size == ctypes.sizeof(hip.MiStepState)
     for name, _ in hip.MiStepState._fields_:
         if name != "pad_":
             assert lay.offset(name) == getattr(hip.MiStepState, name).offset, name
 
 
-def C_sizeof_state():
-    import ctypes
-    return ctypes.sizeof(hip.MiStepState)
-
-
-def test_layout_reference_offsets_and_pack():
-    """The reference's default layout (t_max 8, gamma_max 7): 8 pending tokens, 7 drafts / confidences."""
+def test_default_layout_offsets_and_packing():
+    """t_max 8 / gamma_max 7: 8 pending tokens, 7 drafts and confidences, 176 bytes; pack / unpack invert."""
     lay = StepStateLayout()
-    assert lay.offset("pending_tokens") == 16 and lay.offset("rng_lo") == 48 and lay.offset("draft_tokens") == 64
-    assert lay.offset("confidence") == 92 and lay.offset("verify_len") == 120 and lay.offset("n_chain") == 164
-    assert lay.size == 176
-    v = {"step": 3, "pending_tokens": [5, -1], "confidence": [0.5], "done": 1}
-    u = lay.unpack(lay.pack(v))
-    assert u["step"] == 3 and u["pending_tokens"][:3] == [5, -1, 0] and u["confidence"][0] == 0.5 and u["done"] == 1
+    assert (lay.offset("pending_tokens"), lay.offset("rng_lo"), lay.offset("draft_tokens")) == (16, 48, 64)
+    assert (lay.offset("confidence"), lay.offset("verify_len"), lay.offset("n_chain"), lay.size) == (92, 120, 164, 176)
+    fields = {"step": 9, "pending_tokens": [4, -2], "confidence": [0.25], "error": 2}
+    back = lay.unpack(lay.pack(fields))
+    assert back["step"] == 9 and back["pending_tokens"][:3] == [4, -2, 0] and back["confidence"][0] == 0.25
+    assert back["error"] == 2
     with pytest.raises(ValueError):
         lay.pack({"pending_tokens": list(range(9))})
     with pytest.raises(ValueError):
         StepStateLayout(t_max=4, gamma_max=7)
 
 
-def test_program_json_roundtrip(tmp_path):
-    p = _program(5)
+def test_json_round_trip(tmp_path):
+    p = mixer(5)
     p.save(tmp_path / "program.json")
     q = Program.load(tmp_path / "program.json")
-    assert q.to_json() == p.to_json() and q.ops[1].name == "advance" and q.buffers["params"].init == p.buffers["params"].init
+    assert q.to_json() == p.to_json()
+    assert [o.name for o in q.ops] == ["stir", "emit"] and q.buffers["x"].init == p.buffers["x"].init
     with pytest.raises(ValueError, match="version"):
         Program.from_json('{"version": 2}')
 
 
-def test_toy_sources_compile_without_gpu():
+def test_mixer_compiles_without_a_gpu():
     from monolith_mi355.runtime import native
-    assert len(native.compile_source(SRC)) > 1000
+    assert len(native.compile_source(MIXER)) > 1000
+
+
+def test_host_prediction_is_self_consistent():
+    a, xa = predicted(10)
+    b, xb = predicted(11)
+    assert a == b[:10] and len(set(b)) > 5 and not np.array_equal(xa, xb)
 
 
 # ---- GPU -------------------------------------------------------------------------------------------------------
-@pytest.mark.gpu
-def test_replay_1000_steps_from_one_capture(torch_gpu):
+def _run(stop, steps, ring_slots=256, **kw):
     from monolith_mi355.runtime.engine import Engine
-    eng = Engine(_program(n_stop=1000))
-    rep = eng.run(1000, steps_per_cb=25, in_flight=3)
+    eng = Engine(mixer(stop, ring_slots))
+    return eng, eng.run(steps, **kw)
+
+
+@pytest.mark.gpu
+def test_thousand_steps_from_one_capture(torch_gpu):
+    eng, rep = _run(1000, 1000, steps_per_cb=25, in_flight=3)
+    tokens, x = predicted(1000)
     assert rep.steps == 1000 and rep.done and rep.command_buffers == 40
-    assert rep.tokens == [7 * s for s in range(1, 1001)]
+    assert rep.tokens == tokens
     st = eng.state()
-    assert st["step"] == 1000 and st["position"] == 1000 and st["ring_head"] == 1000
-    h = np.frombuffer(eng.read("h"), dtype=np.float32)
-    assert np.allclose(h, _expected_h(1000), rtol=1e-6)
+    assert (st["step"], st["position"], st["ring_head"]) == (1000, 1000, 1000)
+    assert np.array_equal(np.frombuffer(eng.read("x"), np.uint32), x)
     assert rep.host_fraction < 0.9
     print(f"\n1000 steps: gpu {rep.gpu_ms:.2f} ms, wall {rep.wall_ms:.2f} ms, host busy {rep.host_busy_ms:.2f} ms")
 
 
 @pytest.mark.gpu
-def test_reencode_matches_replay(torch_gpu):
-    from monolith_mi355.runtime.engine import Engine
-    a = Engine(_program(n_stop=300)); ra = a.run(300, steps_per_cb=10, in_flight=2, reencode=False)
-    b = Engine(_program(n_stop=300)); rb = b.run(300, steps_per_cb=10, in_flight=2, reencode=True)
+def test_graph_replay_equals_op_by_op(torch_gpu):
+    a, ra = _run(300, 300, steps_per_cb=10, in_flight=2)
+    b, rb = _run(300, 300, steps_per_cb=10, in_flight=2, reencode=True)
     sa, sb = a.state(), b.state()
-    sa.pop("ring_tail"), sb.pop("ring_tail")      # host-written: the tail drained when the last batch was queued
-    assert ra.tokens == rb.tokens == [7 * s for s in range(1, 301)] and sa == sb
-    assert a.read("h") == b.read("h")
+    sa.pop("ring_tail"), sb.pop("ring_tail")      # host-written: where the drain stood when the last batch was queued
+    assert ra.tokens == rb.tokens == predicted(300)[0] and sa == sb
+    assert a.read("x") == b.read("x")
 
 
 @pytest.mark.gpu
-def test_early_exit_after_done_and_ring_wrap(torch_gpu):
-    from monolith_mi355.runtime.engine import Engine
-    eng = Engine(_program(n_stop=100, ring_cap=64))
-    rep = eng.run(1000, steps_per_cb=4, in_flight=2)
-    assert rep.done and rep.steps <= 100 + 4 * 2 and eng.state()["step"] == 100 and eng.state()["error"] == 0
-    assert rep.tokens == [7 * s for s in range(1, 101)]
-    h = np.frombuffer(eng.read("h"), dtype=np.float32)
-    assert np.allclose(h, _expected_h(100), rtol=1e-6)
+def test_stops_at_done_and_wraps_the_ring(torch_gpu):
+    eng, rep = _run(100, 1000, ring_slots=64, steps_per_cb=4, in_flight=2)
+    st = eng.state()
+    assert rep.done and rep.steps <= 100 + 4 * 2 and st["step"] == 100 and st["error"] == 0
+    tokens, x = predicted(100)
+    assert rep.tokens == tokens
+    assert np.array_equal(np.frombuffer(eng.read("x"), np.uint32), x)    # the steps past done changed nothing
 
 
 @pytest.mark.gpu
-def test_pipeline_cache_survives_engine_replacement(torch_gpu):
+def test_ring_overrun_is_an_error(torch_gpu):
+    """A ring of 16 slots drained only between batches of 25 steps: the emit op refuses to overwrite an undrained
+    slot, flags error 1 and stops; every token that arrived is the right one, in order."""
+    eng, rep = _run(1000, 1000, ring_slots=16, steps_per_cb=25, in_flight=3)
+    st = eng.state()
+    assert st["error"] == 1 and st["done"] == 1
+    assert 0 < len(rep.tokens) <= 16 and rep.tokens == predicted(len(rep.tokens))[0]
+
+
+@pytest.mark.gpu
+def test_compiled_kernels_are_shared_through_the_cache(torch_gpu):
     from monolith_mi355.runtime import native as nt
     from monolith_mi355.runtime.engine import Engine
     device, cache = nt.Device(), {}
-    first = Engine(_program(2), device, pipeline_cache=cache)
-    pipelines = dict(first.pipelines)
-    assert first.run(2).tokens == [7, 14]
+    first = Engine(mixer(2), device, pipeline_cache=cache)
+    kept = dict(first.pipelines)
+    assert first.run(2).tokens == predicted(2)[0]
     del first
-    second = Engine(_program(3), device, pipeline_cache=cache)
-    assert all(second.pipelines[name] is p for name, p in pipelines.items())
-    assert second.run(3).tokens == [7, 14, 21]
-    assert len(cache) == 2
-    changed = Engine(_program(1), device, fast_math=True, pipeline_cache=cache)
-    assert all(changed.pipelines[name] is not p for name, p in pipelines.items())
-    assert changed.run(1).tokens == [7] and len(cache) == 4
+    second = Engine(mixer(3), device, pipeline_cache=cache)
+    assert all(second.pipelines[name] is p for name, p in kept.items())
+    assert second.run(3).tokens == predicted(3)[0] and len(cache) == 2
+    fast = Engine(mixer(1), device, fast_math=True, pipeline_cache=cache)     # other options: compiled anew
+    assert all(fast.pipelines[name] is not p for name, p in kept.items())
+    assert fast.run(1).tokens == predicted(1)[0] and len(cache) == 4
 
 
 @pytest.mark.gpu
-def test_ring_overflow_is_an_error_not_corruption(torch_gpu):
+def test_per_op_gpu_times(torch_gpu):
     from monolith_mi355.runtime.engine import Engine
-    eng = Engine(_program(n_stop=1000, ring_cap=16))
-    rep = eng.run(1000, steps_per_cb=25, in_flight=3)
-    st = eng.state()
-    assert st["error"] == 1 and st["done"] == 1
-    assert rep.tokens == [7 * s for s in range(1, len(rep.tokens) + 1)] and len(rep.tokens) <= 16
-
-
-@pytest.mark.gpu
-def test_profile_gives_per_op_gpu_times(torch_gpu):
-    from monolith_mi355.runtime.engine import Engine
-    eng = Engine(_program(n_stop=50))
+    eng = Engine(mixer(50))
     eng.run(5, steps_per_cb=5, in_flight=1)
     runs = eng.profile(3)
     assert len(runs) == 3 and all(len(r) == 2 for r in runs)
-    for (s0, e0), (s1, e1) in runs:
-        assert 0 <= s0 <= e0 <= s1 + 1e-3 and s1 <= e1 and e1 - s0 < 5.0 and e0 > s0
+    for (s0, e0), (s1, e1) in runs:                # stir, then emit, in order, each a positive span
+        assert 0 <= s0 < e0 <= s1 + 1e-3 and s1 <= e1 and e1 - s0 < 5.0
 
 
 @pytest.mark.gpu
-def test_runner_reports_host_phases(torch_gpu):
-    from monolith_mi355.runtime.engine import Engine
-    eng = Engine(_program(n_stop=20))
-    report = eng.run(20, steps_per_cb=5, in_flight=2)
-    assert report.tokens == [7 * s for s in range(1, 21)]
-    assert report.encode_ms >= 0 and report.wait_ms >= 0
-    assert report.encode_ms + report.commit_ms + report.wait_ms <= report.wall_ms + 0.1
+def test_runner_host_phases_add_up(torch_gpu):
+    _, rep = _run(20, 20, steps_per_cb=5, in_flight=2)
+    assert rep.tokens == predicted(20)[0]
+    assert rep.encode_ms >= 0 and rep.wait_ms >= 0
+    assert rep.encode_ms + rep.commit_ms + rep.wait_ms <= rep.wall_ms + 0.1
 
 
 @pytest.mark.gpu
-def test_file_weights_survive_engine_recreation(torch_gpu, tmp_path):
+def test_weights_from_a_file_window(torch_gpu, tmp_path):
+    """A weights buffer mapped from page 1 of a file (page 0 is zeros): a kernel reads it, a second engine reads it
+    again, the file is never written."""
     from monolith_mi355.runtime.engine import Engine
-    path = tmp_path / "weights.pack"
     page = os.sysconf("SC_PAGESIZE")
-    values = np.arange(page // 4, dtype=np.uint32)
-    path.write_bytes(bytes(page) + values.tobytes())
-    source = r"""extern "C" __global__ void copy_weights(const unsigned* w, unsigned* out) {
-      const unsigned i = blockIdx.x * blockDim.x + threadIdx.x; out[i] = w[i] + 7u; }"""
-    program = _program(1)
-    program.buffers["weights"] = BufferSpec(page, role="weights", file=str(path), file_offset=page)
-    program.buffers["out"] = BufferSpec(page, role="arena")
-    program.kernels["copy"] = KernelSpec(source, "copy_weights")
-    program.ops = [OpSpec("copy", [(0, "weights", 0), (1, "out", 0)], (page // 4 // 128, 1, 1), (128, 1, 1), True)]
+    words = (np.arange(page // 4, dtype=np.uint32) * np.uint32(40503)) ^ np.uint32(0x5A5A5A5A)
+    path = tmp_path / "weights.pack"
+    path.write_bytes(bytes(page) + words.tobytes())
+    src = r"""extern "C" __global__ void xor_in(const unsigned* w, unsigned* out) {
+      const unsigned i = blockIdx.x * blockDim.x + threadIdx.x; out[i] = w[i] ^ 0xFFu; }"""
+    p = mixer(1)
+    p.buffers["w"] = BufferSpec(page, role="weights", file=str(path), file_offset=page)
+    p.buffers["out"] = BufferSpec(page, role="arena")
+    p.kernels["xor"] = KernelSpec(src, "xor_in")
+    p.ops = [OpSpec("xor", [(0, "w", 0), (1, "out", 0)], (page // 4 // 64, 1, 1), (64, 1, 1), True)]
     for _ in range(2):
-        engine = Engine(program)
-        engine.run(1, steps_per_cb=1, in_flight=1)
-        np.testing.assert_array_equal(np.frombuffer(engine.read("out"), dtype=np.uint32), values + 7)
-        del engine
-    assert path.read_bytes() == bytes(page) + values.tobytes()
+        eng = Engine(p)
+        eng.run(1, steps_per_cb=1, in_flight=1)
+        assert np.array_equal(np.frombuffer(eng.read("out"), np.uint32), words ^ np.uint32(0xFF))
+        del eng
+    assert path.read_bytes() == bytes(page) + words.tobytes()

@@ -291,3 +291,47 @@ def test_gqa_rejects_bad_kv_dtype():
     d = hip.MiGqaDesc(**{**base, "kv_dtype": 0})           # the int8 cache needs its scales
     assert lib.mi_gqa_decode(C.byref(d), None) == 1 and "scales" in hip.last_error()
     assert lib.mi_gqa_workspace_bytes(C.byref(hip.MiGqaDesc(**{**base, "kv_dtype": 1}))) > 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("ctx,pos,t", [(4096, 4000, 1), (4096, 3990, 8), (1024, 300, 8)])
+def test_gqa_decode_reference_packed_layout(torch_gpu, ctx, pos, t):
+    """The reference's packed projection (``nn/attention.py:52-64``): rows ``[q | k | v | gate]`` with the RoPE
+    head-dim permutation on q and k, the gate rows from their own buffer (``gate_src``), full-width RoPE pairs over
+    the permuted ``[ctx, D]`` tables and permuted q/k norm weights — against the oracle on the checkpoint layout,
+    two steps, int8 cache (its K dims held in the permuted order)."""
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    from monolith_mi355 import nn as NN
+    from oracle.fp import f32_to_bf16, bf16_to_f32
+    rng = np.random.default_rng(pos + t)
+    rot = 64
+    cfg = _cfg(rot, True, True, rng)
+    spec = NN.GQAAttention(1024, H, KV, D, rot, 1e6, EPS, prefix="", max_context=ctx)
+    perm, core = spec.row_perm(), spec.core_rows
+    hp = NN.rope_head_perm(D, rot)
+    cos_p, sin_p = (f32_to_bf16(x) for x in NN.rope_tables_permuted(1e6, D, rot, ctx))
+    half = rot // 2
+    # the oracle's hf tables [ctx, rot] = cat(freqs, freqs): the same angles, so the same BF16 values
+    cfg["tables"] = tuple(np.concatenate([bf16_to_f32(x[:, :half])] * 2, axis=1) for x in (cos_p, sin_p))
+    kc, ks, vc, vs = _filled_cache(rng, ctx, pos)
+    cache = kernels.KVCache(KV, ctx)
+    _upload(torch, cache, kc[:, :, hp], ks, vc, vs)
+    dev = lambda a: torch.from_numpy(a.astype(np.int16)).view(torch.bfloat16).cuda()
+    qn = torch.from_numpy((1 + cfg["q_norm"])[hp].astype(np.float32)).cuda()
+    kn = torch.from_numpy((1 + cfg["k_norm"])[hp].astype(np.float32)).cuda()
+    n1 = H * 2 * D + 2 * KV * D
+    for step in range(2):
+        print(f"packed layout ctx={ctx} pos={pos} t={t} step {step}", flush=True)
+        proj = rbf(rng.standard_normal((t, n1)))
+        ref = ON.gqa_mix(proj, kc, ks, vc, vs, pos, **cfg)
+        packed = to_dev_bf16(torch, np.ascontiguousarray(proj[:, perm]))
+        y = kernels.gqa_decode(packed[:, :core], cache, pos, heads=H, rope_cos=dev(cos_p), rope_sin=dev(sin_p),
+                               gate=True, q_norm=qn, k_norm=kn, eps=EPS, gate_src=packed[:, core:])
+        torch.cuda.synchronize()
+        _check_out(from_dev_bf16(y), ref, pos + t)
+        gk, gks, gv, gvs = _download(cache)
+        inv = np.argsort(hp)
+        assert np.array_equal(gv[pos: pos + t], vc[pos: pos + t]) and np.array_equal(gvs[pos: pos + t], vs[pos: pos + t])
+        assert np.abs(gk[pos: pos + t][:, :, inv].astype(int) - kc[pos: pos + t].astype(int)).max() <= 1
+        pos += t
