@@ -268,6 +268,15 @@ def main():
                                                             out=y, **prm), count, args.warmup, stream)
                 out[f"gdnstep_m{m}"] = (ms, 2 * per + 2 * conv_dim * 3 * 2 + conv_dim * 4 * 2 + 3 * hv * 4 + d * 4
                                         + m * n1 * 2 + m * hv * d * 2)
+            # the step as the M = 1 layer runs it: the conv done by the input projection's epilogue, the step reading
+            # the convolved q|k|v (pre) and the gates, the read-out left to the output projection (defer_norm)
+            pre = torch.randn(1, conv_dim, generator=gen, device=dev).to(torch.bfloat16)
+            proj = torch.randn(1, n1, generator=gen, device=dev).to(torch.bfloat16)
+            y = torch.empty(1, hv * d, dtype=torch.bfloat16, device=dev)
+            ms = timed_graph(lambda i: kernels.gdn_step(proj, None, None, recs[i % count], recs[i % count], k_heads=hk,
+                                                        v_heads=hv, out=y, pre=pre, defer_norm=True, **prm),
+                             count, args.warmup, stream)
+            out["gdnstep_pre_m1"] = (ms, 2 * per + conv_dim * 2 + 2 * hv * 2 + 3 * hv * 4 + hv * d * 2)
             del recs, convs
             torch.cuda.empty_cache()
         if args.only in (None, "attn"):
@@ -411,6 +420,9 @@ def main():
         "gdn_step_m1": dict(entry("gdnstep_m1", 1), workload="configs[3]: Gated DeltaNet step alone (hk16/hv48 x128, "
                             "conv 4, gated norm, bf16 out), rotated over >= 2 GiB of recurrent states"),
         "gdn_step_m8": entry("gdnstep_m8", 8),
+        "gdn_step_m1_conv_in_projection": dict(entry("gdnstep_pre_m1", 1), workload="the same step as the M = 1 layer "
+                                               "runs it: q|k|v already convolved by the input projection's epilogue, "
+                                               "read-out left to the output projection"),
         "int4_gateup_m1": dict(entry("int4_gateup_m1", 1), workload="affine 4-bit gate|up 34816x5120 + silu_mul"),
         "int4_gateup_m8": entry("int4_gateup_m8", 8),
         "moe_block_m1": dict(entry("moe_m1", 1), workload="MoE feed-forward: router + top-8 of 256 NVFP4 experts "

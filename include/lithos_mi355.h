@@ -159,6 +159,23 @@ typedef struct mi_gemv_desc {
   /* with route_logits: the logits row's width in elements (route_experts <= route_ld; the shared gate's column
    * route_gate_col < route_ld), so the launch never reads past the row */
   int32_t route_ld;
+  /* the Gated DeltaNet short causal conv in the input projection's epilogue (dense, m <= 2; no counterpart in the
+   * reference, whose conv runs inside gdn_mixer, gdn_mixer.metal:300-420): output rows conv_row0 ..
+   * conv_row0 + conv_channels (whole tiles) are the conv's channels q | k | v. Each is convolved over
+   * [its W-1 = 3 state inputs | the m new BF16 outputs] with its 4 BF16 taps conv_w [channels][4], as the oracle
+   * does (y = Σ w·x in order, then bf16(silu(bf16(y)))), into conv_out [m][ld_conv] (channel order; the step then
+   * reads it through mi_gdn_desc.pre), and the new state (the last 3 inputs) goes to the conv state's output slot.
+   * State slots as mi_gdn_desc: with conv_step, conv_in holds [2][channels][3], read at slot step & 1 and written
+   * at the other (conv_out_state NULL); without, conv_in / conv_out_state name them. conv_done set: no token — the
+   * state is copied unchanged and conv_out is not written. conv_w NULL = off. The projection rows are written as
+   * usual. */
+  const uint16_t* conv_w;
+  const uint16_t* conv_in;
+  uint16_t* conv_out_state;
+  uint16_t* conv_out;
+  int32_t conv_row0, conv_channels, ld_conv;
+  const uint32_t* conv_step;
+  const uint32_t* conv_done;
 } mi_gemv_desc;
 size_t mi_gemv_workspace_bytes(const mi_gemv_desc* d);   /* 0 when the plan needs none */
 int mi_gemv(const mi_gemv_desc* d, void* stream);
@@ -249,6 +266,11 @@ typedef struct mi_gdn_desc {
                                 [2][conv_dim][W-1] at conv_in (conv_out = NULL), chosen by the step's parity — read
                                 slot step & 1, write the other (gdn_mixer.metal:25-37's SLOTS = 2); the commit pass
                                 runs after the accept scan advanced step, so it reads slot (step + 1) & 1 */
+  /* the conv already done by the input projection (mi_gemv_desc.conv_*): pre [t][ld_pre] holds the convolved,
+   * SiLU'd q | k | v channels (BF16, channel order) and the step reads them instead of running the conv; the conv
+   * state is then the projection's business (conv_in / conv_out unused, may be NULL). Not with commit. NULL = off */
+  const uint16_t* pre;
+  int32_t ld_pre;
 } mi_gdn_desc;
 int mi_gdn_step(const mi_gdn_desc* d, void* stream);
 

@@ -47,6 +47,8 @@ struct GdnArgs {
   const uint32_t* done;     // the step state's stop flag, or null: when set the step takes no token
   const uint32_t* step;     // the step state's step counter, or null: conv_in is then two slots chosen by parity
   long long conv_slot;      // elements per conv-state slot
+  const uint16_t* pre;      // the convolved q|k|v [t][ld_pre] (the conv ran in the input projection), or null
+  int ld_pre;
 };
 
 // tokens this launch takes: the device count (commit pass) or t, and none once the program has stopped — with
@@ -64,7 +66,9 @@ __device__ __forceinline__ float bf(const uint16_t* p, long long i) { return bf1
 // TT: a bound on the tokens (>= a.t), so the conv waves' loads are a fixed, unconditional set
 // SC: columns per state wave — 16 (two state waves, 32 rows of the column per lane) or 8 (four state waves, 16 rows
 // per lane: half the serial work per token, for launches of several tokens)
-template <int TT, int SC>
+// PRE: the conv is done (the input projection's epilogue wrote the convolved q|k|v to a.pre): the conv waves read
+// those values instead, and the conv state is not touched
+template <int TT, int SC, bool PRE>
 __global__ __launch_bounds__(64 * (SLICE / SC + CONV_WAVES)) void gdn_step(GdnArgs a) {
   constexpr int WAVES = SLICE / SC, RG = 64 / SC, R = DK / RG;
   __shared__ float qs[TMAX][DK];   // conv → silu → L2-norm (q also /√dk)
@@ -100,7 +104,7 @@ __global__ __launch_bounds__(64 * (SLICE / SC + CONV_WAVES)) void gdn_step(GdnAr
     const int ct = tid - 64 * WAVES;
     const int tl = a.t - 1;
     const bool kw_writer = (h % rep) == 0 && sl == 0;   // the workgroup that writes its key head's q/k conv state
-    const uint16_t* slot1 = a.step ? a.conv_in + a.conv_slot : a.conv_in;
+    const uint16_t* slot1 = a.step && !PRE ? a.conv_in + a.conv_slot : a.conv_in;
     int chs[CPT], offs[CPT];
     uint2 wv[CPT];
     uint16_t cs[2][CPT][CW - 1], xp[CPT][TT];
@@ -110,6 +114,11 @@ __global__ __launch_bounds__(64 * (SLICE / SC + CONV_WAVES)) void gdn_step(GdnAr
       const int i = cidx < DK ? cidx : cidx < 2 * DK ? cidx - DK : cidx - 2 * DK;
       chs[k] = cidx < DK ? kh * DK + i : cidx < 2 * DK ? key_dim + kh * DK + i : 2 * key_dim + h * DV + sl * SLICE + i;
       offs[k] = cidx < DK ? a.q_off + kh * DK + i : cidx < 2 * DK ? a.k_off + kh * DK + i : a.v_off + h * DV + sl * SLICE + i;
+      if constexpr (PRE) {                        // the convolved values, in channel order
+#pragma unroll
+        for (int t = 0; t < TT; ++t) xp[k][t] = a.pre[(long long)min(t, tl) * a.ld_pre + chs[k]];
+        continue;
+      }
       wv[k] = *reinterpret_cast<const uint2*>(a.conv_w + (long long)chs[k] * CW);   // CW = 4 BF16 taps, 8 bytes
 #pragma unroll
       for (int j = 0; j < CW - 1; ++j) {
@@ -132,6 +141,14 @@ __global__ __launch_bounds__(64 * (SLICE / SC + CONV_WAVES)) void gdn_step(GdnAr
       const int i = cidx < DK ? cidx : cidx < 2 * DK ? cidx - DK : cidx - 2 * DK;
       float* dst = cidx < DK ? &qs[0][i] : cidx < 2 * DK ? &ks[0][i] : &vs[0][i];
       const int ld = cidx < 2 * DK ? DK : SLICE;
+      if constexpr (PRE) {
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+          if (t >= T) break;
+          dst[t * ld] = bf16_bits_to_f32(xp[k][t]);
+        }
+        continue;
+      }
       const bool writer = cidx < 2 * DK ? kw_writer : true;   // which workgroup writes this channel's conv state
       const float w[CW] = {bf16_bits_to_f32(wv[k].x & 0xFFFFu), bf16_bits_to_f32(wv[k].x >> 16),
                            bf16_bits_to_f32(wv[k].y & 0xFFFFu), bf16_bits_to_f32(wv[k].y >> 16)};
@@ -264,9 +281,12 @@ extern "C" int mi_gdn_step(const mi_gdn_desc* d, void* stream) {
   MI_REQUIRE(d->t >= 1 && d->t <= TMAX, "mi_gdn_step: t=%d must be in 1..%d", d->t, TMAX);
   MI_REQUIRE(d->dk == DK && d->dv == DV && d->conv_width == CW, "mi_gdn_step: built for dk=dv=%d, conv width %d", DK, CW);
   MI_REQUIRE(d->k_heads > 0 && d->v_heads > 0 && d->v_heads % d->k_heads == 0, "mi_gdn_step: v_heads must be a multiple of k_heads");
-  MI_REQUIRE(d->proj && d->conv_w && d->neg_exp_a && d->dt_bias && d->norm_w && d->conv_in && (d->conv_out || d->step) &&
-             d->rec_in && d->rec_out && (d->y || d->commit), "mi_gdn_step: null pointer");
-  MI_REQUIRE(d->step ? !d->conv_out : d->conv_in != d->conv_out,
+  MI_REQUIRE(d->proj && d->neg_exp_a && d->dt_bias && d->norm_w && d->rec_in && d->rec_out && (d->y || d->commit) &&
+             (d->pre || (d->conv_w && d->conv_in && (d->conv_out || d->step))), "mi_gdn_step: null pointer");
+  MI_REQUIRE(!d->pre || (!d->commit && d->t <= 2 && d->ld_pre >= 2 * d->k_heads * d->dk + d->v_heads * d->dv),
+             "mi_gdn_step: pre (the projection's conv) is for a step of at most 2 tokens, not the commit pass, with "
+             "ld_pre >= the conv channels");
+  MI_REQUIRE(d->pre || (d->step ? !d->conv_out : d->conv_in != d->conv_out),
              "mi_gdn_step: conv_in and conv_out must be distinct buffers (shared key heads); with step, conv_in holds "
              "both slots and conv_out is NULL");
   // rec_in and rec_out may alias, in the commit pass too: each workgroup holds its state columns in registers from
@@ -280,20 +300,24 @@ extern "C" int mi_gdn_step(const mi_gdn_desc* d, void* stream) {
   a.y = d->y; a.ldy = d->ld_y; a.eps = d->eps;
   a.commit = d->commit; a.t_dev = d->t_dev; a.done = d->done;
   a.step = d->step;
+  a.pre = d->pre; a.ld_pre = d->ld_pre;
   a.conv_slot = (long long)(2 * d->k_heads * d->dk + d->v_heads * d->dv) * (d->conv_width - 1);
   hipStream_t s = static_cast<hipStream_t>(stream);
   // several tokens: four state waves of 8 columns (MI_GDN_SC=16 keeps two of 16)
   static const bool narrow_ok = [] { const char* e = getenv("MI_GDN_SC"); return !(e && atoi(e) == 16); }();
   const dim3 grid(d->v_heads, NSLICE), b16(64 * (SLICE / 16 + CONV_WAVES)), b8(64 * (SLICE / 8 + CONV_WAVES));
-  if (d->t == 1) hipLaunchKernelGGL((gdn_step<1, 16>), grid, b16, 0, s, a);
-  else if (d->t <= 2) hipLaunchKernelGGL((gdn_step<2, 16>), grid, b16, 0, s, a);
+  if (d->pre) {                                 // the conv done by the projection (t <= 2)
+    if (d->t == 1) hipLaunchKernelGGL((gdn_step<1, 16, true>), grid, b16, 0, s, a);
+    else hipLaunchKernelGGL((gdn_step<2, 16, true>), grid, b16, 0, s, a);
+  } else if (d->t == 1) hipLaunchKernelGGL((gdn_step<1, 16, false>), grid, b16, 0, s, a);
+  else if (d->t <= 2) hipLaunchKernelGGL((gdn_step<2, 16, false>), grid, b16, 0, s, a);
   else if (!narrow_ok) {
-    if (d->t <= 4) hipLaunchKernelGGL((gdn_step<4, 16>), grid, b16, 0, s, a);
-    else if (d->t <= 8) hipLaunchKernelGGL((gdn_step<8, 16>), grid, b16, 0, s, a);
-    else hipLaunchKernelGGL((gdn_step<TMAX, 16>), grid, b16, 0, s, a);
-  } else if (d->t <= 4) hipLaunchKernelGGL((gdn_step<4, 8>), grid, b8, 0, s, a);
-  else if (d->t <= 8) hipLaunchKernelGGL((gdn_step<8, 8>), grid, b8, 0, s, a);
-  else hipLaunchKernelGGL((gdn_step<TMAX, 8>), grid, b8, 0, s, a);
+    if (d->t <= 4) hipLaunchKernelGGL((gdn_step<4, 16, false>), grid, b16, 0, s, a);
+    else if (d->t <= 8) hipLaunchKernelGGL((gdn_step<8, 16, false>), grid, b16, 0, s, a);
+    else hipLaunchKernelGGL((gdn_step<TMAX, 16, false>), grid, b16, 0, s, a);
+  } else if (d->t <= 4) hipLaunchKernelGGL((gdn_step<4, 8, false>), grid, b8, 0, s, a);
+  else if (d->t <= 8) hipLaunchKernelGGL((gdn_step<8, 8, false>), grid, b8, 0, s, a);
+  else hipLaunchKernelGGL((gdn_step<TMAX, 8, false>), grid, b8, 0, s, a);
   MI_TRY_HIP(hipGetLastError(), "gdn_step launch");
   if (!d->defer_norm && !d->commit) {
     hipLaunchKernelGGL(gdn_gated_norm, dim3(d->v_heads, d->t), dim3(64), 0, s, a);

@@ -80,7 +80,69 @@ struct Args {
   float* route_weights;
   int32_t* route_groups;
   int passes;               // gemv_row, dense M > 2: tokens taken MT per workgroup along grid z (0 / 1: none)
+  // gemv_row, M <= 2: the Gated DeltaNet short conv over output rows conv_row0 .. conv_row0 + conv_ch (null conv_w:
+  // off); the state in conv_in (two slots chosen by *conv_step when given) → conv_out_state, outputs in conv_out
+  const uint16_t* conv_w;
+  const uint16_t* conv_in;
+  uint16_t* conv_out_state;
+  uint16_t* conv_out;
+  int conv_row0, conv_ch, ld_conv;
+  const uint32_t* conv_step;
+  const uint32_t* conv_done;
 };
+
+// The conv's per-row inputs, loaded at the start of the launch (independent of the GEMV): the 4 taps, the W-1 = 3
+// state inputs of both slots (the slot is chosen by value, so every load is unconditional), the step and stop words
+struct ConvIn {
+  uint2 w;
+  uint16_t s[2][3];
+  uint32_t step, done;
+};
+
+__device__ __forceinline__ void conv_load(const Args& a, int ch, ConvIn& c) {
+  c.w = *reinterpret_cast<const uint2*>(a.conv_w + (long long)ch * 4);
+  const uint16_t* s1 = a.conv_step ? a.conv_in + (long long)a.conv_ch * 3 : a.conv_in;
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    c.s[0][j] = a.conv_in[(long long)ch * 3 + j];
+    c.s[1][j] = s1[(long long)ch * 3 + j];
+  }
+  c.step = a.conv_step ? *a.conv_step : 0u;
+  c.done = a.conv_done ? *a.conv_done : 0u;
+}
+
+// Channel ch's conv over [3 state inputs | the cnt new outputs x (BF16-valued)]: out_t = bf16(silu(bf16(Σ_j w_j·
+// x_{t+j}))), summed in tap order as the oracle (and gdn_step's own conv) does; the new state is the last 3 inputs.
+// Stopped (done): the state passes to the output slot unchanged and nothing else is written.
+template <int MT>
+__device__ __forceinline__ void conv_emit(const Args& a, int ch, const ConvIn& c, const float (&x)[MT], int cnt) {
+  const uint32_t rd = a.conv_step ? (c.step & 1u) : 0u;
+  uint16_t* sout = a.conv_step ? const_cast<uint16_t*>(a.conv_in) + (long long)(rd ^ 1u) * a.conv_ch * 3
+                               : a.conv_out_state;
+  float xs[3 + MT];
+#pragma unroll
+  for (int j = 0; j < 3; ++j) xs[j] = bf16_bits_to_f32(rd ? c.s[1][j] : c.s[0][j]);
+  const int T = c.done ? 0 : cnt;
+#pragma unroll
+  for (int t = 0; t < MT; ++t) xs[3 + t] = t < T ? x[t] : 0.0f;
+  const float w[4] = {bf16_bits_to_f32(c.w.x & 0xFFFFu), bf16_bits_to_f32(c.w.x >> 16),
+                      bf16_bits_to_f32(c.w.y & 0xFFFFu), bf16_bits_to_f32(c.w.y >> 16)};
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    if (t >= T) break;
+    float y = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) y = __fadd_rn(y, __fmul_rn(w[j], xs[j + t]));
+    a.conv_out[(long long)t * a.ld_conv + ch] = f32_to_bf16_bits(silu_f(round_bf16(y)));
+  }
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    float v = xs[j];
+#pragma unroll
+    for (int t = 1; t <= MT; ++t) v = (t == T) ? xs[t + j] : v;
+    sout[(long long)ch * 3 + j] = f32_to_bf16_bits(v);
+  }
+}
 
 // ---- weight decode ---------------------------------------------------------------------------------------------
 // E4M3 block-scale byte pair → (power-of-two parts, signed mantissa factors as F16)
@@ -293,6 +355,11 @@ __global__ __launch_bounds__(KW == 16 ? 640 : 1024) void gemv_row(Args a) {
   const int kwl = max(kw, 1);
   const int cols = kwl * KC;
   const uint8_t* tbase = a.w + (long long)expert * a.expert_stride + (long long)tile * a.tile_stride;
+  // the conv's inputs for wave 0's rows (a tile lies wholly inside or outside the conv channels): issued first,
+  // used in the epilogue
+  const bool conv_tile = a.conv_w && tile * 16 >= a.conv_row0 && tile * 16 < a.conv_row0 + a.conv_ch;
+  ConvIn cvin{};
+  if (conv_tile && wave == 0) conv_load(a, tile * 16 + (lane & 15) - a.conv_row0, cvin);
 
   // ---- loads: activations, norm weights, scale pieces, then every weight chunk of the slice --------------------
   const int per_row = cols / 8;
@@ -581,13 +648,16 @@ __global__ __launch_bounds__(KW == 16 ? 640 : 1024) void gemv_row(Args a) {
     if (lane == 0) __hip_atomic_store(a.fold_cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   const float rs = a.row_scale != nullptr ? a.row_scale[(long long)expert * a.n_tiles * 16 + row] : 1.0f;
+  float xb[MT];                                 // the BF16 outputs (the conv's new inputs)
 #pragma unroll
   for (int t = 0; t < MT; ++t) {
     float v = vt[t];
     v *= rs;
+    xb[t] = round_bf16(v);
     const float up = __shfl_down(v, 8, 16);
     if (g == 0 && t < cnt) emit_row(a, epilogue_of(a, expert), pairs ? pairs[t] : t0 + t, cnt, tile, true, m_row, t, v, up);
   }
+  if (conv_tile && g == 0) conv_emit<MT>(a, row - a.conv_row0, cvin, xb, cnt);
 }
 
 // ---- gemv_rowp: M = 1, a workgroup over several tiles ------------------------------------------------------------------------------------------
@@ -1767,6 +1837,18 @@ int check_desc(const mi_gemv_desc* d) {
                "mi_gemv: gnorm_z must be 16-byte aligned with ld_gnorm_z %% 8 == 0 and >= k");
     MI_REQUIRE(((uintptr_t)d->gnorm_w & 15) == 0, "mi_gemv: gnorm_w must be 16-byte aligned");
   }
+  if (d->conv_w) {
+    MI_REQUIRE(!d->groups && d->m <= 2 && !d->out_f32 && d->epilogue == MI_EPI_NONE,
+               "mi_gemv: the fused conv runs on a dense projection of at most 2 tokens with a plain BF16 output");
+    MI_REQUIRE(d->conv_row0 >= 0 && d->conv_row0 % 16 == 0 && d->conv_channels > 0 && d->conv_channels % 16 == 0 &&
+                   d->conv_row0 + d->conv_channels <= d->n,
+               "mi_gemv: conv rows [%d, %d) must be whole tiles inside the %d outputs", d->conv_row0,
+               d->conv_row0 + d->conv_channels, d->n);
+    MI_REQUIRE(d->conv_in && d->conv_out && d->ld_conv >= d->conv_channels && ((uintptr_t)d->conv_w & 7) == 0 &&
+                   (d->conv_step ? !d->conv_out_state : (d->conv_out_state && d->conv_out_state != d->conv_in)),
+               "mi_gemv: the conv needs conv_in, conv_out (ld_conv >= channels), 8-byte aligned taps, and either "
+               "conv_step (two slots in conv_in) or a distinct conv_out_state");
+  }
   return MI_OK;
 }
 
@@ -2043,6 +2125,15 @@ bool wants_prenorm(const mi_gemv_desc* d) {
 }
 
 Plan make_plan(const mi_gemv_desc* d) {
+  if (d->conv_w) {                              // the conv epilogue lives in gemv_row: one tile per workgroup
+    Plan p = make_plan_fused(d);
+    if (p.kernel == 1 && p.rt > 1) {
+      p.rt = 1;
+      p.G = (d->n + 15) / 16;
+      p.lds_bytes = (size_t)p.S * p.row_wave_lds + (size_t)p.S * 2 * 4 + (size_t)p.S * p.lds_rows * 16 * 4;
+    }
+    return p.kernel == 1 ? p : Plan{};
+  }
   if (!wants_prenorm(d)) return make_plan_fused(d);
   mi_gemv_desc plain = *d;
   plain.norm_w = nullptr;
@@ -2273,6 +2364,15 @@ int gemv_impl(const mi_gemv_desc* d, void* stream, void* fixed_ws, size_t fixed_
   a.row_ld = p.row_ld;
   a.row_wave_lds = p.row_wave_lds;
   a.passes = d->groups ? 0 : p.passes;
+  a.conv_w = d->conv_w;
+  a.conv_in = d->conv_in;
+  a.conv_out_state = d->conv_out_state;
+  a.conv_out = d->conv_out;
+  a.conv_row0 = d->conv_row0;
+  a.conv_ch = d->conv_channels;
+  a.ld_conv = d->ld_conv;
+  a.conv_step = d->conv_step;
+  a.conv_done = d->conv_done;
   const size_t need = workspace_need(d, p);
   void* ws = nullptr;
   if (need) {
@@ -2303,6 +2403,7 @@ int gemv_impl(const mi_gemv_desc* d, void* stream, void* fixed_ws, size_t fixed_
     static const bool fold = !(getenv("MI_GEMV_FOLD") && getenv("MI_GEMV_FOLD")[0] == '0');
     if (p.kernel == 1 && fold && a.n_tiles <= kFoldTiles) a.fold_cnt = static_cast<uint32_t*>(ws);
   }
+  MI_REQUIRE(!d->conv_w || p.ks == 1 || a.fold_cnt, "%s: the fused conv needs the K splits folded in the kernel", name);
   const int groups = d->groups ? d->max_groups : 1;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (d->format == FMT_NVFP4) launch<FMT_NVFP4>(a, p, groups, s);

@@ -109,6 +109,11 @@ def _gemv_desc(ctx: EmitContext, op: POp, *, out_f32: bool = False):
         gw, gz, geps = gated
         scalars.update(ld_gnorm_z=ctx.ld(gz), gnorm_eps=float(geps))
         ptrs.update(gnorm_w=gw, gnorm_z=gz)
+    conv = a.get("conv")                                              # the GDN short conv in the epilogue
+    if conv is not None:
+        scalars.update(conv_row0=int(conv["row0"]), conv_channels=int(conv["channels"]), ld_conv=ctx.ld(conv["out"]))
+        ptrs.update(conv_w=conv["w"], conv_in=conv["state"], conv_out=conv["out"], conv_step=ctx.field("step"),
+                    conv_done=ctx.field("done"))
     return scalars, ptrs
 
 
@@ -124,7 +129,8 @@ def gemv(ctx: EmitContext, op: POp):
     """``gemv`` (``ops/gemv.py:1-12``): y = x·Wᵀ, the norm fused on load, residual / silu·mul epilogues."""
     scalars, ptrs = _gemv_desc(ctx, op)
     _workspace(ctx, scalars, ptrs)
-    return lib_op(ctx, "mi_gemv", hip.MiGemvDesc, scalars, ptrs, f"gemv:{op.inputs[1].name}", writes=("y",))
+    return lib_op(ctx, "mi_gemv", hip.MiGemvDesc, scalars, ptrs, f"gemv:{op.inputs[1].name}",
+                  writes=("y", "conv_in", "conv_out"))
 
 
 def lm_head(ctx: EmitContext, op: POp):
@@ -261,6 +267,9 @@ def _gdn(ctx: EmitContext, op: POp, commit: bool):
                                 step=ctx.field("step"))
     if ab is not None:                               # a|b in their own slab's output (a second storage format)
         ptrs["ab"] = ctx.buf(ab[0])
+    if a.get("pre") is not None and not commit:       # the conv ran in the input projection
+        ptrs["pre"] = a["pre"]
+        scalars["ld_pre"] = ctx.ld(a["pre"])
     if commit:
         ptrs["t_dev"] = ctx.field("checkpoint_index")
     else:

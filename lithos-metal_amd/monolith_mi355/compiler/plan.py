@@ -18,6 +18,8 @@ terms, each pass checking the pattern it folds and leaving anything else as it i
 * ``fold_norm_apply`` — a ``norm_apply`` whose output feeds only GEMVs becomes their fused input norm;
 * ``fuse_gdn`` — ``gdn_mixer`` + its ``gdn_norm`` become one ``mi_gdn_step``; at T ≤ 2 the norm moves onto the
   output projection's load (``defer``), as the hand-built layer does;
+* ``fold_gdn_conv`` — at T ≤ 2 the GDN short conv runs in the input projection's epilogue, and the step reads the
+  convolved values;
 * ``fuse_gqa`` — ``gqa_decode`` + ``gqa_merge`` become one ``mi_gqa_decode`` (the merge and the gate inside);
 * ``fuse_shared_expert`` — a MoE block whose shared expert has the routed experts' shape and sits right after them
   in the pack runs it as one more slot of the grouped launches and the combine (its weight bf16(σ(gate)) written by
@@ -300,6 +302,36 @@ def fuse_gdn(p: Plan, defer_max_t: int = 2) -> None:
         p.bump("fuse_gdn")
 
 
+def fold_gdn_conv(p: Plan) -> None:
+    """At T <= 2 the GDN short conv moves into the input projection's epilogue (``mi_gemv_desc.conv_*``): the GEMV
+    that produces the step's q|k|v rows convolves each of them where it is computed and writes the convolved values
+    to a buffer the step reads (``mi_gdn_desc.pre``); the step then skips its conv section (≈ 4 µs of dependent
+    loads at one token). The commit pass of a speculative program keeps its own conv."""
+    if p.t > 2:
+        return
+    for op in p.ops:
+        if op.kind != "gdn_mixer":
+            continue
+        a = op.attrs
+        ps = a["proj_segments"]
+        qkv_val = op.inputs[ps["in_proj_qkv"][0]]
+        root, col = p.root(qkv_val)
+        prod = next((o for o in p.ops if o.kind == "gemv" and o.outputs[0].name == root), None)
+        if prod is None or prod.attrs.get("epilogue") is not None or prod.attrs.get("row_range") is not None:
+            continue
+        n_main = 1 + max(idx for idx, _, _ in ps.values())
+        cs = op.inputs[n_main]
+        conv_w = op.inputs[n_main + 2]
+        channels = 2 * a["k_heads"] * a["dk"] + a["v_heads"] * a["dv"]
+        row0 = col + ps["in_proj_qkv"][1]
+        if row0 % 16 or channels % 16:
+            continue
+        pre = p.new_value(f"{op.outputs[0].name}.pre", (p.t, channels), "bf16")
+        prod.attrs["conv"] = dict(w=conv_w, state=cs, out=pre, row0=row0, channels=channels)
+        a["pre"] = pre
+        p.bump("fold_gdn_conv")
+
+
 def fuse_gqa(p: Plan) -> None:
     for op in list(p.ops):
         if op.kind != "gqa_decode":
@@ -400,7 +432,7 @@ def plan_moe_groups(p: Plan) -> None:
 
 
 PASSES: Tuple[Callable[[Plan], None], ...] = (merge_row_ranges, merge_adjacent_slabs, fuse_norm_stat, fold_norm_apply,
-                                              fuse_gdn, fuse_gqa, fuse_shared_expert, plan_moe_groups)
+                                              fuse_gdn, fold_gdn_conv, fuse_gqa, fuse_shared_expert, plan_moe_groups)
 
 
 def run_passes(p: Plan, passes: Sequence[Callable[[Plan], None]] = PASSES) -> Plan:

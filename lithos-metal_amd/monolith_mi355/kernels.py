@@ -77,16 +77,45 @@ def _bf16_2d(t, name, aligned=True):
 
 
 def gemv(w: PackedWeight, x, *, epilogue=None, residual=None, norm_w=None, eps: float = 1e-6, out=None,
-         stream=None, workspace=None, out_f32: bool = False, gated_norm=None):
+         stream=None, workspace=None, out_f32: bool = False, gated_norm=None, conv=None):
     """``gemv`` (``ops/gemv.py:1-12``): ``y = x·Wᵀ`` for ``x [M, K]`` bf16, M ≤ 16; ``epilogue`` None | "residual" |
     "silu_mul" (rows gate|up interleaved by 8, output N/2 columns) | "silu_mul_rounded"; ``norm_w`` = the (1 + w)
     float32 weight of a fused input RMSNorm; ``out_f32`` writes the unrounded FP32 result (``lm_head``).
     ``gated_norm = (w [128] float32, z [M, K] bf16 view, eps)`` applies the Gated DeltaNet output norm
-    (``gdn_norm``, ``nn/gdn.py:86-93``) to x per 128-column head while staging it."""
+    (``gdn_norm``, ``nn/gdn.py:86-93``) to x per 128-column head while staging it. ``conv`` runs the Gated
+    DeltaNet short conv in the epilogue (M ≤ 2): ``dict(w=taps [C, 4] bf16, state=…, out=[M, C] bf16, row0=first
+    output row of the C channels, out_state=…, step=…, done=…)`` — ``state`` is ``[C, 3]`` with ``out_state`` the
+    other slot, or both slots ``[2, C, 3]`` with ``step`` (a one-element device int32) choosing by parity; ``done`` a
+    stop flag. ``out`` then feeds :func:`gdn_step` as ``pre``."""
     d, out = _gemv_desc(w, x, epilogue=epilogue, residual=residual, norm_w=norm_w, eps=eps, out=out,
                         workspace=workspace, out_f32=out_f32, gated_norm=gated_norm)
+    if conv is not None:
+        _gemv_conv(d, conv, x.shape[0], w)
     hip.call("mi_gemv", C.byref(d), hip.stream_handle(stream))
     return out
+
+
+def _gemv_conv(d, conv, m: int, w) -> None:
+    """The conv fields of a GEMV descriptor, checked."""
+    torch = _torch()
+    taps, state, cout = conv["w"], conv["state"], conv["out"]
+    ch = taps.shape[0]
+    step, out_state = conv.get("step"), conv.get("out_state")
+    if taps.dtype != torch.bfloat16 or tuple(taps.shape) != (ch, 4) or not taps.is_contiguous():
+        raise ValueError("gemv conv: w must be contiguous bf16 [C, 4]")
+    want = (2, ch, 3) if step is not None else (ch, 3)
+    for name, t in (("state", state),) + ((("out_state", out_state),) if step is None else ()):
+        if t is None or t.dtype != torch.bfloat16 or tuple(t.shape) != want or not t.is_contiguous():
+            raise ValueError(f"gemv conv: {name} must be contiguous bf16 {want}")
+    _bf16_2d(cout, "gemv conv out", aligned=False)
+    if cout.shape[0] < m or cout.shape[1] < ch:
+        raise ValueError("gemv conv: out must be [M, C]")
+    _check_flag(step, "gemv conv", "step")
+    _check_flag(conv.get("done"), "gemv conv")
+    d.conv_w, d.conv_in, d.conv_out = hip.ptr(taps), hip.ptr(state), hip.ptr(cout)
+    d.conv_out_state = hip.ptr(out_state) if step is None else 0
+    d.conv_row0, d.conv_channels, d.ld_conv = int(conv["row0"]), ch, cout.stride(0)
+    d.conv_step, d.conv_done = hip.ptr(step), hip.ptr(conv.get("done"))
 
 
 def _gemv_desc(w: PackedWeight, x, *, epilogue=None, residual=None, norm_w=None, eps: float = 1e-6, out=None,
@@ -202,7 +231,7 @@ def dequant(w: PackedWeight, expert: int = 0, stream=None):
 
 def gdn_step(proj, conv_in, conv_out, rec_in, rec_out, *, conv_w, neg_exp_a, dt_bias, norm_w, k_heads, v_heads,
              dk=128, dv=128, conv_width=4, eps=1e-6, ab=None, offsets=None, out=None, stream=None,
-             defer_norm: bool = False, commit: bool = False, t_dev=None, done=None, step=None):
+             defer_norm: bool = False, commit: bool = False, t_dev=None, done=None, step=None, pre=None):
     """``gdn_mixer`` + ``gdn_norm`` (``ops/gdn.py:1-24``) for ``proj [T, N1]`` bf16 in part order
     ``z | q | k | v | a | b`` (``nn/gdn.py:48-52``) unless ``offsets`` (z, q, k, v, a, b) says otherwise.
     Conv state ``[conv_dim, W-1]`` bf16 is read from ``conv_in`` and written to ``conv_out`` (distinct); the FP32
@@ -215,7 +244,9 @@ def gdn_step(proj, conv_in, conv_out, rec_in, rec_out, *, conv_w, neg_exp_a, dt_
     the states pass through unchanged (``gdn_mixer.metal:281,330`` return at done). ``step``: a step program's step
     counter (one-element device int32): ``conv_in`` is then both conv-state slots ``[2, conv_dim, W-1]`` and
     ``conv_out`` is None — the step reads slot ``step & 1`` and writes the other (the reference's two slots by step
-    parity), so one captured step serves every step of a replay."""
+    parity), so one captured step serves every step of a replay. ``pre``: the convolved q|k|v ``[T, conv_dim]``
+    bf16 written by the input projection's conv epilogue (``gemv(..., conv=…)``, T ≤ 2); the step then skips the
+    conv, and ``conv_in`` / ``conv_out`` may be None."""
     torch = _torch()
     _bf16_2d(proj, "gdn proj", aligned=False)
     t = proj.shape[0]
@@ -229,6 +260,11 @@ def gdn_step(proj, conv_in, conv_out, rec_in, rec_out, *, conv_w, neg_exp_a, dt_
     conv_shapes = ((("conv_in", conv_in, (2, conv_dim, conv_width - 1), torch.bfloat16),) if step is not None else
                    (("conv_in", conv_in, (conv_dim, conv_width - 1), torch.bfloat16),
                     ("conv_out", conv_out, (conv_dim, conv_width - 1), torch.bfloat16)))
+    if pre is not None:
+        _bf16_2d(pre, "gdn pre", aligned=False)
+        if commit or t > 2 or pre.shape[0] < t or pre.shape[1] < conv_dim:
+            raise ValueError("gdn_step: pre is [T, conv_dim] bf16 for a step of T <= 2 (not the commit pass)")
+        conv_shapes = tuple(c for c in conv_shapes if c[1] is not None)
     for name, tns, shape, dt in conv_shapes + (
                                  ("rec_in", rec_in, (v_heads, dk, dv), torch.float32),
                                  ("rec_out", rec_out, (v_heads, dk, dv), torch.float32),
@@ -239,8 +275,6 @@ def gdn_step(proj, conv_in, conv_out, rec_in, rec_out, *, conv_w, neg_exp_a, dt_
             raise ValueError(f"gdn_step: {name} must be a contiguous {dt} {shape}, got {tns.dtype} {tuple(tns.shape)}")
     if max(offsets[:4]) + dk > proj.shape[1] and ab is None:
         raise ValueError("gdn_step: proj is narrower than the z|q|k|v|a|b offsets")
-    if commit and rec_in.data_ptr() == rec_out.data_ptr():
-        raise ValueError("gdn_step: the commit pass needs distinct rec_in / rec_out (two state slots)")
     if t_dev is not None and (t_dev.dtype != torch.int32 or t_dev.numel() != 1):
         raise ValueError("gdn_step: t_dev must be a one-element int32 device tensor")
     _check_flag(done, "gdn_step")
@@ -251,11 +285,12 @@ def gdn_step(proj, conv_in, conv_out, rec_in, rec_out, *, conv_w, neg_exp_a, dt_
                       ld_proj=proj.stride(0), z_off=z_off, q_off=q_off, k_off=k_off, v_off=v_off, ab=hip.ptr(ab),
                       ld_ab=ab.stride(0) if ab is not None else 0, a_off=a_off, b_off=b_off, conv_w=hip.ptr(conv_w),
                       neg_exp_a=hip.ptr(neg_exp_a), dt_bias=hip.ptr(dt_bias), norm_w=hip.ptr(norm_w),
-                      conv_in=hip.ptr(conv_in), conv_out=hip.ptr(conv_out) if conv_out is not None else 0,
+                      conv_in=hip.ptr(conv_in) if conv_in is not None else 0,
+                      conv_out=hip.ptr(conv_out) if conv_out is not None else 0,
                       rec_in=hip.ptr(rec_in),
                       rec_out=hip.ptr(rec_out), y=hip.ptr(out), ld_y=out.stride(0) if out is not None else 0, eps=eps,
                       defer_norm=int(defer_norm), commit=int(commit), t_dev=hip.ptr(t_dev), done=hip.ptr(done),
-                      step=hip.ptr(step))
+                      step=hip.ptr(step), pre=hip.ptr(pre), ld_pre=pre.stride(0) if pre is not None else 0)
     hip.call("mi_gdn_step", C.byref(d), hip.stream_handle(stream))
     return out
 

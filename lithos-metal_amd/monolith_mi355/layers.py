@@ -31,6 +31,10 @@ def _torch():
 # persistent GEMV chain launch (kernels.gemv_chain) instead of one launch per GEMV. Off by default: at the 27B shapes
 # the chain measured slower (MLP 46–48 µs against 38–41 µs for the two launches)
 CHAIN_TAIL = os.environ.get("MI_LAYER_CHAIN", "0") == "1"
+# At one or two tokens the Gated DeltaNet short conv runs in the input projection's epilogue (each projection row of
+# the q|k|v channels is convolved where it is produced) and the step reads the convolved values; MI_GDN_FOLD=0 keeps
+# the conv inside gdn_step (A/B comparisons)
+FOLD_CONV = os.environ.get("MI_GDN_FOLD", "1") != "0"
 
 
 @dataclass
@@ -131,6 +135,16 @@ class GdnDecoderLayer:
         self.parity = 0
         self._bufs: Dict[int, tuple] = {}
 
+    def pre(self, m: int):
+        """The convolved q|k|v [m, conv_dim] the input projection writes when it runs the conv (m <= 2)."""
+        key = ("pre", m)
+        if key not in self._bufs:
+            self._bufs[key] = _torch().empty(m, self.conv_dim, dtype=_torch().bfloat16, device=self.rec_state.device)
+        return self._bufs[key]
+
+    def folds_conv(self, m: int, verify: bool = False) -> bool:
+        return FOLD_CONV and m <= 2 and not verify
+
     def buffers(self, m: int):
         torch = _torch()
         if m not in self._bufs:
@@ -179,17 +193,20 @@ class GdnDecoderLayer:
         program's stop flag; once set the state passes through unchanged."""
         proj, o, h1, act, h2 = self.buffers(h.shape[0])
         out = h2 if out is None else out
-        kernels.gemv(self.w_in.packed, h, norm_w=self.norm_w, eps=self.eps, out=proj)
+        cin, cout = self.conv_state[self.parity], self.conv_state[1 - self.parity]
+        fold = self.folds_conv(h.shape[0], verify)
+        pre = self.pre(h.shape[0]) if fold else None
+        conv = dict(w=self.conv_w, state=cin, out_state=cout, out=pre, row0=self.hv * self.dv, done=done) if fold else None
+        kernels.gemv(self.w_in.packed, h, norm_w=self.norm_w, eps=self.eps, out=proj, conv=conv)
         rec = self.rec_slots[self.slot]
         defer = self.defers_norm(h.shape[0])
-        cin, cout = self.conv_state[self.parity], self.conv_state[1 - self.parity]
         if verify:                              # the verify pass writes the other slots; commit() settles them
             rec_out = self._second_slot()
         else:
             rec_out = rec
         kernels.gdn_step(proj, cin, cout, rec, rec_out, conv_w=self.conv_w, neg_exp_a=self.neg_exp_a,
                          dt_bias=self.dt_bias, norm_w=self.gdn_norm_w, k_heads=self.hk, v_heads=self.hv, dk=self.dk,
-                         dv=self.dv, conv_width=self.conv, eps=self.eps, out=o, defer_norm=defer, done=done)
+                         dv=self.dv, conv_width=self.conv, eps=self.eps, out=o, defer_norm=defer, done=done, pre=pre)
         if verify:
             self._verify_proj = proj
         else:

@@ -38,7 +38,10 @@ class MiGemvDesc(C.Structure):
                 ("shared_expert", C.c_int32), ("shared_epilogue", C.c_int32), ("route_logits", C.c_void_p),
                 ("route_experts", C.c_int32), ("route_top_k", C.c_int32), ("route_renorm", C.c_int32),
                 ("route_gate_col", C.c_int32), ("route_ids", C.c_void_p), ("route_weights", C.c_void_p),
-                ("group_max_pairs", C.c_int32), ("route_ld", C.c_int32)]
+                ("group_max_pairs", C.c_int32), ("route_ld", C.c_int32), ("conv_w", C.c_void_p),
+                ("conv_in", C.c_void_p), ("conv_out_state", C.c_void_p), ("conv_out", C.c_void_p),
+                ("conv_row0", C.c_int32), ("conv_channels", C.c_int32), ("ld_conv", C.c_int32),
+                ("conv_step", C.c_void_p), ("conv_done", C.c_void_p)]
 
 
 class MiGdnDesc(C.Structure):
@@ -49,7 +52,8 @@ class MiGdnDesc(C.Structure):
                 ("neg_exp_a", C.c_void_p), ("dt_bias", C.c_void_p), ("norm_w", C.c_void_p), ("conv_in", C.c_void_p),
                 ("conv_out", C.c_void_p), ("rec_in", C.c_void_p), ("rec_out", C.c_void_p), ("y", C.c_void_p),
                 ("ld_y", C.c_int32), ("eps", C.c_float), ("defer_norm", C.c_int32), ("commit", C.c_int32),
-                ("t_dev", C.c_void_p), ("done", C.c_void_p), ("step", C.c_void_p)]
+                ("t_dev", C.c_void_p), ("done", C.c_void_p), ("step", C.c_void_p), ("pre", C.c_void_p),
+                ("ld_pre", C.c_int32)]
 
 
 MI_KV_INT8, MI_KV_BF16 = 0, 1

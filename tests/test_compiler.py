@@ -135,7 +135,8 @@ def test_emit_reference_graph(tmp_path):
                           pre0 + "mlp.down.down_proj"]
     assert names[6:11] == [pre1 + "self_attn.qkv.q_proj+k_proj+v_proj", "gqa_decode", pre1 + "self_attn.o_proj.o_proj",
                            pre1 + "mlp.gate_up.gate_proj+up_proj", pre1 + "mlp.down.down_proj"]
-    assert p.plan_report == {"merge_row_ranges": 2, "fuse_norm_stat": 5, "fuse_gdn": 1, "fuse_gqa": 1}
+    assert p.plan_report == {"merge_row_ranges": 2, "fuse_norm_stat": 5, "fuse_gdn": 1, "fold_gdn_conv": 1,
+                             "fuse_gqa": 1}
     # weights come from the pack file, by name
     weights = {n: b for n, b in p.buffers.items() if b.role == "weights"}
     assert weights and all(b.file == str(pack.dir / "weights.pack") for b in weights.values())
@@ -148,6 +149,11 @@ def test_emit_reference_graph(tmp_path):
     f = _fields(hip.MiGdnDesc, gdn)
     assert f["step"] == ("step_state", p.layout.offset("step")) and f["done"] == ("step_state", p.layout.offset("done"))
     assert f["rec_in"] == f["rec_out"] and d["defer_norm"] == 1
+    # at one token the projection runs the conv (rows 512.. of its output) and the step reads the result
+    pf = _fields(hip.MiGemvDesc, proj)
+    assert proj.meta["desc"]["conv_row0"] == 512 and proj.meta["desc"]["conv_channels"] == 1024
+    assert pf["conv_out"] == f["pre"] and pf["conv_in"][0] == "layers.0.linear_attn.conv_state"
+    assert pf["conv_step"] == ("step_state", p.layout.offset("step")) and d["ld_pre"] == 1024
     # the out_proj applies the gated norm to z, read in the projection's buffer at its row stride
     of = _fields(hip.MiGemvDesc, p.ops[3])
     assert of["gnorm_z"] == _fields(hip.MiGemvDesc, proj)["y"] and p.ops[3].meta["desc"]["ld_gnorm_z"] == 1544

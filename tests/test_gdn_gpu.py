@@ -170,18 +170,80 @@ def test_gdn_commit_replays_the_accepted_prefix(torch_gpu, n_commit, via_device)
     assert np.array_equal(rec_a.cpu().numpy(), rec)                          # the input slot is untouched
 
 
-def test_gdn_commit_needs_two_slots(torch_gpu):
+def test_gdn_commit_in_place_equals_two_slots(torch_gpu):
+    """The commit pass may write the recurrent state over its input (each workgroup holds its state columns from
+    the first load to the last store): in place gives what writing a second slot gives, bit for bit."""
     torch = torch_gpu
     from monolith_mi355 import kernels
-    hk, hv = 2, 2
+    hk, hv, t = 2, 6, 4
     rng = np.random.default_rng(3)
     dp = _dev_params(torch, _params(rng, hk, hv))
     conv_dim = 2 * hk * 128 + hv * 128
-    proj = to_dev_bf16(torch, rbf(rng.standard_normal((1, hv * 128 + conv_dim + 2 * hv))))
-    rec = torch.zeros(hv, 128, 128, device="cuda")
-    c0, c1 = torch.zeros(conv_dim, 3, dtype=torch.bfloat16, device="cuda"), torch.zeros(conv_dim, 3, dtype=torch.bfloat16, device="cuda")
-    with pytest.raises(ValueError):
-        kernels.gdn_step(proj, c0, c1, rec, rec, k_heads=hk, v_heads=hv, commit=True, **dp)
+    proj = to_dev_bf16(torch, rbf(rng.standard_normal((t, hv * 128 + conv_dim + 2 * hv))))
+    rec = torch.from_numpy((rng.standard_normal((hv, 128, 128)) * 0.1).astype(np.float32)).cuda()
+    conv = to_dev_bf16(torch, rbf(rng.standard_normal((conv_dim, 3)) * 0.5))
+    n = torch.tensor([2], dtype=torch.int32, device="cuda")
+    other, in_place = torch.zeros_like(rec), rec.clone()
+    c1, c2 = (torch.zeros(conv_dim, 3, dtype=torch.bfloat16, device="cuda") for _ in range(2))
+    kernels.gdn_step(proj, conv, c1, rec, other, k_heads=hk, v_heads=hv, commit=True, t_dev=n, eps=EPS, **dp)
+    kernels.gdn_step(proj, conv, c2, in_place, in_place, k_heads=hk, v_heads=hv, commit=True, t_dev=n, eps=EPS, **dp)
+    torch.cuda.synchronize()
+    assert torch.equal(other, in_place) and torch.equal(c1, c2) and not torch.equal(in_place, rec)
+
+
+@pytest.mark.parametrize("t", [1, 2])
+@pytest.mark.parametrize("parity", [False, True])
+def test_gdn_conv_in_the_projection_epilogue(torch_gpu, t, parity):
+    """The short conv run by the input projection (``gemv(conv=…)``, the step reading ``pre``) against the conv inside
+    the step: projection, read-out, both conv slots and the recurrent state bit for bit, over three steps — slots
+    named explicitly or chosen by the step counter — and a fourth with the stop flag set (the state passes to the
+    other slot unchanged, nothing else is written)."""
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    from monolith_mi355.layers import nvfp4_matrix
+    hk, hv, hidden = 4, 8, 1024
+    rng = np.random.default_rng(50 + t + 2 * parity)
+    p = _params(rng, hk, hv)
+    dp = _dev_params(torch, p)
+    conv_dim = 2 * hk * 128 + hv * 128
+    n1 = hv * 128 + conv_dim + 2 * hv
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5)
+    w = nvfp4_matrix(n1, hidden, gen, "cuda").packed
+    norm_w = torch.from_numpy((1 + rng.standard_normal(hidden) * 0.1).astype(np.float32)).cuda()
+    conv0 = to_dev_bf16(torch, rbf(rng.standard_normal((conv_dim, 3)) * 0.5))
+    rec0 = torch.from_numpy((rng.standard_normal((hv, 128, 128)) * 0.1).astype(np.float32)).cuda()
+    slots = {k: torch.zeros(2, conv_dim, 3, dtype=torch.bfloat16, device="cuda") for k in "ab"}
+    for k in "ab":
+        slots[k][0] = conv0
+    rec = {k: rec0.clone() for k in "ab"}
+    step = torch.zeros(1, dtype=torch.int32, device="cuda")
+    done = torch.zeros(1, dtype=torch.int32, device="cuda")
+    pre = torch.empty(t, conv_dim, dtype=torch.bfloat16, device="cuda")
+    for s in range(4):
+        if s == 3:
+            done.fill_(1)
+        h = to_dev_bf16(torch, rbf(rng.standard_normal((t, hidden))))
+        outs = {}
+        for k in "ab":
+            proj = torch.empty(t, n1, dtype=torch.bfloat16, device="cuda")
+            y = torch.zeros(t, hv * 128, dtype=torch.bfloat16, device="cuda")
+            if parity:
+                cin, cout, st = slots[k], None, dict(step=step)
+            else:
+                cin, cout, st = slots[k][s & 1], slots[k][(s + 1) & 1], {}
+            conv = None
+            if k == "b":
+                conv = dict(w=dp["conv_w"], state=cin, out_state=cout, out=pre, row0=hv * 128, done=done, **st)
+            kernels.gemv(w, h, norm_w=norm_w, eps=EPS, out=proj, conv=conv)
+            kernels.gdn_step(proj, cin, cout, rec[k], rec[k], k_heads=hk, v_heads=hv, eps=EPS, out=y, done=done,
+                             pre=pre if k == "b" else None, **st, **dp)
+            outs[k] = (proj, y)
+        torch.cuda.synchronize()
+        assert torch.equal(outs["a"][0], outs["b"][0]), s
+        assert torch.equal(outs["a"][1], outs["b"][1]), s
+        assert torch.equal(slots["a"], slots["b"]) and torch.equal(rec["a"], rec["b"]), s
+        step += 1
 
 
 def test_gdn_conv_slots_by_step_parity(torch_gpu):
