@@ -412,7 +412,7 @@ def main():
         "gemv_down_m1": dict(entry("down_m1", 1), workload="configs[1]: NVFP4 down 5120x17408 + residual"),
         "gemv_down_m8": entry("down_m8", 8),
         "gqa_core": {f"ctx{c}k_m{m}": entry(f"gqa_{c}k_m{m}", m) for c in (4, 16, 32) for m in (1, 8)},
-        "gqa_core_workload": "configs[2]: gqa_prep + gqa_decode + gqa_merge alone (24 q / 4 KV heads x 128, int8 KV, "
+        "gqa_core_workload": "configs[2]: the attention core alone (query and key preparation, cache append, attention, merge, gate) (24 q / 4 KV heads x 128, int8 KV, "
                              "q/k norm, RoPE 64 of 128, gate), position ctx-16, rotated over >= 2 GiB of KV caches",
         "gqa_core_reference_geometry": {f"ctx32k_m{m}": entry(f"gqa_ref_m{m}", m) for m in (1, 8)},
         "gqa_core_reference_geometry_workload": "the reference's attention (24 q / 4 KV heads x 256, BF16 KV cache, "

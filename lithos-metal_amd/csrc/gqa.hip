@@ -8,23 +8,25 @@
 // × bf16(σ(gate)). With the BF16 cache (the reference's own, nn/attention.py:87-89) the fresh k/v are stored as they
 // are and the scores use them directly. Head dims 128 and 256 (the reference's 27B attention layer is 24/4/256).
 //
-// MI355X design, three launches:
+// MI355X design, one launch (two where the partials are many):
 //  * Cache layout (this backend's): K [kv][ctx][D]; V [kv][ctx/64][D][64] — transposed inside blocks of 64 keys, so a
 //    P·V B tile is 8 consecutive keys of one dim and a chunk of keys is contiguous, like K's; int8 codes with f16
 //    scales [kv][ctx], or BF16 values. Every chunk is two contiguous streams read with 16- and 8-byte loads. A
 //    chunk is 64 keys (int8, D = 128) or 32 (BF16, or D = 256), sized so a wave holds one in registers and the next
 //    in flight.
-//  * gqa_prep: one wave per (head or KV head, token), all in parallel: q rows normed, roped and (int8 cache)
-//    prescaled by a power of two into F16 — the MFMA B operand, in the workspace; k/v quantized (or stored as BF16)
-//    and appended to the cache.
-//  * gqa_decode: a workgroup of 4 waves per (KV head, key range) — 8 at head dim 128 with one row tile on a long
-//    cache (one chunk per wave, two waves per SIMD); each wave streams its share of the range in chunks with the next
-//    chunk's K side prefetched into registers (4 waves). The rep·T query rows of the KV head are A
-//    tiles of v_mfma_f32_16x16x32_f16; int8 codes become exact F16 with an XOR / byte-permute / packed subtract;
-//    QKᵀ and P·V run on MFMA, the softmax online; the V scale folds into P (with a per-chunk power of two so it
-//    stays in F16 range). The BF16 cache feeds v_mfma_f32_16x16x32_bf16 as it is (q, P and the cache are all
-//    BF16-valued: the products are exact). The 4 waves fold their (O, m, l) in LDS; the workgroup writes one partial.
-//  * gqa_merge: one wave per (head, token) folds the partials in key order and applies the gate — deterministic.
+//  * gqa_decode: a workgroup of 4 waves per (KV head, key range[, row tile]) — 8 at head dim 128 with one row tile
+//    on a long cache (one chunk per wave, two waves per SIMD). Each workgroup prepares its own query rows (q
+//    RMSNorm, RoPE in registers, power-of-two prescale into F16: the MFMA B operand, in LDS); the workgroups whose
+//    range holds the step's new tokens first quantize their keys and values into the cache. Each wave streams its
+//    share of the range in chunks with the next chunk prefetched into registers. The rep·T query rows of the KV head
+//    are A tiles of v_mfma_f32_16x16x32_f16; int8 codes become exact F16 with an XOR / byte-permute / packed
+//    subtract; QKᵀ and P·V run on MFMA, the softmax online; the V scale folds into P (with a per-chunk power of two
+//    so it stays in F16 range). The BF16 cache feeds v_mfma_f32_16x16x32_bf16 as it is (q, P and the cache are all
+//    BF16-valued: the products are exact). The waves fold their (O, m, l) in LDS; the workgroup writes one partial.
+//    With at most 16 partials per KV head the last workgroup to finish (a device-scope arrival counter) merges them
+//    in group order and applies the gate.
+//  * gqa_merge: otherwise, one wave per (head, token) folds the partials in key order and applies the gate —
+//    deterministic either way.
 #include "mi_common.h"
 
 #include <algorithm>
@@ -49,12 +51,23 @@ struct GqaArgs {
   const float* q_norm; const float* k_norm;     // (1 + w), [D]
   float eps, scaling;
   void* kc; uint16_t* ks; void* vc; uint16_t* vs;   // int8 codes + f16 scales, or BF16 values (no scales)
-  uint16_t* qf; float* qsc;                     // [kv][64][D] query rows (F16 prescaled, or BF16), [kv][64] 2^p
-  float* part_o; float* part_ml;                // [kv][group][rows][D], [kv][group][rows][2]
+  float* part_o; float* part_ml;                // [kv][group][rows][D], [kv][rows][group][2]
+  uint32_t* cnt;                                // [kv] arrival counters (zero between calls) for the in-kernel merge
+  uint16_t* qf; float* qsc;                     // gqa_prep's query rows [kv][64][D] (F16 prescaled, or BF16) and
+                                                // their 2^p [kv][64]; null: each decode workgroup prepares its own
+  int fmerge;                                   // 1: the last workgroup of a KV head to finish merges its partials
   uint16_t* y; int ldy;
   const int32_t* pos_dev;                       // device-resident position (a step program's StepState), or null
   const uint32_t* done;                         // the step state's stop flag, or null: set = append nothing
 };
+
+// A workgroup barrier that orders LDS only: the waves' outstanding global loads (the next chunks in flight) stay in
+// flight across it, where __syncthreads' release would first wait for every one of them.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 
 __device__ __forceinline__ bool stopped(const GqaArgs& a) { return a.done && *a.done; }
 
@@ -105,10 +118,13 @@ __device__ __forceinline__ void load_head(const GqaArgs& a, const uint16_t* src,
   }
 }
 
-// the vector after the optional (1+w) RMSNorm and partial RoPE, into dst[D] (BF16 values as f32); the whole wave
-// cooperates
+// The vector after the optional (1+w) RMSNorm and partial RoPE (BF16 values as f32), in the lane's registers
+// (o[u]: dim lane + 64·u). RoPE pairs dim i with i ± rot/2: at rot/2 = 32 that is lane l ^ 32 of the same register (a
+// lane swap), at a multiple of 64 the same lane's register u ± rot/128; other rotary widths go through tmp[D] (the
+// wave's LDS scratch).
 template <int DH>
-__device__ void prep_vec(const GqaArgs& a, const HeadIn<DH>& in, float* dst, int lane) {
+__device__ __forceinline__ void norm_rope(const GqaArgs& a, const HeadIn<DH>& in, float (&o)[DH / 64], float* tmp,
+                                          int lane) {
   constexpr int U = DH / 64;
   float x[U];
 #pragma unroll
@@ -121,37 +137,54 @@ __device__ void prep_vec(const GqaArgs& a, const HeadIn<DH>& in, float* dst, int
 #pragma unroll
     for (int u = 0; u < U; ++u) x[u] = round_bf16((x[u] * r) * in.w[u]);
   }
-#pragma unroll
-  for (int u = 0; u < U; ++u) dst[lane + 64 * u] = x[u];
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  __builtin_amdgcn_wave_barrier();
   const int half = a.rot / 2;
-  float o[U];
+  float pr[U];                                          // the partner dim's value
+  if (half == 32) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(x[u]), __float_as_int(x[u]), false, false);
+      pr[u] = __int_as_float((lane & 32) ? r[0] : r[1]);
+    }
+  } else if ((half & 63) == 0) {
+    const int sh = half >> 6;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float v = 0.0f;
+#pragma unroll
+      for (int q = 0; q < U; ++q) v = (q == u + sh || q == u - sh) && (q == u + sh) == (u < sh) ? x[q] : v;
+      pr[u] = v;
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < U; ++u) tmp[lane + 64 * u] = x[u];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = lane + 64 * u;
+      pr[u] = i < a.rot ? tmp[i < half ? i + half : i - half] : 0.0f;
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int i = lane + 64 * u;
     if (i < a.rot) {
-      const float rot = i < half ? -dst[i + half] : dst[i - half];
+      const float rot = i < half ? -pr[u] : pr[u];
       o[u] = round_bf16(round_bf16(x[u] * in.c[u]) + round_bf16(rot * in.s[u]));
     } else {
       o[u] = x[u];
     }
   }
-  __builtin_amdgcn_wave_barrier();
-#pragma unroll
-  for (int u = 0; u < U; ++u) dst[lane + 64 * u] = o[u];
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  __builtin_amdgcn_wave_barrier();
 }
 
-// store a BF16-valued vector src[D] (LDS) as one cache row (wave cooperative): int8 codes at codes + stride·i and the
-// f16 scale at *scale_out, or BF16 values at values + stride·i
+// store a BF16-valued vector (registers, dims lane + 64·u) as one cache row (wave cooperative): int8 codes at
+// codes + stride·i and the f16 scale at *scale_out, or BF16 values at values + stride·i
 template <int DH, bool BF>
-__device__ void store_row(const float* src, void* dst, long long stride, uint16_t* scale_out, int lane) {
+__device__ __forceinline__ void store_row(const float (&x)[DH / 64], void* dst, long long stride, uint16_t* scale_out,
+                                          int lane) {
   constexpr int U = DH / 64;
-  float x[U];
-#pragma unroll
-  for (int u = 0; u < U; ++u) x[u] = src[lane + 64 * u];
   if constexpr (BF) {
 #pragma unroll
     for (int u = 0; u < U; ++u) static_cast<uint16_t*>(dst)[stride * (lane + 64 * u)] = f32_to_bf16_bits(x[u]);
@@ -189,62 +222,174 @@ __device__ __forceinline__ int prescale_exp(float mx) {   // 2^-p·mx in [2^14, 
 // and dim for a 64-key int8 chunk.
 __device__ __forceinline__ int vblock_pos(int k) { return ((k & 15) >> 2) * 16 + (k >> 5) * 8 + ((k >> 4) & 1) * 4 + (k & 3); }
 
+// Query row `row` of KV head j (row = token·rep + head within the group): its inputs (issued, not waited for).
+template <int DH>
+__device__ __forceinline__ void load_q(const GqaArgs& a, int j, int row, int pos, int lane, HeadIn<DH>& in) {
+  const int q_cols = a.gate && !a.gsrc ? 2 * DH : DH;
+  const int t = row / a.rep, h = j * a.rep + (row - t * a.rep);
+  // a device position past the cache (a stopped program's queued steps) must not read past the RoPE tables
+  load_head<DH>(a, a.proj + (long long)t * a.ldp + h * q_cols, a.q_norm, min(pos + t, a.ctx - 1), lane, in);
+}
+
+// The query row normed, roped and — int8 cache — prescaled by a power of two into F16 (exact above 2^-14 of the
+// row's max; its 2^p to *sc), or BF16 as it is (the BF16 MFMA takes it exactly), into dst[D] (LDS); tmp[D]: the
+// wave's LDS scratch.
+template <int DH, bool BF>
+__device__ void finish_q(const GqaArgs& a, const HeadIn<DH>& in, float* tmp, uint16_t* dst, float* sc, int lane) {
+  constexpr int U = DH / 64;
+  float o[U];
+  norm_rope<DH>(a, in, o, tmp, lane);
+  if constexpr (BF) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) dst[lane + 64 * u] = f32_to_bf16_bits(o[u]);
+    if (lane == 0) *sc = 1.0f;
+  } else {
+    float m = 0.0f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) m = fmaxf(m, fabsf(o[u]));
+    const int p = prescale_exp(wave_max(m));
+    const float inv = pow2f(-p);
+#pragma unroll
+    for (int u = 0; u < U; ++u) dst[lane + 64 * u] = __builtin_bit_cast(uint16_t, (f16_t)(o[u] * inv));
+    if (lane == 0) *sc = pow2f(p);
+  }
+}
+
+// Token t's key and value rows of KV head j: their inputs (issued, not waited for).
+template <int DH>
+struct KvIn {
+  HeadIn<DH> k;
+  float v[DH / 64];
+};
+template <int DH>
+__device__ __forceinline__ void load_kv(const GqaArgs& a, int j, int t, int pos, int lane, KvIn<DH>& in) {
+  const int q_cols = a.gate && !a.gsrc ? 2 * DH : DH;
+  const uint16_t* row = a.proj + (long long)t * a.ldp;
+  load_head<DH>(a, row + a.heads * q_cols + j * DH, a.k_norm, min(pos + t, a.ctx - 1), lane, in.k);
+  const uint16_t* v = row + a.heads * q_cols + a.kv * DH + j * DH;
+#pragma unroll
+  for (int u = 0; u < DH / 64; ++u) in.v[u] = bfv(v, lane + 64 * u);
+}
+
+// ... appended to the cache: the key normed and roped, both quantized to int8 codes + f16 scale (or stored as BF16)
+template <int DH, bool BF>
+__device__ void append_kv(const GqaArgs& a, int j, int t, int pos, const KvIn<DH>& in, float* tmp, int lane) {
+  constexpr int U = DH / 64;
+  const int p = pos + t;
+  if (p >= a.ctx) return;                         // past the cache (a device position the host cannot check)
+  constexpr int ES = BF ? 2 : 1;                  // bytes per cache element
+  char* kc = static_cast<char*>(a.kc);
+  char* vc = static_cast<char*>(a.vc);
+  float k[U];
+  norm_rope<DH>(a, in.k, k, tmp, lane);
+  store_row<DH, BF>(k, kc + ((long long)j * a.ctx + p) * DH * ES, 1, a.ks ? a.ks + (long long)j * a.ctx + p : nullptr,
+                    lane);
+  store_row<DH, BF>(in.v, vc + (((long long)j * a.ctx + (p & ~(BLOCK - 1))) * DH + vblock_pos(p & (BLOCK - 1))) * ES,
+                    BLOCK, a.vs ? a.vs + (long long)j * a.ctx + p : nullptr, lane);
+}
+
+// The separate preparation launch, where in-workgroup preparation would cost more than a launch (many rows per
+// workgroup, or more workgroups than one round of CUs): one wave per (head or KV head, token) — a query row into
+// the workspace, or a token's key and value into the cache.
 template <int DH, bool BF>
 __global__ __launch_bounds__(64) void gqa_prep(GqaArgs a) {
-  constexpr int U = DH / 64;
   __shared__ float tmp[DH];
   const int lane = threadIdx.x, x = blockIdx.x, t = blockIdx.y;
   if (stopped(a)) return;
-  const int q_cols = a.gate && !a.gsrc ? 2 * DH : DH;
-  const uint16_t* row = a.proj + (long long)t * a.ldp;
   const int pos = cur_pos(a);
-  // a device position past the cache (a stopped program's queued steps) must not read past the RoPE tables
-  const int pr = min(pos + t, a.ctx - 1);
-  HeadIn<DH> in;
   if (x < a.heads) {
-    load_head<DH>(a, row + x * q_cols, a.q_norm, pr, lane, in);
-    __builtin_amdgcn_sched_barrier(0);
-    const int j = x / a.rep, qrow = t * a.rep + (x - j * a.rep);
-    prep_vec<DH>(a, in, tmp, lane);
-    uint16_t* dst = a.qf + ((long long)j * MAXROWS + qrow) * DH;
-    if constexpr (BF) {                           // BF16 rows as they are (the BF16 MFMA takes them exactly)
-#pragma unroll
-      for (int u = 0; u < U; ++u) dst[lane + 64 * u] = f32_to_bf16_bits(tmp[lane + 64 * u]);
-      if (lane == 0) a.qsc[j * MAXROWS + qrow] = 1.0f;
-    } else {                                      // F16 prescaled by a power of two (exact above 2^-14 of the max)
-      float m = 0.0f;
-#pragma unroll
-      for (int u = 0; u < U; ++u) m = fmaxf(m, fabsf(tmp[lane + 64 * u]));
-      const int p = prescale_exp(wave_max(m));
-      const float inv = pow2f(-p);
-#pragma unroll
-      for (int u = 0; u < U; ++u) dst[lane + 64 * u] = __builtin_bit_cast(uint16_t, (f16_t)(tmp[lane + 64 * u] * inv));
-      if (lane == 0) a.qsc[j * MAXROWS + qrow] = pow2f(p);
-    }
+    const int j = x / a.rep, row = t * a.rep + (x - j * a.rep);
+    HeadIn<DH> in;
+    load_q<DH>(a, j, row, pos, lane, in);
+    finish_q<DH, BF>(a, in, tmp, a.qf + ((long long)j * MAXROWS + row) * DH, a.qsc + j * MAXROWS + row, lane);
   } else {
-    const int j = x - a.heads, p = pos + t;
-    if (p >= a.ctx) return;                       // past the cache (a device position the host cannot check)
-    // the key's inputs and the value row, all loaded before any is used
-    load_head<DH>(a, row + a.heads * q_cols + j * DH, a.k_norm, pr, lane, in);
-    const uint16_t* v = row + a.heads * q_cols + a.kv * DH + j * DH;
-    float vv[U];
+    KvIn<DH> in;
+    load_kv<DH>(a, x - a.heads, t, pos, lane, in);
+    append_kv<DH, BF>(a, x - a.heads, t, pos, in, tmp, lane);
+  }
+}
+
+// ---- device-scope (coherent across the XCDs' L2s) partial stores and loads, for the in-kernel merge -------------
+__device__ __forceinline__ void st_dev(float* p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev2(float* p, float x, float y) {
+  __hip_atomic_store(reinterpret_cast<unsigned long long*>(p),
+                     (unsigned long long)__float_as_uint(x) | ((unsigned long long)__float_as_uint(y) << 32),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev4(float* p, f32x4 v) {
+  auto* q = reinterpret_cast<unsigned long long*>(p);
+  __hip_atomic_store(q, (unsigned long long)__float_as_uint(v[0]) | ((unsigned long long)__float_as_uint(v[1]) << 32),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(q + 1, (unsigned long long)__float_as_uint(v[2]) | ((unsigned long long)__float_as_uint(v[3]) << 32),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long ld_dev2(const float* p) {
+  return __hip_atomic_load(reinterpret_cast<const unsigned long long*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float lo_f(unsigned long long u) { return __uint_as_float((uint32_t)u); }
+__device__ __forceinline__ float hi_f(unsigned long long u) { return __uint_as_float((uint32_t)(u >> 32)); }
+
+// The merge of KV head j's partials inside the decode launch, by the workgroup that finished last: each half-wave
+// takes rows hr, hr + 2·NW, … (lane: E = D/32 dims, the pairs 64·e + 2·lane + {0, 1}, so an 8-byte load
+// instruction reads 256 contiguous bytes); per row the common max and the weights over the groups (lane g holds
+// group g's (m, l)), l by a fixed-order half-wave sum, O in group order with every group's partial in flight at
+// once (G ≤ MG); normalize, BF16, × bf16(σ(gate)) — deterministic. The partials are read with device-scope loads:
+// they were written from other XCDs. Instruction count matters here: one wave per SIMD issues a vector instruction
+// every 4 cycles, so the loop carries no division and no per-item address arithmetic beyond one add.
+constexpr int MG = 16;          // groups the in-kernel merge takes (more: the gqa_merge launch)
+bool merge_fits(int n_groups, int rows, int nw) { return n_groups <= MG && rows <= 4 * nw; }
+
+template <int DH, int NW>
+__device__ void merge_head(const GqaArgs& a, int j, int w, int lane) {
+  constexpr int E = DH / 32, E2 = E / 2;          // dims per lane, in 8-byte loads
+  const int G = a.n_groups, hl = lane & 31, hw = lane >> 5;
+  for (int row = 2 * w + hw; row < a.rows; row += 2 * NW) {     // the two halves of a wave may end apart
+    const int t = row / a.rep, h = j * a.rep + (row - t * a.rep);
+    const uint16_t* gp = a.gsrc ? a.gsrc + (long long)t * a.ldg + h * DH
+                                : a.proj + (long long)t * a.ldp + (a.gate ? h * 2 * DH + DH : 0);
+    const float* po = a.part_o + ((long long)j * G * a.rows + row) * DH + 2 * hl;   // group g at + g·rows·D
+    const long long gstride = (long long)a.rows * DH;
+    unsigned long long it[MG][E2];
 #pragma unroll
-    for (int u = 0; u < U; ++u) vv[u] = bfv(v, lane + 64 * u);
-    __builtin_amdgcn_sched_barrier(0);
-    constexpr int ES = BF ? 2 : 1;                // bytes per cache element
-    char* kc = static_cast<char*>(a.kc);
-    char* vc = static_cast<char*>(a.vc);
-    prep_vec<DH>(a, in, tmp, lane);
-    store_row<DH, BF>(tmp, kc + ((long long)j * a.ctx + p) * DH * ES, 1, a.ks ? a.ks + (long long)j * a.ctx + p : nullptr,
-                      lane);
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
+    for (int g = 0; g < MG; ++g)
 #pragma unroll
-    for (int u = 0; u < U; ++u) tmp[lane + 64 * u] = vv[u];
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    store_row<DH, BF>(tmp, vc + (((long long)j * a.ctx + (p & ~(BLOCK - 1))) * DH + vblock_pos(p & (BLOCK - 1))) * ES,
-                      BLOCK, a.vs ? a.vs + (long long)j * a.ctx + p : nullptr, lane);
+      for (int e = 0; e < E2; ++e) it[g][e] = g < G ? ld_dev2(po + g * gstride + 64 * e) : 0ull;
+    const unsigned long long mlv = hl < G ? ld_dev2(a.part_ml + ((long long)(j * a.rows + row) * G + hl) * 2)
+                                          : 0xFF800000ull;      // (m, l) = (-inf, 0)
+    uint32_t gb[E2];                                            // the gate's BF16 pairs
+#pragma unroll
+    for (int e = 0; e < E2; ++e) gb[e] = *reinterpret_cast<const uint32_t*>(gp + 64 * e + 2 * hl);
+    const float m = lo_f(mlv);
+    const float M = max_xor16(max16(m));
+    const float wl = m == -INFINITY ? 0.0f : __expf(m - M);
+    const float l = add_xor16(sum16(wl * hi_f(mlv)));
+    float o[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) o[e] = 0.0f;
+#pragma unroll
+    for (int g = 0; g < MG; ++g) {
+      // group g's weight from lane g of this half (the two halves hold different rows)
+      const float wa = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), g));
+      const float wb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), 32 + g));
+      const float wg = hw ? wb : wa;
+#pragma unroll
+      for (int e = 0; e < E2; ++e) {
+        o[2 * e] += wg * lo_f(it[g][e]);
+        o[2 * e + 1] += wg * hi_f(it[g][e]);
+      }
+    }
+    uint16_t* yp = a.y + (long long)t * a.ldy + h * DH + 2 * hl;
+#pragma unroll
+    for (int e = 0; e < E2; ++e) {
+      float y0 = round_bf16(o[2 * e] / l), y1 = round_bf16(o[2 * e + 1] / l);
+      if (a.gate) {
+        y0 = round_bf16(y0 * round_bf16(1.0f / (1.0f + __expf(-bf16_bits_to_f32((uint16_t)(gb[e] & 0xFFFF))))));
+        y1 = round_bf16(y1 * round_bf16(1.0f / (1.0f + __expf(-bf16_bits_to_f32((uint16_t)(gb[e] >> 16))))));
+      }
+      *reinterpret_cast<uint32_t*>(yp + 64 * e) = f32_to_bf16_bits(y0) | ((uint32_t)f32_to_bf16_bits(y1) << 16);
+    }
   }
 }
 
@@ -325,7 +470,7 @@ __device__ __forceinline__ float f16_hi(uint32_t u) { return (float)__builtin_bi
 // lane owns one query row (row = 16·rt + m16): Sᵀ = K·Qᵀ (A = the K tile, B = the query rows), softmax over the
 // lane's keys plus the lanes l ^ 16, l ^ 32, l ^ 48 of the same row, and Oᵀ += Vᵀ·Pᵀ with Pᵀ straight from the score
 // registers (no LDS round trip) — every per-row quantity is lane-local.
-template <int RT, int DH, bool BF, int NW>
+template <int RT, int DH, bool BF, int NW, bool OWN>
 __global__ __launch_bounds__(64 * NW, 1) void gqa_decode(GqaArgs a) {
   using G = Geo<DH, BF>;
   using OpT = typename std::conditional<BF, bf16x8, f16x8>::type;
@@ -336,6 +481,10 @@ __global__ __launch_bounds__(64 * NW, 1) void gqa_decode(GqaArgs a) {
   __shared__ __attribute__((aligned(16))) float red[TREE ? 1 : RT * 16][DH + 4];   // the workgroup's O, row-major
   __shared__ __attribute__((aligned(16))) float slab[TREE ? NW - 1 : 1][16][DH + 4];
   __shared__ float mls[NW][RT * 16][2];
+  __shared__ __attribute__((aligned(16))) uint16_t qs[RT * 16][DH];   // the workgroup's query rows (B operands)
+  __shared__ float qss[RT * 16];                                      // their 2^p (int8 cache)
+  __shared__ float ptmp[NW][DH];                                      // each wave's scratch for the row preparation
+  __shared__ uint32_t last_in;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: the key range is a scalar loop
   // the workgroup's (key range g, KV head j, row-tile group zt): from the grid, or — row tiles spread over
@@ -363,27 +512,51 @@ __global__ __launch_bounds__(64 * NW, 1) void gqa_decode(GqaArgs a) {
   const int k_end = min(ke, kb + ((w + 1) * nch / NW) * CH);
   const int m16 = lane & 15, kg = lane >> 4;
 
-  // the query rows as B tiles (k-permuted: lane holds dims (DH/4)·kg + 8·s + i of row r0 + 16·rt + m16), zero past
-  // rows; r0: the first of this workgroup's row tiles (blockIdx.z > 0 when the row tiles are split over workgroups)
-  const int r0 = zt * RT * 16;
+  const int r0 = zt * RT * 16;                          // this workgroup's first query row
   const int nrows = min(RT * 16, a.rows - r0);
+  // The query rows are prepared in every workgroup (norm, RoPE, prescale: a few hundred bytes of input per row);
+  // the workgroups whose key range holds new tokens first append the tokens' keys and values to the cache (the same
+  // bytes in every such workgroup; the tokens spread over the waves), so that their own reads of the range see
+  // them. The wave's query rows (at most 16) have their inputs issued ahead of the chunk loads, and are finished
+  // while those are in flight. (Appending by the one wave whose keys they are, with no workgroup barrier, measured
+  // slower: 4K M = 1 13.0 vs 12.3 µs, M = 8 20.9 vs 15.1 µs.)
+  constexpr int QB = (RT * 16 + NW - 1) / NW;
+  static_assert(QB <= 16, "a wave prepares at most 16 query rows");
+  constexpr bool own = OWN;                             // the rows (and the append) are this launch's, or gqa_prep's
+  HeadIn<DH> qin[own ? QB : 1];
+  // the query rows as B tiles (k-permuted: lane holds dims (DH/4)·kg + 8·s + i of row r0 + 16·rt + m16), zero past
+  // rows: from LDS once this workgroup has prepared them, or straight from gqa_prep's workspace
   OpT qb[RT][G::NS];
   float rsc[RT];                                        // the lane's row: 2^p of its prescale (int8 cache)
   int qlim[RT];                                         // the lane's row: last key it may see (causal)
+  if constexpr (own) {
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    const int row = r0 + rt * 16 + m16;
-    const bool ok = row < a.rows;
-    const uint16_t* src = a.qf + ((long long)j * MAXROWS + (ok ? row : 0)) * DH + (DH / 4) * kg;
+    for (int i = 0; i < QB; ++i) load_q<DH>(a, j, r0 + min(w + NW * i, nrows - 1), pos, lane, qin[i]);
+  } else {
 #pragma unroll
-    for (int s = 0; s < G::NS; ++s) {
-      const uint4 u = *reinterpret_cast<const uint4*>(src + 8 * s);
-      qb[rt][s] = __builtin_bit_cast(OpT, ok ? u : uint4{0u, 0u, 0u, 0u});
+    for (int rt = 0; rt < RT; ++rt) {
+      const int row = r0 + rt * 16 + m16;
+      const bool ok = row < a.rows;
+      const uint16_t* src = a.qf + ((long long)j * MAXROWS + (ok ? row : 0)) * DH + (DH / 4) * kg;
+#pragma unroll
+      for (int s = 0; s < G::NS; ++s) {
+        const uint4 u = *reinterpret_cast<const uint4*>(src + 8 * s);
+        qb[rt][s] = __builtin_bit_cast(OpT, ok ? u : uint4{0u, 0u, 0u, 0u});
+      }
+      rsc[rt] = ok ? a.qsc[j * MAXROWS + row] : 1.0f;
+      qlim[rt] = ok ? pos + row / a.rep : n_keys;       // rows past `rows` hold q = 0: finite, never written
     }
-    rsc[rt] = ok ? a.qsc[j * MAXROWS + row] : 1.0f;
-    qlim[rt] = ok ? pos + row / a.rep : n_keys;         // rows past `rows` hold q = 0: finite, never written
   }
-
+  if (own && kb < n_keys && ke > pos) {                 // workgroup-uniform: the range holds new tokens
+    constexpr int AT = (TMAX + NW - 1) / NW;          // tokens a wave appends: their inputs loaded together
+    KvIn<DH> kin[AT];
+#pragma unroll
+    for (int i = 0; i < AT; ++i) load_kv<DH>(a, j, min(w + NW * i, a.t - 1), pos, lane, kin[i]);
+#pragma unroll
+    for (int i = 0; i < AT; ++i)
+      if (w + NW * i < a.t) append_kv<DH, BF>(a, j, w + NW * i, pos, kin[i], ptmp[w], lane);
+    __syncthreads();                                    // the appended rows visible to every wave of the workgroup
+  }
   // Where the registers allow (VA), two chunks in flight: buffer A holds chunks k_begin, k_begin + 2·CH, …, B the
   // ones between, each chunk's K and V loaded one chunk ahead; otherwise each chunk is loaded as it starts.
   // Every load is issued whether or not its chunk exists (a chunk past the wave's range re-reads the last one in
@@ -398,9 +571,34 @@ __global__ __launch_bounds__(64 * NW, 1) void gqa_decode(GqaArgs a) {
     load_v<DH, BF>(a, j, kk, m16, kg, c);
     __builtin_amdgcn_sched_barrier(0);                // the loads stay here, ahead of the chunk's math
   };
-  if constexpr (VA) {
-    load_chunk(ca, k_begin);
-    load_chunk(cb, k_begin + CH);
+  // the wave's first chunk in flight while the query rows are prepared; the second (if the wave has one) is issued
+  // after them, so the rows' waits never cover the chunk loads. With more than one row tile the rows and a chunk do
+  // not fit the registers together: the rows are finished first.
+  constexpr bool QFIRST = RT > 1;
+  if constexpr (VA && !QFIRST) load_chunk(ca, k_begin);
+  if constexpr (own) {
+#pragma unroll
+    for (int i = 0; i < QB; ++i) {
+      const int r = w + NW * i;
+      if (r < nrows) finish_q<DH, BF>(a, qin[i], ptmp[w], qs[r], &qss[r], lane);
+    }
+  }
+  if constexpr (VA && QFIRST) load_chunk(ca, k_begin);
+  if constexpr (own) {
+    lds_barrier();
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const int lr = rt * 16 + m16, row = r0 + lr;
+      const bool ok = row < a.rows;
+      const uint16_t* src = &qs[ok ? lr : 0][(DH / 4) * kg];
+#pragma unroll
+      for (int s = 0; s < G::NS; ++s) {
+        const uint4 u = *reinterpret_cast<const uint4*>(src + 8 * s);
+        qb[rt][s] = __builtin_bit_cast(OpT, ok ? u : uint4{0u, 0u, 0u, 0u});
+      }
+      rsc[rt] = ok ? qss[lr] : 1.0f;
+      qlim[rt] = ok ? pos + row / a.rep : n_keys;         // rows past `rows` hold q = 0: finite, never written
+    }
   }
 
   f32x4 o[RT][G::NC];                                   // o[rt][ct][i] = O[row 16·rt + m16][dim 16·ct + 4·kg + i]
@@ -530,9 +728,14 @@ __global__ __launch_bounds__(64 * NW, 1) void gqa_decode(GqaArgs a) {
   // compiler's waits are exact; in the loop the waits of the chunk at its head drain both buffers), the rest in the
   // loop. Larger geometries do not have the registers for the extra copies of the chunk code.
   constexpr bool SL = RT == 1 && DH == 128;
+  // A wave with one chunk (every wave up to 32K keys at 4 KV heads) issues no other loads: a load left in flight
+  // past the last chunk is waited for where its registers are reused, one more memory round trip on the way out.
   if constexpr (!VA) {
     for (int k0 = k_begin; k0 < k_end; k0 += CH) process(ca, k0);
+  } else if (k_begin + CH >= k_end) {
+    if (k_begin < k_end) process(ca, k_begin);
   } else if (!SL) {
+    load_chunk(cb, k_begin + CH);
     for (int k0 = k_begin; k0 < k_end; k0 += 2 * CH) {
       process(ca, k0);
       load_chunk(ca, k0 + 2 * CH);
@@ -540,7 +743,8 @@ __global__ __launch_bounds__(64 * NW, 1) void gqa_decode(GqaArgs a) {
       process(cb, k0 + CH);
       load_chunk(cb, k0 + 3 * CH);
     }
-  } else if (k_begin < k_end) {
+  } else {
+    load_chunk(cb, k_begin + CH);
     process(ca, k_begin);
     load_chunk(ca, k_begin + 2 * CH);
     if (k_begin + CH < k_end) {
@@ -566,7 +770,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gqa_decode(GqaArgs a) {
       mls[w][rt * 16 + m16][1] = l;
     }
   }
-  __syncthreads();
+  lds_barrier();
   const float unscale = pow2f(pv_cur);
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
@@ -590,7 +794,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gqa_decode(GqaArgs a) {
         for (int ct = 0; ct < G::NC; ++ct)
           *reinterpret_cast<f32x4*>(&slab[w - 1][m16][ct * 16 + 4 * kg]) = o[0][ct];
       }
-      __syncthreads();
+      lds_barrier();
       if (w < half) {
 #pragma unroll
         for (int ct = 0; ct < G::NC; ++ct)
@@ -599,8 +803,11 @@ __global__ __launch_bounds__(64 * NW, 1) void gqa_decode(GqaArgs a) {
     }
     if (w == 0 && m16 < nrows) {                        // wave 0 holds the workgroup's O: straight to its partial
 #pragma unroll
-      for (int ct = 0; ct < G::NC; ++ct)
-        *reinterpret_cast<f32x4*>(a.part_o + (base + m16) * DH + ct * 16 + 4 * kg) = o[0][ct];
+      for (int ct = 0; ct < G::NC; ++ct) {
+        float* dst = a.part_o + (base + m16) * DH + ct * 16 + 4 * kg;
+        if (a.fmerge) st_dev4(dst, o[0][ct]);
+        else *reinterpret_cast<f32x4*>(dst) = o[0][ct];
+      }
     }
   } else {
     for (int ww = 0; ww < NW; ++ww) {
@@ -613,18 +820,39 @@ __global__ __launch_bounds__(64 * NW, 1) void gqa_decode(GqaArgs a) {
             *dst = ww == 0 ? o[rt][ct] : *dst + o[rt][ct];
           }
       }
-      __syncthreads();
+      lds_barrier();
     }
-    for (int idx = threadIdx.x; idx < nrows * DH; idx += 64 * NW) a.part_o[base * DH + idx] = red[idx / DH][idx % DH];
+    for (int idx = threadIdx.x; idx < nrows * DH; idx += 64 * NW) {
+      if (a.fmerge) st_dev(a.part_o + base * DH + idx, red[idx / DH][idx % DH]);
+      else a.part_o[base * DH + idx] = red[idx / DH][idx % DH];
+    }
   }
   for (int row = threadIdx.x; row < nrows; row += 64 * NW) {
     float M = -INFINITY, L = 0.0f;
     for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, mls[ww][row][0]);
     for (int ww = 0; ww < NW; ++ww)
       if (mls[ww][row][0] != -INFINITY) L += __expf(mls[ww][row][0] - M) * mls[ww][row][1];
-    a.part_ml[(base + row) * 2] = M;
-    a.part_ml[(base + row) * 2 + 1] = L;
+    if (a.fmerge) {
+      st_dev2(a.part_ml + ((long long)(j * a.rows + r0 + row) * a.n_groups + g) * 2, M, L);
+    } else {
+      a.part_ml[((long long)(j * a.rows + r0 + row) * a.n_groups + g) * 2] = M;
+      a.part_ml[((long long)(j * a.rows + r0 + row) * a.n_groups + g) * 2 + 1] = L;
+    }
   }
+  if (!a.fmerge) return;
+  // The in-kernel merge: the partial's device-scope stores acknowledged (every wave), then one arrival on the KV
+  // head's counter; the workgroup that brings it to the head's workgroup count merges and re-arms it. No fence: the
+  // stores were performed at the device's coherence point before the count moved, and the merge reads there.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t total = (uint32_t)(a.n_groups * max(1, a.xcd_tiles));
+    const uint32_t prev = __hip_atomic_fetch_add(a.cnt + j, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_in = prev == total - 1;
+    if (prev == total - 1) __hip_atomic_store(a.cnt + j, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  lds_barrier();
+  if (last_in) merge_head<DH, NW>(a, j, w, lane);
 }
 
 // one workgroup of MW waves per (query head, token): wave w folds partials w, w + MW, … (all its loads in flight
@@ -642,6 +870,7 @@ __global__ __launch_bounds__(64 * MW) void gqa_merge(GqaArgs a) {
   const int j = h / a.rep;
   const int row = t * a.rep + (h - j * a.rep);
   const long long b0 = (long long)j * a.n_groups * a.rows + row;      // partial g at b0 + g·rows
+  const long long mb = (long long)(j * a.rows + row) * a.n_groups;     // its (m, l) at mb + g
   // the gate first (an independent load; without a gate the row's first values are read and unused)
   const uint16_t* gp = a.gsrc ? a.gsrc + (long long)t * a.ldg + h * DH
                               : a.proj + (long long)t * a.ldp + (a.gate ? h * 2 * DH + DH : 0);
@@ -658,8 +887,9 @@ __global__ __launch_bounds__(64 * MW) void gqa_merge(GqaArgs a) {
 #pragma unroll
     for (int i = 0; i < GB; ++i) {
       const long long b = b0 + (long long)min(w + MW * i, a.n_groups - 1) * a.rows;
-      pm[i] = a.part_ml[b * 2];
-      pl[i] = a.part_ml[b * 2 + 1];
+      const long long bm = mb + min(w + MW * i, a.n_groups - 1);
+      pm[i] = a.part_ml[bm * 2];
+      pl[i] = a.part_ml[bm * 2 + 1];
 #pragma unroll
       for (int u = 0; u < U; ++u) po[i][u] = a.part_o[b * DH + lane + 64 * u];
     }
@@ -681,12 +911,12 @@ __global__ __launch_bounds__(64 * MW) void gqa_merge(GqaArgs a) {
       for (int u = 0; u < U; ++u) o[u] += wgt * po[i][u];
     }
   } else {
-    for (int g = lane; g < a.n_groups; g += 64) M = fmaxf(M, a.part_ml[(b0 + (long long)g * a.rows) * 2]);
+    for (int g = lane; g < a.n_groups; g += 64) M = fmaxf(M, a.part_ml[(mb + g) * 2]);
     M = wave_max(M);
 #pragma unroll 8
     for (int g = w; g < a.n_groups; g += MW) {
       const long long b = b0 + (long long)g * a.rows;
-      const float m = a.part_ml[b * 2], lg = a.part_ml[b * 2 + 1];
+      const float m = a.part_ml[(mb + g) * 2], lg = a.part_ml[(mb + g) * 2 + 1];
       const float wgt = m == -INFINITY ? 0.0f : __expf(m - M);
       l += wgt * lg;
 #pragma unroll
@@ -737,13 +967,25 @@ Plan plan(int pos, int kv, int rows, int nw) {
   return {std::max(1, (pos + len - 1) / len), len};
 }
 
+// The merge runs inside the decode launch (the KV head's last workgroup) where its share of partials fits one pass
+// (merge_fits); otherwise the gqa_merge launch. MI_GQA_FMERGE=0 pins the launch (comparisons).
+bool fused_merge(int n_groups, int rows, int nw, int d) {
+  const char* e = getenv("MI_GQA_FMERGE");
+  if (e && atoi(e) == 0) return false;
+  (void)d;
+  return merge_fits(n_groups, rows, nw);
+}
+
 size_t align256(size_t b) { return (b + 255) / 256 * 256; }
 
-struct Layout { size_t qf, qsc, part_o, part_ml, total; };
+// the arrival counters first, at a fixed place: a workspace shared by calls of other shapes keeps them zero
+constexpr int KVMAX = 64;
+struct Layout { size_t cnt, qf, qsc, part_o, part_ml, total; };
 Layout layout(int kv, int n_groups, int rows, int d) {
   Layout l{};
-  l.qf = 0;
-  l.qsc = align256((size_t)kv * MAXROWS * d * sizeof(uint16_t));
+  l.cnt = 0;
+  l.qf = align256(KVMAX * sizeof(uint32_t));
+  l.qsc = l.qf + align256((size_t)kv * MAXROWS * d * sizeof(uint16_t));
   l.part_o = l.qsc + align256((size_t)kv * MAXROWS * sizeof(float));
   l.part_ml = l.part_o + align256((size_t)kv * n_groups * rows * d * sizeof(float));
   l.total = l.part_ml + align256((size_t)kv * n_groups * rows * 2 * sizeof(float));
@@ -751,29 +993,54 @@ Layout layout(int kv, int n_groups, int rows, int d) {
 }
 
 template <int DH, bool BF>
-int launch(const GqaArgs& a, int rows, int nw, hipStream_t s) {
-  hipLaunchKernelGGL((gqa_prep<DH, BF>), dim3(a.heads + a.kv, a.t), dim3(64), 0, s, a);
-  MI_TRY_HIP(hipGetLastError(), "gqa_prep launch");
+int launch(const GqaArgs& a0, int rows, int nw, hipStream_t s) {
+  GqaArgs a = a0;
   const dim3 grid(a.n_groups, a.kv), block(64 * nw);
   const int rt = (rows + 15) / 16;
-  if constexpr (DH == 256) {     // one row tile per workgroup: more tiles' accumulators would spill
-    if (rt > 1) {                // a key range's row tiles on one XCD (gqa_decode's 1-D grid)
-      GqaArgs b = a;
-      b.xcd_tiles = rt;
-      const int slots = (a.n_groups * a.kv + 7) / 8 * rt;
-      hipLaunchKernelGGL((gqa_decode<1, DH, BF, kNW>), dim3(slots * 8), block, 0, s, b);
-    } else {
-      hipLaunchKernelGGL((gqa_decode<1, DH, BF, kNW>), dim3(a.n_groups, a.kv, 1), block, 0, s, a);
-    }
-  } else if (nw == 8) {          // one row tile (gqa_waves): more tiles' accumulators would spill at 2 waves / SIMD
-    hipLaunchKernelGGL((gqa_decode<1, DH, BF, 8>), grid, block, 0, s, a);
+  // Row tiles over workgroups (one tile each, a key range's tiles on one XCD) at head dim 256 — more tiles'
+  // accumulators would spill — and at 128 while the grid stays within one workgroup per CU (4K, M = 8: 192
+  // workgroups, 25.4 → 15.1 µs); MI_GQA_SPLIT=0 keeps several row tiles per workgroup at head dim 128 (comparisons).
+  const char* e = getenv("MI_GQA_SPLIT");
+  const bool split = DH == 256 || (!(e && atoi(e) == 0) && nw == kNW && (long long)a.n_groups * a.kv * rt <= 256);
+  // The query rows and the append in the decode workgroups while each prepares at most 16 rows and the grid is
+  // one round of CUs; otherwise their own launch (MI_GQA_PREP=1 forces it: comparisons).
+  const char* ep = getenv("MI_GQA_PREP");
+  const long long wgs = (long long)a.n_groups * a.kv * (split ? rt : 1);
+  const bool prep = (ep && atoi(ep) == 1) || (split ? 16 : rows) > 16 || wgs > 256;
+  if (prep) {
+    hipLaunchKernelGGL((gqa_prep<DH, BF>), dim3(a.heads + a.kv, a.t), dim3(64), 0, s, a);
+    MI_TRY_HIP(hipGetLastError(), "gqa_prep launch");
   } else {
-    if (rt == 1) hipLaunchKernelGGL((gqa_decode<1, DH, BF, kNW>), grid, block, 0, s, a);
-    else if (rt == 2) hipLaunchKernelGGL((gqa_decode<2, DH, BF, kNW>), grid, block, 0, s, a);
-    else if (rt == 3) hipLaunchKernelGGL((gqa_decode<3, DH, BF, kNW>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((gqa_decode<4, DH, BF, kNW>), grid, block, 0, s, a);
+    a.qf = nullptr;
+    a.qsc = nullptr;
+  }
+  const bool own = !prep;
+  if (split && rt > 1) {
+    GqaArgs b = a;
+    b.xcd_tiles = rt;
+    const dim3 g1((a.n_groups * a.kv + 7) / 8 * rt * 8);
+    if (own) hipLaunchKernelGGL((gqa_decode<1, DH, BF, kNW, true>), g1, block, 0, s, b);
+    else hipLaunchKernelGGL((gqa_decode<1, DH, BF, kNW, false>), g1, block, 0, s, b);
+  } else if (DH == 256 || rt == 1) {
+    bool launched = false;
+    if constexpr (DH == 128) {   // 8 waves: head dim 128, one row tile (gqa_waves)
+      if (nw == 8) {
+        if (own) hipLaunchKernelGGL((gqa_decode<1, DH, BF, 8, true>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((gqa_decode<1, DH, BF, 8, false>), grid, block, 0, s, a);
+        launched = true;
+      }
+    }
+    if (!launched) {
+      if (own) hipLaunchKernelGGL((gqa_decode<1, DH, BF, kNW, true>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((gqa_decode<1, DH, BF, kNW, false>), grid, block, 0, s, a);
+    }
+  } else if constexpr (DH == 128) {   // several row tiles per workgroup: always after gqa_prep (rows > 16)
+    if (rt == 2) hipLaunchKernelGGL((gqa_decode<2, DH, BF, kNW, false>), grid, block, 0, s, a);
+    else if (rt == 3) hipLaunchKernelGGL((gqa_decode<3, DH, BF, kNW, false>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((gqa_decode<4, DH, BF, kNW, false>), grid, block, 0, s, a);
   }
   MI_TRY_HIP(hipGetLastError(), "gqa_decode launch");
+  if (a.fmerge) return MI_OK;
   hipLaunchKernelGGL((gqa_merge<DH>), dim3(a.heads, a.t), dim3(64 * MW), 0, s, a);
   MI_TRY_HIP(hipGetLastError(), "gqa_merge launch");
   return MI_OK;
@@ -798,7 +1065,8 @@ extern "C" int mi_gqa_decode(const mi_gqa_desc* d, void* stream) {
   MI_REQUIRE(d->kv_dtype == MI_KV_INT8 || d->kv_dtype == MI_KV_BF16, "mi_gqa_decode: kv_dtype %d", d->kv_dtype);
   const bool bf = d->kv_dtype == MI_KV_BF16;
   MI_REQUIRE(d->t >= 1 && d->t <= TMAX, "mi_gqa_decode: t=%d must be in 1..%d", d->t, TMAX);
-  MI_REQUIRE(d->kv_heads > 0 && d->heads % d->kv_heads == 0, "mi_gqa_decode: heads must be a multiple of kv_heads");
+  MI_REQUIRE(d->kv_heads > 0 && d->kv_heads <= KVMAX && d->heads % d->kv_heads == 0,
+             "mi_gqa_decode: kv_heads must be in 1..%d and divide heads", KVMAX);
   const int rep = d->heads / d->kv_heads;
   const int rows = rep * d->t;
   MI_REQUIRE(rows <= 64, "mi_gqa_decode: rep·t = %d query rows per KV head exceeds 64", rows);
@@ -823,6 +1091,7 @@ extern "C" int mi_gqa_decode(const mi_gqa_desc* d, void* stream) {
   a.done = d->done;
   a.n_groups = pl.n_groups;
   a.group_len = pl.group_len;
+  a.fmerge = fused_merge(pl.n_groups, rows, nw, d->head_dim);
   a.proj = d->proj; a.ldp = d->ld_proj; a.gsrc = d->gate_src; a.ldg = d->ld_gate; a.cosb = d->rope_cos; a.sinb = d->rope_sin;
   a.q_norm = d->q_norm; a.k_norm = d->k_norm; a.eps = d->eps; a.scaling = d->scaling;
   a.kc = d->k_codes; a.vc = d->v_codes;
@@ -838,6 +1107,7 @@ extern "C" int mi_gqa_decode(const mi_gqa_desc* d, void* stream) {
   }
   const Layout L = layout(d->kv_heads, a.n_groups, rows, d->head_dim);
   char* wb = static_cast<char*>(ws);
+  a.cnt = reinterpret_cast<uint32_t*>(wb + L.cnt);
   a.qf = reinterpret_cast<uint16_t*>(wb + L.qf);
   a.qsc = reinterpret_cast<float*>(wb + L.qsc);
   a.part_o = reinterpret_cast<float*>(wb + L.part_o);
