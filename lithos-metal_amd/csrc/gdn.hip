@@ -180,10 +180,12 @@ __global__ __launch_bounds__(64 * (SLICE / SC + CONV_WAVES)) void gdn_step(GdnAr
       eg_s[ct] = expf(nea * softplus_f(bf16_bits_to_f32(aq) + dtb));
     }
   }
-  __syncthreads();
+  lds_barrier();        // LDS only: the state waves' loads stay in flight across it
 
-  // ---- L2 norms: wave w takes tokens w, w + (waves), …--------------------------------------------------------
-  for (int t = wave; t < T; t += WAVES + CONV_WAVES) {
+  // ---- L2 norms: with at most CONV_WAVES tokens the conv waves take them (while the state streams in), otherwise
+  // wave w takes tokens w, w + (waves), … ----------------------------------------------------------------------
+  const bool few = T <= CONV_WAVES;
+  for (int t = few ? wave - WAVES : wave; t >= 0 && t < T; t += few ? CONV_WAVES : WAVES + CONV_WAVES) {
     const float q0 = qs[t][lane], q1 = qs[t][lane + 64];
     const float k0 = ks[t][lane], k1 = ks[t][lane + 64];
     const float rq = 1.0f / sqrtf(wave_sum(q0 * q0 + q1 * q1) + 1e-6f);
@@ -193,7 +195,7 @@ __global__ __launch_bounds__(64 * (SLICE / SC + CONV_WAVES)) void gdn_step(GdnAr
     ks[t][lane] = k0 * rk;
     ks[t][lane + 64] = k1 * rk;
   }
-  __syncthreads();
+  lds_barrier();
   if (wave >= WAVES) return;
 
   // ---- the recurrence, token by token, state in registers. The token loop is unrolled over the bound TT and the

@@ -37,6 +37,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <type_traits>
 #include <mutex>
 #include <tuple>
 #include <vector>
@@ -853,7 +854,7 @@ void gemv_rowp(Args a) {
   const int g = lane >> 4, m_row = lane & 15;
   // tile jt from uu / ss; as soon as chunk cc is consumed, chunk cc of tile jn (the next, or jt itself at the last)
   // streams into its registers — a whole tile in flight with no second buffer
-  auto tile_dot = [&](Units<FMT> (&uu)[KW], const uint4 (&ss)[NG], int jt, int jn) {
+  auto tile_dot = [&](Units<FMT> (&uu)[KW], const uint4 (&ss)[NG], int jt, int jn, auto more) {
     float acc[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
@@ -962,7 +963,7 @@ void gemv_rowp(Args a) {
 #pragma unroll
     for (int cc = 0; cc < KW; ++cc) {
       if (cc < kw) slice_chunk(cc);
-      issue_chunk(uu, cc, jn);
+      if constexpr (decltype(more)::value) issue_chunk(uu, cc, jn);
     }
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
@@ -970,15 +971,25 @@ void gemv_rowp(Args a) {
       if (g == 0) red[((jt * S + wave) * MT + t) * 16 + m_row] = v;
     }
   };
-  // tiles in pairs, the scale pieces alternating between s0 and s1 (each loaded before the next tile's chunks)
+  // tiles in pairs, the scale pieces alternating between s0 and s1 (each loaded before the next tile's chunks). The
+  // last tile issues nothing after it: a load left in flight there is waited for where its registers are reused (a
+  // round trip on every wave's way out), so whether a call site issues the next tile is fixed at compile time.
+  using Issue = std::true_type;
+  using NoIssue = std::false_type;
   int j = 0;
-  for (; j + 1 < ntl; j += 2) {
+  for (; j + 2 < ntl; j += 2) {
     issue_scales(s1, j + 1);
-    tile_dot(u0, s0, j, j + 1);
-    issue_scales(s0, min(j + 2, ntl - 1));
-    tile_dot(u0, s1, j + 1, min(j + 2, ntl - 1));
+    tile_dot(u0, s0, j, j + 1, Issue{});
+    issue_scales(s0, j + 2);
+    tile_dot(u0, s1, j + 1, j + 2, Issue{});
   }
-  if (j < ntl) tile_dot(u0, s0, j, j);
+  if (j + 1 < ntl) {
+    issue_scales(s1, j + 1);
+    tile_dot(u0, s0, j, j + 1, Issue{});
+    tile_dot(u0, s1, j + 1, j + 1, NoIssue{});
+  } else {
+    tile_dot(u0, s0, j, j, NoIssue{});
+  }
 
   // ---- per tile: the K slices in wave order, then the epilogue (16-lane groups hold one tile's rows) -----------
   __syncthreads();
@@ -1251,17 +1262,38 @@ __global__ __launch_bounds__(768) void gemv_rowm(Args a) {
       if (j + 1 < ntl) issue(u0, s0, sb0, j + 1);
     }
   } else {
-    // tiles j and j + 1 in flight: consume one, issue j + 2 into its place. Every issue happens (past the last
-    // tile it re-reads the last tile, from L2, unused), so each tile's loads are older than exactly one tile's
-    // and its wait leaves the other tile in flight
+    // tiles j and j + 1 in flight: consume one, issue j + 2 into its place, so each tile's loads are older than
+    // exactly one tile's and its wait leaves the other tile in flight. No issue past the last tile: a load left in
+    // flight there is waited for where its registers are reused (a round trip on every wave's way out), so the
+    // tail's call sites are spelled out.
     int j = 0;
-    for (; j + 1 < ntl; j += 2) {
+    if constexpr (FMT == FMT_FP8) {             // the longer FP8 decode: the spelled-out tail spills (40 B / lane)
+      for (; j + 1 < ntl; j += 2) {
+        tile_mma(u0, s0, sb0, j);
+        issue(u0, s0, sb0, min(j + 2, ntl - 1));
+        tile_mma(u1, s1, sb1, j + 1);
+        issue(u1, s1, sb1, min(j + 3, ntl - 1));
+      }
+      if (j < ntl) tile_mma(u0, s0, sb0, j);
+    } else {
+    for (; j + 3 < ntl; j += 2) {
       tile_mma(u0, s0, sb0, j);
-      issue(u0, s0, sb0, min(j + 2, ntl - 1));
+      issue(u0, s0, sb0, j + 2);
       tile_mma(u1, s1, sb1, j + 1);
-      issue(u1, s1, sb1, min(j + 3, ntl - 1));
+      issue(u1, s1, sb1, j + 3);
     }
-    if (j < ntl) tile_mma(u0, s0, sb0, j);
+    if (j + 2 < ntl) {                          // three left: j, j + 1 in flight, j + 2 still to issue
+      tile_mma(u0, s0, sb0, j);
+      issue(u0, s0, sb0, j + 2);
+      tile_mma(u1, s1, sb1, j + 1);
+      tile_mma(u0, s0, sb0, j + 2);
+    } else if (j + 1 < ntl) {
+      tile_mma(u0, s0, sb0, j);
+      tile_mma(u1, s1, sb1, j + 1);
+    } else {
+      tile_mma(u0, s0, sb0, j);
+    }
+    }
   }
 
   // ---- per (tile, token): the K slices in the gemv_row order, then the epilogue --------------------------------

@@ -61,14 +61,6 @@ struct GqaArgs {
   const uint32_t* done;                         // the step state's stop flag, or null: set = append nothing
 };
 
-// A workgroup barrier that orders LDS only: the waves' outstanding global loads (the next chunks in flight) stay in
-// flight across it, where __syncthreads' release would first wait for every one of them.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 __device__ __forceinline__ bool stopped(const GqaArgs& a) { return a.done && *a.done; }
 
 // the cache position of the step's first new token: the descriptor's, or the one a step program keeps on the device

@@ -39,6 +39,14 @@ int mi_library_scratch(int kind, size_t bytes, hipStream_t stream, void** out);
   } while (0)
 
 // ---- BF16 / F16 bit helpers ---------------------------------------------------------------------------------------
+// A workgroup barrier that orders LDS only: the waves' outstanding global loads (the next chunks in flight) stay in
+// flight across it, where __syncthreads' release would first wait for every one of them.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t u16) { return __uint_as_float(u16 << 16); }
 
 // round-to-nearest-even, NaN kept quiet (the reference's f32_to_bf16): gfx950's v_cvt_pk_bf16_f32, branch-free
