@@ -116,6 +116,20 @@ def test_gqa_decode_baseline_contexts(torch_gpu, ctx, pos, t):
     _run(torch_gpu, np.random.default_rng(ctx + t), ctx, pos, t)
 
 
+# The launch structures the library picks among (one launch with the query rows prepared and the partials merged
+# inside it; row tiles spread over workgroups; a separate preparation or merge launch), each forced through its
+# environment switch on the same cases: every one is held to the same oracle bars.
+@pytest.mark.gpu
+@pytest.mark.parametrize("env", [{}, {"MI_GQA_FMERGE": "0"}, {"MI_GQA_SPLIT": "0"}, {"MI_GQA_PREP": "1"},
+                                 {"MI_GQA_NW": "4"}])
+@pytest.mark.parametrize("ctx,pos,t", [(4096, 4000, 1), (4096, 3990, 8), (4096, 1000, 2), (32768, 32752, 1)])
+def test_gqa_decode_launch_structures(torch_gpu, monkeypatch, env, ctx, pos, t):
+    print(f"gqa structures env={env} ctx={ctx} pos={pos} t={t}", flush=True)
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    _run(torch_gpu, np.random.default_rng(pos + t), ctx, pos, t, qk_norm=True)
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("pos", [0, 1, 63, 64, 65, 200])
 @pytest.mark.parametrize("t", [1, 3, 8])
