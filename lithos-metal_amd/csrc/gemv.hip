@@ -284,7 +284,9 @@ __device__ __forceinline__ void load_chunk(Units<FMT>& u, const uint8_t* tb, int
 // ---- gemv_row: M <= 2 ------------------------------------------------------------------------------------------
 // Workgroup = one 16-row tile (blockIdx.x) of one group (blockIdx.y, MoE); wave w = K slice [w·KW, w·KW + KW).
 // LDS: per wave xs[MT][row_ld] (INT4: then seg[MT][KW][8]) | stat[S][2] | red[S][MT][16].
-template <int FMT, int MT, int KW>
+// CONV: the launch carries the GDN conv epilogue (a separate instantiation: its registers and code stay out of the
+// plain GEMV, whose occupancy they would otherwise cut).
+template <int FMT, int MT, int KW, bool CONV>
 __global__ __launch_bounds__(KW == 16 ? 640 : 1024) void gemv_row(Args a) {
   constexpr int KC = chunk_cols(FMT);
   constexpr int NPL = MT * KW * KC / 8 / 64 > 0 ? MT * KW * KC / 8 / 64 : 1;   // activation vectors per lane
@@ -358,9 +360,11 @@ __global__ __launch_bounds__(KW == 16 ? 640 : 1024) void gemv_row(Args a) {
   const uint8_t* tbase = a.w + (long long)expert * a.expert_stride + (long long)tile * a.tile_stride;
   // the conv's inputs for wave 0's rows (a tile lies wholly inside or outside the conv channels): issued first,
   // used in the epilogue
-  const bool conv_tile = a.conv_w && tile * 16 >= a.conv_row0 && tile * 16 < a.conv_row0 + a.conv_ch;
+  const bool conv_tile = CONV && tile * 16 >= a.conv_row0 && tile * 16 < a.conv_row0 + a.conv_ch;
   ConvIn cvin{};
-  if (conv_tile && wave == 0) conv_load(a, tile * 16 + (lane & 15) - a.conv_row0, cvin);
+  if constexpr (CONV) {
+    if (conv_tile && wave == 0) conv_load(a, tile * 16 + (lane & 15) - a.conv_row0, cvin);
+  }
 
   // ---- loads: activations, norm weights, scale pieces, then every weight chunk of the slice --------------------
   const int per_row = cols / 8;
@@ -658,7 +662,9 @@ __global__ __launch_bounds__(KW == 16 ? 640 : 1024) void gemv_row(Args a) {
     const float up = __shfl_down(v, 8, 16);
     if (g == 0 && t < cnt) emit_row(a, epilogue_of(a, expert), pairs ? pairs[t] : t0 + t, cnt, tile, true, m_row, t, v, up);
   }
-  if (conv_tile && g == 0) conv_emit<MT>(a, row - a.conv_row0, cvin, xb, cnt);
+  if constexpr (CONV) {
+    if (conv_tile && g == 0) conv_emit<MT>(a, row - a.conv_row0, cvin, xb, cnt);
+  }
 }
 
 // ---- gemv_rowp: M = 1, a workgroup over several tiles ------------------------------------------------------------------------------------------
@@ -2266,7 +2272,9 @@ void launch_tk_d(const Args& a, const Plan& p, dim3 g, hipStream_t s) {
 template <int FMT, int MT, int KW>
 void launch_row_kw(const Args& a, const Plan& p, dim3 g, hipStream_t s) {
   if (MT == 1 && p.rt > 1) { allow_lds(gemv_rowp<FMT, 1, KW>); hipLaunchKernelGGL((gemv_rowp<FMT, 1, KW>), g, dim3(64 * p.S), p.lds_bytes, s, a); }
-  else { allow_lds(gemv_row<FMT, MT, KW>); hipLaunchKernelGGL((gemv_row<FMT, MT, KW>), g, dim3(64 * p.S), p.lds_bytes, s, a); }
+  else if (a.conv_w) {
+    if constexpr (MT <= 2) { allow_lds(gemv_row<FMT, MT, KW, true>); hipLaunchKernelGGL((gemv_row<FMT, MT, KW, true>), g, dim3(64 * p.S), p.lds_bytes, s, a); }
+  } else { allow_lds(gemv_row<FMT, MT, KW, false>); hipLaunchKernelGGL((gemv_row<FMT, MT, KW, false>), g, dim3(64 * p.S), p.lds_bytes, s, a); }
 }
 
 template <int FMT, int MT>
