@@ -299,7 +299,10 @@ typedef struct mi_gqa_desc {
   uint16_t* v_scales;
   uint16_t* y;
   int32_t ld_y;
-  void* workspace;           /* split partials; NULL = the library's own */
+  void* workspace;           /* key-range partials, prepared query rows and the per-KV-head arrival counters of the
+                                in-launch merge (mi_gqa_workspace_bytes; zero it once before its first use: the
+                                counters return to zero after every call; calls overlapping in time need distinct
+                                workspaces); NULL = the library's own */
   size_t workspace_bytes;
   const int32_t* pos_dev;    /* device-resident position (a step program's mi_step_state.position) or NULL = pos;
                                 the key ranges are then planned for ctx_max - t and the kernels read the position */

@@ -376,7 +376,8 @@ def gqa_decode(proj, cache: KVCache, pos, *, heads: int, rope_cos, rope_sin, gat
     ``pos`` is an int, or a one-element int32 device tensor the kernels read (a step program's StepState position:
     the same launch serves every step of a replayed graph). ``done``: a step program's stop flag (one-element device
     int32): once set, nothing is appended to the cache and ``out`` is not written. ``workspace``: a uint8 tensor of
-    ``mi_gqa_workspace_bytes`` for the key-range partials, or None for the library's own. ``gate_src``: the
+    ``mi_gqa_workspace_bytes`` (key-range partials, prepared query rows, arrival counters: zeroed once before its
+    first use; the counters return to zero after each call), or None for the library's own. ``gate_src``: the
     reference's packed layout (``nn/attention.py:52-64``) — ``proj`` holds ``q | k | v`` and the gate rows are this
     ``[T, heads·D]`` bf16 view; with the RoPE head-dim permutation the tables are ``[ctx_max, D]``."""
     torch = _torch()
