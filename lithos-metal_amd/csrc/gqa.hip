@@ -506,12 +506,13 @@ __global__ __launch_bounds__(64 * NW, 1) void gqa_decode(GqaArgs a) {
 
   const int r0 = zt * RT * 16;                          // this workgroup's first query row
   const int nrows = min(RT * 16, a.rows - r0);
-  // The query rows are prepared in every workgroup (norm, RoPE, prescale: a few hundred bytes of input per row);
+  // OWN: the query rows are prepared in every workgroup (norm, RoPE, prescale: a few hundred bytes of input per row);
   // the workgroups whose key range holds new tokens first append the tokens' keys and values to the cache (the same
   // bytes in every such workgroup; the tokens spread over the waves), so that their own reads of the range see
   // them. The wave's query rows (at most 16) have their inputs issued ahead of the chunk loads, and are finished
   // while those are in flight. (Appending by the one wave whose keys they are, with no workgroup barrier, measured
-  // slower: 4K M = 1 13.0 vs 12.3 µs, M = 8 20.9 vs 15.1 µs.)
+  // slower: 4K M = 1 13.0 vs 12.3 µs, M = 8 20.9 vs 15.1 µs.) Otherwise gqa_prep ran first: the rows come from its
+  // workspace and the cache already holds the new tokens.
   constexpr int QB = (RT * 16 + NW - 1) / NW;
   static_assert(QB <= 16, "a wave prepares at most 16 query rows");
   constexpr bool own = OWN;                             // the rows (and the append) are this launch's, or gqa_prep's
