@@ -1952,6 +1952,9 @@ Plan plan_row(const mi_gemv_desc* d, int fmt, int chunks, int rows, int n_tiles,
   int force_ks = 0, force_kw = kw_pref, force_rt = 0;
   if (const char* env = getenv("MI_GEMV_ROW"))                                   // tuning sweeps
     sscanf(env, "%d,%d,%d", &force_kw, &force_ks, &force_rt);
+  // a long single-split launch without a fused norm takes gemv_rowp too where it needs three or more tiles per
+  // resident workgroup (gate|up alone, 2176 tiles: 3–6 % faster in same-box A/B); MI_GEMV_NO_ROWP=1 keeps gemv_row
+  static const bool no_rowp = getenv("MI_GEMV_NO_ROWP") && atoi(getenv("MI_GEMV_NO_ROWP")) == 1;
   for (int ks : {1, 3, 2, 4}) {
     if (force_ks && ks != force_ks) continue;
     if (ks > 1 && d->groups) break;
@@ -1974,7 +1977,7 @@ Plan plan_row(const mi_gemv_desc* d, int fmt, int chunks, int rows, int n_tiles,
     // gemv_rowp (rt > 1 tiles per workgroup) where the input norm is fused: its statistic then costs once per
     // workgroup instead of once per tile; rt is what keeps ~every workgroup resident at once
     int rt = 1;
-    if (rows == 1 && !d->groups && (d->norm_w || force_rt)) {
+    if (rows == 1 && !d->groups && (d->norm_w || force_rt || (ks == 1 && !no_rowp))) {
       const int per_cu = row_blocks_per_cu(fmt, kw, 64 * S, lds1 + 4 * red1);
       const long long slots = (long long)cu_count() * std::max(per_cu, 1);
       rt = (int)std::min<long long>(4, std::max<long long>(1, ((long long)n_tiles * ks + slots - 1) / slots));
