@@ -500,8 +500,16 @@ __global__ __launch_bounds__(64 * NW, 1) void gqa_decode(GqaArgs a) {
   // ones past the position are empty (their partials fold in with weight 0)
   const int ke = g == a.n_groups - 1 ? n_keys : min(kb + a.group_len, n_keys);
   const int nch = max(0, (ke - kb + CH - 1) / CH);
-  const int k_begin = kb + (w * nch / NW) * CH;
-  const int k_end = min(ke, kb + ((w + 1) * nch / NW) * CH);
+  // Where the registers allow (VA), two chunks in flight per wave (see below). Otherwise, with chunks shorter than a
+  // V block (BF16 cache, or head dim 256), the waves take the range's chunks in turn (wave w: chunks w, w + NW, …):
+  // a 32-key chunk reads half of each 128-byte line of its V block, and the block's two chunks, on neighbouring
+  // waves, then request the same lines together — one chunk after the other in one wave, the line had often left
+  // the L2 before its second half was read (head dim 256, 32K, M = 1: 1.27 × the range's bytes fetched).
+  constexpr bool VA = NW == 4 && DH == 128 && (RT <= 2 || (RT == 3 && BF));   // two chunks: at most 48 loads in flight
+  constexpr bool STRIDE = !VA && CH < BLOCK;
+  const int k_begin = STRIDE ? kb + w * CH : kb + (w * nch / NW) * CH;
+  const int k_end = STRIDE ? ke : min(ke, kb + ((w + 1) * nch / NW) * CH);
+  constexpr int K_STEP = STRIDE ? NW * CH : CH;         // from one of the wave's chunks to the next
   const int m16 = lane & 15, kg = lane >> 4;
 
   const int r0 = zt * RT * 16;                          // this workgroup's first query row
@@ -555,9 +563,8 @@ __global__ __launch_bounds__(64 * NW, 1) void gqa_decode(GqaArgs a) {
   // Every load is issued whether or not its chunk exists (a chunk past the wave's range re-reads the last one in
   // range, or the range's start when it is empty — chunks lie inside the cache: ctx % 64 == 0), after the query
   // rows, so the in-order memory counter lets a chunk's wait leave the other chunk's loads outstanding.
-  constexpr bool VA = NW == 4 && DH == 128 && (RT <= 2 || (RT == 3 && BF));   // two chunks: at most 48 loads in flight
   Chunk<DH, BF> ca, cb;
-  const int k_last = k_begin < k_end ? k_begin + ((k_end - 1 - k_begin) / CH) * CH : min(k_begin, a.ctx - CH);
+  const int k_last = k_begin < k_end ? k_begin + ((k_end - 1 - k_begin) / K_STEP) * K_STEP : min(k_begin, a.ctx - CH);
   auto load_chunk = [&](Chunk<DH, BF>& c, int k0) {
     const int kk = min(k0, k_last);
     load_k<DH, BF>(a, j, kk, m16, kg, c);
@@ -731,7 +738,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gqa_decode(GqaArgs a) {
   // A wave with one chunk (every wave up to 32K keys at 4 KV heads) issues no other loads: a load left in flight
   // past the last chunk is waited for where its registers are reused, one more memory round trip on the way out.
   if constexpr (!VA) {
-    for (int k0 = k_begin; k0 < k_end; k0 += CH) process(ca, k0);
+    for (int k0 = k_begin; k0 < k_end; k0 += K_STEP) process(ca, k0);
   } else if (k_begin + CH >= k_end) {
     if (k_begin < k_end) process(ca, k_begin);
   } else if (!SL) {
