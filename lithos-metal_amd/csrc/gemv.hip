@@ -1950,8 +1950,10 @@ Plan plan_row(const mi_gemv_desc* d, int fmt, int chunks, int rows, int n_tiles,
   Plan best{};
   double best_cost = 1e30;
   int force_ks = 0, force_kw = kw_pref, force_rt = 0;
-  if (const char* env = getenv("MI_GEMV_ROW"))                                   // tuning sweeps
-    sscanf(env, "%d,%d,%d", &force_kw, &force_ks, &force_rt);
+  if (const char* env = getenv("MI_GEMV_ROW")) {                                 // tuning sweeps
+    const char* ke = getenv("MI_GEMV_ROW_K");                                    // only launches of this K
+    if (!ke || atoi(ke) == d->k) sscanf(env, "%d,%d,%d", &force_kw, &force_ks, &force_rt);
+  }
   // a long single-split launch without a fused norm takes gemv_rowp too where it needs three or more tiles per
   // resident workgroup (gate|up alone, 2176 tiles: 3–6 % faster in same-box A/B); MI_GEMV_NO_ROWP=1 keeps gemv_row
   static const bool no_rowp = getenv("MI_GEMV_NO_ROWP") && atoi(getenv("MI_GEMV_NO_ROWP")) == 1;
