@@ -287,6 +287,19 @@ def test_gqa_decode_head_dim_and_bf16_cache(torch_gpu, d, kv_dtype, ctx, pos, t)
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("d,kv_dtype,ctx,pos,t", [
+    (128, "bf16", 32768, 32700, 1),     # 8 waves of one chunk each
+    (128, "bf16", 4096, 3980, 10),      # four row tiles in one workgroup (60 query rows)
+    (256, "bf16", 32768, 32752, 1),     # the reference geometry's cache at its longest bench context
+    (256, "int8", 16384, 16000, 2)])
+def test_gqa_decode_chunks_in_turn(torch_gpu, d, kv_dtype, ctx, pos, t):
+    """Instantiations whose waves hold one 32-key chunk at a time take a key range's chunks in turn (wave w: chunks
+    w, w + waves, …, so a 64-key V block's two halves are read together); every key of the range counted once."""
+    print(f"gqa chunks in turn d={d} cache={kv_dtype} ctx={ctx} pos={pos} t={t}", flush=True)
+    _run_geometry(torch_gpu, np.random.default_rng(d + ctx + pos + t + 11), ctx, pos, t, d, kv_dtype, steps=1)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("d,kv_dtype", [(128, "bf16"), (256, "int8")])
 def test_gqa_decode_head_dim_and_bf16_cache_device_position(torch_gpu, d, kv_dtype):
     print(f"gqa d={d} cache={kv_dtype} device position", flush=True)
