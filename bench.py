@@ -432,7 +432,7 @@ def main():
         "token_loop_2layers_ctx32k": dict(entry("loop", 1), **loop_info,
                                           workload="embed + GDN layer + attention layer (32K) + BF16 lm_head 248320 "
                                                    "+ argmax + advance, graph replay through the native pump"),
-        "roofline": {"kernel": "gemv_row (NVFP4 gate|up 34816x5120, silu_mul, M=1)", "bound": "hbm",
+        "roofline": {"kernel": "gemv_rowp (NVFP4 gate|up 34816x5120, silu_mul, M=1: 768 workgroups over 2-3 tiles each)", "bound": "hbm",
                      "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes": k_bytes, "avg_launch_us": round(k_ms * 1e3, 3)},
