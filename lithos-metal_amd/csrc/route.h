@@ -10,18 +10,20 @@
 constexpr int ROUTE_MAX_PER_LANE = 8;   // E <= 512
 constexpr int ROUTE_MAX_K = 16;
 
-// the whole wave calls it; every lane ends with the same ce[0..k) / cw[0..k)
-__device__ __forceinline__ void route_topk(const uint16_t* logits, int E, int k, int renorm, int lane, int* ce,
-                                           float* cw) {
-  float v[ROUTE_MAX_PER_LANE];
-  uint16_t raw[ROUTE_MAX_PER_LANE];
+// NPL logits per lane (E <= 64·NPL); the whole wave calls it; every lane ends with the same ce[0..k) / cw[0..k)
+template <int NPL>
+__device__ __forceinline__ void route_topk_n(const uint16_t* logits, int E, int k, int renorm, int lane, int* ce,
+                                             float* cw) {
+  static_assert(NPL <= ROUTE_MAX_PER_LANE, "at most 512 experts");
+  float v[NPL];
+  uint16_t raw[NPL];
   // every load unconditional (an index past the experts re-reads the last logit, then masked), so they are all in
   // flight at once: a load whose value meets a branch is waited for there, one round trip each
 #pragma unroll
-  for (int i = 0; i < ROUTE_MAX_PER_LANE; ++i) raw[i] = logits[min(lane + 64 * i, E - 1)];
+  for (int i = 0; i < NPL; ++i) raw[i] = logits[min(lane + 64 * i, E - 1)];
   float m = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < ROUTE_MAX_PER_LANE; ++i) {
+  for (int i = 0; i < NPL; ++i) {
     const int e = lane + 64 * i;
     v[i] = e < E ? bf16_bits_to_f32(raw[i]) : -INFINITY;
     m = fmaxf(m, v[i]);
@@ -29,20 +31,20 @@ __device__ __forceinline__ void route_topk(const uint16_t* logits, int E, int k,
   m = wave_max(m);
   float s = 0.0f;
 #pragma unroll
-  for (int i = 0; i < ROUTE_MAX_PER_LANE; ++i) {
+  for (int i = 0; i < NPL; ++i) {
     const int e = lane + 64 * i;
     v[i] = e < E ? expf(v[i] - m) : 0.0f;
     s += v[i];
   }
   s = wave_sum(s);
 #pragma unroll
-  for (int i = 0; i < ROUTE_MAX_PER_LANE; ++i) v[i] = lane + 64 * i < E ? v[i] / s : -1.0f;   // -1: absent or taken
+  for (int i = 0; i < NPL; ++i) v[i] = lane + 64 * i < E ? v[i] / s : -1.0f;   // -1: absent or taken
   float wsum = 0.0f;
   for (int r = 0; r < k; ++r) {
     float best = -1.0f;
     int bi = 1 << 20;
 #pragma unroll
-    for (int i = 0; i < ROUTE_MAX_PER_LANE; ++i)
+    for (int i = 0; i < NPL; ++i)
       if (v[i] > best) { best = v[i]; bi = lane + 64 * i; }        // strictly greater: the lane's lowest index
     const float gmax = wave_max(best);
     const int e = (int)-wave_max(-(best == gmax ? (float)bi : (float)(1 << 20)));
@@ -52,13 +54,21 @@ __device__ __forceinline__ void route_topk(const uint16_t* logits, int E, int k,
       continue;
     }
 #pragma unroll
-    for (int i = 0; i < ROUTE_MAX_PER_LANE; ++i)
+    for (int i = 0; i < NPL; ++i)
       if (lane + 64 * i == e) v[i] = -1.0f;
     ce[r] = e;
     cw[r] = gmax;
     wsum += gmax;
   }
   for (int r = 0; r < k; ++r) cw[r] = round_bf16(renorm && wsum > 0.0f ? cw[r] / wsum : cw[r]);
+}
+
+// the wave's lanes hold 4 logits each up to 256 experts (the softmax and each pick's compares over half the
+// registers), 8 up to 512; the same picks and weights bit for bit (a lane's absent logits add 0 to its sum)
+__device__ __forceinline__ void route_topk(const uint16_t* logits, int E, int k, int renorm, int lane, int* ce,
+                                           float* cw) {
+  if (E <= 256) route_topk_n<4>(logits, E, k, renorm, lane, ce, cw);
+  else route_topk_n<8>(logits, E, k, renorm, lane, ce, cw);
 }
 
 // the shared expert's weight: bf16(σ(its gate's logit))
