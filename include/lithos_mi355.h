@@ -176,6 +176,15 @@ typedef struct mi_gemv_desc {
   int32_t conv_row0, conv_channels, ld_conv;
   const uint32_t* conv_step;
   const uint32_t* conv_done;
+  /* the next RMSNorm of the output, written with it (dense, BF16 output, epilogue none or residual): next_x =
+   * bf16(y·rsqrt(mean y² + next_eps)·next_norm_w), next_norm_w = (1+w) [n] — what mi_norm_apply over y gives, bit
+   * for bit, and what the next GEMV's M >= 3 input norm computes. Where the plan ends in a split-K reduction launch
+   * (M >= 3) that launch computes it, so the next layer's input norm takes no launch of its own; otherwise a norm
+   * launch follows the GEMV. No counterpart in the reference (its norms run where they are consumed). NULL = off. */
+  const float* next_norm_w;
+  uint16_t* next_x;
+  int32_t ld_next_x;
+  float next_eps;
 } mi_gemv_desc;
 size_t mi_gemv_workspace_bytes(const mi_gemv_desc* d);   /* 0 when the plan needs none */
 int mi_gemv(const mi_gemv_desc* d, void* stream);

@@ -90,6 +90,12 @@ struct Args {
   int conv_row0, conv_ch, ld_conv;
   const uint32_t* conv_step;
   const uint32_t* conv_done;
+  // dense, BF16 output: the next RMSNorm of y (x_next = bf16(y·rsqrt(mean y² + eps)·w)) computed by the split-K
+  // reduction (gemv_reduce_norm); null: off
+  const float* nn_w;
+  uint16_t* nn_x;
+  int ld_nn_x;
+  float nn_eps;
 };
 
 // The conv's per-row inputs, loaded at the start of the launch (independent of the GEMV): the 4 taps, the W-1 = 3
@@ -1775,6 +1781,96 @@ __global__ __launch_bounds__(256) void gemv_tk_reduce(Args a) {
   }
 }
 
+// The split-K reduction of a dense GEMV with BF16 output (epilogue none or residual) and the next RMSNorm of its
+// output in one launch: y as gemv_tk_reduce writes it (splits added in order, row scale, residual, one BF16
+// rounding), then x_next as norm_apply computes it over y — the same per-thread vectors, fma order, wave and
+// workgroup reductions (Σ y² over the row), r = 1 / sqrt(Σ / n + eps), x = bf16((y·r)·w). One workgroup of RN_NT
+// threads per token. Every load (partials, residual, row scales, norm weights) is issued up front at a clamped
+// index, so the launch waits one memory round trip: absent splits are skipped by a select and vectors past the row
+// add 0 to Σ, the order of each sum unchanged (n <= 8·RN_NT·RN_IT, at most RN_KS splits).
+constexpr int RN_NT = 256;
+constexpr int RN_IT = 3;
+constexpr int RN_KS = 4;
+__global__ __launch_bounds__(RN_NT) void gemv_reduce_norm(Args a) {
+  __shared__ float red[RN_NT / 64];
+  const int t = blockIdx.x;
+  const int n_pad = a.n_tiles * 16, nv = a.n / 8;
+  const bool resid = a.epilogue == MI_EPI_RESIDUAL;
+  float4 pp[RN_IT][RN_KS][2], rs[RN_IT][2], wv[RN_IT][2];
+  uint4 rq[RN_IT];
+#pragma unroll
+  for (int it = 0; it < RN_IT; ++it) {
+    const int c = 8 * min((int)threadIdx.x + RN_NT * it, nv - 1);
+#pragma unroll
+    for (int sp = 0; sp < RN_KS; ++sp) {
+      const float* p = a.part + ((long long)min(sp, a.ks - 1) * a.m + t) * n_pad + c;
+      pp[it][sp][0] = *reinterpret_cast<const float4*>(p);
+      pp[it][sp][1] = *reinterpret_cast<const float4*>(p + 4);
+    }
+    const float* rsp = a.row_scale != nullptr ? a.row_scale + c : a.nn_w + c;   // the weights stand in: unused
+    rs[it][0] = *reinterpret_cast<const float4*>(rsp);
+    rs[it][1] = *reinterpret_cast<const float4*>(rsp + 4);
+    rq[it] = *reinterpret_cast<const uint4*>((resid ? a.res + (long long)t * a.ldr : a.nn_x) + c);  // unused if not
+    wv[it][0] = *reinterpret_cast<const float4*>(a.nn_w + c);
+    wv[it][1] = *reinterpret_cast<const float4*>(a.nn_w + c + 4);
+  }
+  uint32_t yb[RN_IT][4];
+  float s = 0.0f;
+#pragma unroll
+  for (int it = 0; it < RN_IT; ++it) {
+    const int j = threadIdx.x + RN_NT * it;
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int sp = 0; sp < RN_KS; ++sp) {
+      const bool on = sp < a.ks;
+      const float4 p0 = pp[it][sp][0], p1 = pp[it][sp][1];
+      const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = on ? v[e] + pv[e] : v[e];     // a select: an absent split leaves v as is
+    }
+    const float rsv[8] = {rs[it][0].x, rs[it][0].y, rs[it][0].z, rs[it][0].w,
+                          rs[it][1].x, rs[it][1].y, rs[it][1].z, rs[it][1].w};
+    const uint32_t rw[4] = {rq[it].x, rq[it].y, rq[it].z, rq[it].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float lo = v[2 * i] * (a.row_scale != nullptr ? rsv[2 * i] : 1.0f);
+      float hi = v[2 * i + 1] * (a.row_scale != nullptr ? rsv[2 * i + 1] : 1.0f);
+      if (resid) {
+        lo += bf16_bits_to_f32(rw[i] & 0xFFFFu);
+        hi += bf16_bits_to_f32(rw[i] >> 16);
+      }
+      yb[it][i] = f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+      const float ylo = j < nv ? bf16_bits_to_f32(yb[it][i] & 0xFFFFu) : 0.0f;
+      const float yhi = j < nv ? bf16_bits_to_f32(yb[it][i] >> 16) : 0.0f;
+      s = fmaf(ylo, ylo, s);
+      s = fmaf(yhi, yhi, s);
+    }
+    if (j < nv)
+      *reinterpret_cast<uint4*>(a.y + (long long)t * a.ldy + 8 * j) = uint4{yb[it][0], yb[it][1], yb[it][2], yb[it][3]};
+  }
+  s = wave_sum(s);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  float ssq = 0.0f;
+#pragma unroll
+  for (int w = 0; w < RN_NT / 64; ++w) ssq += red[w];
+  const float r = 1.0f / sqrtf(ssq / (float)a.n + a.nn_eps);
+#pragma unroll
+  for (int it = 0; it < RN_IT; ++it) {
+    const int j = threadIdx.x + RN_NT * it;
+    const float w8[8] = {wv[it][0].x, wv[it][0].y, wv[it][0].z, wv[it][0].w,
+                         wv[it][1].x, wv[it][1].y, wv[it][1].z, wv[it][1].w};
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float lo = round_bf16((bf16_bits_to_f32(yb[it][i] & 0xFFFFu) * r) * w8[2 * i]);
+      const float hi = round_bf16((bf16_bits_to_f32(yb[it][i] >> 16) * r) * w8[2 * i + 1]);
+      o[i] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+    }
+    if (j < nv) *reinterpret_cast<uint4*>(a.nn_x + (long long)t * a.ld_nn_x + 8 * j) = uint4{o[0], o[1], o[2], o[3]};
+  }
+}
+
 // ---- exact dequantization through the same decode ---------------------------------------------------------------
 template <int FMT>
 __global__ __launch_bounds__(64) void dequant_t16(const uint8_t* w, const float* row_scale, int n, int k, int chunks,
@@ -1862,6 +1958,14 @@ int check_desc(const mi_gemv_desc* d) {
                "mi_gemv: routing in the launch needs one token, groups = slots = route_top_k (+1 with the shared "
                "expert, index <= 512, its gate column inside the route_ld-wide logits row), 1..512 experts, "
                "top_k <= 16 and the route outputs");
+  }
+  if (d->next_norm_w) {
+    MI_REQUIRE(!d->groups && !d->out_f32 && (d->epilogue == MI_EPI_NONE || d->epilogue == MI_EPI_RESIDUAL),
+               "mi_gemv: the next norm follows a dense GEMV with a BF16 output (epilogue none or residual)");
+    MI_REQUIRE(d->n % 8 == 0 && ((uintptr_t)d->y & 15) == 0 && d->ldy % 8 == 0 && ((uintptr_t)d->next_norm_w & 15) == 0,
+               "mi_gemv: the next norm needs n %% 8 == 0, a 16-byte aligned y with ldy %% 8 == 0 and next_norm_w");
+    MI_REQUIRE(d->next_x && ((uintptr_t)d->next_x & 15) == 0 && d->ld_next_x >= d->n && d->ld_next_x % 8 == 0,
+               "mi_gemv: next_x must be 16-byte aligned rows with ld_next_x >= n, multiple of 8");
   }
   MI_REQUIRE(((uintptr_t)d->x & 15) == 0 && d->ldx % 8 == 0, "mi_gemv: x must be 16-byte aligned with ldx %% 8 == 0");
   MI_REQUIRE(((uintptr_t)d->w & 15) == 0, "mi_gemv: weight pack must be 16-byte aligned");
@@ -2289,17 +2393,24 @@ void launch_row_k(const Args& a, const Plan& p, dim3 g, hipStream_t s) {
   else launch_row_kw<FMT, MT, 16>(a, p, g, s);
 }
 
+// the split-K reduction launch: with the next norm (a.nn_w), gemv_reduce_norm; else gemv_tk_reduce
+void launch_reduce(const Args& a, hipStream_t s) {
+  if (a.nn_w) {
+    hipLaunchKernelGGL(gemv_reduce_norm, dim3(a.m), dim3(RN_NT), 0, s, a);
+    return;
+  }
+  const bool silu = a.epilogue == MI_EPI_SILU_MUL || a.epilogue == MI_EPI_SILU_MUL_ROUNDED;
+  const int n_out = silu ? a.n / 2 : a.n;
+  hipLaunchKernelGGL(gemv_tk_reduce, dim3((n_out + 255) / 256, a.m), dim3(256), 0, s, a);
+}
+
 template <int FMT>
 void launch(const Args& a, const Plan& p, int groups, hipStream_t s) {
   if constexpr (FMT == FMT_NVFP4 || FMT == FMT_FP8 || FMT == FMT_INT4) {
     if (p.kernel == 3) {
       allow_lds(gemv_rowm<FMT>);
       hipLaunchKernelGGL(gemv_rowm<FMT>, dim3(p.G, 1, p.ks), dim3(64 * p.S), p.lds_bytes, s, a);
-      if (p.ks > 1) {
-        const bool silu = a.epilogue == MI_EPI_SILU_MUL || a.epilogue == MI_EPI_SILU_MUL_ROUNDED;
-        const int n_out = silu ? a.n / 2 : a.n;
-        hipLaunchKernelGGL(gemv_tk_reduce, dim3((n_out + 255) / 256, a.m), dim3(256), 0, s, a);
-      }
+      if (p.ks > 1) launch_reduce(a, s);
       return;
     }
   }
@@ -2307,11 +2418,7 @@ void launch(const Args& a, const Plan& p, int groups, hipStream_t s) {
     const dim3 g(p.G, groups, p.passes > 1 ? p.passes : p.ks);
     if (p.lds_rows == 2) launch_row_k<FMT, 2>(a, p, g, s);
     else launch_row_k<FMT, 1>(a, p, g, s);
-    if (p.ks > 1 && !a.fold_cnt) {
-      const bool silu = a.epilogue == MI_EPI_SILU_MUL || a.epilogue == MI_EPI_SILU_MUL_ROUNDED;
-      const int n_out = silu ? a.n / 2 : a.n;
-      hipLaunchKernelGGL(gemv_tk_reduce, dim3((n_out + 255) / 256, a.m), dim3(256), 0, s, a);
-    }
+    if (p.ks > 1 && !a.fold_cnt) launch_reduce(a, s);
     return;
   }
   if constexpr (FMT != FMT_FP8) {                // FP8 runs on gemv_row / gemv_rowm only (the planner's choice)
@@ -2319,11 +2426,7 @@ void launch(const Args& a, const Plan& p, int groups, hipStream_t s) {
     if (p.lds_rows > 2) launch_tk_d<FMT, 16>(a, p, g, s);
     else if (p.lds_rows == 2) launch_tk_d<FMT, 2>(a, p, g, s);
     else launch_tk_d<FMT, 1>(a, p, g, s);
-    if (p.ks > 1) {
-      const bool silu = a.epilogue == MI_EPI_SILU_MUL || a.epilogue == MI_EPI_SILU_MUL_ROUNDED;
-      const int n_out = silu ? a.n / 2 : a.n;
-      hipLaunchKernelGGL(gemv_tk_reduce, dim3((n_out + 255) / 256, a.m), dim3(256), 0, s, a);
-    }
+    if (p.ks > 1) launch_reduce(a, s);
   }
 }
 
@@ -2449,6 +2552,17 @@ int gemv_impl(const mi_gemv_desc* d, void* stream, void* fixed_ws, size_t fixed_
     if (p.kernel == 1 && fold && a.n_tiles <= kFoldTiles) a.fold_cnt = static_cast<uint32_t*>(ws);
   }
   MI_REQUIRE(!d->conv_w || p.ks == 1 || a.fold_cnt, "%s: the fused conv needs the K splits folded in the kernel", name);
+  // the next RMSNorm of y: computed by the split-K reduction launch where the plan has one and the row fits one
+  // workgroup's registers; otherwise a norm_apply launch after the GEMV (the same values either way)
+  const bool reduce_launch = p.ks > 1 && !a.fold_cnt && p.passes <= 1;
+  const bool nn_fused = d->next_norm_w && reduce_launch && d->n <= 8 * RN_NT * RN_IT && p.ks <= RN_KS &&
+                        (d->epilogue != MI_EPI_RESIDUAL || (((uintptr_t)d->residual & 15) == 0 && d->ldr % 8 == 0));
+  if (nn_fused) {
+    a.nn_w = d->next_norm_w;
+    a.nn_x = d->next_x;
+    a.ld_nn_x = d->ld_next_x;
+    a.nn_eps = d->next_eps;
+  }
   const int groups = d->groups ? d->max_groups : 1;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (d->format == FMT_NVFP4) launch<FMT_NVFP4>(a, p, groups, s);
@@ -2456,6 +2570,12 @@ int gemv_impl(const mi_gemv_desc* d, void* stream, void* fixed_ws, size_t fixed_
   else if (d->format == FMT_FP8) launch<FMT_FP8>(a, p, groups, s);
   else launch<FMT_BF16>(a, p, groups, s);
   MI_TRY_HIP(hipGetLastError(), "gemv launch");
+  if (d->next_norm_w && !nn_fused) {
+    mi_norm_desc nd{};
+    nd.t = d->m; nd.k = d->n; nd.h = d->y; nd.ldh = d->ldy; nd.stat = nullptr; nd.stat_parts = 1;
+    nd.w = d->next_norm_w; nd.x = d->next_x; nd.ldx = d->ld_next_x; nd.eps = d->next_eps;
+    if (int rc = mi_norm_apply(&nd, stream)) return rc;
+  }
   return MI_OK;
 }
 

@@ -77,7 +77,7 @@ def _bf16_2d(t, name, aligned=True):
 
 
 def gemv(w: PackedWeight, x, *, epilogue=None, residual=None, norm_w=None, eps: float = 1e-6, out=None,
-         stream=None, workspace=None, out_f32: bool = False, gated_norm=None, conv=None):
+         stream=None, workspace=None, out_f32: bool = False, gated_norm=None, conv=None, next_norm=None):
     """``gemv`` (``ops/gemv.py:1-12``): ``y = x·Wᵀ`` for ``x [M, K]`` bf16, M ≤ 16; ``epilogue`` None | "residual" |
     "silu_mul" (rows gate|up interleaved by 8, output N/2 columns) | "silu_mul_rounded"; ``norm_w`` = the (1 + w)
     float32 weight of a fused input RMSNorm; ``out_f32`` writes the unrounded FP32 result (``lm_head``).
@@ -86,13 +86,30 @@ def gemv(w: PackedWeight, x, *, epilogue=None, residual=None, norm_w=None, eps: 
     DeltaNet short conv in the epilogue (M ≤ 2): ``dict(w=taps [C, 4] bf16, state=…, out=[M, C] bf16, row0=first
     output row of the C channels, out_state=…, step=…, done=…)`` — ``state`` is ``[C, 3]`` with ``out_state`` the
     other slot, or both slots ``[2, C, 3]`` with ``step`` (a one-element device int32) choosing by parity; ``done`` a
-    stop flag. ``out`` then feeds :func:`gdn_step` as ``pre``."""
+    stop flag. ``out`` then feeds :func:`gdn_step` as ``pre``. ``next_norm = (w [N] float32 (1 + w), x_next [M, N]
+    bf16 view, eps)`` also writes the next RMSNorm of the output, ``x_next = bf16(y·rsqrt(mean y² + eps)·w)`` — bit
+    for bit :func:`norm_apply` of ``out`` — inside the split-K reduction launch where the plan has one (M ≥ 3), else
+    with a norm launch after the GEMV."""
     d, out = _gemv_desc(w, x, epilogue=epilogue, residual=residual, norm_w=norm_w, eps=eps, out=out,
                         workspace=workspace, out_f32=out_f32, gated_norm=gated_norm)
+    if next_norm is not None:
+        _gemv_next_norm(d, next_norm, x.shape[0], w.n)
     if conv is not None:
         _gemv_conv(d, conv, x.shape[0], w)
     hip.call("mi_gemv", C.byref(d), hip.stream_handle(stream))
     return out
+
+
+def _gemv_next_norm(d, next_norm, m: int, n: int) -> None:
+    """The next-norm fields of a GEMV descriptor, checked."""
+    torch = _torch()
+    nw, nx, neps = next_norm
+    if nw.dtype != torch.float32 or nw.numel() != n or not nw.is_contiguous():
+        raise ValueError("gemv next_norm: w must be a contiguous float32 [N]")
+    _bf16_2d(nx, "gemv next_norm x")
+    if nx.shape[0] < m or nx.shape[1] < n:
+        raise ValueError("gemv next_norm: x too small")
+    d.next_norm_w, d.next_x, d.ld_next_x, d.next_eps = hip.ptr(nw), hip.ptr(nx), nx.stride(0), float(neps)
 
 
 def _gemv_conv(d, conv, m: int, w) -> None:

@@ -89,8 +89,9 @@ class GatedMLP:
         return [(self.gate_up.packed, h, dict(epilogue="silu_mul", norm_w=self.norm_w, eps=self.eps, out=act)),
                 (self.down.packed, act, dict(epilogue="residual", residual=h, out=out))]
 
-    def __call__(self, h, act=None, out=None):
-        if CHAIN_TAIL and h.shape[0] == 1:
+    def __call__(self, h, act=None, out=None, next_norm=None):
+        """``next_norm = (w, x_next, eps)``: also write the next RMSNorm of the output (see :func:`kernels.gemv`)."""
+        if CHAIN_TAIL and h.shape[0] == 1 and next_norm is None:
             torch = _torch()
             if act is None:
                 act = torch.empty(1, self.inter, dtype=torch.bfloat16, device=h.device)
@@ -98,7 +99,7 @@ class GatedMLP:
                 out = torch.empty_like(h)
             return kernels.gemv_chain(self.phases(h, act, out))[1]
         act = kernels.gemv(self.gate_up.packed, h, epilogue="silu_mul", norm_w=self.norm_w, eps=self.eps, out=act)
-        return kernels.gemv(self.down.packed, act, epilogue="residual", residual=h, out=out)
+        return kernels.gemv(self.down.packed, act, epilogue="residual", residual=h, out=out, next_norm=next_norm)
 
     def bytes_per_step(self, m: int) -> int:
         return (_gemv_bytes(2 * self.inter, self.hidden, m, n_out=self.inter) + self.hidden * 4
@@ -186,18 +187,24 @@ class GdnDecoderLayer:
         """The current recurrent state."""
         return self.rec_slots[self.slot]
 
-    def step(self, h, out=None, pos=None, verify: bool = False, done=None):
+    def step(self, h, out=None, pos=None, verify: bool = False, done=None, x_in=None, next_norm=None):
         """One decode step over ``h [M, hidden]`` bf16 (M ≤ 16 tokens): returns the layer output; advances the state.
         ``pos`` is accepted for a uniform layer interface (the recurrence needs no position). ``verify``: a
         speculative verify pass — the outputs for every row, the state left for :meth:`commit`. ``done``: a step
-        program's stop flag; once set the state passes through unchanged."""
+        program's stop flag; once set the state passes through unchanged. At M ≥ 3 a chain of layers hands the
+        input norm over: ``x_in`` = this layer's normalized input (``norm_apply(h, norm_w)``, written by the layer
+        before), and ``next_norm = (w, x_next, eps)`` makes this layer write the next one's (inside the MLP's
+        split-K reduction): the same values as each layer normalizing its own input, one launch fewer a layer."""
         proj, o, h1, act, h2 = self.buffers(h.shape[0])
         out = h2 if out is None else out
         cin, cout = self.conv_state[self.parity], self.conv_state[1 - self.parity]
         fold = self.folds_conv(h.shape[0], verify)
         pre = self.pre(h.shape[0]) if fold else None
         conv = dict(w=self.conv_w, state=cin, out_state=cout, out=pre, row0=self.hv * self.dv, done=done) if fold else None
-        kernels.gemv(self.w_in.packed, h, norm_w=self.norm_w, eps=self.eps, out=proj, conv=conv)
+        if x_in is not None:
+            kernels.gemv(self.w_in.packed, x_in, out=proj, conv=conv)
+        else:
+            kernels.gemv(self.w_in.packed, h, norm_w=self.norm_w, eps=self.eps, out=proj, conv=conv)
         rec = self.rec_slots[self.slot]
         defer = self.defers_norm(h.shape[0])
         if verify:                              # the verify pass writes the other slots; commit() settles them
@@ -213,12 +220,12 @@ class GdnDecoderLayer:
             self.parity ^= 1
         # the gated RMSNorm (gdn_norm) is applied by the output projection while it stages o; z = proj[:, :hv·dv]
         gated = (self.gdn_norm_w, proj[:, : self.hv * self.dv], self.eps) if defer else None
-        if CHAIN_TAIL and h.shape[0] == 1:
+        if CHAIN_TAIL and h.shape[0] == 1 and next_norm is None:
             kernels.gemv_chain([(self.w_out.packed, o, dict(epilogue="residual", residual=h, out=h1, gated_norm=gated))]
                                + self.mlp.phases(h1, act, out))
             return out
         kernels.gemv(self.w_out.packed, o, epilogue="residual", residual=h, out=h1, gated_norm=gated)
-        return self.mlp(h1, act=act, out=out)
+        return self.mlp(h1, act=act, out=out, next_norm=next_norm)
 
     def mixer_bytes(self, m: int) -> int:
         state = 2 * self.hv * self.dk * self.dv * 4 + 2 * self.conv_dim * (self.conv - 1) * 2
@@ -316,22 +323,26 @@ class AttnDecoderLayer:
                              torch.empty(m, self.hidden, dtype=torch.bfloat16, device=dev))
         return self._bufs[m]
 
-    def step(self, h, pos: int, out=None, done=None):
+    def step(self, h, pos: int, out=None, done=None, x_in=None, next_norm=None):
         """One decode step over ``h [M, hidden]`` at positions ``pos..pos+M-1``; the new k/v enter the cache. ``pos``
         is an int or a one-element device int32 tensor (the step state's position in a captured program); ``done``
-        the program's stop flag (once set, nothing enters the cache)."""
+        the program's stop flag (once set, nothing enters the cache). ``x_in`` / ``next_norm``: the input norm
+        handed over between layers at M ≥ 3, as in :meth:`GdnDecoderLayer.step`."""
         proj, o, h1, act, h2 = self.buffers(h.shape[0])
         out = h2 if out is None else out
-        kernels.gemv(self.w_qkv.packed, h, norm_w=self.norm_w, eps=self.eps, out=proj)
+        if x_in is not None:
+            kernels.gemv(self.w_qkv.packed, x_in, out=proj)
+        else:
+            kernels.gemv(self.w_qkv.packed, h, norm_w=self.norm_w, eps=self.eps, out=proj)
         gate_src = proj[:, self.core_rows:] if self.layout == "packed" else None
         kernels.gqa_decode(proj, self.cache, pos, heads=self.heads, rope_cos=self.cos, rope_sin=self.sin, gate=True,
                            q_norm=self.q_norm, k_norm=self.k_norm, eps=self.eps, out=o, done=done, gate_src=gate_src)
-        if CHAIN_TAIL and h.shape[0] == 1:
+        if CHAIN_TAIL and h.shape[0] == 1 and next_norm is None:
             kernels.gemv_chain([(self.w_o.packed, o, dict(epilogue="residual", residual=h, out=h1))]
                                + self.mlp.phases(h1, act, out))
             return out
         kernels.gemv(self.w_o.packed, o, epilogue="residual", residual=h, out=h1)
-        return self.mlp(h1, act=act, out=out)
+        return self.mlp(h1, act=act, out=out, next_norm=next_norm)
 
     def mixer_bytes(self, m: int, pos: int) -> int:
         per_key = self.cache.bytes_per_key()
@@ -432,9 +443,17 @@ class MoeBlock:
             self._xn[m] = _torch().empty(m, self.hidden, dtype=_torch().bfloat16, device=self.norm_w.device)
         return self._xn[m]
 
-    def __call__(self, h, act=None, out=None):
+    def __call__(self, h, act=None, out=None, next_norm=None):
         """``h [M, hidden]`` bf16 → the block's output with the residual added (M ≤ 16). ``act`` is accepted so the
-        block can stand in for a decoder layer's dense MLP (it keeps its own intermediates)."""
+        block can stand in for a decoder layer's dense MLP (it keeps its own intermediates). ``next_norm = (w,
+        x_next, eps)``: also the next RMSNorm of the output (a norm launch after the combine)."""
+        y = self._forward(h, out)
+        if next_norm is not None:
+            nw, nx, neps = next_norm
+            kernels.norm_apply(y, nw, eps=neps, out=nx)
+        return y
+
+    def _forward(self, h, out):
         m = h.shape[0]
         logits, route, act, hk, s_act, s_out, s_gate, y = self.buffers(m)
         out = y if out is None else out

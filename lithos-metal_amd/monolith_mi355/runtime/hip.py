@@ -41,7 +41,8 @@ class MiGemvDesc(C.Structure):
                 ("group_max_pairs", C.c_int32), ("route_ld", C.c_int32), ("conv_w", C.c_void_p),
                 ("conv_in", C.c_void_p), ("conv_out_state", C.c_void_p), ("conv_out", C.c_void_p),
                 ("conv_row0", C.c_int32), ("conv_channels", C.c_int32), ("ld_conv", C.c_int32),
-                ("conv_step", C.c_void_p), ("conv_done", C.c_void_p)]
+                ("conv_step", C.c_void_p), ("conv_done", C.c_void_p), ("next_norm_w", C.c_void_p),
+                ("next_x", C.c_void_p), ("ld_next_x", C.c_int32), ("next_eps", C.c_float)]
 
 
 class MiGdnDesc(C.Structure):

@@ -276,6 +276,9 @@ class SpecProgram(StepProgram):
         dev = state.buf.device
         vocab, hidden = model.embed_table.shape
         self.h0 = torch.empty(self.t, hidden, dtype=torch.bfloat16, device=dev)
+        # at M >= 3 each layer writes the next one's normalized input (two buffers: a layer reads one while its
+        # reduction writes the other); the last writes the final norm's, so the LM head reads it as is
+        self.xn = [torch.empty(self.t, hidden, dtype=torch.bfloat16, device=dev) for _ in range(2)]
         self.logits = torch.empty(self.t, vocab, dtype=torch.bfloat16, device=dev)
         w = -(-gamma // 4) * 4                               # drafts per table row, padded to 16 bytes
         if draft_table.dtype != torch.int32 or draft_table.dim() != 2 or draft_table.shape[1] < gamma:
@@ -294,13 +297,24 @@ class SpecProgram(StepProgram):
         kernels.embed(m.embed_table, st.view("pending_tokens", t), t=t, out=self.h0, stream=s)
         h = self.h0
         pos = st.view("position")
+        hand_over = t >= 3
+        x = None
         with torch.cuda.stream(s):
-            for layer in m.layers:
+            for i, layer in enumerate(m.layers):
+                kw = {}
+                if hand_over:
+                    nxt = m.layers[i + 1] if i + 1 < len(m.layers) else None
+                    w, eps = (nxt.norm_w, nxt.eps) if nxt is not None else (m.norm_w, m.eps)
+                    kw = dict(x_in=x, next_norm=(w, self.xn[i % 2], eps))
                 if getattr(layer, "ping_pong", False):
-                    h = layer.step(h, pos=pos, verify=True, done=st.view("done"))
+                    h = layer.step(h, pos=pos, verify=True, done=st.view("done"), **kw)
                 else:
-                    h = layer.step(h, pos=pos, done=st.view("done"))
-        kernels.gemv(m.lm_head, h, norm_w=m.norm_w, eps=m.eps, out=self.logits, stream=s)
+                    h = layer.step(h, pos=pos, done=st.view("done"), **kw)
+                x = self.xn[i % 2] if hand_over else None
+        if x is not None:
+            kernels.gemv(m.lm_head, x, out=self.logits, stream=s)
+        else:
+            kernels.gemv(m.lm_head, h, norm_w=m.norm_w, eps=m.eps, out=self.logits, stream=s)
         kernels.argmax(self.logits, out=self.ids, stream=s)
         kernels.accept_scan(st.buf, self.ids, st.ring.addr, st.ring_capacity, eos=self.eos, log=self.log,
                             ctx_cap=self.ctx_cap, host_ctl=st.ctl.addr, stream=s)

@@ -327,3 +327,35 @@ def test_gemv_split_k_fold_in_kernel(torch_gpu):
         y = kernels.gemv(w, xd, out_f32=True, workspace=ws)
         torch.cuda.synchronize()
         assert np.array_equal(y.cpu().numpy(), first[i % len(cases)]), i
+
+
+@pytest.mark.parametrize("fmt,n,k,mtok,epi,env", [
+    ("nvfp4", 5120, 17408, 8, "residual", {}),              # gemv_rowm, K splits: the reduction writes x_next
+    ("nvfp4", 5120, 17408, 3, "residual", {}),
+    ("int4_affine", 2048, 8192, 8, "residual", {}),         # gemv_tk splits
+    ("nvfp4", 1040, 17408, 1, "residual", {"MI_GEMV_FOLD": "0"}),   # gemv_row splits through the reduction launch
+    ("nvfp4", 5120, 17408, 1, "residual", {}),              # splits folded in the kernel: a norm launch follows
+    ("nvfp4", 2048, 5120, 8, None, {}),                     # one split: a norm launch follows
+    ("nvfp4", 3000, 12288, 8, None, {}),                    # ragged N (whole 8-column vectors)
+])
+def test_gemv_next_norm(torch_gpu, fmt, n, k, mtok, epi, env, rng, monkeypatch):
+    """``next_norm``: y is bit-identical to the same GEMV without it, and x_next bit-identical to ``norm_apply`` of
+    that y (the next GEMV's M ≥ 3 input norm), whichever launch computes it."""
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    for kk, v in env.items():
+        monkeypatch.setenv(kk, v)
+    m = _matrix(fmt, n, k, rng)
+    w = _upload(torch, m)
+    xd = to_dev_bf16(torch, rbf(rng.standard_normal((mtok, k))))
+    res = to_dev_bf16(torch, rbf(rng.standard_normal((mtok, n)))) if epi else None
+    nw = torch.from_numpy((1.0 + rng.standard_normal(n) * 0.1).astype(np.float32)).cuda()
+    y0 = kernels.gemv(w, xd, epilogue=epi, residual=res)
+    x0 = kernels.norm_apply(y0, nw, eps=1e-6)
+    xn = torch.full((mtok, n), 7.0, dtype=torch.bfloat16, device="cuda")
+    for rep in range(2):
+        y1 = kernels.gemv(w, xd, epilogue=epi, residual=res, next_norm=(nw, xn, 1e-6))
+        torch.cuda.synchronize()
+        assert torch.equal(y1.view(torch.int16), y0.view(torch.int16)), rep
+        assert torch.equal(xn.view(torch.int16), x0.view(torch.int16)), rep
+        xn.fill_(7.0)

@@ -159,3 +159,45 @@ def test_attention_decoder_layer(torch_gpu, geom, ctx, pos, m):
         h1 = ON.linear(o, w_o, epilogue="residual", residual=h)
         _bar(got, _mlp(h1, ex), "layer output", E2E_CEILING[("attn", geom)])
         pos += m
+
+
+@pytest.mark.parametrize("kind", ["gdn", "attn"])
+@pytest.mark.parametrize("m", [3, 8])
+def test_layer_norm_hand_over(torch_gpu, kind, m):
+    """At M ≥ 3 consecutive layers hand the input norm over: a layer given its normalized input (``x_in``) and asked
+    for the next one's (``next_norm``, written by the MLP's split-K reduction) gives the same output and state, bit
+    for bit, as the same layer normalizing its own input, and the x_next it writes is ``norm_apply`` of its output."""
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    from monolith_mi355.layers import AttnDecoderLayer, GdnDecoderLayer
+
+    def make():
+        if kind == "gdn":
+            return GdnDecoderLayer(seed=3)
+        layer = AttnDecoderLayer(ctx=4096, seed=4)
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(5)
+        layer.fill_cache(4000, gen)
+        return layer
+
+    a, b = make(), make()
+    w_next = torch.from_numpy((1.0 + np.random.default_rng(9).standard_normal(a.hidden) * 0.1).astype(np.float32)).cuda()
+    xn = torch.empty(m, a.hidden, dtype=torch.bfloat16, device="cuda")
+    rng = np.random.default_rng(m + 20)
+    pos = 4000
+    for step in range(2):
+        print(f"norm hand-over {kind} m={m} step {step}", flush=True)
+        h = to_dev_bf16(torch, rbf(rng.standard_normal((m, a.hidden))))
+        args = (pos,) if kind == "attn" else ()
+        y_a = a.step(h, *args).clone()
+        x_in = kernels.norm_apply(h, b.norm_w, eps=b.eps)
+        xn.fill_(3.0)
+        y_b = b.step(h, *args, x_in=x_in, next_norm=(w_next, xn, 1e-6)).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(y_a.view(torch.int16), y_b.view(torch.int16)), step
+        assert torch.equal(xn.view(torch.int16), kernels.norm_apply(y_b, w_next, eps=1e-6).view(torch.int16)), step
+        if kind == "gdn":
+            assert torch.equal(a.rec, b.rec) and torch.equal(a.conv_state, b.conv_state)
+        else:
+            assert torch.equal(a.cache.k_codes, b.cache.k_codes) and torch.equal(a.cache.v_codes, b.cache.v_codes)
+        pos += m
