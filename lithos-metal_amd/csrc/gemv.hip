@@ -1783,92 +1783,94 @@ __global__ __launch_bounds__(256) void gemv_tk_reduce(Args a) {
 
 // The split-K reduction of a dense GEMV with BF16 output (epilogue none or residual) and the next RMSNorm of its
 // output in one launch: y as gemv_tk_reduce writes it (splits added in order, row scale, residual, one BF16
-// rounding), then x_next as norm_apply computes it over y — the same per-thread vectors, fma order, wave and
-// workgroup reductions (Σ y² over the row), r = 1 / sqrt(Σ / n + eps), x = bf16((y·r)·w). One workgroup of RN_NT
-// threads per token. Every load (partials, residual, row scales, norm weights) is issued up front at a clamped
-// index, so the launch waits one memory round trip: absent splits are skipped by a select and vectors past the row
-// add 0 to Σ, the order of each sum unchanged (n <= 8·RN_NT·RN_IT, at most RN_KS splits).
-constexpr int RN_NT = 256;
-constexpr int RN_IT = 3;
+// rounding), then x_next as norm_apply computes it over y. One workgroup of RN_NT threads per token, a thread per
+// 8-column vector: all its loads (partials of every split at a clamped index, residual, row scales, norm weights)
+// issued up front, so the launch waits one memory round trip; y goes to LDS, where the first RN_SUM threads take
+// Σ y² exactly as norm_apply's threads do (vectors tid, tid + RN_SUM, … in order, fma, then the waves in order) —
+// the same statistic, bit for bit — and every thread normalizes its vector (n <= 8·RN_NT, at most RN_KS splits).
+constexpr int RN_NT = 1024;
+constexpr int RN_SUM = 256;     // norm_apply's workgroup: its per-thread vectors fix the order of Σ
 constexpr int RN_KS = 4;
 __global__ __launch_bounds__(RN_NT) void gemv_reduce_norm(Args a) {
-  __shared__ float red[RN_NT / 64];
-  const int t = blockIdx.x;
+  __shared__ __attribute__((aligned(16))) uint4 ys[RN_NT];
+  __shared__ float red[RN_SUM / 64];
+  __shared__ float rsh;
+  const int t = blockIdx.x, tid = threadIdx.x;
   const int n_pad = a.n_tiles * 16, nv = a.n / 8;
   const bool resid = a.epilogue == MI_EPI_RESIDUAL;
-  float4 pp[RN_IT][RN_KS][2], rs[RN_IT][2], wv[RN_IT][2];
-  uint4 rq[RN_IT];
+  const int c = 8 * min(tid, nv - 1);
+  float4 pp[RN_KS][2];
 #pragma unroll
-  for (int it = 0; it < RN_IT; ++it) {
-    const int c = 8 * min((int)threadIdx.x + RN_NT * it, nv - 1);
-#pragma unroll
-    for (int sp = 0; sp < RN_KS; ++sp) {
-      const float* p = a.part + ((long long)min(sp, a.ks - 1) * a.m + t) * n_pad + c;
-      pp[it][sp][0] = *reinterpret_cast<const float4*>(p);
-      pp[it][sp][1] = *reinterpret_cast<const float4*>(p + 4);
-    }
-    const float* rsp = a.row_scale != nullptr ? a.row_scale + c : a.nn_w + c;   // the weights stand in: unused
-    rs[it][0] = *reinterpret_cast<const float4*>(rsp);
-    rs[it][1] = *reinterpret_cast<const float4*>(rsp + 4);
-    rq[it] = *reinterpret_cast<const uint4*>((resid ? a.res + (long long)t * a.ldr : a.nn_x) + c);  // unused if not
-    wv[it][0] = *reinterpret_cast<const float4*>(a.nn_w + c);
-    wv[it][1] = *reinterpret_cast<const float4*>(a.nn_w + c + 4);
+  for (int sp = 0; sp < RN_KS; ++sp) {
+    const float* p = a.part + ((long long)min(sp, a.ks - 1) * a.m + t) * n_pad + c;
+    pp[sp][0] = *reinterpret_cast<const float4*>(p);
+    pp[sp][1] = *reinterpret_cast<const float4*>(p + 4);
   }
-  uint32_t yb[RN_IT][4];
-  float s = 0.0f;
+  const float* rsp = a.row_scale != nullptr ? a.row_scale + c : a.nn_w + c;   // the weights stand in: unused
+  const float4 rs0 = *reinterpret_cast<const float4*>(rsp), rs1 = *reinterpret_cast<const float4*>(rsp + 4);
+  const uint4 rq = *reinterpret_cast<const uint4*>((resid ? a.res + (long long)t * a.ldr : a.nn_x) + c);
+  const float4 w0 = *reinterpret_cast<const float4*>(a.nn_w + c), w1 = *reinterpret_cast<const float4*>(a.nn_w + c + 4);
+  float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int it = 0; it < RN_IT; ++it) {
-    const int j = threadIdx.x + RN_NT * it;
-    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int sp = 0; sp < RN_KS; ++sp) {
+    const bool on = sp < a.ks;
+    const float pv[8] = {pp[sp][0].x, pp[sp][0].y, pp[sp][0].z, pp[sp][0].w,
+                         pp[sp][1].x, pp[sp][1].y, pp[sp][1].z, pp[sp][1].w};
 #pragma unroll
-    for (int sp = 0; sp < RN_KS; ++sp) {
-      const bool on = sp < a.ks;
-      const float4 p0 = pp[it][sp][0], p1 = pp[it][sp][1];
-      const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+    for (int e = 0; e < 8; ++e) v[e] = on ? v[e] + pv[e] : v[e];     // a select: an absent split leaves v as is
+  }
+  const float rsv[8] = {rs0.x, rs0.y, rs0.z, rs0.w, rs1.x, rs1.y, rs1.z, rs1.w};
+  const uint32_t rw[4] = {rq.x, rq.y, rq.z, rq.w};
+  uint32_t yb[4];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = on ? v[e] + pv[e] : v[e];     // a select: an absent split leaves v as is
+  for (int i = 0; i < 4; ++i) {
+    float lo = v[2 * i] * (a.row_scale != nullptr ? rsv[2 * i] : 1.0f);
+    float hi = v[2 * i + 1] * (a.row_scale != nullptr ? rsv[2 * i + 1] : 1.0f);
+    if (resid) {
+      lo += bf16_bits_to_f32(rw[i] & 0xFFFFu);
+      hi += bf16_bits_to_f32(rw[i] >> 16);
     }
-    const float rsv[8] = {rs[it][0].x, rs[it][0].y, rs[it][0].z, rs[it][0].w,
-                          rs[it][1].x, rs[it][1].y, rs[it][1].z, rs[it][1].w};
-    const uint32_t rw[4] = {rq[it].x, rq[it].y, rq[it].z, rq[it].w};
+    yb[i] = f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+  }
+  const uint4 y4{yb[0], yb[1], yb[2], yb[3]};
+  if (tid < nv) {
+    *reinterpret_cast<uint4*>(a.y + (long long)t * a.ldy + 8 * tid) = y4;
+    ys[tid] = y4;
+  }
+  lds_barrier();
+  if (tid < RN_SUM) {
+    float s = 0.0f;
+    for (int jj = tid; jj < nv; jj += RN_SUM) {
+      const uint4 q = ys[jj];
+      const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float lo = v[2 * i] * (a.row_scale != nullptr ? rsv[2 * i] : 1.0f);
-      float hi = v[2 * i + 1] * (a.row_scale != nullptr ? rsv[2 * i + 1] : 1.0f);
-      if (resid) {
-        lo += bf16_bits_to_f32(rw[i] & 0xFFFFu);
-        hi += bf16_bits_to_f32(rw[i] >> 16);
+      for (int i = 0; i < 4; ++i) {
+        const float lo = bf16_bits_to_f32(qw[i] & 0xFFFFu), hi = bf16_bits_to_f32(qw[i] >> 16);
+        s = fmaf(lo, lo, s);
+        s = fmaf(hi, hi, s);
       }
-      yb[it][i] = f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
-      const float ylo = j < nv ? bf16_bits_to_f32(yb[it][i] & 0xFFFFu) : 0.0f;
-      const float yhi = j < nv ? bf16_bits_to_f32(yb[it][i] >> 16) : 0.0f;
-      s = fmaf(ylo, ylo, s);
-      s = fmaf(yhi, yhi, s);
     }
-    if (j < nv)
-      *reinterpret_cast<uint4*>(a.y + (long long)t * a.ldy + 8 * j) = uint4{yb[it][0], yb[it][1], yb[it][2], yb[it][3]};
+    s = wave_sum(s);
+    if ((tid & 63) == 0) red[tid >> 6] = s;
   }
-  s = wave_sum(s);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
-  __syncthreads();
-  float ssq = 0.0f;
+  lds_barrier();
+  if (tid == 0) {
+    float ssq = 0.0f;
 #pragma unroll
-  for (int w = 0; w < RN_NT / 64; ++w) ssq += red[w];
-  const float r = 1.0f / sqrtf(ssq / (float)a.n + a.nn_eps);
-#pragma unroll
-  for (int it = 0; it < RN_IT; ++it) {
-    const int j = threadIdx.x + RN_NT * it;
-    const float w8[8] = {wv[it][0].x, wv[it][0].y, wv[it][0].z, wv[it][0].w,
-                         wv[it][1].x, wv[it][1].y, wv[it][1].z, wv[it][1].w};
-    uint32_t o[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float lo = round_bf16((bf16_bits_to_f32(yb[it][i] & 0xFFFFu) * r) * w8[2 * i]);
-      const float hi = round_bf16((bf16_bits_to_f32(yb[it][i] >> 16) * r) * w8[2 * i + 1]);
-      o[i] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
-    }
-    if (j < nv) *reinterpret_cast<uint4*>(a.nn_x + (long long)t * a.ld_nn_x + 8 * j) = uint4{o[0], o[1], o[2], o[3]};
+    for (int w = 0; w < RN_SUM / 64; ++w) ssq += red[w];
+    rsh = 1.0f / sqrtf(ssq / (float)a.n + a.nn_eps);
   }
+  lds_barrier();
+  const float r = rsh;
+  const float w8[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float lo = round_bf16((bf16_bits_to_f32(yb[i] & 0xFFFFu) * r) * w8[2 * i]);
+    const float hi = round_bf16((bf16_bits_to_f32(yb[i] >> 16) * r) * w8[2 * i + 1]);
+    o[i] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+  }
+  if (tid < nv) *reinterpret_cast<uint4*>(a.nn_x + (long long)t * a.ld_nn_x + 8 * tid) = uint4{o[0], o[1], o[2], o[3]};
 }
 
 // ---- exact dequantization through the same decode ---------------------------------------------------------------
@@ -2555,7 +2557,7 @@ int gemv_impl(const mi_gemv_desc* d, void* stream, void* fixed_ws, size_t fixed_
   // the next RMSNorm of y: computed by the split-K reduction launch where the plan has one and the row fits one
   // workgroup's registers; otherwise a norm_apply launch after the GEMV (the same values either way)
   const bool reduce_launch = p.ks > 1 && !a.fold_cnt && p.passes <= 1;
-  const bool nn_fused = d->next_norm_w && reduce_launch && d->n <= 8 * RN_NT * RN_IT && p.ks <= RN_KS &&
+  const bool nn_fused = d->next_norm_w && reduce_launch && d->n <= 8 * RN_NT && p.ks <= RN_KS &&
                         (d->epilogue != MI_EPI_RESIDUAL || (((uintptr_t)d->residual & 15) == 0 && d->ldr % 8 == 0));
   if (nn_fused) {
     a.nn_w = d->next_norm_w;
