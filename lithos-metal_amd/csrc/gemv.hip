@@ -2224,7 +2224,10 @@ Plan plan_rowm(const mi_gemv_desc* d, int chunks, int n_tiles) {
   int ks = (chunks + 12 * kw - 1) / (12 * kw);   // at most 12 waves: the kernel's VGPR budget is 3 waves per SIMD
   if (d->norm_w && ks > 1) return best;          // the fused norm needs the whole row in one workgroup
   int force_ks = 0, force_rt = 0;
-  if (const char* env = getenv("MI_GEMV_ROWM")) sscanf(env, "%d,%d", &force_ks, &force_rt);   // tuning sweeps
+  if (const char* env = getenv("MI_GEMV_ROWM")) {                                // tuning sweeps
+    const char* ke = getenv("MI_GEMV_ROWM_K");                                   // only launches of this K
+    if (!ke || atoi(ke) == d->k) sscanf(env, "%d,%d", &force_ks, &force_rt);
+  }
   if (force_ks) ks = force_ks;
   // one split whose tiles' waves fill under three quarters of the chip's wave slots (12 per CU at this kernel's
   // VGPR budget): three K splits, so the tiles spread over every CU (27B attention o_proj at M = 8, 320 tiles of 6

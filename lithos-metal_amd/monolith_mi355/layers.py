@@ -89,16 +89,20 @@ class GatedMLP:
         return [(self.gate_up.packed, h, dict(epilogue="silu_mul", norm_w=self.norm_w, eps=self.eps, out=act)),
                 (self.down.packed, act, dict(epilogue="residual", residual=h, out=out))]
 
-    def __call__(self, h, act=None, out=None, next_norm=None):
-        """``next_norm = (w, x_next, eps)``: also write the next RMSNorm of the output (see :func:`kernels.gemv`)."""
-        if CHAIN_TAIL and h.shape[0] == 1 and next_norm is None:
+    def __call__(self, h, act=None, out=None, next_norm=None, x_in=None):
+        """``next_norm = (w, x_next, eps)``: also write the next RMSNorm of the output (see :func:`kernels.gemv`);
+        ``x_in``: this MLP's normalized input when the caller has it (M ≥ 3), so its gate|up takes no norm."""
+        if CHAIN_TAIL and h.shape[0] == 1 and next_norm is None and x_in is None:
             torch = _torch()
             if act is None:
                 act = torch.empty(1, self.inter, dtype=torch.bfloat16, device=h.device)
             if out is None:
                 out = torch.empty_like(h)
             return kernels.gemv_chain(self.phases(h, act, out))[1]
-        act = kernels.gemv(self.gate_up.packed, h, epilogue="silu_mul", norm_w=self.norm_w, eps=self.eps, out=act)
+        if x_in is not None:
+            act = kernels.gemv(self.gate_up.packed, x_in, epilogue="silu_mul", out=act)
+        else:
+            act = kernels.gemv(self.gate_up.packed, h, epilogue="silu_mul", norm_w=self.norm_w, eps=self.eps, out=act)
         return kernels.gemv(self.down.packed, act, epilogue="residual", residual=h, out=out, next_norm=next_norm)
 
     def bytes_per_step(self, m: int) -> int:
