@@ -307,7 +307,14 @@ def main():
             blocks = [MoeBlock(seed=80 + i, device=dev) for i in range(2)]
             for m in (1, 8):
                 x = torch.randn(m, 2048, generator=gen, device=dev).to(torch.bfloat16)
-                ms = timed_graph(lambda i: blocks[i % 2](x), args.steps, args.warmup, stream)
+                if m >= 3:      # one block of a chain, the input norm handed over as for the M = 8 layers
+                    xins = [kernels.norm_apply(x, b.norm_w, eps=b.eps) for b in blocks]
+                    xn = torch.empty_like(x)
+                    fn = lambda i: blocks[i % 2](x, x_in=xins[i % 2], next_norm=(blocks[(i + 1) % 2].norm_w, xn,
+                                                                                 blocks[(i + 1) % 2].eps))
+                else:
+                    fn = lambda i: blocks[i % 2](x)
+                ms = timed_graph(fn, args.steps, args.warmup, stream)
                 distinct = [len(set(b.buffers(m)[1][0][:, :b.top_k].flatten().tolist())) for b in blocks]
                 nbytes = sum(b.bytes_per_step(m, d) for b, d in zip(blocks, distinct)) // len(blocks)
                 out[f"moe_m{m}"] = (ms, nbytes)
@@ -439,7 +446,8 @@ def main():
         "int4_gateup_m8": entry("int4_gateup_m8", 8),
         "moe_block_m1": dict(entry("moe_m1", 1), workload="MoE feed-forward: router + top-8 of 256 NVFP4 experts "
                              "(hidden 2048, intermediate 512) + shared expert + combine"),
-        "moe_block_m8": entry("moe_m8", 8),
+        "moe_block_m8": dict(entry("moe_m8", 8), workload="one block of a chain: its normalized input from the layer "
+                             "before, the next one's written by its combine"),
         "spec_round_2layers_ctx32k": spec_info,
         "token_loop_2layers_ctx32k": dict(entry("loop", 1), **loop_info,
                                           workload="embed + GDN layer + attention layer (32K) + BF16 lm_head 248320 "

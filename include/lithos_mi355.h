@@ -370,6 +370,13 @@ typedef struct mi_moe_combine_desc {
   int32_t ldr;
   uint16_t* out;
   int32_t ldo;
+  /* the next RMSNorm of out, written with it: next_x = bf16(out·rsqrt(mean out² + next_eps)·next_norm_w), bit for
+   * bit mi_norm_apply over out (hidden <= 8192: one workgroup per token computes both). No counterpart in the
+   * reference. NULL = off. */
+  const float* next_norm_w;
+  uint16_t* next_x;
+  int32_t ld_next_x;
+  float next_eps;
 } mi_moe_combine_desc;
 int mi_moe_combine(const mi_moe_combine_desc* d, void* stream);
 

@@ -136,6 +136,10 @@ struct CombineArgs {
   const uint16_t* shared_gate;
   const uint16_t* residual;
   uint16_t* out;
+  const float* nn_w;        // the next RMSNorm of out (moe_combine<true>), or null
+  uint16_t* nn_x;
+  int ld_nn_x;
+  float nn_eps;
 };
 
 __device__ __forceinline__ void bf16x8_to_f32(uint4 u, float* f) {
@@ -147,10 +151,9 @@ __device__ __forceinline__ void bf16x8_to_f32(uint4 u, float* f) {
   }
 }
 
-__global__ __launch_bounds__(256) void moe_combine(CombineArgs a) {
-  const int t = blockIdx.y;
-  const int c = (blockIdx.x * 256 + threadIdx.x) * 8;
-  if (c >= a.hidden) return;
+// One 8-column vector of token t's output: Σ_j w·h (in slot order), the shared expert, the residual; one BF16
+// rounding.
+__device__ __forceinline__ uint4 combine_vec(const CombineArgs& a, int t, int c) {
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, x[8];
   for (int j = 0; j < a.top_k; ++j) {
     const float w = a.weights[t * a.top_k + j];
@@ -175,7 +178,69 @@ __global__ __launch_bounds__(256) void moe_combine(CombineArgs a) {
   o.y = f32_to_bf16_bits(acc[2]) | ((uint32_t)f32_to_bf16_bits(acc[3]) << 16);
   o.z = f32_to_bf16_bits(acc[4]) | ((uint32_t)f32_to_bf16_bits(acc[5]) << 16);
   o.w = f32_to_bf16_bits(acc[6]) | ((uint32_t)f32_to_bf16_bits(acc[7]) << 16);
-  *reinterpret_cast<uint4*>(a.out + (long long)t * a.ldo + c) = o;
+  return o;
+}
+
+__global__ __launch_bounds__(256) void moe_combine(CombineArgs a) {
+  const int t = blockIdx.y;
+  const int c = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (c >= a.hidden) return;
+  *reinterpret_cast<uint4*>(a.out + (long long)t * a.ldo + c) = combine_vec(a, t, c);
+}
+
+// The combine with the next RMSNorm of its output (the next layer's normalized input): one workgroup of 1024 per
+// token, a thread per 8-column vector; the output goes to LDS, where the first 256 threads take Σ out² as
+// norm_apply's threads do (vectors tid, tid + 256, … in order, fma, then the waves in order) — the same statistic,
+// bit for bit — and every thread normalizes its vector: x = bf16((out·r)·w). hidden <= 8192.
+constexpr int CN_NT = 1024;
+constexpr int CN_SUM = 256;
+__global__ __launch_bounds__(CN_NT) void moe_combine_norm(CombineArgs a) {
+  __shared__ __attribute__((aligned(16))) uint4 ys[CN_NT];
+  __shared__ float red[CN_SUM / 64];
+  __shared__ float rsh;
+  const int t = blockIdx.x, tid = threadIdx.x, nv = a.hidden / 8;
+  const int c = 8 * min(tid, nv - 1);
+  const float4 w0 = *reinterpret_cast<const float4*>(a.nn_w + c), w1 = *reinterpret_cast<const float4*>(a.nn_w + c + 4);
+  const uint4 o = combine_vec(a, t, c);
+  if (tid < nv) {
+    *reinterpret_cast<uint4*>(a.out + (long long)t * a.ldo + 8 * tid) = o;
+    ys[tid] = o;
+  }
+  lds_barrier();
+  if (tid < CN_SUM) {
+    float s = 0.0f;
+    for (int jj = tid; jj < nv; jj += CN_SUM) {
+      const uint4 q = ys[jj];
+      const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float lo = bf16_bits_to_f32(qw[i] & 0xFFFFu), hi = bf16_bits_to_f32(qw[i] >> 16);
+        s = fmaf(lo, lo, s);
+        s = fmaf(hi, hi, s);
+      }
+    }
+    s = wave_sum(s);
+    if ((tid & 63) == 0) red[tid >> 6] = s;
+  }
+  lds_barrier();
+  if (tid == 0) {
+    float ssq = 0.0f;
+#pragma unroll
+    for (int w = 0; w < CN_SUM / 64; ++w) ssq += red[w];
+    rsh = 1.0f / sqrtf(ssq / (float)a.hidden + a.nn_eps);
+  }
+  lds_barrier();
+  const float r = rsh;
+  const uint32_t ow[4] = {o.x, o.y, o.z, o.w};
+  const float w8[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+  uint32_t xo[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float lo = round_bf16((bf16_bits_to_f32(ow[i] & 0xFFFFu) * r) * w8[2 * i]);
+    const float hi = round_bf16((bf16_bits_to_f32(ow[i] >> 16) * r) * w8[2 * i + 1]);
+    xo[i] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+  }
+  if (tid < nv) *reinterpret_cast<uint4*>(a.nn_x + (long long)t * a.ld_nn_x + 8 * tid) = uint4{xo[0], xo[1], xo[2], xo[3]};
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -221,9 +286,30 @@ extern "C" int mi_moe_combine(const mi_moe_combine_desc* d, void* stream) {
                  (!d->residual || aligned16(d->residual)),
              "mi_moe_combine: 16-byte aligned rows");
   CombineArgs a{d->t, d->hidden, d->top_k, d->ldh, d->ld_shared, d->ld_gate, d->ldr, d->ldo,
-                d->h, d->weights, d->shared, d->shared_gate, d->residual, d->out};
+                d->h, d->weights, d->shared, d->shared_gate, d->residual, d->out, nullptr, nullptr, 0, 0.0f};
+  if (d->next_norm_w) {
+    MI_REQUIRE(aligned16(d->next_norm_w) && d->next_x && aligned16(d->next_x) && d->ld_next_x >= d->hidden &&
+                   d->ld_next_x % 8 == 0,
+               "mi_moe_combine: the next norm needs a 16-byte aligned next_norm_w and next_x rows (ld >= hidden, "
+               "multiple of 8)");
+    if (d->hidden <= 8 * CN_NT) {               // one workgroup per token writes out and its norm
+      a.nn_w = d->next_norm_w;
+      a.nn_x = d->next_x;
+      a.ld_nn_x = d->ld_next_x;
+      a.nn_eps = d->next_eps;
+      hipLaunchKernelGGL(moe_combine_norm, dim3(d->t), dim3(CN_NT), 0, static_cast<hipStream_t>(stream), a);
+      MI_TRY_HIP(hipGetLastError(), "moe_combine_norm launch");
+      return MI_OK;
+    }
+  }
   const dim3 grid((d->hidden / 8 + 255) / 256, d->t);
   hipLaunchKernelGGL(moe_combine, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
   MI_TRY_HIP(hipGetLastError(), "moe_combine launch");
+  if (d->next_norm_w) {                         // a wider row: the norm as its own launch (the same values)
+    mi_norm_desc nd{};
+    nd.t = d->t; nd.k = d->hidden; nd.h = d->out; nd.ldh = d->ldo; nd.stat = nullptr; nd.stat_parts = 1;
+    nd.w = d->next_norm_w; nd.x = d->next_x; nd.ldx = d->ld_next_x; nd.eps = d->next_eps;
+    return mi_norm_apply(&nd, stream);
+  }
   return MI_OK;
 }

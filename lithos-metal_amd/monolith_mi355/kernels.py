@@ -532,9 +532,11 @@ def moe_gemv(w: PackedWeight, x, groups, *, tokens: int, top_k: int, x_per_slot:
     return out
 
 
-def moe_combine(h, weights, *, top_k: int, shared=None, shared_gate=None, residual=None, out=None, stream=None):
+def moe_combine(h, weights, *, top_k: int, shared=None, shared_gate=None, residual=None, out=None, stream=None,
+                next_norm=None):
     """``moe_combine`` (``ops/moe.py``): ``out[t] = Σ_j w[t, j]·h[t·k + j] (+ bf16(σ(shared_gate[t]))·shared[t])
-    (+ residual[t])``, FP32, one BF16 rounding. ``h [T·k, H]``, ``weights [T, k]`` float32."""
+    (+ residual[t])``, FP32, one BF16 rounding. ``h [T·k, H]``, ``weights [T, k]`` float32. ``next_norm = (w [H]
+    float32, x_next [T, H] bf16, eps)`` also writes the next RMSNorm of ``out`` (bit for bit :func:`norm_apply`)."""
     torch = _torch()
     _bf16_2d(h, "moe_combine h")
     t = weights.shape[0]
@@ -557,6 +559,14 @@ def moe_combine(h, weights, *, top_k: int, shared=None, shared_gate=None, residu
                              ld_gate=shared_gate.stride(0) if shared_gate is not None else 0,
                              residual=hip.ptr(residual), ldr=residual.stride(0) if residual is not None else 0,
                              out=hip.ptr(out), ldo=out.stride(0))
+    if next_norm is not None:
+        nw, nx, neps = next_norm
+        if nw.dtype != torch.float32 or nw.numel() != hidden or not nw.is_contiguous():
+            raise ValueError("moe_combine next_norm: w must be a contiguous float32 [H]")
+        _bf16_2d(nx, "moe_combine next_norm x")
+        if nx.shape[0] < t or nx.shape[1] < hidden:
+            raise ValueError("moe_combine next_norm: x too small")
+        d.next_norm_w, d.next_x, d.ld_next_x, d.next_eps = hip.ptr(nw), hip.ptr(nx), nx.stride(0), float(neps)
     hip.call("mi_moe_combine", C.byref(d), hip.stream_handle(stream))
     return out
 

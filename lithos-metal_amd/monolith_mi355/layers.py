@@ -447,17 +447,18 @@ class MoeBlock:
             self._xn[m] = _torch().empty(m, self.hidden, dtype=_torch().bfloat16, device=self.norm_w.device)
         return self._xn[m]
 
-    def __call__(self, h, act=None, out=None, next_norm=None):
+    def __call__(self, h, act=None, out=None, next_norm=None, x_in=None):
         """``h [M, hidden]`` bf16 → the block's output with the residual added (M ≤ 16). ``act`` is accepted so the
         block can stand in for a decoder layer's dense MLP (it keeps its own intermediates). ``next_norm = (w,
-        x_next, eps)``: also the next RMSNorm of the output (a norm launch after the combine)."""
-        y = self._forward(h, out)
-        if next_norm is not None:
+        x_next, eps)``: also the next RMSNorm of the output (written by the combine); ``x_in``: the block's
+        normalized input when the caller has it (M ≥ 3: the block then takes no norm launch of its own)."""
+        y = self._forward(h, out, next_norm, x_in)
+        if next_norm is not None and not self.fused_shared:
             nw, nx, neps = next_norm
             kernels.norm_apply(y, nw, eps=neps, out=nx)
         return y
 
-    def _forward(self, h, out):
+    def _forward(self, h, out, next_norm=None, x_in=None):
         m = h.shape[0]
         logits, route, act, hk, s_act, s_out, s_gate, y = self.buffers(m)
         out = y if out is None else out
@@ -468,7 +469,8 @@ class MoeBlock:
             # normalize the whole [M, K] input again); M <= 2: fused into both GEMVs' loads
             x, nw = h, self.norm_w
             if m > 2:
-                x, nw = kernels.norm_apply(h, self.norm_w, eps=self.eps, out=self._normed(m)), None
+                x, nw = (x_in if x_in is not None
+                         else kernels.norm_apply(h, self.norm_w, eps=self.eps, out=self._normed(m))), None
             kernels.gemv(self.router_gate, x, norm_w=nw, eps=self.eps, out=logits[:, :e + 1])
             ids, wts, groups = route
             if m == 1:                  # one token: the expert gate|up launch routes for itself (one launch fewer)
@@ -483,7 +485,7 @@ class MoeBlock:
                              shared_expert=e, shared_epilogue="silu_mul", route=inline, group_max_pairs=ppr)
             kernels.moe_gemv(self.down_s, act, groups, tokens=m, top_k=k + 1, x_per_slot=True, out=hk,
                              group_max_pairs=ppr)
-            return kernels.moe_combine(hk, wts, top_k=k + 1, residual=h, out=out)
+            return kernels.moe_combine(hk, wts, top_k=k + 1, residual=h, out=out, next_norm=next_norm)
 
         def shared(ws=None):
             kernels.gemv(self.shared_gate_up.packed, h, epilogue="silu_mul", norm_w=self.norm_w, eps=self.eps,

@@ -88,7 +88,8 @@ class MiMoeCombineDesc(C.Structure):
     _fields_ = [("t", C.c_int32), ("hidden", C.c_int32), ("top_k", C.c_int32), ("h", C.c_void_p), ("ldh", C.c_int32),
                 ("weights", C.c_void_p), ("shared", C.c_void_p), ("ld_shared", C.c_int32), ("shared_gate", C.c_void_p),
                 ("ld_gate", C.c_int32), ("residual", C.c_void_p), ("ldr", C.c_int32), ("out", C.c_void_p),
-                ("ldo", C.c_int32)]
+                ("ldo", C.c_int32), ("next_norm_w", C.c_void_p), ("next_x", C.c_void_p), ("ld_next_x", C.c_int32),
+                ("next_eps", C.c_float)]
 
 
 class MiStepState(C.Structure):

@@ -450,3 +450,28 @@ def test_moe_route_records_of_two_pairs(torch_gpu, t, nan_row):
     y2 = kernels.moe_gemv(blk.down_s, act1, g2, tokens=t, top_k=k + 1, x_per_slot=True, group_max_pairs=2)
     torch.cuda.synchronize()
     assert torch.equal(y1.view(torch.int16)[ok], y2.view(torch.int16)[ok])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m", [1, 3, 8])
+def test_moe_block_norm_hand_over(torch_gpu, m):
+    """A MoE block given its normalized input (``x_in``, M ≥ 3) and asked for the next layer's (``next_norm``, written
+    by the combine) gives the same output bit for bit as the block normalizing its own input, and x_next is
+    ``norm_apply`` of that output."""
+    torch = torch_gpu
+    from monolith_mi355 import kernels
+    from monolith_mi355.layers import MoeBlock
+    a, b = MoeBlock(seed=81), MoeBlock(seed=81)
+    rng = np.random.default_rng(m + 30)
+    w_next = torch.from_numpy((1.0 + rng.standard_normal(a.hidden) * 0.1).astype(np.float32)).cuda()
+    xn = torch.empty(m, a.hidden, dtype=torch.bfloat16, device="cuda")
+    for step in range(2):
+        print(f"moe norm hand-over m={m} step {step}", flush=True)
+        h = torch.from_numpy(rng.standard_normal((m, a.hidden)).astype(np.float32)).cuda().to(torch.bfloat16)
+        y_a = a(h).clone()
+        x_in = kernels.norm_apply(h, b.norm_w, eps=b.eps) if m >= 3 else None
+        xn.fill_(3.0)
+        y_b = b(h, x_in=x_in, next_norm=(w_next, xn, 1e-6)).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(y_a.view(torch.int16), y_b.view(torch.int16)), step
+        assert torch.equal(xn.view(torch.int16), kernels.norm_apply(y_b, w_next, eps=1e-6).view(torch.int16)), step
