@@ -1808,7 +1808,9 @@ __global__ __launch_bounds__(RN_NT) void gemv_reduce_norm(Args a) {
   }
   const float* rsp = a.row_scale != nullptr ? a.row_scale + c : a.nn_w + c;   // the weights stand in: unused
   const float4 rs0 = *reinterpret_cast<const float4*>(rsp), rs1 = *reinterpret_cast<const float4*>(rsp + 4);
-  const uint4 rq = *reinterpret_cast<const uint4*>((resid ? a.res + (long long)t * a.ldr : a.nn_x) + c);
+  // no residual: a placeholder load from the (read-only) norm weights, whose value goes unused
+  const uint4 rq = *reinterpret_cast<const uint4*>(
+      (resid ? a.res + (long long)t * a.ldr : reinterpret_cast<const uint16_t*>(a.nn_w)) + c);
   const float4 w0 = *reinterpret_cast<const float4*>(a.nn_w + c), w1 = *reinterpret_cast<const float4*>(a.nn_w + c + 4);
   float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
