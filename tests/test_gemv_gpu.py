@@ -337,6 +337,9 @@ def test_gemv_split_k_fold_in_kernel(torch_gpu):
     ("nvfp4", 5120, 17408, 1, "residual", {}),              # splits folded in the kernel: a norm launch follows
     ("nvfp4", 2048, 5120, 8, None, {}),                     # one split: a norm launch follows
     ("nvfp4", 3000, 12288, 8, None, {}),                    # ragged N (whole 8-column vectors)
+    ("nvfp4", 8192, 12288, 4, "residual", {}),              # the widest row one reduction workgroup takes
+    ("nvfp4", 8200, 12288, 4, "residual", {}),              # wider: the reduction, then a norm launch
+    ("nvfp4", 1032, 12288, 16, "residual", {}),             # N not a multiple of 16, sixteen tokens
 ])
 def test_gemv_next_norm(torch_gpu, fmt, n, k, mtok, epi, env, rng, monkeypatch):
     """``next_norm``: y is bit-identical to the same GEMV without it, and x_next bit-identical to ``norm_apply`` of
@@ -348,7 +351,7 @@ def test_gemv_next_norm(torch_gpu, fmt, n, k, mtok, epi, env, rng, monkeypatch):
     m = _matrix(fmt, n, k, rng)
     w = _upload(torch, m)
     xd = to_dev_bf16(torch, rbf(rng.standard_normal((mtok, k))))
-    res = to_dev_bf16(torch, rbf(rng.standard_normal((mtok, n)))) if epi else None
+    res = to_dev_bf16(torch, rbf(rng.standard_normal((mtok, n + 24))))[:, :n] if epi else None   # row stride > n
     nw = torch.from_numpy((1.0 + rng.standard_normal(n) * 0.1).astype(np.float32)).cuda()
     y0 = kernels.gemv(w, xd, epilogue=epi, residual=res)
     x0 = kernels.norm_apply(y0, nw, eps=1e-6)
