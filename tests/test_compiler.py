@@ -350,28 +350,30 @@ def test_reference_moe_graph_program_equals_step_program(torch_gpu, tmp_path):
 
 
 @pytest.mark.gpu
-def test_speculative_program_equals_spec_program(torch_gpu, tmp_path):
+@pytest.mark.parametrize("moe", [False, True])
+def test_speculative_program_equals_spec_program(torch_gpu, tmp_path, moe):
     """The speculative round compiled from the reference's graph (verify block of 8 rows, accept scan, commit, the
     draft table, a fixed verify length) against the hand-built SpecProgram: the same tokens, the same states. The
-    drafts are the one-token decode's own tokens, so whole blocks are accepted and the commit replays 8 rows."""
+    drafts are the one-token decode's own tokens, so whole blocks are accepted and the commit replays 8 rows. With
+    MoE feed-forwards the hand-built verify pass hands each layer's input norm over through the MoE combine."""
     torch = torch_gpu
     from monolith_mi355.compiler import Profile, compile_decoder
     from monolith_mi355.runtime.step import SpecProgram, StepState
-    print("speculative program vs SpecProgram", flush=True)
-    seq = [9] + _step_program(torch, _decoder(torch, 41, "cuda"), 60, token=9)
+    print(f"speculative program vs SpecProgram moe={moe}", flush=True)
+    seq = [9] + _step_program(torch, _decoder(torch, 41, "cuda", moe=moe), 60, token=9)
     table = np.zeros((CTX, 8), np.int32)
     for pos in range(40, CTX):
         for j in range(7):
             i = pos - 40 + 1 + j
             table[pos, j] = seq[i] if i < len(seq) else 0
     steps = 8
-    a = _decoder(torch, 41, "cuda")
+    a = _decoder(torch, 41, "cuda", moe=moe)
     st = StepState(ring_capacity=512)
     prog = SpecProgram(a, st, gamma=7, draft_table=torch.from_numpy(table).cuda(), ctx_cap=240, steps_per_graph=2)
     st.start(position=40, token=9)
     tok_a = prog.step_eager(2) + prog.run(steps - 2, launches_per_batch=2, in_flight=2).tokens
     torch.cuda.synchronize()
-    b = _decoder(torch, 41, "cuda")
+    b = _decoder(torch, 41, "cuda", moe=moe)
     p, _, images = compile_decoder(b, tmp_path, Profile(ring_capacity=512, ctx_cap=240), gamma=7, verify_length=7,
                                    tables={"draft_table": (table, "I32")})
     eng = _engine(p, images)
