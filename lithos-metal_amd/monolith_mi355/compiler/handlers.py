@@ -109,6 +109,11 @@ def _gemv_desc(ctx: EmitContext, op: POp, *, out_f32: bool = False):
         gw, gz, geps = gated
         scalars.update(ld_gnorm_z=ctx.ld(gz), gnorm_eps=float(geps))
         ptrs.update(gnorm_w=gw, gnorm_z=gz)
+    nn = a.get("next_norm")                                           # (norm_w, x_next, eps): the next RMSNorm
+    if nn is not None:
+        nnw, nnx, neps = nn
+        scalars.update(ld_next_x=ctx.ld(nnx), next_eps=float(neps))
+        ptrs.update(next_norm_w=nnw, next_x=nnx)
     conv = a.get("conv")                                              # the GDN short conv in the epilogue
     if conv is not None:
         scalars.update(conv_row0=int(conv["row0"]), conv_channels=int(conv["channels"]), ld_conv=ctx.ld(conv["out"]))
@@ -130,7 +135,7 @@ def gemv(ctx: EmitContext, op: POp):
     scalars, ptrs = _gemv_desc(ctx, op)
     _workspace(ctx, scalars, ptrs)
     return lib_op(ctx, "mi_gemv", hip.MiGemvDesc, scalars, ptrs, f"gemv:{op.inputs[1].name}",
-                  writes=("y", "conv_in", "conv_out"))
+                  writes=("y", "conv_in", "conv_out", "next_x"))
 
 
 def lm_head(ctx: EmitContext, op: POp):
@@ -372,9 +377,13 @@ def moe_combine(ctx: EmitContext, op: POp):
                    ld_shared=ctx.ld(shared) if shared is not None else 0,
                    ld_gate=ctx.ld(gate) if gate is not None else 0,
                    ldr=ctx.ld(residual) if residual is not None else 0, ldo=ctx.ld(out))
-    return lib_op(ctx, "mi_moe_combine", hip.MiMoeCombineDesc, scalars,
-                  dict(h=h, weights=weights, shared=shared, shared_gate=gate, residual=residual, out=out),
-                  "moe_combine", writes=("out",))
+    ptrs = dict(h=h, weights=weights, shared=shared, shared_gate=gate, residual=residual, out=out)
+    nn = a.get("next_norm")                       # (norm_w, x_next, eps): the next RMSNorm, written by the combine
+    if nn is not None:
+        nnw, nnx, neps = nn
+        scalars.update(ld_next_x=ctx.ld(nnx), next_eps=float(neps))
+        ptrs.update(next_norm_w=nnw, next_x=nnx)
+    return lib_op(ctx, "mi_moe_combine", hip.MiMoeCombineDesc, scalars, ptrs, "moe_combine", writes=("out", "next_x"))
 
 
 # ---- the token loop's serial ops ---------------------------------------------------------------------------------

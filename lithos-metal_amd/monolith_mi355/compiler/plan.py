@@ -431,8 +431,52 @@ def plan_moe_groups(p: Plan) -> None:
                 op.attrs.update(groups=groups, pairs_per_record=ppr)
 
 
+def _norm_of(op: POp):
+    """(weight value, eps) of the RMSNorm a GEMV applies on load, or None."""
+    if op.attrs.get("norm"):
+        return op.inputs[3], float(op.attrs.get("eps", 1e-6))
+    if op.attrs.get("fused_norm") is not None:
+        nw, eps = op.attrs["fused_norm"]
+        return nw, float(eps)
+    return None
+
+
+def hand_over_norm(p: Plan) -> None:
+    """At T >= 3 a dense residual GEMV or a MoE combine whose output feeds GEMVs that normalize it on load (the next
+    layer's input projections, the LM head) writes the normalized rows itself — its split-K reduction or the combine
+    computes them (``mi_gemv`` / ``mi_moe_combine`` ``next_norm``) — and those GEMVs read them as they are: the input
+    norm takes no launch of its own. The same values (the norm is ``norm_apply``'s either way); at T <= 2 the GEMVs
+    keep the norm fused on load."""
+    if p.t < 3:
+        return
+    for prod in list(p.ops):
+        dense_res = (prod.kind == "gemv" and prod.attrs.get("epilogue") == "residual"
+                     and prod.attrs.get("gated_norm") is None and not prod.attrs.get("round_residual"))
+        if not (dense_res or prod.kind == "moe_combine"):
+            continue
+        h = prod.outputs[0]
+        users = [u for u in p.consumers(h) if u.inputs[0] is h and u.kind in ("gemv", "lm_head")
+                 and _norm_of(u) is not None]
+        norms = {(id(_norm_of(u)[0]), _norm_of(u)[1]) for u in users}
+        if not users or len(norms) != 1 or p.width(h) % 8:
+            continue
+        nw, eps = _norm_of(users[0])
+        xn = p.new_value(f"{h.name}.normed", (p.t, p.width(h)), "bf16")
+        prod.attrs["next_norm"] = (nw, xn, eps)
+        for u in users:
+            if u.attrs.get("norm"):
+                u.inputs = [xn, u.inputs[1]] + list(u.inputs[4:])
+                u.attrs["norm"] = False
+                u.attrs.pop("stat_computed", None)
+            else:
+                u.inputs[0] = xn
+                u.attrs["fused_norm"] = None
+        p.bump("hand_over_norm")
+
+
 PASSES: Tuple[Callable[[Plan], None], ...] = (merge_row_ranges, merge_adjacent_slabs, fuse_norm_stat, fold_norm_apply,
-                                              fuse_gdn, fold_gdn_conv, fuse_gqa, fuse_shared_expert, plan_moe_groups)
+                                              fuse_gdn, fold_gdn_conv, fuse_gqa, fuse_shared_expert, plan_moe_groups,
+                                              hand_over_norm)
 
 
 def run_passes(p: Plan, passes: Sequence[Callable[[Plan], None]] = PASSES) -> Plan:

@@ -231,6 +231,12 @@ def test_emit_speculative_round(tmp_path):
     assert p.ops[-1].meta["desc"]["mode"] == 2 and p.ops[-1].meta["desc"]["threshold"] == 7.0
     assert p.context_capacity == 240
     assert set(images) == set(p.state_names)
+    # T = 8: each layer's residual GEMV writes the next norm's rows (the next layer's input, then the LM head's), and
+    # the GEMVs that read them apply no norm of their own
+    handing = [o for o in p.ops if o.name.startswith("gemv") and o.meta["desc"].get("ld_next_x", 0) > 0]
+    assert len(handing) >= 2, [o.name for o in handing]
+    lm = p.ops[names.index("lm_head")]
+    assert "norm_w" not in _fields(hip.MiGemvDesc, lm)
 
 
 def test_backend_selection_and_coverage():
