@@ -340,6 +340,8 @@ def test_gemv_split_k_fold_in_kernel(torch_gpu):
     ("nvfp4", 8192, 12288, 4, "residual", {}),              # the widest row one reduction workgroup takes
     ("nvfp4", 8200, 12288, 4, "residual", {}),              # wider: the reduction, then a norm launch
     ("nvfp4", 1032, 12288, 16, "residual", {}),             # N not a multiple of 16, sixteen tokens
+    ("fp8_e4m3", 5120, 17408, 8, "residual", {}),           # per-row scales applied in the reduction
+    ("bf16", 2048, 8192, 8, None, {}),                      # BF16 weights (gemv_tk)
 ])
 def test_gemv_next_norm(torch_gpu, fmt, n, k, mtok, epi, env, rng, monkeypatch):
     """``next_norm``: y is bit-identical to the same GEMV without it, and x_next bit-identical to ``norm_apply`` of
